@@ -1,0 +1,496 @@
+"""Pins the CPU oracle (oracle/int4_oracle.c) before anything is checked
+against it.  Each check is one the reference holds (known answers, invariant
+suites, fixture bins) or one the mathematics fixes (f64 brute force over an
+independent numpy decode, closed forms) -- chosen so that a dropped term, a
+wrong sign/index or a transposed operand in the oracle fails one of them.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, rel_l2
+
+BF16, F16 = 0, 1
+
+
+# ----------------------------------------------------------------------------
+# independent numpy decode (not the oracle's code path)
+# ----------------------------------------------------------------------------
+
+def np_dequant(packed, scales, n, k, group, sdt):
+    p = np.frombuffer(np.ascontiguousarray(packed, np.uint8).tobytes(), np.uint8).reshape(n, k // 2)
+    nib = np.empty((n, k), np.int32)
+    nib[:, 0::2] = p & 0x0F
+    nib[:, 1::2] = p >> 4
+    s16 = np.frombuffer(np.ascontiguousarray(scales, np.uint8).tobytes(), "<u2").reshape(n, k // group)
+    if sdt == F16:
+        s = s16.view(np.float16).astype(np.float64)
+    else:
+        s = (s16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    return (nib - 8).astype(np.float64) * np.repeat(s, group, axis=1)
+
+
+def rand_layout(rng, n, k, group, sdt):
+    packed = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+    sc = np.abs(rng.normal(0, 0.02, n * (k // group))) + 1e-3
+    if sdt == F16:
+        bits = sc.astype(np.float16).view(np.uint16)
+    else:
+        bits = torch.tensor(sc, dtype=torch.float32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    return packed, bits.astype("<u2").view(np.uint8).copy()
+
+
+# reference generator, kernel_avx512_multi.rs:255-291 (and _blocked.rs)
+def ref_make_test_data(n_rows, k_cols, seq):
+    r = np.arange(n_rows)[:, None]
+    c = np.arange(k_cols // 2)[None, :]
+    packed = ((r * 31 + c) & 0xFF).astype(np.uint8).ravel()
+    ng = k_cols // 32
+    g = np.arange(ng)[None, :]
+    s = (0.5 + ((r * 7 + g * 3) % 11).astype(np.float32) * np.float32(0.1)).astype(np.float32)
+    u = s.view(np.uint32).astype(np.uint64)
+    bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype("<u2")
+    t = np.arange(seq)[:, None]
+    cc = np.arange(k_cols)[None, :]
+    xs = (np.sin((t * 17 + cc * 5).astype(np.float32)) * np.float32(0.5)).astype(np.float32)
+    return packed, bits.view(np.uint8).ravel().copy(), xs.ravel()
+
+
+# ----------------------------------------------------------------------------
+# a2: conversions
+# ----------------------------------------------------------------------------
+
+def test_bf16_rne_matches_half_cases(orc):
+    """format.rs:173-201 case list; expected bits from torch's RNE bf16."""
+    cases = [0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 2.0, 0.125, 1.0e-30, np.pi, -42.5]
+    for x in cases:
+        want = int(torch.tensor(x, dtype=torch.float32).to(torch.bfloat16).view(torch.int16).item()) & 0xFFFF
+        assert orc.lib().or_f32_to_bf16(x) == want, x
+    nan = orc.lib().or_f32_to_bf16(float("nan"))
+    assert (nan & 0x7F80) == 0x7F80 and (nan & 0x7F) != 0
+
+
+def test_bf16_rne_random_sweep(orc):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    finite = np.isfinite(x)
+    x = x[finite]
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = orc.f32_to_bf16(x)
+    assert np.array_equal(got, want)
+    # the C scalar agrees with the vectorised helper
+    for v in x[:2000]:
+        assert orc.lib().or_f32_to_bf16(float(v)) == orc.f32_to_bf16(np.float32(v))[()]
+
+
+def test_f16_conversions_match_numpy(orc):
+    rng = np.random.default_rng(2)
+    # every fp16 bit pattern decodes exactly
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = allh.view(np.float16).astype(np.float32)
+    L = orc.lib()
+    got = np.array([L.or_f16_to_f32(int(h)) for h in allh], np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+    # f32 -> f16 RNE incl. subnormals, ties and overflow
+    xs = np.concatenate([
+        rng.normal(0, 1, 20000), rng.normal(0, 1e-5, 20000), rng.normal(0, 3e4, 5000),
+        [65504.0, 65520.0, 65519.99, 2.0**-24, 2.0**-25, 1.5 * 2.0**-25, 2.0**-26, 0.0, -0.0],
+    ]).astype(np.float32)
+    w = xs.astype(np.float16).view(np.uint16)
+    g = np.array([L.or_f32_to_f16(float(v)) for v in xs], np.uint16)
+    assert np.array_equal(g, w)
+
+
+# ----------------------------------------------------------------------------
+# a3/a4: GEMV known answers (kernel.rs:144-181)
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_zero_weight_zero_output(orc, order):
+    n, k = 4, 32
+    packed = np.full(n * k // 2, 0x88, np.uint8)
+    scales = np.tile(np.array([0x80, 0x3F], np.uint8), n * (k // 32))
+    x = np.arange(k, dtype=np.float32) * np.float32(0.1)
+    y = orc.gemv(packed, scales, x, n, k, 32, BF16, order)
+    assert np.all(np.abs(y) < 1e-6)
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_unit_weight_picks_first_column(orc, order):
+    n, k = 1, 32
+    packed = np.full(n * k // 2, 0x88, np.uint8)
+    packed[0] = 0x89  # low nibble 9 -> +1 at column 0
+    scales = np.array([0x80, 0x3F], np.uint8)
+    x = np.arange(k, dtype=np.float32) + 1
+    y = orc.gemv(packed, scales, x, n, k, 32, BF16, order)
+    assert abs(y[0] - 1.0) < 1e-5
+    packed[0] = 0x98  # high nibble -> column 1
+    assert abs(orc.gemv(packed, scales, x, n, k, 32, BF16, order)[0] - 2.0) < 1e-5
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_one_hot_every_position(orc, order):
+    """A +1 code at (row r, col c) with unit scale must return exactly x[c]
+    in row r and 0 elsewhere: pins nibble order, row stride and group index."""
+    n, k, G = 3, 128, 64
+    x = (np.arange(k, dtype=np.float32) * np.float32(0.37) - 3).astype(np.float32)
+    rng = np.random.default_rng(3)
+    for _ in range(40):
+        r, c = int(rng.integers(n)), int(rng.integers(k))
+        sc = rng.choice([0.5, 1.0, 2.0, 0.25])
+        packed = np.full(n * k // 2, 0x88, np.uint8)
+        b = r * (k // 2) + c // 2
+        packed[b] = (0x89 if c % 2 == 0 else 0x98)
+        scales = np.full(n * (k // G), np.float16(sc).view(np.uint16), np.uint16).view(np.uint8)
+        y = orc.gemv(packed, scales, x, n, k, G, F16, order)
+        want = np.zeros(n, np.float32)
+        want[r] = x[c] * np.float32(sc)
+        assert np.array_equal(y, want), (r, c)
+
+
+@pytest.mark.parametrize("group,sdt", [(32, BF16), (32, F16), (64, F16), (128, F16), (128, BF16)])
+def test_dequant_bit_exact_vs_numpy(orc, group, sdt):
+    rng = np.random.default_rng(group + sdt)
+    n, k = 24, 512
+    packed, scales = rand_layout(rng, n, k, group, sdt)
+    got = orc.dequant(packed, scales, n, k, group, sdt)
+    want = np_dequant(packed, scales, n, k, group, sdt).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("order", [0, 1])
+@pytest.mark.parametrize("group,sdt", [(32, BF16), (64, F16), (128, F16)])
+def test_gemv_vs_f64_brute_force(orc, order, group, sdt):
+    rng = np.random.default_rng(7 * group + sdt + order)
+    n, k = 64, 1024
+    packed, scales = rand_layout(rng, n, k, group, sdt)
+    x = rng.normal(0, 1, k).astype(np.float32)
+    y = orc.gemv(packed, scales, x, n, k, group, sdt, order)
+    want = np_dequant(packed, scales, n, k, group, sdt) @ x.astype(np.float64)
+    assert rel_l2(y, want) < 2e-6
+    # a transposed read or a dropped group would be O(1) wrong
+    assert np.max(np.abs(y - want)) < 1e-4 * np.max(np.abs(want))
+
+
+def test_scalar_and_avx512_orders_differ_only_by_rounding(orc):
+    packed, scales, xs = ref_make_test_data(96, 1536, 1)
+    a = orc.gemv(packed, scales, xs, 96, 1536, 32, BF16, 0)
+    b = orc.gemv(packed, scales, xs, 96, 1536, 32, BF16, 1)
+    assert rel_l2(a, b) < 1e-6
+
+
+# ----------------------------------------------------------------------------
+# a5/a6: multi / blocked tiles bit-identical per token
+# (kernel_avx512_multi.rs:293-396, kernel_avx512_multi_blocked.rs:392-595)
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k,seq", [(64, 128, 1), (64, 128, 4), (96, 1536, 8), (65, 256, 5),
+                                     (63, 8192, 16), (128, 256, 2), (32, 256, 64), (16, 256, 65)])
+def test_cpu_tiles_bit_identical_to_per_token(orc, n, k, seq):
+    """The timed AVX-512 tiles (cpu_baseline.c) == per-token restatement,
+    bitwise, on the crate's own generator; odd rows hit the RB=2 tail."""
+    if orc.cpu_isa() != 2:
+        pytest.skip("host has no AVX-512; the tiles then use another order")
+    packed, scales, xs = ref_make_test_data(n, k, seq)
+    want = orc.gemm_multi(packed, scales, xs, n, k, seq, 32, BF16, 1)
+    got = orc.cpu_gemm(packed, scales, xs, n, k, seq, 32, BF16)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("group,sdt", [(128, F16), (32, F16)])
+def test_cpu_tiles_generalised_group(orc, group, sdt):
+    if orc.cpu_isa() != 2:
+        pytest.skip("host has no AVX-512")
+    rng = np.random.default_rng(11)
+    n, k = 48, 1024
+    packed, scales = rand_layout(rng, n, k, group, sdt)
+    for seq in (1, 3, 8, 20):
+        xs = rng.normal(0, 1, seq * k).astype(np.float32)
+        want = orc.gemm_multi(packed, scales, xs, n, k, seq, group, sdt, 1)
+        got = orc.cpu_gemm(packed, scales, xs, n, k, seq, group, sdt)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), seq
+
+
+# ----------------------------------------------------------------------------
+# a7/a8: expert FFN, sparse variants (ffn_sparsity.rs:981-1194)
+# ----------------------------------------------------------------------------
+
+def fake_expert(hidden, inter, gate_b=0x9A, up_b=0x8B, down_b=0x7C):
+    """ffn_sparsity.rs:985-1002: constant bytes, unit bf16 scales, G=32."""
+    one = np.array([0x80, 0x3F], np.uint8)
+    parts = [np.full(inter * hidden // 2, gate_b, np.uint8), np.tile(one, inter * (hidden // 32)),
+             np.full(inter * hidden // 2, up_b, np.uint8), np.tile(one, inter * (hidden // 32)),
+             np.full(hidden * inter // 2, down_b, np.uint8), np.tile(one, hidden * (inter // 32))]
+    return np.concatenate(parts)
+
+
+def test_sparse_tau_zero_matches_dense(orc):
+    h = i = 32
+    flat = fake_expert(h, i)
+    x = orc.f32_to_bf16(np.arange(h, dtype=np.float32) * np.float32(0.05) - np.float32(0.5))
+    dense = orc.expert_forward(x, flat, h, i, 32, BF16)
+    sparse, frac = orc.expert_forward_sparse(x, flat, h, i, 32, BF16, 0.0)
+    assert frac == 1.0 and np.array_equal(dense, sparse)
+
+
+def test_sparse_tau_small_close_to_dense(orc):
+    h = i = 32
+    flat = fake_expert(h, i)
+    x = orc.f32_to_bf16(np.arange(h, dtype=np.float32) * np.float32(0.05) - np.float32(0.5))
+    dense = orc.bf16_to_f32(orc.expert_forward(x, flat, h, i, 32, BF16))
+    sp, frac = orc.expert_forward_sparse(x, flat, h, i, 32, BF16, 0.10)
+    sp = orc.bf16_to_f32(sp)
+    assert 0.0 < frac <= 1.0
+    assert np.max(np.abs(dense - sp)) < np.max(np.abs(dense)) * 2 + 1
+
+
+def test_ffn_f32_tau_zero_matches_inline_dense(orc):
+    """ffn_sparsity.rs:1110-1194: tau 0 == gemv, gemv, swiglu_mul, gemv (bitwise)."""
+    h = i = 32
+    flat = fake_expert(h, i)
+    o, _ = orc.expert_offsets(h, i, 32)
+    x = (np.arange(h, dtype=np.float32) * np.float32(0.05) - np.float32(0.5)).astype(np.float32)
+    g = orc.gemv(flat[o[0]:o[1]], flat[o[1]:o[2]], x, i, h, 32, BF16)
+    u = orc.gemv(flat[o[2]:o[3]], flat[o[3]:o[4]], x, i, h, 32, BF16)
+    m = (g / (np.float32(1) + np.exp(-g))).astype(np.float32) * u
+    ref = orc.gemv(flat[o[4]:o[5]], flat[o[5]:], m.astype(np.float32), h, i, 32, BF16)
+    got, frac = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, 0.0)
+    assert frac == 1.0
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_mask_threshold_cases(orc):
+    _, act = orc.build_active_mask(np.array([1.0, -2.0, 0.5, -0.1], np.float32), 0.0)
+    assert act.tolist() == [0, 1, 2, 3]
+    g = np.array([10.0, 0.001, 5.0, -0.001], np.float32)
+    silu, act = orc.build_active_mask(g, 0.5)
+    assert silu[0] > 5.0 and act.tolist() == [0]
+    _, act2 = orc.build_active_mask(g, 0.1)
+    assert act2.tolist() == [0, 2]
+
+
+def test_rows_subset(orc):
+    n, k = 4, 32
+    packed = (np.arange(n * k // 2) % 256).astype(np.uint8)
+    scales = np.tile(np.array([0x80, 0x3F], np.uint8), n)
+    x = np.arange(k, dtype=np.float32) * np.float32(0.01)
+    dense = orc.gemv(packed, scales, x, n, k, 32, BF16)
+    y = np.zeros(n, np.float32)
+    orc.gemv_rows_subset(packed, scales, x, n, k, 32, BF16, np.arange(n), y)
+    assert np.array_equal(dense, y)
+    y = np.full(n, 123.0, np.float32)
+    orc.gemv_rows_subset(np.full(n * k // 2, 0xAA, np.uint8), scales, np.ones(k, np.float32),
+                         n, k, 32, BF16, [1], y)
+    assert y[0] == 123.0 and y[2] == 123.0 and y[3] == 123.0 and abs(y[1] - 123.0) > 1e-3
+
+
+def ref_pack(w, out, inn, G=32):
+    """ov_moe.rs:837-862 test packer (test-data preparation)."""
+    ng = inn // G
+    wg = w.reshape(out, ng, G)
+    mx = np.abs(wg).max(axis=2)
+    s = np.where(mx > 0, mx / np.float32(7), np.float32(1)).astype(np.float32)
+    q = np.clip(np.round(wg / s[:, :, None]), -8, 7).astype(np.int32)
+    nib = (q + 8).astype(np.uint8).reshape(out, inn)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    u = s.view(np.uint32).astype(np.uint64)
+    bf = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype("<u2")
+    return packed.ravel(), bf.view(np.uint8).ravel()
+
+
+def test_int4_expert_vs_fp32_swiglu(orc):
+    """ov_moe.rs:888-920: int4 expert within rel-L2 0.1 of the fp32 SwiGLU."""
+    h, m = 64, 32
+
+    def mk(n, seed):
+        i = np.arange(n, dtype=np.uint64)
+        v = ((i * 2654435761 + seed) & 0xFFFFFFFF) % 1000
+        return ((v.astype(np.float32) / np.float32(1000) - np.float32(0.5)) * np.float32(0.2)).astype(np.float32)
+
+    gate, up, down, x = mk(m * h, 1), mk(m * h, 2), mk(h * m, 3), mk(h, 4)
+    flat = np.concatenate([*ref_pack(gate, m, h), *ref_pack(up, m, h), *ref_pack(down, h, m)])
+    xb = orc.f32_to_bf16(x)
+    got = orc.bf16_to_f32(orc.expert_forward(xb, flat, h, m, 32, BF16))
+    G, U, D = gate.reshape(m, h), up.reshape(m, h), down.reshape(h, m)
+    g = G @ x
+    u = U @ x
+    want = D @ ((g / (1 + np.exp(-g))) * u)
+    assert rel_l2(got, want) < 0.1
+
+
+# ----------------------------------------------------------------------------
+# reference fixture bins (real exporter output in the crate layout)
+# ----------------------------------------------------------------------------
+
+FIXTURES = [("dsv4_layer_00", 64, 32), ("dsv4_layer_01", 64, 32), ("glm5_layer_01", 32, 32)]
+
+
+def fixture_files():
+    for d, h, i in FIXTURES:
+        for f in sorted(glob.glob(os.path.join(GOLDEN, "fixture_experts", d, "*.bin"))):
+            yield f, h, i
+
+
+def test_fixture_bins_layout_invariants(orc):
+    """Every (row, group) of every section holds a |q| = 7 code and no -8
+    code, or is an all-zero group with scale 1.0 -- the exporter's quantiser
+    (tools/export_deepseek_v4.py:85-94).  A wrong row stride, group width,
+    zero point or section order breaks it."""
+    n_files = 0
+    for f, h, i in fixture_files():
+        flat = np.fromfile(f, np.uint8)
+        assert flat.size == orc.expert_bytes(h, i, 32)
+        o, sz = orc.expert_offsets(h, i, 32)
+        for (rows, cols), (po, so) in zip([(i, h), (i, h), (h, i)], [(0, 1), (2, 3), (4, 5)]):
+            p = flat[o[po]:o[po] + sz[po]].reshape(rows, cols // 2)
+            nib = np.empty((rows, cols), np.int32)
+            nib[:, 0::2] = p & 15
+            nib[:, 1::2] = p >> 4
+            q = (nib - 8).reshape(rows, cols // 32, 32)
+            s = np.frombuffer(flat[o[so]:o[so] + sz[so]].tobytes(), "<u2").reshape(rows, cols // 32)
+            zero = np.all(q == 0, axis=2)
+            assert np.all(s[zero] == 0x3F80)
+            assert np.all(np.abs(q).max(axis=2)[~zero] == 7)
+            assert not np.any(q == -8)
+            sf = (s.astype(np.uint32) << 16).view(np.float32)
+            assert np.all(sf > 0) and np.all(np.isfinite(sf))
+        n_files += 1
+    assert n_files == 23
+
+
+def test_fixture_expert_forward_vs_f64(orc):
+    """expert_forward on every fixture expert vs an f64 numpy SwiGLU over an
+    independent decode, both rounded at the crate's points."""
+    rng = np.random.default_rng(5)
+    for f, h, i in fixture_files():
+        flat = np.fromfile(f, np.uint8)
+        o, sz = orc.expert_offsets(h, i, 32)
+        Wg = np_dequant(flat[o[0]:o[1]], flat[o[1]:o[2]], i, h, 32, BF16)
+        Wu = np_dequant(flat[o[2]:o[3]], flat[o[3]:o[4]], i, h, 32, BF16)
+        Wd = np_dequant(flat[o[4]:o[5]], flat[o[5]:], h, i, 32, BF16)
+        xb = orc.f32_to_bf16(rng.normal(0, 1, h).astype(np.float32))
+        x = orc.bf16_to_f32(xb).astype(np.float64)
+        g, u = Wg @ x, Wu @ x
+        want = Wd @ ((g / (1 + np.exp(-g))) * u)
+        got = orc.bf16_to_f32(orc.expert_forward(xb, flat, h, i, 32, BF16))
+        assert rel_l2(got, want) < 4e-3, f  # bf16 output rounding dominates
+        sh, _ = orc.ffn_forward_f32(x.astype(np.float32), flat, h, i, 32, BF16, 0.0)
+        assert rel_l2(sh, want) < 1e-5, f
+
+
+# ----------------------------------------------------------------------------
+# a9: routing
+# ----------------------------------------------------------------------------
+
+def test_glm_gate_tie_breaks_to_lower_id(orc):
+    """glm/gate.rs:67-80."""
+    ids, w = orc.route_sigmoid_bias([0, 0, 0, 0], [0.1, 0.1, 0, 0], 2, 2.5, True)
+    assert ids.tolist() == [0, 1]
+    assert abs(w[0] - 1.25) < 1e-6 and abs(w[1] - 1.25) < 1e-6
+
+
+def test_glm_gate_no_norm_at_top1(orc):
+    """glm/gate.rs:82-89."""
+    ids, w = orc.route_sigmoid_bias([10.0, -10.0], [0, 0], 1, 2.0, True)
+    assert ids.tolist() == [0]
+    assert abs(w[0] - 2.0 * (1 / (1 + np.exp(-10.0)))) < 1e-6
+
+
+def test_k26_router_vs_numpy(orc):
+    """shell_int4.rs:588-620: stable descending sort of sigmoid+bias."""
+    rng = np.random.default_rng(9)
+    for _ in range(50):
+        l = rng.normal(0, 1, 384).astype(np.float32)
+        l[rng.integers(384, size=20)] = l[0]  # plant ties
+        b = (rng.normal(0, 0.01, 384) * rng.integers(0, 2)).astype(np.float32)
+        ids, w = orc.route_sigmoid_bias(l, b, 8, 2.827, True)
+        sc = (1 / (1 + np.exp(-l.astype(np.float64))))
+        ch = sc.astype(np.float32) + b
+        order = np.argsort(-ch, kind="stable")[:8]
+        assert ids.tolist() == order.tolist()
+        ww = sc[order] / (sc[order].sum() + 1e-20) * 2.827
+        assert np.allclose(w, ww, rtol=1e-5)
+
+
+def test_softmax_topk_vs_numpy(orc):
+    rng = np.random.default_rng(10)
+    for _ in range(50):
+        l = rng.normal(0, 1, 256).astype(np.float32)
+        l[5] = l[200] = l.max() + 1  # tie at the top -> lower id first
+        ids, w = orc.route_softmax_topk(l, 8)
+        order = np.argsort(-l, kind="stable")[:8]
+        assert ids.tolist() == order.tolist() and ids[0] == 5 and ids[1] == 200
+        e = np.exp(l[order].astype(np.float64) - l[order].max())
+        assert np.allclose(w, e / e.sum(), rtol=1e-6)
+        assert abs(float(w.sum()) - 1.0) < 1e-6
+
+
+# ----------------------------------------------------------------------------
+# a10: per-token dispatch + combine (runner.rs:1806-1832)
+# ----------------------------------------------------------------------------
+
+def test_moe_combine_slot_order_and_threshold(orc):
+    h, i, E, k, T = 64, 32, 8, 2, 3
+    files = sorted(glob.glob(os.path.join(GOLDEN, "fixture_experts", "dsv4_layer_00", "expert_0*.bin")))
+    experts = np.concatenate([np.fromfile(f, np.uint8) for f in files])
+    shared = np.fromfile(os.path.join(GOLDEN, "fixture_experts", "dsv4_layer_00", "expert_shared.bin"), np.uint8)
+    rng = np.random.default_rng(12)
+    x = rng.normal(0, 1, (T, h)).astype(np.float32)
+    ids = np.array([[3, 1], [0, 7], [5, 5]], np.int64)
+    w = np.array([[0.7, 0.3], [0.05, 0.95], [0.5, 0.25]], np.float32)
+    got = orc.moe_routed(x, experts, E, h, i, 32, BF16, ids, w, threshold=0.1)
+    stride = experts.size // E
+    for t in range(T):
+        acc = np.zeros(h, np.float32)
+        xb = orc.f32_to_bf16(x[t])
+        for s in range(k):
+            if w[t, s] < 0.1:
+                continue
+            y = orc.bf16_to_f32(orc.expert_forward(xb, experts[ids[t, s] * stride:(ids[t, s] + 1) * stride], h, i, 32, BF16))
+            acc = (acc + w[t, s] * y).astype(np.float32)
+        assert np.array_equal(got[t], acc)
+    layer = orc.moe_layer(x, experts, E, shared, i, h, i, 32, BF16, ids, w, threshold=0.1)
+    for t in range(T):
+        sh, _ = orc.ffn_forward_f32(x[t], shared, h, i, 32, BF16, 0.0)
+        assert np.array_equal(layer[t], ((x[t] + sh).astype(np.float32) + got[t]).astype(np.float32))
+
+
+# ----------------------------------------------------------------------------
+# a11: load-time quantiser (shell_int4.rs:148-212)
+# ----------------------------------------------------------------------------
+
+def test_quantize_roundtrip(orc):
+    rng = np.random.default_rng(13)
+    n, k = 16, 256
+    w = rng.normal(0, 0.05, (n, k)).astype(np.float32)
+    w[3, :32] = 0.0  # all-zero group -> scale 1e-10, codes 8
+    wb = orc.f32_to_bf16(w)
+    packed, scales = orc.quantize_int4_group(wb, n, k, 32)
+    deq = np_dequant(packed, scales, n, k, 32, BF16)
+    wf = orc.bf16_to_f32(wb).reshape(n, k).astype(np.float64)
+    s = np.repeat((np.frombuffer(scales.tobytes(), "<u2").astype(np.uint32) << 16).view(np.float32).reshape(n, k // 32), 32, axis=1)
+    assert np.all(np.abs(deq - wf) <= 0.5 * s + 1e-12)
+    assert np.all(packed[3 * (k // 2):3 * (k // 2) + 16] == 0x88)
+
+
+# ----------------------------------------------------------------------------
+# generators
+# ----------------------------------------------------------------------------
+
+def test_generators_deterministic_and_distributed(orc):
+    a = orc.fill_bytes(0, 1, 1 << 16)
+    assert np.array_equal(a, orc.fill_bytes(0, 1, 1 << 16))
+    assert not np.array_equal(a, orc.fill_bytes(0, 2, 1 << 16))
+    nib = np.concatenate([a & 15, a >> 4])
+    counts = np.bincount(nib, minlength=16)
+    assert counts.min() > 0.9 * nib.size / 16 and counts.max() < 1.1 * nib.size / 16
+    z = orc.fill_normal_f32(0, 3, 100000)
+    assert abs(z.mean()) < 0.02 and abs(z.std() - 1) < 0.02
+    s = orc.fill_scales(0, 4, 100000, F16).view(np.float16).astype(np.float64)
+    assert s.min() >= 1e-3 * 0.999 and abs((s - 1e-3).mean() - 0.02 * np.sqrt(2 / np.pi)) < 5e-4
