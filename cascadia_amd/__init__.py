@@ -1,0 +1,26 @@
+"""cascadia_amd -- MI355X (gfx950) implementation of cascadia-int4-gemm's INT4
+weight-only matmul hot path, behind the C ABI of include/cascadia_int4.h.
+
+Importing the package loads libcascadia_int4_hip.so; it raises if the library
+was not built (``python cascadia_amd/build.py``).  There is no CPU fallback.
+"""
+from ._lib import (CascadiaInt4Error, LIB_PATH, SCALE_BF16, SCALE_F16, SIGNATURES, check,
+                   lib)
+
+lib()  # fail loudly at import when the HIP library is missing
+
+from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertWeights,  # noqa: E402
+                  debug_dequant, dequant_gemm_int4_multi_auto,
+                  dequant_gemm_int4_multi_blocked_auto, dequant_gemv_int4,
+                  dequant_gemv_int4_auto, expert_bytes, expert_forward, expert_forward_sparse,
+                  ffn_forward_sparse_f32, ffn_workspace_bytes, fill_bytes, fill_normal,
+                  fill_scales, gate_up_silu, gemm_int4_bf16)
+
+__all__ = [
+    "CascadiaInt4Error", "LIB_PATH", "SCALE_BF16", "SCALE_F16", "SIGNATURES", "check", "lib",
+    "GROUP_SIZE", "HIDDEN", "INTERMEDIATE", "NIBBLES_PER_INT32", "ExpertWeights",
+    "debug_dequant", "dequant_gemm_int4_multi_auto", "dequant_gemm_int4_multi_blocked_auto",
+    "dequant_gemv_int4", "dequant_gemv_int4_auto", "expert_bytes", "expert_forward",
+    "expert_forward_sparse", "ffn_forward_sparse_f32", "ffn_workspace_bytes", "fill_bytes",
+    "fill_normal", "fill_scales", "gate_up_silu", "gemm_int4_bf16",
+]

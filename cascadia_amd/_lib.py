@@ -1,0 +1,85 @@
+"""ctypes binding of libcascadia_int4_hip.so (the C ABI in include/cascadia_int4.h).
+
+Loading fails loudly: there is no CPU fallback anywhere in this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "libcascadia_int4_hip.so")
+
+OK = 0
+ERR_NULL = -1
+ERR_ARG = -2
+ERR_DEVICE = -3
+ERR_NOMEM = -4
+SCALE_BF16 = 0
+SCALE_F16 = 1
+
+_ERRS = {ERR_NULL: "null pointer", ERR_ARG: "invalid argument (shape/length/alignment)",
+         ERR_DEVICE: "HIP device error", ERR_NOMEM: "device allocation failed"}
+
+
+class CascadiaInt4Error(RuntimeError):
+    def __init__(self, fn: str, rc: int):
+        super().__init__(f"{fn} returned {rc} ({_ERRS.get(rc, 'unknown')})")
+        self.rc = rc
+
+
+class Layout(C.Structure):
+    _fields_ = [("n_rows", C.c_uint32), ("k_cols", C.c_uint32),
+                ("group_size", C.c_uint32), ("scale_dtype", C.c_uint32)]
+
+
+class Expert(C.Structure):
+    _fields_ = [("gate_packed", C.c_void_p), ("gate_scale", C.c_void_p),
+                ("up_packed", C.c_void_p), ("up_scale", C.c_void_p),
+                ("down_packed", C.c_void_p), ("down_scale", C.c_void_p)]
+
+
+_vp, _u32, _u64, _sz, _f64, _i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_size_t, C.c_double, C.c_int
+_LP, _EP = C.POINTER(Layout), C.POINTER(Expert)
+
+# Every symbol declared in include/cascadia_int4.h: (restype, argtypes).
+SIGNATURES = {
+    "cascadia_int4_version": (C.c_char_p, []),
+    "cascadia_int4_synchronize": (_i32, [_vp]),
+    "cascadia_int4_dequant_gemv": (_i32, [_LP, _vp, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_dequant_gemm_multi": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
+    "cascadia_int4_dequant_gemm_bf16in": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
+    "cascadia_int4_gemm_bf16": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
+    "cascadia_int4_expert_bytes": (_sz, [_u32, _u32, _u32]),
+    "cascadia_int4_expert_from_flat": (_i32, [_vp, _u32, _u32, _u32, _EP]),
+    "cascadia_int4_ffn_workspace_bytes": (_sz, [_u32, _u32, _u32]),
+    "cascadia_int4_expert_forward": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
+    "cascadia_int4_ffn_forward_f32": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
+    "cascadia_int4_gate_up_silu": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _u32, _vp, _vp]),
+    "cascadia_int4_debug_dequant": (_i32, [_LP, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_fill_synthetic": (_i32, [_u32, _u64, _u64, _sz, _f64, _f64, _u32, _vp, _vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the library (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python cascadia_amd/build.py` "
+                "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(fn: str, rc: int) -> None:
+    if rc != OK:
+        raise CascadiaInt4Error(fn, rc)

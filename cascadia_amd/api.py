@@ -1,0 +1,305 @@
+"""Python mirror of cascadia-int4-gemm's public API over HBM-resident tensors.
+
+Same function names, argument order and meaning as the crate
+(crates/cascadia-int4-gemm/src/lib.rs:29-78), with torch device tensors in
+place of Rust slices.  Where the crate panics on a length mismatch
+(assert_eq!, kernel.rs:39-43) these raise ValueError before any GPU work.
+Work is enqueued on torch's current stream; reading a result back (e.g.
+``.cpu()``) waits for it, as the crate's synchronous call would.
+
+torch is plumbing here (device memory, streams); every computation runs in
+libcascadia_int4_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from ._lib import Expert, Layout, SCALE_BF16, SCALE_F16, check, lib
+
+# K2.6 constants of the crate (lib.rs:71-78)
+HIDDEN = 7168
+INTERMEDIATE = 2048
+GROUP_SIZE = 32
+NIBBLES_PER_INT32 = 8
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a device (HBM) tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def _expect(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _is_bf16_bits(t: torch.Tensor) -> bool:
+    return t.dtype in (torch.bfloat16, torch.int16, torch.uint16)
+
+
+def _layout(n_rows, k_cols, group_size, scale_dtype) -> Layout:
+    return Layout(n_rows, k_cols, group_size, scale_dtype)
+
+
+def _check_weights(packed, scale_bits, n_rows, k_cols, group_size):
+    _dev(packed, "packed")
+    _dev(scale_bits, "scale_bits")
+    _expect(group_size % 32 == 0 and k_cols % group_size == 0,
+            f"k_cols {k_cols} must be a multiple of group_size {group_size} (a multiple of 32)")
+    _expect(_nbytes(packed) == n_rows * (k_cols // 2),
+            f"packed has {_nbytes(packed)} bytes, expected n_rows*k_cols/2 = {n_rows * (k_cols // 2)}")
+    _expect(_nbytes(scale_bits) == n_rows * (k_cols // group_size) * 2,
+            f"scale_bits has {_nbytes(scale_bits)} bytes, expected {n_rows * (k_cols // group_size) * 2}")
+
+
+# ---------------------------------------------------------------------------
+# GEMV / GEMM
+# ---------------------------------------------------------------------------
+
+def dequant_gemv_int4(packed, scale_bits, x, n_rows, k_cols, y, group_size=GROUP_SIZE,
+                      scale_dtype=SCALE_BF16):
+    """y = W x (kernel.rs:31-71).  x f32 [k_cols], y f32 [n_rows]."""
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    _dev(x, "x"), _dev(y, "y")
+    _expect(x.dtype == torch.float32 and x.numel() == k_cols, "x must be f32 [k_cols]")
+    _expect(y.dtype == torch.float32 and y.numel() == n_rows, "y must be f32 [n_rows]")
+    L = _layout(n_rows, k_cols, group_size, scale_dtype)
+    check("cascadia_int4_dequant_gemv", lib().cascadia_int4_dequant_gemv(
+        C.byref(L), packed.data_ptr(), scale_bits.data_ptr(), x.data_ptr(), y.data_ptr(),
+        _stream()))
+    return y
+
+
+dequant_gemv_int4_auto = dequant_gemv_int4  # kernel_avx512.rs:274-297
+
+
+def dequant_gemm_int4_multi_auto(packed, scale_bits, xs, n_rows, k_cols, seq, ys,
+                                 group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
+    """ys[t*n_rows + r] for t < seq (kernel_avx512_multi.rs:207-245).
+    xs f32 [seq, k_cols]; bf16 xs use the exact bf16 MFMA path."""
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    _dev(xs, "xs"), _dev(ys, "ys")
+    _expect(seq >= 1, "seq must be >= 1")
+    _expect(xs.numel() == seq * k_cols, f"xs must hold seq*k_cols = {seq * k_cols} values")
+    _expect(ys.dtype == torch.float32 and ys.numel() == seq * n_rows,
+            f"ys must be f32 [seq*n_rows = {seq * n_rows}]")
+    L = _layout(n_rows, k_cols, group_size, scale_dtype)
+    if xs.dtype == torch.float32:
+        fn = "cascadia_int4_dequant_gemm_multi"
+    else:
+        _expect(_is_bf16_bits(xs), "xs must be f32 or bf16")
+        fn = "cascadia_int4_dequant_gemm_bf16in"
+    check(fn, getattr(lib(), fn)(C.byref(L), packed.data_ptr(), scale_bits.data_ptr(),
+                                 xs.data_ptr(), seq, ys.data_ptr(), _stream()))
+    return ys
+
+
+dequant_gemm_int4_multi_blocked_auto = dequant_gemm_int4_multi_auto  # _blocked.rs:295-347
+
+
+def gemm_int4_bf16(packed, scale_bits, xs_bf16, n_rows, k_cols, seq, ys_bf16,
+                   group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
+    """Prefill GEMM: bf16 [seq, k_cols] in, bf16 [seq, n_rows] out (f32 inside)."""
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    _dev(xs_bf16, "xs_bf16"), _dev(ys_bf16, "ys_bf16")
+    _expect(_is_bf16_bits(xs_bf16) and xs_bf16.numel() == seq * k_cols, "xs_bf16 [seq, k_cols] bf16")
+    _expect(_is_bf16_bits(ys_bf16) and ys_bf16.numel() == seq * n_rows, "ys_bf16 [seq, n_rows] bf16")
+    L = _layout(n_rows, k_cols, group_size, scale_dtype)
+    check("cascadia_int4_gemm_bf16", lib().cascadia_int4_gemm_bf16(
+        C.byref(L), packed.data_ptr(), scale_bits.data_ptr(), xs_bf16.data_ptr(), seq,
+        ys_bf16.data_ptr(), _stream()))
+    return ys_bf16
+
+
+# ---------------------------------------------------------------------------
+# expert FFN
+# ---------------------------------------------------------------------------
+
+def expert_bytes(hidden: int, inter: int, group_size: int = GROUP_SIZE) -> int:
+    return int(lib().cascadia_int4_expert_bytes(hidden, inter, group_size))
+
+
+class ExpertWeights:
+    """One expert's flat blob in HBM with the six slice accessors of
+    format.rs:51-126 (any hidden / inter / group size)."""
+
+    def __init__(self, flat: torch.Tensor, hidden: int, inter: int, group_size: int = GROUP_SIZE,
+                 scale_dtype: int = SCALE_BF16):
+        _dev(flat, "flat")
+        _expect(flat.dtype == torch.uint8, "flat must be uint8")
+        _expect(flat.numel() >= expert_bytes(hidden, inter, group_size),
+                f"flat expert too small: {flat.numel()} < {expert_bytes(hidden, inter, group_size)}")
+        self.flat, self.hidden, self.inter = flat, hidden, inter
+        self.group_size, self.scale_dtype = group_size, scale_dtype
+        gp, gs = inter * hidden // 2, inter * (hidden // group_size) * 2
+        dp, ds = hidden * inter // 2, hidden * (inter // group_size) * 2
+        o = [0, gp, gp + gs, 2 * gp + gs, 2 * (gp + gs), 2 * (gp + gs) + dp]
+        sz = [gp, gs, gp, gs, dp, ds]
+        self._slices = [flat[a:a + n] for a, n in zip(o, sz)]
+
+    def gate_packed_bytes(self): return self._slices[0]
+    def gate_scale_bits(self): return self._slices[1]
+    def up_packed_bytes(self): return self._slices[2]
+    def up_scale_bits(self): return self._slices[3]
+    def down_packed_bytes(self): return self._slices[4]
+    def down_scale_bits(self): return self._slices[5]
+
+    def slices(self):
+        return tuple(self._slices)
+
+
+def _expert_struct(gp, gs, up, us, dp, ds) -> Expert:
+    for t, n in zip((gp, gs, up, us, dp, ds), ("gate_packed", "gate_scale", "up_packed",
+                                                 "up_scale", "down_packed", "down_scale")):
+        _dev(t, n)
+    return Expert(gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), dp.data_ptr(),
+                  ds.data_ptr())
+
+
+def _ffn_dims(x, gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
+              group_size, hidden=None):
+    hidden = hidden if hidden is not None else x.shape[-1]
+    _expect(hidden % group_size == 0, "hidden must be a multiple of group_size")
+    # kernel.rs:86: intermediate inferred from the gate scale length
+    inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
+    _expect(inter > 0 and inter % group_size == 0, "intermediate must be a multiple of group_size")
+    _expect(_nbytes(gate_packed) == inter * hidden // 2 and _nbytes(up_packed) == inter * hidden // 2,
+            "gate/up packed lengths must be inter*hidden/2")
+    _expect(_nbytes(up_scale) == _nbytes(gate_scale), "up_scale length must equal gate_scale")
+    _expect(_nbytes(down_packed) == hidden * inter // 2, "down packed length must be hidden*inter/2")
+    _expect(_nbytes(down_scale) == hidden * (inter // group_size) * 2, "down scale length mismatch")
+    return hidden, inter
+
+
+def gate_up_silu(x, gate_packed, gate_scale, up_packed, up_scale, inter_out,
+                 group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
+    """inter = silu(gate·x) ⊙ (up·x), f32 [n_tokens, inter] (kernel.rs:96-120).
+    x: bf16 or f32 [n_tokens, hidden]."""
+    _dev(x, "x"), _dev(inter_out, "inter_out")
+    hidden = x.shape[-1]
+    _expect(hidden % group_size == 0, "hidden must be a multiple of group_size")
+    inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
+    _expect(_nbytes(gate_packed) == inter * hidden // 2 and _nbytes(up_packed) == inter * hidden // 2
+            and _nbytes(up_scale) == _nbytes(gate_scale), "gate/up slice lengths")
+    T = x.numel() // hidden
+    _expect(inter_out.dtype == torch.float32 and inter_out.numel() == T * inter, "inter_out f32 [T, inter]")
+    xf32 = x.dtype == torch.float32
+    _expect(xf32 or _is_bf16_bits(x), "x must be f32 or bf16")
+    e = Expert(gate_packed.data_ptr(), gate_scale.data_ptr(), up_packed.data_ptr(),
+               up_scale.data_ptr(), gate_packed.data_ptr(), gate_scale.data_ptr())
+    check("cascadia_int4_gate_up_silu", lib().cascadia_int4_gate_up_silu(
+        hidden, inter, group_size, scale_dtype, C.byref(e), x.data_ptr(), 1 if xf32 else 0, T,
+        inter_out.data_ptr(), _stream()))
+    return inter_out
+
+
+def ffn_workspace_bytes(hidden, inter, n_tokens) -> int:
+    return int(lib().cascadia_int4_ffn_workspace_bytes(hidden, inter, n_tokens))
+
+
+def expert_forward(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                   down_scale, out_bf16, group_size=GROUP_SIZE, scale_dtype=SCALE_BF16,
+                   workspace=None):
+    """out = bf16(down · (silu(gate·x) ⊙ up·x)) (kernel.rs:75-136).
+    x_bf16 / out_bf16: bf16 [hidden] or [n_tokens, hidden] (rows independent)."""
+    _dev(x_bf16, "x_bf16"), _dev(out_bf16, "out_bf16")
+    _expect(_is_bf16_bits(x_bf16) and _is_bf16_bits(out_bf16), "x and out must be bf16")
+    hidden, inter = _ffn_dims(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                              down_scale, group_size)
+    T = x_bf16.numel() // hidden
+    _expect(x_bf16.numel() == T * hidden and out_bf16.numel() == T * hidden,
+            "x and out must both be [n_tokens, hidden]")
+    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale)
+    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
+    check("cascadia_int4_expert_forward", lib().cascadia_int4_expert_forward(
+        hidden, inter, group_size, scale_dtype, C.byref(e), x_bf16.data_ptr(), T,
+        out_bf16.data_ptr(), ws, _stream()))
+    return out_bf16
+
+
+def expert_forward_sparse(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                          down_scale, out_bf16, threshold, group_size=GROUP_SIZE,
+                          scale_dtype=SCALE_BF16):
+    """ffn_sparsity.rs:756-783.  threshold <= 0 is expert_forward (returns 1.0)."""
+    if threshold > 0.0:
+        raise NotImplementedError("activation-sparse (tau > 0) expert path is not built yet")
+    expert_forward(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                   down_scale, out_bf16, group_size, scale_dtype)
+    return 1.0
+
+
+def ffn_forward_sparse_f32(x_f32, hidden, intermediate, gate_packed, gate_scale, up_packed,
+                           up_scale, down_packed, down_scale, out_f32, threshold,
+                           group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, workspace=None):
+    """Dense SwiGLU FFN, f32 in/out (ffn_sparsity.rs:373-496 at tau = 0).
+    x_f32 / out_f32: [hidden] or [n_tokens, hidden].  Returns the active
+    fraction (1.0)."""
+    if threshold > 0.0:
+        raise NotImplementedError("activation-sparse (tau > 0) FFN path is not built yet")
+    _dev(x_f32, "x_f32"), _dev(out_f32, "out_f32")
+    _expect(x_f32.dtype == torch.float32 and out_f32.dtype == torch.float32, "f32 in/out")
+    h, inter = _ffn_dims(x_f32, gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                         down_scale, group_size, hidden)
+    _expect(inter == intermediate, f"intermediate {intermediate} != {inter} implied by gate_scale")
+    T = x_f32.numel() // hidden
+    _expect(x_f32.numel() == T * hidden and out_f32.numel() == T * hidden, "[n_tokens, hidden]")
+    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale)
+    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
+    check("cascadia_int4_ffn_forward_f32", lib().cascadia_int4_ffn_forward_f32(
+        hidden, inter, group_size, scale_dtype, C.byref(e), x_f32.data_ptr(), T,
+        out_f32.data_ptr(), ws, _stream()))
+    return 1.0
+
+
+# ---------------------------------------------------------------------------
+# debug / synthetic data
+# ---------------------------------------------------------------------------
+
+def debug_dequant(packed, scale_bits, n_rows, k_cols, group_size=GROUP_SIZE,
+                  scale_dtype=SCALE_BF16, out=None):
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    if out is None:
+        out = torch.empty((n_rows, k_cols), dtype=torch.float32, device=packed.device)
+    L = _layout(n_rows, k_cols, group_size, scale_dtype)
+    check("cascadia_int4_debug_dequant", lib().cascadia_int4_debug_dequant(
+        C.byref(L), packed.data_ptr(), scale_bits.data_ptr(), out.data_ptr(), _stream()))
+    return out
+
+
+def fill_bytes(out: torch.Tensor, seed: int, stream_id: int):
+    _dev(out, "out")
+    check("cascadia_int4_fill_synthetic", lib().cascadia_int4_fill_synthetic(
+        0, seed, stream_id, _nbytes(out), 0.0, 0.0, 0, out.data_ptr(), _stream()))
+    return out
+
+
+def fill_scales(out: torch.Tensor, seed: int, stream_id: int, scale_dtype=SCALE_F16,
+                sigma=0.02, offset=1e-3):
+    _dev(out, "out")
+    check("cascadia_int4_fill_synthetic", lib().cascadia_int4_fill_synthetic(
+        1, seed, stream_id, _nbytes(out) // 2, sigma, offset, scale_dtype, out.data_ptr(),
+        _stream()))
+    return out
+
+
+def fill_normal(out: torch.Tensor, seed: int, stream_id: int):
+    """f32 or bf16 N(0, 1)."""
+    _dev(out, "out")
+    kind = 2 if out.dtype == torch.float32 else 3
+    n = out.numel()
+    check("cascadia_int4_fill_synthetic", lib().cascadia_int4_fill_synthetic(
+        kind, seed, stream_id, n, 0.0, 0.0, 0, out.data_ptr(), _stream()))
+    return out

@@ -1,0 +1,299 @@
+// abi.hip -- the extern "C" boundary (include/cascadia_int4.h).
+//
+// Argument validation mirrors the crate's assert_eq! length checks
+// (kernel.rs:39-43, kernel_avx512_multi.rs:75-80) but returns
+// CASCADIA_INT4_ERR_ARG instead of panicking; nothing throws across the ABI.
+#include <mutex>
+#include <new>
+
+#include "../../include/cascadia_int4.h"
+#include "int4_common.hpp"
+#include "skinny.hpp"
+#include "synth.hpp"
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+  int num_cus = 0;
+  void *ws = nullptr;  // library-owned workspace (grow-only)
+  size_t ws_bytes = 0;
+};
+
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+
+int current_device(int *dev) {
+  if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kMaxDevices)
+    return CASCADIA_INT4_ERR_DEVICE;
+  return CASCADIA_INT4_OK;
+}
+
+int num_cus(int dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState &d = g_dev[dev];
+  if (d.num_cus == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    d.num_cus = n;
+  }
+  return d.num_cus;
+}
+
+// Library workspace of at least `bytes` on the current device.
+int lib_workspace(int dev, size_t bytes, void **out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState &d = g_dev[dev];
+  if (d.ws_bytes < bytes) {
+    if (d.ws) {
+      if (hipDeviceSynchronize() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+      (void)hipFree(d.ws);
+      d.ws = nullptr;
+      d.ws_bytes = 0;
+    }
+    size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
+    if (hipMalloc(&d.ws, sz) != hipSuccess) {
+      d.ws = nullptr;
+      return CASCADIA_INT4_ERR_NOMEM;
+    }
+    d.ws_bytes = sz;
+  }
+  *out = d.ws;
+  return CASCADIA_INT4_OK;
+}
+
+inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_layout(const cascadia_int4_layout *L) {
+  if (!L) return CASCADIA_INT4_ERR_NULL;
+  if (L->n_rows == 0 || L->k_cols == 0 || L->group_size == 0) return CASCADIA_INT4_ERR_ARG;
+  if (L->group_size % 32 != 0 || L->k_cols % L->group_size != 0) return CASCADIA_INT4_ERR_ARG;
+  if (L->scale_dtype > CASCADIA_INT4_SCALE_F16) return CASCADIA_INT4_ERR_ARG;
+  if (L->n_rows > (1u << 30) || L->k_cols > (1u << 30)) return CASCADIA_INT4_ERR_ARG;
+  return CASCADIA_INT4_OK;
+}
+
+int check_weights(const uint8_t *packed, const uint8_t *scales) {
+  if (!packed || !scales) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(packed, 16) || !aligned(scales, 2)) return CASCADIA_INT4_ERR_ARG;
+  return CASCADIA_INT4_OK;
+}
+
+int hip_status(hipError_t e) { return e == hipSuccess ? CASCADIA_INT4_OK : CASCADIA_INT4_ERR_DEVICE; }
+
+// One skinny GEMM (any M), f32 output or fused epilogue.
+int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint8_t *s1,
+             int N, int K, int G, int sdt, const void *x, bool xf32, int M, void *out,
+             int epi, hipStream_t st) {
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  cai4::SkinnyArgs a{};
+  a.w0 = w0;
+  a.s0 = s0;
+  a.w1 = w1;
+  a.s1 = s1;
+  a.x = x;
+  a.out = out;
+  a.N = N;
+  a.K = K;
+  a.G = G;
+  a.M = M;
+  a.ldx = K;
+  a.ldo = N;
+  a.sdt = sdt;
+  const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, M, xf32, epi, num_cus(dev));
+  return hip_status(cai4::skinny_launch(a, p, xf32, epi, st));
+}
+
+void expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[6]) {
+  const size_t gp = (size_t)inter * hidden / 2, gs = (size_t)inter * (hidden / group) * 2;
+  const size_t dp = (size_t)hidden * inter / 2;
+  off[0] = 0;
+  off[1] = gp;
+  off[2] = gp + gs;
+  off[3] = 2 * gp + gs;
+  off[4] = 2 * (gp + gs);
+  off[5] = off[4] + dp;
+}
+
+int check_expert(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
+                 const cascadia_int4_expert *e) {
+  if (!e) return CASCADIA_INT4_ERR_NULL;
+  if (!e->gate_packed || !e->gate_scale || !e->up_packed || !e->up_scale || !e->down_packed ||
+      !e->down_scale)
+    return CASCADIA_INT4_ERR_NULL;
+  if (hidden == 0 || inter == 0 || group == 0 || group % 32) return CASCADIA_INT4_ERR_ARG;
+  if (hidden % group || inter % group || sdt > 1) return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(e->gate_packed, 16) || !aligned(e->up_packed, 16) ||
+      !aligned(e->down_packed, 16))
+    return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(e->gate_scale, 2) || !aligned(e->up_scale, 2) || !aligned(e->down_scale, 2))
+    return CASCADIA_INT4_ERR_ARG;
+  return CASCADIA_INT4_OK;
+}
+
+int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
+               const cascadia_int4_expert *e, const void *x, bool x_f32, uint32_t n_tokens,
+               void *out, bool out_bf16, void *workspace, hipStream_t st) {
+  if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
+  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
+  if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (!aligned(x, 16)) return CASCADIA_INT4_ERR_ARG;
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const size_t need = cascadia_int4_ffn_workspace_bytes(hidden, inter, n_tokens);
+  void *ws = workspace;
+  if (!ws) {
+    if (int rc = lib_workspace(dev, need, &ws)) return rc;
+  } else if (!aligned(ws, 16)) {
+    return CASCADIA_INT4_ERR_ARG;
+  }
+  float *inter_buf = reinterpret_cast<float *>(ws);
+  int rc = run_gemm(e->gate_packed, e->gate_scale, e->up_packed, e->up_scale, (int)inter,
+                    (int)hidden, (int)group, (int)sdt, x, x_f32, (int)n_tokens, inter_buf,
+                    cai4::EPI_SWIGLU, st);
+  if (rc) return rc;
+  return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
+                  (int)group, (int)sdt, inter_buf, true, (int)n_tokens, out,
+                  out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *cascadia_int4_version(void) { return "cascadia-int4-hip 0.1.0 (gfx950)"; }
+
+int cascadia_int4_synchronize(void *stream) {
+  return hip_status(hipStreamSynchronize((hipStream_t)stream));
+}
+
+int cascadia_int4_dequant_gemv(const cascadia_int4_layout *L, const uint8_t *packed,
+                               const uint8_t *scale_bits, const float *x, float *y,
+                               void *stream) {
+  return cascadia_int4_dequant_gemm_multi(L, packed, scale_bits, x, 1, y, stream);
+}
+
+int cascadia_int4_dequant_gemm_multi(const cascadia_int4_layout *L, const uint8_t *packed,
+                                     const uint8_t *scale_bits, const float *xs, uint32_t seq,
+                                     float *ys, void *stream) {
+  if (int rc = check_layout(L)) return rc;
+  if (int rc = check_weights(packed, scale_bits)) return rc;
+  if (!xs || !ys) return CASCADIA_INT4_ERR_NULL;
+  if (seq == 0) return CASCADIA_INT4_ERR_ARG;  // the crate asserts seq >= 1
+  if (!aligned(xs, 16) || !aligned(ys, 4)) return CASCADIA_INT4_ERR_ARG;
+  return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
+                  (int)L->group_size, (int)L->scale_dtype, xs, true, (int)seq, ys,
+                  cai4::EPI_F32, (hipStream_t)stream);
+}
+
+int cascadia_int4_dequant_gemm_bf16in(const cascadia_int4_layout *L, const uint8_t *packed,
+                                      const uint8_t *scale_bits, const uint16_t *xs_bf16,
+                                      uint32_t seq, float *ys, void *stream) {
+  if (int rc = check_layout(L)) return rc;
+  if (int rc = check_weights(packed, scale_bits)) return rc;
+  if (!xs_bf16 || !ys) return CASCADIA_INT4_ERR_NULL;
+  if (seq == 0) return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(xs_bf16, 16) || !aligned(ys, 4)) return CASCADIA_INT4_ERR_ARG;
+  return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
+                  (int)L->group_size, (int)L->scale_dtype, xs_bf16, false, (int)seq, ys,
+                  cai4::EPI_F32, (hipStream_t)stream);
+}
+
+int cascadia_int4_gemm_bf16(const cascadia_int4_layout *L, const uint8_t *packed,
+                            const uint8_t *scale_bits, const uint16_t *xs_bf16, uint32_t seq,
+                            uint16_t *ys_bf16, void *stream) {
+  if (int rc = check_layout(L)) return rc;
+  if (int rc = check_weights(packed, scale_bits)) return rc;
+  if (!xs_bf16 || !ys_bf16) return CASCADIA_INT4_ERR_NULL;
+  if (seq == 0) return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(xs_bf16, 16) || !aligned(ys_bf16, 2)) return CASCADIA_INT4_ERR_ARG;
+  return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
+                  (int)L->group_size, (int)L->scale_dtype, xs_bf16, false, (int)seq, ys_bf16,
+                  cai4::EPI_BF16, (hipStream_t)stream);
+}
+
+size_t cascadia_int4_expert_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size) {
+  if (group_size == 0) return 0;
+  size_t off[6];
+  expert_sections(hidden, inter, group_size, off);
+  return off[5] + (size_t)hidden * (inter / group_size) * 2;
+}
+
+int cascadia_int4_expert_from_flat(const uint8_t *flat, uint32_t hidden, uint32_t inter,
+                                   uint32_t group_size, cascadia_int4_expert *out) {
+  if (!flat || !out) return CASCADIA_INT4_ERR_NULL;
+  if (group_size == 0 || group_size % 32 || hidden % group_size || inter % group_size)
+    return CASCADIA_INT4_ERR_ARG;
+  size_t off[6];
+  expert_sections(hidden, inter, group_size, off);
+  out->gate_packed = flat + off[0];
+  out->gate_scale = flat + off[1];
+  out->up_packed = flat + off[2];
+  out->up_scale = flat + off[3];
+  out->down_packed = flat + off[4];
+  out->down_scale = flat + off[5];
+  return CASCADIA_INT4_OK;
+}
+
+size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32_t n_tokens) {
+  (void)hidden;
+  return (size_t)n_tokens * inter * sizeof(float);
+}
+
+int cascadia_int4_expert_forward(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                 uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                 const uint16_t *x_bf16, uint32_t n_tokens, uint16_t *out_bf16,
+                                 void *workspace, void *stream) {
+  return ffn_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false,
+                    n_tokens, out_bf16, true, workspace, (hipStream_t)stream);
+}
+
+int cascadia_int4_ffn_forward_f32(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                  uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                  const float *x, uint32_t n_tokens, float *out,
+                                  void *workspace, void *stream) {
+  return ffn_common(hidden, inter, group_size, scale_dtype, expert, x, true, n_tokens, out,
+                    false, workspace, (hipStream_t)stream);
+}
+
+int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                               uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                               const void *x, uint32_t x_is_f32, uint32_t n_tokens,
+                               float *inter_out, void *stream) {
+  if (int rc = check_expert(hidden, inter, group_size, scale_dtype, expert)) return rc;
+  if (!x || !inter_out) return CASCADIA_INT4_ERR_NULL;
+  if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (!aligned(x, 16) || !aligned(inter_out, 4)) return CASCADIA_INT4_ERR_ARG;
+  return run_gemm(expert->gate_packed, expert->gate_scale, expert->up_packed, expert->up_scale,
+                  (int)inter, (int)hidden, (int)group_size, (int)scale_dtype, x, x_is_f32 != 0,
+                  (int)n_tokens, inter_out, cai4::EPI_SWIGLU, (hipStream_t)stream);
+}
+
+int cascadia_int4_debug_dequant(const cascadia_int4_layout *L, const uint8_t *packed,
+                                const uint8_t *scale_bits, float *w_out, void *stream) {
+  if (int rc = check_layout(L)) return rc;
+  if (!packed || !scale_bits || !w_out) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(packed, 4) || !aligned(scale_bits, 2) || !aligned(w_out, 4))
+    return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::debug_dequant(packed, scale_bits, (int)L->n_rows, (int)L->k_cols,
+                                        (int)L->group_size, (int)L->scale_dtype, w_out,
+                                        (hipStream_t)stream));
+}
+
+int cascadia_int4_fill_synthetic(uint32_t kind, uint64_t seed, uint64_t stream_id, size_t n,
+                                 double p0, double p1, uint32_t dtype, void *out,
+                                 void *stream) {
+  if (!out) return CASCADIA_INT4_ERR_NULL;
+  if (kind > 3 || dtype > 1) return CASCADIA_INT4_ERR_ARG;
+  if (kind == 0 && !aligned(out, 8)) return CASCADIA_INT4_ERR_ARG;
+  if (kind == 2 && !aligned(out, 4)) return CASCADIA_INT4_ERR_ARG;
+  if ((kind == 1 || kind == 3) && !aligned(out, 2)) return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::fill_synthetic((int)kind, seed, stream_id, n, p0, p1, (int)dtype, out,
+                                         (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,168 @@
+/*
+ * cascadia_int4.h -- C ABI of libcascadia_int4_hip.so, the MI355X (gfx950)
+ * implementation of cascadia-int4-gemm's INT4 weight-only matmul path.
+ *
+ * Drop-in boundary.  Every entry point below replaces one function of the
+ * reference crate (labscommunity/cascadia, crates/cascadia-int4-gemm) and
+ * cites it.  Differences a caller must know:
+ *   - Weight, activation and output pointers are DEVICE pointers (HBM).  The
+ *     weights stay resident; nothing is copied per call.  The byte layout is
+ *     the crate's, unchanged (src/format.rs:3-17, src/kernel.rs:3-13).
+ *   - The crate hard-codes group 32 / bf16 scales (src/lib.rs:73); here the
+ *     layout carries the group size G (a multiple of 32 dividing K) and the
+ *     scale dtype (bf16 = the crate's, or fp16).
+ *   - Length mismatches panic in the crate (assert_eq!, kernel.rs:39-43);
+ *     here they return CASCADIA_INT4_ERR_ARG.  No abort or exception ever
+ *     crosses this ABI.
+ *   - Calls are enqueued on `stream` (a hipStream_t; NULL = the null stream)
+ *     and return without waiting; outputs are complete once the stream is
+ *     synchronised (cascadia_int4_synchronize).  The crate's calls are
+ *     synchronous; a caller that needs that calls cascadia_int4_synchronize.
+ *   - Outputs are fully overwritten, as in the crate.  Calls are reentrant
+ *     for distinct output buffers; a shared workspace (workspace == NULL, the
+ *     library's own) makes concurrent calls on different streams race.
+ */
+#ifndef CASCADIA_INT4_H
+#define CASCADIA_INT4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes (c_ffi.rs returns 0 / -1 / -2 / -3 for its own calls). */
+#define CASCADIA_INT4_OK 0
+#define CASCADIA_INT4_ERR_NULL (-1)   /* a required pointer is NULL */
+#define CASCADIA_INT4_ERR_ARG (-2)    /* shape / length / alignment invalid */
+#define CASCADIA_INT4_ERR_DEVICE (-3) /* HIP runtime error, or I/O error on open */
+#define CASCADIA_INT4_ERR_NOMEM (-4)  /* device allocation failed */
+
+#define CASCADIA_INT4_SCALE_BF16 0u /* the crate's format (format.rs:16-17) */
+#define CASCADIA_INT4_SCALE_F16 1u
+
+/* Routing rules for the MoE entry point. */
+#define CASCADIA_INT4_ROUTE_IDS 0u          /* caller supplies ids/weights */
+#define CASCADIA_INT4_ROUTE_SIGMOID_BIAS 1u /* shell_int4.rs:588-620 / glm/gate.rs:24-62 */
+#define CASCADIA_INT4_ROUTE_SOFTMAX_TOPK 2u /* softmax over the top-k logits */
+
+/* One packed INT4 matrix: packed u8 [n_rows, k_cols/2] (byte i of a row =
+ * column 2i in the low nibble, 2i+1 in the high nibble, q = nibble - 8) and
+ * scale_bits u16 LE [n_rows, k_cols/group_size].  w = f32(q) * f32(scale). */
+typedef struct cascadia_int4_layout {
+  uint32_t n_rows;      /* N, output rows */
+  uint32_t k_cols;      /* K, a multiple of group_size */
+  uint32_t group_size;  /* G, a multiple of 32 (the crate: 32) */
+  uint32_t scale_dtype; /* CASCADIA_INT4_SCALE_BF16 or _F16 */
+} cascadia_int4_layout;
+
+/* Library version string. */
+const char *cascadia_int4_version(void);
+
+/* Wait for all work enqueued on `stream`. */
+int cascadia_int4_synchronize(void *stream);
+
+/* y[r] = sum_c (nibble[r,c]-8) * scale[r, c/G] * x[c] for one f32 vector.
+ * Replaces dequant_gemv_int4 (src/kernel.rs:31-71) and
+ * dequant_gemv_int4_auto (src/kernel_avx512.rs:274-297).
+ * x: f32 [k_cols], y: f32 [n_rows]. */
+int cascadia_int4_dequant_gemv(const cascadia_int4_layout *layout, const uint8_t *packed,
+                               const uint8_t *scale_bits, const float *x, float *y,
+                               void *stream);
+
+/* ys[t*n_rows + r] for t < seq, f32 activations xs [seq, k_cols].
+ * Replaces dequant_gemm_int4_multi_auto (src/kernel_avx512_multi.rs:207-245)
+ * and dequant_gemm_int4_multi_blocked_auto
+ * (src/kernel_avx512_multi_blocked.rs:295-347); any seq >= 1. */
+int cascadia_int4_dequant_gemm_multi(const cascadia_int4_layout *layout,
+                                     const uint8_t *packed, const uint8_t *scale_bits,
+                                     const float *xs, uint32_t seq, float *ys, void *stream);
+
+/* As cascadia_int4_dequant_gemm_multi with bf16 activations (exact in the
+ * MFMA): xs_bf16 [seq, k_cols] bf16 bits, ys f32 [seq, n_rows].  The crate
+ * converts bf16 -> f32 before its GEMV (kernel.rs:89-93); same values. */
+int cascadia_int4_dequant_gemm_bf16in(const cascadia_int4_layout *layout,
+                                      const uint8_t *packed, const uint8_t *scale_bits,
+                                      const uint16_t *xs_bf16, uint32_t seq, float *ys,
+                                      void *stream);
+
+/* Prefill GEMM, bf16 activations -> bf16 output (f32 accumulation, one RNE
+ * rounding): ys_bf16[t*n_rows + r].  For seq > 64 the crate runs the
+ * per-token GEMV loop (kernel_avx512_multi.rs:240-244); same contract. */
+int cascadia_int4_gemm_bf16(const cascadia_int4_layout *layout, const uint8_t *packed,
+                            const uint8_t *scale_bits, const uint16_t *xs_bf16, uint32_t seq,
+                            uint16_t *ys_bf16, void *stream);
+
+/* One expert's six weight slices (device pointers), as expert_forward takes
+ * them (src/kernel.rs:75-84): gate/up are [inter, hidden], down is
+ * [hidden, inter], each packed u8 + scale u16 in the layout above.  Packed
+ * slices must be 16-byte aligned, scale slices 2-byte aligned. */
+typedef struct cascadia_int4_expert {
+  const uint8_t *gate_packed;
+  const uint8_t *gate_scale;
+  const uint8_t *up_packed;
+  const uint8_t *up_scale;
+  const uint8_t *down_packed;
+  const uint8_t *down_scale;
+} cascadia_int4_expert;
+
+/* Size in bytes of one flat expert blob: gate_p, gate_s, up_p, up_s, down_p,
+ * down_s contiguous (format.rs:35-47 / ov_moe.rs:792-806, any dims/G). */
+size_t cascadia_int4_expert_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size);
+
+/* Fill *out with the six slices of a flat expert blob at `flat`
+ * (the slicing of ov_moe.rs:792-806 / format.rs:63-96). */
+int cascadia_int4_expert_from_flat(const uint8_t *flat, uint32_t hidden, uint32_t inter,
+                                   uint32_t group_size, cascadia_int4_expert *out);
+
+/* Workspace bytes the expert / FFN entry points need for n_tokens rows. */
+size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32_t n_tokens);
+
+/* expert_forward for n_tokens independent rows: out = bf16(W_d ·
+ * (silu(W_g·x) ⊙ (W_u·x))) with x bf16, everything inside f32, one RNE
+ * rounding of the output (src/kernel.rs:75-136; ffn_sparsity.rs:756 at
+ * tau = 0).  x_bf16, out_bf16: [n_tokens, hidden] bf16 bits.  workspace:
+ * >= cascadia_int4_ffn_workspace_bytes bytes, 16-byte aligned, or NULL to use
+ * the library's per-device buffer. */
+int cascadia_int4_expert_forward(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                 uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                 const uint16_t *x_bf16, uint32_t n_tokens, uint16_t *out_bf16,
+                                 void *workspace, void *stream);
+
+/* First half of the expert FFN: inter[t, i] = silu(W_g·x_t)[i] * (W_u·x_t)[i]
+ * in f32 (kernel.rs:96-120; the batched gate/up + swiglu_mul of
+ * shell_int4.rs:1112-1130).  x: [n_tokens, hidden], bf16 bits when x_is_f32
+ * is 0, else f32.  inter_out: f32 [n_tokens, inter].  Only the gate/up
+ * slices of *expert are read. */
+int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                               uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                               const void *x, uint32_t x_is_f32, uint32_t n_tokens,
+                               float *inter_out, void *stream);
+
+/* Dense SwiGLU FFN, f32 in / f32 out, no rounding: ffn_forward_sparse_f32 at
+ * tau = 0 (src/ffn_sparsity.rs:373-496), used for the shared expert
+ * (shell_int4.rs:629).  x, out: [n_tokens, hidden] f32. */
+int cascadia_int4_ffn_forward_f32(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                  uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                  const float *x, uint32_t n_tokens, float *out,
+                                  void *workspace, void *stream);
+
+/* Dequantise to f32 [n_rows, k_cols] (bit-exact w = q*s; the kernel's own
+ * decode path).  No crate counterpart; the parity check of the weights. */
+int cascadia_int4_debug_dequant(const cascadia_int4_layout *layout, const uint8_t *packed,
+                                const uint8_t *scale_bits, float *w_out, void *stream);
+
+/* Seeded synthetic data, the same generator as the test oracle.
+ * kind 0: bytes (uniform nibbles), n = byte count, out u8.
+ * kind 1: scales fp16/bf16(|N(0,sigma)| + offset), n = count, out u16
+ *         (p0 = sigma, p1 = offset, dtype = scale dtype).
+ * kind 2: f32 N(0,1), out f32.   kind 3: bf16 N(0,1), out u16. */
+int cascadia_int4_fill_synthetic(uint32_t kind, uint64_t seed, uint64_t stream_id, size_t n,
+                                 double p0, double p1, uint32_t dtype, void *out,
+                                 void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CASCADIA_INT4_H */

@@ -1,0 +1,85 @@
+"""The C-ABI library loads and exports every symbol include/*.h declares; the
+host-only entry points (no GPU work) behave as documented."""
+import ctypes as C
+import glob
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def header_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        src = open(h).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        for m in re.finditer(r"\b(cascadia_int4_[a-z0-9_]+)\s*\(", src):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def cl():
+    import cascadia_amd
+
+    return cascadia_amd
+
+
+def test_library_exports_every_declared_symbol(cl):
+    names = header_functions()
+    assert len(names) >= 10
+    L = C.CDLL(cl.LIB_PATH)
+    missing = [n for n in sorted(names) if not hasattr(L, n)]
+    assert not missing, missing
+    # and the ctypes signature table covers exactly the header
+    assert set(cl.SIGNATURES) == names
+
+
+def test_version(cl):
+    assert b"gfx950" in cl.lib().cascadia_int4_version()
+
+
+def test_expert_bytes_matches_oracle(cl, orc):
+    for h, i, g in [(7168, 2048, 32), (3072, 1536, 128), (4096, 14336, 128), (64, 32, 32)]:
+        assert cl.expert_bytes(h, i, g) == orc.expert_bytes(h, i, g)
+    assert cl.expert_bytes(7168, 2048, 32) == 2 * (2048 * 3584 + 2048 * 224 * 2) + 7168 * 1024 + 7168 * 64 * 2
+
+
+def test_expert_from_flat_offsets(cl, orc):
+    e = cl._lib.Expert()
+    base = 1 << 20
+    rc = cl.lib().cascadia_int4_expert_from_flat(base, 64, 32, 32, C.byref(e))
+    assert rc == 0
+    offs, _ = orc.expert_offsets(64, 32, 32)
+    got = [e.gate_packed, e.gate_scale, e.up_packed, e.up_scale, e.down_packed, e.down_scale]
+    assert [g - base for g in got] == offs
+    assert cl.lib().cascadia_int4_expert_from_flat(base, 64, 32, 48, C.byref(e)) == cl._lib.ERR_ARG
+    assert cl.lib().cascadia_int4_expert_from_flat(None, 64, 32, 32, C.byref(e)) == cl._lib.ERR_NULL
+
+
+def test_argument_errors_before_device_work(cl):
+    L = cl.lib()
+    lay = cl._lib.Layout(64, 128, 32, 0)
+    # NULL layout / NULL weights
+    assert L.cascadia_int4_dequant_gemv(None, 16, 16, 16, 16, None) == cl._lib.ERR_NULL
+    assert L.cascadia_int4_dequant_gemv(C.byref(lay), None, 16, 16, 16, None) == cl._lib.ERR_NULL
+    # group not a multiple of 32, K not a multiple of G, bad scale dtype, seq 0
+    for bad in [cl._lib.Layout(64, 128, 48, 0), cl._lib.Layout(64, 100, 32, 0),
+                cl._lib.Layout(64, 128, 32, 7), cl._lib.Layout(0, 128, 32, 0)]:
+        assert L.cascadia_int4_dequant_gemv(C.byref(bad), 16, 16, 16, 16, None) == cl._lib.ERR_ARG
+    assert L.cascadia_int4_dequant_gemm_multi(C.byref(lay), 16, 16, 16, 0, 16, None) == cl._lib.ERR_ARG
+    # misaligned packed pointer
+    assert L.cascadia_int4_dequant_gemv(C.byref(lay), 17, 16, 16, 16, None) == cl._lib.ERR_ARG
+    assert L.cascadia_int4_fill_synthetic(9, 0, 0, 16, 0.0, 0.0, 0, 16, None) == cl._lib.ERR_ARG
+    assert L.cascadia_int4_expert_forward(64, 32, 32, 0, None, 16, 1, 16, None, None) == cl._lib.ERR_NULL
+
+
+def test_python_mirror_rejects_host_tensors(cl):
+    import torch
+
+    p = torch.zeros(64 * 64, dtype=torch.uint8)
+    s = torch.zeros(64 * 2 * 2, dtype=torch.uint8)
+    with pytest.raises(ValueError):
+        cl.dequant_gemv_int4(p, s, torch.zeros(128), 64, 128, torch.zeros(64))

@@ -1,0 +1,222 @@
+"""GPU parity: the HIP kernels, called through the C ABI (via the Python
+mirror), against the CPU oracle on the same seeded inputs.
+
+Bars (north star): f32 outputs rel-L2 <= 1e-3 and max-abs <= 2e-2 against the
+fp32-accumulated oracle; dequantised weights bit-exact; integer/byte work
+bit-exact.  bf16 outputs are compared with the oracle rounded at the crate's
+own rounding point (kernel.rs:133-135): rel-L2 <= 1e-3 and every element
+within one bf16 ulp of the oracle's bf16 value (a last-place rounding flip
+when the two f32 sums straddle a rounding boundary is the only allowed
+difference; an absolute bar is meaningless at |y| >> 1 where one ulp > 2e-2).
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, MAX_ABS_TOL, REL_L2_TOL, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+BF16, F16 = 0, 1
+
+
+@pytest.fixture(scope="module")
+def cl():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import cascadia_amd
+
+    return cascadia_amd
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def weights(orc, n, k, group, sdt, seed):
+    packed = orc.fill_bytes(seed, 11, n * k // 2)
+    scales = orc.fill_scales(seed, 12, n * (k // group), sdt).view(np.uint8).copy()
+    return packed, scales
+
+
+def bf16_ulp(v_bf16_bits):
+    f = np.abs((v_bf16_bits.astype(np.uint32) << 16).view(np.float32)).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(f, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def assert_f32_close(got, want, what=""):
+    r, m = rel_l2(got, want), max_abs(got, want)
+    assert r <= REL_L2_TOL and m <= MAX_ABS_TOL, f"{what}: rel_l2={r:.3g} max_abs={m:.3g}"
+
+
+def assert_bf16_close(got_bits, want_bits, what=""):
+    g = (got_bits.astype(np.uint32) << 16).view(np.float32)
+    w = (want_bits.astype(np.uint32) << 16).view(np.float32)
+    r = rel_l2(g, w)
+    d = np.abs(g.astype(np.float64) - w.astype(np.float64))
+    ulp = bf16_ulp(want_bits)
+    worst = float(np.max(d / ulp)) if d.size else 0.0
+    assert r <= REL_L2_TOL and worst <= 1.0, f"{what}: rel_l2={r:.3g} worst={worst:.2f} ulp"
+
+
+# ----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("group,sdt", [(32, BF16), (32, F16), (128, F16), (64, BF16)])
+def test_debug_dequant_bit_exact(cl, orc, group, sdt):
+    n, k = 96, 1024
+    packed, scales = weights(orc, n, k, group, sdt, 3)
+    got = host(cl.debug_dequant(dev(packed), dev(scales), n, k, group, sdt))
+    want = orc.dequant(packed, scales, n, k, group, sdt)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_synthetic_generators_match_oracle(cl, orc):
+    t = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    assert np.array_equal(host(cl.fill_bytes(t, 5, 7)), orc.fill_bytes(5, 7, 1 << 20))
+    t = torch.empty(333, dtype=torch.uint8, device="cuda")  # ragged tail
+    assert np.array_equal(host(cl.fill_bytes(t, 5, 7)), orc.fill_bytes(5, 7, 333))
+    s = torch.empty(100000, dtype=torch.int16, device="cuda")
+    g = host(cl.fill_scales(s, 5, 8, F16)).view(np.uint16)
+    w = orc.fill_scales(5, 8, 100000, F16)
+    assert np.mean(g == w) > 0.9999 and np.max(np.abs(g.astype(int) - w.astype(int))) <= 1
+    x = torch.empty(100000, dtype=torch.float32, device="cuda")
+    assert rel_l2(host(cl.fill_normal(x, 5, 9)), orc.fill_normal_f32(5, 9, 100000)) < 1e-6
+
+
+def test_gemv_config0(cl, orc):
+    """Config 0: 4096x4096, G128, fp16 scales, x f32 N(0,1) seed 0."""
+    n = k = 4096
+    packed, scales = weights(orc, n, k, 128, F16, 0)
+    x = orc.fill_normal_f32(0, 13, k)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    cl.dequant_gemv_int4(dev(packed), dev(scales), dev(x), n, k, y, group_size=128, scale_dtype=F16)
+    want = orc.gemv(packed, scales, x, n, k, 128, F16)
+    assert_f32_close(host(y), want, "gemv config0")
+
+
+SHAPES = [  # n, k, group, sdt, seq
+    (64, 128, 32, BF16, 1), (96, 1536, 32, BF16, 8), (50, 256, 64, F16, 3),
+    (130, 384, 128, F16, 17), (33, 96, 32, BF16, 5), (64, 4096, 128, F16, 64),
+    (40, 512, 128, F16, 65), (17, 160, 32, F16, 2), (256, 2048, 32, F16, 16),
+    (7, 32, 32, BF16, 9), (300, 7168, 32, F16, 1),
+]
+
+
+@pytest.mark.parametrize("n,k,group,sdt,seq", SHAPES)
+def test_gemm_multi_f32_and_bf16_inputs(cl, orc, n, k, group, sdt, seq):
+    packed, scales = weights(orc, n, k, group, sdt, n + k + seq)
+    xs = orc.fill_normal_f32(seq, 14, seq * k)
+    ys = torch.empty(seq * n, dtype=torch.float32, device="cuda")
+    cl.dequant_gemm_int4_multi_auto(dev(packed), dev(scales), dev(xs), n, k, seq, ys,
+                                    group_size=group, scale_dtype=sdt)
+    want = orc.gemm_multi(packed, scales, xs, n, k, seq, group, sdt)
+    assert_f32_close(host(ys).reshape(seq, n), want, f"f32 in {n}x{k} G{group} seq{seq}")
+    # bf16 activations (exact in the MFMA)
+    xb = orc.f32_to_bf16(xs)
+    cl.dequant_gemm_int4_multi_auto(dev(packed), dev(scales), dev(xb.view(np.int16)), n, k, seq,
+                                    ys, group_size=group, scale_dtype=sdt)
+    want_b = orc.gemm_multi(packed, scales, orc.bf16_to_f32(xb), n, k, seq, group, sdt)
+    assert_f32_close(host(ys).reshape(seq, n), want_b, f"bf16 in {n}x{k} G{group} seq{seq}")
+
+
+def test_crate_generator_known_layout(cl, orc):
+    """The crate's own multi-token test generator (kernel_avx512_multi.rs:255-291)."""
+    from test_oracle import ref_make_test_data
+
+    for n, k, seq in [(64, 128, 1), (64, 128, 4), (96, 1536, 8)]:
+        packed, scales, xs = ref_make_test_data(n, k, seq)
+        ys = torch.empty(seq * n, dtype=torch.float32, device="cuda")
+        cl.dequant_gemm_int4_multi_auto(dev(packed), dev(scales), dev(xs), n, k, seq, ys)
+        want = orc.gemm_multi(packed, scales, xs, n, k, seq, 32, BF16)
+        assert_f32_close(host(ys).reshape(seq, n), want, f"crate gen {n}x{k} seq{seq}")
+
+
+def test_zero_and_one_hot_weights(cl, orc):
+    """kernel.rs:144-181 known answers on the GPU."""
+    n, k = 4, 32
+    packed = np.full(n * k // 2, 0x88, np.uint8)
+    scales = np.tile(np.array([0x80, 0x3F], np.uint8), n)
+    x = np.arange(k, dtype=np.float32) * np.float32(0.1)
+    y = torch.full((n,), 999.0, device="cuda")
+    cl.dequant_gemv_int4(dev(packed), dev(scales), dev(x), n, k, y)
+    assert np.all(np.abs(host(y)) < 1e-6)
+    packed[0] = 0x89
+    x = np.arange(k, dtype=np.float32) + 1
+    cl.dequant_gemv_int4(dev(packed), dev(scales), dev(x), n, k, y)
+    assert abs(host(y)[0] - 1.0) < 1e-5 and np.all(host(y)[1:] == 0)
+
+
+def fixture_experts():
+    out = []
+    for d, h, i in [("dsv4_layer_00", 64, 32), ("dsv4_layer_01", 64, 32), ("glm5_layer_01", 32, 32)]:
+        for f in sorted(glob.glob(os.path.join(GOLDEN, "fixture_experts", d, "*.bin"))):
+            out.append((f, h, i))
+    return out
+
+
+def test_expert_forward_fixture_bins(cl, orc):
+    """Every reference fixture expert, 5 tokens each, vs the oracle."""
+    rng = np.random.default_rng(21)
+    for f, h, i in fixture_experts():
+        flat = np.fromfile(f, np.uint8)
+        W = cl.ExpertWeights(dev(flat), h, i, 32, BF16)
+        T = 5
+        xb = orc.f32_to_bf16(rng.normal(0, 1, (T, h)).astype(np.float32))
+        out = torch.empty(T * h, dtype=torch.int16, device="cuda")
+        cl.expert_forward(dev(xb.view(np.int16)), *W.slices(), out)
+        got = host(out).view(np.uint16).reshape(T, h)
+        want = np.stack([orc.expert_forward(xb[t], flat, h, i, 32, BF16) for t in range(T)])
+        assert_bf16_close(got, want, os.path.basename(f))
+        # shared-expert form: f32 in / f32 out
+        xf = orc.bf16_to_f32(xb)
+        o32 = torch.empty(T * h, dtype=torch.float32, device="cuda")
+        cl.ffn_forward_sparse_f32(dev(xf), h, i, *W.slices(), o32, 0.0)
+        want32 = np.stack([orc.ffn_forward_f32(xf[t], flat, h, i, 32, BF16)[0] for t in range(T)])
+        assert_f32_close(host(o32).reshape(T, h), want32, os.path.basename(f) + " f32")
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_expert_forward_config1_llama_ffn(cl, orc, M):
+    """Config 1: Llama-3-8B FFN, H 4096, I 14336, G128 fp16, bf16 x, M tokens."""
+    h, i, g = 4096, 14336, 128
+    nbytes = orc.expert_bytes(h, i, g)
+    flat = orc.fill_bytes(1, 21, nbytes)
+    offs, sizes = orc.expert_offsets(h, i, g)
+    for s in (1, 3, 5):  # scale sections
+        flat[offs[s]:offs[s] + sizes[s]] = orc.fill_scales(1, 30 + s, sizes[s] // 2, F16).view(np.uint8)
+    xb = orc.fill_normal_bf16(M, 22, M * h)
+    W = cl.ExpertWeights(dev(flat), h, i, g, F16)
+    out = torch.empty(M * h, dtype=torch.int16, device="cuda")
+    cl.expert_forward(dev(xb.view(np.int16)), *W.slices(), out, group_size=g, scale_dtype=F16)
+    got = host(out).view(np.uint16).reshape(M, h)
+    want = orc.cpu_expert_forward(xb, M, flat, h, i, g, F16)
+    assert_bf16_close(got, want, f"config1 M={M}")
+
+
+def test_prefill_gemm_bf16_small(cl, orc):
+    n, k, m, g = 192, 1024, 100, 128
+    packed, scales = weights(orc, n, k, g, F16, 31)
+    xb = orc.fill_normal_bf16(3, 32, m * k)
+    ys = torch.empty(m * n, dtype=torch.int16, device="cuda")
+    cl.gemm_int4_bf16(dev(packed), dev(scales), dev(xb.view(np.int16)), n, k, m, ys, group_size=g,
+                      scale_dtype=F16)
+    want = orc.f32_to_bf16(orc.gemm_multi(packed, scales, orc.bf16_to_f32(xb), n, k, m, g, F16))
+    assert_bf16_close(host(ys).view(np.uint16).reshape(m, n), want, "prefill small")
+
+
+def test_length_mismatch_raises(cl, orc):
+    packed, scales = weights(orc, 64, 128, 32, BF16, 1)
+    y = torch.empty(64, dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError):
+        cl.dequant_gemv_int4(dev(packed[:-1]), dev(scales), dev(np.zeros(128, np.float32)), 64, 128, y)
+    with pytest.raises(ValueError):
+        cl.dequant_gemv_int4(dev(packed), dev(scales), dev(np.zeros(127, np.float32)), 64, 128, y)
