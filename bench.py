@@ -116,7 +116,7 @@ def cpu_baseline(cl, torch, copies, x, m, seconds):
 
     h, i, g = copies.h, copies.i, copies.g
     host = [c.cpu().numpy() for c in copies.flat[:3]]
-    xb = x.cpu().numpy().view(np.uint16)
+    xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
     out = np.empty((m, h), np.uint16)
     orc.cpu_expert_forward(xb, m, host[0], h, i, g, orc.SCALE_F16, out)  # warm-up
     n = 0

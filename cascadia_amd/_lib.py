@@ -17,6 +17,8 @@ ERR_DEVICE = -3
 ERR_NOMEM = -4
 SCALE_BF16 = 0
 SCALE_F16 = 1
+TILING_CRATE = 0
+TILING_MFMA = 1
 
 _ERRS = {ERR_NULL: "null pointer", ERR_ARG: "invalid argument (shape/length/alignment)",
          ERR_DEVICE: "HIP device error", ERR_NOMEM: "device allocation failed"}
@@ -30,13 +32,15 @@ class CascadiaInt4Error(RuntimeError):
 
 class Layout(C.Structure):
     _fields_ = [("n_rows", C.c_uint32), ("k_cols", C.c_uint32),
-                ("group_size", C.c_uint32), ("scale_dtype", C.c_uint32)]
+                ("group_size", C.c_uint32), ("scale_dtype", C.c_uint32),
+                ("tiling", C.c_uint32)]
 
 
 class Expert(C.Structure):
     _fields_ = [("gate_packed", C.c_void_p), ("gate_scale", C.c_void_p),
                 ("up_packed", C.c_void_p), ("up_scale", C.c_void_p),
-                ("down_packed", C.c_void_p), ("down_scale", C.c_void_p)]
+                ("down_packed", C.c_void_p), ("down_scale", C.c_void_p),
+                ("tiling", C.c_uint32)]
 
 
 _vp, _u32, _u64, _sz, _f64, _i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_size_t, C.c_double, C.c_int
@@ -50,7 +54,11 @@ SIGNATURES = {
     "cascadia_int4_dequant_gemm_multi": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
     "cascadia_int4_dequant_gemm_bf16in": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
     "cascadia_int4_gemm_bf16": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
+    "cascadia_int4_tiled_sizes": (_i32, [_LP, C.POINTER(_sz), C.POINTER(_sz)]),
+    "cascadia_int4_tile_weights": (_i32, [_LP, _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_expert_bytes": (_sz, [_u32, _u32, _u32]),
+    "cascadia_int4_expert_tiled_bytes": (_sz, [_u32, _u32, _u32]),
+    "cascadia_int4_tile_expert": (_i32, [_u32, _u32, _u32, _EP, _vp, _EP, _vp]),
     "cascadia_int4_expert_from_flat": (_i32, [_vp, _u32, _u32, _u32, _EP]),
     "cascadia_int4_ffn_workspace_bytes": (_sz, [_u32, _u32, _u32]),
     "cascadia_int4_expert_forward": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),

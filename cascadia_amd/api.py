@@ -16,7 +16,8 @@ import ctypes as C
 
 import torch
 
-from ._lib import Expert, Layout, SCALE_BF16, SCALE_F16, check, lib
+from ._lib import (Expert, Layout, SCALE_BF16, SCALE_F16, TILING_CRATE, TILING_MFMA, check,
+                   lib)
 
 # K2.6 constants of the crate (lib.rs:71-78)
 HIDDEN = 7168
@@ -50,19 +51,42 @@ def _is_bf16_bits(t: torch.Tensor) -> bool:
     return t.dtype in (torch.bfloat16, torch.int16, torch.uint16)
 
 
-def _layout(n_rows, k_cols, group_size, scale_dtype) -> Layout:
-    return Layout(n_rows, k_cols, group_size, scale_dtype)
+def _layout(n_rows, k_cols, group_size, scale_dtype, tiling=TILING_CRATE) -> Layout:
+    return Layout(n_rows, k_cols, group_size, scale_dtype, tiling)
 
 
-def _check_weights(packed, scale_bits, n_rows, k_cols, group_size):
+def tiled_sizes(n_rows, k_cols, group_size=GROUP_SIZE):
+    """(packed, scale) byte sizes of the MFMA-tiled copy of a matrix."""
+    pb, sb = C.c_size_t(), C.c_size_t()
+    L = _layout(n_rows, k_cols, group_size, SCALE_BF16)
+    check("cascadia_int4_tiled_sizes", lib().cascadia_int4_tiled_sizes(C.byref(L), C.byref(pb), C.byref(sb)))
+    return pb.value, sb.value
+
+
+def _check_weights(packed, scale_bits, n_rows, k_cols, group_size, tiling=TILING_CRATE):
     _dev(packed, "packed")
     _dev(scale_bits, "scale_bits")
     _expect(group_size % 32 == 0 and k_cols % group_size == 0,
             f"k_cols {k_cols} must be a multiple of group_size {group_size} (a multiple of 32)")
-    _expect(_nbytes(packed) == n_rows * (k_cols // 2),
-            f"packed has {_nbytes(packed)} bytes, expected n_rows*k_cols/2 = {n_rows * (k_cols // 2)}")
-    _expect(_nbytes(scale_bits) == n_rows * (k_cols // group_size) * 2,
-            f"scale_bits has {_nbytes(scale_bits)} bytes, expected {n_rows * (k_cols // group_size) * 2}")
+    if tiling == TILING_MFMA:
+        pb, sb = tiled_sizes(n_rows, k_cols, group_size)
+    else:
+        pb, sb = n_rows * (k_cols // 2), n_rows * (k_cols // group_size) * 2
+    _expect(_nbytes(packed) == pb, f"packed has {_nbytes(packed)} bytes, expected {pb}")
+    _expect(_nbytes(scale_bits) == sb, f"scale_bits has {_nbytes(scale_bits)} bytes, expected {sb}")
+
+
+def tile_weights(packed, scale_bits, n_rows, k_cols, group_size=GROUP_SIZE):
+    """MFMA-tiled copies (packed, scales) of a crate-layout matrix."""
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    pb, sb = tiled_sizes(n_rows, k_cols, group_size)
+    pt = torch.empty(pb, dtype=torch.uint8, device=packed.device)
+    st = torch.empty(sb, dtype=torch.uint8, device=packed.device)
+    L = _layout(n_rows, k_cols, group_size, SCALE_BF16)
+    check("cascadia_int4_tile_weights", lib().cascadia_int4_tile_weights(
+        C.byref(L), packed.data_ptr(), scale_bits.data_ptr(), pt.data_ptr(), st.data_ptr(),
+        _stream()))
+    return pt, st
 
 
 # ---------------------------------------------------------------------------
@@ -70,13 +94,13 @@ def _check_weights(packed, scale_bits, n_rows, k_cols, group_size):
 # ---------------------------------------------------------------------------
 
 def dequant_gemv_int4(packed, scale_bits, x, n_rows, k_cols, y, group_size=GROUP_SIZE,
-                      scale_dtype=SCALE_BF16):
+                      scale_dtype=SCALE_BF16, tiling=TILING_CRATE):
     """y = W x (kernel.rs:31-71).  x f32 [k_cols], y f32 [n_rows]."""
-    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size, tiling)
     _dev(x, "x"), _dev(y, "y")
     _expect(x.dtype == torch.float32 and x.numel() == k_cols, "x must be f32 [k_cols]")
     _expect(y.dtype == torch.float32 and y.numel() == n_rows, "y must be f32 [n_rows]")
-    L = _layout(n_rows, k_cols, group_size, scale_dtype)
+    L = _layout(n_rows, k_cols, group_size, scale_dtype, tiling)
     check("cascadia_int4_dequant_gemv", lib().cascadia_int4_dequant_gemv(
         C.byref(L), packed.data_ptr(), scale_bits.data_ptr(), x.data_ptr(), y.data_ptr(),
         _stream()))
@@ -87,16 +111,17 @@ dequant_gemv_int4_auto = dequant_gemv_int4  # kernel_avx512.rs:274-297
 
 
 def dequant_gemm_int4_multi_auto(packed, scale_bits, xs, n_rows, k_cols, seq, ys,
-                                 group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
+                                 group_size=GROUP_SIZE, scale_dtype=SCALE_BF16,
+                                 tiling=TILING_CRATE):
     """ys[t*n_rows + r] for t < seq (kernel_avx512_multi.rs:207-245).
     xs f32 [seq, k_cols]; bf16 xs use the exact bf16 MFMA path."""
-    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size, tiling)
     _dev(xs, "xs"), _dev(ys, "ys")
     _expect(seq >= 1, "seq must be >= 1")
     _expect(xs.numel() == seq * k_cols, f"xs must hold seq*k_cols = {seq * k_cols} values")
     _expect(ys.dtype == torch.float32 and ys.numel() == seq * n_rows,
             f"ys must be f32 [seq*n_rows = {seq * n_rows}]")
-    L = _layout(n_rows, k_cols, group_size, scale_dtype)
+    L = _layout(n_rows, k_cols, group_size, scale_dtype, tiling)
     if xs.dtype == torch.float32:
         fn = "cascadia_int4_dequant_gemm_multi"
     else:
@@ -111,13 +136,13 @@ dequant_gemm_int4_multi_blocked_auto = dequant_gemm_int4_multi_auto  # _blocked.
 
 
 def gemm_int4_bf16(packed, scale_bits, xs_bf16, n_rows, k_cols, seq, ys_bf16,
-                   group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
+                   group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, tiling=TILING_CRATE):
     """Prefill GEMM: bf16 [seq, k_cols] in, bf16 [seq, n_rows] out (f32 inside)."""
-    _check_weights(packed, scale_bits, n_rows, k_cols, group_size)
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size, tiling)
     _dev(xs_bf16, "xs_bf16"), _dev(ys_bf16, "ys_bf16")
     _expect(_is_bf16_bits(xs_bf16) and xs_bf16.numel() == seq * k_cols, "xs_bf16 [seq, k_cols] bf16")
     _expect(_is_bf16_bits(ys_bf16) and ys_bf16.numel() == seq * n_rows, "ys_bf16 [seq, n_rows] bf16")
-    L = _layout(n_rows, k_cols, group_size, scale_dtype)
+    L = _layout(n_rows, k_cols, group_size, scale_dtype, tiling)
     check("cascadia_int4_gemm_bf16", lib().cascadia_int4_gemm_bf16(
         C.byref(L), packed.data_ptr(), scale_bits.data_ptr(), xs_bf16.data_ptr(), seq,
         ys_bf16.data_ptr(), _stream()))
@@ -137,18 +162,40 @@ class ExpertWeights:
     format.rs:51-126 (any hidden / inter / group size)."""
 
     def __init__(self, flat: torch.Tensor, hidden: int, inter: int, group_size: int = GROUP_SIZE,
-                 scale_dtype: int = SCALE_BF16):
+                 scale_dtype: int = SCALE_BF16, tiling: int = TILING_CRATE):
         _dev(flat, "flat")
         _expect(flat.dtype == torch.uint8, "flat must be uint8")
-        _expect(flat.numel() >= expert_bytes(hidden, inter, group_size),
-                f"flat expert too small: {flat.numel()} < {expert_bytes(hidden, inter, group_size)}")
         self.flat, self.hidden, self.inter = flat, hidden, inter
-        self.group_size, self.scale_dtype = group_size, scale_dtype
-        gp, gs = inter * hidden // 2, inter * (hidden // group_size) * 2
-        dp, ds = hidden * inter // 2, hidden * (inter // group_size) * 2
-        o = [0, gp, gp + gs, 2 * gp + gs, 2 * (gp + gs), 2 * (gp + gs) + dp]
-        sz = [gp, gs, gp, gs, dp, ds]
+        self.group_size, self.scale_dtype, self.tiling = group_size, scale_dtype, tiling
+        if tiling == TILING_MFMA:
+            gp, gs = tiled_sizes(inter, hidden, group_size)
+            dp, ds = tiled_sizes(hidden, inter, group_size)
+            sz = [gp, gs, gp, gs, dp, ds]
+            o = [0]
+            for n in sz[:-1]:
+                o.append(o[-1] + ((n + 255) // 256) * 256)
+            need = int(lib().cascadia_int4_expert_tiled_bytes(hidden, inter, group_size))
+        else:
+            gp, gs = inter * hidden // 2, inter * (hidden // group_size) * 2
+            dp, ds = hidden * inter // 2, hidden * (inter // group_size) * 2
+            o = [0, gp, gp + gs, 2 * gp + gs, 2 * (gp + gs), 2 * (gp + gs) + dp]
+            sz = [gp, gs, gp, gs, dp, ds]
+            need = expert_bytes(hidden, inter, group_size)
+        _expect(flat.numel() >= need, f"flat expert too small: {flat.numel()} < {need}")
         self._slices = [flat[a:a + n] for a, n in zip(o, sz)]
+
+    def tiled(self) -> "ExpertWeights":
+        """The MFMA-tiled copy of this (crate-layout) expert."""
+        _expect(self.tiling == TILING_CRATE, "already tiled")
+        nb = int(lib().cascadia_int4_expert_tiled_bytes(self.hidden, self.inter, self.group_size))
+        dst = torch.empty(nb, dtype=torch.uint8, device=self.flat.device)
+        src = _expert_struct(*self._slices)
+        out = Expert()
+        check("cascadia_int4_tile_expert", lib().cascadia_int4_tile_expert(
+            self.hidden, self.inter, self.group_size, C.byref(src), dst.data_ptr(), C.byref(out),
+            _stream()))
+        return ExpertWeights(dst, self.hidden, self.inter, self.group_size, self.scale_dtype,
+                             TILING_MFMA)
 
     def gate_packed_bytes(self): return self._slices[0]
     def gate_scale_bits(self): return self._slices[1]
@@ -161,45 +208,53 @@ class ExpertWeights:
         return tuple(self._slices)
 
 
-def _expert_struct(gp, gs, up, us, dp, ds) -> Expert:
+def _expert_struct(gp, gs, up, us, dp, ds, tiling=TILING_CRATE) -> Expert:
     for t, n in zip((gp, gs, up, us, dp, ds), ("gate_packed", "gate_scale", "up_packed",
                                                  "up_scale", "down_packed", "down_scale")):
         _dev(t, n)
     return Expert(gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), dp.data_ptr(),
-                  ds.data_ptr())
+                  ds.data_ptr(), tiling)
 
 
 def _ffn_dims(x, gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
-              group_size, hidden=None):
+              group_size, hidden=None, tiling=TILING_CRATE):
     hidden = hidden if hidden is not None else x.shape[-1]
     _expect(hidden % group_size == 0, "hidden must be a multiple of group_size")
-    # kernel.rs:86: intermediate inferred from the gate scale length
-    inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
+    if tiling == TILING_MFMA:
+        # tiled scales: [ceil(inter/16)*16, hidden/G] u16
+        inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
+        gp, gs = tiled_sizes(inter, hidden, group_size)
+        dp, ds = tiled_sizes(hidden, inter, group_size)
+    else:
+        # kernel.rs:86: intermediate inferred from the gate scale length
+        inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
+        gp, gs = inter * hidden // 2, inter * (hidden // group_size) * 2
+        dp, ds = hidden * inter // 2, hidden * (inter // group_size) * 2
     _expect(inter > 0 and inter % group_size == 0, "intermediate must be a multiple of group_size")
-    _expect(_nbytes(gate_packed) == inter * hidden // 2 and _nbytes(up_packed) == inter * hidden // 2,
-            "gate/up packed lengths must be inter*hidden/2")
-    _expect(_nbytes(up_scale) == _nbytes(gate_scale), "up_scale length must equal gate_scale")
-    _expect(_nbytes(down_packed) == hidden * inter // 2, "down packed length must be hidden*inter/2")
-    _expect(_nbytes(down_scale) == hidden * (inter // group_size) * 2, "down scale length mismatch")
+    _expect(_nbytes(gate_packed) == gp and _nbytes(up_packed) == gp, "gate/up packed lengths")
+    _expect(_nbytes(up_scale) == gs and _nbytes(gate_scale) == gs, "gate/up scale lengths")
+    _expect(_nbytes(down_packed) == dp, "down packed length")
+    _expect(_nbytes(down_scale) == ds, "down scale length")
     return hidden, inter
 
 
 def gate_up_silu(x, gate_packed, gate_scale, up_packed, up_scale, inter_out,
-                 group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
+                 group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, tiling=TILING_CRATE):
     """inter = silu(gate·x) ⊙ (up·x), f32 [n_tokens, inter] (kernel.rs:96-120).
     x: bf16 or f32 [n_tokens, hidden]."""
     _dev(x, "x"), _dev(inter_out, "inter_out")
     hidden = x.shape[-1]
     _expect(hidden % group_size == 0, "hidden must be a multiple of group_size")
     inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
-    _expect(_nbytes(gate_packed) == inter * hidden // 2 and _nbytes(up_packed) == inter * hidden // 2
+    gp = tiled_sizes(inter, hidden, group_size)[0] if tiling == TILING_MFMA else inter * hidden // 2
+    _expect(_nbytes(gate_packed) == gp and _nbytes(up_packed) == gp
             and _nbytes(up_scale) == _nbytes(gate_scale), "gate/up slice lengths")
     T = x.numel() // hidden
     _expect(inter_out.dtype == torch.float32 and inter_out.numel() == T * inter, "inter_out f32 [T, inter]")
     xf32 = x.dtype == torch.float32
     _expect(xf32 or _is_bf16_bits(x), "x must be f32 or bf16")
     e = Expert(gate_packed.data_ptr(), gate_scale.data_ptr(), up_packed.data_ptr(),
-               up_scale.data_ptr(), gate_packed.data_ptr(), gate_scale.data_ptr())
+               up_scale.data_ptr(), gate_packed.data_ptr(), gate_scale.data_ptr(), tiling)
     check("cascadia_int4_gate_up_silu", lib().cascadia_int4_gate_up_silu(
         hidden, inter, group_size, scale_dtype, C.byref(e), x.data_ptr(), 1 if xf32 else 0, T,
         inter_out.data_ptr(), _stream()))
@@ -212,17 +267,18 @@ def ffn_workspace_bytes(hidden, inter, n_tokens) -> int:
 
 def expert_forward(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
                    down_scale, out_bf16, group_size=GROUP_SIZE, scale_dtype=SCALE_BF16,
-                   workspace=None):
+                   workspace=None, tiling=TILING_CRATE):
     """out = bf16(down · (silu(gate·x) ⊙ up·x)) (kernel.rs:75-136).
     x_bf16 / out_bf16: bf16 [hidden] or [n_tokens, hidden] (rows independent)."""
     _dev(x_bf16, "x_bf16"), _dev(out_bf16, "out_bf16")
     _expect(_is_bf16_bits(x_bf16) and _is_bf16_bits(out_bf16), "x and out must be bf16")
     hidden, inter = _ffn_dims(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
-                              down_scale, group_size)
+                              down_scale, group_size, tiling=tiling)
     T = x_bf16.numel() // hidden
     _expect(x_bf16.numel() == T * hidden and out_bf16.numel() == T * hidden,
             "x and out must both be [n_tokens, hidden]")
-    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale)
+    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
+                       tiling)
     ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
     check("cascadia_int4_expert_forward", lib().cascadia_int4_expert_forward(
         hidden, inter, group_size, scale_dtype, C.byref(e), x_bf16.data_ptr(), T,
@@ -243,7 +299,8 @@ def expert_forward_sparse(x_bf16, gate_packed, gate_scale, up_packed, up_scale, 
 
 def ffn_forward_sparse_f32(x_f32, hidden, intermediate, gate_packed, gate_scale, up_packed,
                            up_scale, down_packed, down_scale, out_f32, threshold,
-                           group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, workspace=None):
+                           group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, workspace=None,
+                           tiling=TILING_CRATE):
     """Dense SwiGLU FFN, f32 in/out (ffn_sparsity.rs:373-496 at tau = 0).
     x_f32 / out_f32: [hidden] or [n_tokens, hidden].  Returns the active
     fraction (1.0)."""
@@ -252,11 +309,12 @@ def ffn_forward_sparse_f32(x_f32, hidden, intermediate, gate_packed, gate_scale,
     _dev(x_f32, "x_f32"), _dev(out_f32, "out_f32")
     _expect(x_f32.dtype == torch.float32 and out_f32.dtype == torch.float32, "f32 in/out")
     h, inter = _ffn_dims(x_f32, gate_packed, gate_scale, up_packed, up_scale, down_packed,
-                         down_scale, group_size, hidden)
+                         down_scale, group_size, hidden, tiling)
     _expect(inter == intermediate, f"intermediate {intermediate} != {inter} implied by gate_scale")
     T = x_f32.numel() // hidden
     _expect(x_f32.numel() == T * hidden and out_f32.numel() == T * hidden, "[n_tokens, hidden]")
-    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale)
+    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
+                       tiling)
     ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
     check("cascadia_int4_ffn_forward_f32", lib().cascadia_int4_ffn_forward_f32(
         hidden, inter, group_size, scale_dtype, C.byref(e), x_f32.data_ptr(), T,

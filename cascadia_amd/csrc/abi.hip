@@ -8,6 +8,7 @@
 
 #include "../../include/cascadia_int4.h"
 #include "int4_common.hpp"
+#include "layout.hpp"
 #include "skinny.hpp"
 #include "synth.hpp"
 
@@ -72,6 +73,7 @@ int check_layout(const cascadia_int4_layout *L) {
   if (L->n_rows == 0 || L->k_cols == 0 || L->group_size == 0) return CASCADIA_INT4_ERR_ARG;
   if (L->group_size % 32 != 0 || L->k_cols % L->group_size != 0) return CASCADIA_INT4_ERR_ARG;
   if (L->scale_dtype > CASCADIA_INT4_SCALE_F16) return CASCADIA_INT4_ERR_ARG;
+  if (L->tiling > CASCADIA_INT4_TILING_MFMA) return CASCADIA_INT4_ERR_ARG;
   if (L->n_rows > (1u << 30) || L->k_cols > (1u << 30)) return CASCADIA_INT4_ERR_ARG;
   return CASCADIA_INT4_OK;
 }
@@ -86,8 +88,8 @@ int hip_status(hipError_t e) { return e == hipSuccess ? CASCADIA_INT4_OK : CASCA
 
 // One skinny GEMM (any M), f32 output or fused epilogue.
 int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint8_t *s1,
-             int N, int K, int G, int sdt, const void *x, bool xf32, int M, void *out,
-             int epi, hipStream_t st) {
+             int N, int K, int G, int sdt, int tiled, const void *x, const void *x2, int amode,
+             int M, void *out, void *out2, int epi, hipStream_t st) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
   cai4::SkinnyArgs a{};
@@ -96,7 +98,9 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   a.w1 = w1;
   a.s1 = s1;
   a.x = x;
+  a.x2 = x2;
   a.out = out;
+  a.out2 = out2;
   a.N = N;
   a.K = K;
   a.G = G;
@@ -104,8 +108,10 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   a.ldx = K;
   a.ldo = N;
   a.sdt = sdt;
-  const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, M, xf32, epi, num_cus(dev));
-  return hip_status(cai4::skinny_launch(a, p, xf32, epi, st));
+  a.glog2 = (G & (G - 1)) == 0 ? __builtin_ctz((unsigned)G) : -1;
+  a.tiled = tiled;
+  const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, M, amode, epi, num_cus(dev));
+  return hip_status(cai4::skinny_launch(a, p, amode, epi, st));
 }
 
 void expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[6]) {
@@ -127,6 +133,7 @@ int check_expert(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
     return CASCADIA_INT4_ERR_NULL;
   if (hidden == 0 || inter == 0 || group == 0 || group % 32) return CASCADIA_INT4_ERR_ARG;
   if (hidden % group || inter % group || sdt > 1) return CASCADIA_INT4_ERR_ARG;
+  if (e->tiling > CASCADIA_INT4_TILING_MFMA) return CASCADIA_INT4_ERR_ARG;
   if (!aligned(e->gate_packed, 16) || !aligned(e->up_packed, 16) ||
       !aligned(e->down_packed, 16))
     return CASCADIA_INT4_ERR_ARG;
@@ -151,13 +158,16 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   } else if (!aligned(ws, 16)) {
     return CASCADIA_INT4_ERR_ARG;
   }
-  float *inter_buf = reinterpret_cast<float *>(ws);
+  // the SwiGLU intermediate as two bf16 planes (hi, lo): [n_tokens, inter] each
+  uint16_t *hi = reinterpret_cast<uint16_t *>(ws);
+  uint16_t *lo = hi + (size_t)n_tokens * inter;
   int rc = run_gemm(e->gate_packed, e->gate_scale, e->up_packed, e->up_scale, (int)inter,
-                    (int)hidden, (int)group, (int)sdt, x, x_f32, (int)n_tokens, inter_buf,
-                    cai4::EPI_SWIGLU, st);
+                    (int)hidden, (int)group, (int)sdt, (int)e->tiling, x, nullptr,
+                    x_f32 ? cai4::A_XF32 : cai4::A_BF16, (int)n_tokens, hi, lo,
+                    cai4::EPI_SWIGLU_HILO, st);
   if (rc) return rc;
   return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
-                  (int)group, (int)sdt, inter_buf, true, (int)n_tokens, out,
+                  (int)group, (int)sdt, (int)e->tiling, hi, lo, cai4::A_HILO, (int)n_tokens, out, nullptr,
                   out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st);
 }
 
@@ -186,8 +196,8 @@ int cascadia_int4_dequant_gemm_multi(const cascadia_int4_layout *L, const uint8_
   if (seq == 0) return CASCADIA_INT4_ERR_ARG;  // the crate asserts seq >= 1
   if (!aligned(xs, 16) || !aligned(ys, 4)) return CASCADIA_INT4_ERR_ARG;
   return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
-                  (int)L->group_size, (int)L->scale_dtype, xs, true, (int)seq, ys,
-                  cai4::EPI_F32, (hipStream_t)stream);
+                  (int)L->group_size, (int)L->scale_dtype, (int)L->tiling, xs, nullptr, cai4::A_XF32, (int)seq,
+                  ys, nullptr, cai4::EPI_F32, (hipStream_t)stream);
 }
 
 int cascadia_int4_dequant_gemm_bf16in(const cascadia_int4_layout *L, const uint8_t *packed,
@@ -199,8 +209,9 @@ int cascadia_int4_dequant_gemm_bf16in(const cascadia_int4_layout *L, const uint8
   if (seq == 0) return CASCADIA_INT4_ERR_ARG;
   if (!aligned(xs_bf16, 16) || !aligned(ys, 4)) return CASCADIA_INT4_ERR_ARG;
   return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
-                  (int)L->group_size, (int)L->scale_dtype, xs_bf16, false, (int)seq, ys,
-                  cai4::EPI_F32, (hipStream_t)stream);
+                  (int)L->group_size, (int)L->scale_dtype, (int)L->tiling, xs_bf16, nullptr,
+                  cai4::A_BF16,
+                  (int)seq, ys, nullptr, cai4::EPI_F32, (hipStream_t)stream);
 }
 
 int cascadia_int4_gemm_bf16(const cascadia_int4_layout *L, const uint8_t *packed,
@@ -212,8 +223,9 @@ int cascadia_int4_gemm_bf16(const cascadia_int4_layout *L, const uint8_t *packed
   if (seq == 0) return CASCADIA_INT4_ERR_ARG;
   if (!aligned(xs_bf16, 16) || !aligned(ys_bf16, 2)) return CASCADIA_INT4_ERR_ARG;
   return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
-                  (int)L->group_size, (int)L->scale_dtype, xs_bf16, false, (int)seq, ys_bf16,
-                  cai4::EPI_BF16, (hipStream_t)stream);
+                  (int)L->group_size, (int)L->scale_dtype, (int)L->tiling, xs_bf16, nullptr,
+                  cai4::A_BF16,
+                  (int)seq, ys_bf16, nullptr, cai4::EPI_BF16, (hipStream_t)stream);
 }
 
 size_t cascadia_int4_expert_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size) {
@@ -236,6 +248,77 @@ int cascadia_int4_expert_from_flat(const uint8_t *flat, uint32_t hidden, uint32_
   out->up_scale = flat + off[3];
   out->down_packed = flat + off[4];
   out->down_scale = flat + off[5];
+  out->tiling = CASCADIA_INT4_TILING_CRATE;
+  return CASCADIA_INT4_OK;
+}
+
+int cascadia_int4_tiled_sizes(const cascadia_int4_layout *L, size_t *packed_bytes,
+                              size_t *scale_bytes) {
+  if (int rc = check_layout(L)) return rc;
+  if (!packed_bytes || !scale_bytes) return CASCADIA_INT4_ERR_NULL;
+  cai4::tiled_sizes((int)L->n_rows, (int)L->k_cols, (int)L->group_size, packed_bytes,
+                    scale_bytes);
+  return CASCADIA_INT4_OK;
+}
+
+int cascadia_int4_tile_weights(const cascadia_int4_layout *L, const uint8_t *packed,
+                               const uint8_t *scale_bits, uint8_t *packed_tiled,
+                               uint8_t *scale_tiled, void *stream) {
+  if (int rc = check_layout(L)) return rc;
+  if (int rc = check_weights(packed, scale_bits)) return rc;
+  if (!packed_tiled || !scale_tiled) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(packed_tiled, 16) || !aligned(scale_tiled, 2)) return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::tile_weights(packed, scale_bits, (int)L->n_rows, (int)L->k_cols,
+                                       (int)L->group_size, packed_tiled, scale_tiled,
+                                       (hipStream_t)stream));
+}
+
+namespace {
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+// offsets of the six sections of a tiled expert blob
+void tiled_expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[7]) {
+  size_t gp, gs, dp, ds;
+  cai4::tiled_sizes((int)inter, (int)hidden, (int)group, &gp, &gs);
+  cai4::tiled_sizes((int)hidden, (int)inter, (int)group, &dp, &ds);
+  const size_t sz[6] = {gp, gs, gp, gs, dp, ds};
+  off[0] = 0;
+  for (int i = 0; i < 6; ++i) off[i + 1] = off[i] + align256(sz[i]);
+}
+}  // namespace
+
+size_t cascadia_int4_expert_tiled_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size) {
+  if (group_size == 0 || group_size % 32 || hidden % group_size || inter % group_size) return 0;
+  size_t off[7];
+  tiled_expert_sections(hidden, inter, group_size, off);
+  return off[6];
+}
+
+int cascadia_int4_tile_expert(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                              const cascadia_int4_expert *src, uint8_t *dst,
+                              cascadia_int4_expert *out, void *stream) {
+  if (!dst || !out) return CASCADIA_INT4_ERR_NULL;
+  if (int rc = check_expert(hidden, inter, group_size, 0, src)) return rc;
+  if (src->tiling != CASCADIA_INT4_TILING_CRATE) return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(dst, 256)) return CASCADIA_INT4_ERR_ARG;
+  size_t off[7];
+  tiled_expert_sections(hidden, inter, group_size, off);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = cai4::tile_weights(src->gate_packed, src->gate_scale, (int)inter, (int)hidden,
+                                    (int)group_size, dst + off[0], dst + off[1], st);
+  if (e == hipSuccess)
+    e = cai4::tile_weights(src->up_packed, src->up_scale, (int)inter, (int)hidden,
+                           (int)group_size, dst + off[2], dst + off[3], st);
+  if (e == hipSuccess)
+    e = cai4::tile_weights(src->down_packed, src->down_scale, (int)hidden, (int)inter,
+                           (int)group_size, dst + off[4], dst + off[5], st);
+  if (e != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+  out->gate_packed = dst + off[0];
+  out->gate_scale = dst + off[1];
+  out->up_packed = dst + off[2];
+  out->up_scale = dst + off[3];
+  out->down_packed = dst + off[4];
+  out->down_scale = dst + off[5];
+  out->tiling = CASCADIA_INT4_TILING_MFMA;
   return CASCADIA_INT4_OK;
 }
 
@@ -269,13 +352,16 @@ int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_s
   if (n_tokens == 0) return CASCADIA_INT4_OK;
   if (!aligned(x, 16) || !aligned(inter_out, 4)) return CASCADIA_INT4_ERR_ARG;
   return run_gemm(expert->gate_packed, expert->gate_scale, expert->up_packed, expert->up_scale,
-                  (int)inter, (int)hidden, (int)group_size, (int)scale_dtype, x, x_is_f32 != 0,
-                  (int)n_tokens, inter_out, cai4::EPI_SWIGLU, (hipStream_t)stream);
+                  (int)inter, (int)hidden, (int)group_size, (int)scale_dtype,
+                  (int)expert->tiling, x, nullptr,
+                  x_is_f32 ? cai4::A_XF32 : cai4::A_BF16, (int)n_tokens, inter_out, nullptr,
+                  cai4::EPI_SWIGLU, (hipStream_t)stream);
 }
 
 int cascadia_int4_debug_dequant(const cascadia_int4_layout *L, const uint8_t *packed,
                                 const uint8_t *scale_bits, float *w_out, void *stream) {
   if (int rc = check_layout(L)) return rc;
+  if (L->tiling != CASCADIA_INT4_TILING_CRATE) return CASCADIA_INT4_ERR_ARG;
   if (!packed || !scale_bits || !w_out) return CASCADIA_INT4_ERR_NULL;
   if (!aligned(packed, 4) || !aligned(scale_bits, 2) || !aligned(w_out, 4))
     return CASCADIA_INT4_ERR_ARG;

@@ -1,0 +1,13 @@
+// layout.hpp -- the MFMA-tiled device layout of an INT4 matrix.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cai4 {
+
+void tiled_sizes(int N, int K, int G, size_t *packed_bytes, size_t *scale_bytes);
+hipError_t tile_weights(const uint8_t *packed, const uint8_t *scale_bits, int N, int K, int G,
+                        uint8_t *packed_tiled, uint8_t *scale_tiled, hipStream_t st);
+
+}  // namespace cai4

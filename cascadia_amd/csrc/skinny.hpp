@@ -6,16 +6,26 @@
 
 namespace cai4 {
 
-enum Epilogue { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_BF16 = 2 };
+// Epilogues: f32 out, bf16 (RNE) out, SwiGLU of a gate/up tile pair as f32,
+// or as the two bf16 planes (hi, lo) that A_HILO consumes.
+enum Epilogue { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_BF16 = 2, EPI_SWIGLU_HILO = 3 };
+
+// Activation modes: bf16; f32 split in-kernel into hi/lo bf16; precomputed
+// hi/lo bf16 planes (x = hi plane, x2 = lo plane).
+enum AMode { A_BF16 = 0, A_XF32 = 1, A_HILO = 2 };
 
 struct SkinnyArgs {
-  const uint8_t *w0;  // packed [N, K/2]           (gate for EPI_SWIGLU)
-  const uint8_t *w1;  // packed [N, K/2] up matrix (EPI_SWIGLU only)
+  const uint8_t *w0;  // packed [N, K/2]           (gate for the SwiGLU epilogues)
+  const uint8_t *w1;  // packed [N, K/2] up matrix (SwiGLU epilogues only)
   const uint8_t *s0;  // scales u16 [N, K/G]
   const uint8_t *s1;
-  const void *x;      // activations [M, ldx]: bf16 bits or f32
-  void *out;          // [M, ldo]: f32 (EPI_F32, EPI_SWIGLU) or bf16 bits (EPI_BF16)
+  const void *x;      // activations [M, ldx]: bf16 bits, f32, or the hi plane
+  const void *x2;     // A_HILO: the lo plane [M, ldx]
+  void *out;          // [M, ldo]: f32, bf16 bits, or the hi plane (EPI_SWIGLU_HILO)
+  void *out2;         // EPI_SWIGLU_HILO: the lo plane
   int N, K, G, M, ldx, ldo, sdt;
+  int glog2;  // log2(G) when G is a power of two, else -1
+  int tiled;  // weights/scales in the MFMA-tiled device layout (layout.hip)
 };
 
 struct SkinnyPlan {
@@ -23,8 +33,8 @@ struct SkinnyPlan {
   size_t lds_bytes;
 };
 
-SkinnyPlan skinny_plan(int N, int K, int M, bool xf32, int epi, int num_cus);
-hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, bool xf32, int epi,
+SkinnyPlan skinny_plan(int N, int K, int M, int amode, int epi, int num_cus);
+hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, int epi,
                          hipStream_t st);
 
 }  // namespace cai4

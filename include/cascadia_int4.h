@@ -42,6 +42,14 @@ extern "C" {
 #define CASCADIA_INT4_SCALE_BF16 0u /* the crate's format (format.rs:16-17) */
 #define CASCADIA_INT4_SCALE_F16 1u
 
+/* Weight byte layouts.  CRATE is the crate's row-major layout, unchanged.
+ * MFMA is the tiled device layout made by cascadia_int4_tile_weights: each
+ * (16-row tile, 128-column k-block) is one contiguous 1 KB block in MFMA lane
+ * order, so the decode kernels stream HBM sequentially.  Same codes and
+ * scale bits, moved; results are bit-identical between the two. */
+#define CASCADIA_INT4_TILING_CRATE 0u
+#define CASCADIA_INT4_TILING_MFMA 1u
+
 /* Routing rules for the MoE entry point. */
 #define CASCADIA_INT4_ROUTE_IDS 0u          /* caller supplies ids/weights */
 #define CASCADIA_INT4_ROUTE_SIGMOID_BIAS 1u /* shell_int4.rs:588-620 / glm/gate.rs:24-62 */
@@ -55,7 +63,19 @@ typedef struct cascadia_int4_layout {
   uint32_t k_cols;      /* K, a multiple of group_size */
   uint32_t group_size;  /* G, a multiple of 32 (the crate: 32) */
   uint32_t scale_dtype; /* CASCADIA_INT4_SCALE_BF16 or _F16 */
+  uint32_t tiling;      /* CASCADIA_INT4_TILING_CRATE or _MFMA */
 } cascadia_int4_layout;
+
+/* Byte sizes of the MFMA-tiled copy of a matrix (rows padded to 16, columns
+ * to 128).  layout->tiling is ignored. */
+int cascadia_int4_tiled_sizes(const cascadia_int4_layout *layout, size_t *packed_bytes,
+                              size_t *scale_bytes);
+
+/* Write the MFMA-tiled copy of a crate-layout matrix (done once, when the
+ * weights are uploaded).  layout->tiling is ignored (the source is CRATE). */
+int cascadia_int4_tile_weights(const cascadia_int4_layout *layout, const uint8_t *packed,
+                               const uint8_t *scale_bits, uint8_t *packed_tiled,
+                               uint8_t *scale_tiled, void *stream);
 
 /* Library version string. */
 const char *cascadia_int4_version(void);
@@ -105,16 +125,28 @@ typedef struct cascadia_int4_expert {
   const uint8_t *up_scale;
   const uint8_t *down_packed;
   const uint8_t *down_scale;
+  uint32_t tiling; /* CASCADIA_INT4_TILING_CRATE or _MFMA, for all six slices */
 } cascadia_int4_expert;
 
 /* Size in bytes of one flat expert blob: gate_p, gate_s, up_p, up_s, down_p,
  * down_s contiguous (format.rs:35-47 / ov_moe.rs:792-806, any dims/G). */
 size_t cascadia_int4_expert_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size);
 
-/* Fill *out with the six slices of a flat expert blob at `flat`
- * (the slicing of ov_moe.rs:792-806 / format.rs:63-96). */
+/* Fill *out with the six slices of a crate-layout flat expert blob at `flat`
+ * (the slicing of ov_moe.rs:792-806 / format.rs:63-96); tiling = CRATE. */
 int cascadia_int4_expert_from_flat(const uint8_t *flat, uint32_t hidden, uint32_t inter,
                                    uint32_t group_size, cascadia_int4_expert *out);
+
+/* Bytes of the MFMA-tiled copy of one expert (six 256-byte-aligned
+ * sections in the flat-blob order). */
+size_t cascadia_int4_expert_tiled_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size);
+
+/* Tile the six crate-layout slices of *src into the blob at dst (at least
+ * cascadia_int4_expert_tiled_bytes, 256-byte aligned) and describe the
+ * tiled slices in *out (tiling = MFMA). */
+int cascadia_int4_tile_expert(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                              const cascadia_int4_expert *src, uint8_t *dst,
+                              cascadia_int4_expert *out, void *stream);
 
 /* Workspace bytes the expert / FFN entry points need for n_tokens rows. */
 size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32_t n_tokens);
