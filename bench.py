@@ -1,20 +1,26 @@
 """Benchmark of the INT4 weight-only matmul hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--extra]
+    python bench.py --profile        # the headline kernels only, for rocprofv3
 
 Headline: the Llama-3-8B-shaped decode FFN chain,
 gate/up 14336x4096 + down 4096x14336, INT4 group 128 with fp16 scales, bf16
 activations, M tokens.  One step = one expert_forward chain (two kernels:
 fused gate/up/SiLU*up, then down with the bf16 output rounding) over one
-batch of M tokens, with the weights rotated through enough distinct copies
+batch of M tokens.  The weights are synthetic (seeded), made in the crate's
+layout and converted once to the MFMA-tiled device layout (the upload step,
+outside the timed region); steps rotate through enough distinct copies
 (> 2 x 256 MB Infinity Cache) that every step streams its weights from HBM.
+The K timed steps are captured once as a HIP graph and replayed once,
+bracketed by synchronisations, as a server's decode loop would run them.
 
-`value` = algorithmic bytes per step (3 x (packed + scales) + M*H*2*2, the
+`value` = algorithmic bytes per step (3 x (packed + scales) + M*H*2*2: the
 weights read once plus activations in and out) x steps / wall time of the
 timed region -> GB/s.  The roofline object covers the dominant kernel (the
-fused gate/up kernel), timed with HIP events on the stream it runs on.  The
-CPU baseline is the oracle's AVX-512 port of the crate's kernels on the host
-cores, on a bounded sample of the same workload (same bytes, copied back).
+fused gate/up kernel), timed the same way with HIP events recorded on the
+stream the kernels run on.  The CPU baseline is the oracle's AVX-512 port of
+the crate's kernels on the host cores, on a bounded sample of the same
+workload (same bytes).
 """
 from __future__ import annotations
 
@@ -31,6 +37,7 @@ sys.path.insert(0, ROOT)
 MALL_BYTES = 256 << 20
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "config1_gate_up_traffic.json")
 
 
 def parse():
@@ -42,6 +49,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--extra", action="store_true", help="also time configs 0 and 2, M=4/16")
+    ap.add_argument("--profile", action="store_true",
+                    help="launch the headline kernels and a 256 MiB copy (counter calibration) "
+                         "eagerly, without timing, for rocprofv3")
     return ap.parse_args()
 
 
@@ -55,12 +65,12 @@ def gate_up_bytes(h, i, g, m):
 
 
 class Copies:
-    """`n` distinct synthetic experts resident in HBM."""
+    """`n` distinct synthetic experts: crate layout, tiled once for the GPU."""
 
-    def __init__(self, cl, torch, h, i, g, sdt, n, seed=1):
+    def __init__(self, cl, torch, h, i, g, sdt, n, seed=1, keep_crate=3):
         self.h, self.i, self.g = h, i, g
         nb = cl.expert_bytes(h, i, g)
-        self.flat = []
+        self.crate = []  # a few crate-layout blobs for the CPU baseline
         self.w = []
         for c in range(n):
             f = torch.empty(nb, dtype=torch.uint8, device="cuda")
@@ -68,54 +78,64 @@ class Copies:
             W = cl.ExpertWeights(f, h, i, g, sdt)
             for j, s in enumerate((W.gate_scale_bits(), W.up_scale_bits(), W.down_scale_bits())):
                 cl.fill_scales(s, seed, 1000 + 10 * c + j, sdt)
-            self.flat.append(f)
-            self.w.append(W)
+            self.w.append(W.tiled())
+            if len(self.crate) < keep_crate:
+                self.crate.append(f)
+            del W, f
         torch.cuda.synchronize()
 
 
-def time_chain(cl, torch, copies, x, out, steps, warmup, sdt):
+def graph_time(torch, fn, steps):
+    """Capture `steps` calls as one HIP graph and time one replay: wall clock
+    between synchronisations, and HIP events on the replay stream."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for k in range(steps):
+                fn(k)
+        g.replay()  # the first replay uploads the graph
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    torch.cuda.current_stream().wait_stream(s)
+    del g
+    return t1 - t0, e0.elapsed_time(e1) / 1e3
+
+
+def chain_fn(cl, copies, x, out, sdt):
     nc = len(copies.w)
-    for s in range(warmup):
-        cl.expert_forward(x, *copies.w[s % nc].slices(), out, group_size=copies.g, scale_dtype=sdt)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for s in range(steps):
-        cl.expert_forward(x, *copies.w[s % nc].slices(), out, group_size=copies.g, scale_dtype=sdt)
-    e1.record()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    return (t1 - t0), e0.elapsed_time(e1) / 1e3
+
+    def fn(k):
+        cl.expert_forward(x, *copies.w[k % nc].slices(), out, group_size=copies.g,
+                          scale_dtype=sdt, tiling=cl.TILING_MFMA)
+    return fn
 
 
-def time_gate_up(cl, torch, copies, x, inter, steps, warmup, sdt):
-    """Average duration of the fused gate/up kernel alone (HIP events on the
-    current stream, which is the stream the kernel is launched on)."""
+def gate_up_fn(cl, copies, x, inter, sdt):
     nc = len(copies.w)
-    for s in range(warmup):
-        W = copies.w[s % nc]
+
+    def fn(k):
+        W = copies.w[k % nc]
         cl.gate_up_silu(x, W.gate_packed_bytes(), W.gate_scale_bits(), W.up_packed_bytes(),
-                        W.up_scale_bits(), inter, group_size=copies.g, scale_dtype=sdt)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for s in range(steps):
-        W = copies.w[s % nc]
-        cl.gate_up_silu(x, W.gate_packed_bytes(), W.gate_scale_bits(), W.up_packed_bytes(),
-                        W.up_scale_bits(), inter, group_size=copies.g, scale_dtype=sdt)
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / steps
+                        W.up_scale_bits(), inter, group_size=copies.g, scale_dtype=sdt,
+                        tiling=cl.TILING_MFMA)
+    return fn
 
 
-def cpu_baseline(cl, torch, copies, x, m, seconds):
+def cpu_baseline(torch, copies, x, m, seconds):
     import numpy as np
 
     import oracle as orc
 
     h, i, g = copies.h, copies.i, copies.g
-    host = [c.cpu().numpy() for c in copies.flat[:3]]
+    host = [c.cpu().numpy() for c in copies.crate]
     xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
     out = np.empty((m, h), np.uint16)
     orc.cpu_expert_forward(xb, m, host[0], h, i, g, orc.SCALE_F16, out)  # warm-up
@@ -137,58 +157,81 @@ def cpu_baseline(cl, torch, copies, x, m, seconds):
     }
 
 
-def extra_measurements(cl, torch, args, sdt):
-    """Secondary numbers (not the headline): config 0 GEMV, M=4/16 chains,
-    prefill GEMM."""
-    import numpy as np
+def read_traffic(m):
+    """HBM bytes per launch of the gate/up kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), if present."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            d = json.load(f)
+        v = d.get(f"M{m}", {}).get("hbm_bytes_per_launch")
+        return None if v is None else int(v)
+    except (OSError, ValueError):
+        return None
 
+
+def extra_measurements(cl, torch, args, sdt, copies):
+    """Secondary numbers (not the headline): M=4/16 chains, config 0 GEMV,
+    config 2 prefill GEMM."""
     res = {}
-    # config 0: 4096x4096 GEMV, f32 x, rotate > 2x MALL of weight copies
+    h, i, g = copies.h, copies.i, copies.g
+    for mm in (4, 16):
+        xm = cl.fill_normal(torch.empty((mm, h), dtype=torch.bfloat16, device="cuda"), 0, 22)
+        om = torch.empty((mm, h), dtype=torch.bfloat16, device="cuda")
+        fn = chain_fn(cl, copies, xm, om, sdt)
+        for k in range(10):
+            fn(k)
+        w2, _ = graph_time(torch, fn, args.steps)
+        res[f"config1_M{mm}"] = {"GB/s": round(ffn_bytes(h, i, g, mm) * args.steps / w2 / 1e9, 1),
+                                 "us_per_chain": round(w2 / args.steps * 1e6, 2),
+                                 "tokens_per_s": round(mm * args.steps / w2, 1)}
+    # config 0: 4096x4096 GEMV, f32 x, rotating > 2x MALL of weight copies
     n = k = 4096
-    g = 128
-    nb = n * k // 2
-    nsb = n * (k // g) * 2
+    nb, nsb = n * k // 2, n * (k // g) * 2
     ncp = math.ceil(2 * MALL_BYTES / (nb + nsb)) + 1
-    P = [cl.fill_bytes(torch.empty(nb, dtype=torch.uint8, device="cuda"), 0, 200 + c) for c in range(ncp)]
-    S = [cl.fill_scales(torch.empty(nsb, dtype=torch.uint8, device="cuda"), 0, 300 + c, sdt) for c in range(ncp)]
+    PS = []
+    for c in range(ncp):
+        p = cl.fill_bytes(torch.empty(nb, dtype=torch.uint8, device="cuda"), 0, 200 + c)
+        s = cl.fill_scales(torch.empty(nsb, dtype=torch.uint8, device="cuda"), 0, 300 + c, sdt)
+        PS.append(cl.tile_weights(p, s, n, k, g))
+        del p, s
     x = cl.fill_normal(torch.empty(k, dtype=torch.float32, device="cuda"), 0, 13)
     y = torch.empty(n, dtype=torch.float32, device="cuda")
-    for s in range(20):
-        cl.dequant_gemv_int4(P[s % ncp], S[s % ncp], x, n, k, y, group_size=g, scale_dtype=sdt)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    steps = 2000
-    e0.record()
-    for s in range(steps):
-        cl.dequant_gemv_int4(P[s % ncp], S[s % ncp], x, n, k, y, group_size=g, scale_dtype=sdt)
-    e1.record()
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / 1e3 / steps
+
+    def gemv(r):
+        pt, st = PS[r % ncp]
+        cl.dequant_gemv_int4(pt, st, x, n, k, y, group_size=g, scale_dtype=sdt,
+                             tiling=cl.TILING_MFMA)
+    for r in range(10):
+        gemv(r)
+    steps = 1000
+    w, _ = graph_time(torch, gemv, steps)
+    t = w / steps
     b = nb + nsb + k * 4 + n * 4
     res["config0_gemv"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(b / t / 1e9, 1),
                            "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4), "copies": ncp}
-    del P, S
-    # config 2: prefill GEMM M=512, N=4096, K=4096 (bf16 in/out)
+    del PS
+    # config 2: prefill GEMM (bf16 in/out)
     for (m, nn) in [(512, 4096), (2048, 14336)]:
         kk = 4096
         pk = cl.fill_bytes(torch.empty(nn * kk // 2, dtype=torch.uint8, device="cuda"), 2, 1)
-        sc = cl.fill_scales(torch.empty(nn * (kk // g) * 2, dtype=torch.uint8, device="cuda"), 2, 2, sdt)
+        sc = cl.fill_scales(torch.empty(nn * (kk // g) * 2, dtype=torch.uint8, device="cuda"),
+                            2, 2, sdt)
+        pt, st = cl.tile_weights(pk, sc, nn, kk, g)
         xb = cl.fill_normal(torch.empty(m * kk, dtype=torch.bfloat16, device="cuda"), 2, 3)
         yb = torch.empty(m * nn, dtype=torch.bfloat16, device="cuda")
-        for _ in range(3):
-            cl.gemm_int4_bf16(pk, sc, xb, nn, kk, m, yb, group_size=g, scale_dtype=sdt)
-        torch.cuda.synchronize()
+
+        def pre(r):
+            cl.gemm_int4_bf16(pt, st, xb, nn, kk, m, yb, group_size=g, scale_dtype=sdt,
+                              tiling=cl.TILING_MFMA)
+        pre(0)
         reps = 10
-        e0.record()
-        for _ in range(reps):
-            cl.gemm_int4_bf16(pk, sc, xb, nn, kk, m, yb, group_size=g, scale_dtype=sdt)
-        e1.record()
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) / 1e3 / reps
+        w, _ = graph_time(torch, pre, reps)
+        t = w / reps
         tf = 2.0 * m * nn * kk / t / 1e12
-        res[f"config2_prefill_M{m}_N{nn}"] = {"us_per_call": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
+        res[f"config2_prefill_M{m}_N{nn}"] = {"us_per_call": round(t * 1e6, 1),
+                                              "TFLOP/s": round(tf, 1),
                                               "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
-        del pk, sc, xb, yb
+        del pk, sc, pt, st, xb, yb
     return res
 
 
@@ -209,13 +252,33 @@ def main():
     copies = Copies(cl, torch, h, i, g, sdt, ncopies)
     x = cl.fill_normal(torch.empty((m, h), dtype=torch.bfloat16, device="cuda"), 0, 22)
     out = torch.empty((m, h), dtype=torch.bfloat16, device="cuda")
-
-    wall, ev = time_chain(cl, torch, copies, x, out, args.steps, args.warmup, sdt)
-    step_bytes = ffn_bytes(h, i, g, m)
-    value = step_bytes * args.steps / wall / 1e9
-
     inter = torch.empty((m, i), dtype=torch.float32, device="cuda")
-    t_gu = time_gate_up(cl, torch, copies, x, inter, args.steps, args.warmup, sdt)
+    fn = chain_fn(cl, copies, x, out, sdt)
+    gu = gate_up_fn(cl, copies, x, inter, sdt)
+
+    if args.profile:
+        for k in range(args.steps):
+            fn(k)
+        for k in range(args.steps):
+            gu(k)
+        a = torch.zeros(64 << 20, dtype=torch.float32, device="cuda")  # 256 MiB
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)  # calibration: reads 256 MiB, writes 256 MiB per launch
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": "done", "steps": args.steps, "M": m}), flush=True)
+        return
+
+    for k in range(args.warmup):
+        fn(k)
+    torch.cuda.synchronize()
+    wall, ev = graph_time(torch, fn, args.steps)
+    value = ffn_bytes(h, i, g, m) * args.steps / wall / 1e9
+
+    for k in range(args.warmup):
+        gu(k)
+    _, ev_gu = graph_time(torch, gu, args.steps)
+    t_gu = ev_gu / args.steps
     gu_bytes = gate_up_bytes(h, i, g, m)
     achieved = gu_bytes / t_gu / 1e9
 
@@ -234,27 +297,22 @@ def main():
         "data": "synthetic",
         "config": {"workload": "config1_llama3_8b_decode_ffn_chain", "M": m, "hidden": h,
                    "inter": i, "group": g, "scales": "fp16", "weight_copies": ncopies,
+                   "weight_layout": "mfma_tiled, converted once from the crate layout",
+                   "timing": "one HIP-graph replay of the K steps",
                    "tokens_per_s": round(m * args.steps / wall, 1),
                    "event_ms_per_step": round(ev / args.steps * 1e3, 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "skinny_kernel (fused gate/up + SiLU*up)",
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(m),
+                     "kernel": "skinny_kernel, fused gate/up + SiLU*up (EPI_SWIGLU)",
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cl, torch, copies, x, m, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(torch, copies, x, m, args.cpu_seconds)
     if args.extra:
-        for mm in (4, 16):
-            xm = cl.fill_normal(torch.empty((mm, h), dtype=torch.bfloat16, device="cuda"), 0, 22)
-            om = torch.empty((mm, h), dtype=torch.bfloat16, device="cuda")
-            w2, _ = time_chain(cl, torch, copies, xm, om, args.steps, args.warmup, sdt)
-            line.setdefault("extra", {})[f"config1_M{mm}"] = {
-                "GB/s": round(ffn_bytes(h, i, g, mm) * args.steps / w2 / 1e9, 1),
-                "us_per_chain": round(w2 / args.steps * 1e6, 2),
-                "tokens_per_s": round(mm * args.steps / w2, 1)}
-        line.setdefault("extra", {}).update(extra_measurements(cl, torch, args, sdt))
-    print(json.dumps(line))
+        line["extra"] = extra_measurements(cl, torch, args, sdt, copies)
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

@@ -261,8 +261,10 @@ def gate_up_silu(x, gate_packed, gate_scale, up_packed, up_scale, inter_out,
     return inter_out
 
 
-def ffn_workspace_bytes(hidden, inter, n_tokens) -> int:
-    return int(lib().cascadia_int4_ffn_workspace_bytes(hidden, inter, n_tokens))
+def ffn_workspace_bytes(hidden, inter, n_tokens, group_size=GROUP_SIZE) -> int:
+    """Workspace bytes of expert_forward / ffn_forward_sparse_f32 for n_tokens
+    rows on the current device."""
+    return int(lib().cascadia_int4_ffn_workspace_bytes(hidden, inter, group_size, n_tokens))
 
 
 def expert_forward(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,

@@ -18,6 +18,7 @@ constexpr int kMaxDevices = 64;
 
 struct DeviceState {
   int num_cus = 0;
+  size_t max_lds = 0;
   void *ws = nullptr;  // library-owned workspace (grow-only)
   size_t ws_bytes = 0;
 };
@@ -31,17 +32,23 @@ int current_device(int *dev) {
   return CASCADIA_INT4_OK;
 }
 
-int num_cus(int dev) {
+// CU count and per-workgroup LDS limit of a device (queried once).
+cai4::SkinnyDevice device_props(int dev) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState &d = g_dev[dev];
   if (d.num_cus == 0) {
-    int n = 0;
+    int n = 0, l = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
+    if (hipDeviceGetAttribute(&l, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) !=
+            hipSuccess ||
+        l <= 0)
+      l = 64 * 1024;
     d.num_cus = n;
+    d.max_lds = (size_t)l;
   }
-  return d.num_cus;
+  return cai4::SkinnyDevice{d.num_cus, d.max_lds};
 }
 
 // Library workspace of at least `bytes` on the current device.
@@ -86,13 +93,27 @@ int check_weights(const uint8_t *packed, const uint8_t *scales) {
 
 int hip_status(hipError_t e) { return e == hipSuccess ? CASCADIA_INT4_OK : CASCADIA_INT4_ERR_DEVICE; }
 
-// One skinny GEMM (any M), f32 output or fused epilogue.
+int glog2_of(int G) { return (G & (G - 1)) == 0 ? __builtin_ctz((unsigned)G) : -1; }
+
+// Activation bytes a skinny GEMM addresses with 32-bit offsets.
+bool act_fits(int M, int K, int amode) {
+  return (size_t)M * K * (amode == cai4::A_XF32 ? 4 : 2) < 0x7FFFFFFFu;
+}
+
+// One skinny GEMM (any M), f32 output or fused epilogue.  `partials` is
+// workspace for split-K partial sums (null: the library's own workspace).
 int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint8_t *s1,
              int N, int K, int G, int sdt, int tiled, const void *x, const void *x2, int amode,
-             int M, void *out, void *out2, int epi, hipStream_t st) {
+             int M, void *out, void *out2, int epi, hipStream_t st, void *partials = nullptr) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
+  if (!act_fits(M, K, amode)) return CASCADIA_INT4_ERR_ARG;
+  const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, G, M, amode, epi, device_props(dev));
+  if (p.partial_bytes && !partials) {
+    if (int rc = lib_workspace(dev, p.partial_bytes, &partials)) return rc;
+  }
   cai4::SkinnyArgs a{};
+  a.partials = partials;
   a.w0 = w0;
   a.s0 = s0;
   a.w1 = w1;
@@ -108,10 +129,27 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   a.ldx = K;
   a.ldo = N;
   a.sdt = sdt;
-  a.glog2 = (G & (G - 1)) == 0 ? __builtin_ctz((unsigned)G) : -1;
+  a.glog2 = glog2_of(G);
   a.tiled = tiled;
-  const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, M, amode, epi, num_cus(dev));
   return hip_status(cai4::skinny_launch(a, p, amode, epi, st));
+}
+
+// Workspace of an expert FFN: the SwiGLU intermediate as two bf16 planes,
+// then the split-K partials of whichever of its two GEMMs needs more.
+struct FfnWorkspace {
+  size_t planes, partials;
+};
+FfnWorkspace ffn_workspace(int dev, uint32_t hidden, uint32_t inter, uint32_t group,
+                           uint32_t n_tokens, bool x_f32) {
+  const cai4::SkinnyDevice d = device_props(dev);
+  const cai4::SkinnyPlan gu =
+      cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens,
+                        x_f32 ? cai4::A_XF32 : cai4::A_BF16, cai4::EPI_SWIGLU_HILO, d);
+  const cai4::SkinnyPlan dn = cai4::skinny_plan((int)hidden, (int)inter, (int)group,
+                                                (int)n_tokens, cai4::A_HILO, cai4::EPI_F32, d);
+  const size_t planes = ((size_t)n_tokens * inter * 2 * sizeof(uint16_t) + 255) & ~(size_t)255;
+  return FfnWorkspace{planes, gu.partial_bytes > dn.partial_bytes ? gu.partial_bytes
+                                                                  : dn.partial_bytes};
 }
 
 void expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[6]) {
@@ -151,24 +189,28 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   if (!aligned(x, 16)) return CASCADIA_INT4_ERR_ARG;
   int dev;
   if (int rc = current_device(&dev)) return rc;
-  const size_t need = cascadia_int4_ffn_workspace_bytes(hidden, inter, n_tokens);
+  if (!act_fits((int)n_tokens, (int)hidden, x_f32 ? cai4::A_XF32 : cai4::A_BF16) ||
+      !act_fits((int)n_tokens, (int)inter, cai4::A_HILO))
+    return CASCADIA_INT4_ERR_ARG;
+  const FfnWorkspace need = ffn_workspace(dev, hidden, inter, group, n_tokens, x_f32);
   void *ws = workspace;
   if (!ws) {
-    if (int rc = lib_workspace(dev, need, &ws)) return rc;
+    if (int rc = lib_workspace(dev, need.planes + need.partials, &ws)) return rc;
   } else if (!aligned(ws, 16)) {
     return CASCADIA_INT4_ERR_ARG;
   }
   // the SwiGLU intermediate as two bf16 planes (hi, lo): [n_tokens, inter] each
   uint16_t *hi = reinterpret_cast<uint16_t *>(ws);
   uint16_t *lo = hi + (size_t)n_tokens * inter;
+  void *part = need.partials ? static_cast<uint8_t *>(ws) + need.planes : nullptr;
   int rc = run_gemm(e->gate_packed, e->gate_scale, e->up_packed, e->up_scale, (int)inter,
                     (int)hidden, (int)group, (int)sdt, (int)e->tiling, x, nullptr,
                     x_f32 ? cai4::A_XF32 : cai4::A_BF16, (int)n_tokens, hi, lo,
-                    cai4::EPI_SWIGLU_HILO, st);
+                    cai4::EPI_SWIGLU_HILO, st, part);
   if (rc) return rc;
   return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
-                  (int)group, (int)sdt, (int)e->tiling, hi, lo, cai4::A_HILO, (int)n_tokens, out, nullptr,
-                  out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st);
+                  (int)group, (int)sdt, (int)e->tiling, hi, lo, cai4::A_HILO, (int)n_tokens,
+                  out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st, part);
 }
 
 }  // namespace
@@ -322,9 +364,14 @@ int cascadia_int4_tile_expert(uint32_t hidden, uint32_t inter, uint32_t group_si
   return CASCADIA_INT4_OK;
 }
 
-size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32_t n_tokens) {
-  (void)hidden;
-  return (size_t)n_tokens * inter * sizeof(float);
+size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                         uint32_t n_tokens) {
+  int dev;
+  if (current_device(&dev)) return 0;
+  if (group_size == 0 || group_size % 32) return 0;
+  const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group_size, n_tokens, true);
+  const FfnWorkspace b = ffn_workspace(dev, hidden, inter, group_size, n_tokens, false);
+  return f.planes + (f.partials > b.partials ? f.partials : b.partials);
 }
 
 int cascadia_int4_expert_forward(uint32_t hidden, uint32_t inter, uint32_t group_size,

@@ -1,5 +1,5 @@
-// skinny.hip -- decode-regime INT4 weight-only GEMM for gfx950 (M <= 64 per
-// pass; larger M loops over M chunks).
+// skinny.hip -- decode-regime INT4 weight-only GEMM for gfx950 (up to 64
+// tokens per pass; larger M loops over M chunks).
 //
 // y[t, r] = sum_g s[r, g] * sum_{c in g} (nibble[r, c] - 8) * x[t, c]
 //
@@ -8,23 +8,31 @@
 // kernel_avx512_multi.rs:66-245) and, with fused epilogues, of the
 // gate/up -> SiLU*up -> down chain of expert_forward (kernel.rs:75-136).
 //
-// Work decomposition.  A workgroup owns a row block (16*NT weight rows; for
-// the SwiGLU epilogues one gate tile + one up tile of the same 16 output
-// rows) and the whole K range; its waves each take a contiguous run of
-// 128-column k-blocks.  Per k-block a lane loads 16 packed bytes of one row
-// (lanes 0-15: 16 rows; lane row lane/16: the 16-byte chunk of the 64-byte
-// k-block).  Weights, scales and activations of U consecutive k-blocks are in
-// flight per wave (a register ring).  All loads are buffer loads: the
-// resource descriptor (SGPRs) spans exactly the valid bytes, so rows past N,
-// tokens past M, tail chunks and prefetches past the wave's range read 0
-// from the hardware range check instead of being clamped, and per-lane
-// offsets are 32-bit constants.  Partial sums are reduced across waves
-// through LDS in fixed wave order (deterministic; no atomics), then wave 0
-// applies the epilogue.
+// Why it is shaped this way.  Decode streams every weight byte exactly once,
+// so the k-loop must issue nothing but 16-byte weight loads: one
+// buffer_load_dwordx4 per lane moves one 1 KB k-block of a 16-row tile.  The
+// activations and scales, which every tile re-reads, are staged into LDS once
+// per workgroup with wide cooperative loads (f32 activations are split into
+// their hi/lo bf16 planes there, once, instead of at every use); the k-loop
+// reads them with ds_read_b128 / ds_read_b32, off the vector-memory path.
+//
+// Work decomposition.  A workgroup has rw x kw waves.  Wave (r, k) owns the
+// nt weight tiles of row unit (blockIdx.x * rw + r) -- one gate tile + one up
+// tile of the same 16 output rows for the SwiGLU epilogues -- and the k-th
+// contiguous span of the workgroup's k-blocks (128 columns each).  The rw row
+// groups share the staged activations.  A register ring keeps U k-blocks of
+// weights in flight per wave.  Partial sums of the kw spans are added through
+// LDS in fixed wave order; with ksplit > 1 workgroups also split K and
+// splitk_reduce_kernel adds their partials in fixed split order.  Every sum
+// has one fixed order: results are deterministic (no atomics).
 //
 // Weight layouts.  CRATE (the crate's row-major bytes) or TILED (layout.hip:
-// each 16-row x 128-column block is 1 KB contiguous in lane order, nibbles
-// of a dword swizzled so that the decode yields natural column order).
+// each 16-row x 128-column block is 1 KB contiguous in lane order, nibbles of
+// a dword swizzled so that the decode yields natural column order).  All
+// weight loads are buffer loads whose descriptor spans exactly the tile's
+// valid bytes: rows past N read 0 from the hardware range check, and a dead
+// prefetch (past the wave's span) uses an out-of-range offset, so it moves no
+// data.
 //
 // k-slot mapping.  G % 128 == 0 ("contiguous"): MFMA step s of a k-block
 // takes dword s of each lane's chunk; all 128 columns share one scale.
@@ -33,13 +41,11 @@
 // s covers columns 32s..32s+31 of the block -- inside one group for any G
 // that is a multiple of 32.  K must be a multiple of 32 and of G.
 //
-// Activation modes (token slots of a 16-slot M tile):
-//   A_BF16: slot i = token i, bf16 (exact in the MFMA);
-//   A_XF32: f32 activations split in-kernel into hi (truncated bf16) and lo
-//           (bf16 of the exact remainder): slots 0-7 hi, 8-15 lo of tokens
-//           0-7; y = D[hi] + D[lo];
-//   A_HILO: the same split, precomputed as two bf16 planes (x and x2; the
-//           SwiGLU intermediate is written that way by the gate/up epilogue).
+// Token slots of a 16-slot MFMA tile:
+//   A_BF16: slot i = token i (exact bf16 products);
+//   A_XF32 / A_HILO: slots 0-7 = hi plane of tokens 0-7, slots 8-15 = lo plane
+//   (hi = f32 truncated to bf16, lo = bf16 of the exact remainder); the two
+//   halves of the MFMA result are added: y = D[hi] + D[lo].
 #include <stdlib.h>
 
 #include "int4_common.hpp"
@@ -56,29 +62,29 @@ CAI4_DEV rsrc_t make_rsrc(const void *base, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, kRsrcFlags);
 }
 
-template <int AM>
-struct AModeTraits {
-  static constexpr int TPM = AM == A_BF16 ? 16 : 8;  // tokens per M tile
-  static constexpr int NA = AM == A_XF32 ? 2 : 1;    // 16-byte loads per step
-  static constexpr int ESZ = AM == A_XF32 ? 4 : 2;   // activation element bytes
+// Everything a launch needs (SkinnyArgs + SkinnyPlan), passed by value.
+struct KParams {
+  const uint8_t *w0, *w1, *s0, *s1;
+  const void *x, *x2;
+  void *out, *out2;
+  f32x4_t *part;
+  int N, K, G, M, ldx, ldo, sdt, glog2, tiled, amode, epi;
+  int rw, kw, kper;
+  int act_rows, act_stride, scale_off;
 };
 
-// One k-block of a wave: weights, scales and activations.
-template <int NT, int MT, int AM, bool TR>
-struct Stage {
-  u32x4_t b[NT];
-  uint32_t sb[NT][TR ? 4 : 1];
-  u32x4_t a[MT][4][AModeTraits<AM>::NA];
-};
+// Threads per workgroup the register file allows for an M-tile count.
+constexpr int skinny_max_threads(int mt) { return mt >= 4 ? 512 : 1024; }
 
-template <int NT, int MT>
-struct WaveSrc {
-  rsrc_t wr[NT], sr[NT], ar;
-  uint32_t wv[NT], sv[NT], av[MT];  // per-lane byte offsets
-  uint32_t wk, sk;                  // bytes per k-block (weights), per group (scales)
-};
+// k-blocks of weights in flight per wave.  Measured on MI355X: about 10-16 MB
+// in flight chip-wide streams best; deeper rings lose bandwidth.
+constexpr int skinny_ring_depth(int nt) { return nt == 1 ? 4 : 2; }
 
-// 8 consecutive f32 -> hi / lo bf16 in natural order.
+// ---------------------------------------------------------------------------
+// staging into LDS
+// ---------------------------------------------------------------------------
+
+// 8 consecutive f32 -> hi / lo bf16 in natural column order.
 CAI4_DEV u32x4_t act_split_f32_nat(const f32x4_t &a, const f32x4_t &b, bool lo) {
   const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   uint32_t w[4];
@@ -97,62 +103,185 @@ CAI4_DEV u32x4_t act_split_f32_nat(const f32x4_t &a, const f32x4_t &b, bool lo) 
   return u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
-template <int NT, int MT, int AM, bool TR>
-CAI4_DEV void load_stage(Stage<NT, MT, AM, TR> &S, const WaveSrc<NT, MT> &W, int kb, int G,
-                         int glog2) {
-  const int kbase = kb * 128;
+// Activations of tokens [m0, m0 + mcount) and k-blocks [kr0, kr1) go to LDS as
+// bf16 planes [plane][row][column], row pitch act_stride bytes, columns in the
+// k-slot order of the weight layout (natural when tiled, the decode8 order of
+// the crate bytes otherwise), columns past K zero.  Staging is split in two:
+// act_issue loads one batch of 16-byte chunks into registers with
+// unconditional buffer loads -- invalid items get an out-of-range offset and
+// read 0 -- and act_store writes it.  The kernel issues the first batch
+// before the weight ring, so that storing it waits only for its own loads
+// (loads complete in order).
+//
+// Item i of a batch is chunk c of row t, i = t * cpr + c; a thread's items
+// are tid, tid + nth, ...  Pos steps (t, c) by nth without dividing.
+struct Pos {
+  int t, c;
+};
+CAI4_DEV Pos pos_start(int i, int per_row) {
+  const int t = i / per_row;
+  return Pos{t, i - t * per_row};
+}
+CAI4_DEV void pos_step(Pos &p, int dt, int dc, int per_row) {
+  p.t += dt;
+  p.c += dc;
+  if (p.c >= per_row) {
+    p.c -= per_row;
+    p.t += 1;
+  }
+}
+
+template <int B>
+CAI4_DEV void act_issue(const KParams &a, int m0, int mcount, int kr0, int kr1, Pos p, int dt,
+                        int dc, u32x4_t (&v)[2][B]) {
+  const int cpr = (kr1 - kr0) * 16;
+  const bool xf32 = a.amode == A_XF32, hilo = a.amode == A_HILO;
+  const uint32_t esz = xf32 ? 4u : 2u;
+  const size_t bytes = (size_t)a.M * a.ldx * esz;
+  const rsrc_t r0 = make_rsrc(a.x, bytes);
+  const rsrc_t r1 = make_rsrc(hilo ? a.x2 : a.x, bytes);
+#pragma unroll
+  for (int j = 0; j < B; ++j) {
+    const int col = kr0 * 128 + 8 * p.c;
+    const bool ok = p.t < mcount && col < a.K;
+    const uint32_t off = ok ? ((uint32_t)(m0 + p.t) * a.ldx + col) * esz : kOOB;
+    v[0][j] = __builtin_amdgcn_raw_buffer_load_b128(r0, off, 0, 0);
+    // second source: the lo plane, or the upper 4 floats of an f32 chunk
+    v[1][j] = __builtin_amdgcn_raw_buffer_load_b128(
+        r1, (ok && (hilo || xf32)) ? off + (xf32 ? 16u : 0u) : kOOB, 0, 0);
+    pos_step(p, dt, dc, cpr);
+  }
+}
+
+template <int B>
+CAI4_DEV void act_store(const KParams &a, uint8_t *lds, int mcount, int kr0, int kr1, Pos p,
+                        int dt, int dc, const u32x4_t (&v)[2][B]) {
+  const int cpr = (kr1 - kr0) * 16;
+  const uint32_t plane_bytes = (uint32_t)a.act_rows * a.act_stride;
+#pragma unroll
+  for (int j = 0; j < B; ++j) {
+    if (p.t >= mcount) break;
+    uint8_t *d = lds + (uint32_t)p.t * a.act_stride + 16 * p.c;
+    if (a.amode == A_XF32) {
+      const f32x4_t lo4 = __builtin_bit_cast(f32x4_t, v[0][j]);
+      const f32x4_t hi4 = __builtin_bit_cast(f32x4_t, v[1][j]);
+      *reinterpret_cast<u32x4_t *>(d) =
+          a.tiled ? act_split_f32_nat(lo4, hi4, false) : act_split_f32(lo4, hi4, false);
+      *reinterpret_cast<u32x4_t *>(d + plane_bytes) =
+          a.tiled ? act_split_f32_nat(lo4, hi4, true) : act_split_f32(lo4, hi4, true);
+    } else {
+      *reinterpret_cast<u32x4_t *>(d) = a.tiled ? v[0][j] : act_perm_bf16(v[0][j]);
+      if (a.amode == A_HILO)
+        *reinterpret_cast<u32x4_t *>(d + plane_bytes) = a.tiled ? v[1][j] : act_perm_bf16(v[1][j]);
+    }
+    pos_step(p, dt, dc, cpr);
+  }
+}
+
+// First row of weight tile `nt` of row unit `unit`.
+template <int NT, bool SW>
+CAI4_DEV int tile_row0(int unit, int nt) {
+  return SW ? 16 * unit : 16 * (unit * NT + nt);
+}
+
+// Scales of the workgroup's rw * NT tiles, groups [g_lo, g_lo + ngw), go to LDS
+// as f32 [slot][group][16 rows] (slot = r * NT + nt); rows past N read 0.
+// Tiled: an item is 8 rows of one group (16 contiguous bytes); crate: one
+// scale.  Positions (t = row group, c = item of the slot) step like the
+// activations'.  Issue / store split as for the activations.
+template <int NT, bool SW, int B>
+CAI4_DEV void sc_issue(const KParams &a, int unit0, int g_lo, int ngw, Pos p0, int dt, int dc,
+                       u32x4_t (&v)[NT][B]) {
+  const int NG = a.K / a.G;
+  const int per_slot = ngw * (a.tiled ? 2 : 16);
+  const size_t bytes =
+      a.tiled ? (size_t)((a.N + 15) / 16) * NG * 32 : (size_t)a.N * NG * 2;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    S.b[nt] = __builtin_amdgcn_raw_buffer_load_b128(W.wr[nt], W.wv[nt], kb * W.wk, 0);
-    if constexpr (TR) {
+    const rsrc_t rs = make_rsrc((SW && nt == 1) ? a.s1 : a.s0, bytes);
+    Pos p = p0;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int col = kbase + 32 * s;
-        const int g = glog2 >= 0 ? (col >> glog2) : col / G;
-        S.sb[nt][s] = __builtin_amdgcn_raw_buffer_load_b16(W.sr[nt], W.sv[nt], g * W.sk, 0);
+    for (int j = 0; j < B; ++j) {
+      const int row0 = tile_row0<NT, SW>(unit0 + p.t, nt);
+      if (a.tiled) {
+        const int g = p.c >> 1, h = p.c & 1;
+        const bool ok = p.t < a.rw && row0 < a.N;
+        const uint32_t off = ok ? (uint32_t)(((row0 >> 4) * NG + g_lo + g) * 16 + 8 * h) * 2 : kOOB;
+        v[nt][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+      } else {
+        const int g = p.c >> 4, row = row0 + (p.c & 15);
+        const bool ok = p.t < a.rw && row < a.N;
+        const uint32_t off = ok ? (uint32_t)(row * NG + g_lo + g) * 2 : kOOB;
+        v[nt][j] = u32x4_t{(uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0), 0u, 0u, 0u};
       }
-    } else {
-      const int g = glog2 >= 0 ? (kbase >> glog2) : kbase / G;
-      S.sb[nt][0] = __builtin_amdgcn_raw_buffer_load_b16(W.sr[nt], W.sv[nt], g * W.sk, 0);
-    }
-  }
-  constexpr int ESZ = AModeTraits<AM>::ESZ;
-  const int ks = kbase * ESZ;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      // step s sits at a constant column offset from the lane's first column
-      const uint32_t off = W.av[mt] + (TR ? 32 * s : 8 * s) * ESZ;
-      S.a[mt][s][0] = __builtin_amdgcn_raw_buffer_load_b128(W.ar, off, ks, 0);
-      if constexpr (AM == A_XF32)
-        S.a[mt][s][1] = __builtin_amdgcn_raw_buffer_load_b128(W.ar, off + 16, ks, 0);
+      pos_step(p, dt, dc, per_slot);
     }
   }
 }
 
-template <int AM, bool TILED>
-CAI4_DEV u32x4_t act_fragment(const u32x4_t (&r)[AModeTraits<AM>::NA], bool lo_half) {
-  if constexpr (AM == A_XF32) {
-    const f32x4_t a = __builtin_bit_cast(f32x4_t, r[0]), b = __builtin_bit_cast(f32x4_t, r[1]);
-    return TILED ? act_split_f32_nat(a, b, lo_half) : act_split_f32(a, b, lo_half);
-  } else {
-    return TILED ? r[0] : act_perm_bf16(r[0]);
+CAI4_DEV float scale_bits_f32(uint32_t bits, int sdt) {
+  return sdt ? scale_to_f32<SCALE_F16>(bits & 0xFFFFu) : scale_to_f32<SCALE_BF16>(bits & 0xFFFFu);
+}
+
+template <int NT, int B>
+CAI4_DEV void sc_store(const KParams &a, float *dst, int ngw, Pos p0, int dt, int dc,
+                       const u32x4_t (&v)[NT][B]) {
+  const int per_slot = ngw * (a.tiled ? 2 : 16);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    Pos p = p0;
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      if (p.t >= a.rw) break;
+      float *slot = dst + (size_t)(p.t * NT + nt) * ngw * 16;
+      if (a.tiled) {
+        const int g = p.c >> 1, h = p.c & 1;
+        const u32x4_t w = v[nt][j];
+        const f32x4_t f0 = {scale_bits_f32(w.x, a.sdt), scale_bits_f32(w.x >> 16, a.sdt),
+                            scale_bits_f32(w.y, a.sdt), scale_bits_f32(w.y >> 16, a.sdt)};
+        const f32x4_t f1 = {scale_bits_f32(w.z, a.sdt), scale_bits_f32(w.z >> 16, a.sdt),
+                            scale_bits_f32(w.w, a.sdt), scale_bits_f32(w.w >> 16, a.sdt)};
+        f32x4_t *d = reinterpret_cast<f32x4_t *>(slot + g * 16 + 8 * h);
+        d[0] = f0;
+        d[1] = f1;
+      } else {
+        slot[(p.c >> 4) * 16 + (p.c & 15)] = scale_bits_f32(v[nt][j].x, a.sdt);
+      }
+      pos_step(p, dt, dc, per_slot);
+    }
   }
 }
 
-// MFMAs of one k-block.
-template <int NT, int MT, int AM, bool TR, bool TILED>
-CAI4_DEV void compute_stage(Stage<NT, MT, AM, TR> &S, int kb, int K, int sdt, bool lo_half,
-                            f32x4_t (&acc)[MT][NT]) {
+// ---------------------------------------------------------------------------
+// the k-loop
+// ---------------------------------------------------------------------------
+
+template <int NT>
+CAI4_DEV void load_w(u32x4_t (&b)[NT], const rsrc_t (&wr)[NT], const uint32_t (&wv)[NT], int kb,
+                     uint32_t wk, bool live) {
+  const uint32_t koff = (uint32_t)kb * wk;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    b[nt] = __builtin_amdgcn_raw_buffer_load_b128(wr[nt], live ? wv[nt] + koff : kOOB, 0, 0);
+}
+
+// MFMAs of one k-block: weights from registers, activations and scales from LDS.
+template <int NT, int MT, bool TR>
+CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&abase)[MT],
+                         const uint32_t (&sbase)[NT], int k, int kr0, int g_lo, int K, int G,
+                         int glog2, f32x4_t (&acc)[MT][NT]) {
   const u32x4_t B136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
   const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  const uint32_t koff = (uint32_t)(k - kr0) * 256;
   u32x4_t af[MT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) af[mt][s] = act_fragment<AM, TILED>(S.a[mt][s], lo_half);
+    for (int s = 0; s < 4; ++s)
+      af[mt][s] = *reinterpret_cast<const u32x4_t *>(lds + abase[mt] + koff + (TR ? 64 * s : 16 * s));
+  const int kbase = k * 128;
   if constexpr (!TR) {
+    const int g = (glog2 >= 0 ? (kbase >> glog2) : kbase / G) - g_lo;
     f32x4_t corr[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -163,10 +292,9 @@ CAI4_DEV void compute_stage(Stage<NT, MT, AM, TR> &S, int kb, int K, int sdt, bo
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float sc =
-          sdt ? scale_to_f32<SCALE_F16>(S.sb[nt][0]) : scale_to_f32<SCALE_BF16>(S.sb[nt][0]);
-      const u32x4_t d0 = decode8(S.b[nt].x), d1 = decode8(S.b[nt].y);
-      const u32x4_t d2 = decode8(S.b[nt].z), d3 = decode8(S.b[nt].w);
+      const float sc = *reinterpret_cast<const float *>(lds + sbase[nt] + 64 * g);
+      const u32x4_t d0 = decode8(b[nt].x), d1 = decode8(b[nt].y);
+      const u32x4_t d2 = decode8(b[nt].z), d3 = decode8(b[nt].w);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         f32x4_t p = mfma_bf16(af[mt][0], d0, corr[mt]);
@@ -177,21 +305,21 @@ CAI4_DEV void compute_stage(Stage<NT, MT, AM, TR> &S, int kb, int K, int sdt, bo
       }
     }
   } else {
-    const int nsteps = min(4, (K - kb * 128) >> 5);
+    const int nsteps = min(4, (K - kbase) >> 5);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) S.b[nt] = xpose_rows(S.b[nt]);
+    for (int nt = 0; nt < NT; ++nt) b[nt] = xpose_rows(b[nt]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s >= nsteps) break;
+      const int col = kbase + 32 * s;
+      const int g = (glog2 >= 0 ? (col >> glog2) : col / G) - g_lo;
       f32x4_t corr[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) corr[mt] = mfma_bf16(af[mt][s], B136, zero4);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const float sc = sdt ? scale_to_f32<SCALE_F16>(S.sb[nt][s])
-                             : scale_to_f32<SCALE_BF16>(S.sb[nt][s]);
-        const uint32_t dw =
-            s == 0 ? S.b[nt].x : s == 1 ? S.b[nt].y : s == 2 ? S.b[nt].z : S.b[nt].w;
+        const float sc = *reinterpret_cast<const float *>(lds + sbase[nt] + 64 * g);
+        const uint32_t dw = s == 0 ? b[nt].x : s == 1 ? b[nt].y : s == 2 ? b[nt].z : b[nt].w;
         const u32x4_t d = decode8(dw);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -201,54 +329,6 @@ CAI4_DEV void compute_stage(Stage<NT, MT, AM, TR> &S, int kb, int K, int sdt, bo
       }
     }
   }
-}
-
-// One wave's k-blocks [kb0, kb1) through a U-deep register ring.
-template <int NT, int MT, int AM, bool TR, bool TILED, int U>
-CAI4_DEV void skinny_accumulate(const WaveSrc<NT, MT> &W, int K, int G, int glog2, int sdt,
-                                int kb0, int kb1, f32x4_t (&acc)[MT][NT]) {
-  const bool lo_half = AM != A_BF16 && (threadIdx.x & 15) >= 8;
-  Stage<NT, MT, AM, TR> ring[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) load_stage<NT, MT, AM, TR>(ring[u], W, kb0 + u, G, glog2);
-  for (int kb = kb0; kb < kb1; kb += U) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = kb + u;
-      if (k < kb1) {
-        compute_stage<NT, MT, AM, TR, TILED>(ring[u], k, K, sdt, lo_half, acc);
-        // past kb1 this prefetch reads other valid bytes or 0; never consumed
-        load_stage<NT, MT, AM, TR>(ring[u], W, k + U, G, glog2);
-      }
-    }
-  }
-}
-
-// Sum the per-wave accumulators of a workgroup in wave order through LDS.
-// Returns true in wave 0, which then holds the totals.
-template <int MT, int NT>
-CAI4_DEV bool wg_reduce(f32x4_t (&acc)[MT][NT], f32x4_t *red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  constexpr int NI = MT * NT;
-  if (nw > 1) {
-    if (wave > 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          red[((size_t)(wave - 1) * NI + mt * NT + nt) * 64 + lane] = acc[mt][nt];
-    }
-    __syncthreads();
-    if (wave != 0) return false;
-    for (int w = 1; w < nw; ++w) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          acc[mt][nt] += red[((size_t)(w - 1) * NI + mt * NT + nt) * 64 + lane];
-    }
-  }
-  return true;
 }
 
 // hi + lo token slots: lanes 0-31 receive the lo half from lanes 32-63.
@@ -266,105 +346,34 @@ CAI4_DEV void fold_hilo(f32x4_t (&acc)[MT][NT]) {
       }
 }
 
-// Threads per workgroup the register file allows for an M-tile count.
-constexpr int skinny_max_threads(int mt) { return mt >= 4 ? 256 : (mt == 2 ? 512 : 1024); }
-
-template <int NT, int MT, int AM, bool TR, bool TILED, int EPI, int U>
-__global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(SkinnyArgs a) {
-  extern __shared__ f32x4_t red[];
+// Output of one wave's row unit: D lane l holds weight row l % 16 and token
+// slots 4 * (l / 16) + v.
+template <int NT, int MT, bool SW>
+CAI4_DEV void epilogue(const KParams &a, f32x4_t (&acc)[MT][NT], int unit, int m0,
+                       int mcount) {
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
-  constexpr int TPM = AModeTraits<AM>::TPM;
-  constexpr int ESZ = AModeTraits<AM>::ESZ;
-  constexpr bool SWIGLU = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_HILO;
-  constexpr int NOUT = SWIGLU ? NT / 2 : NT;
-
-  const int out_row0 = blockIdx.x * 16 * NOUT;
-  const int m0 = blockIdx.y * TPM * MT;
-  const int mcount = min(a.M - m0, TPM * MT);
-  const int kb_total = (a.K + 127) / 128;
-  const int ngroups = a.K / a.G;
-
-  WaveSrc<NT, MT> W;
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const bool up = SWIGLU && nt >= NOUT;
-    const int r0 = out_row0 + 16 * (up ? nt - NOUT : nt);  // the tile's first row (uniform)
-    const uint8_t *wb = up ? a.w1 : a.w0;
-    const uint8_t *sb = up ? a.s1 : a.s0;
-    const size_t rows_left = r0 < a.N ? (size_t)(a.N - r0) : 0;
-    if (TILED) {
-      const size_t T = (size_t)(r0 >> 4);
-      const bool live = rows_left > 0;
-      W.wr[nt] = make_rsrc(wb + T * kb_total * 1024, live ? (size_t)kb_total * 1024 : 0);
-      W.sr[nt] = make_rsrc(sb + T * ngroups * 32, live ? (size_t)ngroups * 32 : 0);
-      W.wv[nt] = 16 * lane;
-      W.sv[nt] = 2 * lr;
-    } else {
-      const size_t rb = (size_t)a.K / 2;
-      W.wr[nt] = make_rsrc(wb + (size_t)r0 * rb, rows_left * rb);
-      W.sr[nt] = make_rsrc(sb + (size_t)r0 * ngroups * 2, rows_left * ngroups * 2);
-      W.wv[nt] = lr * (uint32_t)rb + 16 * lg;
-      W.sv[nt] = lr * (uint32_t)ngroups * 2;
-    }
-  }
-  W.wk = TILED ? 1024 : 64;
-  W.sk = TILED ? 32 : 2;
-  // activations: one descriptor over [x, x + M rows) (both planes for A_HILO)
-  {
-    const size_t plane = (size_t)a.M * a.ldx * ESZ;
-    const size_t gap =
-        AM == A_HILO ? (size_t)((const uint8_t *)a.x2 - (const uint8_t *)a.x) : (size_t)0;
-    W.ar = make_rsrc(a.x, gap + plane);
-    const uint32_t plane_off = (AM == A_HILO && lr >= 8) ? (uint32_t)gap : 0u;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int idx = mt * TPM + (AM == A_BF16 ? lr : (lr & 7));
-      const int col0 = TR ? 8 * lg : 32 * lg;
-      W.av[mt] = idx < mcount
-                     ? plane_off + (uint32_t)(((size_t)(m0 + idx) * a.ldx + col0) * ESZ)
-                     : kOOB;  // past M: reads 0, never stored
-    }
-  }
-
-  const int per = (kb_total + nw - 1) / nw;
-  const int kb0 = min(wave * per, kb_total), kb1 = min(kb0 + per, kb_total);
-
-  f32x4_t acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  if (mcount > 0 && kb0 < kb1)
-    skinny_accumulate<NT, MT, AM, TR, TILED, U>(W, a.K, a.G, a.glog2, a.sdt, kb0, kb1, acc);
-
-  if (!wg_reduce<MT, NT>(acc, red)) return;
-  if (mcount <= 0) return;
-  if constexpr (AM != A_BF16) {
+  const bool hilo = a.amode != A_BF16;
+  const int tpm = hilo ? 8 : 16;
+  constexpr int NOUT = SW ? NT / 2 : NT;
+  if (hilo) {
     fold_hilo<MT, NT>(acc);
     if (lg >= 2) return;
   }
-
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int nt = 0; nt < NOUT; ++nt) {
-      const int row = out_row0 + 16 * nt + lr;
+      const int row = tile_row0<NT, SW>(unit, nt) + lr;
       if (row >= a.N) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int ti = mt * TPM + 4 * lg + v;
+        const int ti = mt * tpm + 4 * lg + v;
         if (ti >= mcount) continue;
         const size_t o = (size_t)(m0 + ti) * a.ldo + row;
         const float y = acc[mt][nt][v];
-        if constexpr (EPI == EPI_F32) {
-          reinterpret_cast<float *>(a.out)[o] = y;
-        } else if constexpr (EPI == EPI_BF16) {
-          reinterpret_cast<uint16_t *>(a.out)[o] = (uint16_t)f32_to_bf16_rne(y);
-        } else {
+        if constexpr (SW) {
           const float h = silu_f32(y) * acc[mt][nt + NOUT][v];
-          if constexpr (EPI == EPI_SWIGLU) {
+          if (a.epi == EPI_SWIGLU) {
             reinterpret_cast<float *>(a.out)[o] = h;
           } else {
             // hi = h truncated to bf16, lo = bf16(h - hi): the A_HILO planes
@@ -373,112 +382,347 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(SkinnyAr
             reinterpret_cast<uint16_t *>(a.out)[o] = (uint16_t)hb;
             reinterpret_cast<uint16_t *>(a.out2)[o] = (uint16_t)f32_to_bf16_rne(lo);
           }
+        } else {
+          if (a.epi == EPI_BF16)
+            reinterpret_cast<uint16_t *>(a.out)[o] = (uint16_t)f32_to_bf16_rne(y);
+          else
+            reinterpret_cast<float *>(a.out)[o] = y;
         }
       }
     }
   }
 }
 
+template <int NT, int MT, bool TR, bool SW>
+__global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int U = skinny_ring_depth(NT);
+  constexpr int NI = MT * NT;
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rwi = wave % a.rw, kwi = wave / a.rw;
+  const bool hilo = a.amode != A_BF16;
+  const int tpm = hilo ? 8 : 16;
+  const int unit0 = blockIdx.x * a.rw, unit = unit0 + rwi;
+  const int m0 = blockIdx.y * tpm * MT;
+  const int mcount = min(a.M - m0, tpm * MT);
+  const int kb_total = (a.K + 127) >> 7;
+  const int kr0 = blockIdx.z * a.kper, kr1 = min(kr0 + a.kper, kb_total);
+  const int col_hi = min(a.K, kr1 * 128);
+  const int g_lo = (kr0 * 128) / a.G, ngw = (col_hi + a.G - 1) / a.G - g_lo;
+
+  // weight sources of this wave's tiles
+  rsrc_t wr[NT];
+  uint32_t wv[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int r0 = tile_row0<NT, SW>(unit, nt);
+    const uint8_t *wb = (SW && nt == 1) ? a.w1 : a.w0;
+    const size_t rows_left = r0 < a.N ? (size_t)(a.N - r0) : 0;
+    if (a.tiled) {
+      const size_t T = (size_t)(r0 >> 4);
+      wr[nt] = make_rsrc(wb + T * kb_total * 1024, rows_left ? (size_t)kb_total * 1024 : 0);
+      wv[nt] = 16 * lane;
+    } else {
+      const size_t rb = (size_t)a.K / 2;
+      wr[nt] = make_rsrc(wb + (size_t)r0 * rb, rows_left * rb);
+      wv[nt] = lr * (uint32_t)rb + 16 * lg;
+    }
+  }
+  const uint32_t wk = a.tiled ? 1024u : 64u;
+
+  // this wave's span of k-blocks
+  const int nkb = kr1 - kr0, per = (nkb + a.kw - 1) / a.kw;
+  const int kb0 = kr0 + min(kwi * per, nkb), kb1 = kr0 + min(kwi * per + per, nkb);
+
+  // Staging loads first, then the weight ring: loads complete in order, so
+  // storing the staged batch waits only for the staging loads.
+  constexpr int BA = 4, BS = 2;
+  const int nth = blockDim.x, tid = threadIdx.x;
+  const int cpr = (kr1 - kr0) * 16, spr = ngw * (a.tiled ? 2 : 16);
+  // thread positions and per-item steps (one division each, per thread)
+  const Pos pa = pos_start(tid, cpr), ps = pos_start(tid, spr);
+  const Pos da = pos_start(nth, cpr), ds = pos_start(nth, spr);
+  float *lds_sc = reinterpret_cast<float *>(lds + a.scale_off);
+  u32x4_t av[2][BA];
+  u32x4_t sv[NT][BS];
+  act_issue<BA>(a, m0, mcount, kr0, kr1, pa, da.t, da.c, av);
+  sc_issue<NT, SW, BS>(a, unit0, g_lo, ngw, ps, ds.t, ds.c, sv);
+  u32x4_t ring[U][NT];
+#pragma unroll
+  for (int u = 0; u < U; ++u) load_w<NT>(ring[u], wr, wv, kb0 + u, wk, kb0 + u < kb1);
+  act_store<BA>(a, lds, mcount, kr0, kr1, pa, da.t, da.c, av);
+  sc_store<NT, BS>(a, lds_sc, ngw, ps, ds.t, ds.c, sv);
+  // larger stagings: the remaining batches (these wait for the ring too)
+  for (int base = BA * nth; base < mcount * cpr; base += BA * nth) {
+    const Pos p = pos_start(base + tid, cpr);
+    act_issue<BA>(a, m0, mcount, kr0, kr1, p, da.t, da.c, av);
+    act_store<BA>(a, lds, mcount, kr0, kr1, p, da.t, da.c, av);
+  }
+  for (int base = BS * nth; base < a.rw * spr; base += BS * nth) {
+    const Pos p = pos_start(base + tid, spr);
+    sc_issue<NT, SW, BS>(a, unit0, g_lo, ngw, p, ds.t, ds.c, sv);
+    sc_store<NT, BS>(a, lds_sc, ngw, p, ds.t, ds.c, sv);
+  }
+  __syncthreads();
+
+  // Token slots past mcount read token 0's row: MFMA rows are independent and
+  // those output rows are never stored, so no predicate is needed.
+  uint32_t abase[MT];
+  const uint32_t plane_bytes = (uint32_t)a.act_rows * a.act_stride;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int tok = mt * tpm + (hilo ? (lr & 7) : lr);
+    abase[mt] = (hilo && lr >= 8 ? plane_bytes : 0u) +
+                (uint32_t)(tok < mcount ? tok : 0) * a.act_stride + (TR ? 16u * lg : 64u * lg);
+  }
+  uint32_t sbase[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    sbase[nt] = a.scale_off + (uint32_t)(((rwi * NT + nt) * ngw * 16 + lr) * 4);
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  if (mcount > 0) {
+    for (int kb = kb0; kb < kb1; kb += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = kb + u;
+        if (k < kb1) {
+          compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, k, kr0, g_lo, a.K, a.G, a.glog2,
+                                 acc);
+          load_w<NT>(ring[u], wr, wv, k + U, wk, k + U < kb1);
+        }
+      }
+    }
+  }
+
+  // add the kw spans of each row group in wave order (LDS reused)
+  __syncthreads();
+  f32x4_t *red = reinterpret_cast<f32x4_t *>(lds);
+  if (a.kw > 1) {
+    if (kwi > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          red[((size_t)((kwi - 1) * a.rw + rwi) * NI + mt * NT + nt) * 64 + lane] = acc[mt][nt];
+    }
+    __syncthreads();
+    if (kwi > 0) return;
+    for (int w = 1; w < a.kw; ++w) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] += red[((size_t)((w - 1) * a.rw + rwi) * NI + mt * NT + nt) * 64 + lane];
+    }
+  }
+  if (mcount <= 0) return;
+  if (gridDim.z > 1) {
+    const size_t base =
+        (((size_t)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * a.rw + rwi) * NI;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) a.part[(base + mt * NT + nt) * 64 + lane] = acc[mt][nt];
+    return;
+  }
+  epilogue<NT, MT, SW>(a, acc, unit, m0, mcount);
+}
+
+// Split-K: add the ksplit partials of each row unit in split order, then the
+// epilogue.  One wave per row unit.
+template <int NT, int MT, bool SW>
+__global__ __launch_bounds__(1024) void splitk_reduce_kernel(KParams a, int ksplit) {
+  constexpr int NI = MT * NT;
+  const int lane = threadIdx.x & 63;
+  const int rwi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tpm = a.amode != A_BF16 ? 8 : 16;
+  const int m0 = blockIdx.y * tpm * MT;
+  const int mcount = min(a.M - m0, tpm * MT);
+  if (mcount <= 0) return;
+  const size_t zstride = (size_t)gridDim.y * gridDim.x * a.rw * NI * 64;
+  const size_t base =
+      (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * a.rw + rwi) * NI * 64 + lane;
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = a.part[base + (mt * NT + nt) * 64];
+  for (int z = 1; z < ksplit; ++z) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[mt][nt] += a.part[z * zstride + base + (mt * NT + nt) * 64];
+  }
+  epilogue<NT, MT, SW>(a, acc, blockIdx.x * a.rw + rwi, m0, mcount);
+}
+
 // ---------------------------------------------------------------------------
 // host-side planning and dispatch
 // ---------------------------------------------------------------------------
 
-// k-blocks in flight per wave (register ring depth), chosen so that MT = 1
-// stays within 128 VGPRs (4 waves per SIMD).
-constexpr int skinny_ring_depth(int nt, int mt, int am, bool tr) {
-  return mt == 1 ? ((am == A_XF32 || tr) ? 2 : (nt == 1 ? 4 : 3)) : 2;
+namespace {
+
+int env_int(const char *name, int lo, int hi) {
+  if (const char *ev = getenv(name)) {
+    const int v = atoi(ev);
+    if (v >= lo && v <= hi) return v;
+  }
+  return 0;
 }
 
-SkinnyPlan skinny_plan(int N, int K, int M, int amode, int epi, int num_cus) {
+size_t round16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+}  // namespace
+
+SkinnyPlan skinny_plan(int N, int K, int G, int M, int amode, int epi, const SkinnyDevice &d) {
   SkinnyPlan p{};
   const int tpm = amode == A_BF16 ? 16 : 8;
+  const int planes = amode == A_BF16 ? 1 : 2;
   int mt = (M + tpm - 1) / tpm;
   if (mt > 4) mt = 4;
   if (mt == 3) mt = 4;
-  if (amode == A_XF32 && mt > 2) mt = 2;  // f32 activations: at most 16 tokens per pass
   p.mt = mt;
   p.m_chunks = (M + tpm * mt - 1) / (tpm * mt);
-  const bool swiglu = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
+  p.act_rows = M < tpm * mt ? M : tpm * mt;
+  const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
   const int kb_total = (K + 127) / 128;
-  const int maxw = (mt >= 4 ? 256 : (mt == 2 ? 512 : 1024)) / 64;
-  // aim for ~4 resident waves per SIMD across the chip
-  const long target = 16L * num_cus;
-  auto rows_per_block = [&](int nt) { return 16 * (swiglu ? nt / 2 : nt); };
+  const int maxw = skinny_max_threads(mt) / 64;
+  const long target = 16L * d.num_cus;  // about 4 resident waves per SIMD
+  // weight tiles per wave: a gate/up pair, else 2 unless that leaves too few waves
   p.nt = 2;
-  if (!swiglu) {
-    const long rb2 = (N + 31) / 32;
-    if (rb2 * p.m_chunks * maxw < target) p.nt = 1;  // too few row blocks: halve them
+  if (!sw && (long)((N + 31) / 32) * p.m_chunks * maxw < target) p.nt = 1;
+  const int nout = sw ? 1 : p.nt;
+  const long units = (N + 16 * nout - 1) / (16 * nout);
+  // row groups sharing one copy of the staged activations: grow until the
+  // staging traffic is at most half the weight bytes, and beyond that while
+  // every CU still gets a workgroup (fewer, fuller workgroups stage less)
+  const double wbytes = (sw ? 2.0 : 1.0) * N * (K / 2.0);
+  int rw = 1;
+  while (rw < maxw && rw < units) {
+    const double sbytes =
+        (double)((units + rw - 1) / rw) * p.m_chunks * p.act_rows * planes * 2.0 * K;
+    const long wgs_next = (units + 2 * rw - 1) / (2 * rw) * p.m_chunks;
+    if (2.0 * sbytes <= wbytes && (rw >= 2 || wgs_next < d.num_cus)) break;
+    rw *= 2;
   }
-  p.row_blocks = (N + rows_per_block(p.nt) - 1) / rows_per_block(p.nt);
-  long w = target / ((long)p.row_blocks * p.m_chunks);  // never beyond one resident round
-  int waves = (int)(w < 1 ? 1 : (w > maxw ? maxw : w));
-  // tuning override: CASCADIA_INT4_SKINNY_WAVES=<1..16>
-  if (const char *ev = getenv("CASCADIA_INT4_SKINNY_WAVES")) {
-    const int v = atoi(ev);
-    if (v >= 1 && v <= 16) waves = v;
+  if (rw > maxw) rw = maxw;
+  if (int v = env_int("CASCADIA_INT4_SKINNY_RW", 1, 16)) rw = v <= maxw ? v : maxw;
+  p.rw = rw;
+  p.row_blocks = (int)((units + rw - 1) / rw);
+  const long wgs0 = (long)p.row_blocks * p.m_chunks;
+  auto lds_need = [&](int kper, int kw) {
+    const size_t stride = (size_t)kper * 256 + 16;
+    const size_t act = (size_t)planes * p.act_rows * stride;
+    const size_t ngw = ((size_t)kper * 128 + G - 1) / G + 1;
+    const size_t sc = (size_t)rw * p.nt * ngw * 64;
+    const size_t red = (size_t)(kw - 1) * rw * mt * p.nt * 1024;
+    const size_t st = round16(act) + sc;
+    return st > red ? st : red;
+  };
+  const int ks_env = env_int("CASCADIA_INT4_SKINNY_KSPLIT", 1, 64);
+  const int kw_env = env_int("CASCADIA_INT4_SKINNY_WAVES", 1, 16);
+  int ksplit = 1, kper = kb_total, kw = 1;
+  // a forced split is a minimum: LDS must fit whatever the override says
+  for (int ks = ks_env ? ks_env : 1; ks <= kb_total; ++ks) {
+    kper = (kb_total + ks - 1) / ks;
+    ksplit = (kb_total + kper - 1) / kper;
+    long w = target / (wgs0 * ksplit * rw);
+    kw = (int)(w < 1 ? 1 : (w > maxw / rw ? maxw / rw : w));
+    if (kw_env) kw = kw_env / rw < 1 ? 1 : (kw_env / rw > maxw / rw ? maxw / rw : kw_env / rw);
+    if (kw > kper) kw = kper;
+    const size_t budget = (size_t)((double)d.max_lds * rw * kw / 16.0);
+    const size_t need = lds_need(kper, kw);
+    if (need > d.max_lds && ksplit < kb_total) continue;
+    const bool fits = need <= (budget < 16384 ? 16384 : budget);
+    // every CU gets a workgroup, and the chip at least half its target waves
+    const bool full = wgs0 * ksplit >= d.num_cus && wgs0 * ksplit * rw * kw * 2 >= target;
+    if (ks_env || (fits && full) || ksplit >= 64) break;
   }
-  if (waves > maxw) waves = maxw;
-  if (waves > kb_total) waves = kb_total < 1 ? 1 : kb_total;
-  p.waves = waves;
-  p.lds_bytes = (size_t)(waves - 1) * p.mt * p.nt * 64 * sizeof(f32x4_t);
+  p.ksplit = ksplit;
+  p.kper = kper;
+  p.kw = kw;
+  p.act_stride = kper * 256 + 16;
+  p.scale_off = (int)round16((size_t)planes * p.act_rows * p.act_stride);
+  p.lds_bytes = lds_need(kper, kw);
+  p.partial_bytes =
+      ksplit > 1 ? (size_t)ksplit * wgs0 * rw * mt * p.nt * 64 * sizeof(f32x4_t) : 0;
   return p;
 }
 
-template <int NT, int MT, int AM, bool TR, bool TILED, int EPI>
-static hipError_t launch_one(const SkinnyArgs &a, const SkinnyPlan &p, hipStream_t st) {
-  dim3 grid(p.row_blocks, p.m_chunks, 1), block(64 * p.waves, 1, 1);
-  constexpr int U = skinny_ring_depth(NT, MT, AM, TR);
-  hipLaunchKernelGGL((skinny_kernel<NT, MT, AM, TR, TILED, EPI, U>), grid, block, p.lds_bytes, st,
-                     a);
-  return hipGetLastError();
-}
+namespace {
 
-template <int AM, bool TR, bool TILED, int EPI>
-static hipError_t launch_mt(const SkinnyArgs &a, const SkinnyPlan &p, hipStream_t st) {
-  constexpr bool SW = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_HILO;
-  if constexpr (!SW) {
-    if (p.nt == 1) {
-      if (p.mt == 1) return launch_one<1, 1, AM, TR, TILED, EPI>(a, p, st);
-      if constexpr (AM == A_XF32) return launch_one<1, 2, AM, TR, TILED, EPI>(a, p, st);
-      if (p.mt == 2) return launch_one<1, 2, AM, TR, TILED, EPI>(a, p, st);
-      if constexpr (AM != A_XF32) return launch_one<1, 4, AM, TR, TILED, EPI>(a, p, st);
-    }
+template <int NT, int MT, bool TR, bool SW>
+hipError_t launch_one(const KParams &k, const SkinnyPlan &p, hipStream_t st) {
+  dim3 grid(p.row_blocks, p.m_chunks, p.ksplit), block(64 * p.rw * p.kw, 1, 1);
+  hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW>), grid, block, p.lds_bytes, st, k);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (p.ksplit > 1) {
+    dim3 g2(p.row_blocks, p.m_chunks, 1), b2(64 * p.rw, 1, 1);
+    hipLaunchKernelGGL((splitk_reduce_kernel<NT, MT, SW>), g2, b2, 0, st, k, p.ksplit);
+    return hipGetLastError();
   }
-  if (p.mt == 1) return launch_one<2, 1, AM, TR, TILED, EPI>(a, p, st);
-  if constexpr (AM == A_XF32) return launch_one<2, 2, AM, TR, TILED, EPI>(a, p, st);
-  if (p.mt == 2) return launch_one<2, 2, AM, TR, TILED, EPI>(a, p, st);
-  if constexpr (AM != A_XF32) return launch_one<2, 4, AM, TR, TILED, EPI>(a, p, st);
-  return hipErrorInvalidValue;
+  return hipSuccess;
 }
 
-template <int AM, bool TR, bool TILED>
-static hipError_t launch_epi(const SkinnyArgs &a, const SkinnyPlan &p, int epi,
-                             hipStream_t st) {
-  switch (epi) {
-    case EPI_F32: return launch_mt<AM, TR, TILED, EPI_F32>(a, p, st);
-    case EPI_BF16: return launch_mt<AM, TR, TILED, EPI_BF16>(a, p, st);
-    case EPI_SWIGLU: return launch_mt<AM, TR, TILED, EPI_SWIGLU>(a, p, st);
-    default: return launch_mt<AM, TR, TILED, EPI_SWIGLU_HILO>(a, p, st);
+template <int NT, bool TR, bool SW>
+hipError_t launch_mt(const KParams &k, const SkinnyPlan &p, hipStream_t st) {
+  switch (p.mt) {
+    case 1: return launch_one<NT, 1, TR, SW>(k, p, st);
+    case 2: return launch_one<NT, 2, TR, SW>(k, p, st);
+    default: return launch_one<NT, 4, TR, SW>(k, p, st);
   }
 }
 
-template <int AM>
-static hipError_t launch_tr(const SkinnyArgs &a, const SkinnyPlan &p, int epi, hipStream_t st) {
-  const bool tr = (a.G % 128) != 0;
-  if (a.tiled)
-    return tr ? launch_epi<AM, true, true>(a, p, epi, st)
-              : launch_epi<AM, false, true>(a, p, epi, st);
-  return tr ? launch_epi<AM, true, false>(a, p, epi, st)
-            : launch_epi<AM, false, false>(a, p, epi, st);
+template <bool TR>
+hipError_t launch_nt(const KParams &k, const SkinnyPlan &p, bool sw, hipStream_t st) {
+  if (sw) return launch_mt<2, TR, true>(k, p, st);
+  if (p.nt == 1) return launch_mt<1, TR, false>(k, p, st);
+  return launch_mt<2, TR, false>(k, p, st);
 }
+
+}  // namespace
 
 hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, int epi,
                          hipStream_t st) {
-  switch (amode) {
-    case A_BF16: return launch_tr<A_BF16>(a, p, epi, st);
-    case A_XF32: return launch_tr<A_XF32>(a, p, epi, st);
-    default: return launch_tr<A_HILO>(a, p, epi, st);
-  }
+  if (p.ksplit > 1 && !a.partials) return hipErrorInvalidValue;
+  KParams k{};
+  k.w0 = a.w0;
+  k.w1 = a.w1;
+  k.s0 = a.s0;
+  k.s1 = a.s1;
+  k.x = a.x;
+  k.x2 = a.x2;
+  k.out = a.out;
+  k.out2 = a.out2;
+  k.part = static_cast<f32x4_t *>(a.partials);
+  k.N = a.N;
+  k.K = a.K;
+  k.G = a.G;
+  k.M = a.M;
+  k.ldx = a.ldx;
+  k.ldo = a.ldo;
+  k.sdt = a.sdt;
+  k.glog2 = a.glog2;
+  k.tiled = a.tiled;
+  k.amode = amode;
+  k.epi = epi;
+  k.rw = p.rw;
+  k.kw = p.kw;
+  k.kper = p.kper;
+  k.act_rows = p.act_rows;
+  k.act_stride = p.act_stride;
+  k.scale_off = p.scale_off;
+  const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
+  const bool tr = (a.G % 128) != 0;
+  return tr ? launch_nt<true>(k, p, sw, st) : launch_nt<false>(k, p, sw, st);
 }
 
 }  // namespace cai4

@@ -10,30 +10,42 @@ namespace cai4 {
 // or as the two bf16 planes (hi, lo) that A_HILO consumes.
 enum Epilogue { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_BF16 = 2, EPI_SWIGLU_HILO = 3 };
 
-// Activation modes: bf16; f32 split in-kernel into hi/lo bf16; precomputed
-// hi/lo bf16 planes (x = hi plane, x2 = lo plane).
+// Activation modes: bf16; f32 (split into hi/lo bf16 planes while staged);
+// precomputed hi/lo bf16 planes (x = hi plane, x2 = lo plane).
 enum AMode { A_BF16 = 0, A_XF32 = 1, A_HILO = 2 };
 
 struct SkinnyArgs {
-  const uint8_t *w0;  // packed [N, K/2]           (gate for the SwiGLU epilogues)
-  const uint8_t *w1;  // packed [N, K/2] up matrix (SwiGLU epilogues only)
-  const uint8_t *s0;  // scales u16 [N, K/G]
+  const uint8_t *w0;  // packed weights (gate for the SwiGLU epilogues)
+  const uint8_t *w1;  // up matrix (SwiGLU epilogues only)
+  const uint8_t *s0;  // scales u16
   const uint8_t *s1;
   const void *x;      // activations [M, ldx]: bf16 bits, f32, or the hi plane
   const void *x2;     // A_HILO: the lo plane [M, ldx]
   void *out;          // [M, ldo]: f32, bf16 bits, or the hi plane (EPI_SWIGLU_HILO)
   void *out2;         // EPI_SWIGLU_HILO: the lo plane
+  void *partials;     // split-K partial sums (SkinnyPlan::partial_bytes), or null
   int N, K, G, M, ldx, ldo, sdt;
   int glog2;  // log2(G) when G is a power of two, else -1
   int tiled;  // weights/scales in the MFMA-tiled device layout (layout.hip)
 };
 
+// Launch plan.  A workgroup has rw x kw waves: rw row groups (each nt weight
+// tiles of 16 rows) share the activations staged in LDS; kw waves split the
+// workgroup's k-range.  ksplit > 1 splits K across workgroups, whose partial
+// sums a second kernel adds in a fixed order.
 struct SkinnyPlan {
-  int nt, mt, waves, row_blocks, m_chunks;
-  size_t lds_bytes;
+  int nt, mt, rw, kw, ksplit, kper, row_blocks, m_chunks;
+  int act_rows, act_stride, scale_off;
+  size_t lds_bytes, partial_bytes;
 };
 
-SkinnyPlan skinny_plan(int N, int K, int M, int amode, int epi, int num_cus);
+// Device properties the planner uses (the library caches them per device).
+struct SkinnyDevice {
+  int num_cus;
+  size_t max_lds;  // LDS bytes a workgroup may use
+};
+
+SkinnyPlan skinny_plan(int N, int K, int G, int M, int amode, int epi, const SkinnyDevice &d);
 hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, int epi,
                          hipStream_t st);
 

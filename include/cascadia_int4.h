@@ -148,8 +148,11 @@ int cascadia_int4_tile_expert(uint32_t hidden, uint32_t inter, uint32_t group_si
                               const cascadia_int4_expert *src, uint8_t *dst,
                               cascadia_int4_expert *out, void *stream);
 
-/* Workspace bytes the expert / FFN entry points need for n_tokens rows. */
-size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32_t n_tokens);
+/* Workspace bytes the expert / FFN entry points need for n_tokens rows on the
+ * current device (the launch plan depends on its CU count); 0 on bad
+ * arguments.  No counterpart in the crate, which allocates per call. */
+size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                         uint32_t n_tokens);
 
 /* expert_forward for n_tokens independent rows: out = bf16(W_d ·
  * (silu(W_g·x) ⊙ (W_u·x))) with x bf16, everything inside f32, one RNE

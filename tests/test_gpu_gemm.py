@@ -130,6 +130,59 @@ def test_gemm_multi_f32_and_bf16_inputs(cl, orc, n, k, group, sdt, seq):
     assert_f32_close(host(ys).reshape(seq, n), want_b, f"bf16 in {n}x{k} G{group} seq{seq}")
 
 
+PLANS = [  # forced launch plans: row groups, waves per workgroup, split-K
+    {"CASCADIA_INT4_SKINNY_RW": "2", "CASCADIA_INT4_SKINNY_WAVES": "4"},
+    {"CASCADIA_INT4_SKINNY_KSPLIT": "3", "CASCADIA_INT4_SKINNY_WAVES": "2"},
+    {"CASCADIA_INT4_SKINNY_RW": "4", "CASCADIA_INT4_SKINNY_KSPLIT": "2"},
+    {"CASCADIA_INT4_SKINNY_WAVES": "16", "CASCADIA_INT4_SKINNY_KSPLIT": "5"},
+]
+
+
+@pytest.mark.parametrize("plan", range(len(PLANS)))
+@pytest.mark.parametrize("n,k,group,sdt,seq", [(96, 1536, 32, BF16, 8), (130, 1152, 128, F16, 17),
+                                                (300, 2048, 64, F16, 1), (64, 4096, 128, F16, 40)])
+def test_forced_launch_plans(cl, orc, monkeypatch, plan, n, k, group, sdt, seq):
+    """Every decomposition (row groups sharing staged activations, k-spans per
+    workgroup, split-K across workgroups + the reduce kernel) matches the
+    oracle, for both weight layouts and all activation kinds."""
+    for key, val in PLANS[plan].items():
+        monkeypatch.setenv(key, val)
+    packed, scales = weights(orc, n, k, group, sdt, 3 * n + seq)
+    P, S = dev(packed), dev(scales)
+    pt, st = cl.tile_weights(P, S, n, k, group)
+    xs = orc.fill_normal_f32(seq, 17, seq * k)
+    xb = orc.f32_to_bf16(xs)
+    want = orc.gemm_multi(packed, scales, xs, n, k, seq, group, sdt)
+    want_b = orc.gemm_multi(packed, scales, orc.bf16_to_f32(xb), n, k, seq, group, sdt)
+    for tiling, (pp, ss) in ((cl.TILING_CRATE, (P, S)), (cl.TILING_MFMA, (pt, st))):
+        ys = torch.empty(seq * n, dtype=torch.float32, device="cuda")
+        cl.dequant_gemm_int4_multi_auto(pp, ss, dev(xs), n, k, seq, ys, group_size=group,
+                                        scale_dtype=sdt, tiling=tiling)
+        assert_f32_close(host(ys).reshape(seq, n), want, f"plan{plan} f32 tiling{tiling}")
+        cl.dequant_gemm_int4_multi_auto(pp, ss, dev(xb.view(np.int16)), n, k, seq, ys,
+                                        group_size=group, scale_dtype=sdt, tiling=tiling)
+        assert_f32_close(host(ys).reshape(seq, n), want_b, f"plan{plan} bf16 tiling{tiling}")
+
+
+@pytest.mark.parametrize("plan", range(len(PLANS)))
+def test_forced_launch_plans_expert(cl, orc, monkeypatch, plan):
+    """The fused gate/up (SwiGLU, hi/lo planes) and down kernels under forced plans."""
+    for key, val in PLANS[plan].items():
+        monkeypatch.setenv(key, val)
+    h, i, g, M = 1024, 768, 64, 6
+    flat = orc.fill_bytes(5, 50, orc.expert_bytes(h, i, g))
+    offs, sizes = orc.expert_offsets(h, i, g)
+    for s_ in (1, 3, 5):
+        flat[offs[s_]:offs[s_] + sizes[s_]] = orc.fill_scales(5, 51 + s_, sizes[s_] // 2, F16).view(np.uint8)
+    xb = orc.fill_normal_bf16(M, 52, M * h)
+    W = cl.ExpertWeights(dev(flat), h, i, g, F16)
+    out = torch.empty(M * h, dtype=torch.int16, device="cuda")
+    cl.expert_forward(dev(xb.view(np.int16).reshape(M, h)), *W.slices(), out, group_size=g,
+                      scale_dtype=F16)
+    want = orc.cpu_expert_forward(xb, M, flat, h, i, g, F16)
+    assert_bf16_close(host(out).view(np.uint16).reshape(M, h), want, f"expert plan{plan}")
+
+
 def test_crate_generator_known_layout(cl, orc):
     """The crate's own multi-token test generator (kernel_avx512_multi.rs:255-291)."""
     from test_oracle import ref_make_test_data
