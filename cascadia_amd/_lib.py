@@ -61,7 +61,7 @@ SIGNATURES = {
     "cascadia_int4_tile_expert": (_i32, [_u32, _u32, _u32, _EP, _vp, _EP, _vp]),
     "cascadia_int4_expert_from_flat": (_i32, [_vp, _u32, _u32, _u32, _EP]),
     "cascadia_int4_ffn_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
-    "cascadia_int4_expert_forward": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
+    "cascadia_int4_expert_forward_device": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
     "cascadia_int4_ffn_forward_f32": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
     "cascadia_int4_gate_up_silu": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _u32, _vp, _vp]),
     "cascadia_int4_debug_dequant": (_i32, [_LP, _vp, _vp, _vp, _vp]),

@@ -282,7 +282,7 @@ def expert_forward(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_pa
     e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
                        tiling)
     ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
-    check("cascadia_int4_expert_forward", lib().cascadia_int4_expert_forward(
+    check("cascadia_int4_expert_forward_device", lib().cascadia_int4_expert_forward_device(
         hidden, inter, group_size, scale_dtype, C.byref(e), x_bf16.data_ptr(), T,
         out_bf16.data_ptr(), ws, _stream()))
     return out_bf16

@@ -374,10 +374,10 @@ size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32
   return f.planes + (f.partials > b.partials ? f.partials : b.partials);
 }
 
-int cascadia_int4_expert_forward(uint32_t hidden, uint32_t inter, uint32_t group_size,
-                                 uint32_t scale_dtype, const cascadia_int4_expert *expert,
-                                 const uint16_t *x_bf16, uint32_t n_tokens, uint16_t *out_bf16,
-                                 void *workspace, void *stream) {
+int cascadia_int4_expert_forward_device(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                        uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                        const uint16_t *x_bf16, uint32_t n_tokens,
+                                        uint16_t *out_bf16, void *workspace, void *stream) {
   return ffn_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false,
                     n_tokens, out_bf16, true, workspace, (hipStream_t)stream);
 }

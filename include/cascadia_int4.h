@@ -159,11 +159,13 @@ size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32
  * rounding of the output (src/kernel.rs:75-136; ffn_sparsity.rs:756 at
  * tau = 0).  x_bf16, out_bf16: [n_tokens, hidden] bf16 bits.  workspace:
  * >= cascadia_int4_ffn_workspace_bytes bytes, 16-byte aligned, or NULL to use
- * the library's per-device buffer. */
-int cascadia_int4_expert_forward(uint32_t hidden, uint32_t inter, uint32_t group_size,
-                                 uint32_t scale_dtype, const cascadia_int4_expert *expert,
-                                 const uint16_t *x_bf16, uint32_t n_tokens, uint16_t *out_bf16,
-                                 void *workspace, void *stream);
+ * the library's per-device buffer.  Named _device because the crate's C FFI
+ * already exports cascadia_int4_expert_forward for its safetensors-handle
+ * call (c_ffi.rs:308-341, f32 in/out); that name stays reserved for it. */
+int cascadia_int4_expert_forward_device(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                        uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                        const uint16_t *x_bf16, uint32_t n_tokens,
+                                        uint16_t *out_bf16, void *workspace, void *stream);
 
 /* First half of the expert FFN: inter[t, i] = silu(W_g·x_t)[i] * (W_u·x_t)[i]
  * in f32 (kernel.rs:96-120; the batched gate/up + swiglu_mul of

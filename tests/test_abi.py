@@ -73,7 +73,7 @@ def test_argument_errors_before_device_work(cl):
     # misaligned packed pointer
     assert L.cascadia_int4_dequant_gemv(C.byref(lay), 17, 16, 16, 16, None) == cl._lib.ERR_ARG
     assert L.cascadia_int4_fill_synthetic(9, 0, 0, 16, 0.0, 0.0, 0, 16, None) == cl._lib.ERR_ARG
-    assert L.cascadia_int4_expert_forward(64, 32, 32, 0, None, 16, 1, 16, None, None) == cl._lib.ERR_NULL
+    assert L.cascadia_int4_expert_forward_device(64, 32, 32, 0, None, 16, 1, 16, None, None) == cl._lib.ERR_NULL
 
 
 def test_python_mirror_rejects_host_tensors(cl):
