@@ -4,8 +4,9 @@ weight-only matmul hot path, behind the C ABI of include/cascadia_int4.h.
 Importing the package loads libcascadia_int4_hip.so; it raises if the library
 was not built (``python cascadia_amd/build.py``).  There is no CPU fallback.
 """
-from ._lib import (CascadiaInt4Error, LIB_PATH, SCALE_BF16, SCALE_F16, SIGNATURES, TILING_CRATE,
-                   TILING_MFMA, check, lib)
+from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, CascadiaInt4Error,
+                   LIB_PATH, SCALE_BF16, SCALE_F16, SIGNATURES, TILING_CRATE, TILING_MFMA, check,
+                   lib)
 
 lib()  # fail loudly at import when the HIP library is missing
 
@@ -14,7 +15,8 @@ from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertWei
                   dequant_gemm_int4_multi_blocked_auto, dequant_gemv_int4,
                   dequant_gemv_int4_auto, expert_bytes, expert_forward, expert_forward_sparse,
                   ffn_forward_sparse_f32, ffn_workspace_bytes, fill_bytes, fill_normal,
-                  fill_scales, gate_up_silu, gemm_int4_bf16, tile_weights, tiled_sizes)
+                  fill_scales, gate_up_silu, gemm_int4_bf16, MoEExperts, moe_forward,
+                  moe_workspace_bytes, tile_weights, tiled_sizes)
 
 __all__ = [
     "CascadiaInt4Error", "LIB_PATH", "SCALE_BF16", "SCALE_F16", "SIGNATURES", "check", "lib",
@@ -23,5 +25,6 @@ __all__ = [
     "dequant_gemv_int4", "dequant_gemv_int4_auto", "expert_bytes", "expert_forward",
     "expert_forward_sparse", "ffn_forward_sparse_f32", "ffn_workspace_bytes", "fill_bytes",
     "fill_normal", "fill_scales", "gate_up_silu", "gemm_int4_bf16", "tile_weights",
-    "tiled_sizes", "TILING_CRATE", "TILING_MFMA",
+    "tiled_sizes", "TILING_CRATE", "TILING_MFMA", "MoEExperts", "moe_forward",
+    "moe_workspace_bytes", "ROUTE_IDS", "ROUTE_SIGMOID_BIAS", "ROUTE_SOFTMAX_TOPK",
 ]

@@ -43,8 +43,27 @@ class Expert(C.Structure):
                 ("tiling", C.c_uint32)]
 
 
+ROUTE_IDS = 0
+ROUTE_SIGMOID_BIAS = 1
+ROUTE_SOFTMAX_TOPK = 2
+
+
+class MoeLayer(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("inter", C.c_uint32), ("group_size", C.c_uint32),
+                ("scale_dtype", C.c_uint32), ("tiling", C.c_uint32), ("n_experts", C.c_uint32),
+                ("experts", C.c_void_p), ("expert_stride", C.c_size_t), ("shared", Expert),
+                ("shared_inter", C.c_uint32)]
+
+
+class Routing(C.Structure):
+    _fields_ = [("mode", C.c_uint32), ("top_k", C.c_uint32), ("logits", C.c_void_p),
+                ("bias", C.c_void_p), ("scale", C.c_float), ("normalize", C.c_uint32),
+                ("ids", C.c_void_p), ("weights", C.c_void_p), ("threshold", C.c_float)]
+
+
 _vp, _u32, _u64, _sz, _f64, _i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_size_t, C.c_double, C.c_int
 _LP, _EP = C.POINTER(Layout), C.POINTER(Expert)
+_MP, _RP = C.POINTER(MoeLayer), C.POINTER(Routing)
 
 # Every symbol declared in include/cascadia_int4.h: (restype, argtypes).
 SIGNATURES = {
@@ -64,6 +83,8 @@ SIGNATURES = {
     "cascadia_int4_expert_forward_device": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
     "cascadia_int4_ffn_forward_f32": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
     "cascadia_int4_gate_up_silu": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _u32, _vp, _vp]),
+    "cascadia_int4_moe_workspace_bytes": (_sz, [_MP, _u32, _u32]),
+    "cascadia_int4_moe_forward": (_i32, [_MP, _RP, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_debug_dequant": (_i32, [_LP, _vp, _vp, _vp, _vp]),
     "cascadia_int4_fill_synthetic": (_i32, [_u32, _u64, _u64, _sz, _f64, _f64, _u32, _vp, _vp]),
 }

@@ -16,8 +16,8 @@ import ctypes as C
 
 import torch
 
-from ._lib import (Expert, Layout, SCALE_BF16, SCALE_F16, TILING_CRATE, TILING_MFMA, check,
-                   lib)
+from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, Expert, Layout, MoeLayer,
+                   Routing, SCALE_BF16, SCALE_F16, TILING_CRATE, TILING_MFMA, check, lib)
 
 # K2.6 constants of the crate (lib.rs:71-78)
 HIDDEN = 7168
@@ -322,6 +322,129 @@ def ffn_forward_sparse_f32(x_f32, hidden, intermediate, gate_packed, gate_scale,
         hidden, inter, group_size, scale_dtype, C.byref(e), x_f32.data_ptr(), T,
         out_f32.data_ptr(), ws, _stream()))
     return 1.0
+
+
+# ---------------------------------------------------------------------------
+# sparse-MoE layer
+# ---------------------------------------------------------------------------
+
+def _align256(n: int) -> int:
+    return (n + 255) // 256 * 256
+
+
+class MoEExperts:
+    """The routed experts of one layer resident in HBM: expert e's blob at
+    byte e * stride of one uint8 tensor, in the crate's flat layout
+    (format.rs:35-47) or tiled (ExpertWeights.tiled()); plus an optional shared
+    expert (an ExpertWeights of its own)."""
+
+    def __init__(self, blobs: torch.Tensor, n_experts: int, hidden: int, inter: int,
+                 group_size: int = GROUP_SIZE, scale_dtype: int = SCALE_BF16,
+                 tiling: int = TILING_CRATE, stride: int | None = None,
+                 shared: "ExpertWeights | None" = None):
+        _dev(blobs, "blobs")
+        _expect(blobs.dtype == torch.uint8, "blobs must be uint8")
+        per = (int(lib().cascadia_int4_expert_tiled_bytes(hidden, inter, group_size))
+               if tiling == TILING_MFMA else expert_bytes(hidden, inter, group_size))
+        self.stride = stride if stride is not None else _align256(per)
+        _expect(self.stride >= per and self.stride % 256 == 0, "stride: >= expert bytes, multiple of 256")
+        _expect(blobs.numel() >= self.stride * (n_experts - 1) + per, "blobs too small")
+        _expect(blobs.data_ptr() % 256 == 0, "blobs must be 256-byte aligned")
+        if shared is not None:
+            _expect(shared.hidden == hidden and shared.group_size == group_size
+                    and shared.scale_dtype == scale_dtype, "shared expert dims")
+        self.blobs, self.n_experts, self.hidden, self.inter = blobs, n_experts, hidden, inter
+        self.group_size, self.scale_dtype, self.tiling, self.shared = group_size, scale_dtype, tiling, shared
+
+    @staticmethod
+    def from_crate(blobs: torch.Tensor, n_experts: int, hidden: int, inter: int,
+                   group_size: int = GROUP_SIZE, scale_dtype: int = SCALE_BF16,
+                   stride: int | None = None, shared=None, tiled: bool = True) -> "MoEExperts":
+        """Experts given as crate-layout blobs at `stride`; tiled=True converts
+        every expert (and the shared one) to the MFMA layout once."""
+        crate = MoEExperts(blobs, n_experts, hidden, inter, group_size, scale_dtype,
+                           TILING_CRATE, stride, shared)
+        if not tiled:
+            return crate
+        per = int(lib().cascadia_int4_expert_tiled_bytes(hidden, inter, group_size))
+        st = _align256(per)
+        dst = torch.empty(st * n_experts, dtype=torch.uint8, device=blobs.device)
+        for e in range(n_experts):
+            src = ExpertWeights(blobs[e * crate.stride:e * crate.stride + expert_bytes(hidden, inter, group_size)],
+                                hidden, inter, group_size, scale_dtype)
+            out = Expert()
+            check("cascadia_int4_tile_expert", lib().cascadia_int4_tile_expert(
+                hidden, inter, group_size, C.byref(_expert_struct(*src.slices())),
+                dst.data_ptr() + e * st, C.byref(out), _stream()))
+        sh = shared.tiled() if (shared is not None and shared.tiling == TILING_CRATE) else shared
+        return MoEExperts(dst, n_experts, hidden, inter, group_size, scale_dtype, TILING_MFMA, st, sh)
+
+    def _struct(self) -> MoeLayer:
+        L = MoeLayer()
+        L.hidden, L.inter, L.group_size = self.hidden, self.inter, self.group_size
+        L.scale_dtype, L.tiling, L.n_experts = self.scale_dtype, self.tiling, self.n_experts
+        L.experts, L.expert_stride = self.blobs.data_ptr(), self.stride
+        if self.shared is not None:
+            L.shared = _expert_struct(*self.shared.slices(), self.shared.tiling)
+            L.shared_inter = self.shared.inter
+        return L
+
+
+def moe_workspace_bytes(experts: MoEExperts, top_k: int, n_tokens: int) -> int:
+    return int(lib().cascadia_int4_moe_workspace_bytes(C.byref(experts._struct()), top_k, n_tokens))
+
+
+def moe_forward(experts: MoEExperts, x, out, *, top_k: int, logits=None, bias=None,
+                mode: int = ROUTE_SIGMOID_BIAS, scale: float = 1.0, normalize: bool = True,
+                ids=None, weights=None, threshold: float = 0.0, residual=None,
+                ids_out=None, weights_out=None, workspace=None):
+    """One MoE layer (runner.rs:1806-1832, batched over tokens):
+    out = residual + shared(x) + sum_k w_k * bf16(expert_k(bf16(x))).
+    x, out, residual: f32 [n_tokens, hidden] device tensors.  Routing from
+    logits (f32 [n_tokens, n_experts]; sigmoid + bias, or softmax over the
+    top-k) or given ids (int32) / weights (f32) [n_tokens, top_k]."""
+    _dev(x, "x"), _dev(out, "out")
+    H = experts.hidden
+    _expect(x.dtype == torch.float32 and out.dtype == torch.float32, "x and out must be f32")
+    T = x.numel() // H
+    _expect(x.numel() == T * H and out.numel() == T * H and T >= 1, "x/out must be [n_tokens, hidden]")
+    R = Routing()
+    R.mode, R.top_k, R.scale, R.normalize, R.threshold = mode, top_k, scale, int(normalize), threshold
+    if mode == ROUTE_IDS:
+        _expect(ids is not None and weights is not None, "ROUTE_IDS needs ids and weights")
+        _dev(ids, "ids"), _dev(weights, "weights")
+        _expect(ids.dtype == torch.int32 and ids.numel() == T * top_k, "ids: int32 [n_tokens, top_k]")
+        _expect(weights.dtype == torch.float32 and weights.numel() == T * top_k, "weights: f32 [n_tokens, top_k]")
+        R.ids, R.weights = ids.data_ptr(), weights.data_ptr()
+    else:
+        _expect(logits is not None, "routing needs logits")
+        _dev(logits, "logits")
+        _expect(logits.dtype == torch.float32 and logits.numel() == T * experts.n_experts,
+                "logits: f32 [n_tokens, n_experts]")
+        R.logits = logits.data_ptr()
+        if bias is not None:
+            _dev(bias, "bias")
+            _expect(bias.dtype == torch.float32 and bias.numel() == experts.n_experts, "bias: f32 [n_experts]")
+            R.bias = bias.data_ptr()
+    res = 0
+    if residual is not None:
+        _dev(residual, "residual")
+        _expect(residual.dtype == torch.float32 and residual.numel() == T * H, "residual: f32 [n_tokens, hidden]")
+        res = residual.data_ptr()
+    io = wo = 0
+    if ids_out is not None:
+        _dev(ids_out, "ids_out")
+        _expect(ids_out.dtype == torch.int32 and ids_out.numel() == T * top_k, "ids_out: int32 [n_tokens, top_k]")
+        io = ids_out.data_ptr()
+    if weights_out is not None:
+        _dev(weights_out, "weights_out")
+        _expect(weights_out.dtype == torch.float32 and weights_out.numel() == T * top_k, "weights_out: f32")
+        wo = weights_out.data_ptr()
+    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
+    check("cascadia_int4_moe_forward", lib().cascadia_int4_moe_forward(
+        C.byref(experts._struct()), C.byref(R), x.data_ptr(), res, T, out.data_ptr(), io, wo, ws,
+        _stream()))
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -9,6 +9,7 @@
 #include "../../include/cascadia_int4.h"
 #include "int4_common.hpp"
 #include "layout.hpp"
+#include "moe.hpp"
 #include "skinny.hpp"
 #include "synth.hpp"
 
@@ -213,6 +214,203 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
                   out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st, part);
 }
 
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+// offsets of the six sections of a tiled expert blob
+void tiled_expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[7]) {
+  size_t gp, gs, dp, ds;
+  cai4::tiled_sizes((int)inter, (int)hidden, (int)group, &gp, &gs);
+  cai4::tiled_sizes((int)hidden, (int)inter, (int)group, &dp, &ds);
+  const size_t sz[6] = {gp, gs, gp, gs, dp, ds};
+  off[0] = 0;
+  for (int i = 0; i < 6; ++i) off[i + 1] = off[i] + align256(sz[i]);
+}
+size_t expert_blob_bytes(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t tiling) {
+  if (tiling) {
+    size_t off[7];
+    tiled_expert_sections(hidden, inter, group, off);
+    return off[6];
+  }
+  size_t off[6];
+  expert_sections(hidden, inter, group, off);
+  return off[5] + (size_t)hidden * (inter / group) * 2;
+}
+
+void expert_blob_sections(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t tiling,
+                          size_t off[6]) {
+  if (tiling) {
+    size_t o[7];
+    tiled_expert_sections(hidden, inter, group, o);
+    for (int i = 0; i < 6; ++i) off[i] = o[i];
+  } else {
+    expert_sections(hidden, inter, group, off);
+  }
+}
+
+// ---- sparse-MoE layer ----
+
+bool has_shared(const cascadia_int4_moe_layer *L) {
+  const cascadia_int4_expert &e = L->shared;
+  return e.gate_packed || e.gate_scale || e.up_packed || e.up_scale || e.down_packed ||
+         e.down_scale;
+}
+
+int moe_check(const cascadia_int4_moe_layer *L, uint32_t top_k, uint32_t T) {
+  if (!L || !L->experts) return CASCADIA_INT4_ERR_NULL;
+  const uint32_t H = L->hidden, I = L->inter, G = L->group_size;
+  if (G == 0 || G % 32 || H == 0 || I == 0 || H % G || I % G) return CASCADIA_INT4_ERR_ARG;
+  if (L->scale_dtype > 1 || L->tiling > 1) return CASCADIA_INT4_ERR_ARG;
+  if (L->n_experts == 0 || L->n_experts > (uint32_t)cai4::kMoeMaxExperts) return CASCADIA_INT4_ERR_ARG;
+  if (top_k == 0 || top_k > (uint32_t)cai4::kMoeMaxTopK || top_k > L->n_experts)
+    return CASCADIA_INT4_ERR_ARG;
+  if (T == 0 || (size_t)T * top_k > 65535) return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(L->experts, 256) || L->expert_stride % 256 ||
+      L->expert_stride < expert_blob_bytes(H, I, G, L->tiling))
+    return CASCADIA_INT4_ERR_ARG;
+  const size_t rows = (size_t)T * top_k;
+  if (rows * H * 2 >= 0x7FFFFFFFu || rows * I * 2 >= 0x7FFFFFFFu) return CASCADIA_INT4_ERR_ARG;
+  if (has_shared(L)) {
+    if (L->shared_inter == 0 || L->shared_inter % G) return CASCADIA_INT4_ERR_ARG;
+    if (int rc = check_expert(H, L->shared_inter, G, L->scale_dtype, &L->shared)) return rc;
+  }
+  return CASCADIA_INT4_OK;
+}
+
+struct MoePlan {
+  cai4::SkinnyPlan gu, dn;
+  cai4::MoeWorkspace ws;
+};
+
+MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint32_t T) {
+  const cai4::SkinnyDevice d = device_props(dev);
+  const int H = (int)L->hidden, I = (int)L->inter, G = (int)L->group_size;
+  const int C = cai4::moe_chunk_rows((int)T);
+  const int maxc = cai4::moe_max_chunks((int)T, (int)L->n_experts, (int)top_k, C);
+  MoePlan m{};
+  m.gu = cai4::skinny_plan_grouped(I, H, G, C, maxc, cai4::A_BF16, cai4::EPI_SWIGLU_HILO, d);
+  m.dn = cai4::skinny_plan_grouped(H, I, G, C, maxc, cai4::A_HILO, cai4::EPI_BF16, d);
+  const size_t part = m.gu.partial_bytes > m.dn.partial_bytes ? m.gu.partial_bytes
+                                                              : m.dn.partial_bytes;
+  size_t sh = 0, sh_ws = 0;
+  if (has_shared(L)) {
+    const FfnWorkspace f = ffn_workspace(dev, L->hidden, L->shared_inter, L->group_size, T, true);
+    sh = (size_t)T * H * sizeof(float);
+    sh_ws = f.planes + f.partials;
+  }
+  m.ws = cai4::moe_workspace((int)T, H, I, (int)L->n_experts, (int)top_k, part, sh, sh_ws);
+  return m;
+}
+
+int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R, const float *x,
+                const float *residual, uint32_t T, float *out, int32_t *ids_out,
+                float *weights_out, void *workspace, hipStream_t st) {
+  if (!R || !x || !out) return CASCADIA_INT4_ERR_NULL;
+  if (int rc = moe_check(L, R->top_k, T)) return rc;
+  if (R->mode > CASCADIA_INT4_ROUTE_SOFTMAX_TOPK) return CASCADIA_INT4_ERR_ARG;
+  if (R->mode == CASCADIA_INT4_ROUTE_IDS ? (!R->ids || !R->weights) : !R->logits)
+    return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(x, 16) || !aligned(out, 16) || (residual && !aligned(residual, 16)))
+    return CASCADIA_INT4_ERR_ARG;
+  if ((ids_out && !aligned(ids_out, 4)) || (weights_out && !aligned(weights_out, 4)))
+    return CASCADIA_INT4_ERR_ARG;
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const MoePlan m = moe_plan(dev, L, R->top_k, T);
+  void *ws = workspace;
+  if (!ws) {
+    if (int rc = lib_workspace(dev, m.ws.total, &ws)) return rc;
+  } else if (!aligned(ws, 256)) {
+    return CASCADIA_INT4_ERR_ARG;
+  }
+  uint8_t *W = static_cast<uint8_t *>(ws);
+  const int H = (int)L->hidden, I = (int)L->inter, E = (int)L->n_experts, k = (int)R->top_k;
+  const size_t n = (size_t)T * k;
+  int32_t *ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(W + m.ws.ids);
+  float *wts = weights_out ? weights_out : reinterpret_cast<float *>(W + m.ws.weights);
+  hipError_t e = hipSuccess;
+  if (R->mode == CASCADIA_INT4_ROUTE_IDS) {
+    e = hipMemcpyAsync(ids, R->ids, n * 4, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(wts, R->weights, n * 4, hipMemcpyDeviceToDevice, st);
+  } else {
+    cai4::MoeRouting r{};
+    r.mode = (int)R->mode;
+    r.top_k = k;
+    r.logits = R->logits;
+    r.bias = R->bias;
+    r.scale = R->scale;
+    r.normalize = (int)R->normalize;
+    e = cai4::moe_route(r, (int)T, E, ids, wts, st);
+  }
+  int32_t *pos = reinterpret_cast<int32_t *>(W + m.ws.pos);
+  int32_t *row_map = reinterpret_cast<int32_t *>(W + m.ws.row_map);
+  cai4::SkinnyChunk *chunks = reinterpret_cast<cai4::SkinnyChunk *>(W + m.ws.chunks);
+  int32_t *counts = reinterpret_cast<int32_t *>(W + m.ws.counts);
+  uint16_t *xg = reinterpret_cast<uint16_t *>(W + m.ws.xg);
+  uint16_t *hi = reinterpret_cast<uint16_t *>(W + m.ws.hi);
+  uint16_t *lo = reinterpret_cast<uint16_t *>(W + m.ws.lo);
+  uint16_t *y = reinterpret_cast<uint16_t *>(W + m.ws.y);
+  void *part = W + m.ws.part;  // used only when a grouped GEMM splits K
+  if (e == hipSuccess)
+    e = cai4::moe_group(ids, wts, R->threshold, (int)T, E, k, m.ws.chunk_rows, m.ws.max_chunks,
+                        pos, row_map, chunks, counts, st);
+  if (e == hipSuccess) e = cai4::moe_gather(x, row_map, counts, (int)T, H, k, xg, st);
+  size_t off[6];
+  expert_blob_sections(L->hidden, L->inter, L->group_size, L->tiling, off);
+  const int G = (int)L->group_size;
+  if (e == hipSuccess) {
+    cai4::SkinnyArgs a{};
+    a.w0 = L->experts + off[0];
+    a.s0 = L->experts + off[1];
+    a.w1 = L->experts + off[2];
+    a.s1 = L->experts + off[3];
+    a.x = xg;
+    a.out = hi;
+    a.out2 = lo;
+    a.partials = part;
+    a.chunks = chunks;
+    a.expert_stride = L->expert_stride;
+    a.N = I;
+    a.K = H;
+    a.G = G;
+    a.M = (int)n;
+    a.ldx = H;
+    a.ldo = I;
+    a.sdt = (int)L->scale_dtype;
+    a.glog2 = glog2_of(G);
+    a.tiled = (int)L->tiling;
+    e = cai4::skinny_launch(a, m.gu, cai4::A_BF16, cai4::EPI_SWIGLU_HILO, st);
+  }
+  if (e == hipSuccess) {
+    cai4::SkinnyArgs a{};
+    a.w0 = L->experts + off[4];
+    a.s0 = L->experts + off[5];
+    a.x = hi;
+    a.x2 = lo;
+    a.out = y;
+    a.partials = part;
+    a.chunks = chunks;
+    a.expert_stride = L->expert_stride;
+    a.N = H;
+    a.K = I;
+    a.G = G;
+    a.M = (int)n;
+    a.ldx = I;
+    a.ldo = H;
+    a.sdt = (int)L->scale_dtype;
+    a.glog2 = glog2_of(G);
+    a.tiled = (int)L->tiling;
+    e = cai4::skinny_launch(a, m.dn, cai4::A_HILO, cai4::EPI_BF16, st);
+  }
+  if (e != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+  float *sh = nullptr;
+  if (has_shared(L)) {
+    sh = reinterpret_cast<float *>(W + m.ws.shared);
+    if (int rc = ffn_common(L->hidden, L->shared_inter, L->group_size, L->scale_dtype, &L->shared,
+                            x, true, T, sh, false, W + m.ws.shared_ws, st))
+      return rc;
+  }
+  return hip_status(cai4::moe_combine(residual, sh, y, pos, wts, (int)T, H, k, out, st));
+}
+
 }  // namespace
 
 extern "C" {
@@ -315,18 +513,6 @@ int cascadia_int4_tile_weights(const cascadia_int4_layout *L, const uint8_t *pac
                                        (hipStream_t)stream));
 }
 
-namespace {
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-// offsets of the six sections of a tiled expert blob
-void tiled_expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[7]) {
-  size_t gp, gs, dp, ds;
-  cai4::tiled_sizes((int)inter, (int)hidden, (int)group, &gp, &gs);
-  cai4::tiled_sizes((int)hidden, (int)inter, (int)group, &dp, &ds);
-  const size_t sz[6] = {gp, gs, gp, gs, dp, ds};
-  off[0] = 0;
-  for (int i = 0; i < 6; ++i) off[i + 1] = off[i] + align256(sz[i]);
-}
-}  // namespace
 
 size_t cascadia_int4_expert_tiled_bytes(uint32_t hidden, uint32_t inter, uint32_t group_size) {
   if (group_size == 0 || group_size % 32 || hidden % group_size || inter % group_size) return 0;
@@ -427,6 +613,23 @@ int cascadia_int4_fill_synthetic(uint32_t kind, uint64_t seed, uint64_t stream_i
   if ((kind == 1 || kind == 3) && !aligned(out, 2)) return CASCADIA_INT4_ERR_ARG;
   return hip_status(cai4::fill_synthetic((int)kind, seed, stream_id, n, p0, p1, (int)dtype, out,
                                          (hipStream_t)stream));
+}
+
+size_t cascadia_int4_moe_workspace_bytes(const cascadia_int4_moe_layer *layer, uint32_t top_k,
+                                         uint32_t n_tokens) {
+  if (moe_check(layer, top_k, n_tokens)) return 0;
+  int dev;
+  if (current_device(&dev)) return 0;
+  return moe_plan(dev, layer, top_k, n_tokens).ws.total;
+}
+
+int cascadia_int4_moe_forward(const cascadia_int4_moe_layer *layer,
+                              const cascadia_int4_routing *routing, const float *x,
+                              const float *residual, uint32_t n_tokens, float *out,
+                              int32_t *ids_out, float *weights_out, void *workspace,
+                              void *stream) {
+  return moe_forward(layer, routing, x, residual, n_tokens, out, ids_out, weights_out, workspace,
+                     (hipStream_t)stream);
 }
 
 }  // extern "C"

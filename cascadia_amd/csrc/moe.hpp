@@ -1,0 +1,53 @@
+// moe.hpp -- sparse-MoE expert path of one layer on one GPU.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "skinny.hpp"
+
+namespace cai4 {
+
+enum RouteMode { ROUTE_IDS = 0, ROUTE_SIGMOID_BIAS = 1, ROUTE_SOFTMAX_TOPK = 2 };
+
+struct MoeRouting {
+  int mode, top_k;
+  const float *logits;  // [T, E] (modes 1, 2)
+  const float *bias;    // [E] or null (mode 1)
+  float scale;          // mode 1: scaling of the selected weights
+  int normalize;        // mode 1: renormalise the top-k
+  const int32_t *ids;   // [T, top_k] (mode 0)
+  const float *weights; // [T, top_k] (mode 0)
+  float threshold;      // slots with w < threshold are skipped
+};
+
+constexpr int kMoeMaxExperts = 1024;
+constexpr int kMoeMaxTopK = 16;
+
+// Device workspace regions of one moe_forward call (byte offsets).
+struct MoeWorkspace {
+  size_t ids, weights, pos, row_map, chunks, counts, xg, hi, lo, y, shared, part, shared_ws,
+      total;
+  int chunk_rows, max_chunks;
+};
+
+MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, size_t part_bytes,
+                           size_t shared_bytes, size_t shared_ws_bytes);
+
+// Tokens per grouped chunk for T tokens routed to top_k experts.
+int moe_chunk_rows(int T);
+// Upper bound on grouped chunks.
+int moe_max_chunks(int T, int E, int top_k, int chunk_rows);
+
+hipError_t moe_route(const MoeRouting &r, int T, int E, int32_t *ids, float *w,
+                     hipStream_t st);
+hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T, int E,
+                     int top_k, int chunk_rows, int max_chunks, int32_t *pos, int32_t *row_map,
+                     SkinnyChunk *chunks, int32_t *counts, hipStream_t st);
+hipError_t moe_gather(const float *x, const int32_t *row_map, const int32_t *counts, int T,
+                      int H, int top_k, uint16_t *xg, hipStream_t st);
+hipError_t moe_combine(const float *residual, const float *shared, const uint16_t *y,
+                       const int32_t *pos, const float *w, int T, int H, int top_k, float *out,
+                       hipStream_t st);
+
+}  // namespace cai4

@@ -68,6 +68,8 @@ struct KParams {
   const void *x, *x2;
   void *out, *out2;
   f32x4_t *part;
+  const SkinnyChunk *chunks;
+  size_t wstride;
   int N, K, G, M, ldx, ldo, sdt, glog2, tiled, amode, epi;
   int rw, kw, kper;
   int act_rows, act_stride, scale_off;
@@ -404,8 +406,19 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
   const bool hilo = a.amode != A_BF16;
   const int tpm = hilo ? 8 : 16;
   const int unit0 = blockIdx.x * a.rw, unit = unit0 + rwi;
-  const int m0 = blockIdx.y * tpm * MT;
-  const int mcount = min(a.M - m0, tpm * MT);
+  int m0 = blockIdx.y * tpm * MT;
+  int mcount = min(a.M - m0, tpm * MT);
+  if (a.chunks) {  // grouped: this workgroup row is one chunk of one expert
+    const SkinnyChunk c = a.chunks[blockIdx.y];
+    if (c.count <= 0) return;  // uniform, before any barrier
+    const size_t eo = (size_t)c.expert * a.wstride;
+    a.w0 += eo;
+    a.s0 += eo;
+    if (a.w1) a.w1 += eo;
+    if (a.s1) a.s1 += eo;
+    m0 = c.row0;
+    mcount = min(c.count, tpm * MT);
+  }
   const int kb_total = (a.K + 127) >> 7;
   const int kr0 = blockIdx.z * a.kper, kr1 = min(kr0 + a.kper, kb_total);
   const int col_hi = min(a.K, kr1 * 128);
@@ -543,8 +556,13 @@ __global__ __launch_bounds__(1024) void splitk_reduce_kernel(KParams a, int kspl
   const int lane = threadIdx.x & 63;
   const int rwi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tpm = a.amode != A_BF16 ? 8 : 16;
-  const int m0 = blockIdx.y * tpm * MT;
-  const int mcount = min(a.M - m0, tpm * MT);
+  int m0 = blockIdx.y * tpm * MT;
+  int mcount = min(a.M - m0, tpm * MT);
+  if (a.chunks) {
+    const SkinnyChunk c = a.chunks[blockIdx.y];
+    m0 = c.row0;
+    mcount = min(c.count, tpm * MT);
+  }
   if (mcount <= 0) return;
   const size_t zstride = (size_t)gridDim.y * gridDim.x * a.rw * NI * 64;
   const size_t base =
@@ -582,16 +600,21 @@ size_t round16(size_t v) { return (v + 15) & ~(size_t)15; }
 
 }  // namespace
 
-SkinnyPlan skinny_plan(int N, int K, int G, int M, int amode, int epi, const SkinnyDevice &d) {
+namespace {
+
+// m_rows: rows per workgroup row to plan for (M, or a grouped chunk's
+// capacity); m_chunks: workgroup rows (0: derive from m_rows).
+SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, int epi,
+                     const SkinnyDevice &d) {
   SkinnyPlan p{};
   const int tpm = amode == A_BF16 ? 16 : 8;
   const int planes = amode == A_BF16 ? 1 : 2;
-  int mt = (M + tpm - 1) / tpm;
+  int mt = (m_rows + tpm - 1) / tpm;
   if (mt > 4) mt = 4;
   if (mt == 3) mt = 4;
   p.mt = mt;
-  p.m_chunks = (M + tpm * mt - 1) / (tpm * mt);
-  p.act_rows = M < tpm * mt ? M : tpm * mt;
+  p.m_chunks = m_chunks > 0 ? m_chunks : (m_rows + tpm * mt - 1) / (tpm * mt);
+  p.act_rows = m_rows < tpm * mt ? m_rows : tpm * mt;
   const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
   const int kb_total = (K + 127) / 128;
   const int maxw = skinny_max_threads(mt) / 64;
@@ -657,6 +680,17 @@ SkinnyPlan skinny_plan(int N, int K, int G, int M, int amode, int epi, const Ski
   return p;
 }
 
+}  // namespace
+
+SkinnyPlan skinny_plan(int N, int K, int G, int M, int amode, int epi, const SkinnyDevice &d) {
+  return plan_core(N, K, G, M, 0, amode, epi, d);
+}
+
+SkinnyPlan skinny_plan_grouped(int N, int K, int G, int chunk_rows, int max_chunks, int amode,
+                               int epi, const SkinnyDevice &d) {
+  return plan_core(N, K, G, chunk_rows, max_chunks < 1 ? 1 : max_chunks, amode, epi, d);
+}
+
 namespace {
 
 template <int NT, int MT, bool TR, bool SW>
@@ -703,6 +737,8 @@ hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, in
   k.out = a.out;
   k.out2 = a.out2;
   k.part = static_cast<f32x4_t *>(a.partials);
+  k.chunks = a.chunks;
+  k.wstride = a.expert_stride;
   k.N = a.N;
   k.K = a.K;
   k.G = a.G;

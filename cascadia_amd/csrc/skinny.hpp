@@ -14,6 +14,13 @@ enum Epilogue { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_BF16 = 2, EPI_SWIGLU_HILO = 3 }
 // precomputed hi/lo bf16 planes (x = hi plane, x2 = lo plane).
 enum AMode { A_BF16 = 0, A_XF32 = 1, A_HILO = 2 };
 
+// Grouped mode: one row chunk of one expert per workgroup row (blockIdx.y).
+// Weights/scales of expert e are at w0/w1/s0/s1 + e * expert_stride; a chunk
+// with count <= 0 is empty (its workgroups exit at once).
+struct SkinnyChunk {
+  int expert, row0, count, pad;
+};
+
 struct SkinnyArgs {
   const uint8_t *w0;  // packed weights (gate for the SwiGLU epilogues)
   const uint8_t *w1;  // up matrix (SwiGLU epilogues only)
@@ -24,6 +31,8 @@ struct SkinnyArgs {
   void *out;          // [M, ldo]: f32, bf16 bits, or the hi plane (EPI_SWIGLU_HILO)
   void *out2;         // EPI_SWIGLU_HILO: the lo plane
   void *partials;     // split-K partial sums (SkinnyPlan::partial_bytes), or null
+  const SkinnyChunk *chunks;  // grouped mode: [max_chunks] (device), else null
+  size_t expert_stride;       // grouped mode: bytes between experts' weights
   int N, K, G, M, ldx, ldo, sdt;
   int glog2;  // log2(G) when G is a power of two, else -1
   int tiled;  // weights/scales in the MFMA-tiled device layout (layout.hip)
@@ -46,6 +55,9 @@ struct SkinnyDevice {
 };
 
 SkinnyPlan skinny_plan(int N, int K, int G, int M, int amode, int epi, const SkinnyDevice &d);
+// Grouped mode: chunks of at most chunk_rows rows, max_chunks workgroup rows.
+SkinnyPlan skinny_plan_grouped(int N, int K, int G, int chunk_rows, int max_chunks, int amode,
+                               int epi, const SkinnyDevice &d);
 hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, int epi,
                          hipStream_t st);
 

@@ -185,6 +185,61 @@ int cascadia_int4_ffn_forward_f32(uint32_t hidden, uint32_t inter, uint32_t grou
                                   const float *x, uint32_t n_tokens, float *out,
                                   void *workspace, void *stream);
 
+/* ---- sparse-MoE layer (one pipeline stage on one GPU) ---- */
+
+/* The routed experts of one layer, resident in HBM: expert e's blob starts at
+ * experts + e * expert_stride and holds the six sections of an expert in the
+ * crate's flat order (format.rs:35-47, tiling = CRATE) or of
+ * cascadia_int4_tile_expert (tiling = MFMA).  experts and expert_stride must
+ * be multiples of 256.  A shared expert (shell_int4.rs:629) is given by six
+ * non-NULL pointers in `shared` (same tiling) and its intermediate size. */
+typedef struct cascadia_int4_moe_layer {
+  uint32_t hidden, inter, group_size, scale_dtype, tiling;
+  uint32_t n_experts; /* <= 1024 */
+  const uint8_t *experts;
+  size_t expert_stride;
+  cascadia_int4_expert shared; /* all pointers NULL: no shared expert */
+  uint32_t shared_inter;
+} cascadia_int4_moe_layer;
+
+/* Routing of n_tokens tokens to top_k (<= 16) experts.
+ *   ROUTE_SIGMOID_BIAS: s = sigmoid(logit); the top_k by s + bias (bias may be
+ *     NULL), ties to the lower id; w = s / (sum s + 1e-20) * scale when
+ *     normalize (K2.6 / GLM, shell_int4.rs:588-620, glm/gate.rs:24-62), else
+ *     w = s * scale.
+ *   ROUTE_SOFTMAX_TOPK: the top_k logits (ties to the lower id), w = softmax
+ *     over them.
+ *   ROUTE_IDS: ids / weights given, [n_tokens, top_k] int32 / f32.
+ * Slots with w < threshold are skipped (runner.rs:1811). */
+typedef struct cascadia_int4_routing {
+  uint32_t mode, top_k;
+  const float *logits; /* [n_tokens, n_experts] */
+  const float *bias;   /* [n_experts] or NULL */
+  float scale;
+  uint32_t normalize;
+  const int32_t *ids;
+  const float *weights;
+  float threshold;
+} cascadia_int4_routing;
+
+/* Workspace bytes of cascadia_int4_moe_forward on the current device. */
+size_t cascadia_int4_moe_workspace_bytes(const cascadia_int4_moe_layer *layer, uint32_t top_k,
+                                         uint32_t n_tokens);
+
+/* One MoE layer for n_tokens tokens (runner.rs:1806-1832, batched):
+ *   y_{t,k} = bf16 -> f32(expert_forward(bf16(x_t)))   for the routed slots
+ *   out_t   = residual_t + shared(x_t) + sum_k w_{t,k} y_{t,k}   (f32, slot order)
+ * with the shared expert f32 in / f32 out (ffn_forward_sparse_f32 at tau = 0).
+ * x, residual (may be NULL: zero), out: f32 [n_tokens, hidden], 16-byte
+ * aligned.  ids_out / weights_out (may be NULL) receive the routing,
+ * [n_tokens, top_k].  All experts of all tokens run as two grouped GEMM
+ * launches; nothing is synchronised with the host. */
+int cascadia_int4_moe_forward(const cascadia_int4_moe_layer *layer,
+                              const cascadia_int4_routing *routing, const float *x,
+                              const float *residual, uint32_t n_tokens, float *out,
+                              int32_t *ids_out, float *weights_out, void *workspace,
+                              void *stream);
+
 /* Dequantise to f32 [n_rows, k_cols] (bit-exact w = q*s; the kernel's own
  * decode path).  No crate counterpart; the parity check of the weights. */
 int cascadia_int4_debug_dequant(const cascadia_int4_layout *layout, const uint8_t *packed,

@@ -74,6 +74,27 @@ def test_argument_errors_before_device_work(cl):
     assert L.cascadia_int4_dequant_gemv(C.byref(lay), 17, 16, 16, 16, None) == cl._lib.ERR_ARG
     assert L.cascadia_int4_fill_synthetic(9, 0, 0, 16, 0.0, 0.0, 0, 16, None) == cl._lib.ERR_ARG
     assert L.cascadia_int4_expert_forward_device(64, 32, 32, 0, None, 16, 1, 16, None, None) == cl._lib.ERR_NULL
+    # MoE: null layer / routing / x; bad expert count, top_k, stride, alignment
+    R = cl._lib.Routing(mode=cl.ROUTE_SIGMOID_BIAS, top_k=8, logits=256)
+
+    def layer(**kw):
+        f = dict(hidden=256, inter=128, group_size=32, scale_dtype=0, tiling=0, n_experts=16,
+                 experts=1 << 20, expert_stride=1 << 16)
+        f.update(kw)
+        return cl._lib.MoeLayer(**f)
+
+    mf = L.cascadia_int4_moe_forward
+    assert mf(None, C.byref(R), 256, None, 1, 256, None, None, None, None) == cl._lib.ERR_NULL
+    assert mf(C.byref(layer()), None, 256, None, 1, 256, None, None, None, None) == cl._lib.ERR_NULL
+    assert mf(C.byref(layer()), C.byref(R), None, None, 1, 256, None, None, None, None) == cl._lib.ERR_NULL
+    for bad in [layer(n_experts=0), layer(n_experts=1025), layer(n_experts=4),
+                layer(expert_stride=100), layer(expert_stride=256), layer(experts=(1 << 20) + 16),
+                layer(group_size=48), layer(inter=100)]:
+        assert mf(C.byref(bad), C.byref(R), 256, None, 1, 256, None, None, None, None) == cl._lib.ERR_ARG
+    R17 = cl._lib.Routing(mode=cl.ROUTE_SIGMOID_BIAS, top_k=17, logits=256)
+    assert mf(C.byref(layer()), C.byref(R17), 256, None, 1, 256, None, None, None, None) == cl._lib.ERR_ARG
+    assert mf(C.byref(layer()), C.byref(R), 256, None, 0, 256, None, None, None, None) == cl._lib.ERR_ARG
+    assert L.cascadia_int4_moe_workspace_bytes(C.byref(layer(n_experts=0)), 8, 1) == 0
 
 
 def test_python_mirror_rejects_host_tensors(cl):
