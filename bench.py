@@ -235,6 +235,76 @@ def extra_measurements(cl, torch, args, sdt, copies):
     return res
 
 
+def make_experts_dev(cl, torch, E, h, i, g, sdt, seed):
+    """E synthetic experts (crate layout, seeded) tiled into one HBM blob."""
+    per = cl.expert_bytes(h, i, g)
+    stride = (per + 255) // 256 * 256
+    crate = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
+    cl.fill_bytes(crate, seed, 7)
+    for e in range(E):
+        W = cl.ExpertWeights(crate[e * stride:e * stride + per], h, i, g, sdt)
+        for j, s in enumerate((W.gate_scale_bits(), W.up_scale_bits(), W.down_scale_bits())):
+            cl.fill_scales(s, seed, 100000 + 3 * e + j, sdt)
+    ex = cl.MoEExperts.from_crate(crate, E, h, i, g, sdt, stride=stride, tiled=True)
+    del crate
+    torch.cuda.synchronize()
+    return ex
+
+
+def bench_moe(cl, torch, name, E, h, i, g, k, T, layers, mode, scale, shared_inter, steps,
+              zipf=None, nsets=64):
+    """MoE layer(s) for T tokens; steps rotate through `nsets` routing-logit
+    sets so that consecutive steps touch different experts."""
+    sdt = cl.SCALE_F16
+    stacks = []
+    for layer in range(layers):
+        ex = make_experts_dev(cl, torch, E, h, i, g, sdt, 50 + layer)
+        if shared_inter:
+            per = cl.expert_bytes(h, shared_inter, g)
+            f = cl.fill_bytes(torch.empty(per, dtype=torch.uint8, device="cuda"), 60 + layer, 1)
+            W = cl.ExpertWeights(f, h, shared_inter, g, sdt)
+            for j, s in enumerate((W.gate_scale_bits(), W.up_scale_bits(), W.down_scale_bits())):
+                cl.fill_scales(s, 60 + layer, 10 + j, sdt)
+            ex = cl.MoEExperts(ex.blobs, E, h, i, g, sdt, cl.TILING_MFMA, ex.stride, W.tiled())
+        stacks.append(ex)
+    logits = []
+    for sidx in range(nsets):
+        l = cl.fill_normal(torch.empty((T, E), dtype=torch.float32, device="cuda"), 70 + sidx, 1)
+        if zipf is not None:
+            perm = torch.randperm(E, generator=torch.Generator().manual_seed(1))
+            l += (-zipf * torch.log1p(perm.float())).cuda()[None, :]
+        logits.append(l)
+    xb = cl.fill_normal(torch.empty((T, h), dtype=torch.bfloat16, device="cuda"), 80, 1)
+    xs = [xb.float()] + [torch.empty((T, h), dtype=torch.float32, device="cuda") for _ in range(layers)]
+    ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    # unique experts per step and layer (routing only depends on the logits)
+    uniq = []
+    for sidx in range(nsets):
+        cl.moe_forward(stacks[0], xs[0], xs[1], top_k=k, logits=logits[sidx], mode=mode,
+                       scale=scale, residual=xs[0], ids_out=ids)
+        uniq.append(len(set(ids.cpu().flatten().tolist())))
+    u_avg = sum(uniq) / len(uniq)
+
+    def step(r):
+        for layer in range(layers):
+            cl.moe_forward(stacks[layer], xs[layer], xs[layer + 1], top_k=k,
+                           logits=logits[(r + 7 * layer) % nsets], mode=mode, scale=scale,
+                           residual=xs[layer])
+    for r in range(5):
+        step(r)
+    wall, _ = graph_time(torch, step, steps)
+    t = wall / steps
+    per_expert = 3 * (i * h // 2 + i * (h // g) * 2)
+    per_shared = 3 * (shared_inter * h // 2 + shared_inter * (h // g) * 2) if shared_inter else 0
+    byts = layers * (u_avg * per_expert + per_shared + T * h * 6 + T * E * 4 + T * k * 8)
+    res = {"T": T, "layers": layers, "us_per_step": round(t * 1e6, 2),
+           "tokens_per_s": round(T / t, 1), "GB/s": round(byts / t / 1e9, 1),
+           "hbm_frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 4), "unique_experts_avg": round(u_avg, 1)}
+    del stacks, logits
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -312,6 +382,14 @@ def main():
         line["cpu_baseline"] = cpu_baseline(torch, copies, x, m, args.cpu_seconds)
     if args.extra:
         line["extra"] = extra_measurements(cl, torch, args, sdt, copies)
+        for T in (1, 32, 256):
+            line["extra"][f"config3_moe_T{T}"] = bench_moe(
+                cl, torch, "config3", 256, 3072, 1536, 128, 8, T, 1, cl.ROUTE_SOFTMAX_TOPK, 1.0, 0,
+                200 if T < 256 else 40)
+        for T in (1, 8, 64):
+            line["extra"][f"config4_moe_T{T}"] = bench_moe(
+                cl, torch, "config4", 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS, 2.827,
+                2048, 50 if T < 64 else 20, zipf=1.1)
     print(json.dumps(line), flush=True)
 
 

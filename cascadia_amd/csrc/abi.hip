@@ -280,10 +280,12 @@ struct MoePlan {
   cai4::MoeWorkspace ws;
 };
 
-MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint32_t T) {
+MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint32_t T,
+                 bool given_ids) {
   const cai4::SkinnyDevice d = device_props(dev);
   const int H = (int)L->hidden, I = (int)L->inter, G = (int)L->group_size;
-  const int C = cai4::moe_chunk_rows((int)T);
+  // routing picks distinct experts per token; given ids may repeat one
+  const int C = cai4::moe_chunk_rows((int)T, given_ids ? (int)(T * top_k) : (int)T);
   const int maxc = cai4::moe_max_chunks((int)T, (int)L->n_experts, (int)top_k, C);
   MoePlan m{};
   m.gu = cai4::skinny_plan_grouped(I, H, G, C, maxc, cai4::A_BF16, cai4::EPI_SWIGLU_HILO, d);
@@ -296,7 +298,7 @@ MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint
     sh = (size_t)T * H * sizeof(float);
     sh_ws = f.planes + f.partials;
   }
-  m.ws = cai4::moe_workspace((int)T, H, I, (int)L->n_experts, (int)top_k, part, sh, sh_ws);
+  m.ws = cai4::moe_workspace((int)T, H, I, (int)L->n_experts, (int)top_k, C, part, sh, sh_ws);
   return m;
 }
 
@@ -314,7 +316,7 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     return CASCADIA_INT4_ERR_ARG;
   int dev;
   if (int rc = current_device(&dev)) return rc;
-  const MoePlan m = moe_plan(dev, L, R->top_k, T);
+  const MoePlan m = moe_plan(dev, L, R->top_k, T, R->mode == CASCADIA_INT4_ROUTE_IDS);
   void *ws = workspace;
   if (!ws) {
     if (int rc = lib_workspace(dev, m.ws.total, &ws)) return rc;
@@ -620,7 +622,9 @@ size_t cascadia_int4_moe_workspace_bytes(const cascadia_int4_moe_layer *layer, u
   if (moe_check(layer, top_k, n_tokens)) return 0;
   int dev;
   if (current_device(&dev)) return 0;
-  return moe_plan(dev, layer, top_k, n_tokens).ws.total;
+  const MoePlan a = moe_plan(dev, layer, top_k, n_tokens, false);
+  const MoePlan b = moe_plan(dev, layer, top_k, n_tokens, true);
+  return a.ws.total > b.ws.total ? a.ws.total : b.ws.total;
 }
 
 int cascadia_int4_moe_forward(const cascadia_int4_moe_layer *layer,

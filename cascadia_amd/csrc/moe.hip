@@ -27,18 +27,23 @@ namespace {
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 }  // namespace
 
-int moe_chunk_rows(int T) { return T <= 8 ? 8 : (T <= 64 ? 16 : 32); }
-
-int moe_max_chunks(int T, int E, int top_k, int chunk_rows) {
-  const long n = (long)T * top_k;
-  return (int)((n < E ? n : E) + n / chunk_rows);
+int moe_chunk_rows(int T, int per_expert_max) {
+  const int c = T <= 8 ? 8 : (T <= 64 ? 16 : 32);
+  return per_expert_max < c ? per_expert_max : c;
 }
 
-MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, size_t part_bytes,
-                           size_t shared_bytes, size_t shared_ws_bytes) {
+int moe_max_chunks(int T, int E, int top_k, int chunk_rows) {
+  // sum_e ceil(c_e / C) <= A + (n - A) / C for A active experts, largest at
+  // A = min(n, E)
+  const long n = (long)T * top_k, a = n < E ? n : E;
+  return (int)(a + (n - a) / chunk_rows);
+}
+
+MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows,
+                           size_t part_bytes, size_t shared_bytes, size_t shared_ws_bytes) {
   MoeWorkspace w{};
   const size_t n = (size_t)T * top_k;
-  w.chunk_rows = moe_chunk_rows(T);
+  w.chunk_rows = chunk_rows;
   w.max_chunks = moe_max_chunks(T, E, top_k, w.chunk_rows);
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -76,34 +81,39 @@ __global__ __launch_bounds__(256) void moe_route_kernel(MoeRouting r, int T, int
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;  // whole waves; no barriers in this kernel
   const bool sig = r.mode == ROUTE_SIGMOID_BIAS;
+  const int nj = (E + 63) >> 6;  // registers in use per lane
+  // all loads first, branch-free (experts past E read 0 from the range check)
+  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(r.logits + (size_t)t * E), (short)0, E * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(r.bias), (short)0, r.bias ? E * 4 : 0, 0x00020000);
+  float lg[R], bs[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const uint32_t off = j < nj ? (uint32_t)(lane + 64 * j) * 4 : 0x80000000u;
+    lg[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, 0));
+    bs[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
+  }
   float choice[R], val[R];
 #pragma unroll
   for (int j = 0; j < R; ++j) {
-    const int e = lane + 64 * j;
-    choice[j] = -INFINITY;
-    val[j] = 0.f;
-    if (e < E) {
-      const float l = r.logits[(size_t)t * E + e];
-      if (sig) {
-        const float s = 1.0f / (1.0f + expf(-l));
-        val[j] = s;
-        choice[j] = s + (r.bias ? r.bias[e] : 0.0f);
-      } else {
-        val[j] = l;
-        choice[j] = l;
-      }
-    }
+    const bool ok = lane + 64 * j < E;
+    const float s = sig ? 1.0f / (1.0f + expf(-lg[j])) : lg[j];
+    val[j] = s;
+    choice[j] = ok ? (sig ? s + bs[j] : s) : -INFINITY;
   }
+  // k rounds of a wave-wide argmax (ties to the lower id); lane kk keeps
+  // selection kk
   uint32_t taken = 0;
-  float sel[kMoeMaxTopK];
-  int sid[kMoeMaxTopK];
+  float my_val = 0.f;
+  int my_id = 0;
   for (int kk = 0; kk < r.top_k; ++kk) {
     float bc = -INFINITY;
     int bi = 0x7FFFFFFF;
 #pragma unroll
     for (int j = 0; j < R; ++j) {
       const int e = lane + 64 * j;
-      if (e < E && !((taken >> j) & 1u) && better(choice[j], e, bc, bi)) {
+      if (j < nj && e < E && !((taken >> j) & 1u) && better(choice[j], e, bc, bi)) {
         bc = choice[j];
         bi = e;
       }
@@ -120,35 +130,36 @@ __global__ __launch_bounds__(256) void moe_route_kernel(MoeRouting r, int T, int
     const int jj = bi >> 6;
     float mine = 0.f;
 #pragma unroll
-    for (int j = 0; j < R; ++j)
-      if (j == jj) mine = val[j];
+    for (int j = 0; j < R; ++j) mine = j == jj ? val[j] : mine;
+    const float v = __shfl(mine, bi & 63);
     if ((bi & 63) == lane) taken |= 1u << jj;
-    sid[kk] = bi;
-    sel[kk] = __shfl(mine, bi & 63);
+    if (lane == kk) {
+      my_val = v;
+      my_id = bi;
+    }
   }
-  if (lane != 0) return;
+  // weights, summed in selection order as the crate does
   const int k = r.top_k;
+  float w;
   if (sig) {
     if (r.normalize && k > 1) {
       float s = 0.0f;
-      for (int kk = 0; kk < k; ++kk) s += sel[kk];
+      for (int kk = 0; kk < k; ++kk) s += __shfl(my_val, kk);
       s += 1.0e-20f;
-      for (int kk = 0; kk < k; ++kk) sel[kk] = sel[kk] / s * r.scale;
+      w = my_val / s * r.scale;
     } else {
-      for (int kk = 0; kk < k; ++kk) sel[kk] = sel[kk] * r.scale;
+      w = my_val * r.scale;
     }
   } else {
-    const float mx = sel[0];
+    const float mx = __shfl(my_val, 0);
+    const float ex = expf(my_val - mx);
     float s = 0.0f;
-    for (int kk = 0; kk < k; ++kk) {
-      sel[kk] = expf(sel[kk] - mx);
-      s += sel[kk];
-    }
-    for (int kk = 0; kk < k; ++kk) sel[kk] = sel[kk] / s;
+    for (int kk = 0; kk < k; ++kk) s += __shfl(ex, kk);
+    w = ex / s;
   }
-  for (int kk = 0; kk < k; ++kk) {
-    ids[(size_t)t * k + kk] = sid[kk];
-    wout[(size_t)t * k + kk] = sel[kk];
+  if (lane < k) {
+    ids[(size_t)t * k + lane] = my_id;
+    wout[(size_t)t * k + lane] = w;
   }
 }
 
@@ -163,51 +174,58 @@ hipError_t moe_route(const MoeRouting &r, int T, int E, int32_t *ids, float *w, 
 // grouping: one workgroup
 // ---------------------------------------------------------------------------
 
-// Exclusive prefix sum of v[0..n) in place (n <= blockDim.x); returns the total.
-CAI4_DEV int block_exclusive_scan(int *v, int *tmp, int n) {
-  const int tid = threadIdx.x;
-  const int x = tid < n ? v[tid] : 0;
-  tmp[tid] = x;
-  __syncthreads();
-  for (int d = 1; d < (int)blockDim.x; d <<= 1) {
-    const int add = tid >= d ? tmp[tid - d] : 0;
-    __syncthreads();
-    tmp[tid] += add;
-    __syncthreads();
+// Grouping runs in one wave: counts by LDS atomics, then each lane scans a
+// contiguous run of experts and a wave prefix joins the runs.
+CAI4_DEV int wave_exclusive_scan(int x, int *total) {
+  const int lane = threadIdx.x & 63;
+  int inc = x;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(inc, d);
+    if (lane >= d) inc += y;
   }
-  const int total = tmp[blockDim.x - 1];
-  if (tid < n) v[tid] = tmp[tid] - x;
-  __syncthreads();
-  return total;
+  *total = __shfl(inc, 63);
+  return inc - x;
 }
 
-__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *ids, const float *w,
-                                                         float thr, int T, int E, int k, int C,
-                                                         int max_chunks, int32_t *pos,
-                                                         int32_t *row_map, SkinnyChunk *chunks,
-                                                         int32_t *counts) {
-  __shared__ int cnt[kMoeMaxExperts], off[kMoeMaxExperts], nch[kMoeMaxExperts],
-      choff[kMoeMaxExperts], tmp[1024];
-  const int tid = threadIdx.x, nth = blockDim.x;
+__global__ __launch_bounds__(64) void moe_group_kernel(const int32_t *ids, const float *w,
+                                                       float thr, int T, int E, int k, int C,
+                                                       int max_chunks, int32_t *pos,
+                                                       int32_t *row_map, SkinnyChunk *chunks,
+                                                       int32_t *counts) {
+  __shared__ int cnt[kMoeMaxExperts], off[kMoeMaxExperts], choff[kMoeMaxExperts];
+  const int lane = threadIdx.x;
   const int n = T * k;
-  for (int e = tid; e < E; e += nth) cnt[e] = 0;
+  for (int e = lane; e < E; e += 64) cnt[e] = 0;
   __syncthreads();
   // rank of each valid assignment within its expert (kept in pos for now)
-  for (int i = tid; i < n; i += nth) {
+  for (int i = lane; i < n; i += 64) {
     const int e = ids[i];
     const bool ok = !(w[i] < thr) && e >= 0 && e < E;  // runner.rs:1811: skip w < threshold
     pos[i] = ok ? atomicAdd(&cnt[e], 1) : -1;
   }
   __syncthreads();
-  for (int e = tid; e < E; e += nth) {
-    off[e] = cnt[e];
-    nch[e] = (cnt[e] + C - 1) / C;
-    choff[e] = nch[e];
+  const int per = (E + 63) >> 6, e0 = lane * per, e1 = min(E, e0 + per);
+  int rows = 0, chs = 0;
+  for (int e = e0; e < e1; ++e) {
+    rows += cnt[e];
+    chs += (cnt[e] + C - 1) / C;
+  }
+  int total, total_chunks;
+  int ro = wave_exclusive_scan(rows, &total), co = wave_exclusive_scan(chs, &total_chunks);
+  for (int e = e0; e < e1; ++e) {
+    off[e] = ro;
+    choff[e] = co;
+    const int c = cnt[e];
+    for (int q = 0; q * C < c; ++q) {
+      const int left = c - q * C;
+      chunks[co + q] = SkinnyChunk{e, ro + q * C, left < C ? left : C, 0};
+    }
+    ro += c;
+    co += (c + C - 1) / C;
   }
   __syncthreads();
-  const int total = block_exclusive_scan(off, tmp, E);
-  const int total_chunks = block_exclusive_scan(choff, tmp, E);
-  for (int i = tid; i < n; i += nth) {
+  for (int i = lane; i < n; i += 64) {
     const int rk = pos[i];
     if (rk >= 0) {
       const int p = off[ids[i]] + rk;
@@ -215,14 +233,8 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *ids, con
       row_map[p] = i / k;
     }
   }
-  for (int e = tid; e < E; e += nth) {
-    for (int c = 0; c < nch[e]; ++c) {
-      const int left = cnt[e] - c * C;
-      chunks[choff[e] + c] = SkinnyChunk{e, off[e] + c * C, left < C ? left : C, 0};
-    }
-  }
-  for (int j = total_chunks + tid; j < max_chunks; j += nth) chunks[j] = SkinnyChunk{0, 0, 0, 0};
-  if (tid == 0) {
+  for (int j = total_chunks + lane; j < max_chunks; j += 64) chunks[j] = SkinnyChunk{0, 0, 0, 0};
+  if (lane == 0) {
     counts[0] = total;
     counts[1] = total_chunks;
   }
@@ -231,7 +243,7 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *ids, con
 hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T, int E,
                      int top_k, int chunk_rows, int max_chunks, int32_t *pos, int32_t *row_map,
                      SkinnyChunk *chunks, int32_t *counts, hipStream_t st) {
-  hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, st, ids, w, threshold, T, E,
+  hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64), 0, st, ids, w, threshold, T, E,
                      top_k, chunk_rows, max_chunks, pos, row_map, chunks, counts);
   return hipGetLastError();
 }

@@ -31,11 +31,12 @@ struct MoeWorkspace {
   int chunk_rows, max_chunks;
 };
 
-MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, size_t part_bytes,
-                           size_t shared_bytes, size_t shared_ws_bytes);
+MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows,
+                           size_t part_bytes, size_t shared_bytes, size_t shared_ws_bytes);
 
-// Tokens per grouped chunk for T tokens routed to top_k experts.
-int moe_chunk_rows(int T);
+// Rows per grouped chunk for T tokens, no expert receiving more than
+// per_expert_max of them (T when routing picks distinct experts per token).
+int moe_chunk_rows(int T, int per_expert_max);
 // Upper bound on grouped chunks.
 int moe_max_chunks(int T, int E, int top_k, int chunk_rows);
 

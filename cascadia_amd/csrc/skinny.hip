@@ -187,7 +187,8 @@ CAI4_DEV int tile_row0(int unit, int nt) {
 }
 
 // Scales of the workgroup's rw * NT tiles, groups [g_lo, g_lo + ngw), go to LDS
-// as f32 [slot][group][16 rows] (slot = r * NT + nt); rows past N read 0.
+// as their u16 bits [slot][group][16 rows] (slot = r * NT + nt); rows past N
+// read 0.
 // Tiled: an item is 8 rows of one group (16 contiguous bytes); crate: one
 // scale.  Positions (t = row group, c = item of the slot) step like the
 // activations'.  Issue / store split as for the activations.
@@ -226,7 +227,7 @@ CAI4_DEV float scale_bits_f32(uint32_t bits, int sdt) {
 }
 
 template <int NT, int B>
-CAI4_DEV void sc_store(const KParams &a, float *dst, int ngw, Pos p0, int dt, int dc,
+CAI4_DEV void sc_store(const KParams &a, uint16_t *dst, int ngw, Pos p0, int dt, int dc,
                        const u32x4_t (&v)[NT][B]) {
   const int per_slot = ngw * (a.tiled ? 2 : 16);
 #pragma unroll
@@ -235,19 +236,12 @@ CAI4_DEV void sc_store(const KParams &a, float *dst, int ngw, Pos p0, int dt, in
 #pragma unroll
     for (int j = 0; j < B; ++j) {
       if (p.t >= a.rw) break;
-      float *slot = dst + (size_t)(p.t * NT + nt) * ngw * 16;
+      uint16_t *slot = dst + (size_t)(p.t * NT + nt) * ngw * 16;
       if (a.tiled) {
         const int g = p.c >> 1, h = p.c & 1;
-        const u32x4_t w = v[nt][j];
-        const f32x4_t f0 = {scale_bits_f32(w.x, a.sdt), scale_bits_f32(w.x >> 16, a.sdt),
-                            scale_bits_f32(w.y, a.sdt), scale_bits_f32(w.y >> 16, a.sdt)};
-        const f32x4_t f1 = {scale_bits_f32(w.z, a.sdt), scale_bits_f32(w.z >> 16, a.sdt),
-                            scale_bits_f32(w.w, a.sdt), scale_bits_f32(w.w >> 16, a.sdt)};
-        f32x4_t *d = reinterpret_cast<f32x4_t *>(slot + g * 16 + 8 * h);
-        d[0] = f0;
-        d[1] = f1;
+        *reinterpret_cast<u32x4_t *>(slot + g * 16 + 8 * h) = v[nt][j];
       } else {
-        slot[(p.c >> 4) * 16 + (p.c & 15)] = scale_bits_f32(v[nt][j].x, a.sdt);
+        slot[(p.c >> 4) * 16 + (p.c & 15)] = (uint16_t)v[nt][j].x;
       }
       pos_step(p, dt, dc, per_slot);
     }
@@ -271,7 +265,7 @@ CAI4_DEV void load_w(u32x4_t (&b)[NT], const rsrc_t (&wr)[NT], const uint32_t (&
 template <int NT, int MT, bool TR>
 CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&abase)[MT],
                          const uint32_t (&sbase)[NT], int k, int kr0, int g_lo, int K, int G,
-                         int glog2, f32x4_t (&acc)[MT][NT]) {
+                         int glog2, int sdt, f32x4_t (&acc)[MT][NT]) {
   const u32x4_t B136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
   const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
   const uint32_t koff = (uint32_t)(k - kr0) * 256;
@@ -294,7 +288,7 @@ CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float sc = *reinterpret_cast<const float *>(lds + sbase[nt] + 64 * g);
+      const float sc = scale_bits_f32(*reinterpret_cast<const uint16_t *>(lds + sbase[nt] + 32 * g), sdt);
       const u32x4_t d0 = decode8(b[nt].x), d1 = decode8(b[nt].y);
       const u32x4_t d2 = decode8(b[nt].z), d3 = decode8(b[nt].w);
 #pragma unroll
@@ -320,7 +314,8 @@ CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&
       for (int mt = 0; mt < MT; ++mt) corr[mt] = mfma_bf16(af[mt][s], B136, zero4);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const float sc = *reinterpret_cast<const float *>(lds + sbase[nt] + 64 * g);
+        const float sc =
+            scale_bits_f32(*reinterpret_cast<const uint16_t *>(lds + sbase[nt] + 32 * g), sdt);
         const uint32_t dw = s == 0 ? b[nt].x : s == 1 ? b[nt].y : s == 2 ? b[nt].z : b[nt].w;
         const u32x4_t d = decode8(dw);
 #pragma unroll
@@ -456,7 +451,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
   // thread positions and per-item steps (one division each, per thread)
   const Pos pa = pos_start(tid, cpr), ps = pos_start(tid, spr);
   const Pos da = pos_start(nth, cpr), ds = pos_start(nth, spr);
-  float *lds_sc = reinterpret_cast<float *>(lds + a.scale_off);
+  uint16_t *lds_sc = reinterpret_cast<uint16_t *>(lds + a.scale_off);
   u32x4_t av[2][BA];
   u32x4_t sv[NT][BS];
   act_issue<BA>(a, m0, mcount, kr0, kr1, pa, da.t, da.c, av);
@@ -492,7 +487,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
   uint32_t sbase[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
-    sbase[nt] = a.scale_off + (uint32_t)(((rwi * NT + nt) * ngw * 16 + lr) * 4);
+    sbase[nt] = a.scale_off + (uint32_t)(((rwi * NT + nt) * ngw * 16 + lr) * 2);
 
   f32x4_t acc[MT][NT];
 #pragma unroll
@@ -507,7 +502,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
         const int k = kb + u;
         if (k < kb1) {
           compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, k, kr0, g_lo, a.K, a.G, a.glog2,
-                                 acc);
+                                 a.sdt, acc);
           load_w<NT>(ring[u], wr, wv, k + U, wk, k + U < kb1);
         }
       }
@@ -627,7 +622,8 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   // row groups sharing one copy of the staged activations: grow until the
   // staging traffic is at most half the weight bytes, and beyond that while
   // every CU still gets a workgroup (fewer, fuller workgroups stage less)
-  const double wbytes = (sw ? 2.0 : 1.0) * N * (K / 2.0);
+  // weight bytes the launch streams (grouped: every chunk its own expert's)
+  const double wbytes = (sw ? 2.0 : 1.0) * N * (K / 2.0) * (m_chunks > 0 ? m_chunks : 1);
   int rw = 1;
   while (rw < maxw && rw < units) {
     const double sbytes =
@@ -645,7 +641,7 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
     const size_t stride = (size_t)kper * 256 + 16;
     const size_t act = (size_t)planes * p.act_rows * stride;
     const size_t ngw = ((size_t)kper * 128 + G - 1) / G + 1;
-    const size_t sc = (size_t)rw * p.nt * ngw * 64;
+    const size_t sc = (size_t)rw * p.nt * ngw * 32;
     const size_t red = (size_t)(kw - 1) * rw * mt * p.nt * 1024;
     const size_t st = round16(act) + sc;
     return st > red ? st : red;
@@ -653,21 +649,27 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   const int ks_env = env_int("CASCADIA_INT4_SKINNY_KSPLIT", 1, 64);
   const int kw_env = env_int("CASCADIA_INT4_SKINNY_WAVES", 1, 16);
   int ksplit = 1, kper = kb_total, kw = 1;
-  // a forced split is a minimum: LDS must fit whatever the override says
+  // Split K across workgroups only when the staging does not fit in LDS or
+  // fewer than half the CUs would get a workgroup: the reduce launch costs
+  // more than that.  Waves per workgroup: enough that the workgroups sharing
+  // a CU (as many as LDS allows, at most those the grid has per CU) bring
+  // about 16 waves.  A forced split is a minimum.
   for (int ks = ks_env ? ks_env : 1; ks <= kb_total; ++ks) {
     kper = (kb_total + ks - 1) / ks;
     ksplit = (kb_total + kper - 1) / kper;
-    long w = target / (wgs0 * ksplit * rw);
+    const long wgs = wgs0 * ksplit;
+    const size_t need1 = lds_need(kper, 1);
+    if (need1 > d.max_lds && ksplit < kb_total) continue;
+    long per_cu = (long)(d.max_lds / (need1 ? need1 : 1));
+    const long grid_per_cu = (wgs + d.num_cus - 1) / d.num_cus;
+    if (per_cu > grid_per_cu) per_cu = grid_per_cu;
+    if (per_cu < 1) per_cu = 1;
+    long w = target / d.num_cus / (per_cu * rw);
     kw = (int)(w < 1 ? 1 : (w > maxw / rw ? maxw / rw : w));
     if (kw_env) kw = kw_env / rw < 1 ? 1 : (kw_env / rw > maxw / rw ? maxw / rw : kw_env / rw);
     if (kw > kper) kw = kper;
-    const size_t budget = (size_t)((double)d.max_lds * rw * kw / 16.0);
-    const size_t need = lds_need(kper, kw);
-    if (need > d.max_lds && ksplit < kb_total) continue;
-    const bool fits = need <= (budget < 16384 ? 16384 : budget);
-    // every CU gets a workgroup, and the chip at least half its target waves
-    const bool full = wgs0 * ksplit >= d.num_cus && wgs0 * ksplit * rw * kw * 2 >= target;
-    if (ks_env || (fits && full) || ksplit >= 64) break;
+    while (kw > 1 && lds_need(kper, kw) > d.max_lds) --kw;
+    if (ks_env || wgs * 2 >= d.num_cus || ksplit >= 64) break;
   }
   p.ksplit = ksplit;
   p.kper = kper;
