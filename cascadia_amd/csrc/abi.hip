@@ -10,6 +10,7 @@
 #include "int4_common.hpp"
 #include "layout.hpp"
 #include "moe.hpp"
+#include "prefill.hpp"
 #include "skinny.hpp"
 #include "synth.hpp"
 
@@ -246,6 +247,17 @@ void expert_blob_sections(uint32_t hidden, uint32_t inter, uint32_t group, uint3
   }
 }
 
+// Prefill GEMM (M >= 64 tokens, MFMA-tiled weights, K and G multiples of 128).
+int run_prefill(const cascadia_int4_layout *L, const uint8_t *packed, const uint8_t *scales,
+                const uint16_t *x, uint32_t M, void *y, bool out_f32, hipStream_t st) {
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  if ((size_t)M * L->k_cols * 2 >= 0x7FFFFFFFu) return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::prefill_gemm(packed, scales, x, y, (int)M, (int)L->n_rows,
+                                       (int)L->k_cols, (int)L->group_size, (int)L->scale_dtype,
+                                       out_f32 ? 1 : 0, device_props(dev).num_cus, st));
+}
+
 // ---- sparse-MoE layer ----
 
 bool has_shared(const cascadia_int4_moe_layer *L) {
@@ -450,6 +462,9 @@ int cascadia_int4_dequant_gemm_bf16in(const cascadia_int4_layout *L, const uint8
   if (!xs_bf16 || !ys) return CASCADIA_INT4_ERR_NULL;
   if (seq == 0) return CASCADIA_INT4_ERR_ARG;
   if (!aligned(xs_bf16, 16) || !aligned(ys, 4)) return CASCADIA_INT4_ERR_ARG;
+  if (cai4::prefill_supported((int)seq, (int)L->n_rows, (int)L->k_cols, (int)L->group_size,
+                              (int)L->tiling))
+    return run_prefill(L, packed, scale_bits, xs_bf16, seq, ys, true, (hipStream_t)stream);
   return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
                   (int)L->group_size, (int)L->scale_dtype, (int)L->tiling, xs_bf16, nullptr,
                   cai4::A_BF16,
@@ -464,6 +479,9 @@ int cascadia_int4_gemm_bf16(const cascadia_int4_layout *L, const uint8_t *packed
   if (!xs_bf16 || !ys_bf16) return CASCADIA_INT4_ERR_NULL;
   if (seq == 0) return CASCADIA_INT4_ERR_ARG;
   if (!aligned(xs_bf16, 16) || !aligned(ys_bf16, 2)) return CASCADIA_INT4_ERR_ARG;
+  if (cai4::prefill_supported((int)seq, (int)L->n_rows, (int)L->k_cols, (int)L->group_size,
+                              (int)L->tiling))
+    return run_prefill(L, packed, scale_bits, xs_bf16, seq, ys_bf16, false, (hipStream_t)stream);
   return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
                   (int)L->group_size, (int)L->scale_dtype, (int)L->tiling, xs_bf16, nullptr,
                   cai4::A_BF16,

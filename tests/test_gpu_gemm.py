@@ -268,6 +268,46 @@ def test_prefill_gemm_bf16_small(cl, orc):
     assert_bf16_close(host(ys).view(np.uint16).reshape(m, n), want, "prefill small")
 
 
+PREFILL_SHAPES = [  # m, n, k, group: ragged M and N, G 128 / 256
+    (64, 256, 512, 128), (100, 192, 1024, 128), (300, 4112, 1024, 256), (130, 50, 256, 128),
+    (257, 640, 2048, 128),
+]
+
+
+@pytest.mark.parametrize("m,n,k,group", PREFILL_SHAPES)
+def test_prefill_gemm_tiled(cl, orc, m, n, k, group):
+    """The MFMA prefill GEMM (tiled weights, M >= 64): bf16 and f32 outputs
+    against the oracle's f32 sums."""
+    packed, scales = weights(orc, n, k, group, F16, m + n)
+    pt, st = cl.tile_weights(dev(packed), dev(scales), n, k, group)
+    xb = orc.fill_normal_bf16(5, m, m * k)
+    want = orc.gemm_multi(packed, scales, orc.bf16_to_f32(xb), n, k, m, group, F16)
+    yb = torch.empty(m * n, dtype=torch.int16, device="cuda")
+    cl.gemm_int4_bf16(pt, st, dev(xb.view(np.int16)), n, k, m, yb, group_size=group,
+                      scale_dtype=F16, tiling=cl.TILING_MFMA)
+    assert_bf16_close(host(yb).view(np.uint16).reshape(m, n), orc.f32_to_bf16(want),
+                      f"prefill bf16 {m}x{n}x{k} G{group}")
+    yf = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    cl.dequant_gemm_int4_multi_auto(pt, st, dev(xb.view(np.int16)), n, k, m, yf, group_size=group,
+                                    scale_dtype=F16, tiling=cl.TILING_MFMA)
+    assert_f32_close(host(yf).reshape(m, n), want, f"prefill f32 {m}x{n}x{k} G{group}")
+
+
+def test_prefill_gemm_config2(cl, orc):
+    """Config 2 (M 512, N 4096, K 4096, G128 fp16), against the CPU port of
+    the crate's per-token kernels."""
+    m, n, k, g = 512, 4096, 4096, 128
+    packed, scales = weights(orc, n, k, g, F16, 77)
+    pt, st = cl.tile_weights(dev(packed), dev(scales), n, k, g)
+    xb = orc.fill_normal_bf16(2, 3, m * k)
+    want = orc.cpu_gemm(packed, scales, orc.bf16_to_f32(xb), n, k, m, g, F16)
+    yb = torch.empty(m * n, dtype=torch.int16, device="cuda")
+    cl.gemm_int4_bf16(pt, st, dev(xb.view(np.int16)), n, k, m, yb, group_size=g, scale_dtype=F16,
+                      tiling=cl.TILING_MFMA)
+    assert_bf16_close(host(yb).view(np.uint16).reshape(m, n), orc.f32_to_bf16(want.reshape(m, n)),
+                      "prefill config2")
+
+
 def test_length_mismatch_raises(cl, orc):
     packed, scales = weights(orc, 64, 128, 32, BF16, 1)
     y = torch.empty(64, dtype=torch.float32, device="cuda")
@@ -321,7 +361,12 @@ def test_tiled_bit_identical_to_crate_layout(cl, orc, n, k, group, sdt, seq):
         cl.dequant_gemm_int4_multi_auto(P, S, xs, n, k, seq, y0, group_size=group, scale_dtype=sdt)
         cl.dequant_gemm_int4_multi_auto(pt, st, xs, n, k, seq, y1, group_size=group, scale_dtype=sdt,
                                         tiling=cl.TILING_MFMA)
-        assert np.array_equal(host(y0).view(np.uint32), host(y1).view(np.uint32))
+        if xs.dtype != torch.float32 and seq >= 64 and group % 128 == 0 and k % 128 == 0:
+            # tiled bf16 input of 64+ tokens runs the prefill GEMM, the crate
+            # layout the decode kernel: two summation orders, both at the bar
+            assert_f32_close(host(y1), host(y0), f"prefill vs decode kernel {n}x{k} seq{seq}")
+        else:  # the same kernel reads either layout: bit-identical
+            assert np.array_equal(host(y0).view(np.uint32), host(y1).view(np.uint32))
 
 
 @pytest.mark.parametrize("M", [1, 5, 16])
