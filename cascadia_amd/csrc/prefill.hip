@@ -6,30 +6,37 @@
 // result per element is the same sum, y[t, r] = sum_g s[r, g] * sum_{c in g}
 // (nibble - 8) * x[t, c], with products exact and f32 accumulation.
 //
-// Tiling.  A workgroup of 2 x NW waves computes a BM x 64 NW output tile; each
-// wave a (BM / 2) x 64 sub-tile as 16 x 16 MFMA tiles.  K advances one
-// 128-column k-block (one scale group, G a multiple of 128) per stage.
+// Arithmetic.  Weights enter the MFMAs as the bf16 value 128 + nibble; the
+// offset 136 (128 + the zero point 8) is removed by seeding each k-block's
+// partial with xs = -136 * sum(x) over the block's 128 columns, which a
+// pre-pass computes once per (row, k-block) in f32; the group scale is applied
+// in f32 per k-block, acc += s * p.  (G is a multiple of 128, so a k-block
+// lies in one group.)
+//
+// Tiling.  A workgroup of WM x WN waves computes a 16 MS WM x 16 NT WN output
+// tile, each wave a 16 MS x 16 NT sub-tile as 16 x 16 MFMA tiles.  K advances
+// one 128-column k-block per stage, in four 32-column steps: a step's
+// activation fragments are read from LDS one step ahead, so the MFMAs of a
+// step never wait on LDS; each decoded weight fragment serves MS MFMAs.
 //
 // Data movement.  Everything a stage needs -- the BM x 128 bf16 activation
 // tile, the workgroup's 16-row weight tiles of the k-block (1 KB each in the
-// MFMA-tiled layout) and their scales -- goes global -> LDS by buffer loads
-// with an LDS destination (no registers; out-of-range rows read 0), two
-// k-blocks ahead, into three static LDS stages.  Each stage: wait for this
-// wave's loads of the stage (vmcnt), barrier (then every wave's have landed),
-// issue the loads two stages ahead (into the buffer last read one stage ago,
-// which the barrier has freed), then read the fragments and run the MFMAs.
-// The loop is unrolled over the three buffers so each access names its own
-// LDS array.
+// MFMA-tiled layout), their scales and the BM seeds -- goes global -> LDS by
+// buffer loads with an LDS destination (no registers; out-of-range rows read
+// 0), two k-blocks ahead, into three static LDS stages.  Each stage: wait for
+// this wave's loads of the stage (vmcnt), barrier (then every wave's have
+// landed), then the four steps, issuing the loads two stages ahead in eight
+// parts over the steps (into the buffer read one stage ago, which the barrier
+// has freed).  The loop is unrolled over the three buffers so each access
+// names its own LDS array.  (Measured on gfx950: an LDS-destination load costs
+// the LDS several times what a ds_write_b128 of the same bytes does, but
+// staging through registers leaves too few of them for a two-stage lead with
+// this wave tile, and was slower.)
 //
 // Activation rows are stored 256 bytes apart with the 16-byte chunk index
 // XOR-swizzled by the row (chunk q of row r at slot q ^ (r & 15)): a load
 // instruction fills 1 KB of LDS in lane order, and the fragment reads of 16
 // rows at one column hit 16 different bank groups.
-//
-// Arithmetic per k-block: each weight fragment is decoded once into bf16
-// (128 + nibble) and used for every M sub-tile of the wave; one MFMA chain of
-// the activations against the constant bf16 -136 seeds each 16 x 16 partial;
-// the group scale is applied in f32, acc += s * p.
 #include "int4_common.hpp"
 #include "prefill.hpp"
 
@@ -56,173 +63,251 @@ CAI4_DEV void pf_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(n) : "memory");
 }
 
+// The LDS address (M0) of an LDS pointer, as a wave-uniform scalar.
+CAI4_DEV uint32_t lds_addr(const uint8_t *p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void *)p);
+}
+
+// One global -> LDS buffer load of `bytes` (16 or 4) per lane; lane i's data
+// lands at M0 + bytes * i.  Written as asm: the compiler cannot tell the stage
+// buffers apart, and would make every later LDS read of any stage wait for
+// this load (the prefetch two stages ahead) to land.  The stage waits count
+// these loads themselves.
+template <int bytes>
+CAI4_DEV void pf_dma(rsrc_t r, uint32_t lds, uint32_t voff) {
+  if constexpr (bytes == 16)
+    asm volatile("buffer_load_dwordx4 %1, %2, 0 offen lds" ::"{m0}"(lds), "v"(voff), "s"(r)
+                 : "memory");
+  else
+    asm volatile("buffer_load_dword %1, %2, 0 offen lds" ::"{m0}"(lds), "v"(voff), "s"(r)
+                 : "memory");
+}
+
 struct PfArgs {
   const uint8_t *w;   // MFMA-tiled packed weights
   const uint8_t *s;   // tiled scales [T][NG][16] u16
   const uint16_t *x;  // bf16 [M, K]
+  const float *xs;    // seeds [KB][Mp]: -136 * sum of x over each k-block
   void *y;            // [M, N] bf16 or f32
-  int M, N, K, G, sdt, out_f32;
+  int M, N, K, G, sdt, out_f32, Mp;
 };
 
-// LDS of one stage: activations [BM][256 B] swizzled, weight tiles [NT16][1 KB],
-// scales [NT16][16] u16.
-template <int BM, int NW>
-struct Stage {
-  static constexpr int NT16 = 4 * NW;  // 16-row weight tiles of the workgroup
-  static constexpr int A = 0, B = BM * 256, S = B + NT16 * 1024, BYTES = S + NT16 * 32;
-};
-
-template <int BM, int NW>
-struct Pf {
-  static constexpr int MS = BM / 32;                      // 16-row sub-tiles per wave
-  static constexpr int AI = BM * 256 / 1024 / (2 * NW);   // activation loads per wave per stage
-  static constexpr int LOADS = AI + 2 + 1;                // + two weight tiles + the scales
-};
-
-// Issue wave `wave`'s loads of k-block kb into stage buffer `buf`.
-template <int BM, int NW>
-CAI4_DEV void pf_issue(uint8_t *buf, rsrc_t xr, rsrc_t wr, rsrc_t sr, int K, int KB, int NG,
-                       int G, int kb, int wave, int lane) {
-  using P = Pf<BM, NW>;
-  using S = Stage<BM, NW>;
-  // activations: load t fills LDS bytes [(wave AI + t) KB, +1 KB): rows
-  // 4 (wave AI + t) + lane / 16, slot lane & 15 holding chunk slot ^ (row & 15)
+// Seeds: xs[kb][m] = -136 * sum_{c < 128} x[m, 128 kb + c] (f32, fixed order:
+// eight columns per lane, then a butterfly over the 16 lanes of the block);
+// rows M .. Mp - 1 are 0.  One wave per row, four k-blocks per pass.
+__global__ __launch_bounds__(256) void pf_xsum_kernel(const uint16_t *x, float *xs, int M, int K,
+                                                      int Mp) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= Mp) return;
+  const int KB = K >> 7;
+  for (int kb0 = 0; kb0 < KB; kb0 += 4) {
+    const int kb = kb0 + (lane >> 4);
+    float t = 0.f;
+    if (m < M && kb < KB) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t *>(x + (size_t)m * K + kb * 128 +
+                                                           8 * (lane & 15));
 #pragma unroll
-  for (int t = 0; t < P::AI; ++t) {
-    const int blk = wave * P::AI + t;
-    const int row = 4 * blk + (lane >> 4);
-    const int q = (lane & 15) ^ (row & 15);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *)(buf + S::A + blk * 1024), 16,
-                                         (uint32_t)(row * K + kb * 128 + 8 * q) * 2, 0, 0, 0);
-  }
-  // weights: tiles 2 wave, 2 wave + 1 of the workgroup, 1 KB each in lane order
+      for (int e = 0; e < 4; ++e) t += bf16_to_f32(v[e] & 0xFFFFu) + bf16_to_f32(v[e] >> 16);
+    }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int tile = 2 * wave + j;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void *)(buf + S::B + tile * 1024), 16,
-                                         (uint32_t)(tile * KB + kb) * 1024 + 16 * lane, 0, 0, 0);
+    for (int o = 1; o < 16; o <<= 1) t += __shfl_xor(t, o, 64);
+    if ((lane & 15) == 0 && kb < KB) xs[(size_t)kb * Mp + m] = -136.f * t;
   }
-  // scales of those two tiles: 2 x 32 bytes, four bytes from each of lanes
-  // 0-15 (lane i writes LDS slot i: the other lanes must not run the load,
-  // or their slots would overwrite the neighbouring waves' scales)
-  const int g = (kb * 128) / G;
-  const int tile = 2 * wave + ((lane >> 3) & 1);
-  if (lane < 16)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void *)(buf + S::S + 2 * wave * 32), 4,
-                                         (uint32_t)((tile * NG + g) * 16 * 2 + 4 * (lane & 7)),
-                                         0, 0, 0);
 }
 
-template <int BM, int NW>
-CAI4_DEV void pf_compute(const uint8_t *buf, int wm, int wn, int lane, int sdt,
-                         f32x4_t (&acc)[BM / 32][4]) {
-  using P = Pf<BM, NW>;
-  using S = Stage<BM, NW>;
-  const int lr = lane & 15, lg = lane >> 4;
-  const u32x4_t B136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
-  const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-  u32x4_t af[P::MS][4];
-#pragma unroll
-  for (int i = 0; i < P::MS; ++i) {
-    const int row = wm * (BM / 2) + 16 * i + lr;  // row & 15 == lr
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      af[i][s] = *reinterpret_cast<const u32x4_t *>(buf + S::A + row * 256 +
-                                                    16 * ((4 * lg + s) ^ lr));
+// Workgroup geometry and the LDS of one stage: activations [BM][256 B]
+// swizzled, weight tiles [NT16][1 KB], scales [NT16][16] u16, seeds [BM] f32.
+template <int MS, int NT, int WM, int WN>
+struct Pf {
+  static constexpr int W = WM * WN;                 // waves
+  static constexpr int BM = 16 * MS * WM, BN = 16 * NT * WN;
+  static constexpr int RM = 16 * MS;                // rows per wave
+  static constexpr int NT16 = NT * WN;              // 16-row weight tiles per workgroup
+  static constexpr int A = 0, B = BM * 256, S = B + NT16 * 1024, X = S + NT16 * 32,
+                       BYTES = X + BM * 4;
+  static constexpr int AL = BM / (4 * W);           // 1 KB activation loads per wave
+  static constexpr int BL = NT16 / W;               // weight tiles loaded per wave
+  static constexpr int SL = NT16 * 8 / W;           // lanes loading 4 scale bytes each
+  static constexpr int XL = BM / (4 * W);           // lanes loading 4 seeds each
+  static constexpr int LOADS = AL + BL + 2;
+  static_assert(AL >= 1 && BL >= 1 && SL <= 64 && XL >= 1, "workgroup shape");
+};
+
+// Load `l` (0 .. LOADS-1) of wave `wave`'s share of k-block kb into stage
+// buffer `buf`: activation blocks, weight tiles, scales, seeds.
+template <class P>
+CAI4_DEV void pf_load(int l, uint8_t *buf, rsrc_t xr, rsrc_t wr, rsrc_t sr, rsrc_t qr, int K,
+                      int KB, int NG, int G, int Mp, int kb, int wave, int lane) {
+  if (l < P::AL) {
+    // activation block b = 1 KB of LDS in lane order: rows 4 b + lane / 16,
+    // slot lane & 15 holding chunk slot ^ (row & 15)
+    const int blk = wave * P::AL + l;
+    const int row = 4 * blk + (lane >> 4);
+    const int q = (lane & 15) ^ (row & 15);
+    pf_dma<16>(xr, lds_addr(buf + P::A + blk * 1024), (uint32_t)(row * K + kb * 128 + 8 * q) * 2);
+  } else if (l < P::AL + P::BL) {
+    const int tile = wave * P::BL + (l - P::AL);  // 1 KB in lane order
+    pf_dma<16>(wr, lds_addr(buf + P::B + tile * 1024), (uint32_t)(tile * KB + kb) * 1024 + 16 * lane);
+  } else if (l == P::AL + P::BL) {
+    // scales of the wave's BL tiles, 32 bytes each, four bytes per lane (lane
+    // i writes LDS slot i: lanes past SL must not run the load, or they would
+    // overwrite the next wave's slots)
+    const int g = (kb * 128) / G;
+    const int tile = wave * P::BL + (lane >> 3);
+    if (lane < P::SL)
+      pf_dma<4>(sr, lds_addr(buf + P::S + wave * P::SL * 4),
+                (uint32_t)((tile * NG + g) * 16 * 2 + 4 * (lane & 7)));
+  } else {
+    // seeds of rows 4 (wave XL + lane) .. +3, 16 bytes per lane
+    if (lane < P::XL)
+      pf_dma<16>(qr, lds_addr(buf + P::X + wave * P::XL * 16),
+                 (uint32_t)(kb * Mp + 4 * (wave * P::XL + lane)) * 4);
   }
-  u32x4_t b[4];
-  float sc[4];
+}
+
+// The loads one stage issues, for k-block kb two ahead (none past the end).
+struct PfNext {
+  uint8_t *buf;
+  rsrc_t xr, wr, sr, qr;
+  int K, KB, NG, G, Mp, kb, wave, lane;
+};
+
+// Issue the loads of part `part` (of 8): loads [part L / 8, (part + 1) L / 8).
+template <class P>
+CAI4_DEV void pf_issue_part(const PfNext &n, int part) {
+  if (n.kb < n.KB) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tile = 4 * wn + j;
-    b[j] = *reinterpret_cast<const u32x4_t *>(buf + S::B + tile * 1024 + 16 * lane);
-    const uint32_t bits = *reinterpret_cast<const uint16_t *>(buf + S::S + tile * 32 + 2 * lr);
+    for (int l = 0; l < P::LOADS; ++l)
+      if (l >= part * P::LOADS / 8 && l < (part + 1) * P::LOADS / 8)
+        pf_load<P>(l, n.buf, n.xr, n.wr, n.sr, n.qr, n.K, n.KB, n.NG, n.G, n.Mp, n.kb, n.wave,
+                   n.lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Activation fragments of step s: rows wm BM / WM + 16 i + (lane & 15), the
+// 8 columns of chunk 4 (lane / 16) + s.
+template <class P, int MS>
+CAI4_DEV void pf_read_a(const uint8_t *buf, int wm, int lane, int s, u32x4_t (&af)[MS]) {
+  const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < MS; ++i) {
+    const int row = wm * P::RM + 16 * i + lr;  // row & 15 == lr
+    af[i] = *reinterpret_cast<const u32x4_t *>(buf + P::A + row * 256 + 16 * ((4 * lg + s) ^ lr));
+  }
+}
+
+template <class P, int MS, int NT>
+CAI4_DEV void pf_compute(const uint8_t *buf, int wm, int wn, int lane, int sdt, const PfNext &nx,
+                         f32x4_t (&acc)[MS][NT]) {
+  const int lr = lane & 15, lg = lane >> 4;
+  u32x4_t b[NT];
+  float sc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int tile = NT * wn + j;
+    b[j] = *reinterpret_cast<const u32x4_t *>(buf + P::B + tile * 1024 + 16 * lane);
+    const uint32_t bits = *reinterpret_cast<const uint16_t *>(buf + P::S + tile * 32 + 2 * lr);
     sc[j] = sdt ? scale_to_f32<SCALE_F16>(bits) : scale_to_f32<SCALE_BF16>(bits);
   }
-  f32x4_t corr[P::MS];
+  f32x4_t p[MS][NT];
+  u32x4_t af[MS], an[MS];
+  pf_read_a<P, MS>(buf, wm, lane, 0, af);
 #pragma unroll
-  for (int i = 0; i < P::MS; ++i) {
-    corr[i] = mfma_bf16(af[i][0], B136, zero4);
-    corr[i] = mfma_bf16(af[i][1], B136, corr[i]);
-    corr[i] = mfma_bf16(af[i][2], B136, corr[i]);
-    corr[i] = mfma_bf16(af[i][3], B136, corr[i]);
+  for (int i = 0; i < MS; ++i) {
+    // D layout: lane holds rows 4 (lane / 16) + v of the 16-row tile
+    const f32x4_t seed = *reinterpret_cast<const f32x4_t *>(
+        buf + P::X + 4 * (wm * P::RM + 16 * i + 4 * lg));
+#pragma unroll
+    for (int j = 0; j < NT; ++j) p[i][j] = seed;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const u32x4_t d0 = decode8(b[j].x), d1 = decode8(b[j].y);
-    const u32x4_t d2 = decode8(b[j].z), d3 = decode8(b[j].w);
+  for (int s = 0; s < 4; ++s) {
+    if (s < 3) pf_read_a<P, MS>(buf, wm, lane, s + 1, an);
 #pragma unroll
-    for (int i = 0; i < P::MS; ++i) {
-      f32x4_t p = mfma_bf16(af[i][0], d0, corr[i]);
-      p = mfma_bf16(af[i][1], d1, p);
-      p = mfma_bf16(af[i][2], d2, p);
-      p = mfma_bf16(af[i][3], d3, p);
-      acc[i][j] += sc[j] * p;
+    for (int j = 0; j < NT; ++j) {
+      const u32x4_t d = decode8(b[j][s]);
+#pragma unroll
+      for (int i = 0; i < MS; ++i) p[i][j] = mfma_bf16(af[i], d, p[i][j]);
+      if (j == NT / 2 - 1 || j == NT - 1) pf_issue_part<P>(nx, 2 * s + (j == NT - 1));
     }
+#pragma unroll
+    for (int i = 0; i < MS; ++i) af[i] = an[i];
   }
+#pragma unroll
+  for (int i = 0; i < MS; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] += sc[j] * p[i][j];
 }
 
 // One stage: k-block kb from `cur`; the loads of kb + 2 go into `nxt2`.
-template <int BM, int NW>
-CAI4_DEV void pf_stage(uint8_t *cur, uint8_t *nxt2, rsrc_t xr, rsrc_t wr, rsrc_t sr,
+template <class P, int MS, int NT>
+CAI4_DEV void pf_stage(uint8_t *cur, uint8_t *nxt2, rsrc_t xr, rsrc_t wr, rsrc_t sr, rsrc_t qr,
                        const PfArgs &a, int KB, int NG, int kb, int wave, int wm, int wn,
-                       int lane, f32x4_t (&acc)[BM / 32][4]) {
-  using P = Pf<BM, NW>;
+                       int lane, f32x4_t (&acc)[MS][NT]) {
   if (kb >= KB) return;  // uniform
   // this wave's loads of kb are done once only kb + 1's may still be in
-  // flight; after the barrier every wave's have landed
+  // flight (loads complete in order); after the barrier every wave's have
+  // landed
   if (kb + 1 < KB)
     pf_wait_barrier<P::LOADS>();
   else
     pf_wait_barrier<0>();
-  if (kb + 2 < KB) pf_issue<BM, NW>(nxt2, xr, wr, sr, a.K, KB, NG, a.G, kb + 2, wave, lane);
-  pf_compute<BM, NW>(cur, wm, wn, lane, a.sdt, acc);
+  const PfNext nx{nxt2, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, kb + 2, wave, lane};
+  pf_compute<P, MS, NT>(cur, wm, wn, lane, a.sdt, nx, acc);
 }
 
-template <int BM, int NW>
-__global__ __launch_bounds__(128 * NW) void pf_gemm_kernel(PfArgs a) {
-  using P = Pf<BM, NW>;
-  using S = Stage<BM, NW>;
-  __shared__ __attribute__((aligned(16))) uint8_t st0[S::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t st1[S::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t st2[S::BYTES];
+template <int MS, int NT, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void pf_gemm_kernel(PfArgs a) {
+  using P = Pf<MS, NT, WM, WN>;
+  __shared__ __attribute__((aligned(16))) uint8_t st0[P::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t st1[P::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t st2[P::BYTES];
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   // wave index as a scalar: descriptors built from it must be uniform
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * 64 * NW;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave % WM, wn = wave / WM;
+  const int m0 = blockIdx.y * P::BM, n0 = blockIdx.x * P::BN;
   const int KB = a.K >> 7, NG = a.K / a.G;
   const int ntiles = (a.N + 15) >> 4;
   const int T0 = n0 >> 4;
   const int tv =
-      __builtin_amdgcn_readfirstlane(ntiles - T0 > S::NT16 ? S::NT16 : ntiles - T0);
+      __builtin_amdgcn_readfirstlane(ntiles - T0 > P::NT16 ? P::NT16 : ntiles - T0);
   const rsrc_t wr = rsrc(a.w + (size_t)T0 * KB * 1024, (size_t)tv * KB * 1024);
   const rsrc_t sr = rsrc(a.s + (size_t)T0 * NG * 32, (size_t)tv * NG * 32);
   const rsrc_t xr = rsrc(a.x + (size_t)m0 * a.K, (size_t)(a.M - m0) * a.K * 2);
+  const rsrc_t qr = rsrc(a.xs + m0, ((size_t)(KB - 1) * a.Mp + P::BM) * 4);
 
-  f32x4_t acc[P::MS][4];
+  f32x4_t acc[MS][NT];
 #pragma unroll
-  for (int i = 0; i < P::MS; ++i)
+  for (int i = 0; i < MS; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  pf_issue<BM, NW>(st0, xr, wr, sr, a.K, KB, NG, a.G, 0, wave, lane);
-  if (KB > 1) pf_issue<BM, NW>(st1, xr, wr, sr, a.K, KB, NG, a.G, 1, wave, lane);
+#pragma unroll
+  for (int l = 0; l < P::LOADS; ++l)
+    pf_load<P>(l, st0, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, 0, wave, lane);
+  if (KB > 1) {
+#pragma unroll
+    for (int l = 0; l < P::LOADS; ++l)
+      pf_load<P>(l, st1, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, 1, wave, lane);
+  }
   for (int kb = 0; kb < KB; kb += 3) {
-    pf_stage<BM, NW>(st0, st2, xr, wr, sr, a, KB, NG, kb, wave, wm, wn, lane, acc);
-    pf_stage<BM, NW>(st1, st0, xr, wr, sr, a, KB, NG, kb + 1, wave, wm, wn, lane, acc);
-    pf_stage<BM, NW>(st2, st1, xr, wr, sr, a, KB, NG, kb + 2, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT>(st0, st2, xr, wr, sr, qr, a, KB, NG, kb, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT>(st1, st0, xr, wr, sr, qr, a, KB, NG, kb + 1, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT>(st2, st1, xr, wr, sr, qr, a, KB, NG, kb + 2, wave, wm, wn, lane, acc);
   }
 
   // epilogue: D lane l holds column l % 16 and rows 4 * (l / 16) + v
 #pragma unroll
-  for (int i = 0; i < P::MS; ++i) {
+  for (int i = 0; i < MS; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + 64 * wn + 16 * j + lr;
+    for (int j = 0; j < NT; ++j) {
+      const int n = n0 + 16 * (NT * wn + j) + lr;
       if (n >= a.N) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int m = m0 + wm * (BM / 2) + 16 * i + 4 * lg + v;
+        const int m = m0 + wm * P::RM + 16 * i + 4 * lg + v;
         if (m >= a.M) continue;
         const size_t o = (size_t)m * a.N + n;
         if (a.out_f32)
@@ -234,28 +319,37 @@ __global__ __launch_bounds__(128 * NW) void pf_gemm_kernel(PfArgs a) {
   }
 }
 
+template <int MS, int NT, int WM, int WN>
+hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
+  using P = Pf<MS, NT, WM, WN>;
+  hipLaunchKernelGGL((pf_gemm_kernel<MS, NT, WM, WN>),
+                     dim3((a.N + P::BN - 1) / P::BN, (a.M + P::BM - 1) / P::BM), dim3(64 * P::W),
+                     0, st, a);
+  return hipGetLastError();
+}
+
+int pf_rows_padded(int M) { return (M + 127) / 128 * 128; }
+
 }  // namespace
 
 bool prefill_supported(int M, int N, int K, int G, int tiled) {
   return tiled && M >= 64 && K % 128 == 0 && G % 128 == 0 && N >= 16;
 }
 
+size_t prefill_workspace_bytes(int M, int K) { return (size_t)(K / 128) * pf_rows_padded(M) * 4; }
+
 hipError_t prefill_gemm(const uint8_t *w, const uint8_t *s, const uint16_t *x, void *y, int M,
-                        int N, int K, int G, int sdt, int out_f32, int num_cus, hipStream_t st) {
-  PfArgs a{w, s, x, y, M, N, K, G, sdt, out_f32};
+                        int N, int K, int G, int sdt, int out_f32, void *ws, int num_cus,
+                        hipStream_t st) {
+  const int Mp = pf_rows_padded(M);
+  float *xs = static_cast<float *>(ws);
+  hipLaunchKernelGGL(pf_xsum_kernel, dim3(Mp / 4), dim3(256), 0, st, x, xs, M, K, Mp);
+  const PfArgs a{w, s, x, xs, y, M, N, K, G, sdt, out_f32, Mp};
   const long tiles_big = (long)((N + 255) / 256) * ((M + 127) / 128);
   const long tiles_mid = (long)((N + 127) / 128) * ((M + 127) / 128);
-  if (tiles_big >= num_cus) {  // 128 x 256 tiles, 8 waves
-    hipLaunchKernelGGL((pf_gemm_kernel<128, 4>), dim3((N + 255) / 256, (M + 127) / 128),
-                       dim3(512), 0, st, a);
-  } else if (tiles_mid >= num_cus) {  // 128 x 128 tiles, 4 waves
-    hipLaunchKernelGGL((pf_gemm_kernel<128, 2>), dim3((N + 127) / 128, (M + 127) / 128),
-                       dim3(256), 0, st, a);
-  } else {  // 64 x 128 tiles
-    hipLaunchKernelGGL((pf_gemm_kernel<64, 2>), dim3((N + 127) / 128, (M + 63) / 64), dim3(256),
-                       0, st, a);
-  }
-  return hipGetLastError();
+  if (tiles_big >= num_cus) return pf_launch<4, 4, 2, 4>(a, st);  // 128 x 256, 8 waves
+  if (tiles_mid >= num_cus) return pf_launch<4, 4, 2, 2>(a, st);  // 128 x 128, 4 waves
+  return pf_launch<2, 4, 2, 2>(a, st);                            // 64 x 128, 4 waves
 }
 
 }  // namespace cai4

@@ -1,6 +1,7 @@
 // prefill.hpp -- INT4 weight-only GEMM for many tokens (M >= 64).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace cai4 {
@@ -8,8 +9,12 @@ namespace cai4 {
 // The prefill kernel handles MFMA-tiled weights with K and G multiples of 128.
 bool prefill_supported(int M, int N, int K, int G, int tiled);
 
+// Device workspace prefill_gemm needs (16-byte aligned): per-row seeds.
+size_t prefill_workspace_bytes(int M, int K);
+
 // y[M, N] = x[M, K] (bf16) * W^T, f32 accumulation; bf16 (RNE) or f32 output.
 hipError_t prefill_gemm(const uint8_t *w, const uint8_t *s, const uint16_t *x, void *y, int M,
-                        int N, int K, int G, int sdt, int out_f32, int num_cus, hipStream_t st);
+                        int N, int K, int G, int sdt, int out_f32, void *ws, int num_cus,
+                        hipStream_t st);
 
 }  // namespace cai4
