@@ -343,20 +343,16 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   const size_t n = (size_t)T * k;
   int32_t *ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(W + m.ws.ids);
   float *wts = weights_out ? weights_out : reinterpret_cast<float *>(W + m.ws.weights);
-  hipError_t e = hipSuccess;
-  if (R->mode == CASCADIA_INT4_ROUTE_IDS) {
-    e = hipMemcpyAsync(ids, R->ids, n * 4, hipMemcpyDeviceToDevice, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(wts, R->weights, n * 4, hipMemcpyDeviceToDevice, st);
-  } else {
-    cai4::MoeRouting r{};
-    r.mode = (int)R->mode;
-    r.top_k = k;
-    r.logits = R->logits;
-    r.bias = R->bias;
-    r.scale = R->scale;
-    r.normalize = (int)R->normalize;
-    e = cai4::moe_route(r, (int)T, E, ids, wts, st);
-  }
+  cai4::MoeRouting r{};
+  r.mode = (int)R->mode;
+  r.top_k = k;
+  r.logits = R->logits;
+  r.bias = R->bias;
+  r.scale = R->scale;
+  r.normalize = (int)R->normalize;
+  r.ids = R->ids;
+  r.weights = R->weights;
+  r.threshold = R->threshold;
   int32_t *pos = reinterpret_cast<int32_t *>(W + m.ws.pos);
   int32_t *row_map = reinterpret_cast<int32_t *>(W + m.ws.row_map);
   cai4::SkinnyChunk *chunks = reinterpret_cast<cai4::SkinnyChunk *>(W + m.ws.chunks);
@@ -366,10 +362,23 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   uint16_t *lo = reinterpret_cast<uint16_t *>(W + m.ws.lo);
   uint16_t *y = reinterpret_cast<uint16_t *>(W + m.ws.y);
   void *part = W + m.ws.part;  // used only when a grouped GEMM splits K
-  if (e == hipSuccess)
-    e = cai4::moe_group(ids, wts, R->threshold, (int)T, E, k, m.ws.chunk_rows, m.ws.max_chunks,
-                        pos, row_map, chunks, counts, st);
-  if (e == hipSuccess) e = cai4::moe_gather(x, row_map, counts, (int)T, H, k, xg, st);
+  hipError_t e = hipSuccess;
+  if (T <= (uint32_t)cai4::kMoePrepMaxTokens) {
+    // decode batches: routing, grouping and gather in one launch
+    e = cai4::moe_prep(r, x, (int)T, E, H, k, m.ws.chunk_rows, m.ws.max_chunks, ids, wts, pos,
+                       chunks, counts, xg, st);
+  } else {
+    if (R->mode == CASCADIA_INT4_ROUTE_IDS) {
+      e = hipMemcpyAsync(ids, R->ids, n * 4, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(wts, R->weights, n * 4, hipMemcpyDeviceToDevice, st);
+    } else {
+      e = cai4::moe_route(r, (int)T, E, ids, wts, st);
+    }
+    if (e == hipSuccess)
+      e = cai4::moe_group(ids, wts, R->threshold, (int)T, E, k, m.ws.chunk_rows,
+                          m.ws.max_chunks, pos, row_map, chunks, counts, st);
+    if (e == hipSuccess) e = cai4::moe_gather(x, row_map, counts, (int)T, H, k, xg, st);
+  }
   size_t off[6];
   expert_blob_sections(L->hidden, L->inter, L->group_size, L->tiling, off);
   const int G = (int)L->group_size;

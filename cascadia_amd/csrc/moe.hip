@@ -72,70 +72,84 @@ MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows
 // routing: one wave per token
 // ---------------------------------------------------------------------------
 
-CAI4_DEV bool better(float c, int i, float bc, int bi) { return c > bc || (c == bc && i < bi); }
+// Wave-wide max of a float, in every lane: DPP within 16-lane rows (xor 1,
+// xor 2, rotate 4, rotate 8), then row pairs and halves by permlane swaps --
+// no LDS round trips.
+template <int CTRL>
+CAI4_DEV float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+CAI4_DEV float wave_max_f32(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm 1,0,3,2
+  v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm 2,3,0,1
+  v = fmaxf(v, dpp_move<0x124>(v));  // row_ror 4
+  v = fmaxf(v, dpp_move<0x128>(v));  // row_ror 8
+  auto a = __builtin_amdgcn_permlane16_swap(fbits(v), fbits(v), false, false);
+  v = fmaxf(bitsf(a[0]), bitsf(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(fbits(v), fbits(v), false, false);
+  return fmaxf(bitsf(b[0]), bitsf(b[1]));
+}
 
-__global__ __launch_bounds__(256) void moe_route_kernel(MoeRouting r, int T, int E, int32_t *ids,
-                                                        float *wout) {
-  constexpr int R = kMoeMaxExperts / 64;
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;  // whole waves; no barriers in this kernel
+CAI4_DEV float lane_f32(float v, int l) {
+  return bitsf(__builtin_amdgcn_readlane(fbits(v), l));
+}
+
+// Selections of token t in one wave.  Lane l holds experts l * nj .. l * nj +
+// nj - 1, so the lowest lane holding a maximum holds the lowest expert id of
+// it.  Each of the k rounds takes the lane-local best (lowest j among equal
+// keys), a wave-wide max, and the lowest lane whose best equals it.  NaN keys
+// never win.  Lane kk < k returns selection kk: its expert and weight.
+template <int R>  // R >= ceil(E / 64): registers per lane
+CAI4_DEV void route_token(const MoeRouting &r, int t, int E, int lane, int &id_out,
+                          float &w_out) {
   const bool sig = r.mode == ROUTE_SIGMOID_BIAS;
-  const int nj = (E + 63) >> 6;  // registers in use per lane
-  // all loads first, branch-free (experts past E read 0 from the range check)
+  const int nj = (E + 63) >> 6;
   const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(r.logits + (size_t)t * E), (short)0, E * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(r.bias), (short)0, r.bias ? E * 4 : 0, 0x00020000);
-  float lg[R], bs[R];
+  float key[R], val[R];
 #pragma unroll
   for (int j = 0; j < R; ++j) {
-    const uint32_t off = j < nj ? (uint32_t)(lane + 64 * j) * 4 : 0x80000000u;
-    lg[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, 0));
-    bs[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
+    key[j] = -INFINITY;
+    val[j] = 0.f;
+    if (j < nj) {  // uniform
+      const uint32_t off = (uint32_t)(lane * nj + j) * 4;
+      const float lg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, 0));
+      const float bs = sig ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0)) : 0.f;
+      const float sv = sig ? 1.0f / (1.0f + expf(-lg)) : lg;
+      const float c = sig ? sv + bs : sv;
+      val[j] = sv;
+      key[j] = c != c ? -INFINITY : c;
+    }
   }
-  float choice[R], val[R];
+  uint32_t valid = 0;  // experts of this lane that exist and are not yet taken
 #pragma unroll
-  for (int j = 0; j < R; ++j) {
-    const bool ok = lane + 64 * j < E;
-    const float s = sig ? 1.0f / (1.0f + expf(-lg[j])) : lg[j];
-    val[j] = s;
-    choice[j] = ok ? (sig ? s + bs[j] : s) : -INFINITY;
-  }
-  // k rounds of a wave-wide argmax (ties to the lower id); lane kk keeps
-  // selection kk
-  uint32_t taken = 0;
-  float my_val = 0.f;
+  for (int j = 0; j < R; ++j)
+    if (j < nj && lane * nj + j < E) valid |= 1u << j;
   int my_id = 0;
+  float my_val = 0.f;
   for (int kk = 0; kk < r.top_k; ++kk) {
-    float bc = -INFINITY;
-    int bi = 0x7FFFFFFF;
+    float best = -INFINITY, bval = 0.f;
+    int bj = -1;
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-      const int e = lane + 64 * j;
-      if (j < nj && e < E && !((taken >> j) & 1u) && better(choice[j], e, bc, bi)) {
-        bc = choice[j];
-        bi = e;
+      if (((valid >> j) & 1u) && (bj < 0 || key[j] > best)) {
+        best = key[j];
+        bval = val[j];
+        bj = j;
       }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float oc = __shfl_xor(bc, off);
-      const int oi = __shfl_xor(bi, off);
-      if (better(oc, oi, bc, bi)) {
-        bc = oc;
-        bi = oi;
-      }
-    }
-    const int jj = bi >> 6;
-    float mine = 0.f;
-#pragma unroll
-    for (int j = 0; j < R; ++j) mine = j == jj ? val[j] : mine;
-    const float v = __shfl(mine, bi & 63);
-    if ((bi & 63) == lane) taken |= 1u << jj;
+    const float m = wave_max_f32(bj < 0 ? -INFINITY : best);
+    const uint64_t hit = __ballot(bj >= 0 && best == m);
+    const int sl = __builtin_amdgcn_readfirstlane(__builtin_ffsll((long long)hit) - 1);
+    const int sj = __builtin_amdgcn_readlane(bj, sl);
+    const float sv = lane_f32(bval, sl);
+    if (lane == sl) valid &= ~(1u << sj);
     if (lane == kk) {
-      my_val = v;
-      my_id = bi;
+      my_id = sl * nj + sj;
+      my_val = sv;
     }
   }
   // weights, summed in selection order as the crate does
@@ -144,29 +158,54 @@ __global__ __launch_bounds__(256) void moe_route_kernel(MoeRouting r, int T, int
   if (sig) {
     if (r.normalize && k > 1) {
       float s = 0.0f;
-      for (int kk = 0; kk < k; ++kk) s += __shfl(my_val, kk);
+      for (int kk = 0; kk < k; ++kk) s += lane_f32(my_val, kk);
       s += 1.0e-20f;
       w = my_val / s * r.scale;
     } else {
       w = my_val * r.scale;
     }
   } else {
-    const float mx = __shfl(my_val, 0);
+    const float mx = lane_f32(my_val, 0);
     const float ex = expf(my_val - mx);
     float s = 0.0f;
-    for (int kk = 0; kk < k; ++kk) s += __shfl(ex, kk);
+    for (int kk = 0; kk < k; ++kk) s += lane_f32(ex, kk);
     w = ex / s;
   }
-  if (lane < k) {
-    ids[(size_t)t * k + lane] = my_id;
-    wout[(size_t)t * k + lane] = w;
+  id_out = my_id;
+  w_out = w;
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void moe_route_kernel(MoeRouting r, int T, int E, int32_t *ids,
+                                                        float *wout) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves; no barriers in this kernel
+  int id;
+  float w;
+  route_token<R>(r, t, E, lane, id, w);
+  if (lane < r.top_k) {
+    ids[(size_t)t * r.top_k + lane] = id;
+    wout[(size_t)t * r.top_k + lane] = w;
   }
 }
 
+// Instantiations by registers per lane, ceil(E / 64) rounded up to a power
+// of two: the loops over a lane's experts are unrolled.
+#define CAI4_MOE_DISPATCH(E, CALL)           \
+  do {                                       \
+    const int nj_ = ((E) + 63) / 64;         \
+    if (nj_ <= 1) { constexpr int R = 1; CALL; }        \
+    else if (nj_ <= 2) { constexpr int R = 2; CALL; }   \
+    else if (nj_ <= 4) { constexpr int R = 4; CALL; }   \
+    else if (nj_ <= 8) { constexpr int R = 8; CALL; }   \
+    else { constexpr int R = 16; CALL; }                \
+  } while (0)
+
 hipError_t moe_route(const MoeRouting &r, int T, int E, int32_t *ids, float *w, hipStream_t st) {
   const int waves = 4;
-  hipLaunchKernelGGL(moe_route_kernel, dim3((T + waves - 1) / waves), dim3(64 * waves), 0, st, r,
-                     T, E, ids, w);
+  CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_route_kernel<R>, dim3((T + waves - 1) / waves),
+                                          dim3(64 * waves), 0, st, r, T, E, ids, w));
   return hipGetLastError();
 }
 
@@ -174,77 +213,206 @@ hipError_t moe_route(const MoeRouting &r, int T, int E, int32_t *ids, float *w, 
 // grouping: one workgroup
 // ---------------------------------------------------------------------------
 
-// Grouping runs in one wave: counts by LDS atomics, then each lane scans a
-// contiguous run of experts and a wave prefix joins the runs.
+// Exclusive prefix sum over the 64 lanes of a wave, by DPP: Kogge-Stone
+// within each 16-lane row (row_shr 1, 2, 4, 8), then the row totals carried
+// by row_bcast 15 and 31.  *total gets the sum of all lanes.
+template <int CTRL, int ROWS>
+CAI4_DEV int dpp_add_in(int v) {
+  return v + __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, true);
+}
 CAI4_DEV int wave_exclusive_scan(int x, int *total) {
-  const int lane = threadIdx.x & 63;
-  int inc = x;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(inc, d);
-    if (lane >= d) inc += y;
-  }
-  *total = __shfl(inc, 63);
-  return inc - x;
+  int v = x;
+  v = dpp_add_in<0x111, 0xF>(v);  // row_shr 1
+  v = dpp_add_in<0x112, 0xF>(v);  // row_shr 2
+  v = dpp_add_in<0x114, 0xF>(v);  // row_shr 4
+  v = dpp_add_in<0x118, 0xF>(v);  // row_shr 8
+  v = dpp_add_in<0x142, 0xA>(v);  // row_bcast 15 into rows 1, 3
+  v = dpp_add_in<0x143, 0xC>(v);  // row_bcast 31 into rows 2, 3
+  *total = __builtin_amdgcn_readlane(v, 63);
+  return v - x;
 }
 
+// Grouping of the n = T k assignments by expert, by every thread of the
+// workgroup: counts by LDS atomics (rank of each valid assignment within its
+// expert in rank[]), then wave 0 scans contiguous runs of experts per lane and
+// writes the chunks, then every thread places its assignments.  ids/w may be
+// global or LDS.  On return (after a barrier) rowmap[p] is the token of
+// grouped row p, and *total / *nchunks hold the counts.
+// Barrier for LDS data only: the global stores of these kernels are read by
+// later launches, never by another thread of the same workgroup, so they need
+// not be waited for (__syncthreads would wait for every store to complete).
+CAI4_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ceil(a / C) for 0 <= a < 2^20 and 1 <= C <= 64: a float estimate, then one
+// correction step each way (exact; no integer division).
+CAI4_DEV int ceil_div_small(int a, int C, float invC) {
+  const int n = a + C - 1;
+  int q = (int)((float)n * invC);
+  if (q * C > n) --q;
+  if ((q + 1) * C <= n) ++q;
+  return q;
+}
+
+struct GroupLds {
+  int cnt[kMoeMaxExperts], off[kMoeMaxExperts];
+  int total, nchunks;
+};
+
+template <int PMAX>  // PMAX >= ceil(E / 64)
+CAI4_DEV void group_assignments(const int32_t *ids, const float *w, float thr, int T, int E,
+                                int k, int C, int max_chunks, int *rank, GroupLds &g,
+                                int32_t *pos, int *rowmap, SkinnyChunk *chunks,
+                                int32_t *counts) {
+  const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63;
+  const int n = T * k;
+  for (int e = tid; e < E; e += nth) g.cnt[e] = 0;
+  lds_barrier();
+  for (int i = tid; i < n; i += nth) {
+    const int e = ids[i];
+    const bool ok = !(w[i] < thr) && e >= 0 && e < E;  // runner.rs:1811: skip w < threshold
+    rank[i] = ok ? atomicAdd(&g.cnt[e], 1) : -1;
+  }
+  lds_barrier();
+  if (tid < 64) {
+    // lane l scans experts l * per .. l * per + per - 1 (all its counts read
+    // at once: the loop carries no LDS latency)
+    const int per = (E + 63) >> 6, e0 = lane * per;
+    const float invC = 1.0f / (float)C;
+    int c[PMAX], nc[PMAX];
+    int rows = 0, chs = 0;
+#pragma unroll
+    for (int q = 0; q < PMAX; ++q) {
+      c[q] = q < per && e0 + q < E ? g.cnt[e0 + q] : 0;
+      nc[q] = ceil_div_small(c[q], C, invC);
+      rows += c[q];
+      chs += nc[q];
+    }
+    int total, total_chunks;
+    int ro = wave_exclusive_scan(rows, &total), co = wave_exclusive_scan(chs, &total_chunks);
+#pragma unroll
+    for (int q = 0; q < PMAX; ++q) {
+      if (q < per && e0 + q < E) {
+        const int e = e0 + q;
+        g.off[e] = ro;
+        for (int h = 0; h < nc[q]; ++h) {
+          const int left = c[q] - h * C;
+          chunks[co + h] = SkinnyChunk{e, ro + h * C, left < C ? left : C, 0};
+        }
+      }
+      ro += c[q];
+      co += nc[q];
+    }
+    for (int j = total_chunks + lane; j < max_chunks; j += 64) chunks[j] = SkinnyChunk{0, 0, 0, 0};
+    if (lane == 0) {
+      g.total = total;
+      g.nchunks = total_chunks;
+      counts[0] = total;
+      counts[1] = total_chunks;
+    }
+  }
+  lds_barrier();
+  for (int i = tid; i < n; i += nth) {
+    const int rk = rank[i];
+    int p = -1;
+    if (rk >= 0) {
+      p = g.off[ids[i]] + rk;
+      rowmap[p] = i / k;
+    }
+    pos[i] = p;
+  }
+  lds_barrier();
+}
+
+template <int R>
 __global__ __launch_bounds__(64) void moe_group_kernel(const int32_t *ids, const float *w,
                                                        float thr, int T, int E, int k, int C,
                                                        int max_chunks, int32_t *pos,
                                                        int32_t *row_map, SkinnyChunk *chunks,
                                                        int32_t *counts) {
-  __shared__ int cnt[kMoeMaxExperts], off[kMoeMaxExperts], choff[kMoeMaxExperts];
-  const int lane = threadIdx.x;
-  const int n = T * k;
-  for (int e = lane; e < E; e += 64) cnt[e] = 0;
-  __syncthreads();
-  // rank of each valid assignment within its expert (kept in pos for now)
-  for (int i = lane; i < n; i += 64) {
-    const int e = ids[i];
-    const bool ok = !(w[i] < thr) && e >= 0 && e < E;  // runner.rs:1811: skip w < threshold
-    pos[i] = ok ? atomicAdd(&cnt[e], 1) : -1;
-  }
-  __syncthreads();
-  const int per = (E + 63) >> 6, e0 = lane * per, e1 = min(E, e0 + per);
-  int rows = 0, chs = 0;
-  for (int e = e0; e < e1; ++e) {
-    rows += cnt[e];
-    chs += (cnt[e] + C - 1) / C;
-  }
-  int total, total_chunks;
-  int ro = wave_exclusive_scan(rows, &total), co = wave_exclusive_scan(chs, &total_chunks);
-  for (int e = e0; e < e1; ++e) {
-    off[e] = ro;
-    choff[e] = co;
-    const int c = cnt[e];
-    for (int q = 0; q * C < c; ++q) {
-      const int left = c - q * C;
-      chunks[co + q] = SkinnyChunk{e, ro + q * C, left < C ? left : C, 0};
-    }
-    ro += c;
-    co += (c + C - 1) / C;
-  }
-  __syncthreads();
-  for (int i = lane; i < n; i += 64) {
-    const int rk = pos[i];
-    if (rk >= 0) {
-      const int p = off[ids[i]] + rk;
-      pos[i] = p;
-      row_map[p] = i / k;
-    }
-  }
-  for (int j = total_chunks + lane; j < max_chunks; j += 64) chunks[j] = SkinnyChunk{0, 0, 0, 0};
-  if (lane == 0) {
-    counts[0] = total;
-    counts[1] = total_chunks;
-  }
+  __shared__ GroupLds g;
+  // pos doubles as the rank array: each slot is read before it is written
+  group_assignments<R>(ids, w, thr, T, E, k, C, max_chunks, pos, g, pos, row_map, chunks,
+                      counts);
 }
 
 hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T, int E,
                      int top_k, int chunk_rows, int max_chunks, int32_t *pos, int32_t *row_map,
                      SkinnyChunk *chunks, int32_t *counts, hipStream_t st) {
-  hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64), 0, st, ids, w, threshold, T, E,
-                     top_k, chunk_rows, max_chunks, pos, row_map, chunks, counts);
+  CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_group_kernel<R>, dim3(1), dim3(64), 0, st, ids, w,
+                                          threshold, T, E, top_k, chunk_rows, max_chunks, pos,
+                                          row_map, chunks, counts));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// decode batches: routing, grouping and gather in one workgroup
+// ---------------------------------------------------------------------------
+
+// One bf16 row chunk of the gather: xg[p, j .. j + 7] = bf16(x[t, j .. j + 7]).
+CAI4_DEV void gather8(const float *x, int t, int p, int j, int H, uint16_t *xg) {
+  const f32x4_t *src = reinterpret_cast<const f32x4_t *>(x + (size_t)t * H + j);
+  const f32x4_t a = src[0], b = src[1];
+  u32x4_t o;
+  o.x = f32_to_bf16_rne(a.x) | (f32_to_bf16_rne(a.y) << 16);
+  o.y = f32_to_bf16_rne(a.z) | (f32_to_bf16_rne(a.w) << 16);
+  o.z = f32_to_bf16_rne(b.x) | (f32_to_bf16_rne(b.y) << 16);
+  o.w = f32_to_bf16_rne(b.z) | (f32_to_bf16_rne(b.w) << 16);
+  *reinterpret_cast<u32x4_t *>(xg + (size_t)p * H + j) = o;
+}
+
+// T <= kMoePrepMaxTokens: wave w routes tokens w, w + 8, ... (or copies the
+// given ids), the selections stay in LDS for the grouping, and the gather
+// reads the row map from LDS: one launch instead of three dependent ones.
+template <int R>
+__global__ __launch_bounds__(512) void moe_prep_kernel(MoeRouting r, const float *x, int T,
+                                                        int E, int H, int k, int C,
+                                                        int max_chunks, int32_t *ids, float *wts,
+                                                        int32_t *pos, SkinnyChunk *chunks,
+                                                        int32_t *counts, uint16_t *xg) {
+  constexpr int NMAX = kMoePrepMaxTokens * kMoeMaxTopK;
+  __shared__ int s_ids[NMAX], s_rank[NMAX], s_row[NMAX];
+  __shared__ float s_w[NMAX];
+  __shared__ GroupLds g;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // touch every 128-byte line of x now, so the gather at the end finds it in
+  // cache (and its pages mapped) instead of waiting on memory after routing
+  float touch = 0.f;
+  for (int i = threadIdx.x; i < T * H / 32; i += blockDim.x) touch += x[(size_t)i * 32];
+  for (int t = wave; t < T; t += nw) {
+    int id = 0;
+    float w = 0.f;
+    if (r.mode == ROUTE_IDS) {
+      if (lane < k) {
+        id = r.ids[(size_t)t * k + lane];
+        w = r.weights[(size_t)t * k + lane];
+      }
+    } else {
+      route_token<R>(r, t, E, lane, id, w);
+    }
+    if (lane < k) {
+      s_ids[t * k + lane] = id;
+      s_w[t * k + lane] = w;
+      ids[(size_t)t * k + lane] = id;
+      wts[(size_t)t * k + lane] = w;
+    }
+  }
+  lds_barrier();
+  group_assignments<R>(s_ids, s_w, r.threshold, T, E, k, C, max_chunks, s_rank, g, pos, s_row,
+                       chunks, counts);
+  const int per_row = H / 8;
+  for (int q = threadIdx.x; q < g.total * per_row; q += blockDim.x) {
+    const int p = q / per_row, j = (q - p * per_row) * 8;
+    gather8(x, s_row[p], p, j, H, xg);
+  }
+  if (__builtin_bit_cast(uint32_t, touch) == 0x7FC0DEADu) counts[2] = 0;  // keeps the touch loads
+}
+
+hipError_t moe_prep(const MoeRouting &r, const float *x, int T, int E, int H, int top_k,
+                    int chunk_rows, int max_chunks, int32_t *ids, float *w, int32_t *pos,
+                    SkinnyChunk *chunks, int32_t *counts, uint16_t *xg, hipStream_t st) {
+  CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_prep_kernel<R>, dim3(1), dim3(512), 0, st, r, x, T,
+                                          E, H, top_k, chunk_rows, max_chunks, ids, w, pos,
+                                          chunks, counts, xg));
   return hipGetLastError();
 }
 
@@ -259,15 +427,7 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const float *x, const i
   if (p >= counts[0]) return;
   const int j = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (j >= H) return;
-  const int t = row_map[p];
-  const f32x4_t *src = reinterpret_cast<const f32x4_t *>(x + (size_t)t * H + j);
-  const f32x4_t a = src[0], b = src[1];
-  u32x4_t o;
-  o.x = f32_to_bf16_rne(a.x) | (f32_to_bf16_rne(a.y) << 16);
-  o.y = f32_to_bf16_rne(a.z) | (f32_to_bf16_rne(a.w) << 16);
-  o.z = f32_to_bf16_rne(b.x) | (f32_to_bf16_rne(b.y) << 16);
-  o.w = f32_to_bf16_rne(b.z) | (f32_to_bf16_rne(b.w) << 16);
-  *reinterpret_cast<u32x4_t *>(xg + (size_t)p * H + j) = o;
+  gather8(x, row_map[p], p, j, H, xg);
 }
 
 hipError_t moe_gather(const float *x, const int32_t *row_map, const int32_t *counts, int T,
@@ -291,15 +451,25 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float *residual,
   f32x4_t h = {0.f, 0.f, 0.f, 0.f};
   if (residual) h = *reinterpret_cast<const f32x4_t *>(residual + o);
   if (shared) h += *reinterpret_cast<const f32x4_t *>(shared + o);
+  // all slot loads first (k <= kMoeMaxTopK), then the sum in slot order
+  int ps[kMoeMaxTopK];
+  float ws[kMoeMaxTopK];
+#pragma unroll
+  for (int kk = 0; kk < kMoeMaxTopK; ++kk) {
+    ps[kk] = kk < k ? pos[(size_t)t * k + kk] : -1;
+    ws[kk] = kk < k ? w[(size_t)t * k + kk] : 0.f;
+  }
+  u32x2_t yy[kMoeMaxTopK];
+#pragma unroll
+  for (int kk = 0; kk < kMoeMaxTopK; ++kk)
+    if (ps[kk] >= 0) yy[kk] = *reinterpret_cast<const u32x2_t *>(y + (size_t)ps[kk] * H + j);
   f32x4_t moe = {0.f, 0.f, 0.f, 0.f};
-  for (int kk = 0; kk < k; ++kk) {
-    const int p = pos[(size_t)t * k + kk];
-    if (p < 0) continue;
-    const float wk = w[(size_t)t * k + kk];
-    const u32x2_t yy = *reinterpret_cast<const u32x2_t *>(y + (size_t)p * H + j);
-    const f32x4_t yf = {bf16_to_f32(yy.x & 0xFFFFu), bf16_to_f32(yy.x >> 16),
-                        bf16_to_f32(yy.y & 0xFFFFu), bf16_to_f32(yy.y >> 16)};
-    moe += wk * yf;
+#pragma unroll
+  for (int kk = 0; kk < kMoeMaxTopK; ++kk) {
+    if (ps[kk] < 0) continue;
+    const f32x4_t yf = {bf16_to_f32(yy[kk].x & 0xFFFFu), bf16_to_f32(yy[kk].x >> 16),
+                        bf16_to_f32(yy[kk].y & 0xFFFFu), bf16_to_f32(yy[kk].y >> 16)};
+    moe += ws[kk] * yf;
   }
   *reinterpret_cast<f32x4_t *>(out + o) = h + moe;
 }
