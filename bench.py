@@ -49,6 +49,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--extra", action="store_true", help="also time configs 0 and 2, M=4/16")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="launch the config 2 prefill GEMMs eagerly, without timing, for rocprofv3")
+    ap.add_argument("--profile-moe", action="store_true",
+                    help="run configs 3 and 4 at T=1 (a few steps), for rocprofv3")
     ap.add_argument("--profile", action="store_true",
                     help="launch the headline kernels and a 256 MiB copy (counter calibration) "
                          "eagerly, without timing, for rocprofv3")
@@ -211,28 +215,37 @@ def extra_measurements(cl, torch, args, sdt, copies):
                            "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4), "copies": ncp}
     del PS
     # config 2: prefill GEMM (bf16 in/out)
-    for (m, nn) in [(512, 4096), (2048, 14336)]:
-        kk = 4096
-        pk = cl.fill_bytes(torch.empty(nn * kk // 2, dtype=torch.uint8, device="cuda"), 2, 1)
-        sc = cl.fill_scales(torch.empty(nn * (kk // g) * 2, dtype=torch.uint8, device="cuda"),
-                            2, 2, sdt)
-        pt, st = cl.tile_weights(pk, sc, nn, kk, g)
-        xb = cl.fill_normal(torch.empty(m * kk, dtype=torch.bfloat16, device="cuda"), 2, 3)
-        yb = torch.empty(m * nn, dtype=torch.bfloat16, device="cuda")
-
-        def pre(r):
-            cl.gemm_int4_bf16(pt, st, xb, nn, kk, m, yb, group_size=g, scale_dtype=sdt,
-                              tiling=cl.TILING_MFMA)
+    for (m, nn) in PREFILL_SHAPES:
+        pre = prefill_fn(cl, torch, m, nn, 4096, g, sdt)
         pre(0)
         reps = 10
         w, _ = graph_time(torch, pre, reps)
         t = w / reps
-        tf = 2.0 * m * nn * kk / t / 1e12
+        tf = 2.0 * m * nn * 4096 / t / 1e12
         res[f"config2_prefill_M{m}_N{nn}"] = {"us_per_call": round(t * 1e6, 1),
                                               "TFLOP/s": round(tf, 1),
                                               "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
-        del pk, sc, pt, st, xb, yb
+        del pre
     return res
+
+
+PREFILL_SHAPES = [(512, 4096), (512, 14336), (2048, 4096), (2048, 14336)]
+
+
+def prefill_fn(cl, torch, m, nn, kk, g, sdt):
+    """One config 2 prefill GEMM (bf16 x, MFMA-tiled weights, bf16 out)."""
+    pk = cl.fill_bytes(torch.empty(nn * kk // 2, dtype=torch.uint8, device="cuda"), 2, 1)
+    sc = cl.fill_scales(torch.empty(nn * (kk // g) * 2, dtype=torch.uint8, device="cuda"), 2, 2,
+                        sdt)
+    pt, st = cl.tile_weights(pk, sc, nn, kk, g)
+    del pk, sc
+    xb = cl.fill_normal(torch.empty(m * kk, dtype=torch.bfloat16, device="cuda"), 2, 3)
+    yb = torch.empty(m * nn, dtype=torch.bfloat16, device="cuda")
+
+    def pre(r):
+        cl.gemm_int4_bf16(pt, st, xb, nn, kk, m, yb, group_size=g, scale_dtype=sdt,
+                          tiling=cl.TILING_MFMA)
+    return pre
 
 
 def make_experts_dev(cl, torch, E, h, i, g, sdt, seed):
@@ -316,6 +329,23 @@ def main():
     import cascadia_amd as cl
 
     sdt = cl.SCALE_F16
+    if args.profile_prefill:
+        for (pm, pn) in PREFILL_SHAPES:
+            pre = prefill_fn(cl, torch, pm, pn, 4096, 128, sdt)
+            for r in range(5):
+                pre(r)
+            torch.cuda.synchronize()
+            del pre
+        print(json.dumps({"profile": "prefill", "shapes": PREFILL_SHAPES, "launches": 5}),
+              flush=True)
+        return
+    if args.profile_moe:
+        r3 = bench_moe(cl, torch, "config3", 256, 3072, 1536, 128, 8, 1, 1,
+                       cl.ROUTE_SOFTMAX_TOPK, 1.0, 0, 50, nsets=16)
+        r4 = bench_moe(cl, torch, "config4", 384, 7168, 2048, 32, 8, 1, 4, cl.ROUTE_SIGMOID_BIAS,
+                       2.827, 2048, 20, zipf=1.1, nsets=16)
+        print(json.dumps({"profile": "moe", "config3_T1": r3, "config4_T1": r4}), flush=True)
+        return
     h, i, g, m = 4096, 14336, 128, args.m
     per_copy = cl.expert_bytes(h, i, g)
     ncopies = math.ceil(2 * MALL_BYTES / per_copy) + 1

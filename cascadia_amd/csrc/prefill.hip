@@ -93,26 +93,43 @@ struct PfArgs {
 };
 
 // Seeds: xs[kb][m] = -136 * sum_{c < 128} x[m, 128 kb + c] (f32, fixed order:
-// eight columns per lane, then a butterfly over the 16 lanes of the block);
-// rows M .. Mp - 1 are 0.  One wave per row, four k-blocks per pass.
+// eight columns per lane, then the 16 lanes of a DPP row, which hold one
+// k-block); rows M .. Mp - 1 are 0.  One wave per row; a pass covers four
+// k-blocks, and a wave issues the loads of up to eight passes before summing.
+template <int CTRL>
+CAI4_DEV float dpp_row_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                           0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 __global__ __launch_bounds__(256) void pf_xsum_kernel(const uint16_t *x, float *xs, int M, int K,
                                                       int Mp) {
+  constexpr int P = 8;  // passes in flight
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= Mp) return;
-  const int KB = K >> 7;
-  for (int kb0 = 0; kb0 < KB; kb0 += 4) {
-    const int kb = kb0 + (lane >> 4);
-    float t = 0.f;
-    if (m < M && kb < KB) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t *>(x + (size_t)m * K + kb * 128 +
-                                                           8 * (lane & 15));
+  const int KB = K >> 7, passes = (KB + 3) >> 2;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(x + (size_t)(m < M ? m : 0) * K), (short)0, m < M ? K * 2 : 0,
+      0x00020000);
+  for (int p0 = 0; p0 < passes; p0 += P) {
+    u32x4_t v[P];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) t += bf16_to_f32(v[e] & 0xFFFFu) + bf16_to_f32(v[e] >> 16);
+    for (int q = 0; q < P; ++q)  // columns 512 (p0 + q) + 8 lane; past K reads 0
+      v[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                             xr, (uint32_t)(512 * (p0 + q) + 8 * lane) * 2, 0, 0));
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      float t = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t += bf16_to_f32(v[q][e] & 0xFFFFu) + bf16_to_f32(v[q][e] >> 16);
+      t = dpp_row_add<0xB1>(t);   // quad_perm 1,0,3,2
+      t = dpp_row_add<0x4E>(t);   // quad_perm 2,3,0,1
+      t = dpp_row_add<0x124>(t);  // row_ror 4
+      t = dpp_row_add<0x128>(t);  // row_ror 8
+      const int kb = 4 * (p0 + q) + (lane >> 4);
+      if ((lane & 15) == 0 && kb < KB) xs[(size_t)kb * Mp + m] = -136.f * t;
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) t += __shfl_xor(t, o, 64);
-    if ((lane & 15) == 0 && kb < KB) xs[(size_t)kb * Mp + m] = -136.f * t;
   }
 }
 
