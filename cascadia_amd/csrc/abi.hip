@@ -282,7 +282,9 @@ int moe_check(const cascadia_int4_moe_layer *L, uint32_t top_k, uint32_t T) {
       L->expert_stride < expert_blob_bytes(H, I, G, L->tiling))
     return CASCADIA_INT4_ERR_ARG;
   const size_t rows = (size_t)T * top_k;
-  if (rows * H * 2 >= 0x7FFFFFFFu || rows * I * 2 >= 0x7FFFFFFFu) return CASCADIA_INT4_ERR_ARG;
+  if (rows * H * 2 >= 0x7FFFFFFFu || rows * I * 2 >= 0x7FFFFFFFu ||
+      (size_t)T * H * 4 >= 0x7FFFFFFFu)
+    return CASCADIA_INT4_ERR_ARG;
   if (has_shared(L)) {
     if (L->shared_inter == 0 || L->shared_inter % G) return CASCADIA_INT4_ERR_ARG;
     if (int rc = check_expert(H, L->shared_inter, G, L->scale_dtype, &L->shared)) return rc;
@@ -303,7 +305,7 @@ MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint
   const int C = cai4::moe_chunk_rows((int)T, given_ids ? (int)(T * top_k) : (int)T);
   const int maxc = cai4::moe_max_chunks((int)T, (int)L->n_experts, (int)top_k, C);
   MoePlan m{};
-  m.gu = cai4::skinny_plan_grouped(I, H, G, C, maxc, cai4::A_BF16, cai4::EPI_SWIGLU_HILO, d);
+  m.gu = cai4::skinny_plan_grouped(I, H, G, C, maxc, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d);
   m.dn = cai4::skinny_plan_grouped(H, I, G, C, maxc, cai4::A_HILO, cai4::EPI_BF16, d);
   const size_t part = m.gu.partial_bytes > m.dn.partial_bytes ? m.gu.partial_bytes
                                                               : m.dn.partial_bytes;
@@ -357,16 +359,15 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   int32_t *row_map = reinterpret_cast<int32_t *>(W + m.ws.row_map);
   cai4::SkinnyChunk *chunks = reinterpret_cast<cai4::SkinnyChunk *>(W + m.ws.chunks);
   int32_t *counts = reinterpret_cast<int32_t *>(W + m.ws.counts);
-  uint16_t *xg = reinterpret_cast<uint16_t *>(W + m.ws.xg);
   uint16_t *hi = reinterpret_cast<uint16_t *>(W + m.ws.hi);
   uint16_t *lo = reinterpret_cast<uint16_t *>(W + m.ws.lo);
   uint16_t *y = reinterpret_cast<uint16_t *>(W + m.ws.y);
   void *part = W + m.ws.part;  // used only when a grouped GEMM splits K
   hipError_t e = hipSuccess;
   if (T <= (uint32_t)cai4::kMoePrepMaxTokens) {
-    // decode batches: routing, grouping and gather in one launch
-    e = cai4::moe_prep(r, x, (int)T, E, H, k, m.ws.chunk_rows, m.ws.max_chunks, ids, wts, pos,
-                       chunks, counts, xg, st);
+    // small decode batches: routing and grouping in one launch
+    e = cai4::moe_prep(r, (int)T, E, k, m.ws.chunk_rows, m.ws.max_chunks, ids, wts, pos, row_map,
+                       chunks, counts, st);
   } else {
     if (R->mode == CASCADIA_INT4_ROUTE_IDS) {
       e = hipMemcpyAsync(ids, R->ids, n * 4, hipMemcpyDeviceToDevice, st);
@@ -377,7 +378,6 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     if (e == hipSuccess)
       e = cai4::moe_group(ids, wts, R->threshold, (int)T, E, k, m.ws.chunk_rows,
                           m.ws.max_chunks, pos, row_map, chunks, counts, st);
-    if (e == hipSuccess) e = cai4::moe_gather(x, row_map, counts, (int)T, H, k, xg, st);
   }
   size_t off[6];
   expert_blob_sections(L->hidden, L->inter, L->group_size, L->tiling, off);
@@ -388,7 +388,9 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     a.s0 = L->experts + off[1];
     a.w1 = L->experts + off[2];
     a.s1 = L->experts + off[3];
-    a.x = xg;
+    a.x = x;  // f32 token rows, read through the row map and rounded to bf16 while staged
+    a.row_map = row_map;
+    a.x_rows = (int)T;
     a.out = hi;
     a.out2 = lo;
     a.partials = part;
@@ -403,7 +405,7 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     a.sdt = (int)L->scale_dtype;
     a.glog2 = glog2_of(G);
     a.tiled = (int)L->tiling;
-    e = cai4::skinny_launch(a, m.gu, cai4::A_BF16, cai4::EPI_SWIGLU_HILO, st);
+    e = cai4::skinny_launch(a, m.gu, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, st);
   }
   if (e == hipSuccess) {
     cai4::SkinnyArgs a{};

@@ -57,7 +57,6 @@ MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows
   w.row_map = take(n * 4);
   w.chunks = take((size_t)w.max_chunks * sizeof(SkinnyChunk));
   w.counts = take(16);
-  w.xg = take(n * H * 2);
   w.hi = take(n * I * 2);
   w.lo = take(n * I * 2);
   w.y = take(n * H * 2);
@@ -345,39 +344,22 @@ hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T,
 }
 
 // ---------------------------------------------------------------------------
-// decode batches: routing, grouping and gather in one workgroup
+// decode batches: routing and grouping in one workgroup
 // ---------------------------------------------------------------------------
 
-// One bf16 row chunk of the gather: xg[p, j .. j + 7] = bf16(x[t, j .. j + 7]).
-CAI4_DEV void gather8(const float *x, int t, int p, int j, int H, uint16_t *xg) {
-  const f32x4_t *src = reinterpret_cast<const f32x4_t *>(x + (size_t)t * H + j);
-  const f32x4_t a = src[0], b = src[1];
-  u32x4_t o;
-  o.x = f32_to_bf16_rne(a.x) | (f32_to_bf16_rne(a.y) << 16);
-  o.y = f32_to_bf16_rne(a.z) | (f32_to_bf16_rne(a.w) << 16);
-  o.z = f32_to_bf16_rne(b.x) | (f32_to_bf16_rne(b.y) << 16);
-  o.w = f32_to_bf16_rne(b.z) | (f32_to_bf16_rne(b.w) << 16);
-  *reinterpret_cast<u32x4_t *>(xg + (size_t)p * H + j) = o;
-}
-
-// T <= kMoePrepMaxTokens: wave w routes tokens w, w + 8, ... (or copies the
-// given ids), the selections stay in LDS for the grouping, and the gather
-// reads the row map from LDS: one launch instead of three dependent ones.
+// T <= kMoePrepMaxTokens: wave w routes token w (or copies the given ids),
+// and the selections stay in LDS for the grouping: one launch instead of two
+// dependent ones.
 template <int R>
-__global__ __launch_bounds__(512) void moe_prep_kernel(MoeRouting r, const float *x, int T,
-                                                        int E, int H, int k, int C,
+__global__ __launch_bounds__(512) void moe_prep_kernel(MoeRouting r, int T, int E, int k, int C,
                                                         int max_chunks, int32_t *ids, float *wts,
-                                                        int32_t *pos, SkinnyChunk *chunks,
-                                                        int32_t *counts, uint16_t *xg) {
+                                                        int32_t *pos, int32_t *row_map,
+                                                        SkinnyChunk *chunks, int32_t *counts) {
   constexpr int NMAX = kMoePrepMaxTokens * kMoeMaxTopK;
-  __shared__ int s_ids[NMAX], s_rank[NMAX], s_row[NMAX];
+  __shared__ int s_ids[NMAX], s_rank[NMAX];
   __shared__ float s_w[NMAX];
   __shared__ GroupLds g;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  // touch every 128-byte line of x now, so the gather at the end finds it in
-  // cache (and its pages mapped) instead of waiting on memory after routing
-  float touch = 0.f;
-  for (int i = threadIdx.x; i < T * H / 32; i += blockDim.x) touch += x[(size_t)i * 32];
   for (int t = wave; t < T; t += nw) {
     int id = 0;
     float w = 0.f;
@@ -397,46 +379,22 @@ __global__ __launch_bounds__(512) void moe_prep_kernel(MoeRouting r, const float
     }
   }
   lds_barrier();
-  group_assignments<R>(s_ids, s_w, r.threshold, T, E, k, C, max_chunks, s_rank, g, pos, s_row,
+  group_assignments<R>(s_ids, s_w, r.threshold, T, E, k, C, max_chunks, s_rank, g, pos, row_map,
                        chunks, counts);
-  const int per_row = H / 8;
-  for (int q = threadIdx.x; q < g.total * per_row; q += blockDim.x) {
-    const int p = q / per_row, j = (q - p * per_row) * 8;
-    gather8(x, s_row[p], p, j, H, xg);
-  }
-  if (__builtin_bit_cast(uint32_t, touch) == 0x7FC0DEADu) counts[2] = 0;  // keeps the touch loads
 }
 
-hipError_t moe_prep(const MoeRouting &r, const float *x, int T, int E, int H, int top_k,
-                    int chunk_rows, int max_chunks, int32_t *ids, float *w, int32_t *pos,
-                    SkinnyChunk *chunks, int32_t *counts, uint16_t *xg, hipStream_t st) {
-  CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_prep_kernel<R>, dim3(1), dim3(512), 0, st, r, x, T,
-                                          E, H, top_k, chunk_rows, max_chunks, ids, w, pos,
-                                          chunks, counts, xg));
+hipError_t moe_prep(const MoeRouting &r, int T, int E, int top_k, int chunk_rows, int max_chunks,
+                    int32_t *ids, float *w, int32_t *pos, int32_t *row_map, SkinnyChunk *chunks,
+                    int32_t *counts, hipStream_t st) {
+  CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_prep_kernel<R>, dim3(1), dim3(512), 0, st, r, T, E,
+                                          top_k, chunk_rows, max_chunks, ids, w, pos, row_map,
+                                          chunks, counts));
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// gather (bf16 rows in grouped order) and combine
+// combine
 // ---------------------------------------------------------------------------
-
-__global__ __launch_bounds__(256) void moe_gather_kernel(const float *x, const int32_t *row_map,
-                                                         const int32_t *counts, int H,
-                                                         uint16_t *xg) {
-  const int p = blockIdx.y;
-  if (p >= counts[0]) return;
-  const int j = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
-  if (j >= H) return;
-  gather8(x, row_map[p], p, j, H, xg);
-}
-
-hipError_t moe_gather(const float *x, const int32_t *row_map, const int32_t *counts, int T,
-                      int H, int top_k, uint16_t *xg, hipStream_t st) {
-  const int per_block = 256 * 8;
-  hipLaunchKernelGGL(moe_gather_kernel, dim3((H + per_block - 1) / per_block, T * top_k),
-                     dim3(256), 0, st, x, row_map, counts, H, xg);
-  return hipGetLastError();
-}
 
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float *residual,
                                                           const float *shared,

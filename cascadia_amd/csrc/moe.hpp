@@ -23,12 +23,11 @@ struct MoeRouting {
 
 constexpr int kMoeMaxExperts = 1024;
 constexpr int kMoeMaxTopK = 16;
-constexpr int kMoePrepMaxTokens = 64;  // batches the one-workgroup prep kernel takes
+constexpr int kMoePrepMaxTokens = 8;  // batches the one-workgroup prep kernel takes
 
 // Device workspace regions of one moe_forward call (byte offsets).
 struct MoeWorkspace {
-  size_t ids, weights, pos, row_map, chunks, counts, xg, hi, lo, y, shared, part, shared_ws,
-      total;
+  size_t ids, weights, pos, row_map, chunks, counts, hi, lo, y, shared, part, shared_ws, total;
   int chunk_rows, max_chunks;
 };
 
@@ -43,16 +42,14 @@ int moe_max_chunks(int T, int E, int top_k, int chunk_rows);
 
 hipError_t moe_route(const MoeRouting &r, int T, int E, int32_t *ids, float *w,
                      hipStream_t st);
-// T <= kMoePrepMaxTokens: routing (or the given ids), grouping and gather in
-// one launch; the results as moe_route + moe_group + moe_gather leave them.
-hipError_t moe_prep(const MoeRouting &r, const float *x, int T, int E, int H, int top_k,
-                    int chunk_rows, int max_chunks, int32_t *ids, float *w, int32_t *pos,
-                    SkinnyChunk *chunks, int32_t *counts, uint16_t *xg, hipStream_t st);
+// T <= kMoePrepMaxTokens: routing (or the given ids) and grouping in one
+// launch; the results as moe_route + moe_group leave them.
+hipError_t moe_prep(const MoeRouting &r, int T, int E, int top_k, int chunk_rows, int max_chunks,
+                    int32_t *ids, float *w, int32_t *pos, int32_t *row_map, SkinnyChunk *chunks,
+                    int32_t *counts, hipStream_t st);
 hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T, int E,
                      int top_k, int chunk_rows, int max_chunks, int32_t *pos, int32_t *row_map,
                      SkinnyChunk *chunks, int32_t *counts, hipStream_t st);
-hipError_t moe_gather(const float *x, const int32_t *row_map, const int32_t *counts, int T,
-                      int H, int top_k, uint16_t *xg, hipStream_t st);
 hipError_t moe_combine(const float *residual, const float *shared, const uint16_t *y,
                        const int32_t *pos, const float *w, int T, int H, int top_k, float *out,
                        hipStream_t st);

@@ -42,7 +42,7 @@
 // that is a multiple of 32.  K must be a multiple of 32 and of G.
 //
 // Token slots of a 16-slot MFMA tile:
-//   A_BF16: slot i = token i (exact bf16 products);
+//   A_BF16 / A_GATHER: slot i = token i (exact bf16 products);
 //   A_XF32 / A_HILO: slots 0-7 = hi plane of tokens 0-7, slots 8-15 = lo plane
 //   (hi = f32 truncated to bf16, lo = bf16 of the exact remainder); the two
 //   halves of the MFMA result are added: y = D[hi] + D[lo].
@@ -69,8 +69,9 @@ struct KParams {
   void *out, *out2;
   f32x4_t *part;
   const SkinnyChunk *chunks;
+  const int32_t *row_map;
   size_t wstride;
-  int N, K, G, M, ldx, ldo, sdt, glog2, tiled, amode, epi;
+  int N, K, G, M, ldx, ldo, sdt, glog2, tiled, amode, epi, x_rows;
   int rw, kw, kper;
   int act_rows, act_stride, scale_off;
 };
@@ -137,16 +138,32 @@ template <int B>
 CAI4_DEV void act_issue(const KParams &a, int m0, int mcount, int kr0, int kr1, Pos p, int dt,
                         int dc, u32x4_t (&v)[2][B]) {
   const int cpr = (kr1 - kr0) * 16;
-  const bool xf32 = a.amode == A_XF32, hilo = a.amode == A_HILO;
+  const bool gat = a.amode == A_GATHER;
+  const bool xf32 = a.amode == A_XF32 || gat, hilo = a.amode == A_HILO;
   const uint32_t esz = xf32 ? 4u : 2u;
-  const size_t bytes = (size_t)a.M * a.ldx * esz;
+  const size_t bytes = (size_t)(gat ? a.x_rows : a.M) * a.ldx * esz;
   const rsrc_t r0 = make_rsrc(a.x, bytes);
   const rsrc_t r1 = make_rsrc(hilo ? a.x2 : a.x, bytes);
+  // A_GATHER: the x row of each item's grouped row first (all issued before
+  // the data loads, which depend on them)
+  int row[B];
+  if (gat) {
+    const rsrc_t rm = make_rsrc(a.row_map, (size_t)a.M * 4);
+    Pos q = p;
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const bool ok = q.t < mcount;
+      row[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(rm, ok ? (uint32_t)(m0 + q.t) * 4 : kOOB,
+                                                           0, 0);
+      pos_step(q, dt, dc, cpr);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < B; ++j) {
     const int col = kr0 * 128 + 8 * p.c;
     const bool ok = p.t < mcount && col < a.K;
-    const uint32_t off = ok ? ((uint32_t)(m0 + p.t) * a.ldx + col) * esz : kOOB;
+    const uint32_t r = gat ? (uint32_t)row[j] : (uint32_t)(m0 + p.t);
+    const uint32_t off = ok ? (r * a.ldx + col) * esz : kOOB;
     v[0][j] = __builtin_amdgcn_raw_buffer_load_b128(r0, off, 0, 0);
     // second source: the lo plane, or the upper 4 floats of an f32 chunk
     v[1][j] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -171,6 +188,15 @@ CAI4_DEV void act_store(const KParams &a, uint8_t *lds, int mcount, int kr0, int
           a.tiled ? act_split_f32_nat(lo4, hi4, false) : act_split_f32(lo4, hi4, false);
       *reinterpret_cast<u32x4_t *>(d + plane_bytes) =
           a.tiled ? act_split_f32_nat(lo4, hi4, true) : act_split_f32(lo4, hi4, true);
+    } else if (a.amode == A_GATHER) {
+      // eight f32 -> eight bf16 (RNE) in natural column order
+      const u32x4_t f0 = v[0][j], f1 = v[1][j];
+      u32x4_t b;
+      b.x = f32_to_bf16_rne(bitsf(f0.x)) | (f32_to_bf16_rne(bitsf(f0.y)) << 16);
+      b.y = f32_to_bf16_rne(bitsf(f0.z)) | (f32_to_bf16_rne(bitsf(f0.w)) << 16);
+      b.z = f32_to_bf16_rne(bitsf(f1.x)) | (f32_to_bf16_rne(bitsf(f1.y)) << 16);
+      b.w = f32_to_bf16_rne(bitsf(f1.z)) | (f32_to_bf16_rne(bitsf(f1.w)) << 16);
+      *reinterpret_cast<u32x4_t *>(d) = a.tiled ? b : act_perm_bf16(b);
     } else {
       *reinterpret_cast<u32x4_t *>(d) = a.tiled ? v[0][j] : act_perm_bf16(v[0][j]);
       if (a.amode == A_HILO)
@@ -349,7 +375,7 @@ template <int NT, int MT, bool SW>
 CAI4_DEV void epilogue(const KParams &a, f32x4_t (&acc)[MT][NT], int unit, int m0,
                        int mcount) {
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
-  const bool hilo = a.amode != A_BF16;
+  const bool hilo = !amode_single_plane(a.amode);
   const int tpm = hilo ? 8 : 16;
   constexpr int NOUT = SW ? NT / 2 : NT;
   if (hilo) {
@@ -398,7 +424,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rwi = wave % a.rw, kwi = wave / a.rw;
-  const bool hilo = a.amode != A_BF16;
+  const bool hilo = !amode_single_plane(a.amode);
   const int tpm = hilo ? 8 : 16;
   const int unit0 = blockIdx.x * a.rw, unit = unit0 + rwi;
   int m0 = blockIdx.y * tpm * MT;
@@ -550,7 +576,7 @@ __global__ __launch_bounds__(1024) void splitk_reduce_kernel(KParams a, int kspl
   constexpr int NI = MT * NT;
   const int lane = threadIdx.x & 63;
   const int rwi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tpm = a.amode != A_BF16 ? 8 : 16;
+  const int tpm = amode_single_plane(a.amode) ? 16 : 8;
   int m0 = blockIdx.y * tpm * MT;
   int mcount = min(a.M - m0, tpm * MT);
   if (a.chunks) {
@@ -602,8 +628,8 @@ namespace {
 SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, int epi,
                      const SkinnyDevice &d) {
   SkinnyPlan p{};
-  const int tpm = amode == A_BF16 ? 16 : 8;
-  const int planes = amode == A_BF16 ? 1 : 2;
+  const int tpm = amode_single_plane(amode) ? 16 : 8;
+  const int planes = amode_single_plane(amode) ? 1 : 2;
   int mt = (m_rows + tpm - 1) / tpm;
   if (mt > 4) mt = 4;
   if (mt == 3) mt = 4;
@@ -740,6 +766,8 @@ hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, in
   k.out2 = a.out2;
   k.part = static_cast<f32x4_t *>(a.partials);
   k.chunks = a.chunks;
+  k.row_map = a.row_map;
+  k.x_rows = a.x_rows;
   k.wstride = a.expert_stride;
   k.N = a.N;
   k.K = a.K;

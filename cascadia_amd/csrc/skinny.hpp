@@ -11,8 +11,15 @@ namespace cai4 {
 enum Epilogue { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_BF16 = 2, EPI_SWIGLU_HILO = 3 };
 
 // Activation modes: bf16; f32 (split into hi/lo bf16 planes while staged);
-// precomputed hi/lo bf16 planes (x = hi plane, x2 = lo plane).
-enum AMode { A_BF16 = 0, A_XF32 = 1, A_HILO = 2 };
+// precomputed hi/lo bf16 planes (x = hi plane, x2 = lo plane); f32 rows
+// gathered through a row map (grouped row r is x row row_map[r]) and rounded
+// to bf16 (RNE) while staged -- one bf16 plane, like A_BF16.
+enum AMode { A_BF16 = 0, A_XF32 = 1, A_HILO = 2, A_GATHER = 3 };
+
+// Modes whose staged activations are one bf16 plane (16 token slots per MFMA tile).
+__host__ __device__ inline bool amode_single_plane(int amode) {
+  return amode == A_BF16 || amode == A_GATHER;
+}
 
 // Grouped mode: one row chunk of one expert per workgroup row (blockIdx.y).
 // Weights/scales of expert e are at w0/w1/s0/s1 + e * expert_stride; a chunk
@@ -32,6 +39,8 @@ struct SkinnyArgs {
   void *out2;         // EPI_SWIGLU_HILO: the lo plane
   void *partials;     // split-K partial sums (SkinnyPlan::partial_bytes), or null
   const SkinnyChunk *chunks;  // grouped mode: [max_chunks] (device), else null
+  const int32_t *row_map;     // A_GATHER: x row of each grouped row [M] (device)
+  int x_rows;                 // A_GATHER: rows of x (the descriptor range)
   size_t expert_stride;       // grouped mode: bytes between experts' weights
   int N, K, G, M, ldx, ldo, sdt;
   int glog2;  // log2(G) when G is a power of two, else -1
