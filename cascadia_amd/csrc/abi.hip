@@ -23,9 +23,12 @@ struct DeviceState {
   size_t max_lds = 0;
   void *ws = nullptr;  // library-owned workspace (grow-only)
   size_t ws_bytes = 0;
+  hipStream_t side = nullptr;  // second stream for independent work (default priority)
+  hipEvent_t fork = nullptr, join = nullptr;
 };
 
 std::mutex g_mu;
+std::mutex g_side_mu;  // held from a fork onto the side stream to the join
 DeviceState g_dev[kMaxDevices];
 
 int current_device(int *dev) {
@@ -51,6 +54,32 @@ cai4::SkinnyDevice device_props(int dev) {
     d.max_lds = (size_t)l;
   }
   return cai4::SkinnyDevice{d.num_cus, d.max_lds};
+}
+
+// The side stream of a device and the events that fork work onto it and
+// join it back (created once; non-blocking, default priority, no timing).
+int side_stream(int dev, hipStream_t *side, hipEvent_t *fork, hipEvent_t *join) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState &d = g_dev[dev];
+  if (!d.side) {
+    hipStream_t s = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess)
+      return CASCADIA_INT4_ERR_DEVICE;
+    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+      if (f) (void)hipEventDestroy(f);
+      (void)hipStreamDestroy(s);
+      return CASCADIA_INT4_ERR_DEVICE;
+    }
+    d.side = s;
+    d.fork = f;
+    d.join = j;
+  }
+  *side = d.side;
+  *fork = d.fork;
+  *join = d.join;
+  return CASCADIA_INT4_OK;
 }
 
 // Library workspace of at least `bytes` on the current device.
@@ -363,6 +392,43 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   uint16_t *lo = reinterpret_cast<uint16_t *>(W + m.ws.lo);
   uint16_t *y = reinterpret_cast<uint16_t *>(W + m.ws.y);
   void *part = W + m.ws.part;  // used only when a grouped GEMM splits K
+  // The shared expert depends only on x: it runs on the side stream, forked
+  // here and joined before the combine, so it fills the routed path's gaps.
+  // The guard enqueues the join on every return path once the fork is made.
+  struct Join {
+    hipStream_t st = nullptr;
+    hipEvent_t ev = nullptr;
+    std::unique_lock<std::mutex> lk;
+    hipError_t wait() {
+      hipError_t e = hipSuccess;
+      if (ev) e = hipStreamWaitEvent(st, ev, 0);
+      ev = nullptr;
+      if (lk.owns_lock()) lk.unlock();
+      return e;
+    }
+    ~Join() { (void)wait(); }
+  } join_guard;
+  float *sh = nullptr;
+  if (has_shared(L)) {
+    sh = reinterpret_cast<float *>(W + m.ws.shared);
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    if (side_stream(dev, &side, &fork, &join) == CASCADIA_INT4_OK) {
+      join_guard.lk = std::unique_lock<std::mutex>(g_side_mu);
+      if (hipEventRecord(fork, st) != hipSuccess ||
+          hipStreamWaitEvent(side, fork, 0) != hipSuccess)
+        return CASCADIA_INT4_ERR_DEVICE;
+      const int rc = ffn_common(L->hidden, L->shared_inter, L->group_size, L->scale_dtype,
+                                &L->shared, x, true, T, sh, false, W + m.ws.shared_ws, side);
+      if (hipEventRecord(join, side) != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+      join_guard.st = st;
+      join_guard.ev = join;
+      if (rc) return rc;
+    } else if (int rc = ffn_common(L->hidden, L->shared_inter, L->group_size, L->scale_dtype,
+                                   &L->shared, x, true, T, sh, false, W + m.ws.shared_ws, st)) {
+      return rc;  // no side stream (e.g. first call inside a stream capture): in order on st
+    }
+  }
   hipError_t e = hipSuccess;
   if (T <= (uint32_t)cai4::kMoePrepMaxTokens) {
     // small decode batches: routing and grouping in one launch
@@ -429,13 +495,7 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     e = cai4::skinny_launch(a, m.dn, cai4::A_HILO, cai4::EPI_BF16, st);
   }
   if (e != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
-  float *sh = nullptr;
-  if (has_shared(L)) {
-    sh = reinterpret_cast<float *>(W + m.ws.shared);
-    if (int rc = ffn_common(L->hidden, L->shared_inter, L->group_size, L->scale_dtype, &L->shared,
-                            x, true, T, sh, false, W + m.ws.shared_ws, st))
-      return rc;
-  }
+  if (join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
   return hip_status(cai4::moe_combine(residual, sh, y, pos, wts, (int)T, H, k, out, st));
 }
 
