@@ -10,6 +10,7 @@
 #include "int4_common.hpp"
 #include "layout.hpp"
 #include "moe.hpp"
+#include "gemv.hpp"
 #include "prefill.hpp"
 #include "skinny.hpp"
 #include "synth.hpp"
@@ -139,7 +140,27 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   int dev;
   if (int rc = current_device(&dev)) return rc;
   if (!act_fits(M, K, amode)) return CASCADIA_INT4_ERR_ARG;
-  const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, G, M, amode, epi, device_props(dev));
+  const cai4::SkinnyDevice d = device_props(dev);
+  {  // one token over tiled weights: the streaming GEMV kernel
+    cai4::SkinnyArgs g{};
+    g.w0 = w0;
+    g.s0 = s0;
+    g.w1 = w1;
+    g.s1 = s1;
+    g.x = x;
+    g.x2 = x2;
+    g.out = out;
+    g.out2 = out2;
+    g.N = N;
+    g.K = K;
+    g.G = G;
+    g.M = M;
+    g.sdt = sdt;
+    g.tiled = tiled;
+    if (cai4::gemv_supported(g, amode, epi, d.num_cus))
+      return hip_status(cai4::gemv_launch(g, amode, epi, d.num_cus, st));
+  }
+  const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, G, M, amode, epi, d);
   if (p.partial_bytes && !partials) {
     if (int rc = lib_workspace(dev, p.partial_bytes, &partials)) return rc;
   }

@@ -1,0 +1,329 @@
+// gemv.hip -- INT4 GEMV for one token over MFMA-tiled weights (gfx950): the
+// decode shape of configs 0 and 1 (dequant_gemv_int4, kernel.rs:31-71;
+// expert_forward's gate/up and down, kernel.rs:75-136, at seq = 1).
+//
+// A workgroup owns one 16-row weight tile (or a gate/up tile pair) and its kw
+// waves split K; each wave streams a contiguous run of k-blocks (1 KB per
+// tile each in the tiled layout) and nothing else:
+//   * its slice of the activations (and their per-k-block sums, the
+//     zero-point seeds) goes into the wave's own LDS region once, with no
+//     barrier -- no wave reads another's region;
+//   * the weight fragments and their scales stream through a 4-deep register
+//     ring, the only loads of the k-loop;
+//   * the kw partial sums meet once, through LDS, in wave order.
+// This keeps every wave independent until the end, as a plain streaming read
+// is, which is what the HBM needs at decode size (many short runs in flight).
+//
+// Arithmetic as the skinny kernel's: weights enter the MFMA as bf16 128 + n;
+// each k-block's partial is seeded with -136 * sum(x) over the block (the
+// zero point), the group scale (G a multiple of 128: one per k-block) is
+// applied in f32, acc += s * p.  Activation slots of the 16 x 16 MFMA tile:
+// bf16 x -> every slot holds the token; f32 x or hi/lo planes -> slots 0-7 the
+// hi plane, 8-15 the lo plane, added at the end.
+#include "gemv.hpp"
+#include "int4_common.hpp"
+#include "skinny.hpp"
+
+namespace cai4 {
+
+namespace {
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOBg = 0x80000000u;
+
+CAI4_DEV rsrc_t gv_rsrc(const void *base, size_t bytes) {
+  const int n = bytes > 0x7FFFFFFFu ? 0x7FFFFFFF : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+CAI4_DEV u32x4_t gv_load16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+struct GvParams {
+  const uint8_t *w0, *w1, *s0, *s1;
+  const void *x, *x2;
+  void *out, *out2;
+  int N, K, G, sdt, epi, kw, kpw;
+};
+
+constexpr int kGvRing = 4;
+constexpr int kGvMaxKpw = 16;
+
+// Sum over a 16-lane DPP row (every lane of the row gets it).
+template <int CTRL>
+CAI4_DEV float gv_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+CAI4_DEV float gv_row_sum(float t) {
+  t += gv_dpp<0xB1>(t);   // quad_perm 1,0,3,2
+  t += gv_dpp<0x4E>(t);   // quad_perm 2,3,0,1
+  t += gv_dpp<0x124>(t);  // row_ror 4
+  t += gv_dpp<0x128>(t);  // row_ror 8
+  return t;
+}
+
+CAI4_DEV float bf16_lo(uint32_t w) { return bitsf(w << 16); }
+CAI4_DEV float bf16_hi(uint32_t w) { return bitsf(w & 0xFFFF0000u); }
+CAI4_DEV float sum8_bf16(u32x4_t v) {
+  return ((bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y))) +
+         ((bf16_lo(v.z) + bf16_hi(v.z)) + (bf16_lo(v.w) + bf16_hi(v.w)));
+}
+
+// NT: weight tiles per wave (2 = a gate/up pair, SW epilogue); AM: activation
+// mode (A_BF16, A_XF32, A_HILO).
+template <int NT, int AM>
+__global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr bool two = AM != A_BF16;  // hi/lo planes
+  constexpr int PL = two ? 2 : 1;
+  const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int KB = a.K >> 7, NG = a.K / a.G;  // G a multiple of 128: one scale per k-block
+  const int T = blockIdx.x;          // tile (pair) index
+  const int kb0 = min(wave * a.kpw, KB), kb1 = min(kb0 + a.kpw, KB), nkb = kb1 - kb0;
+  const int rbytes = a.kpw * 256;                // one plane of a wave's slice
+  const int wbytes = PL * rbytes + NT * a.kpw * 32;  // + scales [NT][kpw][16] u16
+  uint8_t *reg = lds + (size_t)wave * wbytes;       // this wave's region
+
+  // ---- activation slice [kb0, kb1) -> registers (issued first) ----
+  // chunk c = 8 columns; lane holds chunks lane + 64 i, i < kpw / 4
+  const int nch = nkb * 16;
+  u32x4_t xa[kGvMaxKpw / 4], xb[kGvMaxKpw / 4];
+  {
+    const size_t xbytes = (size_t)a.K * (AM == A_XF32 ? 4 : 2);
+    const rsrc_t r0 = gv_rsrc(a.x, xbytes);
+    const rsrc_t r1 = gv_rsrc(AM == A_HILO ? a.x2 : a.x, xbytes);
+#pragma unroll
+    for (int i = 0; i < kGvMaxKpw / 4; ++i) {
+      const int c = lane + 64 * i;
+      const bool ok = i * 64 < nch && c < nch;
+      const uint32_t col = (uint32_t)(kb0 * 128 + 8 * c);
+      if (AM == A_XF32) {
+        xa[i] = gv_load16(r0, ok ? col * 4 : kOOBg);
+        xb[i] = gv_load16(r0, ok ? col * 4 + 16 : kOOBg);
+      } else {
+        xa[i] = gv_load16(r0, ok ? col * 2 : kOOBg);
+        if (AM == A_HILO) xb[i] = gv_load16(r1, ok ? col * 2 : kOOBg);
+      }
+    }
+  }
+
+  // ---- scales of the slice: 4-byte pieces, 8 per k-block and tile ----
+  constexpr int kSv = NT * kGvMaxKpw * 8 / 64;  // pieces per lane at most
+  uint32_t sv[kSv];
+  const int nsv = NT * a.kpw * 8;
+  {
+    const rsrc_t sr0 = gv_rsrc(a.s0 + (size_t)T * NG * 32, (size_t)NG * 32);
+    const rsrc_t sr1 = gv_rsrc(NT == 2 ? a.s1 + (size_t)T * NG * 32 : a.s0, (size_t)NG * 32);
+    const int per = a.kpw * 8;  // pieces per tile
+#pragma unroll
+    for (int i = 0; i < kSv; ++i) {
+      const int e = lane + 64 * i, nt = e / per, q = e - nt * per, j = q >> 3;
+      const bool ok = e < nsv && j < nkb;
+      const uint32_t off =
+          ok ? (uint32_t)((((kb0 + j) * 128) / a.G) * 32 + 4 * (q & 7)) : kOOBg;
+      sv[i] = __builtin_amdgcn_raw_buffer_load_b32(nt == 0 ? sr0 : sr1, off, 0, 0);
+    }
+  }
+
+  // ---- weight ring ----
+  const rsrc_t wr0 = gv_rsrc(a.w0 + (size_t)T * KB * 1024, (size_t)KB * 1024);
+  const rsrc_t wr1 = gv_rsrc(NT == 2 ? a.w1 + (size_t)T * KB * 1024 : a.w0, (size_t)KB * 1024);
+  u32x4_t ring[kGvRing][NT];
+  auto issue = [&](int u, int kb) {  // kb past the slice: dead loads (no data moves)
+    const uint32_t wo = kb < kb1 ? (uint32_t)kb * 1024 + 16 * lane : kOOBg;
+    ring[u][0] = gv_load16(wr0, wo);
+    if (NT == 2) ring[u][NT - 1] = gv_load16(wr1, wo);
+  };
+#pragma unroll
+  for (int u = 0; u < kGvRing; ++u) issue(u, kb0 + u);
+
+  // ---- activation slice -> this wave's LDS region, seeds ----
+  float seed_hi[kGvMaxKpw / 4], seed_lo[kGvMaxKpw / 4];
+#pragma unroll
+  for (int i = 0; i < kGvMaxKpw / 4; ++i) {
+    const int c = lane + 64 * i;
+    u32x4_t hi = xa[i], lo = u32x4_t{0u, 0u, 0u, 0u};
+    if (AM == A_XF32) {
+      const f32x4_t fa = __builtin_bit_cast(f32x4_t, xa[i]);
+      const f32x4_t fb = __builtin_bit_cast(f32x4_t, xb[i]);
+      hi = act_split_f32_nat(fa, fb, false);
+      lo = act_split_f32_nat(fa, fb, true);
+    } else if (AM == A_HILO) {
+      lo = xb[i];
+    }
+    if (i * 64 < nch && c < nch) {
+      *reinterpret_cast<u32x4_t *>(reg + 16 * c) = hi;
+      if (two) *reinterpret_cast<u32x4_t *>(reg + rbytes + 16 * c) = lo;
+    }
+    // k-block of chunk c = (c / 16): the 16 lanes of a DPP row
+    seed_hi[i] = -136.f * gv_row_sum(sum8_bf16(hi));
+    seed_lo[i] = two ? -136.f * gv_row_sum(sum8_bf16(lo)) : 0.f;
+  }
+  uint16_t *sreg = reinterpret_cast<uint16_t *>(reg + PL * rbytes);
+#pragma unroll
+  for (int i = 0; i < kSv; ++i)
+    if (lane + 64 * i < nsv) reinterpret_cast<uint32_t *>(sreg)[lane + 64 * i] = sv[i];
+  // own region only: no barrier, just this wave's LDS writes
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+  // ---- k-loop: only the ring's loads ----
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint8_t *arow = reg + 64 * lg + (two && lr >= 8 ? rbytes : 0);
+  const bool lo_slot = two && lg >= 2;  // D rows 8-15: the lo plane
+  for (int k0 = 0; k0 < nkb; k0 += kGvRing) {
+#pragma unroll
+    for (int u = 0; u < kGvRing; ++u) {
+      const int j = k0 + u;  // k-block within the slice
+      if (j < nkb) {
+        u32x4_t af[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          af[s] = *reinterpret_cast<const u32x4_t *>(arow + j * 256 + 16 * s);
+        // seed of k-block j: row j % 4 of register j / 4 (uniform selection)
+        float sh = 0.f, sl = 0.f;
+#pragma unroll
+        for (int i = 0; i < kGvMaxKpw / 4; ++i)
+          if (i == (j >> 2)) {
+            sh = bitsf(__builtin_amdgcn_readlane(fbits(seed_hi[i]), 16 * (j & 3)));
+            if (two) sl = bitsf(__builtin_amdgcn_readlane(fbits(seed_lo[i]), 16 * (j & 3)));
+          }
+        const float sd = lo_slot ? sl : sh;
+        // take the slot's data, then refill it before the arithmetic: the next
+        // load is in flight while this k-block is decoded
+        u32x4_t bc[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) bc[nt] = ring[u][nt];
+        issue(u, kb0 + j + kGvRing);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const float sc = scale_bits_f32(sreg[(nt * a.kpw + j) * 16 + lr], a.sdt);
+          const u32x4_t b = bc[nt];
+          f32x4_t p = mfma_bf16(af[0], decode8(b.x), f32x4_t{sd, sd, sd, sd});
+          p = mfma_bf16(af[1], decode8(b.y), p);
+          p = mfma_bf16(af[2], decode8(b.z), p);
+          p = mfma_bf16(af[3], decode8(b.w), p);
+          // only D row 0 (and row 8, the lo plane) is the token
+          acc[nt][0] += sc * p[0];
+        }
+      }
+    }
+  }
+
+  // ---- the kw partials, added in wave order ----
+  f32x4_t *red = reinterpret_cast<f32x4_t *>(lds + (size_t)a.kw * wbytes);
+  if (wave > 0) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) red[((wave - 1) * NT + nt) * 64 + lane] = acc[nt];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  for (int w = 1; w < a.kw; ++w) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] += red[((w - 1) * NT + nt) * 64 + lane];
+  }
+  if (two) {  // slot 0 (hi) + slot 8 (lo): lanes 0-31 receive lanes 32-63
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      auto sw = __builtin_amdgcn_permlane32_swap(fbits(acc[nt][0]), fbits(acc[nt][0]), false,
+                                                 false);
+      acc[nt][0] += bitsf(sw[1]);
+    }
+  }
+  if (lg != 0) return;  // D row 0 = the token: lanes 0-15, component 0
+  const int row = 16 * T + lr;
+  if (row >= a.N) return;
+  const float y = acc[0][0];
+  if (NT == 2) {
+    const float h = silu_f32(y) * acc[NT - 1][0];
+    if (a.epi == EPI_SWIGLU) {
+      reinterpret_cast<float *>(a.out)[row] = h;
+    } else {  // hi = h truncated to bf16, lo = bf16(h - hi): the A_HILO planes
+      const uint32_t hb = fbits(h) >> 16;
+      reinterpret_cast<uint16_t *>(a.out)[row] = (uint16_t)hb;
+      reinterpret_cast<uint16_t *>(a.out2)[row] = (uint16_t)f32_to_bf16_rne(h - bitsf(hb << 16));
+    }
+  } else if (a.epi == EPI_BF16) {
+    reinterpret_cast<uint16_t *>(a.out)[row] = (uint16_t)f32_to_bf16_rne(y);
+  } else {
+    reinterpret_cast<float *>(a.out)[row] = y;
+  }
+}
+
+}  // namespace
+
+size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt);
+constexpr size_t kGvMaxLds = 160 * 1024;  // gfx950: LDS of one CU
+
+bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus) {
+  if (a.M != 1 || !a.tiled || a.chunks || a.G % 128 || a.K % a.G) return false;
+  if (amode != A_BF16 && amode != A_XF32 && amode != A_HILO) return false;
+  const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
+  if (sw ? !(a.w1 && a.s1) : !(epi == EPI_F32 || epi == EPI_BF16)) return false;
+  const int nt = sw ? 2 : 1;
+  const GemvPlan p = gemv_plan(a.N, a.K, nt, num_cus);  // K > 256 KB blocks: kw > 16
+  return p.kw <= 16 && gemv_lds_bytes(p, amode, nt) <= kGvMaxLds;
+}
+
+GemvPlan gemv_plan(int N, int K, int nt, int num_cus) {
+  const int tiles = (N + 15) / 16, KB = K / 128;
+  // About 64 KB of weight loads in flight per CU: 16 / nt waves of kGvRing x nt
+  // KB each (measured best on the config-1 shapes: fewer waves starve the HBM,
+  // more only queue behind each other).
+  const long waves = (16L / nt) * num_cus;
+  int kw = (int)((2 * waves + tiles) / (2L * tiles));  // nearest
+  if (kw > 16) kw = 16;
+  if (kw < 1) kw = 1;
+  if (kw > KB) kw = KB;
+  int kpw = (KB + kw - 1) / kw;
+  while (kpw > kGvMaxKpw) {
+    ++kw;
+    kpw = (KB + kw - 1) / kw;
+  }
+  kw = (KB + kpw - 1) / kpw;  // no wave without work
+  return GemvPlan{kw, kpw};
+}
+
+size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt) {
+  const int planes = amode == A_BF16 ? 1 : 2;
+  return (size_t)p.kw * (planes * p.kpw * 256 + nt * p.kpw * 32) +
+         (size_t)(p.kw - 1) * nt * 1024 + 16;
+}
+
+hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, hipStream_t st) {
+  const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
+  const GemvPlan p = gemv_plan(a.N, a.K, sw ? 2 : 1, num_cus);
+  GvParams k{};
+  k.w0 = a.w0;
+  k.w1 = a.w1;
+  k.s0 = a.s0;
+  k.s1 = a.s1;
+  k.x = a.x;
+  k.x2 = a.x2;
+  k.out = a.out;
+  k.out2 = a.out2;
+  k.N = a.N;
+  k.K = a.K;
+  k.G = a.G;
+  k.sdt = a.sdt;
+  k.epi = epi;
+  k.kw = p.kw;
+  k.kpw = p.kpw;
+  const size_t lds = gemv_lds_bytes(p, amode, sw ? 2 : 1);
+  const dim3 grid((a.N + 15) / 16), block(64 * p.kw);
+  if (sw) {
+    if (amode == A_BF16) hipLaunchKernelGGL((gemv_kernel<2, A_BF16>), grid, block, lds, st, k);
+    else if (amode == A_XF32) hipLaunchKernelGGL((gemv_kernel<2, A_XF32>), grid, block, lds, st, k);
+    else hipLaunchKernelGGL((gemv_kernel<2, A_HILO>), grid, block, lds, st, k);
+  } else {
+    if (amode == A_BF16) hipLaunchKernelGGL((gemv_kernel<1, A_BF16>), grid, block, lds, st, k);
+    else if (amode == A_XF32) hipLaunchKernelGGL((gemv_kernel<1, A_XF32>), grid, block, lds, st, k);
+    else hipLaunchKernelGGL((gemv_kernel<1, A_HILO>), grid, block, lds, st, k);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace cai4

@@ -129,4 +129,29 @@ CAI4_DEV u32x4_t xpose_rows(u32x4_t v) {
 
 CAI4_DEV float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
+// 8 consecutive f32 -> hi / lo bf16 in natural column order.
+CAI4_DEV u32x4_t act_split_f32_nat(const f32x4_t &a, const f32x4_t &b, bool lo) {
+  const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t w[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float x0 = xs[2 * p], x1 = xs[2 * p + 1];
+    if (!lo) {
+      w[p] = __builtin_amdgcn_perm(fbits(x1), fbits(x0), 0x07060302u);
+    } else {
+      const float r0 = x0 - bitsf(fbits(x0) & 0xFFFF0000u);
+      const float r1 = x1 - bitsf(fbits(x1) & 0xFFFF0000u);
+      f32x2_t v = {r0, r1};
+      w[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+    }
+  }
+  return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
+// Scale bits (u16 in the low half) -> f32: fp16 if sdt, else bf16.
+CAI4_DEV float scale_bits_f32(uint32_t bits, int sdt) {
+  return sdt ? scale_to_f32<SCALE_F16>(bits & 0xFFFFu) : scale_to_f32<SCALE_BF16>(bits & 0xFFFFu);
+}
+
+
 }  // namespace cai4

@@ -87,24 +87,6 @@ constexpr int skinny_ring_depth(int nt) { return nt == 1 ? 4 : 2; }
 // staging into LDS
 // ---------------------------------------------------------------------------
 
-// 8 consecutive f32 -> hi / lo bf16 in natural column order.
-CAI4_DEV u32x4_t act_split_f32_nat(const f32x4_t &a, const f32x4_t &b, bool lo) {
-  const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint32_t w[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const float x0 = xs[2 * p], x1 = xs[2 * p + 1];
-    if (!lo) {
-      w[p] = __builtin_amdgcn_perm(fbits(x1), fbits(x0), 0x07060302u);
-    } else {
-      const float r0 = x0 - bitsf(fbits(x0) & 0xFFFF0000u);
-      const float r1 = x1 - bitsf(fbits(x1) & 0xFFFF0000u);
-      f32x2_t v = {r0, r1};
-      w[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-    }
-  }
-  return u32x4_t{w[0], w[1], w[2], w[3]};
-}
 
 // Activations of tokens [m0, m0 + mcount) and k-blocks [kr0, kr1) go to LDS as
 // bf16 planes [plane][row][column], row pitch act_stride bytes, columns in the
@@ -248,9 +230,6 @@ CAI4_DEV void sc_issue(const KParams &a, int unit0, int g_lo, int ngw, Pos p0, i
   }
 }
 
-CAI4_DEV float scale_bits_f32(uint32_t bits, int sdt) {
-  return sdt ? scale_to_f32<SCALE_F16>(bits & 0xFFFFu) : scale_to_f32<SCALE_BF16>(bits & 0xFFFFu);
-}
 
 template <int NT, int B>
 CAI4_DEV void sc_store(const KParams &a, uint16_t *dst, int ngw, Pos p0, int dt, int dc,

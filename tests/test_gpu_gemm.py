@@ -257,6 +257,60 @@ def test_expert_forward_config1_llama_ffn(cl, orc, M):
     assert_bf16_close(got, want, f"config1 M={M}")
 
 
+GEMV_SHAPES = [  # n, k, group, sdt: one token, tiled weights (the one-token GEMV kernel)
+    (16, 128, 128, F16), (40, 384, 128, BF16), (130, 1024, 256, F16), (33, 2304, 128, F16),
+    (4096, 4096, 128, F16), (300, 14336, 128, F16), (64, 32768, 128, BF16),
+]
+
+
+@pytest.mark.parametrize("n,k,group,sdt", GEMV_SHAPES)
+def test_gemv_tiled_one_token(cl, orc, n, k, group, sdt):
+    """One token over MFMA-tiled weights, G a multiple of 128: f32 and bf16
+    activations, f32 and bf16 outputs, ragged rows and k-slices, 1 to 16
+    waves per tile."""
+    packed, scales = weights(orc, n, k, group, sdt, 5 * n + k)
+    pt, st = cl.tile_weights(dev(packed), dev(scales), n, k, group)
+    xs = orc.fill_normal_f32(n, 18, k)
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    cl.dequant_gemm_int4_multi_auto(pt, st, dev(xs), n, k, 1, y, group_size=group, scale_dtype=sdt,
+                                    tiling=cl.TILING_MFMA)
+    want = orc.gemm_multi(packed, scales, xs, n, k, 1, group, sdt)
+    assert_f32_close(host(y), want.reshape(-1), f"gemv f32 in {n}x{k} G{group}")
+    xb = orc.f32_to_bf16(xs)
+    want_b = orc.gemm_multi(packed, scales, orc.bf16_to_f32(xb), n, k, 1, group, sdt)
+    cl.dequant_gemm_int4_multi_auto(pt, st, dev(xb.view(np.int16)), n, k, 1, y, group_size=group,
+                                    scale_dtype=sdt, tiling=cl.TILING_MFMA)
+    assert_f32_close(host(y), want_b.reshape(-1), f"gemv bf16 in {n}x{k} G{group}")
+    yb = torch.empty(n, dtype=torch.int16, device="cuda")
+    cl.gemm_int4_bf16(pt, st, dev(xb.view(np.int16)), n, k, 1, yb, group_size=group,
+                      scale_dtype=sdt, tiling=cl.TILING_MFMA)
+    assert_bf16_close(host(yb).view(np.uint16), orc.f32_to_bf16(want_b.reshape(-1)),
+                      f"gemv bf16 out {n}x{k} G{group}")
+
+
+@pytest.mark.parametrize("h,i,g", [(1024, 768, 128), (4096, 14336, 128), (512, 2560, 256)])
+def test_gemv_tiled_expert_one_token(cl, orc, h, i, g):
+    """One token through tiled expert weights: fused gate/up (SwiGLU, hi/lo
+    planes or f32) and down, bf16 and f32 forms."""
+    flat = orc.fill_bytes(h, 60, orc.expert_bytes(h, i, g))
+    offs, sizes = orc.expert_offsets(h, i, g)
+    for s_ in (1, 3, 5):
+        flat[offs[s_]:offs[s_] + sizes[s_]] = orc.fill_scales(h, 61 + s_, sizes[s_] // 2, F16).view(np.uint8)
+    Wt = cl.ExpertWeights(dev(flat), h, i, g, F16).tiled()
+    xb = orc.fill_normal_bf16(i, 62, h)
+    out = torch.empty(h, dtype=torch.int16, device="cuda")
+    cl.expert_forward(dev(xb.view(np.int16).reshape(1, h)), *Wt.slices(), out, group_size=g,
+                      scale_dtype=F16, tiling=cl.TILING_MFMA)
+    want = orc.cpu_expert_forward(xb, 1, flat, h, i, g, F16)
+    assert_bf16_close(host(out).view(np.uint16).reshape(1, h), want, f"tiled expert {h}x{i}")
+    xf = orc.bf16_to_f32(xb)
+    o32 = torch.empty(h, dtype=torch.float32, device="cuda")
+    cl.ffn_forward_sparse_f32(dev(xf), h, i, *Wt.slices(), o32, 0.0, group_size=g, scale_dtype=F16,
+                              tiling=cl.TILING_MFMA)
+    want32 = orc.ffn_forward_f32(xf, flat, h, i, g, F16)[0]
+    assert_f32_close(host(o32), want32, f"tiled expert f32 {h}x{i}")
+
+
 def test_prefill_gemm_bf16_small(cl, orc):
     n, k, m, g = 192, 1024, 100, 128
     packed, scales = weights(orc, n, k, g, F16, 31)
