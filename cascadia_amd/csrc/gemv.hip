@@ -28,17 +28,6 @@ namespace cai4 {
 
 namespace {
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr uint32_t kOOBg = 0x80000000u;
-
-CAI4_DEV rsrc_t gv_rsrc(const void *base, size_t bytes) {
-  const int n = bytes > 0x7FFFFFFFu ? 0x7FFFFFFF : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
-}
-CAI4_DEV u32x4_t gv_load16(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-
 struct GvParams {
   const uint8_t *w0, *w1, *s0, *s1;
   const void *x, *x2;
@@ -48,27 +37,6 @@ struct GvParams {
 
 constexpr int kGvRing = 4;
 constexpr int kGvMaxKpw = 16;
-
-// Sum over a 16-lane DPP row (every lane of the row gets it).
-template <int CTRL>
-CAI4_DEV float gv_dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
-                                                               0xF, 0xF, false));
-}
-CAI4_DEV float gv_row_sum(float t) {
-  t += gv_dpp<0xB1>(t);   // quad_perm 1,0,3,2
-  t += gv_dpp<0x4E>(t);   // quad_perm 2,3,0,1
-  t += gv_dpp<0x124>(t);  // row_ror 4
-  t += gv_dpp<0x128>(t);  // row_ror 8
-  return t;
-}
-
-CAI4_DEV float bf16_lo(uint32_t w) { return bitsf(w << 16); }
-CAI4_DEV float bf16_hi(uint32_t w) { return bitsf(w & 0xFFFF0000u); }
-CAI4_DEV float sum8_bf16(u32x4_t v) {
-  return ((bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y))) +
-         ((bf16_lo(v.z) + bf16_hi(v.z)) + (bf16_lo(v.w) + bf16_hi(v.w)));
-}
 
 // NT: weight tiles per wave (2 = a gate/up pair, SW epilogue); AM: activation
 // mode (A_BF16, A_XF32, A_HILO).
@@ -92,19 +60,19 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
   u32x4_t xa[kGvMaxKpw / 4], xb[kGvMaxKpw / 4];
   {
     const size_t xbytes = (size_t)a.K * (AM == A_XF32 ? 4 : 2);
-    const rsrc_t r0 = gv_rsrc(a.x, xbytes);
-    const rsrc_t r1 = gv_rsrc(AM == A_HILO ? a.x2 : a.x, xbytes);
+    const buf_rsrc_t r0 = buf_rsrc(a.x, xbytes);
+    const buf_rsrc_t r1 = buf_rsrc(AM == A_HILO ? a.x2 : a.x, xbytes);
 #pragma unroll
     for (int i = 0; i < kGvMaxKpw / 4; ++i) {
       const int c = lane + 64 * i;
       const bool ok = i * 64 < nch && c < nch;
       const uint32_t col = (uint32_t)(kb0 * 128 + 8 * c);
       if (AM == A_XF32) {
-        xa[i] = gv_load16(r0, ok ? col * 4 : kOOBg);
-        xb[i] = gv_load16(r0, ok ? col * 4 + 16 : kOOBg);
+        xa[i] = buf_load16(r0, ok ? col * 4 : kBufOOB);
+        xb[i] = buf_load16(r0, ok ? col * 4 + 16 : kBufOOB);
       } else {
-        xa[i] = gv_load16(r0, ok ? col * 2 : kOOBg);
-        if (AM == A_HILO) xb[i] = gv_load16(r1, ok ? col * 2 : kOOBg);
+        xa[i] = buf_load16(r0, ok ? col * 2 : kBufOOB);
+        if (AM == A_HILO) xb[i] = buf_load16(r1, ok ? col * 2 : kBufOOB);
       }
     }
   }
@@ -114,27 +82,27 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
   uint32_t sv[kSv];
   const int nsv = NT * a.kpw * 8;
   {
-    const rsrc_t sr0 = gv_rsrc(a.s0 + (size_t)T * NG * 32, (size_t)NG * 32);
-    const rsrc_t sr1 = gv_rsrc(NT == 2 ? a.s1 + (size_t)T * NG * 32 : a.s0, (size_t)NG * 32);
+    const buf_rsrc_t sr0 = buf_rsrc(a.s0 + (size_t)T * NG * 32, (size_t)NG * 32);
+    const buf_rsrc_t sr1 = buf_rsrc(NT == 2 ? a.s1 + (size_t)T * NG * 32 : a.s0, (size_t)NG * 32);
     const int per = a.kpw * 8;  // pieces per tile
 #pragma unroll
     for (int i = 0; i < kSv; ++i) {
       const int e = lane + 64 * i, nt = e / per, q = e - nt * per, j = q >> 3;
       const bool ok = e < nsv && j < nkb;
       const uint32_t off =
-          ok ? (uint32_t)((((kb0 + j) * 128) / a.G) * 32 + 4 * (q & 7)) : kOOBg;
+          ok ? (uint32_t)((((kb0 + j) * 128) / a.G) * 32 + 4 * (q & 7)) : kBufOOB;
       sv[i] = __builtin_amdgcn_raw_buffer_load_b32(nt == 0 ? sr0 : sr1, off, 0, 0);
     }
   }
 
   // ---- weight ring ----
-  const rsrc_t wr0 = gv_rsrc(a.w0 + (size_t)T * KB * 1024, (size_t)KB * 1024);
-  const rsrc_t wr1 = gv_rsrc(NT == 2 ? a.w1 + (size_t)T * KB * 1024 : a.w0, (size_t)KB * 1024);
+  const buf_rsrc_t wr0 = buf_rsrc(a.w0 + (size_t)T * KB * 1024, (size_t)KB * 1024);
+  const buf_rsrc_t wr1 = buf_rsrc(NT == 2 ? a.w1 + (size_t)T * KB * 1024 : a.w0, (size_t)KB * 1024);
   u32x4_t ring[kGvRing][NT];
   auto issue = [&](int u, int kb) {  // kb past the slice: dead loads (no data moves)
-    const uint32_t wo = kb < kb1 ? (uint32_t)kb * 1024 + 16 * lane : kOOBg;
-    ring[u][0] = gv_load16(wr0, wo);
-    if (NT == 2) ring[u][NT - 1] = gv_load16(wr1, wo);
+    const uint32_t wo = kb < kb1 ? (uint32_t)kb * 1024 + 16 * lane : kBufOOB;
+    ring[u][0] = buf_load16(wr0, wo);
+    if (NT == 2) ring[u][NT - 1] = buf_load16(wr1, wo);
   };
 #pragma unroll
   for (int u = 0; u < kGvRing; ++u) issue(u, kb0 + u);
@@ -158,8 +126,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
       if (two) *reinterpret_cast<u32x4_t *>(reg + rbytes + 16 * c) = lo;
     }
     // k-block of chunk c = (c / 16): the 16 lanes of a DPP row
-    seed_hi[i] = -136.f * gv_row_sum(sum8_bf16(hi));
-    seed_lo[i] = two ? -136.f * gv_row_sum(sum8_bf16(lo)) : 0.f;
+    seed_hi[i] = -136.f * row16_sum(sum8_bf16(hi));
+    seed_lo[i] = two ? -136.f * row16_sum(sum8_bf16(lo)) : 0.f;
   }
   uint16_t *sreg = reinterpret_cast<uint16_t *>(reg + PL * rbytes);
 #pragma unroll

@@ -153,5 +153,40 @@ CAI4_DEV float scale_bits_f32(uint32_t bits, int sdt) {
   return sdt ? scale_to_f32<SCALE_F16>(bits & 0xFFFFu) : scale_to_f32<SCALE_BF16>(bits & 0xFFFFu);
 }
 
+// ---- one-token helpers (gemv.hip, chain.hip) ----
+
+typedef __amdgpu_buffer_rsrc_t buf_rsrc_t;
+constexpr uint32_t kBufOOB = 0x80000000u;  // a buffer offset past any range: no data moves
+
+// Raw buffer resource over [base, base + bytes) (clamped to 2^31 - 1 bytes).
+CAI4_DEV buf_rsrc_t buf_rsrc(const void *base, size_t bytes) {
+  const int n = bytes > 0x7FFFFFFFu ? 0x7FFFFFFF : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+CAI4_DEV u32x4_t buf_load16(buf_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+template <int CTRL>
+CAI4_DEV float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+// Sum over a 16-lane DPP row (every lane of the row gets it).
+CAI4_DEV float row16_sum(float t) {
+  t += dpp_f32<0xB1>(t);   // quad_perm 1,0,3,2
+  t += dpp_f32<0x4E>(t);   // quad_perm 2,3,0,1
+  t += dpp_f32<0x124>(t);  // row_ror 4
+  t += dpp_f32<0x128>(t);  // row_ror 8
+  return t;
+}
+
+// Sum of 8 bf16 values (two per dword), exact pairs first.
+CAI4_DEV float sum8_bf16(u32x4_t v) {
+  auto lo = [](uint32_t w) { return bitsf(w << 16); };
+  auto hi = [](uint32_t w) { return bitsf(w & 0xFFFF0000u); };
+  return ((lo(v.x) + hi(v.x)) + (lo(v.y) + hi(v.y))) + ((lo(v.z) + hi(v.z)) + (lo(v.w) + hi(v.w)));
+}
+
 
 }  // namespace cai4

@@ -288,7 +288,8 @@ def test_gemv_tiled_one_token(cl, orc, n, k, group, sdt):
                       f"gemv bf16 out {n}x{k} G{group}")
 
 
-@pytest.mark.parametrize("h,i,g", [(1024, 768, 128), (4096, 14336, 128), (512, 2560, 256)])
+@pytest.mark.parametrize("h,i,g", [(1024, 768, 128), (4096, 14336, 128), (512, 2560, 256),
+                                   (2048, 5632, 128), (3072, 8192, 128)])
 def test_gemv_tiled_expert_one_token(cl, orc, h, i, g):
     """One token through tiled expert weights: fused gate/up (SwiGLU, hi/lo
     planes or f32) and down, bf16 and f32 forms."""
