@@ -8,11 +8,16 @@
 //   * its slice of the activations (and their per-k-block sums, the
 //     zero-point seeds) goes into the wave's own LDS region once, with no
 //     barrier -- no wave reads another's region;
-//   * the weight fragments and their scales stream through a 4-deep register
-//     ring, the only loads of the k-loop;
+//   * so do the slice's scales (4-byte loads);
+//   * the weight fragments stream through a small register ring, the only
+//     loads of the k-loop, each slot refilled before its data is decoded;
 //   * the kw partial sums meet once, through LDS, in wave order.
 // This keeps every wave independent until the end, as a plain streaming read
-// is, which is what the HBM needs at decode size (many short runs in flight).
+// is.  Measured on MI355X, a plain read of ~60 MB is fastest as many short
+// runs (4-8 KB per wave, ~30 waves per CU): the plan aims at 28 resident waves
+// per CU, and waves of at most 4 k-blocks run in a lean kernel of 64-72 VGPRs
+// (7-8 waves per SIMD) -- with the register arrays sized for 16 k-blocks the
+// same plan would not fit and run in two rounds.
 //
 // Arithmetic as the skinny kernel's: weights enter the MFMA as bf16 128 + n;
 // each k-block's partial is seeded with -136 * sum(x) over the block (the
@@ -35,13 +40,18 @@ struct GvParams {
   int N, K, G, sdt, epi, kw, kpw;
 };
 
-constexpr int kGvRing = 4;
 constexpr int kGvMaxKpw = 16;
+constexpr int kGvRing1 = 4;  // k-blocks in flight per wave: single tiles
+constexpr int kGvRing2 = 4;  // gate/up tile pairs
+constexpr int kGvRingLean2 = 2;  // gate/up tile pairs, lean kernel (64 VGPRs)
+constexpr int kGvWavesPerCu = 28;  // planned waves per CU
 
 // NT: weight tiles per wave (2 = a gate/up pair, SW epilogue); AM: activation
-// mode (A_BF16, A_XF32, A_HILO).
-template <int NT, int AM>
-__global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
+// mode (A_BF16, A_XF32, A_HILO); RING: k-blocks in flight per wave; KPWM: most
+// k-blocks per wave (sizes the per-wave register arrays: fewer registers, more
+// resident waves).
+template <int NT, int AM, int RING, int KPWM>
+CAI4_DEV void gemv_body(const GvParams &a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr bool two = AM != A_BF16;  // hi/lo planes
   constexpr int PL = two ? 2 : 1;
@@ -57,13 +67,13 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
   // ---- activation slice [kb0, kb1) -> registers (issued first) ----
   // chunk c = 8 columns; lane holds chunks lane + 64 i, i < kpw / 4
   const int nch = nkb * 16;
-  u32x4_t xa[kGvMaxKpw / 4], xb[kGvMaxKpw / 4];
+  u32x4_t xa[KPWM / 4], xb[KPWM / 4];
   {
     const size_t xbytes = (size_t)a.K * (AM == A_XF32 ? 4 : 2);
     const buf_rsrc_t r0 = buf_rsrc(a.x, xbytes);
     const buf_rsrc_t r1 = buf_rsrc(AM == A_HILO ? a.x2 : a.x, xbytes);
 #pragma unroll
-    for (int i = 0; i < kGvMaxKpw / 4; ++i) {
+    for (int i = 0; i < KPWM / 4; ++i) {
       const int c = lane + 64 * i;
       const bool ok = i * 64 < nch && c < nch;
       const uint32_t col = (uint32_t)(kb0 * 128 + 8 * c);
@@ -78,7 +88,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
   }
 
   // ---- scales of the slice: 4-byte pieces, 8 per k-block and tile ----
-  constexpr int kSv = NT * kGvMaxKpw * 8 / 64;  // pieces per lane at most
+  constexpr int kSv = (NT * KPWM * 8 + 63) / 64;  // pieces per lane at most
   uint32_t sv[kSv];
   const int nsv = NT * a.kpw * 8;
   {
@@ -98,19 +108,19 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
   // ---- weight ring ----
   const buf_rsrc_t wr0 = buf_rsrc(a.w0 + (size_t)T * KB * 1024, (size_t)KB * 1024);
   const buf_rsrc_t wr1 = buf_rsrc(NT == 2 ? a.w1 + (size_t)T * KB * 1024 : a.w0, (size_t)KB * 1024);
-  u32x4_t ring[kGvRing][NT];
+  u32x4_t ring[RING][NT];
   auto issue = [&](int u, int kb) {  // kb past the slice: dead loads (no data moves)
     const uint32_t wo = kb < kb1 ? (uint32_t)kb * 1024 + 16 * lane : kBufOOB;
     ring[u][0] = buf_load16(wr0, wo);
     if (NT == 2) ring[u][NT - 1] = buf_load16(wr1, wo);
   };
 #pragma unroll
-  for (int u = 0; u < kGvRing; ++u) issue(u, kb0 + u);
+  for (int u = 0; u < RING; ++u) issue(u, kb0 + u);
 
   // ---- activation slice -> this wave's LDS region, seeds ----
-  float seed_hi[kGvMaxKpw / 4], seed_lo[kGvMaxKpw / 4];
+  float seed_hi[KPWM / 4], seed_lo[KPWM / 4];
 #pragma unroll
-  for (int i = 0; i < kGvMaxKpw / 4; ++i) {
+  for (int i = 0; i < KPWM / 4; ++i) {
     const int c = lane + 64 * i;
     u32x4_t hi = xa[i], lo = u32x4_t{0u, 0u, 0u, 0u};
     if (AM == A_XF32) {
@@ -137,14 +147,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   // ---- k-loop: only the ring's loads ----
-  f32x4_t acc[NT];
+  float acc[NT];  // D row 0 (and row 8) only: the token
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = 0.f;
   const uint8_t *arow = reg + 64 * lg + (two && lr >= 8 ? rbytes : 0);
   const bool lo_slot = two && lg >= 2;  // D rows 8-15: the lo plane
-  for (int k0 = 0; k0 < nkb; k0 += kGvRing) {
+  for (int k0 = 0; k0 < nkb; k0 += RING) {
 #pragma unroll
-    for (int u = 0; u < kGvRing; ++u) {
+    for (int u = 0; u < RING; ++u) {
       const int j = k0 + u;  // k-block within the slice
       if (j < nkb) {
         u32x4_t af[4];
@@ -154,7 +164,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
         // seed of k-block j: row j % 4 of register j / 4 (uniform selection)
         float sh = 0.f, sl = 0.f;
 #pragma unroll
-        for (int i = 0; i < kGvMaxKpw / 4; ++i)
+        for (int i = 0; i < KPWM / 4; ++i)
           if (i == (j >> 2)) {
             sh = bitsf(__builtin_amdgcn_readlane(fbits(seed_hi[i]), 16 * (j & 3)));
             if (two) sl = bitsf(__builtin_amdgcn_readlane(fbits(seed_lo[i]), 16 * (j & 3)));
@@ -165,7 +175,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
         u32x4_t bc[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) bc[nt] = ring[u][nt];
-        issue(u, kb0 + j + kGvRing);
+        issue(u, kb0 + j + RING);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const float sc = scale_bits_f32(sreg[(nt * a.kpw + j) * 16 + lr], a.sdt);
@@ -175,38 +185,38 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
           p = mfma_bf16(af[2], decode8(b.z), p);
           p = mfma_bf16(af[3], decode8(b.w), p);
           // only D row 0 (and row 8, the lo plane) is the token
-          acc[nt][0] += sc * p[0];
+          acc[nt] += sc * p[0];
         }
       }
     }
   }
 
-  // ---- the kw partials, added in wave order ----
-  f32x4_t *red = reinterpret_cast<f32x4_t *>(lds + (size_t)a.kw * wbytes);
-  if (wave > 0) {
+  if (two) {  // slot 0 (hi) + slot 8 (lo): lanes 0-31 receive lanes 32-63
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) red[((wave - 1) * NT + nt) * 64 + lane] = acc[nt];
+    for (int nt = 0; nt < NT; ++nt) {
+      auto sw = __builtin_amdgcn_permlane32_swap(fbits(acc[nt]), fbits(acc[nt]), false, false);
+      acc[nt] += bitsf(sw[1]);
+    }
+  }
+
+  // ---- the kw partials (D row 0: lanes 0-15), added in wave order ----
+  float *red = reinterpret_cast<float *>(lds + (size_t)a.kw * wbytes);
+  if (wave > 0 && lane < 16) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) red[((wave - 1) * NT + nt) * 16 + lr] = acc[nt];
   }
   __syncthreads();
   if (wave > 0) return;
   for (int w = 1; w < a.kw; ++w) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[nt] += red[((w - 1) * NT + nt) * 64 + lane];
-  }
-  if (two) {  // slot 0 (hi) + slot 8 (lo): lanes 0-31 receive lanes 32-63
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      auto sw = __builtin_amdgcn_permlane32_swap(fbits(acc[nt][0]), fbits(acc[nt][0]), false,
-                                                 false);
-      acc[nt][0] += bitsf(sw[1]);
-    }
+    for (int nt = 0; nt < NT; ++nt) acc[nt] += red[((w - 1) * NT + nt) * 16 + lr];
   }
   if (lg != 0) return;  // D row 0 = the token: lanes 0-15, component 0
   const int row = 16 * T + lr;
   if (row >= a.N) return;
-  const float y = acc[0][0];
+  const float y = acc[0];
   if (NT == 2) {
-    const float h = silu_f32(y) * acc[NT - 1][0];
+    const float h = silu_f32(y) * acc[NT - 1];
     if (a.epi == EPI_SWIGLU) {
       reinterpret_cast<float *>(a.out)[row] = h;
     } else {  // hi = h truncated to bf16, lo = bf16(h - hi): the A_HILO planes
@@ -221,6 +231,23 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
   }
 }
 
+// Up to 4 k-blocks per wave, few registers, many resident waves: bf16
+// activations fit 64 VGPRs (8 waves per SIMD), two activation planes 72 (7).
+template <int NT, int AM>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void gemv_kernel_lean(
+    GvParams a) {
+  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4>(a);
+}
+template <int NT, int AM>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(7))) void gemv_kernel_lean2(
+    GvParams a) {
+  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4>(a);
+}
+template <int NT, int AM, int KPWM>
+__global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
+  gemv_body<NT, AM, NT == 2 ? kGvRing2 : kGvRing1, KPWM>(a);
+}
+
 }  // namespace
 
 size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt);
@@ -232,16 +259,15 @@ bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus) {
   const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
   if (sw ? !(a.w1 && a.s1) : !(epi == EPI_F32 || epi == EPI_BF16)) return false;
   const int nt = sw ? 2 : 1;
-  const GemvPlan p = gemv_plan(a.N, a.K, nt, num_cus);  // K > 256 KB blocks: kw > 16
+  const GemvPlan p = gemv_plan(a.N, a.K, num_cus);  // K > 256 KB blocks: kw > 16
   return p.kw <= 16 && gemv_lds_bytes(p, amode, nt) <= kGvMaxLds;
 }
 
-GemvPlan gemv_plan(int N, int K, int nt, int num_cus) {
+GemvPlan gemv_plan(int N, int K, int num_cus) {
   const int tiles = (N + 15) / 16, KB = K / 128;
-  // About 64 KB of weight loads in flight per CU: 16 / nt waves of kGvRing x nt
-  // KB each (measured best on the config-1 shapes: fewer waves starve the HBM,
-  // more only queue behind each other).
-  const long waves = (16L / nt) * num_cus;
+  // kGvWavesPerCu waves per CU, all resident at once (the register arrays are
+  // sized by the k-blocks per wave): many short independent streams
+  const long waves = (long)kGvWavesPerCu * num_cus;
   int kw = (int)((2 * waves + tiles) / (2L * tiles));  // nearest
   if (kw > 16) kw = 16;
   if (kw < 1) kw = 1;
@@ -258,12 +284,12 @@ GemvPlan gemv_plan(int N, int K, int nt, int num_cus) {
 size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt) {
   const int planes = amode == A_BF16 ? 1 : 2;
   return (size_t)p.kw * (planes * p.kpw * 256 + nt * p.kpw * 32) +
-         (size_t)(p.kw - 1) * nt * 1024 + 16;
+         (size_t)(p.kw - 1) * nt * 16 * 4 + 16;
 }
 
 hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, hipStream_t st) {
   const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
-  const GemvPlan p = gemv_plan(a.N, a.K, sw ? 2 : 1, num_cus);
+  const GemvPlan p = gemv_plan(a.N, a.K, num_cus);
   GvParams k{};
   k.w0 = a.w0;
   k.w1 = a.w1;
@@ -282,15 +308,29 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, hip
   k.kpw = p.kpw;
   const size_t lds = gemv_lds_bytes(p, amode, sw ? 2 : 1);
   const dim3 grid((a.N + 15) / 16), block(64 * p.kw);
+#define CAI4_GV(NT, AM)                                                                    \
+  do {                                                                                     \
+    if (p.kpw <= 4) {                                                                      \
+      if constexpr (AM == A_BF16)                                                          \
+        hipLaunchKernelGGL((gemv_kernel_lean<NT, AM>), grid, block, lds, st, k);           \
+      else                                                                                 \
+        hipLaunchKernelGGL((gemv_kernel_lean2<NT, AM>), grid, block, lds, st, k);          \
+    } else if (p.kpw <= 8) {                                                               \
+      hipLaunchKernelGGL((gemv_kernel<NT, AM, 8>), grid, block, lds, st, k);               \
+    } else {                                                                               \
+      hipLaunchKernelGGL((gemv_kernel<NT, AM, 16>), grid, block, lds, st, k);              \
+    }                                                                                      \
+  } while (0)
   if (sw) {
-    if (amode == A_BF16) hipLaunchKernelGGL((gemv_kernel<2, A_BF16>), grid, block, lds, st, k);
-    else if (amode == A_XF32) hipLaunchKernelGGL((gemv_kernel<2, A_XF32>), grid, block, lds, st, k);
-    else hipLaunchKernelGGL((gemv_kernel<2, A_HILO>), grid, block, lds, st, k);
+    if (amode == A_BF16) CAI4_GV(2, A_BF16);
+    else if (amode == A_XF32) CAI4_GV(2, A_XF32);
+    else CAI4_GV(2, A_HILO);
   } else {
-    if (amode == A_BF16) hipLaunchKernelGGL((gemv_kernel<1, A_BF16>), grid, block, lds, st, k);
-    else if (amode == A_XF32) hipLaunchKernelGGL((gemv_kernel<1, A_XF32>), grid, block, lds, st, k);
-    else hipLaunchKernelGGL((gemv_kernel<1, A_HILO>), grid, block, lds, st, k);
+    if (amode == A_BF16) CAI4_GV(1, A_BF16);
+    else if (amode == A_XF32) CAI4_GV(1, A_XF32);
+    else CAI4_GV(1, A_HILO);
   }
+#undef CAI4_GV
   return hipGetLastError();
 }
 

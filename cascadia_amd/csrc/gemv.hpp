@@ -16,8 +16,7 @@ struct GemvPlan {
 // modes A_BF16 / A_XF32 / A_HILO; epilogues f32, bf16, SwiGLU (f32 or hi/lo); the
 // plan's LDS within one CU's.
 bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus);
-// nt = 2 for a gate/up pair (SwiGLU epilogues), else 1.
-GemvPlan gemv_plan(int N, int K, int nt, int num_cus);
+GemvPlan gemv_plan(int N, int K, int num_cus);
 hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, hipStream_t st);
 
 }  // namespace cai4
