@@ -158,7 +158,7 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
     g.sdt = sdt;
     g.tiled = tiled;
     if (cai4::gemv_supported(g, amode, epi, d.num_cus))
-      return hip_status(cai4::gemv_launch(g, amode, epi, d.num_cus, st));
+      return hip_status(cai4::gemv_launch(g, amode, epi, d.num_cus, 0, st));
   }
   const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, G, M, amode, epi, d);
   if (p.partial_bytes && !partials) {
@@ -492,7 +492,14 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     a.sdt = (int)L->scale_dtype;
     a.glog2 = glog2_of(G);
     a.tiled = (int)L->tiling;
-    e = cai4::skinny_launch(a, m.gu, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, st);
+    // one row per chunk (a decode token over distinct experts): the one-token GEMV
+    const cai4::SkinnyDevice d = device_props(dev);
+    if (cai4::gemv_supported(a, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d.num_cus,
+                             m.ws.chunk_rows, m.ws.max_chunks))
+      e = cai4::gemv_launch(a, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d.num_cus, m.ws.max_chunks,
+                            st);
+    else
+      e = cai4::skinny_launch(a, m.gu, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, st);
   }
   if (e == hipSuccess) {
     cai4::SkinnyArgs a{};
@@ -513,7 +520,12 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     a.sdt = (int)L->scale_dtype;
     a.glog2 = glog2_of(G);
     a.tiled = (int)L->tiling;
-    e = cai4::skinny_launch(a, m.dn, cai4::A_HILO, cai4::EPI_BF16, st);
+    const cai4::SkinnyDevice d = device_props(dev);
+    if (cai4::gemv_supported(a, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, m.ws.chunk_rows,
+                             m.ws.max_chunks))
+      e = cai4::gemv_launch(a, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, m.ws.max_chunks, st);
+    else
+      e = cai4::skinny_launch(a, m.dn, cai4::A_HILO, cai4::EPI_BF16, st);
   }
   if (e != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
   if (join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;

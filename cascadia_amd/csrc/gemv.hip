@@ -38,6 +38,13 @@ struct GvParams {
   const void *x, *x2;
   void *out, *out2;
   int N, K, G, sdt, epi, kw, kpw;
+  // grouped mode: blockIdx.y = chunk of one row of one expert (count <= 1);
+  // the expert's matrices at + expert * expert_stride, the x row
+  // row_map[row0] (or row0), the output row row0; ldx / ldo in elements
+  const SkinnyChunk *chunks;
+  const int32_t *row_map;
+  size_t expert_stride;
+  int ldx, ldo;
 };
 
 constexpr int kGvMaxKpw = 16;
@@ -47,13 +54,14 @@ constexpr int kGvRingLean2 = 2;  // gate/up tile pairs, lean kernel (64 VGPRs)
 constexpr int kGvWavesPerCu = 28;  // planned waves per CU
 
 // NT: weight tiles per wave (2 = a gate/up pair, SW epilogue); AM: activation
-// mode (A_BF16, A_XF32, A_HILO); RING: k-blocks in flight per wave; KPWM: most
+// mode (A_BF16, A_XF32, A_HILO; A_GATHER: f32 x rounded to bf16); RING: k-blocks in flight per wave; KPWM: most
 // k-blocks per wave (sizes the per-wave register arrays: fewer registers, more
 // resident waves).
 template <int NT, int AM, int RING, int KPWM>
 CAI4_DEV void gemv_body(const GvParams &a) {
   extern __shared__ __align__(16) uint8_t lds[];
-  constexpr bool two = AM != A_BF16;  // hi/lo planes
+  constexpr bool two = AM == A_XF32 || AM == A_HILO;  // hi/lo planes
+  constexpr bool xf32 = AM == A_XF32 || AM == A_GATHER;
   constexpr int PL = two ? 2 : 1;
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -64,20 +72,40 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   const int wbytes = PL * rbytes + NT * a.kpw * 32;  // + scales [NT][kpw][16] u16
   uint8_t *reg = lds + (size_t)wave * wbytes;       // this wave's region
 
+  // ---- the matrices, the x row and the output row of this workgroup ----
+  const uint8_t *w0 = a.w0, *w1 = a.w1, *s0 = a.s0, *s1 = a.s1;
+  const uint8_t *xp = static_cast<const uint8_t *>(a.x), *xp2 = static_cast<const uint8_t *>(a.x2);
+  size_t orow = 0;
+  if (a.chunks) {
+    const SkinnyChunk c = a.chunks[blockIdx.y];
+    if (c.count == 0) return;  // the whole workgroup
+    const size_t eo = (size_t)c.expert * a.expert_stride;
+    w0 += eo;
+    s0 += eo;
+    if (NT == 2) {
+      w1 += eo;
+      s1 += eo;
+    }
+    const size_t xr = (size_t)(a.row_map ? a.row_map[c.row0] : c.row0) * a.ldx;
+    xp += xr * (xf32 ? 4 : 2);
+    if (AM == A_HILO) xp2 += xr * 2;
+    orow = (size_t)c.row0 * a.ldo;
+  }
+
   // ---- activation slice [kb0, kb1) -> registers (issued first) ----
   // chunk c = 8 columns; lane holds chunks lane + 64 i, i < kpw / 4
   const int nch = nkb * 16;
   u32x4_t xa[KPWM / 4], xb[KPWM / 4];
   {
-    const size_t xbytes = (size_t)a.K * (AM == A_XF32 ? 4 : 2);
-    const buf_rsrc_t r0 = buf_rsrc(a.x, xbytes);
-    const buf_rsrc_t r1 = buf_rsrc(AM == A_HILO ? a.x2 : a.x, xbytes);
+    const size_t xbytes = (size_t)a.K * (xf32 ? 4 : 2);
+    const buf_rsrc_t r0 = buf_rsrc(xp, xbytes);
+    const buf_rsrc_t r1 = buf_rsrc(AM == A_HILO ? xp2 : xp, xbytes);
 #pragma unroll
     for (int i = 0; i < KPWM / 4; ++i) {
       const int c = lane + 64 * i;
       const bool ok = i * 64 < nch && c < nch;
       const uint32_t col = (uint32_t)(kb0 * 128 + 8 * c);
-      if (AM == A_XF32) {
+      if (xf32) {
         xa[i] = buf_load16(r0, ok ? col * 4 : kBufOOB);
         xb[i] = buf_load16(r0, ok ? col * 4 + 16 : kBufOOB);
       } else {
@@ -92,8 +120,8 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   uint32_t sv[kSv];
   const int nsv = NT * a.kpw * 8;
   {
-    const buf_rsrc_t sr0 = buf_rsrc(a.s0 + (size_t)T * NG * 32, (size_t)NG * 32);
-    const buf_rsrc_t sr1 = buf_rsrc(NT == 2 ? a.s1 + (size_t)T * NG * 32 : a.s0, (size_t)NG * 32);
+    const buf_rsrc_t sr0 = buf_rsrc(s0 + (size_t)T * NG * 32, (size_t)NG * 32);
+    const buf_rsrc_t sr1 = buf_rsrc(NT == 2 ? s1 + (size_t)T * NG * 32 : s0, (size_t)NG * 32);
     const int per = a.kpw * 8;  // pieces per tile
 #pragma unroll
     for (int i = 0; i < kSv; ++i) {
@@ -106,8 +134,8 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   }
 
   // ---- weight ring ----
-  const buf_rsrc_t wr0 = buf_rsrc(a.w0 + (size_t)T * KB * 1024, (size_t)KB * 1024);
-  const buf_rsrc_t wr1 = buf_rsrc(NT == 2 ? a.w1 + (size_t)T * KB * 1024 : a.w0, (size_t)KB * 1024);
+  const buf_rsrc_t wr0 = buf_rsrc(w0 + (size_t)T * KB * 1024, (size_t)KB * 1024);
+  const buf_rsrc_t wr1 = buf_rsrc(NT == 2 ? w1 + (size_t)T * KB * 1024 : w0, (size_t)KB * 1024);
   u32x4_t ring[RING][NT];
   auto issue = [&](int u, int kb) {  // kb past the slice: dead loads (no data moves)
     const uint32_t wo = kb < kb1 ? (uint32_t)kb * 1024 + 16 * lane : kBufOOB;
@@ -130,6 +158,12 @@ CAI4_DEV void gemv_body(const GvParams &a) {
       lo = act_split_f32_nat(fa, fb, true);
     } else if (AM == A_HILO) {
       lo = xb[i];
+    } else if (AM == A_GATHER) {  // eight f32 -> eight bf16 (RNE), natural order
+      const u32x4_t f0 = xa[i], f1 = xb[i];
+      hi.x = f32_to_bf16_rne(bitsf(f0.x)) | (f32_to_bf16_rne(bitsf(f0.y)) << 16);
+      hi.y = f32_to_bf16_rne(bitsf(f0.z)) | (f32_to_bf16_rne(bitsf(f0.w)) << 16);
+      hi.z = f32_to_bf16_rne(bitsf(f1.x)) | (f32_to_bf16_rne(bitsf(f1.y)) << 16);
+      hi.w = f32_to_bf16_rne(bitsf(f1.z)) | (f32_to_bf16_rne(bitsf(f1.w)) << 16);
     }
     if (i * 64 < nch && c < nch) {
       *reinterpret_cast<u32x4_t *>(reg + 16 * c) = hi;
@@ -212,8 +246,9 @@ CAI4_DEV void gemv_body(const GvParams &a) {
     for (int nt = 0; nt < NT; ++nt) acc[nt] += red[((w - 1) * NT + nt) * 16 + lr];
   }
   if (lg != 0) return;  // D row 0 = the token: lanes 0-15, component 0
-  const int row = 16 * T + lr;
-  if (row >= a.N) return;
+  const int r16 = 16 * T + lr;
+  if (r16 >= a.N) return;
+  const size_t row = orow + r16;
   const float y = acc[0];
   if (NT == 2) {
     const float h = silu_f32(y) * acc[NT - 1];
@@ -253,13 +288,22 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
 size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt);
 constexpr size_t kGvMaxLds = 160 * 1024;  // gfx950: LDS of one CU
 
-bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus) {
-  if (a.M != 1 || !a.tiled || a.chunks || a.G % 128 || a.K % a.G) return false;
-  if (amode != A_BF16 && amode != A_XF32 && amode != A_HILO) return false;
+bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int chunk_rows,
+                    int max_chunks) {
+  if (!a.tiled || a.G % 128 || a.K % a.G) return false;
+  if (a.chunks) {  // grouped: one row per chunk, f32 rows gathered / hi-lo rows
+    if (chunk_rows != 1 || max_chunks < 1 || max_chunks > 65535) return false;
+    if (amode != A_GATHER && amode != A_HILO) return false;
+  } else {
+    if (a.M != 1) return false;
+    if (amode != A_BF16 && amode != A_XF32 && amode != A_HILO) return false;
+  }
   const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
   if (sw ? !(a.w1 && a.s1) : !(epi == EPI_F32 || epi == EPI_BF16)) return false;
   const int nt = sw ? 2 : 1;
-  const GemvPlan p = gemv_plan(a.N, a.K, num_cus);  // K > 256 KB blocks: kw > 16
+  const long n_eff = (long)a.N * (a.chunks ? max_chunks : 1);
+  if (n_eff > (1L << 30)) return false;
+  const GemvPlan p = gemv_plan((int)n_eff, a.K, num_cus);  // K > 256 KB blocks: kw > 16
   return p.kw <= 16 && gemv_lds_bytes(p, amode, nt) <= kGvMaxLds;
 }
 
@@ -282,14 +326,16 @@ GemvPlan gemv_plan(int N, int K, int num_cus) {
 }
 
 size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt) {
-  const int planes = amode == A_BF16 ? 1 : 2;
+  const int planes = amode == A_XF32 || amode == A_HILO ? 2 : 1;
   return (size_t)p.kw * (planes * p.kpw * 256 + nt * p.kpw * 32) +
          (size_t)(p.kw - 1) * nt * 16 * 4 + 16;
 }
 
-hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, hipStream_t st) {
+hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int max_chunks,
+                       hipStream_t st) {
   const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
-  const GemvPlan p = gemv_plan(a.N, a.K, num_cus);
+  const int nch = a.chunks ? max_chunks : 1;
+  const GemvPlan p = gemv_plan(a.N * nch, a.K, num_cus);
   GvParams k{};
   k.w0 = a.w0;
   k.w1 = a.w1;
@@ -306,12 +352,17 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, hip
   k.epi = epi;
   k.kw = p.kw;
   k.kpw = p.kpw;
+  k.chunks = a.chunks;
+  k.row_map = a.row_map;
+  k.expert_stride = a.expert_stride;
+  k.ldx = a.ldx;
+  k.ldo = a.ldo;
   const size_t lds = gemv_lds_bytes(p, amode, sw ? 2 : 1);
-  const dim3 grid((a.N + 15) / 16), block(64 * p.kw);
+  const dim3 grid((a.N + 15) / 16, nch), block(64 * p.kw);
 #define CAI4_GV(NT, AM)                                                                    \
   do {                                                                                     \
     if (p.kpw <= 4) {                                                                      \
-      if constexpr (AM == A_BF16)                                                          \
+      if constexpr (AM == A_BF16 || AM == A_GATHER)                                        \
         hipLaunchKernelGGL((gemv_kernel_lean<NT, AM>), grid, block, lds, st, k);           \
       else                                                                                 \
         hipLaunchKernelGGL((gemv_kernel_lean2<NT, AM>), grid, block, lds, st, k);          \
@@ -324,6 +375,7 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, hip
   if (sw) {
     if (amode == A_BF16) CAI4_GV(2, A_BF16);
     else if (amode == A_XF32) CAI4_GV(2, A_XF32);
+    else if (amode == A_GATHER) CAI4_GV(2, A_GATHER);
     else CAI4_GV(2, A_HILO);
   } else {
     if (amode == A_BF16) CAI4_GV(1, A_BF16);

@@ -173,6 +173,29 @@ def test_moe_layer_small(cl, orc, T, mode, shared_inter, tiled, thr):
         assert (w < thr).any(), "threshold case should skip some slots"
 
 
+@pytest.mark.parametrize("mode,shared_inter,thr", [(1, 128, 0.0), (2, 0, 0.2), (1, 0, 0.3)])
+def test_moe_one_token_g128(cl, orc, mode, shared_inter, thr):
+    """One routed token over tiled G128 experts: one row per expert chunk, the
+    one-token GEMV in grouped mode (gathered f32 row, then hi/lo planes); slots
+    under the threshold leave empty chunks (all of them at thr 0.3 with four
+    sigmoid weights near 0.25)."""
+    E, k, h, i, g, sdt, T = 16, 4, 512, 384, 128, F16, 1
+    blob, shared, ex = build(cl, orc, E, h, i, g, sdt, 17, shared_inter, True)
+    logits = orc.fill_normal_f32(18, T, T * E).reshape(T, E)
+    x = orc.fill_normal_f32(19, T, T * h).reshape(T, h)
+    out = torch.empty((T, h), dtype=torch.float32, device="cuda")
+    ids_o = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w_o = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    xd = dev(x)
+    cl.moe_forward(ex, xd, out, top_k=k, logits=dev(logits), mode=mode, scale=1.0, threshold=thr,
+                   residual=xd, ids_out=ids_o, weights_out=w_o)
+    got, ids, w = host(out), host(ids_o), host(w_o)
+    check_layer(orc, got, x, blob, shared, shared_inter, E, h, i, g, sdt, ids, w, thr,
+                f"one token mode={mode} shared={shared_inter} thr={thr}")
+    if thr > 0:
+        assert (w < thr).any(), "threshold case should skip some slots"
+
+
 @pytest.mark.parametrize("T", [24, 70])
 def test_moe_given_ids_and_determinism(cl, orc, T):
     """ROUTE_IDS with repeated experts across tokens; two calls bit-identical."""
