@@ -33,6 +33,19 @@ namespace cai4 {
 
 namespace {
 
+// Sum over aligned groups of 16 / GPB lanes (every lane of a group gets it).
+template <int GPB>
+CAI4_DEV float group_sum(float t) {
+  if constexpr (GPB == 1) {
+    return row16_sum(t);
+  } else {
+    t += dpp_f32<0xB1>(t);  // quad_perm 1,0,3,2
+    t += dpp_f32<0x4E>(t);  // quad_perm 2,3,0,1
+    if constexpr (GPB == 2) t += __shfl_xor(t, 4);
+    return t;
+  }
+}
+
 struct GvParams {
   const uint8_t *w0, *w1, *s0, *s1;
   const void *x, *x2;
@@ -56,8 +69,12 @@ constexpr int kGvWavesPerCu = 28;  // planned waves per CU
 // NT: weight tiles per wave (2 = a gate/up pair, SW epilogue); AM: activation
 // mode (A_BF16, A_XF32, A_HILO; A_GATHER: f32 x rounded to bf16); RING: k-blocks in flight per wave; KPWM: most
 // k-blocks per wave (sizes the per-wave register arrays: fewer registers, more
-// resident waves).
-template <int NT, int AM, int RING, int KPWM>
+// resident waves); GPB: scale groups per 128-column k-block (128 / G for G of
+// 32 or 64, else 1).  With GPB > 1 each MFMA step must cover whole groups: the
+// weight fragment's four dwords are transposed across the four 16-lane rows
+// (step s then holds columns 32 s .. 32 s + 31) and the activations are read
+// to match; every group gets its own seed and scale.
+template <int NT, int AM, int RING, int KPWM, int GPB>
 CAI4_DEV void gemv_body(const GvParams &a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr bool two = AM == A_XF32 || AM == A_HILO;  // hi/lo planes
@@ -65,11 +82,11 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   constexpr int PL = two ? 2 : 1;
   const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int KB = a.K >> 7, NG = a.K / a.G;  // G a multiple of 128: one scale per k-block
+  const int KB = a.K >> 7, NG = a.K / a.G;
   const int T = blockIdx.x;          // tile (pair) index
   const int kb0 = min(wave * a.kpw, KB), kb1 = min(kb0 + a.kpw, KB), nkb = kb1 - kb0;
   const int rbytes = a.kpw * 256;                // one plane of a wave's slice
-  const int wbytes = PL * rbytes + NT * a.kpw * 32;  // + scales [NT][kpw][16] u16
+  const int wbytes = PL * rbytes + NT * a.kpw * GPB * 32;  // + scales [NT][kpw][GPB][16] u16
   uint8_t *reg = lds + (size_t)wave * wbytes;       // this wave's region
 
   // ---- the matrices, the x row and the output row of this workgroup ----
@@ -115,20 +132,21 @@ CAI4_DEV void gemv_body(const GvParams &a) {
     }
   }
 
-  // ---- scales of the slice: 4-byte pieces, 8 per k-block and tile ----
-  constexpr int kSv = (NT * KPWM * 8 + 63) / 64;  // pieces per lane at most
+  // ---- scales of the slice: 4-byte pieces, 8 GPB per k-block and tile ----
+  constexpr int kSv = (NT * KPWM * 8 * GPB + 63) / 64;  // pieces per lane at most
   uint32_t sv[kSv];
-  const int nsv = NT * a.kpw * 8;
+  const int nsv = NT * a.kpw * 8 * GPB;
   {
     const buf_rsrc_t sr0 = buf_rsrc(s0 + (size_t)T * NG * 32, (size_t)NG * 32);
     const buf_rsrc_t sr1 = buf_rsrc(NT == 2 ? s1 + (size_t)T * NG * 32 : s0, (size_t)NG * 32);
-    const int per = a.kpw * 8;  // pieces per tile
+    const int per = a.kpw * 8 * GPB;  // pieces per tile
 #pragma unroll
     for (int i = 0; i < kSv; ++i) {
-      const int e = lane + 64 * i, nt = e / per, q = e - nt * per, j = q >> 3;
+      const int e = lane + 64 * i, nt = e / per, q = e - nt * per, j = q / (8 * GPB);
       const bool ok = e < nsv && j < nkb;
+      // the k-block's first group, then its GPB groups' 32-byte rows in turn
       const uint32_t off =
-          ok ? (uint32_t)((((kb0 + j) * 128) / a.G) * 32 + 4 * (q & 7)) : kBufOOB;
+          ok ? (uint32_t)((((kb0 + j) * 128) / a.G) * 32 + 4 * (q - j * 8 * GPB)) : kBufOOB;
       sv[i] = __builtin_amdgcn_raw_buffer_load_b32(nt == 0 ? sr0 : sr1, off, 0, 0);
     }
   }
@@ -169,9 +187,9 @@ CAI4_DEV void gemv_body(const GvParams &a) {
       *reinterpret_cast<u32x4_t *>(reg + 16 * c) = hi;
       if (two) *reinterpret_cast<u32x4_t *>(reg + rbytes + 16 * c) = lo;
     }
-    // k-block of chunk c = (c / 16): the 16 lanes of a DPP row
-    seed_hi[i] = -136.f * row16_sum(sum8_bf16(hi));
-    seed_lo[i] = two ? -136.f * row16_sum(sum8_bf16(lo)) : 0.f;
+    // group of chunk c: 16 / GPB consecutive chunks (lanes) of k-block c / 16
+    seed_hi[i] = -136.f * group_sum<GPB>(sum8_bf16(hi));
+    seed_lo[i] = two ? -136.f * group_sum<GPB>(sum8_bf16(lo)) : 0.f;
   }
   uint16_t *sreg = reinterpret_cast<uint16_t *>(reg + PL * rbytes);
 #pragma unroll
@@ -184,7 +202,8 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   float acc[NT];  // D row 0 (and row 8) only: the token
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = 0.f;
-  const uint8_t *arow = reg + 64 * lg + (two && lr >= 8 ? rbytes : 0);
+  // step s of lane group lg: columns 32 lg + 8 s (GPB 1) or 32 s + 8 lg (GPB > 1)
+  const uint8_t *arow = reg + (GPB > 1 ? 16 : 64) * lg + (two && lr >= 8 ? rbytes : 0);
   const bool lo_slot = two && lg >= 2;  // D rows 8-15: the lo plane
   for (int k0 = 0; k0 < nkb; k0 += RING) {
 #pragma unroll
@@ -194,16 +213,22 @@ CAI4_DEV void gemv_body(const GvParams &a) {
         u32x4_t af[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          af[s] = *reinterpret_cast<const u32x4_t *>(arow + j * 256 + 16 * s);
-        // seed of k-block j: row j % 4 of register j / 4 (uniform selection)
-        float sh = 0.f, sl = 0.f;
+          af[s] = *reinterpret_cast<const u32x4_t *>(arow + j * 256 + (GPB > 1 ? 64 : 16) * s);
+        // seed of group q of k-block j: lane 16 (j % 4) + q 16 / GPB of register
+        // j / 4 (uniform selection)
+        float sd[GPB];
 #pragma unroll
-        for (int i = 0; i < KPWM / 4; ++i)
-          if (i == (j >> 2)) {
-            sh = bitsf(__builtin_amdgcn_readlane(fbits(seed_hi[i]), 16 * (j & 3)));
-            if (two) sl = bitsf(__builtin_amdgcn_readlane(fbits(seed_lo[i]), 16 * (j & 3)));
-          }
-        const float sd = lo_slot ? sl : sh;
+        for (int q = 0; q < GPB; ++q) {
+          float sh = 0.f, sl = 0.f;
+#pragma unroll
+          for (int i = 0; i < KPWM / 4; ++i)
+            if (i == (j >> 2)) {
+              const int ln = 16 * (j & 3) + q * (16 / GPB);
+              sh = bitsf(__builtin_amdgcn_readlane(fbits(seed_hi[i]), ln));
+              if (two) sl = bitsf(__builtin_amdgcn_readlane(fbits(seed_lo[i]), ln));
+            }
+          sd[q] = lo_slot ? sl : sh;
+        }
         // take the slot's data, then refill it before the arithmetic: the next
         // load is in flight while this k-block is decoded
         u32x4_t bc[NT];
@@ -212,14 +237,18 @@ CAI4_DEV void gemv_body(const GvParams &a) {
         issue(u, kb0 + j + RING);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          const float sc = scale_bits_f32(sreg[(nt * a.kpw + j) * 16 + lr], a.sdt);
-          const u32x4_t b = bc[nt];
-          f32x4_t p = mfma_bf16(af[0], decode8(b.x), f32x4_t{sd, sd, sd, sd});
-          p = mfma_bf16(af[1], decode8(b.y), p);
-          p = mfma_bf16(af[2], decode8(b.z), p);
-          p = mfma_bf16(af[3], decode8(b.w), p);
-          // only D row 0 (and row 8, the lo plane) is the token
-          acc[nt] += sc * p[0];
+          const u32x4_t b = GPB > 1 ? xpose_rows(bc[nt]) : bc[nt];
+          const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+          for (int q = 0; q < GPB; ++q) {
+            const float sc = scale_bits_f32(sreg[((nt * a.kpw + j) * GPB + q) * 16 + lr], a.sdt);
+            f32x4_t p = f32x4_t{sd[q], sd[q], sd[q], sd[q]};
+#pragma unroll
+            for (int s = q * (4 / GPB); s < (q + 1) * (4 / GPB); ++s)
+              p = mfma_bf16(af[s], decode8(bw[s]), p);
+            // only D row 0 (and row 8, the lo plane) is the token
+            acc[nt] += sc * p[0];
+          }
         }
       }
     }
@@ -266,31 +295,42 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   }
 }
 
-// Up to 4 k-blocks per wave, few registers, many resident waves: bf16
-// activations fit 64 VGPRs (8 waves per SIMD), two activation planes 72 (7).
-template <int NT, int AM>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void gemv_kernel_lean(
+// Up to 4 k-blocks per wave, few registers, many resident waves: one scale
+// group per k-block and bf16 activations fit 64 VGPRs (8 waves per SIMD);
+// two activation planes or small groups 72 (7), both 80 (6).
+template <int NT, int AM, int GPB>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void gemv_kernel_lean8(
     GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4>(a);
+  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4, GPB>(a);
 }
-template <int NT, int AM>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(7))) void gemv_kernel_lean2(
+template <int NT, int AM, int GPB>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(7))) void gemv_kernel_lean7(
     GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4>(a);
+  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4, GPB>(a);
 }
-template <int NT, int AM, int KPWM>
+template <int NT, int AM, int GPB>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void gemv_kernel_lean6(
+    GvParams a) {
+  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4, GPB>(a);
+}
+template <int NT, int AM, int KPWM, int GPB>
 __global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRing2 : kGvRing1, KPWM>(a);
+  gemv_body<NT, AM, NT == 2 ? kGvRing2 : kGvRing1, KPWM, GPB>(a);
 }
 
 }  // namespace
 
-size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt);
+size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt, int gpb);
 constexpr size_t kGvMaxLds = 160 * 1024;  // gfx950: LDS of one CU
+
+// Scale groups per 128-column k-block: 4 (G 32), 2 (G 64), 1 (G a multiple of
+// 128); 0 = not supported.
+int gemv_gpb(int G) { return G == 32 ? 4 : G == 64 ? 2 : (G % 128 == 0 ? 1 : 0); }
 
 bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int chunk_rows,
                     int max_chunks) {
-  if (!a.tiled || a.G % 128 || a.K % a.G) return false;
+  const int gpb = gemv_gpb(a.G);
+  if (!a.tiled || !gpb || a.K % 128 || a.K % a.G) return false;
   if (a.chunks) {  // grouped: one row per chunk, f32 rows gathered / hi-lo rows
     if (chunk_rows != 1 || max_chunks < 1 || max_chunks > 65535) return false;
     if (amode != A_GATHER && amode != A_HILO) return false;
@@ -304,7 +344,8 @@ bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int ch
   const long n_eff = (long)a.N * (a.chunks ? max_chunks : 1);
   if (n_eff > (1L << 30)) return false;
   const GemvPlan p = gemv_plan((int)n_eff, a.K, num_cus);  // K > 256 KB blocks: kw > 16
-  return p.kw <= 16 && gemv_lds_bytes(p, amode, nt) <= kGvMaxLds;
+  if (gpb > 1 && p.kpw > 8) return false;  // no 16-k-block instantiation for small groups
+  return p.kw <= 16 && gemv_lds_bytes(p, amode, nt, gpb) <= kGvMaxLds;
 }
 
 GemvPlan gemv_plan(int N, int K, int num_cus) {
@@ -325,9 +366,9 @@ GemvPlan gemv_plan(int N, int K, int num_cus) {
   return GemvPlan{kw, kpw};
 }
 
-size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt) {
+size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt, int gpb) {
   const int planes = amode == A_XF32 || amode == A_HILO ? 2 : 1;
-  return (size_t)p.kw * (planes * p.kpw * 256 + nt * p.kpw * 32) +
+  return (size_t)p.kw * (planes * p.kpw * 256 + nt * p.kpw * gpb * 32) +
          (size_t)(p.kw - 1) * nt * 16 * 4 + 16;
 }
 
@@ -357,20 +398,30 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int
   k.expert_stride = a.expert_stride;
   k.ldx = a.ldx;
   k.ldo = a.ldo;
-  const size_t lds = gemv_lds_bytes(p, amode, sw ? 2 : 1);
+  const int gpb = gemv_gpb(a.G);
+  const size_t lds = gemv_lds_bytes(p, amode, sw ? 2 : 1, gpb);
   const dim3 grid((a.N + 15) / 16, nch), block(64 * p.kw);
-#define CAI4_GV(NT, AM)                                                                    \
+#define CAI4_GV_G(NT, AM, GPB)                                                             \
   do {                                                                                     \
     if (p.kpw <= 4) {                                                                      \
-      if constexpr (AM == A_BF16 || AM == A_GATHER)                                        \
-        hipLaunchKernelGGL((gemv_kernel_lean<NT, AM>), grid, block, lds, st, k);           \
+      constexpr int budget = (AM == A_BF16 || AM == A_GATHER ? 0 : 1) + (GPB > 1 ? 1 : 0);  \
+      if constexpr (budget == 0)                                                           \
+        hipLaunchKernelGGL((gemv_kernel_lean8<NT, AM, GPB>), grid, block, lds, st, k);     \
+      else if constexpr (budget == 1)                                                      \
+        hipLaunchKernelGGL((gemv_kernel_lean7<NT, AM, GPB>), grid, block, lds, st, k);     \
       else                                                                                 \
-        hipLaunchKernelGGL((gemv_kernel_lean2<NT, AM>), grid, block, lds, st, k);          \
+        hipLaunchKernelGGL((gemv_kernel_lean6<NT, AM, GPB>), grid, block, lds, st, k);     \
     } else if (p.kpw <= 8) {                                                               \
-      hipLaunchKernelGGL((gemv_kernel<NT, AM, 8>), grid, block, lds, st, k);               \
-    } else {                                                                               \
-      hipLaunchKernelGGL((gemv_kernel<NT, AM, 16>), grid, block, lds, st, k);              \
+      hipLaunchKernelGGL((gemv_kernel<NT, AM, 8, GPB>), grid, block, lds, st, k);          \
+    } else if constexpr (GPB == 1) {                                                       \
+      hipLaunchKernelGGL((gemv_kernel<NT, AM, 16, 1>), grid, block, lds, st, k);           \
     }                                                                                      \
+  } while (0)
+#define CAI4_GV(NT, AM)                                \
+  do {                                                 \
+    if (gpb == 4) CAI4_GV_G(NT, AM, 4);                \
+    else if (gpb == 2) CAI4_GV_G(NT, AM, 2);           \
+    else CAI4_GV_G(NT, AM, 1);                         \
   } while (0)
   if (sw) {
     if (amode == A_BF16) CAI4_GV(2, A_BF16);
@@ -382,6 +433,7 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int
     else if (amode == A_XF32) CAI4_GV(1, A_XF32);
     else CAI4_GV(1, A_HILO);
   }
+#undef CAI4_GV_G
 #undef CAI4_GV
   return hipGetLastError();
 }

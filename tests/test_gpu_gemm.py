@@ -260,6 +260,8 @@ def test_expert_forward_config1_llama_ffn(cl, orc, M):
 GEMV_SHAPES = [  # n, k, group, sdt: one token, tiled weights (the one-token GEMV kernel)
     (16, 128, 128, F16), (40, 384, 128, BF16), (130, 1024, 256, F16), (33, 2304, 128, F16),
     (4096, 4096, 128, F16), (300, 14336, 128, F16), (64, 32768, 128, BF16),
+    (64, 4096, 32, F16), (130, 1024, 64, BF16), (300, 7168, 32, F16), (48, 128, 32, BF16),
+    (200, 16384, 32, F16),
 ]
 
 
@@ -289,7 +291,8 @@ def test_gemv_tiled_one_token(cl, orc, n, k, group, sdt):
 
 
 @pytest.mark.parametrize("h,i,g", [(1024, 768, 128), (4096, 14336, 128), (512, 2560, 256),
-                                   (2048, 5632, 128), (3072, 8192, 128)])
+                                   (2048, 5632, 128), (3072, 8192, 128), (7168, 2048, 32),
+                                   (1024, 1536, 64)])
 def test_gemv_tiled_expert_one_token(cl, orc, h, i, g):
     """One token through tiled expert weights: fused gate/up (SwiGLU, hi/lo
     planes or f32) and down, bf16 and f32 forms."""
@@ -420,6 +423,9 @@ def test_tiled_bit_identical_to_crate_layout(cl, orc, n, k, group, sdt, seq):
             # tiled bf16 input of 64+ tokens runs the prefill GEMM, the crate
             # layout the decode kernel: two summation orders, both at the bar
             assert_f32_close(host(y1), host(y0), f"prefill vs decode kernel {n}x{k} seq{seq}")
+        elif seq == 1 and k % 128 == 0 and (group in (32, 64) or group % 128 == 0):
+            # one token over tiled weights runs the one-token GEMV
+            assert_f32_close(host(y1), host(y0), f"one-token vs decode kernel {n}x{k}")
         else:  # the same kernel reads either layout: bit-identical
             assert np.array_equal(host(y0).view(np.uint32), host(y1).view(np.uint32))
 
@@ -441,4 +447,7 @@ def test_tiled_expert_bit_identical(cl, orc, M):
         o1 = torch.empty(M * h, dtype=torch.int16, device="cuda")
         cl.expert_forward(xb, *W.slices(), o0)
         cl.expert_forward(xb, *Wt.slices(), o1, tiling=cl.TILING_MFMA)
-        assert np.array_equal(host(o0), host(o1))
+        if M == 1 and h % 128 == 0 and i % 128 == 0:  # tiled: the one-token GEMV
+            assert_bf16_close(host(o1).view(np.uint16), host(o0).view(np.uint16), f"M=1 {h}x{i}")
+        else:
+            assert np.array_equal(host(o0), host(o1))
