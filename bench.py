@@ -404,7 +404,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(m),
-                     "kernel": "gemv_kernel_lean<2, A_BF16>: one-token fused gate/up + SiLU*up (EPI_SWIGLU)",
+                     "kernel": "gemv_kernel<2, A_BF16, 4, 1>: one-token fused gate/up + SiLU*up (EPI_SWIGLU)",
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
     }

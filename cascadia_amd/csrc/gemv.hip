@@ -15,9 +15,10 @@
 // This keeps every wave independent until the end, as a plain streaming read
 // is.  Measured on MI355X, a plain read of ~60 MB is fastest as many short
 // runs (4-8 KB per wave, ~30 waves per CU): the plan aims at 28 resident waves
-// per CU, and waves of at most 4 k-blocks run in a lean kernel of 64-72 VGPRs
-// (7-8 waves per SIMD) -- with the register arrays sized for 16 k-blocks the
-// same plan would not fit and run in two rounds.
+// per CU, and each instantiation sizes its register arrays for the k-blocks
+// per wave it serves and is compiled for the waves per SIMD that plan needs
+// (64-80 VGPRs) -- with arrays sized for 16 k-blocks the same plan would not
+// fit and run in two rounds.
 //
 // Arithmetic as the skinny kernel's: weights enter the MFMA as bf16 128 + n;
 // each k-block's partial is seeded with -136 * sum(x) over the block (the
@@ -62,8 +63,7 @@ struct GvParams {
 
 constexpr int kGvMaxKpw = 16;
 constexpr int kGvRing1 = 4;  // k-blocks in flight per wave: single tiles
-constexpr int kGvRing2 = 4;  // gate/up tile pairs
-constexpr int kGvRingLean2 = 2;  // gate/up tile pairs, lean kernel (64 VGPRs)
+constexpr int kGvRing2 = 2;  // gate/up tile pairs
 constexpr int kGvWavesPerCu = 28;  // planned waves per CU
 
 // NT: weight tiles per wave (2 = a gate/up pair, SW epilogue); AM: activation
@@ -295,26 +295,23 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   }
 }
 
-// Up to 4 k-blocks per wave, few registers, many resident waves: one scale
-// group per k-block and bf16 activations fit 64 VGPRs (8 waves per SIMD);
-// two activation planes or small groups 72 (7), both 80 (6).
-template <int NT, int AM, int GPB>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void gemv_kernel_lean8(
-    GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4, GPB>(a);
-}
-template <int NT, int AM, int GPB>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(7))) void gemv_kernel_lean7(
-    GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4, GPB>(a);
-}
-template <int NT, int AM, int GPB>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(6))) void gemv_kernel_lean6(
-    GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRingLean2 : kGvRing1, 4, GPB>(a);
-}
+// Waves per SIMD each instantiation is compiled for (its VGPR budget: 512 /
+// waves, rounded down to 8): the plan's 28 waves per CU are 7 per SIMD.  Up to
+// 4 k-blocks per wave with one scale group and one activation plane fit 64
+// VGPRs (8); each of two planes and small groups costs one wave less; 8
+// k-blocks fit 72 (7), or 80 (6) for a gate/up pair over two planes; 16 fit 80
+// (96 for that pair).
 template <int NT, int AM, int KPWM, int GPB>
-__global__ __launch_bounds__(1024) void gemv_kernel(GvParams a) {
+constexpr int gv_waves_per_simd() {
+  constexpr bool two = AM == A_XF32 || AM == A_HILO;
+  if constexpr (KPWM == 4) return 8 - (two ? 1 : 0) - (GPB > 1 ? 1 : 0);
+  if constexpr (KPWM == 8) return 7 - (two && NT == 2 ? 1 : 0);
+  return two && NT == 2 ? 5 : 6;
+}
+
+template <int NT, int AM, int KPWM, int GPB>
+__global__ __launch_bounds__(1024) __attribute__((
+    amdgpu_waves_per_eu(gv_waves_per_simd<NT, AM, KPWM, GPB>()))) void gemv_kernel(GvParams a) {
   gemv_body<NT, AM, NT == 2 ? kGvRing2 : kGvRing1, KPWM, GPB>(a);
 }
 
@@ -403,19 +400,12 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int
   const dim3 grid((a.N + 15) / 16, nch), block(64 * p.kw);
 #define CAI4_GV_G(NT, AM, GPB)                                                             \
   do {                                                                                     \
-    if (p.kpw <= 4) {                                                                      \
-      constexpr int budget = (AM == A_BF16 || AM == A_GATHER ? 0 : 1) + (GPB > 1 ? 1 : 0);  \
-      if constexpr (budget == 0)                                                           \
-        hipLaunchKernelGGL((gemv_kernel_lean8<NT, AM, GPB>), grid, block, lds, st, k);     \
-      else if constexpr (budget == 1)                                                      \
-        hipLaunchKernelGGL((gemv_kernel_lean7<NT, AM, GPB>), grid, block, lds, st, k);     \
-      else                                                                                 \
-        hipLaunchKernelGGL((gemv_kernel_lean6<NT, AM, GPB>), grid, block, lds, st, k);     \
-    } else if (p.kpw <= 8) {                                                               \
+    if (p.kpw <= 4)                                                                        \
+      hipLaunchKernelGGL((gemv_kernel<NT, AM, 4, GPB>), grid, block, lds, st, k);          \
+    else if (p.kpw <= 8)                                                                   \
       hipLaunchKernelGGL((gemv_kernel<NT, AM, 8, GPB>), grid, block, lds, st, k);          \
-    } else if constexpr (GPB == 1) {                                                       \
+    else if constexpr (GPB == 1)                                                           \
       hipLaunchKernelGGL((gemv_kernel<NT, AM, 16, 1>), grid, block, lds, st, k);           \
-    }                                                                                      \
   } while (0)
 #define CAI4_GV(NT, AM)                                \
   do {                                                 \
