@@ -450,6 +450,84 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       return rc;  // no side stream (e.g. first call inside a stream capture): in order on st
     }
   }
+  size_t off[6];
+  expert_blob_sections(L->hidden, L->inter, L->group_size, L->tiling, off);
+  const int G = (int)L->group_size;
+  const cai4::SkinnyDevice d = device_props(dev);
+  // one token: the grouped down of one-row chunks (when the fused down + combine
+  // does not fit one round of workgroups)
+  cai4::SkinnyArgs dn1{};
+  dn1.w0 = L->experts + off[4];
+  dn1.s0 = L->experts + off[5];
+  dn1.x = hi;
+  dn1.x2 = lo;
+  dn1.out = y;
+  dn1.chunks = chunks;
+  dn1.expert_stride = L->expert_stride;
+  dn1.N = H;
+  dn1.K = I;
+  dn1.G = G;
+  dn1.M = k;
+  dn1.ldx = I;
+  dn1.ldo = H;
+  dn1.sdt = (int)L->scale_dtype;
+  dn1.glog2 = glog2_of(G);
+  dn1.tiled = (int)L->tiling;
+  const bool fused1 = T == 1 && cai4::gemv_moe1_down_fused(H, I, G, k, d.num_cus);
+  if (T == 1 && L->tiling == CASCADIA_INT4_TILING_MFMA &&
+      cai4::gemv_moe1_supported(H, I, G, k, E, d.num_cus) &&
+      (fused1 || cai4::gemv_supported(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, 1, k))) {
+    // one token: routing inside the gate/up GEMV, the combine inside the down GEMV
+    cai4::Moe1Args q{};
+    q.gate = L->experts + off[0];
+    q.gate_s = L->experts + off[1];
+    q.up = L->experts + off[2];
+    q.up_s = L->experts + off[3];
+    q.down = L->experts + off[4];
+    q.down_s = L->experts + off[5];
+    q.expert_stride = L->expert_stride;
+    q.x = x;
+    q.route = r;
+    q.E = E;
+    q.top_k = k;
+    q.ids = ids;
+    q.wts = wts;
+    q.pos = pos;
+    q.hi = hi;
+    q.lo = lo;
+    q.residual = residual;
+    q.shared = sh;
+    q.out = out;
+    q.H = H;
+    q.I = I;
+    q.G = G;
+    q.sdt = (int)L->scale_dtype;
+    if (R->mode != CASCADIA_INT4_ROUTE_IDS && !cai4::gemv_moe1_routes(r, E)) {
+      // many experts: route in a launch of its own, the GEMV reads the result
+      if (cai4::moe_route(r, 1, E, ids, wts, st) != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+      q.route.mode = cai4::ROUTE_IDS;
+      q.route.ids = ids;
+      q.route.weights = wts;
+    }
+    const bool fused = fused1;
+    if (!fused) {  // the gate/up launch also leaves one-row chunks for the grouped down
+      q.chunks = chunks;
+      q.row_map = row_map;
+    }
+    if (cai4::gemv_moe1_gate_up(q, d.num_cus, st) != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+    if (fused) {
+      if (!sh) return hip_status(cai4::gemv_moe1_down(q, st));  // combine included
+      // a shared expert: the routed down runs beside it, the sum is finished after the join
+      q.moe_sum = reinterpret_cast<float *>(y);  // [H] f32 fits the [k, H] bf16 region
+      if (cai4::gemv_moe1_down(q, st) != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+      if (join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+      return hip_status(cai4::moe_finish(residual, sh, q.moe_sum, H, out, st));
+    }
+    if (cai4::gemv_launch(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, k, st) != hipSuccess)
+      return CASCADIA_INT4_ERR_DEVICE;
+    if (join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+    return hip_status(cai4::moe_combine(residual, sh, y, pos, wts, 1, H, k, out, st));
+  }
   hipError_t e = hipSuccess;
   if (T <= (uint32_t)cai4::kMoePrepMaxTokens) {
     // small decode batches: routing and grouping in one launch
@@ -466,9 +544,6 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       e = cai4::moe_group(ids, wts, R->threshold, (int)T, E, k, m.ws.chunk_rows,
                           m.ws.max_chunks, pos, row_map, chunks, counts, st);
   }
-  size_t off[6];
-  expert_blob_sections(L->hidden, L->inter, L->group_size, L->tiling, off);
-  const int G = (int)L->group_size;
   if (e == hipSuccess) {
     cai4::SkinnyArgs a{};
     a.w0 = L->experts + off[0];
@@ -493,7 +568,6 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     a.glog2 = glog2_of(G);
     a.tiled = (int)L->tiling;
     // one row per chunk (a decode token over distinct experts): the one-token GEMV
-    const cai4::SkinnyDevice d = device_props(dev);
     if (cai4::gemv_supported(a, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d.num_cus,
                              m.ws.chunk_rows, m.ws.max_chunks))
       e = cai4::gemv_launch(a, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d.num_cus, m.ws.max_chunks,
@@ -520,7 +594,6 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     a.sdt = (int)L->scale_dtype;
     a.glog2 = glog2_of(G);
     a.tiled = (int)L->tiling;
-    const cai4::SkinnyDevice d = device_props(dev);
     if (cai4::gemv_supported(a, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, m.ws.chunk_rows,
                              m.ws.max_chunks))
       e = cai4::gemv_launch(a, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, m.ws.max_chunks, st);

@@ -28,6 +28,8 @@
 // hi plane, 8-15 the lo plane, added at the end.
 #include "gemv.hpp"
 #include "int4_common.hpp"
+#include "moe.hpp"
+#include "moe_route.hpp"
 #include "skinny.hpp"
 
 namespace cai4 {
@@ -59,7 +61,36 @@ struct GvParams {
   const int32_t *row_map;
   size_t expert_stride;
   int ldx, ldo;
+  // one MoE token (MODE 1: routed gate/up; MODE 2: down + weighted combine):
+  // the routing (or given ids) over E experts, top_k slots; MODE 1 writes
+  // ids / weights / pos (slot or -1 under the threshold), MODE 2 reads them
+  MoeRouting route;
+  int E, top_k;
+  int32_t *ids;
+  float *wts;
+  int32_t *pos;
+  const float *residual, *shared;  // MODE 2: out = (residual + shared) + sum_k w_k y_k
+  int moe_partial;                 // MODE 2: out = sum_k w_k y_k only
+  SkinnyChunk *chunks_out;         // MODE 1: [top_k] chunk table of one row per slot, or null
+  int32_t *row_map_out;            // MODE 1: [top_k] (all token 0), or null
 };
+
+// Slot kk of the one token: its expert, weight, position (kk, or -1 when
+// skipped) and, for a grouped launch after this one, its chunk of one row.
+CAI4_DEV void moe1_record(const GvParams &a, int kk, int id, float w, bool keep) {
+  a.ids[kk] = id;
+  a.wts[kk] = w;
+  a.pos[kk] = keep ? kk : -1;
+  if (a.chunks_out) {
+    a.chunks_out[kk] = SkinnyChunk{keep ? id : 0, kk, keep ? 1 : 0, 0};
+    a.row_map_out[kk] = 0;
+  }
+}
+
+// Kernel modes: a plain or grouped GEMV; one MoE token's routed gate/up (the
+// workgroup row = the slot, the routing recomputed by each workgroup); one MoE
+// token's down projections of all its slots with the combine.
+enum GvMode { GV_PLAIN = 0, GV_MOE_GATE_UP = 1, GV_MOE_DOWN = 2 };
 
 constexpr int kGvMaxKpw = 16;
 constexpr int kGvRing1 = 4;  // k-blocks in flight per wave: single tiles
@@ -73,8 +104,9 @@ constexpr int kGvWavesPerCu = 28;  // planned waves per CU
 // 32 or 64, else 1).  With GPB > 1 each MFMA step must cover whole groups: the
 // weight fragment's four dwords are transposed across the four 16-lane rows
 // (step s then holds columns 32 s .. 32 s + 31) and the activations are read
-// to match; every group gets its own seed and scale.
-template <int NT, int AM, int RING, int KPWM, int GPB>
+// to match; every group gets its own seed and scale.  MODE: GvMode; R: routing
+// registers per lane (GV_MOE_GATE_UP; 0: given ids and weights only).
+template <int NT, int AM, int RING, int KPWM, int GPB, int MODE, int R>
 CAI4_DEV void gemv_body(const GvParams &a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr bool two = AM == A_XF32 || AM == A_HILO;  // hi/lo planes
@@ -84,7 +116,10 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KB = a.K >> 7, NG = a.K / a.G;
   const int T = blockIdx.x;          // tile (pair) index
-  const int kb0 = min(wave * a.kpw, KB), kb1 = min(kb0 + a.kpw, KB), nkb = kb1 - kb0;
+  // GV_MOE_DOWN: a.kw waves per slot; slot `slot`, k-range `wis` of it
+  const int slot = MODE == GV_MOE_DOWN ? wave / a.kw : 0;
+  const int wis = MODE == GV_MOE_DOWN ? wave - slot * a.kw : wave;
+  const int kb0 = min(wis * a.kpw, KB), kb1 = min(kb0 + a.kpw, KB), nkb = kb1 - kb0;
   const int rbytes = a.kpw * 256;                // one plane of a wave's slice
   const int wbytes = PL * rbytes + NT * a.kpw * GPB * 32;  // + scales [NT][kpw][GPB][16] u16
   uint8_t *reg = lds + (size_t)wave * wbytes;       // this wave's region
@@ -93,7 +128,59 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   const uint8_t *w0 = a.w0, *w1 = a.w1, *s0 = a.s0, *s1 = a.s1;
   const uint8_t *xp = static_cast<const uint8_t *>(a.x), *xp2 = static_cast<const uint8_t *>(a.x2);
   size_t orow = 0;
-  if (a.chunks) {
+  bool live = true;  // false: this wave's slot is skipped, all its loads read nothing
+  const int nw = blockDim.x >> 6;
+  float *red = reinterpret_cast<float *>(lds + (size_t)nw * wbytes);  // partials [nw - 1][NT][16]
+  if constexpr (MODE == GV_MOE_GATE_UP) {
+    const int k = a.top_k;
+    int e;
+    if constexpr (R == 0) {  // given ids and weights (or another launch's routing)
+      const int kk = blockIdx.y;
+      const int id = a.route.ids[kk];
+      const float w = a.route.weights[kk];
+      // runner.rs:1811: skip w < threshold
+      e = !(w < a.route.threshold) && id >= 0 && id < a.E ? id : -1;
+      if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0 && lane < k) {
+        const int li = a.route.ids[lane];
+        const float lw = a.route.weights[lane];
+        const bool keep = !(lw < a.route.threshold) && li >= 0 && li < a.E;
+        moe1_record(a, lane, li, lw, keep);
+      }
+    } else {  // every workgroup routes the token itself (wave 0), then broadcasts its slot
+      int *bcast = reinterpret_cast<int *>(red + (nw - 1) * NT * 16);  // past the partials
+      if (wave == 0) {
+        int id = 0;
+        float w = 0.f;
+        if (a.route.mode == ROUTE_IDS) {
+          if (lane < k) {
+            id = a.route.ids[lane];
+            w = a.route.weights[lane];
+          }
+        } else {
+          route_token<R>(a.route, 0, a.E, lane, id, w);
+        }
+        const bool keep = !(w < a.route.threshold) && id >= 0 && id < a.E;
+        if (blockIdx.x == 0 && blockIdx.y == 0 && lane < k) moe1_record(a, lane, id, w, keep);
+        if (lane == (int)blockIdx.y) *bcast = keep ? id : -1;
+      }
+      __syncthreads();
+      e = *bcast;
+    }
+    if (e < 0) return;  // the whole workgroup
+    const size_t eo = (size_t)e * a.expert_stride;
+    w0 += eo;
+    s0 += eo;
+    w1 += eo;
+    s1 += eo;
+    orow = (size_t)blockIdx.y * a.ldo;
+  } else if constexpr (MODE == GV_MOE_DOWN) {
+    live = a.pos[slot] >= 0;
+    const size_t eo = live ? (size_t)a.ids[slot] * a.expert_stride : 0;
+    w0 += eo;
+    s0 += eo;
+    xp += (size_t)slot * a.ldx * 2;
+    xp2 += (size_t)slot * a.ldx * 2;
+  } else if (a.chunks) {
     const SkinnyChunk c = a.chunks[blockIdx.y];
     if (c.count == 0) return;  // the whole workgroup
     const size_t eo = (size_t)c.expert * a.expert_stride;
@@ -114,7 +201,7 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   const int nch = nkb * 16;
   u32x4_t xa[KPWM / 4], xb[KPWM / 4];
   {
-    const size_t xbytes = (size_t)a.K * (xf32 ? 4 : 2);
+    const size_t xbytes = live ? (size_t)a.K * (xf32 ? 4 : 2) : 0;
     const buf_rsrc_t r0 = buf_rsrc(xp, xbytes);
     const buf_rsrc_t r1 = buf_rsrc(AM == A_HILO ? xp2 : xp, xbytes);
 #pragma unroll
@@ -137,8 +224,9 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   uint32_t sv[kSv];
   const int nsv = NT * a.kpw * 8 * GPB;
   {
-    const buf_rsrc_t sr0 = buf_rsrc(s0 + (size_t)T * NG * 32, (size_t)NG * 32);
-    const buf_rsrc_t sr1 = buf_rsrc(NT == 2 ? s1 + (size_t)T * NG * 32 : s0, (size_t)NG * 32);
+    const size_t sbytes = live ? (size_t)NG * 32 : 0;
+    const buf_rsrc_t sr0 = buf_rsrc(s0 + (size_t)T * NG * 32, sbytes);
+    const buf_rsrc_t sr1 = buf_rsrc(NT == 2 ? s1 + (size_t)T * NG * 32 : s0, sbytes);
     const int per = a.kpw * 8 * GPB;  // pieces per tile
 #pragma unroll
     for (int i = 0; i < kSv; ++i) {
@@ -152,8 +240,9 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   }
 
   // ---- weight ring ----
-  const buf_rsrc_t wr0 = buf_rsrc(w0 + (size_t)T * KB * 1024, (size_t)KB * 1024);
-  const buf_rsrc_t wr1 = buf_rsrc(NT == 2 ? w1 + (size_t)T * KB * 1024 : w0, (size_t)KB * 1024);
+  const size_t wbytes_t = live ? (size_t)KB * 1024 : 0;
+  const buf_rsrc_t wr0 = buf_rsrc(w0 + (size_t)T * KB * 1024, wbytes_t);
+  const buf_rsrc_t wr1 = buf_rsrc(NT == 2 ? w1 + (size_t)T * KB * 1024 : w0, wbytes_t);
   u32x4_t ring[RING][NT];
   auto issue = [&](int u, int kb) {  // kb past the slice: dead loads (no data moves)
     const uint32_t wo = kb < kb1 ? (uint32_t)kb * 1024 + 16 * lane : kBufOOB;
@@ -262,8 +351,31 @@ CAI4_DEV void gemv_body(const GvParams &a) {
     }
   }
 
+  if constexpr (MODE == GV_MOE_DOWN) {
+    // ---- every slot's partials -> y_k (RNE bf16) -> the combine in slot order
+    // (runner.rs:1806-1832: moe += w * y, multiply then add; h = residual +
+    // shared + moe), as moe_combine_kernel does for more tokens ----
+    if (lane < 16) red[wave * 16 + lr] = acc[0];
+    __syncthreads();
+    if (wave > 0 || lane >= 16) return;
+    const int r16 = 16 * T + lr;
+    if (r16 >= a.N) return;
+    float h = a.residual ? a.residual[r16] : 0.f;
+    if (a.shared) h = __fadd_rn(h, a.shared[r16]);
+    float moe = 0.f;
+    for (int kk = 0; kk < a.top_k; ++kk) {
+      if (a.pos[kk] < 0) continue;
+      float y = 0.f;
+      for (int v = 0; v < a.kw; ++v) y += red[(kk * a.kw + v) * 16 + lr];
+      moe = __fadd_rn(moe, __fmul_rn(a.wts[kk], bf16_to_f32(f32_to_bf16_rne(y))));
+    }
+    // the whole combine, or the weighted expert sum only (residual and shared
+    // added later, in the same order)
+    reinterpret_cast<float *>(a.out)[r16] = a.moe_partial ? moe : __fadd_rn(h, moe);
+    return;
+  }
+
   // ---- the kw partials (D row 0: lanes 0-15), added in wave order ----
-  float *red = reinterpret_cast<float *>(lds + (size_t)a.kw * wbytes);
   if (wave > 0 && lane < 16) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) red[((wave - 1) * NT + nt) * 16 + lr] = acc[nt];
@@ -300,19 +412,20 @@ CAI4_DEV void gemv_body(const GvParams &a) {
 // 4 k-blocks per wave with one scale group and one activation plane fit 64
 // VGPRs (8); each of two planes and small groups costs one wave less; 8
 // k-blocks fit 72 (7), or 80 (6) for a gate/up pair over two planes; 16 fit 80
-// (96 for that pair).
-template <int NT, int AM, int KPWM, int GPB>
+// (96 for that pair); the routed gate/up with small groups takes one wave less.
+template <int NT, int AM, int KPWM, int GPB, int MODE, int R>
 constexpr int gv_waves_per_simd() {
   constexpr bool two = AM == A_XF32 || AM == A_HILO;
-  if constexpr (KPWM == 4) return 8 - (two ? 1 : 0) - (GPB > 1 ? 1 : 0);
-  if constexpr (KPWM == 8) return 7 - (two && NT == 2 ? 1 : 0);
+  constexpr int routed = MODE == GV_MOE_GATE_UP && R > 0 && GPB > 1 ? 1 : 0;  // routing registers
+  if constexpr (KPWM == 4) return 8 - (two ? 1 : 0) - (GPB > 1 ? 1 : 0) - routed;
+  if constexpr (KPWM == 8) return 7 - (two && NT == 2 ? 1 : 0) - routed;
   return two && NT == 2 ? 5 : 6;
 }
 
-template <int NT, int AM, int KPWM, int GPB>
+template <int NT, int AM, int KPWM, int GPB, int MODE = GV_PLAIN, int R = 1>
 __global__ __launch_bounds__(1024) __attribute__((
-    amdgpu_waves_per_eu(gv_waves_per_simd<NT, AM, KPWM, GPB>()))) void gemv_kernel(GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRing2 : kGvRing1, KPWM, GPB>(a);
+    amdgpu_waves_per_eu(gv_waves_per_simd<NT, AM, KPWM, GPB, MODE, R>()))) void gemv_kernel(GvParams a) {
+  gemv_body<NT, AM, NT == 2 ? kGvRing2 : kGvRing1, KPWM, GPB, MODE, R>(a);
 }
 
 }  // namespace
@@ -342,11 +455,12 @@ bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int ch
   if (n_eff > (1L << 30)) return false;
   const GemvPlan p = gemv_plan((int)n_eff, a.K, num_cus);  // K > 256 KB blocks: kw > 16
   if (gpb > 1 && p.kpw > 8) return false;  // no 16-k-block instantiation for small groups
-  return p.kw <= 16 && gemv_lds_bytes(p, amode, nt, gpb) <= kGvMaxLds;
+  return p.kw >= 1 && p.kw <= 16 && gemv_lds_bytes(p, amode, nt, gpb) <= kGvMaxLds;
 }
 
 GemvPlan gemv_plan(int N, int K, int num_cus) {
   const int tiles = (N + 15) / 16, KB = K / 128;
+  if (KB < 1 || tiles < 1 || num_cus < 1) return GemvPlan{0, 0};  // not supported
   // kGvWavesPerCu waves per CU, all resident at once (the register arrays are
   // sized by the k-blocks per wave): many short independent streams
   const long waves = (long)kGvWavesPerCu * num_cus;
@@ -425,6 +539,146 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int
   }
 #undef CAI4_GV_G
 #undef CAI4_GV
+  return hipGetLastError();
+}
+
+namespace {
+
+// GV_MOE_DOWN: waves per slot and k-blocks per wave (0 waves: not supported).
+GemvPlan moe1_down_plan(int I, int top_k) {
+  const int KB = I / 128, kw = top_k > 0 ? 16 / top_k : 0;
+  if (kw < 1 || KB < 1) return GemvPlan{0, 0};
+  const int kpw = (KB + kw - 1) / kw;
+  return GemvPlan{(KB + kpw - 1) / kpw, kpw};
+}
+
+size_t moe1_down_lds(const GemvPlan &p, int top_k, int gpb) {
+  const int nw = top_k * p.kw;
+  return (size_t)nw * (2 * p.kpw * 256 + p.kpw * gpb * 32) + (size_t)nw * 64 + 16;
+}
+
+}  // namespace
+
+bool gemv_moe1_supported(int H, int I, int G, int top_k, int E, int num_cus) {
+  const int gpb = gemv_gpb(G);
+  if (!gpb || H % 128 || I % 128 || H % G || I % G) return false;
+  if (top_k < 1 || top_k > kMoeMaxTopK || E < 1 || E > kMoeMaxExperts) return false;
+  if ((long)I * top_k > (1L << 30)) return false;
+  const GemvPlan gu = gemv_plan(I * top_k, H, num_cus);
+  if (gu.kw < 1 || gu.kw > 16 || gu.kpw > 8) return false;
+  return gemv_lds_bytes(gu, A_GATHER, 2, gpb) <= kGvMaxLds;
+}
+
+bool gemv_moe1_down_fused(int H, int I, int G, int top_k, int num_cus) {
+  const int gpb = gemv_gpb(G);
+  if (!gpb || H % 128 || I % 128 || H % G || I % G) return false;
+  if ((H + 15) / 16 > num_cus) return false;  // one round of workgroups
+  const GemvPlan dn = moe1_down_plan(I, top_k);
+  if (dn.kw < 1 || dn.kpw > 8) return false;
+  return moe1_down_lds(dn, top_k, gpb) <= kGvMaxLds;
+}
+
+hipError_t gemv_moe1_gate_up(const Moe1Args &m, int num_cus, hipStream_t st) {
+  const int gpb = gemv_gpb(m.G);
+  const GemvPlan p = gemv_plan(m.I * m.top_k, m.H, num_cus);
+  GvParams k{};
+  k.w0 = m.gate;
+  k.s0 = m.gate_s;
+  k.w1 = m.up;
+  k.s1 = m.up_s;
+  k.x = m.x;
+  k.x2 = m.x;
+  k.out = m.hi;
+  k.out2 = m.lo;
+  k.N = m.I;
+  k.K = m.H;
+  k.G = m.G;
+  k.sdt = m.sdt;
+  k.epi = EPI_SWIGLU_HILO;
+  k.kw = p.kw;
+  k.kpw = p.kpw;
+  k.expert_stride = m.expert_stride;
+  k.ldx = m.H;
+  k.ldo = m.I;
+  k.route = m.route;
+  k.E = m.E;
+  k.top_k = m.top_k;
+  k.ids = m.ids;
+  k.wts = m.wts;
+  k.pos = m.pos;
+  k.chunks_out = m.chunks;
+  k.row_map_out = m.row_map;
+  const size_t lds = gemv_lds_bytes(p, A_GATHER, 2, gpb);
+  const dim3 grid((m.I + 15) / 16, m.top_k), block(64 * p.kw);
+#define CAI4_GVR(KP, GP, R) \
+  hipLaunchKernelGGL((gemv_kernel<2, A_GATHER, KP, GP, GV_MOE_GATE_UP, R>), grid, block, lds, st, k)
+#define CAI4_GVR_E(KP, GP)                                    \
+  do {                                                        \
+    if (m.route.mode != ROUTE_IDS && m.E <= 256) CAI4_GVR(KP, GP, 4); \
+    else CAI4_GVR(KP, GP, 0);                                 \
+  } while (0)
+#define CAI4_GVR_K(GP)                        \
+  do {                                        \
+    if (p.kpw <= 4) CAI4_GVR_E(4, GP);        \
+    else CAI4_GVR_E(8, GP);                   \
+  } while (0)
+  if (gpb == 4) CAI4_GVR_K(4);
+  else if (gpb == 2) CAI4_GVR_K(2);
+  else CAI4_GVR_K(1);
+#undef CAI4_GVR_K
+#undef CAI4_GVR_E
+#undef CAI4_GVR
+  return hipGetLastError();
+}
+
+hipError_t gemv_moe1_down(const Moe1Args &m, hipStream_t st) {
+  const int gpb = gemv_gpb(m.G);
+  const GemvPlan p = moe1_down_plan(m.I, m.top_k);
+  GvParams k{};
+  k.w0 = m.down;
+  k.s0 = m.down_s;
+  k.w1 = m.down;
+  k.s1 = m.down_s;
+  k.x = m.hi;
+  k.x2 = m.lo;
+  k.out = m.out;
+  k.N = m.H;
+  k.K = m.I;
+  k.G = m.G;
+  k.sdt = m.sdt;
+  k.epi = EPI_F32;
+  k.kw = p.kw;
+  k.kpw = p.kpw;
+  k.expert_stride = m.expert_stride;
+  k.ldx = m.I;
+  k.ldo = m.H;
+  k.E = m.E;
+  k.top_k = m.top_k;
+  k.ids = m.ids;
+  k.wts = m.wts;
+  k.pos = m.pos;
+  k.residual = m.residual;
+  k.shared = m.shared;
+  if (m.moe_sum) {  // the weighted expert sum only (a shared expert finishes later)
+    k.out = m.moe_sum;
+    k.residual = nullptr;
+    k.shared = nullptr;
+    k.moe_partial = 1;
+  }
+  const size_t lds = moe1_down_lds(p, m.top_k, gpb);
+  const dim3 grid((m.H + 15) / 16), block(64 * m.top_k * p.kw);
+#define CAI4_GVD(KP, GP) \
+  hipLaunchKernelGGL((gemv_kernel<1, A_HILO, KP, GP, GV_MOE_DOWN, 1>), grid, block, lds, st, k)
+#define CAI4_GVD_K(GP)               \
+  do {                               \
+    if (p.kpw <= 4) CAI4_GVD(4, GP); \
+    else CAI4_GVD(8, GP);            \
+  } while (0)
+  if (gpb == 4) CAI4_GVD_K(4);
+  else if (gpb == 2) CAI4_GVD_K(2);
+  else CAI4_GVD_K(1);
+#undef CAI4_GVD_K
+#undef CAI4_GVD
   return hipGetLastError();
 }
 

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "moe.hpp"
 #include "skinny.hpp"
 
 namespace cai4 {
@@ -21,5 +22,40 @@ bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int ch
 GemvPlan gemv_plan(int N, int K, int num_cus);
 hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int max_chunks,
                        hipStream_t st);
+
+// One MoE token (T = 1) over MFMA-tiled experts, in two launches: the gate/up
+// of every slot (each workgroup recomputes the token's routing for up to 256
+// experts, or reads the ids and weights in route -- given, or left by
+// moe_route; writes ids / weights / pos and the SwiGLU hi/lo rows per slot),
+// then the down projections of all slots with the weighted combine.  With
+// moe_sum set the second launch writes only the weighted expert sum there (no
+// residual, no shared term: moe_finish adds them); else the shared expert's
+// output must be complete before it.
+struct Moe1Args {
+  const uint8_t *gate, *gate_s, *up, *up_s, *down, *down_s;  // expert 0's sections
+  size_t expert_stride;
+  const float *x;  // [H]
+  MoeRouting route;
+  int E, top_k;
+  int32_t *ids;
+  float *wts;
+  int32_t *pos;
+  uint16_t *hi, *lo;               // [top_k, I] each
+  const float *residual, *shared;  // [H] or null
+  float *out;                      // [H]
+  float *moe_sum;                  // [H] or null
+  SkinnyChunk *chunks;             // [top_k] one-row chunks for a grouped down launch, or null
+  int32_t *row_map;                // [top_k], with chunks
+  int H, I, G, sdt;
+};
+// Whether the gate/up launch routes in-kernel (else route must hold ids).
+inline bool gemv_moe1_routes(const MoeRouting &r, int E) { return r.mode != ROUTE_IDS && E <= 256; }
+bool gemv_moe1_supported(int H, int I, int G, int top_k, int E, int num_cus);
+// Whether the down + combine launch fits (its workgroups of top_k slots each
+// cover one 16-row tile; more tiles than CUs would run in two rounds: then
+// the grouped down GEMV over the chunk table and the combine kernel instead).
+bool gemv_moe1_down_fused(int H, int I, int G, int top_k, int num_cus);
+hipError_t gemv_moe1_gate_up(const Moe1Args &m, int num_cus, hipStream_t st);
+hipError_t gemv_moe1_down(const Moe1Args &m, hipStream_t st);
 
 }  // namespace cai4

@@ -20,6 +20,7 @@
 
 #include "int4_common.hpp"
 #include "moe.hpp"
+#include "moe_route.hpp"
 
 namespace cai4 {
 
@@ -68,111 +69,8 @@ MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows
 }
 
 // ---------------------------------------------------------------------------
-// routing: one wave per token
+// routing: one wave per token (route_token: moe_route.hpp)
 // ---------------------------------------------------------------------------
-
-// Wave-wide max of a float, in every lane: DPP within 16-lane rows (xor 1,
-// xor 2, rotate 4, rotate 8), then row pairs and halves by permlane swaps --
-// no LDS round trips.
-template <int CTRL>
-CAI4_DEV float dpp_move(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
-                                                               0xF, 0xF, false));
-}
-CAI4_DEV float wave_max_f32(float v) {
-  v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm 1,0,3,2
-  v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm 2,3,0,1
-  v = fmaxf(v, dpp_move<0x124>(v));  // row_ror 4
-  v = fmaxf(v, dpp_move<0x128>(v));  // row_ror 8
-  auto a = __builtin_amdgcn_permlane16_swap(fbits(v), fbits(v), false, false);
-  v = fmaxf(bitsf(a[0]), bitsf(a[1]));
-  auto b = __builtin_amdgcn_permlane32_swap(fbits(v), fbits(v), false, false);
-  return fmaxf(bitsf(b[0]), bitsf(b[1]));
-}
-
-CAI4_DEV float lane_f32(float v, int l) {
-  return bitsf(__builtin_amdgcn_readlane(fbits(v), l));
-}
-
-// Selections of token t in one wave.  Lane l holds experts l * nj .. l * nj +
-// nj - 1, so the lowest lane holding a maximum holds the lowest expert id of
-// it.  Each of the k rounds takes the lane-local best (lowest j among equal
-// keys), a wave-wide max, and the lowest lane whose best equals it.  NaN keys
-// never win.  Lane kk < k returns selection kk: its expert and weight.
-template <int R>  // R >= ceil(E / 64): registers per lane
-CAI4_DEV void route_token(const MoeRouting &r, int t, int E, int lane, int &id_out,
-                          float &w_out) {
-  const bool sig = r.mode == ROUTE_SIGMOID_BIAS;
-  const int nj = (E + 63) >> 6;
-  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float *>(r.logits + (size_t)t * E), (short)0, E * 4, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float *>(r.bias), (short)0, r.bias ? E * 4 : 0, 0x00020000);
-  float key[R], val[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    key[j] = -INFINITY;
-    val[j] = 0.f;
-    if (j < nj) {  // uniform
-      const uint32_t off = (uint32_t)(lane * nj + j) * 4;
-      const float lg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, 0));
-      const float bs = sig ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0)) : 0.f;
-      const float sv = sig ? 1.0f / (1.0f + expf(-lg)) : lg;
-      const float c = sig ? sv + bs : sv;
-      val[j] = sv;
-      key[j] = c != c ? -INFINITY : c;
-    }
-  }
-  uint32_t valid = 0;  // experts of this lane that exist and are not yet taken
-#pragma unroll
-  for (int j = 0; j < R; ++j)
-    if (j < nj && lane * nj + j < E) valid |= 1u << j;
-  int my_id = 0;
-  float my_val = 0.f;
-  for (int kk = 0; kk < r.top_k; ++kk) {
-    float best = -INFINITY, bval = 0.f;
-    int bj = -1;
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      if (((valid >> j) & 1u) && (bj < 0 || key[j] > best)) {
-        best = key[j];
-        bval = val[j];
-        bj = j;
-      }
-    }
-    const float m = wave_max_f32(bj < 0 ? -INFINITY : best);
-    const uint64_t hit = __ballot(bj >= 0 && best == m);
-    const int sl = __builtin_amdgcn_readfirstlane(__builtin_ffsll((long long)hit) - 1);
-    const int sj = __builtin_amdgcn_readlane(bj, sl);
-    const float sv = lane_f32(bval, sl);
-    if (lane == sl) valid &= ~(1u << sj);
-    if (lane == kk) {
-      my_id = sl * nj + sj;
-      my_val = sv;
-    }
-  }
-  // weights, summed in selection order as the crate does
-  const int k = r.top_k;
-  float w;
-  if (sig) {
-    if (r.normalize && k > 1) {
-      float s = 0.0f;
-      for (int kk = 0; kk < k; ++kk) s += lane_f32(my_val, kk);
-      s += 1.0e-20f;
-      w = my_val / s * r.scale;
-    } else {
-      w = my_val * r.scale;
-    }
-  } else {
-    const float mx = lane_f32(my_val, 0);
-    const float ex = expf(my_val - mx);
-    float s = 0.0f;
-    for (int kk = 0; kk < k; ++kk) s += lane_f32(ex, kk);
-    w = ex / s;
-  }
-  id_out = my_id;
-  w_out = w;
-}
 
 template <int R>
 __global__ __launch_bounds__(256) void moe_route_kernel(MoeRouting r, int T, int E, int32_t *ids,
@@ -438,6 +336,25 @@ hipError_t moe_combine(const float *residual, const float *shared, const uint16_
   const int per_block = 256 * 4;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((H + per_block - 1) / per_block, T), dim3(256), 0,
                      st, residual, shared, y, pos, w, H, top_k, out);
+  return hipGetLastError();
+}
+
+// out = (residual + shared) + moe, per element: the combine's last two adds
+// when the weighted expert sum `moe` came from another kernel.
+__global__ __launch_bounds__(256) void moe_finish_kernel(const float *residual,
+                                                         const float *shared, const float *moe,
+                                                         int H, float *out) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= H) return;
+  float h = residual ? residual[j] : 0.f;
+  if (shared) h = __fadd_rn(h, shared[j]);
+  out[j] = __fadd_rn(h, moe[j]);
+}
+
+hipError_t moe_finish(const float *residual, const float *shared, const float *moe, int H,
+                      float *out, hipStream_t st) {
+  hipLaunchKernelGGL(moe_finish_kernel, dim3((H + 255) / 256), dim3(256), 0, st, residual, shared,
+                     moe, H, out);
   return hipGetLastError();
 }
 

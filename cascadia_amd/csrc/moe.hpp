@@ -53,5 +53,8 @@ hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T,
 hipError_t moe_combine(const float *residual, const float *shared, const uint16_t *y,
                        const int32_t *pos, const float *w, int T, int H, int top_k, float *out,
                        hipStream_t st);
+// One token: out = (residual + shared) + moe (residual / shared may be null).
+hipError_t moe_finish(const float *residual, const float *shared, const float *moe, int H,
+                      float *out, hipStream_t st);
 
 }  // namespace cai4

@@ -196,6 +196,74 @@ def test_moe_one_token_g128(cl, orc, mode, shared_inter, thr):
         assert (w < thr).any(), "threshold case should skip some slots"
 
 
+@pytest.mark.parametrize("k,thr", [(6, 0.0), (6, 0.3), (16, 0.0)])
+def test_moe_one_token_given_ids(cl, orc, k, thr):
+    """One token, given ids with repeats (one expert in several slots), tiled
+    G128 experts: each slot is its own row; slots under the threshold skipped;
+    top-k 16 leaves one wave per slot in the down + combine launch."""
+    E, h, i, g, T = 20, 384, 256, 128, 1
+    blob, shared, ex = build(cl, orc, E, h, i, g, F16, 23, 128, True)
+    rng = np.random.default_rng(k)
+    ids = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    ids[0, 1] = ids[0, 0]
+    ids[0, 3] = ids[0, 0]
+    w = rng.random((T, k)).astype(np.float32)
+    x = orc.fill_normal_f32(24, T, T * h).reshape(T, h)
+    xd = dev(x)
+    out = torch.empty((T, h), dtype=torch.float32, device="cuda")
+    cl.moe_forward(ex, xd, out, top_k=k, mode=cl.ROUTE_IDS, ids=dev(ids), weights=dev(w),
+                   threshold=thr, residual=xd)
+    check_layer(orc, host(out), x, blob, shared, 128, E, h, i, g, F16, ids, w, thr,
+                f"one token given ids k={k} thr={thr}")
+
+
+@pytest.mark.parametrize("E,shared_inter,mode", [(300, 128, 1), (300, 0, 2), (40, 128, 1)])
+def test_moe_one_token_routing_launch(cl, orc, E, shared_inter, mode):
+    """One token: more than 256 experts route in a launch of their own (the
+    gate/up GEMV reads its slots), 256 or fewer inside the GEMV; with a shared
+    expert the routed down writes the weighted sum and the finish adds
+    residual + shared after the join."""
+    k, h, i, g, T = 8, 256, 256, 32, 1
+    blob, shared, ex = build(cl, orc, E, h, i, g, F16, 27, shared_inter, True)
+    logits = orc.fill_normal_f32(28, T, T * E).reshape(T, E)
+    bias = orc.fill_normal_f32(29, 1, E) * np.float32(0.1)
+    x = orc.fill_normal_f32(30, T, T * h).reshape(T, h)
+    out = torch.empty((T, h), dtype=torch.float32, device="cuda")
+    ids_o = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w_o = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    xd = dev(x)
+    kw = dict(bias=dev(bias), scale=2.5, normalize=True) if mode == 1 else {}
+    cl.moe_forward(ex, xd, out, top_k=k, logits=dev(logits), mode=mode, residual=xd,
+                   ids_out=ids_o, weights_out=w_o, **kw)
+    ids, w = host(ids_o), host(w_o)
+    want_ids, want_w = route_oracle(orc, logits, bias if mode == 1 else None, k, mode,
+                                    2.5 if mode == 1 else 1.0, True)
+    assert np.array_equal(ids, want_ids), "routing ids differ"
+    check_layer(orc, host(out), x, blob, shared, shared_inter, E, h, i, g, F16, ids, w, 0.0,
+                f"one token E={E} shared={shared_inter} mode={mode}")
+
+
+@pytest.mark.parametrize("E,h,i,g,mode", [(24, 7168, 2048, 32, 1), (260, 4608, 128, 128, 1)])
+def test_moe_one_token_wide_hidden(cl, orc, E, h, i, g, mode):
+    """One token with more 16-row output tiles than CUs (hidden > 4096): the
+    gate/up launch leaves a chunk table of one row per slot, the grouped down
+    and the combine kernel follow; config 4 dims (G32, shared expert) on a
+    24-expert subset, and 260 experts (routing in a launch of its own)."""
+    k, T, si = 8, 1, 256
+    blob, shared, ex = build(cl, orc, E, h, i, g, F16, 33, si, True)
+    logits = orc.fill_normal_f32(34, T, T * E).reshape(T, E)
+    bias = orc.fill_normal_f32(35, 1, E) * np.float32(0.1)
+    x = orc.fill_normal_f32(36, T, T * h).reshape(T, h)
+    out = torch.empty((T, h), dtype=torch.float32, device="cuda")
+    ids_o = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w_o = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    xd = dev(x)
+    cl.moe_forward(ex, xd, out, top_k=k, logits=dev(logits), bias=dev(bias), mode=mode,
+                   scale=2.827, normalize=True, residual=xd, ids_out=ids_o, weights_out=w_o)
+    check_layer(orc, host(out), x, blob, shared, si, E, h, i, g, F16, host(ids_o), host(w_o),
+                0.0, f"one token E={E} h={h}")
+
+
 @pytest.mark.parametrize("T", [24, 70])
 def test_moe_given_ids_and_determinism(cl, orc, T):
     """ROUTE_IDS with repeated experts across tokens; two calls bit-identical."""
