@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--profile-prefill", action="store_true",
                     help="launch the config 2 prefill GEMMs eagerly, without timing, for rocprofv3")
     ap.add_argument("--profile-moe", action="store_true",
-                    help="run configs 3 and 4 at T=1 (a few steps), for rocprofv3")
+                    help="run configs 3 and 4 at T=--moe-tokens (a few steps), for rocprofv3")
+    ap.add_argument("--moe-tokens", type=int, default=1, help="tokens of --profile-moe")
     ap.add_argument("--profile", action="store_true",
                     help="launch the headline kernels and a 256 MiB copy (counter calibration) "
                          "eagerly, without timing, for rocprofv3")
@@ -340,11 +341,13 @@ def main():
               flush=True)
         return
     if args.profile_moe:
-        r3 = bench_moe(cl, torch, "config3", 256, 3072, 1536, 128, 8, 1, 1,
+        T = args.moe_tokens
+        r3 = bench_moe(cl, torch, "config3", 256, 3072, 1536, 128, 8, T, 1,
                        cl.ROUTE_SOFTMAX_TOPK, 1.0, 0, 50, nsets=16)
-        r4 = bench_moe(cl, torch, "config4", 384, 7168, 2048, 32, 8, 1, 4, cl.ROUTE_SIGMOID_BIAS,
+        r4 = bench_moe(cl, torch, "config4", 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS,
                        2.827, 2048, 20, zipf=1.1, nsets=16)
-        print(json.dumps({"profile": "moe", "config3_T1": r3, "config4_T1": r4}), flush=True)
+        print(json.dumps({"profile": "moe", f"config3_T{T}": r3, f"config4_T{T}": r4}),
+              flush=True)
         return
     h, i, g, m = 4096, 14336, 128, args.m
     per_copy = cl.expert_bytes(h, i, g)
