@@ -304,7 +304,10 @@ int run_prefill(const cascadia_int4_layout *L, const uint8_t *packed, const uint
   if (int rc = current_device(&dev)) return rc;
   if ((size_t)M * L->k_cols * 2 >= 0x7FFFFFFFu) return CASCADIA_INT4_ERR_ARG;
   void *ws = nullptr;
-  if (int rc = lib_workspace(dev, cai4::prefill_workspace_bytes((int)M, (int)L->k_cols), &ws))
+  if (int rc = lib_workspace(dev,
+                             cai4::prefill_workspace_bytes((int)M, (int)L->n_rows, (int)L->k_cols,
+                                                           device_props(dev).num_cus),
+                             &ws))
     return rc;
   return hip_status(cai4::prefill_gemm(packed, scales, x, y, (int)M, (int)L->n_rows,
                                        (int)L->k_cols, (int)L->group_size, (int)L->scale_dtype,

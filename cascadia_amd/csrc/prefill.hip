@@ -90,6 +90,8 @@ struct PfArgs {
   const float *xs;    // seeds [KB][Mp]: -136 * sum of x over each k-block
   void *y;            // [M, N] bf16 or f32
   int M, N, K, G, sdt, out_f32, Mp;
+  int kper;           // k-blocks per workgroup slice of K (blockIdx.z)
+  float *part;        // ksplit > 1: f32 partial sums [ksplit][M][N], else null
 };
 
 // Seeds: xs[kb][m] = -136 * sum_{c < 128} x[m, 128 kb + c] (f32, fixed order:
@@ -188,12 +190,13 @@ struct PfNext {
   uint8_t *buf;
   rsrc_t xr, wr, sr, qr;
   int K, KB, NG, G, Mp, kb, wave, lane;
+  int KE;  // end of the workgroup's k-blocks (KB: the tile stride of the weights)
 };
 
 // Issue the loads of part `part` (of 8): loads [part L / 8, (part + 1) L / 8).
 template <class P>
 CAI4_DEV void pf_issue_part(const PfNext &n, int part) {
-  if (n.kb < n.KB) {
+  if (n.kb < n.KE) {
 #pragma unroll
     for (int l = 0; l < P::LOADS; ++l)
       if (l >= part * P::LOADS / 8 && l < (part + 1) * P::LOADS / 8)
@@ -261,17 +264,17 @@ CAI4_DEV void pf_compute(const uint8_t *buf, int wm, int wn, int lane, int sdt, 
 // One stage: k-block kb from `cur`; the loads of kb + 2 go into `nxt2`.
 template <class P, int MS, int NT>
 CAI4_DEV void pf_stage(uint8_t *cur, uint8_t *nxt2, rsrc_t xr, rsrc_t wr, rsrc_t sr, rsrc_t qr,
-                       const PfArgs &a, int KB, int NG, int kb, int wave, int wm, int wn,
+                       const PfArgs &a, int KB, int KE, int NG, int kb, int wave, int wm, int wn,
                        int lane, f32x4_t (&acc)[MS][NT]) {
-  if (kb >= KB) return;  // uniform
+  if (kb >= KE) return;  // uniform
   // this wave's loads of kb are done once only kb + 1's may still be in
   // flight (loads complete in order); after the barrier every wave's have
   // landed
-  if (kb + 1 < KB)
+  if (kb + 1 < KE)
     pf_wait_barrier<P::LOADS>();
   else
     pf_wait_barrier<0>();
-  const PfNext nx{nxt2, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, kb + 2, wave, lane};
+  const PfNext nx{nxt2, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, kb + 2, wave, lane, KE};
   pf_compute<P, MS, NT>(cur, wm, wn, lane, a.sdt, nx, acc);
 }
 
@@ -301,18 +304,20 @@ __global__ __launch_bounds__(64 * WM * WN) void pf_gemm_kernel(PfArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // this workgroup's k-blocks [kb0, KE): all of K, or slice blockIdx.z of it
+  const int kb0 = blockIdx.z * a.kper, KE = min(KB, kb0 + a.kper);
 #pragma unroll
   for (int l = 0; l < P::LOADS; ++l)
-    pf_load<P>(l, st0, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, 0, wave, lane);
-  if (KB > 1) {
+    pf_load<P>(l, st0, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, kb0, wave, lane);
+  if (kb0 + 1 < KE) {
 #pragma unroll
     for (int l = 0; l < P::LOADS; ++l)
-      pf_load<P>(l, st1, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, 1, wave, lane);
+      pf_load<P>(l, st1, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, kb0 + 1, wave, lane);
   }
-  for (int kb = 0; kb < KB; kb += 3) {
-    pf_stage<P, MS, NT>(st0, st2, xr, wr, sr, qr, a, KB, NG, kb, wave, wm, wn, lane, acc);
-    pf_stage<P, MS, NT>(st1, st0, xr, wr, sr, qr, a, KB, NG, kb + 1, wave, wm, wn, lane, acc);
-    pf_stage<P, MS, NT>(st2, st1, xr, wr, sr, qr, a, KB, NG, kb + 2, wave, wm, wn, lane, acc);
+  for (int kb = kb0; kb < KE; kb += 3) {
+    pf_stage<P, MS, NT>(st0, st2, xr, wr, sr, qr, a, KB, KE, NG, kb, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT>(st1, st0, xr, wr, sr, qr, a, KB, KE, NG, kb + 1, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT>(st2, st1, xr, wr, sr, qr, a, KB, KE, NG, kb + 2, wave, wm, wn, lane, acc);
   }
 
   // epilogue: D lane l holds column l % 16 and rows 4 * (l / 16) + v
@@ -327,7 +332,9 @@ __global__ __launch_bounds__(64 * WM * WN) void pf_gemm_kernel(PfArgs a) {
         const int m = m0 + wm * P::RM + 16 * i + 4 * lg + v;
         if (m >= a.M) continue;
         const size_t o = (size_t)m * a.N + n;
-        if (a.out_f32)
+        if (a.part)  // a slice of K: the f32 partial, summed by pf_reduce_kernel
+          a.part[(size_t)blockIdx.z * a.M * a.N + o] = acc[i][j][v];
+        else if (a.out_f32)
           reinterpret_cast<float *>(a.y)[o] = acc[i][j][v];
         else
           reinterpret_cast<uint16_t *>(a.y)[o] = (uint16_t)f32_to_bf16_rne(acc[i][j][v]);
@@ -336,13 +343,50 @@ __global__ __launch_bounds__(64 * WM * WN) void pf_gemm_kernel(PfArgs a) {
   }
 }
 
+// y = sum over the ksplit partials, in slice order; bf16 (RNE) or f32.
+__global__ __launch_bounds__(256) void pf_reduce_kernel(const float *part, void *y, size_t n,
+                                                        int ksplit, int out_f32) {
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;  // n is a multiple of 4
+  f32x4_t s = *reinterpret_cast<const f32x4_t *>(part + i);
+  for (int z = 1; z < ksplit; ++z) s += *reinterpret_cast<const f32x4_t *>(part + z * n + i);
+  if (out_f32) {
+    *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(y) + i) = s;
+  } else {
+    u32x2_t o;
+    o.x = f32_to_bf16_rne(s.x) | (f32_to_bf16_rne(s.y) << 16);
+    o.y = f32_to_bf16_rne(s.z) | (f32_to_bf16_rne(s.w) << 16);
+    *reinterpret_cast<u32x2_t *>(reinterpret_cast<uint16_t *>(y) + i) = o;
+  }
+}
+
 template <int MS, int NT, int WM, int WN>
-hipError_t pf_launch(const PfArgs &a, hipStream_t st) {
+hipError_t pf_launch(const PfArgs &a, int ksplit, hipStream_t st) {
   using P = Pf<MS, NT, WM, WN>;
   hipLaunchKernelGGL((pf_gemm_kernel<MS, NT, WM, WN>),
-                     dim3((a.N + P::BN - 1) / P::BN, (a.M + P::BM - 1) / P::BM), dim3(64 * P::W),
-                     0, st, a);
-  return hipGetLastError();
+                     dim3((a.N + P::BN - 1) / P::BN, (a.M + P::BM - 1) / P::BM, ksplit),
+                     dim3(64 * P::W), 0, st, a);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (ksplit > 1) {
+    const size_t n = (size_t)a.M * a.N;
+    hipLaunchKernelGGL(pf_reduce_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st,
+                       a.part, a.y, n, ksplit, a.out_f32);
+    return hipGetLastError();
+  }
+  return hipSuccess;
+}
+
+// K slices for the 128 x 256 tile: enough workgroups to cover 7/8 of the CUs,
+// at most 4 slices of at least 6 k-blocks (the three-stage pipeline); 0: none
+// fits (smaller tiles instead).  1: no split.
+int pf_ksplit(int M, int N, int K, int num_cus) {
+  const long tiles = (long)((N + 255) / 256) * ((M + 127) / 128);
+  const int KB = K / 128;
+  for (int s = 1; s <= 4; ++s) {
+    if (s > 1 && (KB / s < 6 || (long)M * N % 4)) break;
+    if (8 * tiles * s >= 7L * num_cus) return s;
+  }
+  return 0;
 }
 
 int pf_rows_padded(int M) { return (M + 127) / 128 * 128; }
@@ -353,7 +397,11 @@ bool prefill_supported(int M, int N, int K, int G, int tiled) {
   return tiled && M >= 64 && K % 128 == 0 && G % 128 == 0 && N >= 16;
 }
 
-size_t prefill_workspace_bytes(int M, int K) { return (size_t)(K / 128) * pf_rows_padded(M) * 4; }
+size_t prefill_workspace_bytes(int M, int N, int K, int num_cus) {
+  const int ks = pf_ksplit(M, N, K, num_cus);
+  const size_t seeds = (((size_t)(K / 128) * pf_rows_padded(M) * 4) + 255) & ~(size_t)255;
+  return seeds + (ks > 1 ? (size_t)ks * M * N * 4 : 0);
+}
 
 hipError_t prefill_gemm(const uint8_t *w, const uint8_t *s, const uint16_t *x, void *y, int M,
                         int N, int K, int G, int sdt, int out_f32, void *ws, int num_cus,
@@ -361,12 +409,19 @@ hipError_t prefill_gemm(const uint8_t *w, const uint8_t *s, const uint16_t *x, v
   const int Mp = pf_rows_padded(M);
   float *xs = static_cast<float *>(ws);
   hipLaunchKernelGGL(pf_xsum_kernel, dim3(Mp / 4), dim3(256), 0, st, x, xs, M, K, Mp);
-  const PfArgs a{w, s, x, xs, y, M, N, K, G, sdt, out_f32, Mp};
-  const long tiles_big = (long)((N + 255) / 256) * ((M + 127) / 128);
+  PfArgs a{w, s, x, xs, y, M, N, K, G, sdt, out_f32, Mp, K / 128, nullptr};
+  const int ks = pf_ksplit(M, N, K, num_cus);
+  if (ks >= 1) {  // 128 x 256, 8 waves (in ks slices of K)
+    if (ks > 1) {
+      a.kper = (K / 128 + ks - 1) / ks;
+      const size_t seeds = (((size_t)(K / 128) * Mp * 4) + 255) & ~(size_t)255;
+      a.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + seeds);
+    }
+    return pf_launch<4, 4, 2, 4>(a, (K / 128 + a.kper - 1) / a.kper, st);
+  }
   const long tiles_mid = (long)((N + 127) / 128) * ((M + 127) / 128);
-  if (tiles_big >= num_cus) return pf_launch<4, 4, 2, 4>(a, st);  // 128 x 256, 8 waves
-  if (tiles_mid >= num_cus) return pf_launch<4, 4, 2, 2>(a, st);  // 128 x 128, 4 waves
-  return pf_launch<2, 4, 2, 2>(a, st);                            // 64 x 128, 4 waves
+  if (tiles_mid >= num_cus) return pf_launch<4, 4, 2, 2>(a, 1, st);  // 128 x 128, 4 waves
+  return pf_launch<2, 4, 2, 2>(a, 1, st);                            // 64 x 128, 4 waves
 }
 
 }  // namespace cai4

@@ -329,6 +329,8 @@ def test_prefill_gemm_bf16_small(cl, orc):
 PREFILL_SHAPES = [  # m, n, k, group: ragged M and N, G 128 / 256
     (64, 256, 512, 128), (100, 192, 1024, 128), (300, 4112, 1024, 256), (130, 50, 256, 128),
     (257, 640, 2048, 128),
+    # 128 x 256 tiles over K in 4 and 2 slices (f32 partials, fixed-order reduce)
+    (512, 3584, 3072, 128), (500, 7168, 1536, 128),
 ]
 
 
