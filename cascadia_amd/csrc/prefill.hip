@@ -96,8 +96,11 @@ struct PfArgs {
 
 // Seeds: xs[kb][m] = -136 * sum_{c < 128} x[m, 128 kb + c] (f32, fixed order:
 // eight columns per lane, then the 16 lanes of a DPP row, which hold one
-// k-block); rows M .. Mp - 1 are 0.  One wave per row; a pass covers four
-// k-blocks, and a wave issues the loads of up to eight passes before summing.
+// k-block); rows M .. Mp - 1 are 0.  One wave per row and kPfXsumPasses passes
+// of four k-blocks (blockIdx.y: which), all loads issued before summing: the
+// pass is latency-bound, so it is spread over as many waves as possible.
+constexpr int kPfXsumPasses = 2;
+
 template <int CTRL>
 CAI4_DEV float dpp_row_add(float v) {
   return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
@@ -106,32 +109,30 @@ CAI4_DEV float dpp_row_add(float v) {
 
 __global__ __launch_bounds__(256) void pf_xsum_kernel(const uint16_t *x, float *xs, int M, int K,
                                                       int Mp) {
-  constexpr int P = 8;  // passes in flight
+  constexpr int P = kPfXsumPasses;
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= Mp) return;
-  const int KB = K >> 7, passes = (KB + 3) >> 2;
+  const int KB = K >> 7, p0 = blockIdx.y * P;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(x + (size_t)(m < M ? m : 0) * K), (short)0, m < M ? K * 2 : 0,
       0x00020000);
-  for (int p0 = 0; p0 < passes; p0 += P) {
-    u32x4_t v[P];
+  u32x4_t v[P];
 #pragma unroll
-    for (int q = 0; q < P; ++q)  // columns 512 (p0 + q) + 8 lane; past K reads 0
-      v[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                             xr, (uint32_t)(512 * (p0 + q) + 8 * lane) * 2, 0, 0));
+  for (int q = 0; q < P; ++q)  // columns 512 (p0 + q) + 8 lane; past K reads 0
+    v[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                           xr, (uint32_t)(512 * (p0 + q) + 8 * lane) * 2, 0, 0));
 #pragma unroll
-    for (int q = 0; q < P; ++q) {
-      float t = 0.f;
+  for (int q = 0; q < P; ++q) {
+    float t = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) t += bf16_to_f32(v[q][e] & 0xFFFFu) + bf16_to_f32(v[q][e] >> 16);
-      t = dpp_row_add<0xB1>(t);   // quad_perm 1,0,3,2
-      t = dpp_row_add<0x4E>(t);   // quad_perm 2,3,0,1
-      t = dpp_row_add<0x124>(t);  // row_ror 4
-      t = dpp_row_add<0x128>(t);  // row_ror 8
-      const int kb = 4 * (p0 + q) + (lane >> 4);
-      if ((lane & 15) == 0 && kb < KB) xs[(size_t)kb * Mp + m] = -136.f * t;
-    }
+    for (int e = 0; e < 4; ++e) t += bf16_to_f32(v[q][e] & 0xFFFFu) + bf16_to_f32(v[q][e] >> 16);
+    t = dpp_row_add<0xB1>(t);   // quad_perm 1,0,3,2
+    t = dpp_row_add<0x4E>(t);   // quad_perm 2,3,0,1
+    t = dpp_row_add<0x124>(t);  // row_ror 4
+    t = dpp_row_add<0x128>(t);  // row_ror 8
+    const int kb = 4 * (p0 + q) + (lane >> 4);
+    if ((lane & 15) == 0 && kb < KB) xs[(size_t)kb * Mp + m] = -136.f * t;
   }
 }
 
@@ -218,8 +219,8 @@ CAI4_DEV void pf_read_a(const uint8_t *buf, int wm, int lane, int s, u32x4_t (&a
   }
 }
 
-template <class P, int MS, int NT>
-CAI4_DEV void pf_compute(const uint8_t *buf, int wm, int wn, int lane, int sdt, const PfNext &nx,
+template <class P, int MS, int NT, int SDT>
+CAI4_DEV void pf_compute(const uint8_t *buf, int wm, int wn, int lane, const PfNext &nx,
                          f32x4_t (&acc)[MS][NT]) {
   const int lr = lane & 15, lg = lane >> 4;
   u32x4_t b[NT];
@@ -229,28 +230,35 @@ CAI4_DEV void pf_compute(const uint8_t *buf, int wm, int wn, int lane, int sdt, 
     const int tile = NT * wn + j;
     b[j] = *reinterpret_cast<const u32x4_t *>(buf + P::B + tile * 1024 + 16 * lane);
     const uint32_t bits = *reinterpret_cast<const uint16_t *>(buf + P::S + tile * 32 + 2 * lr);
-    sc[j] = sdt ? scale_to_f32<SCALE_F16>(bits) : scale_to_f32<SCALE_BF16>(bits);
+    sc[j] = scale_to_f32<SDT>(bits);
   }
   f32x4_t p[MS][NT];
   u32x4_t af[MS], an[MS];
   pf_read_a<P, MS>(buf, wm, lane, 0, af);
+  f32x4_t seed[MS];
 #pragma unroll
-  for (int i = 0; i < MS; ++i) {
+  for (int i = 0; i < MS; ++i)
     // D layout: lane holds rows 4 (lane / 16) + v of the 16-row tile
-    const f32x4_t seed = *reinterpret_cast<const f32x4_t *>(
-        buf + P::X + 4 * (wm * P::RM + 16 * i + 4 * lg));
-#pragma unroll
-    for (int j = 0; j < NT; ++j) p[i][j] = seed;
-  }
+    seed[i] = *reinterpret_cast<const f32x4_t *>(buf + P::X + 4 * (wm * P::RM + 16 * i + 4 * lg));
+  // half a step at a time: decode NT / 2 weight fragments, then their MS x NT / 2
+  // MFMAs (the first step's take the seeds as their accumulator input)
+  static_assert(NT % 2 == 0, "weight tiles per wave");
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     if (s < 3) pf_read_a<P, MS>(buf, wm, lane, s + 1, an);
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const u32x4_t d = decode8(b[j][s]);
+    for (int h = 0; h < 2; ++h) {
+      u32x4_t d[NT / 2];
 #pragma unroll
-      for (int i = 0; i < MS; ++i) p[i][j] = mfma_bf16(af[i], d, p[i][j]);
-      if (j == NT / 2 - 1 || j == NT - 1) pf_issue_part<P>(nx, 2 * s + (j == NT - 1));
+      for (int j = 0; j < NT / 2; ++j) d[j] = decode8(b[h * NT / 2 + j][s]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < NT / 2; ++j)
+#pragma unroll
+        for (int i = 0; i < MS; ++i)
+          p[i][h * NT / 2 + j] = mfma_bf16(af[i], d[j], s == 0 ? seed[i] : p[i][h * NT / 2 + j]);
+      __builtin_amdgcn_sched_barrier(0);
+      pf_issue_part<P>(nx, 2 * s + h);
     }
 #pragma unroll
     for (int i = 0; i < MS; ++i) af[i] = an[i];
@@ -262,7 +270,7 @@ CAI4_DEV void pf_compute(const uint8_t *buf, int wm, int wn, int lane, int sdt, 
 }
 
 // One stage: k-block kb from `cur`; the loads of kb + 2 go into `nxt2`.
-template <class P, int MS, int NT>
+template <class P, int MS, int NT, int SDT>
 CAI4_DEV void pf_stage(uint8_t *cur, uint8_t *nxt2, rsrc_t xr, rsrc_t wr, rsrc_t sr, rsrc_t qr,
                        const PfArgs &a, int KB, int KE, int NG, int kb, int wave, int wm, int wn,
                        int lane, f32x4_t (&acc)[MS][NT]) {
@@ -275,10 +283,10 @@ CAI4_DEV void pf_stage(uint8_t *cur, uint8_t *nxt2, rsrc_t xr, rsrc_t wr, rsrc_t
   else
     pf_wait_barrier<0>();
   const PfNext nx{nxt2, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, kb + 2, wave, lane, KE};
-  pf_compute<P, MS, NT>(cur, wm, wn, lane, a.sdt, nx, acc);
+  pf_compute<P, MS, NT, SDT>(cur, wm, wn, lane, nx, acc);
 }
 
-template <int MS, int NT, int WM, int WN>
+template <int MS, int NT, int WM, int WN, int SDT>
 __global__ __launch_bounds__(64 * WM * WN) void pf_gemm_kernel(PfArgs a) {
   using P = Pf<MS, NT, WM, WN>;
   __shared__ __attribute__((aligned(16))) uint8_t st0[P::BYTES];
@@ -315,9 +323,9 @@ __global__ __launch_bounds__(64 * WM * WN) void pf_gemm_kernel(PfArgs a) {
       pf_load<P>(l, st1, xr, wr, sr, qr, a.K, KB, NG, a.G, a.Mp, kb0 + 1, wave, lane);
   }
   for (int kb = kb0; kb < KE; kb += 3) {
-    pf_stage<P, MS, NT>(st0, st2, xr, wr, sr, qr, a, KB, KE, NG, kb, wave, wm, wn, lane, acc);
-    pf_stage<P, MS, NT>(st1, st0, xr, wr, sr, qr, a, KB, KE, NG, kb + 1, wave, wm, wn, lane, acc);
-    pf_stage<P, MS, NT>(st2, st1, xr, wr, sr, qr, a, KB, KE, NG, kb + 2, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT, SDT>(st0, st2, xr, wr, sr, qr, a, KB, KE, NG, kb, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT, SDT>(st1, st0, xr, wr, sr, qr, a, KB, KE, NG, kb + 1, wave, wm, wn, lane, acc);
+    pf_stage<P, MS, NT, SDT>(st2, st1, xr, wr, sr, qr, a, KB, KE, NG, kb + 2, wave, wm, wn, lane, acc);
   }
 
   // epilogue: D lane l holds column l % 16 and rows 4 * (l / 16) + v
@@ -363,9 +371,11 @@ __global__ __launch_bounds__(256) void pf_reduce_kernel(const float *part, void 
 template <int MS, int NT, int WM, int WN>
 hipError_t pf_launch(const PfArgs &a, int ksplit, hipStream_t st) {
   using P = Pf<MS, NT, WM, WN>;
-  hipLaunchKernelGGL((pf_gemm_kernel<MS, NT, WM, WN>),
-                     dim3((a.N + P::BN - 1) / P::BN, (a.M + P::BM - 1) / P::BM, ksplit),
-                     dim3(64 * P::W), 0, st, a);
+  const dim3 grid((a.N + P::BN - 1) / P::BN, (a.M + P::BM - 1) / P::BM, ksplit), block(64 * P::W);
+  if (a.sdt == SCALE_F16)
+    hipLaunchKernelGGL((pf_gemm_kernel<MS, NT, WM, WN, SCALE_F16>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((pf_gemm_kernel<MS, NT, WM, WN, SCALE_BF16>), grid, block, 0, st, a);
   if (hipError_t e = hipGetLastError()) return e;
   if (ksplit > 1) {
     const size_t n = (size_t)a.M * a.N;
@@ -408,7 +418,9 @@ hipError_t prefill_gemm(const uint8_t *w, const uint8_t *s, const uint16_t *x, v
                         hipStream_t st) {
   const int Mp = pf_rows_padded(M);
   float *xs = static_cast<float *>(ws);
-  hipLaunchKernelGGL(pf_xsum_kernel, dim3(Mp / 4), dim3(256), 0, st, x, xs, M, K, Mp);
+  const int passes = (K / 128 + 3) / 4;
+  hipLaunchKernelGGL(pf_xsum_kernel, dim3(Mp / 4, (passes + kPfXsumPasses - 1) / kPfXsumPasses),
+                     dim3(256), 0, st, x, xs, M, K, Mp);
   PfArgs a{w, s, x, xs, y, M, N, K, G, sdt, out_f32, Mp, K / 128, nullptr};
   const int ks = pf_ksplit(M, N, K, num_cus);
   if (ks >= 1) {  // 128 x 256, 8 waves (in ks slices of K)
