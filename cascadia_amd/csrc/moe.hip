@@ -76,7 +76,8 @@ template <int R>
 __global__ __launch_bounds__(256) void moe_route_kernel(MoeRouting r, int T, int E, int32_t *ids,
                                                         float *wout) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  // the token as a scalar: the logits' buffer descriptor must be uniform
+  const int t = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= T) return;  // whole waves; no barriers in this kernel
   int id;
   float w;

@@ -42,17 +42,23 @@ CAI4_DEV void route_token(const MoeRouting &r, int t, int E, int lane, int &id_o
       const_cast<float *>(r.logits + (size_t)t * E), (short)0, E * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(r.bias), (short)0, r.bias ? E * 4 : 0, 0x00020000);
+  // every load first (registers past nj read nothing), then the keys: one
+  // memory round trip, not one per register
+  float lg[R], bs[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const uint32_t off = j < nj ? (uint32_t)(lane * nj + j) * 4 : kBufOOB;
+    lg[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, 0));
+    bs[j] = sig ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0)) : 0.f;
+  }
   float key[R], val[R];
 #pragma unroll
   for (int j = 0; j < R; ++j) {
     key[j] = -INFINITY;
     val[j] = 0.f;
     if (j < nj) {  // uniform
-      const uint32_t off = (uint32_t)(lane * nj + j) * 4;
-      const float lg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, off, 0, 0));
-      const float bs = sig ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0)) : 0.f;
-      const float sv = sig ? 1.0f / (1.0f + expf(-lg)) : lg;
-      const float c = sig ? sv + bs : sv;
+      const float sv = sig ? 1.0f / (1.0f + expf(-lg[j])) : lg[j];
+      const float c = sig ? sv + bs[j] : sv;
       val[j] = sv;
       key[j] = c != c ? -INFINITY : c;
     }
