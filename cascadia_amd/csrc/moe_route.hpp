@@ -73,12 +73,11 @@ CAI4_DEV void route_token(const MoeRouting &r, int t, int E, int lane, int &id_o
     float best = -INFINITY, bval = 0.f;
     int bj = -1;
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
-      if (((valid >> j) & 1u) && (bj < 0 || key[j] > best)) {
-        best = key[j];
-        bval = val[j];
-        bj = j;
-      }
+    for (int j = 0; j < R; ++j) {  // selects, not branches: no exec-mask round trips
+      const bool take = ((valid >> j) & 1u) & ((bj < 0) | (key[j] > best));
+      best = take ? key[j] : best;
+      bval = take ? val[j] : bval;
+      bj = take ? j : bj;
     }
     const float m = wave_max_f32(bj < 0 ? -INFINITY : best);
     const uint64_t hit = __ballot(bj >= 0 && best == m);
