@@ -72,7 +72,7 @@ struct KParams {
   const int32_t *row_map;
   size_t wstride;
   int N, K, G, M, ldx, ldo, sdt, glog2, tiled, amode, epi, x_rows;
-  int rw, kw, kper;
+  int rw, kw, kper, kslice;
   int act_rows, act_stride, scale_off;
 };
 
@@ -395,7 +395,7 @@ CAI4_DEV void epilogue(const KParams &a, f32x4_t (&acc)[MT][NT], int unit, int m
   }
 }
 
-template <int NT, int MT, bool TR, bool SW>
+template <int NT, int MT, bool TR, bool SW, bool SLICED>
 __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int U = skinny_ring_depth(NT);
@@ -421,8 +421,6 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
   }
   const int kb_total = (a.K + 127) >> 7;
   const int kr0 = blockIdx.z * a.kper, kr1 = min(kr0 + a.kper, kb_total);
-  const int col_hi = min(a.K, kr1 * 128);
-  const int g_lo = (kr0 * 128) / a.G, ngw = (col_hi + a.G - 1) / a.G - g_lo;
 
   // weight sources of this wave's tiles
   rsrc_t wr[NT];
@@ -444,41 +442,6 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
   }
   const uint32_t wk = a.tiled ? 1024u : 64u;
 
-  // this wave's span of k-blocks
-  const int nkb = kr1 - kr0, per = (nkb + a.kw - 1) / a.kw;
-  const int kb0 = kr0 + min(kwi * per, nkb), kb1 = kr0 + min(kwi * per + per, nkb);
-
-  // Staging loads first, then the weight ring: loads complete in order, so
-  // storing the staged batch waits only for the staging loads.
-  constexpr int BA = 4, BS = 2;
-  const int nth = blockDim.x, tid = threadIdx.x;
-  const int cpr = (kr1 - kr0) * 16, spr = ngw * (a.tiled ? 2 : 16);
-  // thread positions and per-item steps (one division each, per thread)
-  const Pos pa = pos_start(tid, cpr), ps = pos_start(tid, spr);
-  const Pos da = pos_start(nth, cpr), ds = pos_start(nth, spr);
-  uint16_t *lds_sc = reinterpret_cast<uint16_t *>(lds + a.scale_off);
-  u32x4_t av[2][BA];
-  u32x4_t sv[NT][BS];
-  act_issue<BA>(a, m0, mcount, kr0, kr1, pa, da.t, da.c, av);
-  sc_issue<NT, SW, BS>(a, unit0, g_lo, ngw, ps, ds.t, ds.c, sv);
-  u32x4_t ring[U][NT];
-#pragma unroll
-  for (int u = 0; u < U; ++u) load_w<NT>(ring[u], wr, wv, kb0 + u, wk, kb0 + u < kb1);
-  act_store<BA>(a, lds, mcount, kr0, kr1, pa, da.t, da.c, av);
-  sc_store<NT, BS>(a, lds_sc, ngw, ps, ds.t, ds.c, sv);
-  // larger stagings: the remaining batches (these wait for the ring too)
-  for (int base = BA * nth; base < mcount * cpr; base += BA * nth) {
-    const Pos p = pos_start(base + tid, cpr);
-    act_issue<BA>(a, m0, mcount, kr0, kr1, p, da.t, da.c, av);
-    act_store<BA>(a, lds, mcount, kr0, kr1, p, da.t, da.c, av);
-  }
-  for (int base = BS * nth; base < a.rw * spr; base += BS * nth) {
-    const Pos p = pos_start(base + tid, spr);
-    sc_issue<NT, SW, BS>(a, unit0, g_lo, ngw, p, ds.t, ds.c, sv);
-    sc_store<NT, BS>(a, lds_sc, ngw, p, ds.t, ds.c, sv);
-  }
-  __syncthreads();
-
   // Token slots past mcount read token 0's row: MFMA rows are independent and
   // those output rows are never stored, so no predicate is needed.
   uint32_t abase[MT];
@@ -489,10 +452,6 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
     abase[mt] = (hilo && lr >= 8 ? plane_bytes : 0u) +
                 (uint32_t)(tok < mcount ? tok : 0) * a.act_stride + (TR ? 16u * lg : 64u * lg);
   }
-  uint32_t sbase[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    sbase[nt] = a.scale_off + (uint32_t)(((rwi * NT + nt) * ngw * 16 + lr) * 2);
 
   f32x4_t acc[MT][NT];
 #pragma unroll
@@ -500,18 +459,75 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  if (mcount > 0) {
-    for (int kb = kb0; kb < kb1; kb += U) {
+  // The workgroup's k-blocks [kr0, kr1) at once, or (SLICED) in slices of
+  // kslice: each slice's activations and scales are staged into LDS, then
+  // every wave runs its span of the slice.  Partial sums stay in registers
+  // across slices, so a staging too large for LDS costs a barrier per slice
+  // rather than a split of K across workgroups (whose f32 partials a second
+  // launch must write and read back).  The unsliced instantiation keeps the
+  // single stage's register budget.
+  constexpr int BA = 4, BS = 2;
+  const int nth = blockDim.x, tid = threadIdx.x;
+  uint16_t *lds_sc = reinterpret_cast<uint16_t *>(lds + a.scale_off);
+  auto run_slice = [&](const int s0, const int s1) {
+    const int col_hi = min(a.K, s1 * 128);
+    const int g_lo = (s0 * 128) / a.G, ngw = (col_hi + a.G - 1) / a.G - g_lo;
+    // this wave's span of the slice
+    const int nkb = s1 - s0, per = (nkb + a.kw - 1) / a.kw;
+    const int kb0 = s0 + min(kwi * per, nkb), kb1 = s0 + min(kwi * per + per, nkb);
+
+    // Staging loads first, then the weight ring: loads complete in order, so
+    // storing the staged batch waits only for the staging loads.
+    const int cpr = (s1 - s0) * 16, spr = ngw * (a.tiled ? 2 : 16);
+    // thread positions and per-item steps (one division each, per thread)
+    const Pos pa = pos_start(tid, cpr), ps = pos_start(tid, spr);
+    const Pos da = pos_start(nth, cpr), ds = pos_start(nth, spr);
+    u32x4_t av[2][BA];
+    u32x4_t sv[NT][BS];
+    act_issue<BA>(a, m0, mcount, s0, s1, pa, da.t, da.c, av);
+    sc_issue<NT, SW, BS>(a, unit0, g_lo, ngw, ps, ds.t, ds.c, sv);
+    u32x4_t ring[U][NT];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int k = kb + u;
-        if (k < kb1) {
-          compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, k, kr0, g_lo, a.K, a.G, a.glog2,
-                                 a.sdt, acc);
-          load_w<NT>(ring[u], wr, wv, k + U, wk, k + U < kb1);
+    for (int u = 0; u < U; ++u) load_w<NT>(ring[u], wr, wv, kb0 + u, wk, kb0 + u < kb1);
+    if (s0 > kr0) __syncthreads();  // every wave is done with the previous slice's LDS
+    act_store<BA>(a, lds, mcount, s0, s1, pa, da.t, da.c, av);
+    sc_store<NT, BS>(a, lds_sc, ngw, ps, ds.t, ds.c, sv);
+    // larger stagings: the remaining batches (these wait for the ring too)
+    for (int base = BA * nth; base < mcount * cpr; base += BA * nth) {
+      const Pos p = pos_start(base + tid, cpr);
+      act_issue<BA>(a, m0, mcount, s0, s1, p, da.t, da.c, av);
+      act_store<BA>(a, lds, mcount, s0, s1, p, da.t, da.c, av);
+    }
+    for (int base = BS * nth; base < a.rw * spr; base += BS * nth) {
+      const Pos p = pos_start(base + tid, spr);
+      sc_issue<NT, SW, BS>(a, unit0, g_lo, ngw, p, ds.t, ds.c, sv);
+      sc_store<NT, BS>(a, lds_sc, ngw, p, ds.t, ds.c, sv);
+    }
+    __syncthreads();
+
+    uint32_t sbase[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      sbase[nt] = a.scale_off + (uint32_t)(((rwi * NT + nt) * ngw * 16 + lr) * 2);
+
+    if (mcount > 0) {
+      for (int kb = kb0; kb < kb1; kb += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int k = kb + u;
+          if (k < kb1) {
+            compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, k, s0, g_lo, a.K, a.G, a.glog2,
+                                   a.sdt, acc);
+            load_w<NT>(ring[u], wr, wv, k + U, wk, k + U < kb1);
+          }
         }
       }
     }
+  };
+  if constexpr (SLICED) {
+    for (int s0 = kr0; s0 < kr1; s0 += a.kslice) run_slice(s0, min(s0 + a.kslice, kr1));
+  } else {
+    run_slice(kr0, kr1);
   }
 
   // add the kw spans of each row group in wave order (LDS reused)
@@ -659,35 +675,58 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   };
   const int ks_env = env_int("CASCADIA_INT4_SKINNY_KSPLIT", 1, 64);
   const int kw_env = env_int("CASCADIA_INT4_SKINNY_WAVES", 1, 16);
-  int ksplit = 1, kper = kb_total, kw = 1;
-  // Split K across workgroups only when the staging does not fit in LDS or
-  // fewer than half the CUs would get a workgroup: the reduce launch costs
-  // more than that.  Waves per workgroup: enough that the workgroups sharing
-  // a CU (as many as LDS allows, at most those the grid has per CU) bring
-  // about 16 waves.  A forced split is a minimum.
-  for (int ks = ks_env ? ks_env : 1; ks <= kb_total; ++ks) {
-    kper = (kb_total + ks - 1) / ks;
-    ksplit = (kb_total + kper - 1) / kper;
-    const long wgs = wgs0 * ksplit;
-    const size_t need1 = lds_need(kper, 1);
-    if (need1 > d.max_lds && ksplit < kb_total) continue;
-    long per_cu = (long)(d.max_lds / (need1 ? need1 : 1));
-    const long grid_per_cu = (wgs + d.num_cus - 1) / d.num_cus;
-    if (per_cu > grid_per_cu) per_cu = grid_per_cu;
-    if (per_cu < 1) per_cu = 1;
-    long w = target / d.num_cus / (per_cu * rw);
-    kw = (int)(w < 1 ? 1 : (w > maxw / rw ? maxw / rw : w));
-    if (kw_env) kw = kw_env / rw < 1 ? 1 : (kw_env / rw > maxw / rw ? maxw / rw : kw_env / rw);
-    if (kw > kper) kw = kper;
-    while (kw > 1 && lds_need(kper, kw) > d.max_lds) --kw;
-    if (ks_env || wgs * 2 >= d.num_cus || ksplit >= 64) break;
-  }
+  // K decomposition.  Split K across workgroups when fewer than half the CUs
+  // would get a workgroup (the reduce launch costs more than that), and --
+  // unsliced -- also when the staging does not fit in LDS; or (sliced) stage
+  // such a range in slices of K inside the workgroup.  Waves per workgroup:
+  // enough that the workgroups sharing a CU (as many as LDS allows, at most
+  // those the grid has per CU) bring about 16 waves.  A forced split is a
+  // minimum.
+  struct KPlan {
+    int ksplit, kper, kslice, kw;
+  };
+  auto plan_k = [&](bool sliced) {
+    KPlan q{1, kb_total, kb_total, 1};
+    for (int ks = ks_env ? ks_env : 1; ks <= kb_total; ++ks) {
+      q.kper = (kb_total + ks - 1) / ks;
+      q.ksplit = (kb_total + q.kper - 1) / q.kper;
+      const long wgs = wgs0 * q.ksplit;
+      q.kslice = q.kper;
+      if (sliced)
+        while (q.kslice > 1 && lds_need(q.kslice, 1) > d.max_lds) --q.kslice;
+      const size_t need1 = lds_need(q.kslice, 1);
+      if (!sliced && need1 > d.max_lds && q.ksplit < kb_total) continue;
+      long per_cu = (long)(d.max_lds / (need1 ? need1 : 1));
+      const long grid_per_cu = (wgs + d.num_cus - 1) / d.num_cus;
+      if (per_cu > grid_per_cu) per_cu = grid_per_cu;
+      if (per_cu < 1) per_cu = 1;
+      long w = target / d.num_cus / (per_cu * rw);
+      q.kw = (int)(w < 1 ? 1 : (w > maxw / rw ? maxw / rw : w));
+      if (kw_env)
+        q.kw = kw_env / rw < 1 ? 1 : (kw_env / rw > maxw / rw ? maxw / rw : kw_env / rw);
+      if (q.kw > q.kslice) q.kw = q.kslice;
+      while (q.kw > 1 && lds_need(q.kslice, q.kw) > d.max_lds) --q.kw;
+      if (ks_env || wgs * 2 >= d.num_cus || q.ksplit >= 64) break;
+    }
+    return q;
+  };
+  auto partials = [&](const KPlan &q) {
+    return q.ksplit > 1 ? (double)q.ksplit * wgs0 * rw * mt * p.nt * 64 * sizeof(f32x4_t) : 0.0;
+  };
+  // Slices when the split's f32 partials (written, then read back) would add
+  // more than a fifth of the weight bytes: measured, config 3 at 256 tokens
+  // 777 -> 608 us per layer; with fewer partial bytes (config 4 gate/up at 8
+  // tokens: 7 %) the split ran faster.
+  KPlan q = plan_k(false);
+  if (2.0 * partials(q) > 0.2 * wbytes) q = plan_k(true);
+  const int ksplit = q.ksplit, kper = q.kper, kslice = q.kslice, kw = q.kw;
   p.ksplit = ksplit;
   p.kper = kper;
+  p.kslice = kslice;
   p.kw = kw;
-  p.act_stride = kper * 256 + 16;
+  p.act_stride = kslice * 256 + 16;
   p.scale_off = (int)round16((size_t)planes * p.act_rows * p.act_stride);
-  p.lds_bytes = lds_need(kper, kw);
+  p.lds_bytes = lds_need(kslice, kw);
   p.partial_bytes =
       ksplit > 1 ? (size_t)ksplit * wgs0 * rw * mt * p.nt * 64 * sizeof(f32x4_t) : 0;
   return p;
@@ -709,7 +748,10 @@ namespace {
 template <int NT, int MT, bool TR, bool SW>
 hipError_t launch_one(const KParams &k, const SkinnyPlan &p, hipStream_t st) {
   dim3 grid(p.row_blocks, p.m_chunks, p.ksplit), block(64 * p.rw * p.kw, 1, 1);
-  hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW>), grid, block, p.lds_bytes, st, k);
+  if (p.kslice < p.kper)
+    hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, true>), grid, block, p.lds_bytes, st, k);
+  else
+    hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, false>), grid, block, p.lds_bytes, st, k);
   if (hipError_t e = hipGetLastError()) return e;
   if (p.ksplit > 1) {
     dim3 g2(p.row_blocks, p.m_chunks, 1), b2(64 * p.rw, 1, 1);
@@ -768,6 +810,7 @@ hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, in
   k.rw = p.rw;
   k.kw = p.kw;
   k.kper = p.kper;
+  k.kslice = p.kslice;
   k.act_rows = p.act_rows;
   k.act_stride = p.act_stride;
   k.scale_off = p.scale_off;

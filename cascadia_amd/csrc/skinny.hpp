@@ -52,7 +52,7 @@ struct SkinnyArgs {
 // workgroup's k-range.  ksplit > 1 splits K across workgroups, whose partial
 // sums a second kernel adds in a fixed order.
 struct SkinnyPlan {
-  int nt, mt, rw, kw, ksplit, kper, row_blocks, m_chunks;
+  int nt, mt, rw, kw, ksplit, kper, kslice, row_blocks, m_chunks;
   int act_rows, act_stride, scale_off;
   size_t lds_bytes, partial_bytes;
 };
