@@ -221,8 +221,11 @@ CAI4_DEV void group_assignments(const int32_t *ids, const float *w, float thr, i
   lds_barrier();
 }
 
+// One workgroup of 1024 threads: each thread's assignments are a couple of
+// independent loads and LDS atomics (one wave took 26 us at 2048 assignments,
+// its loop of dependent global loads and atomics being latency-bound).
 template <int R>
-__global__ __launch_bounds__(64) void moe_group_kernel(const int32_t *ids, const float *w,
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *ids, const float *w,
                                                        float thr, int T, int E, int k, int C,
                                                        int max_chunks, int32_t *pos,
                                                        int32_t *row_map, SkinnyChunk *chunks,
@@ -236,7 +239,7 @@ __global__ __launch_bounds__(64) void moe_group_kernel(const int32_t *ids, const
 hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T, int E,
                      int top_k, int chunk_rows, int max_chunks, int32_t *pos, int32_t *row_map,
                      SkinnyChunk *chunks, int32_t *counts, hipStream_t st) {
-  CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_group_kernel<R>, dim3(1), dim3(64), 0, st, ids, w,
+  CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_group_kernel<R>, dim3(1), dim3(1024), 0, st, ids, w,
                                           threshold, T, E, top_k, chunk_rows, max_chunks, pos,
                                           row_map, chunks, counts));
   return hipGetLastError();
