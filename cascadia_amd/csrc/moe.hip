@@ -28,8 +28,14 @@ namespace {
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 }  // namespace
 
+// Rows per chunk: the grouped GEMMs stage (and compute for) that many rows per
+// chunk, and every chunk streams its expert's weights.  Measured on configs 3
+// and 4: 16 rows beat 32 at 256 tokens (config 3 598 -> 432 us per layer: the
+// 32-row down ran 8 waves per CU); 8 rows beat 16 at 32 tokens on config 3
+// (-6 %) but lost 16 % at 64 tokens on config 4, whose skewed routing gives
+// its hot experts many rows -- so 16 from 9 tokens up.
 int moe_chunk_rows(int T, int per_expert_max) {
-  const int c = T <= 8 ? 8 : (T <= 64 ? 16 : 32);
+  const int c = T <= 8 ? 8 : 16;
   return per_expert_max < c ? per_expert_max : c;
 }
 
