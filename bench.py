@@ -175,8 +175,8 @@ def read_traffic(m):
 
 
 def extra_measurements(cl, torch, args, sdt, copies):
-    """Secondary numbers (not the headline): M=4/16 chains, config 0 GEMV,
-    config 2 prefill GEMM."""
+    """Secondary numbers (not the headline): M=4/16 chains, config 0 GEMV, the
+    K2.6 shell projections at one token, config 2 prefill GEMM."""
     res = {}
     h, i, g = copies.h, copies.i, copies.g
     for mm in (4, 16):
@@ -215,6 +215,42 @@ def extra_measurements(cl, torch, args, sdt, copies):
     res["config0_gemv"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(b / t / 1e9, 1),
                            "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4), "copies": ncp}
     del PS
+    # the K2.6 shell projections at one token (q_a, q_b, kv_a, kv_b, o_proj,
+    # router; shell_int4.rs:404-660) in the crate's format (G = 32, bf16
+    # scales): six one-token GEMVs per step over rotating weight copies
+    shapes = [(1536, 7168), (12288, 1536), (576, 7168), (16384, 512), (7168, 8192), (384, 7168)]
+    gs, sbf = 32, cl.SCALE_BF16
+    per = sum(nn * kk // 2 + nn * (kk // gs) * 2 for nn, kk in shapes)
+    ncs = math.ceil(2 * MALL_BYTES / per) + 1
+    SH = []
+    for c in range(ncs):
+        mats = []
+        for j, (nn, kk) in enumerate(shapes):
+            p = cl.fill_bytes(torch.empty(nn * kk // 2, dtype=torch.uint8, device="cuda"), 1, 400 + 8 * c + j)
+            sc = cl.fill_scales(torch.empty(nn * (kk // gs) * 2, dtype=torch.uint8, device="cuda"),
+                                1, 500 + 8 * c + j, sbf)
+            mats.append(cl.tile_weights(p, sc, nn, kk, gs))
+            del p, sc
+        SH.append(mats)
+    xs_ = {kk: cl.fill_normal(torch.empty(kk, dtype=torch.float32, device="cuda"), 1, kk)
+           for _, kk in shapes}
+    ys_ = [torch.empty(nn, dtype=torch.float32, device="cuda") for nn, _ in shapes]
+
+    def shell(r):
+        for j, (nn, kk) in enumerate(shapes):
+            pt, st = SH[r % ncs][j]
+            cl.dequant_gemv_int4(pt, st, xs_[kk], nn, kk, ys_[j], group_size=gs, scale_dtype=sbf,
+                                 tiling=cl.TILING_MFMA)
+    for r in range(5):
+        shell(r)
+    steps = 200
+    w, _ = graph_time(torch, shell, steps)
+    t = w / steps
+    b = per + sum(kk * 4 + nn * 4 for nn, kk in shapes)
+    res["shell_projections_M1"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1),
+                                   "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+                                   "bytes_per_step": b, "copies": ncs}
+    del SH
     # config 2: prefill GEMM (bf16 in/out)
     for (m, nn) in PREFILL_SHAPES:
         pre = prefill_fn(cl, torch, m, nn, 4096, g, sdt)

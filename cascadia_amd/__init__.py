@@ -16,7 +16,7 @@ from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertWei
                   dequant_gemv_int4_auto, expert_bytes, expert_forward, expert_forward_sparse,
                   ffn_forward_sparse_f32, ffn_workspace_bytes, fill_bytes, fill_normal,
                   fill_scales, gate_up_silu, gemm_int4_bf16, MoEExperts, moe_forward,
-                  moe_workspace_bytes, tile_weights, tiled_sizes)
+                  moe_workspace_bytes, quantize_int4_group, tile_weights, tiled_sizes)
 
 __all__ = [
     "CascadiaInt4Error", "LIB_PATH", "SCALE_BF16", "SCALE_F16", "SIGNATURES", "check", "lib",
@@ -26,5 +26,6 @@ __all__ = [
     "expert_forward_sparse", "ffn_forward_sparse_f32", "ffn_workspace_bytes", "fill_bytes",
     "fill_normal", "fill_scales", "gate_up_silu", "gemm_int4_bf16", "tile_weights",
     "tiled_sizes", "TILING_CRATE", "TILING_MFMA", "MoEExperts", "moe_forward",
-    "moe_workspace_bytes", "ROUTE_IDS", "ROUTE_SIGMOID_BIAS", "ROUTE_SOFTMAX_TOPK",
+    "moe_workspace_bytes", "quantize_int4_group", "ROUTE_IDS", "ROUTE_SIGMOID_BIAS",
+    "ROUTE_SOFTMAX_TOPK",
 ]

@@ -462,6 +462,29 @@ def debug_dequant(packed, scale_bits, n_rows, k_cols, group_size=GROUP_SIZE,
     return out
 
 
+def quantize_int4_group(weight_bf16: torch.Tensor, n_rows: int, k_cols: int,
+                        group_size: int = GROUP_SIZE):
+    """Quantise bf16 weights [n_rows, k_cols] on the device into the crate
+    layout: (packed u8 [n_rows * k_cols / 2], scales u8 [n_rows * k_cols /
+    group_size * 2], bf16 little-endian).  shell_int4.rs:148-212, which asserts
+    the length and that k_cols is a multiple of the group (32 there): those
+    raise ValueError here.  `weight_bf16` holds the bf16 bits (bfloat16, int16
+    or uint16 elements, or the raw bytes as uint8)."""
+    _dev(weight_bf16, "weight_bf16")
+    _expect(_nbytes(weight_bf16) == n_rows * k_cols * 2,
+            f"weight_bf16 holds {_nbytes(weight_bf16)} bytes, expected {n_rows * k_cols * 2}")
+    _expect(group_size > 0 and group_size % 32 == 0 and k_cols % group_size == 0,
+            f"k_cols {k_cols} must be a multiple of group_size {group_size} (a multiple of 32)")
+    _expect(weight_bf16.is_contiguous(), "weight_bf16 must be contiguous")
+    packed = torch.empty(n_rows * k_cols // 2, dtype=torch.uint8, device=weight_bf16.device)
+    scales = torch.empty(n_rows * (k_cols // group_size) * 2, dtype=torch.uint8,
+                         device=weight_bf16.device)
+    check("cascadia_int4_quantize_bf16", lib().cascadia_int4_quantize_bf16(
+        weight_bf16.data_ptr(), n_rows, k_cols, group_size, packed.data_ptr(), scales.data_ptr(),
+        _stream()))
+    return packed, scales
+
+
 def fill_bytes(out: torch.Tensor, seed: int, stream_id: int):
     _dev(out, "out")
     check("cascadia_int4_fill_synthetic", lib().cascadia_int4_fill_synthetic(

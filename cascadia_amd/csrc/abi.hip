@@ -12,6 +12,7 @@
 #include "moe.hpp"
 #include "gemv.hpp"
 #include "prefill.hpp"
+#include "quant.hpp"
 #include "skinny.hpp"
 #include "synth.hpp"
 
@@ -804,6 +805,19 @@ int cascadia_int4_debug_dequant(const cascadia_int4_layout *L, const uint8_t *pa
   return hip_status(cai4::debug_dequant(packed, scale_bits, (int)L->n_rows, (int)L->k_cols,
                                         (int)L->group_size, (int)L->scale_dtype, w_out,
                                         (hipStream_t)stream));
+}
+
+int cascadia_int4_quantize_bf16(const uint16_t *w_bf16, uint32_t n_rows, uint32_t k_cols,
+                                uint32_t group_size, uint8_t *packed, uint16_t *scale_bits,
+                                void *stream) {
+  if (!w_bf16 || !packed || !scale_bits) return CASCADIA_INT4_ERR_NULL;
+  if (n_rows == 0 || k_cols == 0 || group_size == 0 || group_size % 32 ||
+      k_cols % group_size || n_rows > (1u << 30) || k_cols > (1u << 30))
+    return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(w_bf16, 16) || !aligned(packed, 4) || !aligned(scale_bits, 2))
+    return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::quantize_group(w_bf16, (int)n_rows, (int)k_cols, (int)group_size,
+                                         packed, scale_bits, (hipStream_t)stream));
 }
 
 int cascadia_int4_fill_synthetic(uint32_t kind, uint64_t seed, uint64_t stream_id, size_t n,

@@ -245,6 +245,17 @@ int cascadia_int4_moe_forward(const cascadia_int4_moe_layer *layer,
 int cascadia_int4_debug_dequant(const cascadia_int4_layout *layout, const uint8_t *packed,
                                 const uint8_t *scale_bits, float *w_out, void *stream);
 
+/* Load-time quantiser: bf16 weights [n_rows, k_cols] (device, 16-byte
+ * aligned) -> packed nibbles [n_rows, k_cols/2] and bf16 group scales
+ * [n_rows, k_cols/group_size], the crate layout.  Replaces
+ * quantize_int4_group (src/shell_int4.rs:148-212: G = 32 there; here any
+ * multiple of 32 dividing k_cols), bytes identical to it: scale =
+ * bf16(max|w| / 7) (1e-10 for an all-zero group), q = clamp(round(w / scale),
+ * -8, 7), nibble q + 8. */
+int cascadia_int4_quantize_bf16(const uint16_t *w_bf16, uint32_t n_rows, uint32_t k_cols,
+                                uint32_t group_size, uint8_t *packed, uint16_t *scale_bits,
+                                void *stream);
+
 /* Seeded synthetic data, the same generator as the test oracle.
  * kind 0: bytes (uniform nibbles), n = byte count, out u8.
  * kind 1: scales fp16/bf16(|N(0,sigma)| + offset), n = count, out u16

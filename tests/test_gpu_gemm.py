@@ -292,6 +292,28 @@ def test_gemv_tiled_one_token(cl, orc, n, k, group, sdt):
                       f"gemv bf16 out {n}x{k} G{group}")
 
 
+SHELL_SHAPES = [  # K2.6 shell projections (shell_int4.rs:404-660): q_a, q_b, kv_a, kv_b, o_proj, router
+    (1536, 7168), (12288, 1536), (576, 7168), (16384, 512), (7168, 8192), (384, 7168),
+]
+
+
+@pytest.mark.parametrize("n,k", SHELL_SHAPES)
+def test_shell_projection_shapes(cl, orc, n, k):
+    """The shell's INT4 projections in the crate's own format (G = 32, bf16
+    scales), tiled: one token (the one-token GEMV) and four tokens (the skinny
+    GEMM), f32 activations, against the oracle."""
+    g = 32
+    packed, scales = weights(orc, n, k, g, BF16, n + 3 * k)
+    pt, st = cl.tile_weights(dev(packed), dev(scales), n, k, g)
+    for seq in (1, 4):
+        xs = orc.fill_normal_f32(seq, 15, seq * k)
+        ys = torch.empty(seq * n, dtype=torch.float32, device="cuda")
+        cl.dequant_gemm_int4_multi_auto(pt, st, dev(xs), n, k, seq, ys, group_size=g,
+                                        scale_dtype=BF16, tiling=cl.TILING_MFMA)
+        want = orc.gemm_multi(packed, scales, xs, n, k, seq, g, BF16)
+        assert_f32_close(host(ys).reshape(seq, n), want, f"shell {n}x{k} seq{seq}")
+
+
 @pytest.mark.parametrize("h,i,g", [(1024, 768, 128), (4096, 14336, 128), (512, 2560, 256),
                                    (2048, 5632, 128), (3072, 8192, 128), (7168, 2048, 32),
                                    (1024, 1536, 64)])

@@ -479,6 +479,23 @@ def test_quantize_roundtrip(orc):
     assert np.all(packed[3 * (k // 2):3 * (k // 2) + 16] == 0x88)
 
 
+def test_quantize_known_answers(orc):
+    """Closed-form codes: a group whose max is 0.875 has scale 0.875 / 7 =
+    0.125 exactly (bf16 0x3E00) and 1 / scale = 8, so w = (2m + 1) / 16 lands
+    on m + 0.5 and rounds away from zero (Rust f32::round) to m + 1 (m < 7: every
+    |w| below the max)."""
+    g = 32
+    j = np.arange(g)
+    w = ((j % 7) * 2 + 1) * 0.0625 * np.where(j % 2, -1.0, 1.0)
+    w[0] = 0.875
+    packed, scales = orc.quantize_int4_group(orc.f32_to_bf16(w.astype(np.float32)), 1, g, g)
+    assert scales.view("<u2")[0] == 0x3E00
+    q = np.stack([packed & 15, packed >> 4], 1).reshape(-1).astype(np.int32) - 8
+    want = (j % 7 + 1) * np.where(j % 2, -1, 1)
+    want[0] = 7
+    assert np.array_equal(q, want)
+
+
 # ----------------------------------------------------------------------------
 # generators
 # ----------------------------------------------------------------------------
