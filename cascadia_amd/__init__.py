@@ -10,7 +10,8 @@ from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, CascadiaIn
 
 lib()  # fail loudly at import when the HIP library is missing
 
-from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertWeights,  # noqa: E402
+from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertSource,  # noqa: E402
+                  ExpertWeights,
                   debug_dequant, dequant_gemm_int4_multi_auto,
                   dequant_gemm_int4_multi_blocked_auto, dequant_gemv_int4,
                   dequant_gemv_int4_auto, expert_bytes, expert_forward, expert_forward_sparse,
@@ -20,7 +21,7 @@ from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertWei
 
 __all__ = [
     "CascadiaInt4Error", "LIB_PATH", "SCALE_BF16", "SCALE_F16", "SIGNATURES", "check", "lib",
-    "GROUP_SIZE", "HIDDEN", "INTERMEDIATE", "NIBBLES_PER_INT32", "ExpertWeights",
+    "GROUP_SIZE", "HIDDEN", "INTERMEDIATE", "NIBBLES_PER_INT32", "ExpertSource", "ExpertWeights",
     "debug_dequant", "dequant_gemm_int4_multi_auto", "dequant_gemm_int4_multi_blocked_auto",
     "dequant_gemv_int4", "dequant_gemv_int4_auto", "expert_bytes", "expert_forward",
     "expert_forward_sparse", "ffn_forward_sparse_f32", "ffn_workspace_bytes", "fill_bytes",

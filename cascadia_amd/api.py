@@ -485,6 +485,47 @@ def quantize_int4_group(weight_bf16: torch.Tensor, n_rows: int, k_cols: int,
     return packed, scales
 
 
+class ExpertSource:
+    """The crate's C handle API (c_ffi.rs:35-341) as its ctypes callers use it:
+    a safetensors model directory, experts run one f32 vector at a time on
+    host arrays of the model's hidden size.  Experts are uploaded and tiled
+    into HBM on first use (or by prewarm) and stay resident until close.
+    Errors raise CascadiaInt4Error with the crate's code (-1 null, -2 path
+    or expert, -3 directory or HIP)."""
+
+    def __init__(self, model_dir: str):
+        h = C.c_void_p()
+        check("cascadia_int4_open_source",
+              lib().cascadia_int4_open_source(model_dir.encode(), C.byref(h)))
+        self._h = h
+
+    def prewarm(self, layer: int, expert: int) -> None:
+        check("cascadia_int4_prewarm", lib().cascadia_int4_prewarm(self._h, layer, expert))
+
+    def expert_forward(self, layer: int, expert: int, x_f32, out_f32) -> None:
+        """x_f32, out_f32: contiguous host float32 numpy arrays of the hidden size."""
+        import numpy as np
+
+        _expect(isinstance(x_f32, np.ndarray) and x_f32.dtype == np.float32 and
+                x_f32.flags.c_contiguous, "x_f32 must be a contiguous float32 numpy array")
+        _expect(isinstance(out_f32, np.ndarray) and out_f32.dtype == np.float32 and
+                out_f32.flags.c_contiguous and out_f32.size == x_f32.size,
+                "out_f32 must be a contiguous float32 numpy array of x's size")
+        check("cascadia_int4_expert_forward", lib().cascadia_int4_expert_forward(
+            self._h, layer, expert, x_f32.ctypes.data, out_f32.ctypes.data))
+
+    def close(self) -> None:
+        if self._h:
+            lib().cascadia_int4_destroy_source(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def fill_bytes(out: torch.Tensor, seed: int, stream_id: int):
     _dev(out, "out")
     check("cascadia_int4_fill_synthetic", lib().cascadia_int4_fill_synthetic(

@@ -1,0 +1,530 @@
+// source.hip -- the crate's C handle API (crates/cascadia-int4-gemm/src/c_ffi.rs:35-341):
+// a safetensors model directory opened as an expert source, experts brought
+// into HBM on first use, and one expert run on one f32 vector.
+//
+//   cascadia_int4_open_source(model_dir, &h)   c_ffi.rs:35-56
+//   cascadia_int4_destroy_source(h)            c_ffi.rs:58-64
+//   cascadia_int4_prewarm(h, layer, expert)    c_ffi.rs:66-106
+//   cascadia_int4_expert_forward(h, layer, expert, x_f32, out_f32)
+//                                              c_ffi.rs:305-341
+//
+// The source follows safetensors_source.rs:205-380: `model.safetensors.index.json`
+// maps tensor names to shard files; a shard is an 8-byte little-endian header
+// length, a JSON header {name: {dtype, shape, data_offsets}} and the data.
+// Expert (L, E) is the six tensors
+// `language_model.model.layers.L.mlp.experts.E.{gate,up,down}_proj.weight_{packed,scale}`
+// (compressed-tensors: packed int32 [rows, cols / 8], whose little-endian
+// bytes are the crate layout; scales bf16 or f16 [rows, cols / G]).
+//
+// Where the crate mmaps the shards and lets the OS page an expert in
+// (prewarm touches its pages), here an expert is read from the shards once,
+// uploaded, tiled into the MFMA layout and kept resident in HBM for the life
+// of the handle: prewarm does that load.  expert_forward converts x to bf16
+// as the crate does (bf16::from_f32: RNE, NaN made quiet), runs
+// cascadia_int4_expert_forward_device and widens the bf16 result to f32; it
+// is synchronous, like the crate's.  The hidden size is the model's (7168 in
+// the crate's HIDDEN); x and out hold that many floats.
+//
+// Return codes as the crate's: 0 OK, -1 null argument, -2 invalid UTF-8 path
+// (open) or an expert that cannot be read (prewarm / forward), -3 a model
+// directory that cannot be opened; a HIP failure returns -3 as well.
+#include <fcntl.h>
+#include <unistd.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/cascadia_int4.h"
+#include "int4_common.hpp"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// a small JSON reader (objects, arrays, strings, numbers, literals): enough
+// for the index file and safetensors headers
+// ---------------------------------------------------------------------------
+
+struct Json {
+  enum Kind { NUL, BOOL, NUM, STR, ARR, OBJ } kind = NUL;
+  double num = 0;
+  std::string str;
+  std::vector<Json> arr;
+  std::vector<std::pair<std::string, Json>> obj;
+  const Json *get(const std::string &k) const {
+    for (const auto &kv : obj)
+      if (kv.first == k) return &kv.second;
+    return nullptr;
+  }
+};
+
+struct JsonParser {
+  const char *p, *end;
+  bool ok = true;
+  void ws() {
+    while (p < end && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p;
+  }
+  bool lit(const char *s) {
+    const size_t n = strlen(s);
+    if ((size_t)(end - p) < n || strncmp(p, s, n) != 0) return false;
+    p += n;
+    return true;
+  }
+  static void utf8(std::string &out, unsigned c) {
+    if (c < 0x80) {
+      out += (char)c;
+    } else if (c < 0x800) {
+      out += (char)(0xC0 | (c >> 6));
+      out += (char)(0x80 | (c & 0x3F));
+    } else if (c < 0x10000) {
+      out += (char)(0xE0 | (c >> 12));
+      out += (char)(0x80 | ((c >> 6) & 0x3F));
+      out += (char)(0x80 | (c & 0x3F));
+    } else {
+      out += (char)(0xF0 | (c >> 18));
+      out += (char)(0x80 | ((c >> 12) & 0x3F));
+      out += (char)(0x80 | ((c >> 6) & 0x3F));
+      out += (char)(0x80 | (c & 0x3F));
+    }
+  }
+  bool hex4(unsigned &v) {
+    if (end - p < 4) return false;
+    v = 0;
+    for (int i = 0; i < 4; ++i) {
+      const char c = *p++;
+      v <<= 4;
+      if (c >= '0' && c <= '9') v |= (unsigned)(c - '0');
+      else if (c >= 'a' && c <= 'f') v |= (unsigned)(c - 'a' + 10);
+      else if (c >= 'A' && c <= 'F') v |= (unsigned)(c - 'A' + 10);
+      else return false;
+    }
+    return true;
+  }
+  bool string(std::string &out) {
+    if (p >= end || *p != '"') return false;
+    ++p;
+    while (p < end && *p != '"') {
+      if (*p == '\\') {
+        if (++p >= end) return false;
+        const char e = *p++;
+        switch (e) {
+          case '"': out += '"'; break;
+          case '\\': out += '\\'; break;
+          case '/': out += '/'; break;
+          case 'b': out += '\b'; break;
+          case 'f': out += '\f'; break;
+          case 'n': out += '\n'; break;
+          case 'r': out += '\r'; break;
+          case 't': out += '\t'; break;
+          case 'u': {
+            unsigned c;
+            if (!hex4(c)) return false;
+            if (c >= 0xD800 && c < 0xDC00 && end - p >= 6 && p[0] == '\\' && p[1] == 'u') {
+              p += 2;
+              unsigned lo;
+              if (!hex4(lo)) return false;
+              c = 0x10000 + ((c - 0xD800) << 10) + (lo - 0xDC00);
+            }
+            utf8(out, c);
+            break;
+          }
+          default: return false;
+        }
+      } else {
+        out += *p++;
+      }
+    }
+    if (p >= end) return false;
+    ++p;
+    return true;
+  }
+  bool value(Json &v, int depth) {
+    if (depth > 64) return false;
+    ws();
+    if (p >= end) return false;
+    if (*p == '{') {
+      ++p;
+      v.kind = Json::OBJ;
+      ws();
+      if (p < end && *p == '}') return ++p, true;
+      for (;;) {
+        ws();
+        std::string k;
+        if (!string(k)) return false;
+        ws();
+        if (p >= end || *p != ':') return false;
+        ++p;
+        Json c;
+        if (!value(c, depth + 1)) return false;
+        v.obj.emplace_back(std::move(k), std::move(c));
+        ws();
+        if (p < end && *p == ',') { ++p; continue; }
+        if (p < end && *p == '}') return ++p, true;
+        return false;
+      }
+    }
+    if (*p == '[') {
+      ++p;
+      v.kind = Json::ARR;
+      ws();
+      if (p < end && *p == ']') return ++p, true;
+      for (;;) {
+        Json c;
+        if (!value(c, depth + 1)) return false;
+        v.arr.push_back(std::move(c));
+        ws();
+        if (p < end && *p == ',') { ++p; continue; }
+        if (p < end && *p == ']') return ++p, true;
+        return false;
+      }
+    }
+    if (*p == '"') {
+      v.kind = Json::STR;
+      return string(v.str);
+    }
+    if (lit("true")) { v.kind = Json::BOOL; v.num = 1; return true; }
+    if (lit("false")) { v.kind = Json::BOOL; return true; }
+    if (lit("null")) { v.kind = Json::NUL; return true; }
+    const std::string s(p, (size_t)(end - p) < 64 ? (size_t)(end - p) : 64);
+    char *stop = nullptr;
+    const double d = strtod(s.c_str(), &stop);
+    if (stop == s.c_str()) return false;
+    p += stop - s.c_str();
+    v.kind = Json::NUM;
+    v.num = d;
+    return true;
+  }
+};
+
+bool parse_json(const std::string &text, Json &out) {
+  JsonParser jp{text.data(), text.data() + text.size()};
+  if (!jp.value(out, 0)) return false;
+  jp.ws();
+  return jp.p == jp.end;
+}
+
+bool read_file(const std::string &path, std::string &out) {
+  const int fd = open(path.c_str(), O_RDONLY);
+  if (fd < 0) return false;
+  out.clear();
+  char buf[1 << 16];
+  for (;;) {
+    const ssize_t n = read(fd, buf, sizeof buf);
+    if (n < 0) { close(fd); return false; }
+    if (n == 0) break;
+    out.append(buf, (size_t)n);
+  }
+  close(fd);
+  return true;
+}
+
+bool pread_all(int fd, void *dst, size_t n, size_t off) {
+  uint8_t *d = static_cast<uint8_t *>(dst);
+  while (n) {
+    const ssize_t r = pread(fd, d, n, (off_t)off);
+    if (r <= 0) return false;
+    d += r;
+    n -= (size_t)r;
+    off += (size_t)r;
+  }
+  return true;
+}
+
+bool valid_utf8(const char *s) {
+  const unsigned char *u = reinterpret_cast<const unsigned char *>(s);
+  while (*u) {
+    int n = *u < 0x80 ? 0 : (*u >> 5) == 6 ? 1 : (*u >> 4) == 14 ? 2 : (*u >> 3) == 30 ? 3 : -1;
+    if (n < 0) return false;
+    ++u;
+    while (n--) {
+      if ((*u & 0xC0) != 0x80) return false;
+      ++u;
+    }
+  }
+  return true;
+}
+
+// bf16::from_f32 (half 2.7.1, as c_ffi.rs:323 calls it): RNE, NaN made quiet.
+uint16_t f32_to_bf16_host(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x0040u);
+  return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// the source
+// ---------------------------------------------------------------------------
+
+struct TensorRef {
+  std::string dtype;
+  std::vector<int64_t> shape;
+  size_t offset = 0, bytes = 0;  // absolute file offset, length
+};
+
+struct Shard {
+  int fd = -1;
+  std::unordered_map<std::string, TensorRef> tensors;
+  ~Shard() {
+    if (fd >= 0) close(fd);
+  }
+};
+
+struct DeviceExpert {
+  void *blob = nullptr;  // the tiled sections
+  cascadia_int4_expert e{};
+  uint32_t hidden = 0, inter = 0, group = 0, sdt = 0;
+};
+
+}  // namespace
+
+struct CascadiaInt4Source {
+  std::string dir;
+  int device = 0;
+  std::unordered_map<std::string, std::string> weight_map;  // tensor -> shard file
+  std::unordered_map<std::string, std::unique_ptr<Shard>> shards;
+  std::map<std::pair<uint32_t, uint32_t>, DeviceExpert> experts;
+  hipStream_t stream = nullptr;
+  uint16_t *x_dev = nullptr, *out_dev = nullptr;
+  void *ws = nullptr;
+  size_t io_elems = 0, ws_bytes = 0;
+  std::mutex mu;
+};
+
+namespace {
+
+Shard *shard_of(CascadiaInt4Source *s, const std::string &file) {
+  auto it = s->shards.find(file);
+  if (it != s->shards.end()) return it->second.get();
+  auto sh = std::make_unique<Shard>();
+  sh->fd = open((s->dir + "/" + file).c_str(), O_RDONLY);
+  if (sh->fd < 0) return nullptr;
+  uint8_t hl[8];
+  if (!pread_all(sh->fd, hl, 8, 0)) return nullptr;
+  uint64_t n = 0;
+  for (int i = 7; i >= 0; --i) n = (n << 8) | hl[i];
+  if (n > (1ull << 30)) return nullptr;
+  std::string hdr(n, '\0');
+  if (!pread_all(sh->fd, &hdr[0], n, 8)) return nullptr;
+  Json j;
+  if (!parse_json(hdr, j) || j.kind != Json::OBJ) return nullptr;
+  const size_t data0 = 8 + n;
+  for (const auto &kv : j.obj) {
+    if (kv.first == "__metadata__") continue;
+    const Json *off = kv.second.get("data_offsets");
+    if (!off || off->kind != Json::ARR || off->arr.size() != 2) return nullptr;
+    const double a = off->arr[0].num, b = off->arr[1].num;
+    if (b < a) continue;  // safetensors_source.rs:107-109
+    TensorRef t;
+    t.offset = data0 + (size_t)a;
+    t.bytes = (size_t)(b - a);
+    if (const Json *d = kv.second.get("dtype")) t.dtype = d->str;
+    if (const Json *sh2 = kv.second.get("shape"))
+      for (const auto &e : sh2->arr) t.shape.push_back((int64_t)e.num);
+    sh->tensors.emplace(kv.first, std::move(t));
+  }
+  Shard *raw = sh.get();
+  s->shards.emplace(file, std::move(sh));
+  return raw;
+}
+
+bool tensor(CascadiaInt4Source *s, const std::string &name, Shard **sh, const TensorRef **t) {
+  auto it = s->weight_map.find(name);
+  if (it == s->weight_map.end()) return false;
+  *sh = shard_of(s, it->second);
+  if (!*sh) return false;
+  auto jt = (*sh)->tensors.find(name);
+  if (jt == (*sh)->tensors.end()) return false;
+  *t = &jt->second;
+  return true;
+}
+
+// 0, -2 (the expert's tensors missing or inconsistent), -3 (HIP failure)
+int load_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, DeviceExpert **out) {
+  const auto key = std::make_pair(layer, expert);
+  auto it = s->experts.find(key);
+  if (it != s->experts.end()) {
+    *out = &it->second;
+    return 0;
+  }
+  const std::string base = "language_model.model.layers." + std::to_string(layer) +
+                           ".mlp.experts." + std::to_string(expert) + ".";
+  static const char *kNames[6] = {"gate_proj.weight_packed", "gate_proj.weight_scale",
+                                  "up_proj.weight_packed",   "up_proj.weight_scale",
+                                  "down_proj.weight_packed", "down_proj.weight_scale"};
+  Shard *sh[6];
+  const TensorRef *t[6];
+  for (int i = 0; i < 6; ++i)
+    if (!tensor(s, base + kNames[i], &sh[i], &t[i])) return -2;
+  // dims from the gate tensors: packed [inter, hidden / 8] int32 (or bytes of
+  // inter * hidden / 2), scales [inter, hidden / G]
+  if (t[0]->shape.size() != 2 || t[1]->shape.size() != 2) return -2;
+  const int64_t inter = t[0]->shape[0];
+  const int64_t hidden = t[0]->dtype == "U8" || t[0]->dtype == "I8" ? t[0]->shape[1] * 2
+                                                                     : t[0]->shape[1] * 8;
+  if (inter <= 0 || hidden <= 0 || t[1]->shape[0] != inter || t[1]->shape[1] <= 0 ||
+      hidden % t[1]->shape[1])
+    return -2;
+  const int64_t group = hidden / t[1]->shape[1];
+  const uint32_t sdt = t[1]->dtype == "F16" ? CASCADIA_INT4_SCALE_F16 : CASCADIA_INT4_SCALE_BF16;
+  const size_t pin = (size_t)inter * hidden / 2, sin = (size_t)inter * (hidden / group) * 2;
+  const size_t pdn = (size_t)hidden * inter / 2, sdn = (size_t)hidden * (inter / group) * 2;
+  const size_t want[6] = {pin, sin, pin, sin, pdn, sdn};
+  for (int i = 0; i < 6; ++i)
+    if (t[i]->bytes != want[i]) return -2;
+  if (group % 32 || inter % group || inter > (1 << 30) || hidden > (1 << 30)) return -2;
+
+  const size_t flat = cascadia_int4_expert_bytes((uint32_t)hidden, (uint32_t)inter, (uint32_t)group);
+  const size_t tiled =
+      cascadia_int4_expert_tiled_bytes((uint32_t)hidden, (uint32_t)inter, (uint32_t)group);
+  if (!flat || !tiled) return -2;
+  void *host = nullptr, *dflat = nullptr, *dtiled = nullptr;
+  int rc = 0;
+  if (hipHostMalloc(&host, flat, hipHostMallocDefault) != hipSuccess) return -3;
+  {  // the six tensors in flat-blob order (format.rs:35-47)
+    size_t off = 0;
+    for (int i = 0; i < 6 && !rc; ++i) {
+      if (!pread_all(sh[i]->fd, static_cast<uint8_t *>(host) + off, want[i], t[i]->offset))
+        rc = -2;
+      off += want[i];
+    }
+  }
+  DeviceExpert de;
+  cascadia_int4_expert src{};
+  if (!rc && (hipMalloc(&dflat, flat) != hipSuccess || hipMalloc(&dtiled, tiled) != hipSuccess))
+    rc = -3;
+  if (!rc && hipMemcpyAsync(dflat, host, flat, hipMemcpyHostToDevice, s->stream) != hipSuccess)
+    rc = -3;
+  if (!rc && cascadia_int4_expert_from_flat(static_cast<uint8_t *>(dflat), (uint32_t)hidden,
+                                            (uint32_t)inter, (uint32_t)group, &src) != 0)
+    rc = -2;
+  if (!rc && cascadia_int4_tile_expert((uint32_t)hidden, (uint32_t)inter, (uint32_t)group, &src,
+                                       static_cast<uint8_t *>(dtiled), &de.e, s->stream) != 0)
+    rc = -3;
+  if (!rc && hipStreamSynchronize(s->stream) != hipSuccess) rc = -3;
+  (void)hipHostFree(host);
+  if (dflat) (void)hipFree(dflat);
+  if (rc) {
+    if (dtiled) (void)hipFree(dtiled);
+    return rc;
+  }
+  de.blob = dtiled;
+  de.hidden = (uint32_t)hidden;
+  de.inter = (uint32_t)inter;
+  de.group = (uint32_t)group;
+  de.sdt = sdt;
+  *out = &s->experts.emplace(key, de).first->second;
+  return 0;
+}
+
+// Make the handle's device current for the call; restore the caller's after.
+struct DeviceScope {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceScope(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) return;
+    ok = prev == dev || hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceScope() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int cascadia_int4_open_source(const char *model_dir, CascadiaInt4Source **out_handle) {
+  if (!model_dir || !out_handle) return -1;
+  if (!valid_utf8(model_dir)) return -2;
+  auto s = std::make_unique<CascadiaInt4Source>();
+  s->dir = model_dir;
+  std::string text;
+  Json idx;
+  if (!read_file(s->dir + "/model.safetensors.index.json", text) || !parse_json(text, idx))
+    return -3;
+  const Json *wm = idx.get("weight_map");
+  if (!wm || wm->kind != Json::OBJ) return -3;
+  for (const auto &kv : wm->obj)
+    if (kv.second.kind == Json::STR) s->weight_map.emplace(kv.first, kv.second.str);
+  if (hipGetDevice(&s->device) != hipSuccess) return -3;
+  if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) return -3;
+  *out_handle = s.release();
+  return 0;
+}
+
+void cascadia_int4_destroy_source(CascadiaInt4Source *handle) {
+  if (!handle) return;
+  {
+    DeviceScope ds(handle->device);
+    if (handle->stream) (void)hipStreamSynchronize(handle->stream);
+    for (auto &kv : handle->experts) (void)hipFree(kv.second.blob);
+    if (handle->x_dev) (void)hipFree(handle->x_dev);
+    if (handle->out_dev) (void)hipFree(handle->out_dev);
+    if (handle->ws) (void)hipFree(handle->ws);
+    if (handle->stream) (void)hipStreamDestroy(handle->stream);
+  }
+  delete handle;
+}
+
+int cascadia_int4_prewarm(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert) {
+  if (!handle) return -1;
+  std::lock_guard<std::mutex> lk(handle->mu);
+  DeviceScope ds(handle->device);
+  if (!ds.ok) return -3;
+  DeviceExpert *de = nullptr;
+  return load_expert(handle, layer, expert, &de);
+}
+
+int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert,
+                                 const float *x_f32, float *out_f32) {
+  if (!handle || !x_f32 || !out_f32) return -1;
+  std::lock_guard<std::mutex> lk(handle->mu);
+  DeviceScope ds(handle->device);
+  if (!ds.ok) return -3;
+  DeviceExpert *de = nullptr;
+  if (int rc = load_expert(handle, layer, expert, &de)) return rc;
+  const uint32_t h = de->hidden;
+  const size_t need_ws = cascadia_int4_ffn_workspace_bytes(h, de->inter, de->group, 1);
+  if (handle->io_elems < h) {
+    if (handle->x_dev) (void)hipFree(handle->x_dev);
+    if (handle->out_dev) (void)hipFree(handle->out_dev);
+    handle->x_dev = handle->out_dev = nullptr;
+    handle->io_elems = 0;
+    if (hipMalloc(&handle->x_dev, (size_t)h * 2) != hipSuccess ||
+        hipMalloc(&handle->out_dev, (size_t)h * 2) != hipSuccess)
+      return -3;
+    handle->io_elems = h;
+  }
+  if (handle->ws_bytes < need_ws) {
+    if (handle->ws) (void)hipFree(handle->ws);
+    handle->ws = nullptr;
+    handle->ws_bytes = 0;
+    if (hipMalloc(&handle->ws, need_ws) != hipSuccess) return -3;
+    handle->ws_bytes = need_ws;
+  }
+  std::vector<uint16_t> xb(h), ob(h);
+  for (uint32_t i = 0; i < h; ++i) xb[i] = f32_to_bf16_host(x_f32[i]);  // c_ffi.rs:323
+  if (hipMemcpyAsync(handle->x_dev, xb.data(), (size_t)h * 2, hipMemcpyHostToDevice,
+                     handle->stream) != hipSuccess)
+    return -3;
+  if (cascadia_int4_expert_forward_device(h, de->inter, de->group, de->sdt, &de->e, handle->x_dev,
+                                          1, handle->out_dev, handle->ws, handle->stream) != 0)
+    return -3;
+  if (hipMemcpyAsync(ob.data(), handle->out_dev, (size_t)h * 2, hipMemcpyDeviceToHost,
+                     handle->stream) != hipSuccess ||
+      hipStreamSynchronize(handle->stream) != hipSuccess)
+    return -3;
+  for (uint32_t i = 0; i < h; ++i) {  // bf16 -> f32, c_ffi.rs:336-338
+    const uint32_t b = (uint32_t)ob[i] << 16;
+    memcpy(&out_f32[i], &b, 4);
+  }
+  return 0;
+}
+
+}  // extern "C"

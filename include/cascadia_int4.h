@@ -245,6 +245,26 @@ int cascadia_int4_moe_forward(const cascadia_int4_moe_layer *layer,
 int cascadia_int4_debug_dequant(const cascadia_int4_layout *layout, const uint8_t *packed,
                                 const uint8_t *scale_bits, float *w_out, void *stream);
 
+/* The crate's C handle API (src/c_ffi.rs:35-341), same names, signatures
+ * and codes.  A source is a safetensors model directory
+ * (model.safetensors.index.json + shards; expert tensors
+ * language_model.model.layers.L.mlp.experts.E.{gate,up,down}_proj.weight_{packed,scale},
+ * packed int32 = the crate's bytes, scales bf16 or f16).  Experts are read
+ * once, uploaded and tiled into HBM on first use (prewarm does that load, the
+ * analogue of the crate's page-in) and stay resident until destroy.
+ * expert_forward is synchronous and takes host arrays of the model's hidden
+ * size (the crate's HIDDEN = 7168): x f32 -> bf16 (RNE, NaN quiet), the
+ * expert FFN, bf16 -> f32.  Codes: 0 OK; -1 null; -2 invalid UTF-8 path
+ * (open) or an expert that cannot be read (prewarm / forward); -3 a
+ * directory that cannot be opened, or a HIP failure.  A handle serialises
+ * its calls. */
+typedef struct CascadiaInt4Source CascadiaInt4Source;
+int cascadia_int4_open_source(const char *model_dir, CascadiaInt4Source **out_handle);
+void cascadia_int4_destroy_source(CascadiaInt4Source *handle);
+int cascadia_int4_prewarm(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert);
+int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert,
+                                 const float *x_f32, float *out_f32);
+
 /* Load-time quantiser: bf16 weights [n_rows, k_cols] (device, 16-byte
  * aligned) -> packed nibbles [n_rows, k_cols/2] and bf16 group scales
  * [n_rows, k_cols/group_size], the crate layout.  Replaces

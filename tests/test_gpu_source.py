@@ -1,0 +1,113 @@
+"""The crate's C handle API (c_ffi.rs:35-341) over a safetensors model
+directory: open, prewarm, expert_forward (f32 in, bf16-rounded f32 out),
+destroy.  The directory is written by the test: an index file mapping tensor
+names to two shards, experts in the compressed-tensors form (packed int32 =
+the crate's bytes, bf16 or f16 scales), from the oracle's seeded generators;
+each result is compared with the oracle's expert_forward on the same bytes.
+The error codes that need no GPU are checked in the CPU tests below."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_gemm import assert_bf16_close
+
+BF16, F16 = 0, 1
+
+
+def write_model(path, experts):
+    """experts: {(layer, expert): (hidden, inter, group, sdt, flat bytes)}.
+    Even layers go to shard 0, odd to shard 1."""
+    shards = [{}, {}]
+    for (layer, e), (h, i, g, sdt, flat) in experts.items():
+        base = f"language_model.model.layers.{layer}.mlp.experts.{e}."
+        sdtype = "F16" if sdt == F16 else "BF16"
+        off = 0
+        for name, rows, cols in (("gate_proj", i, h), ("up_proj", i, h), ("down_proj", h, i)):
+            pb, sb = rows * cols // 2, rows * (cols // g) * 2
+            shards[layer % 2][base + name + ".weight_packed"] = ("I32", [rows, cols // 8], flat[off:off + pb])
+            off += pb
+            shards[layer % 2][base + name + ".weight_scale"] = (sdtype, [rows, cols // g], flat[off:off + sb])
+            off += sb
+    weight_map = {}
+    for si, tensors in enumerate(shards):
+        fname = f"model-{si + 1:05d}-of-00002.safetensors"
+        hdr, data, pos = {"__metadata__": {"format": "pt"}}, [], 0
+        for name, (dt, shape, b) in tensors.items():
+            hdr[name] = {"dtype": dt, "shape": shape, "data_offsets": [pos, pos + len(b)]}
+            data.append(bytes(b))
+            pos += len(b)
+            weight_map[name] = fname
+        hj = json.dumps(hdr).encode()
+        with open(os.path.join(path, fname), "wb") as f:
+            f.write(len(hj).to_bytes(8, "little"))
+            f.write(hj)
+            for b in data:
+                f.write(b)
+    with open(os.path.join(path, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {"total_size": 0}, "weight_map": weight_map}, f)
+
+
+def make_expert(orc, h, i, g, sdt, seed):
+    flat = orc.fill_bytes(seed, 60, orc.expert_bytes(h, i, g))
+    offs, sizes = orc.expert_offsets(h, i, g)
+    for s_ in (1, 3, 5):
+        flat[offs[s_]:offs[s_] + sizes[s_]] = orc.fill_scales(seed, 61 + s_, sizes[s_] // 2, sdt).view(np.uint8)
+    return flat
+
+
+@pytest.mark.gpu
+def test_handle_api_matches_oracle(orc, tmp_path):
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import cascadia_amd as cl
+
+    ex = {(0, 0): (512, 256, 32, BF16), (0, 3): (512, 256, 32, BF16), (1, 1): (512, 384, 64, F16),
+          (3, 2): (7168, 2048, 32, BF16)}  # the last at the crate's HIDDEN / INTERMEDIATE / G
+    data = {k: (*v, make_expert(orc, *v, 7 + 3 * k[0] + k[1])) for k, v in ex.items()}
+    write_model(str(tmp_path), data)
+    src = cl.ExpertSource(str(tmp_path))
+    src.prewarm(0, 3)
+    for (layer, e), (h, i, g, sdt, flat) in data.items():
+        x = orc.fill_normal_f32(layer * 10 + e, 77, h)
+        out = np.empty(h, np.float32)
+        src.expert_forward(layer, e, x, out)
+        want_bits = orc.cpu_expert_forward(orc.f32_to_bf16(x), 1, flat, h, i, g, sdt).reshape(-1)
+        # output is bf16 widened to f32 (c_ffi.rs:336-338)
+        assert np.all((out.view(np.uint32) & 0xFFFF) == 0), "not bf16-valued"
+        assert_bf16_close((out.view(np.uint32) >> 16).astype(np.uint16), want_bits, f"expert ({layer}, {e})")
+        # a second call (expert resident) gives the same bits
+        out2 = np.empty(h, np.float32)
+        src.expert_forward(layer, e, x, out2)
+        assert np.array_equal(out, out2)
+    with pytest.raises(cl.CascadiaInt4Error) as ei:
+        src.expert_forward(2, 0, np.zeros(512, np.float32), np.zeros(512, np.float32))
+    assert ei.value.rc == -2
+    with pytest.raises(cl.CascadiaInt4Error) as ei:
+        src.prewarm(0, 1)
+    assert ei.value.rc == -2
+    src.close()
+
+
+def test_handle_api_error_codes(tmp_path):
+    """Codes that need no GPU: null arguments -1, invalid UTF-8 -2, a directory
+    without an index -3, a malformed index -3 (c_ffi.rs:35-56)."""
+    import ctypes as C
+
+    import cascadia_amd as cl
+
+    L = cl.lib()
+    h = C.c_void_p()
+    assert L.cascadia_int4_open_source(None, C.byref(h)) == -1
+    assert L.cascadia_int4_open_source(str(tmp_path).encode(), None) == -1
+    assert L.cascadia_int4_open_source(b"\xff\xfe-not-utf8", C.byref(h)) == -2
+    assert L.cascadia_int4_open_source(str(tmp_path / "missing").encode(), C.byref(h)) == -3
+    (tmp_path / "model.safetensors.index.json").write_text('{"weight_map": {"a": ')
+    assert L.cascadia_int4_open_source(str(tmp_path).encode(), C.byref(h)) == -3
+    (tmp_path / "model.safetensors.index.json").write_text('{"metadata": {}}')
+    assert L.cascadia_int4_open_source(str(tmp_path).encode(), C.byref(h)) == -3
+    assert L.cascadia_int4_prewarm(None, 0, 0) == -1
+    assert L.cascadia_int4_expert_forward(None, 0, 0, None, None) == -1
+    L.cascadia_int4_destroy_source(None)  # null-safe
