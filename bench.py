@@ -251,6 +251,35 @@ def extra_measurements(cl, torch, args, sdt, copies):
                                    "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
                                    "bytes_per_step": b, "copies": ncs}
     del SH
+    # the activation-sparse expert (tau > 0, ffn_sparsity.rs:756-867) at one
+    # token: gate and down in full, up for the active rows only.  Called
+    # through the C entry point with no count output, so it captures.
+    import ctypes as C
+    xs1 = cl.fill_normal(torch.empty(h, dtype=torch.bfloat16, device="cuda"), 0, 23)
+    os1 = torch.empty(h, dtype=torch.bfloat16, device="cuda")
+    nc = len(copies.w)
+    for tau in (0.1, 0.3):
+        fr = cl.expert_forward_sparse(xs1.view(torch.int16), *copies.w[0].slices(),
+                                      os1.view(torch.int16), tau, group_size=g, scale_dtype=sdt,
+                                      tiling=cl.TILING_MFMA)
+        ex = [cl._lib.Expert(*(t.data_ptr() for t in W.slices()), cl.TILING_MFMA)
+              for W in copies.w]
+
+        def sparse(r, tau=tau):
+            cl.check("cascadia_int4_expert_forward_sparse", cl.lib().cascadia_int4_expert_forward_sparse(
+                h, i, g, sdt, C.byref(ex[r % nc]), xs1.data_ptr(), 1, tau, None, os1.data_ptr(),
+                None, None, torch.cuda.current_stream().cuda_stream))
+        for r in range(10):
+            sparse(r)
+        steps = 200
+        w, _ = graph_time(torch, sparse, steps)
+        t = w / steps
+        mat = i * h // 2 + i * (h // g) * 2
+        b = 2 * mat + int(round(fr * i)) * (h // 2 + (h // g) * 2) + h * 2 * 2
+        res[f"sparse_expert_M1_tau{tau}"] = {"us_per_call": round(t * 1e6, 2),
+                                             "active_frac": round(fr, 4),
+                                             "GB/s": round(b / t / 1e9, 1),
+                                             "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
     # config 2: prefill GEMM (bf16 in/out)
     for (m, nn) in PREFILL_SHAPES:
         pre = prefill_fn(cl, torch, m, nn, 4096, g, sdt)

@@ -15,7 +15,9 @@ from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertSou
                   debug_dequant, dequant_gemm_int4_multi_auto,
                   dequant_gemm_int4_multi_blocked_auto, dequant_gemv_int4,
                   dequant_gemv_int4_auto, expert_bytes, expert_forward, expert_forward_sparse,
-                  ffn_forward_sparse_f32, ffn_workspace_bytes, fill_bytes, fill_normal,
+                  expert_forward_sparse_per_channel, ffn_forward_sparse_f32,
+                  ffn_forward_sparse_f32_per_channel, ffn_sparse_workspace_bytes,
+                  ffn_workspace_bytes, fill_bytes, fill_normal,
                   fill_scales, gate_up_silu, gemm_int4_bf16, MoEExperts, moe_forward,
                   moe_workspace_bytes, quantize_int4_group, tile_weights, tiled_sizes)
 
@@ -24,7 +26,8 @@ __all__ = [
     "GROUP_SIZE", "HIDDEN", "INTERMEDIATE", "NIBBLES_PER_INT32", "ExpertSource", "ExpertWeights",
     "debug_dequant", "dequant_gemm_int4_multi_auto", "dequant_gemm_int4_multi_blocked_auto",
     "dequant_gemv_int4", "dequant_gemv_int4_auto", "expert_bytes", "expert_forward",
-    "expert_forward_sparse", "ffn_forward_sparse_f32", "ffn_workspace_bytes", "fill_bytes",
+    "expert_forward_sparse", "expert_forward_sparse_per_channel", "ffn_forward_sparse_f32",
+    "ffn_forward_sparse_f32_per_channel", "ffn_sparse_workspace_bytes", "ffn_workspace_bytes", "fill_bytes",
     "fill_normal", "fill_scales", "gate_up_silu", "gemm_int4_bf16", "tile_weights",
     "tiled_sizes", "TILING_CRATE", "TILING_MFMA", "MoEExperts", "moe_forward",
     "moe_workspace_bytes", "quantize_int4_group", "ROUTE_IDS", "ROUTE_SIGMOID_BIAS",

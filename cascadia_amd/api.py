@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes as C
 
+import numpy as np
 import torch
 
 from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, Expert, Layout, MoeLayer,
@@ -288,40 +289,94 @@ def expert_forward(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_pa
     return out_bf16
 
 
+def _sparse_call(x, weights, out, threshold, thresholds, group_size, scale_dtype, workspace,
+                 tiling, x_f32, hidden=None, intermediate=None):
+    """The shared body of the sparse entry points: returns the active
+    fraction per token row (a float for a 1-D x, else a list)."""
+    gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale = weights
+    _dev(x, "x"), _dev(out, "out")
+    if x_f32:
+        _expect(x.dtype == torch.float32 and out.dtype == torch.float32, "f32 in/out")
+    else:
+        _expect(_is_bf16_bits(x) and _is_bf16_bits(out), "x and out must be bf16")
+    h, inter = _ffn_dims(x, gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                         down_scale, group_size, hidden, tiling)
+    if intermediate is not None:
+        _expect(inter == intermediate,
+                f"intermediate {intermediate} != {inter} implied by gate_scale")
+    T = x.numel() // h
+    _expect(x.numel() == T * h and out.numel() == T * h, "x and out must be [n_tokens, hidden]")
+    thr = 0
+    if thresholds is not None:
+        _dev(thresholds, "thresholds")
+        # ffn_sparsity.rs:116-123: one threshold per intermediate lane
+        _expect(thresholds.dtype == torch.float32 and thresholds.numel() == inter,
+                f"per-channel thresholds length {thresholds.numel()} != gate_out length {inter}")
+        thr = thresholds.contiguous().data_ptr()
+    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
+                       tiling)
+    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
+    dense = thresholds is None and not threshold > 0.0  # SparsityMode::is_dense
+    counts = None if dense else torch.empty(T, dtype=torch.int32, device=x.device)
+    name = "cascadia_int4_ffn_forward_sparse_f32" if x_f32 else "cascadia_int4_expert_forward_sparse"
+    check(name, getattr(lib(), name)(h, inter, group_size, scale_dtype, C.byref(e), x.data_ptr(),
+                                     T, float(threshold), thr, out.data_ptr(),
+                                     0 if dense else counts.data_ptr(), ws, _stream()))
+    # the dense branch returns 1.0 without a host round trip (ffn_sparsity.rs:465-496)
+    # count / inter in f32, as the crate computes it (ffn_sparsity.rs:500)
+    frac = [1.0] * T if dense else [
+        float(np.float32(c) / np.float32(inter)) for c in counts.cpu().tolist()]
+    return frac[0] if x.dim() == 1 else frac
+
+
+def ffn_sparse_workspace_bytes(hidden, inter, n_tokens, group_size=GROUP_SIZE) -> int:
+    """Workspace bytes of the sparse entry points for n_tokens rows."""
+    return int(lib().cascadia_int4_ffn_sparse_workspace_bytes(hidden, inter, group_size,
+                                                              n_tokens))
+
+
 def expert_forward_sparse(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
                           down_scale, out_bf16, threshold, group_size=GROUP_SIZE,
-                          scale_dtype=SCALE_BF16):
-    """ffn_sparsity.rs:756-783.  threshold <= 0 is expert_forward (returns 1.0)."""
-    if threshold > 0.0:
-        raise NotImplementedError("activation-sparse (tau > 0) expert path is not built yet")
-    expert_forward(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
-                   down_scale, out_bf16, group_size, scale_dtype)
-    return 1.0
+                          scale_dtype=SCALE_BF16, workspace=None, tiling=TILING_CRATE):
+    """ffn_sparsity.rs:756-783: bf16 in/out, activation-sparse with the global
+    threshold (<= 0: expert_forward).  Returns the active fraction."""
+    return _sparse_call(x_bf16, (gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                                 down_scale), out_bf16, threshold, None, group_size,
+                        scale_dtype, workspace, tiling, False)
+
+
+def expert_forward_sparse_per_channel(x_bf16, gate_packed, gate_scale, up_packed, up_scale,
+                                      down_packed, down_scale, out_bf16, thresholds,
+                                      group_size=GROUP_SIZE, scale_dtype=SCALE_BF16,
+                                      workspace=None, tiling=TILING_CRATE):
+    """ffn_sparsity.rs:785-815: thresholds, device f32 [intermediate]."""
+    return _sparse_call(x_bf16, (gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                                 down_scale), out_bf16, 0.0, thresholds, group_size,
+                        scale_dtype, workspace, tiling, False)
 
 
 def ffn_forward_sparse_f32(x_f32, hidden, intermediate, gate_packed, gate_scale, up_packed,
                            up_scale, down_packed, down_scale, out_f32, threshold,
                            group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, workspace=None,
                            tiling=TILING_CRATE):
-    """Dense SwiGLU FFN, f32 in/out (ffn_sparsity.rs:373-496 at tau = 0).
+    """SwiGLU FFN, f32 in/out (ffn_sparsity.rs:373-538): threshold <= 0 is the
+    dense branch (the shared expert), > 0 the activation-sparse one.
     x_f32 / out_f32: [hidden] or [n_tokens, hidden].  Returns the active
-    fraction (1.0)."""
-    if threshold > 0.0:
-        raise NotImplementedError("activation-sparse (tau > 0) FFN path is not built yet")
-    _dev(x_f32, "x_f32"), _dev(out_f32, "out_f32")
-    _expect(x_f32.dtype == torch.float32 and out_f32.dtype == torch.float32, "f32 in/out")
-    h, inter = _ffn_dims(x_f32, gate_packed, gate_scale, up_packed, up_scale, down_packed,
-                         down_scale, group_size, hidden, tiling)
-    _expect(inter == intermediate, f"intermediate {intermediate} != {inter} implied by gate_scale")
-    T = x_f32.numel() // hidden
-    _expect(x_f32.numel() == T * hidden and out_f32.numel() == T * hidden, "[n_tokens, hidden]")
-    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
-                       tiling)
-    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
-    check("cascadia_int4_ffn_forward_f32", lib().cascadia_int4_ffn_forward_f32(
-        hidden, inter, group_size, scale_dtype, C.byref(e), x_f32.data_ptr(), T,
-        out_f32.data_ptr(), ws, _stream()))
-    return 1.0
+    fraction."""
+    return _sparse_call(x_f32, (gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                                down_scale), out_f32, threshold, None, group_size, scale_dtype,
+                        workspace, tiling, True, hidden, intermediate)
+
+
+def ffn_forward_sparse_f32_per_channel(x_f32, hidden, intermediate, gate_packed, gate_scale,
+                                       up_packed, up_scale, down_packed, down_scale, out_f32,
+                                       thresholds, group_size=GROUP_SIZE,
+                                       scale_dtype=SCALE_BF16, workspace=None,
+                                       tiling=TILING_CRATE):
+    """ffn_sparsity.rs:407-436: thresholds, device f32 [intermediate]."""
+    return _sparse_call(x_f32, (gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                                down_scale), out_f32, 0.0, thresholds, group_size, scale_dtype,
+                        workspace, tiling, True, hidden, intermediate)
 
 
 # ---------------------------------------------------------------------------

@@ -14,6 +14,7 @@
 #include "prefill.hpp"
 #include "quant.hpp"
 #include "skinny.hpp"
+#include "sparse.hpp"
 #include "synth.hpp"
 
 namespace {
@@ -267,6 +268,92 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Workspace of the activation-sparse FFN: gate output, SiLU, active lanes and
+// the intermediate ([n_tokens, inter] each), per-token counts, then split-K
+// partials of the largest of its GEMMs; at least what the dense branch needs.
+struct SparseWorkspace {
+  size_t lanes, counts, partials, total;
+};
+SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint32_t group,
+                                 uint32_t n_tokens) {
+  const cai4::SkinnyDevice d = device_props(dev);
+  size_t part = 0;
+  const cai4::SkinnyPlan plans[4] = {
+      cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_XF32,
+                        cai4::EPI_F32, d),
+      cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_BF16,
+                        cai4::EPI_F32, d),
+      cai4::skinny_plan((int)hidden, (int)inter, (int)group, (int)n_tokens, cai4::A_XF32,
+                        cai4::EPI_F32, d),
+      cai4::skinny_plan((int)hidden, (int)inter, (int)group, (int)n_tokens, cai4::A_XF32,
+                        cai4::EPI_BF16, d)};
+  for (const cai4::SkinnyPlan &p : plans) part = p.partial_bytes > part ? p.partial_bytes : part;
+  SparseWorkspace w;
+  w.lanes = align256((size_t)n_tokens * inter * 4);
+  w.counts = align256((size_t)n_tokens * 4);
+  w.partials = part;
+  w.total = 4 * w.lanes + w.counts + part;
+  const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group, n_tokens, true);
+  const FfnWorkspace b = ffn_workspace(dev, hidden, inter, group, n_tokens, false);
+  const size_t dense = f.planes + (f.partials > b.partials ? f.partials : b.partials);
+  if (dense > w.total) w.total = dense;
+  return w;
+}
+
+// ffn_forward_sparse_f32_mode / expert_forward_sparse_mode
+// (ffn_sparsity.rs:438-538, 756-867): thresholds == nullptr is the global
+// tau, dense (the ordinary FFN) when tau <= 0.
+int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
+                  const cascadia_int4_expert *e, const void *x, bool x_f32, uint32_t n_tokens,
+                  float tau, const float *thr, void *out, bool out_bf16, uint32_t *counts,
+                  void *workspace, hipStream_t st) {
+  if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
+  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
+  if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (n_tokens > 65535 || !aligned(x, 16) || (thr && !aligned(thr, 4)) ||
+      (counts && !aligned(counts, 4)) || (workspace && !aligned(workspace, 16)))
+    return CASCADIA_INT4_ERR_ARG;
+  if (!thr && tau <= 0.0f) {
+    int rc = ffn_common(hidden, inter, group, sdt, e, x, x_f32, n_tokens, out, out_bf16,
+                        workspace, st);
+    if (rc || !counts) return rc;
+    return hip_status(cai4::fill_u32(counts, (int)n_tokens, inter, st));
+  }
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const int amode = x_f32 ? cai4::A_XF32 : cai4::A_BF16;
+  if (!act_fits((int)n_tokens, (int)hidden, amode) ||
+      !act_fits((int)n_tokens, (int)inter, cai4::A_XF32))
+    return CASCADIA_INT4_ERR_ARG;
+  const SparseWorkspace w = sparse_workspace(dev, hidden, inter, group, n_tokens);
+  void *ws = workspace;
+  if (!ws) {
+    if (int rc = lib_workspace(dev, w.total, &ws)) return rc;
+  }
+  uint8_t *b = static_cast<uint8_t *>(ws);
+  float *gate = reinterpret_cast<float *>(b);
+  float *sg = reinterpret_cast<float *>(b + w.lanes);
+  uint32_t *act = reinterpret_cast<uint32_t *>(b + 2 * w.lanes);
+  float *mid = reinterpret_cast<float *>(b + 3 * w.lanes);
+  uint32_t *cnt = reinterpret_cast<uint32_t *>(b + 4 * w.lanes);
+  void *part = w.partials ? b + 4 * w.lanes + w.counts : nullptr;
+  int rc = run_gemm(e->gate_packed, e->gate_scale, nullptr, nullptr, (int)inter, (int)hidden,
+                    (int)group, (int)sdt, (int)e->tiling, x, nullptr, amode, (int)n_tokens, gate,
+                    nullptr, cai4::EPI_F32, st, part);
+  if (rc) return rc;
+  if ((rc = hip_status(cai4::sparse_mask(gate, (int)n_tokens, (int)inter, tau, thr, sg, act, cnt,
+                                         counts, mid, st))))
+    return rc;
+  if ((rc = hip_status(cai4::rows_subset_up(e->up_packed, e->up_scale, (int)inter, (int)hidden,
+                                            (int)group, (int)sdt, (int)e->tiling, x, x_f32,
+                                            (int)n_tokens, act, cnt, sg, mid, st))))
+    return rc;
+  return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
+                  (int)group, (int)sdt, (int)e->tiling, mid, nullptr, cai4::A_XF32,
+                  (int)n_tokens, out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st,
+                  part);
+}
 // offsets of the six sections of a tiled expert blob
 void tiled_expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[7]) {
   size_t gp, gs, dp, ds;
@@ -778,6 +865,37 @@ int cascadia_int4_ffn_forward_f32(uint32_t hidden, uint32_t inter, uint32_t grou
                                   void *workspace, void *stream) {
   return ffn_common(hidden, inter, group_size, scale_dtype, expert, x, true, n_tokens, out,
                     false, workspace, (hipStream_t)stream);
+}
+
+size_t cascadia_int4_ffn_sparse_workspace_bytes(uint32_t hidden, uint32_t inter,
+                                                uint32_t group_size, uint32_t n_tokens) {
+  int dev;
+  if (current_device(&dev)) return 0;
+  if (group_size == 0 || group_size % 32) return 0;
+  return sparse_workspace(dev, hidden, inter, group_size, n_tokens).total;
+}
+
+int cascadia_int4_ffn_forward_sparse_f32(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                         uint32_t scale_dtype,
+                                         const cascadia_int4_expert *expert, const float *x,
+                                         uint32_t n_tokens, float threshold,
+                                         const float *thresholds, float *out,
+                                         uint32_t *active_counts, void *workspace,
+                                         void *stream) {
+  return sparse_common(hidden, inter, group_size, scale_dtype, expert, x, true, n_tokens,
+                       threshold, thresholds, out, false, active_counts, workspace,
+                       (hipStream_t)stream);
+}
+
+int cascadia_int4_expert_forward_sparse(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                        uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                        const uint16_t *x_bf16, uint32_t n_tokens,
+                                        float threshold, const float *thresholds,
+                                        uint16_t *out_bf16, uint32_t *active_counts,
+                                        void *workspace, void *stream) {
+  return sparse_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false, n_tokens,
+                       threshold, thresholds, out_bf16, true, active_counts, workspace,
+                       (hipStream_t)stream);
 }
 
 int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_size,

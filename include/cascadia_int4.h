@@ -177,6 +177,35 @@ int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_s
                                const void *x, uint32_t x_is_f32, uint32_t n_tokens,
                                float *inter_out, void *stream);
 
+/* Activation-sparse expert FFN (src/ffn_sparsity.rs:438-538
+ * ffn_forward_sparse_f32_mode, :756-867 expert_forward_sparse_mode; the
+ * mask :131-179): gate in full, s = stable SiLU(gate), lanes with |s| >=
+ * cutoff * max|s| active (cutoff = threshold, or thresholds[i] when
+ * thresholds, device f32 [inter], is not NULL: SparsityMode::PerChannel), up
+ * for the active rows only, intermediate s * up on them and 0 elsewhere, down
+ * in full.  threshold <= 0 with thresholds NULL is the dense FFN
+ * (cascadia_int4_ffn_forward_f32 / cascadia_int4_expert_forward_device).
+ * Every token row is masked on its own; active_counts (device u32
+ * [n_tokens], may be NULL) receives each row's active-lane count (the
+ * crate's return value is count / inter).  _f32: x, out f32; _sparse: x, out
+ * bf16 bits, out one RNE rounding of the f32 result.  workspace: >=
+ * cascadia_int4_ffn_sparse_workspace_bytes, or NULL for the library's. */
+size_t cascadia_int4_ffn_sparse_workspace_bytes(uint32_t hidden, uint32_t inter,
+                                                uint32_t group_size, uint32_t n_tokens);
+int cascadia_int4_ffn_forward_sparse_f32(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                         uint32_t scale_dtype,
+                                         const cascadia_int4_expert *expert, const float *x,
+                                         uint32_t n_tokens, float threshold,
+                                         const float *thresholds, float *out,
+                                         uint32_t *active_counts, void *workspace,
+                                         void *stream);
+int cascadia_int4_expert_forward_sparse(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                        uint32_t scale_dtype, const cascadia_int4_expert *expert,
+                                        const uint16_t *x_bf16, uint32_t n_tokens,
+                                        float threshold, const float *thresholds,
+                                        uint16_t *out_bf16, uint32_t *active_counts,
+                                        void *workspace, void *stream);
+
 /* Dense SwiGLU FFN, f32 in / f32 out, no rounding: ffn_forward_sparse_f32 at
  * tau = 0 (src/ffn_sparsity.rs:373-496), used for the shared expert
  * (shell_int4.rs:629).  x, out: [n_tokens, hidden] f32. */

@@ -64,6 +64,9 @@ def _declare(L):
         "or_ffn_forward_f32": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp]),
         "or_expert_forward_sparse": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp]),
         "or_build_active_mask": (sz, [vp, sz, f32, vp, vp]),
+        "or_build_active_mask_mode": (sz, [vp, sz, f32, vp, vp, vp]),
+        "or_ffn_forward_f32_mode": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp, vp]),
+        "or_expert_forward_sparse_mode": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp, vp]),
         "or_route_sigmoid_bias": (None, [vp, vp, sz, sz, f32, i32, vp, vp]),
         "or_route_softmax_topk": (None, [vp, sz, sz, vp, vp]),
         "or_moe_routed": (None, [vp, sz, sz, sz, sz, i32, i32, vp, sz, sz, vp, vp, sz, f32, vp]),
@@ -173,26 +176,40 @@ def expert_forward(x_bf16, flat, hidden, inter, group, sdt, order=ORDER_AVX512) 
     return out
 
 
-def ffn_forward_f32(x, flat, hidden, inter, group, sdt, tau=0.0, order=ORDER_AVX512):
+def _thr(thresholds, n):
+    if thresholds is None:
+        return None, None
+    t = _c(thresholds, np.float32)
+    assert t.size == n, "one threshold per intermediate lane"
+    return t, _p(t)
+
+
+def ffn_forward_f32(x, flat, hidden, inter, group, sdt, tau=0.0, order=ORDER_AVX512,
+                    thresholds=None):
     x, flat = _c(x, np.float32), _c(flat, np.uint8)
+    t, tp = _thr(thresholds, inter)
     out = np.empty(hidden, np.float32)
-    frac = lib().or_ffn_forward_f32(_p(x), hidden, inter, group, sdt, order, _p(flat), tau, _p(out))
+    frac = lib().or_ffn_forward_f32_mode(_p(x), hidden, inter, group, sdt, order, _p(flat),
+                                         tau, tp, _p(out))
     return out, float(frac)
 
 
-def expert_forward_sparse(x_bf16, flat, hidden, inter, group, sdt, tau, order=ORDER_AVX512):
+def expert_forward_sparse(x_bf16, flat, hidden, inter, group, sdt, tau, order=ORDER_AVX512,
+                          thresholds=None):
     x_bf16, flat = _c(x_bf16, np.uint16), _c(flat, np.uint8)
+    t, tp = _thr(thresholds, inter)
     out = np.empty(hidden, np.uint16)
-    frac = lib().or_expert_forward_sparse(_p(x_bf16), hidden, inter, group, sdt, order,
-                                          _p(flat), tau, _p(out))
+    frac = lib().or_expert_forward_sparse_mode(_p(x_bf16), hidden, inter, group, sdt, order,
+                                               _p(flat), tau, tp, _p(out))
     return out, float(frac)
 
 
-def build_active_mask(gate_out, tau):
+def build_active_mask(gate_out, tau, thresholds=None):
     g = _c(gate_out, np.float32)
+    t, tp = _thr(thresholds, g.size)
     silu = np.empty_like(g)
     act = np.empty(g.size, np.uint32)
-    n = lib().or_build_active_mask(_p(g), g.size, tau, _p(silu), _p(act))
+    n = lib().or_build_active_mask_mode(_p(g), g.size, tau, tp, _p(silu), _p(act))
     return silu, act[:n].copy()
 
 

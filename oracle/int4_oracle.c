@@ -273,10 +273,13 @@ void or_expert_forward(const uint16_t *x_bf16, size_t hidden, size_t inter, size
   free(o);
 }
 
-/* ffn_sparsity.rs:131-179 (Global mode).  Returns the number of active
+/* ffn_sparsity.rs:131-179 (build_active_mask_mode).  thresholds == NULL is
+ * SparsityMode::Global(tau); otherwise PerChannel(thresholds[0..n]), dense
+ * when every threshold is <= 0 (:85-90).  Returns the number of active
  * lanes; active_out receives them in ascending order. */
-size_t or_build_active_mask(const float *gate_out, size_t n, float tau, float *silu_out,
-                            uint32_t *active_out) {
+size_t or_build_active_mask_mode(const float *gate_out, size_t n, float tau,
+                                 const float *thresholds, float *silu_out,
+                                 uint32_t *active_out) {
   float max_abs = 0.0f;
   for (size_t i = 0; i < n; i++) {
     float g = gate_out[i], s;
@@ -290,21 +293,32 @@ size_t or_build_active_mask(const float *gate_out, size_t n, float tau, float *s
     float a = fabsf(s);
     if (a > max_abs) max_abs = a;
   }
+  int dense = thresholds ? 1 : tau <= 0.0f;
+  if (thresholds)
+    for (size_t i = 0; i < n; i++)
+      if (!(thresholds[i] <= 0.0f)) dense = 0;
   size_t cnt = 0;
-  if (max_abs == 0.0f || tau <= 0.0f) {
+  if (max_abs == 0.0f || dense) {
     for (size_t i = 0; i < n; i++) active_out[cnt++] = (uint32_t)i;
     return cnt;
   }
-  float cutoff = tau * max_abs;
-  for (size_t i = 0; i < n; i++)
+  for (size_t i = 0; i < n; i++) {
+    float cutoff = (thresholds ? thresholds[i] : tau) * max_abs;
     if (fabsf(silu_out[i]) >= cutoff) active_out[cnt++] = (uint32_t)i;
+  }
   return cnt;
 }
 
-/* ffn_sparsity.rs:438-538 (Global mode). */
-float or_ffn_forward_f32(const float *x, size_t hidden, size_t inter, size_t group,
-                         int scale_dtype, int order, const uint8_t *expert_flat,
-                         float tau, float *out) {
+size_t or_build_active_mask(const float *gate_out, size_t n, float tau, float *silu_out,
+                            uint32_t *active_out) {
+  return or_build_active_mask_mode(gate_out, n, tau, NULL, silu_out, active_out);
+}
+
+/* ffn_sparsity.rs:438-538 (ffn_forward_sparse_f32_mode; thresholds as in
+ * or_build_active_mask_mode). */
+float or_ffn_forward_f32_mode(const float *x, size_t hidden, size_t inter, size_t group,
+                              int scale_dtype, int order, const uint8_t *expert_flat,
+                              float tau, const float *thresholds, float *out) {
   size_t off[6];
   or_expert_offsets(hidden, inter, group, off);
   float *g = (float *)malloc(inter * sizeof(float));
@@ -313,14 +327,18 @@ float or_ffn_forward_f32(const float *x, size_t hidden, size_t inter, size_t gro
   float frac = 1.0f;
   or_gemv(expert_flat + off[0], expert_flat + off[1], x, inter, hidden, group, scale_dtype,
           order, g);
-  if (tau <= 0.0f) { /* dense branch :465-496 */
+  int dense = thresholds ? 1 : tau <= 0.0f;
+  if (thresholds)
+    for (size_t i = 0; i < inter; i++)
+      if (!(thresholds[i] <= 0.0f)) dense = 0;
+  if (dense) { /* dense branch :465-496 */
     or_gemv(expert_flat + off[2], expert_flat + off[3], x, inter, hidden, group,
             scale_dtype, order, u);
     for (size_t i = 0; i < inter; i++) m[i] = silu_plain(g[i]) * u[i];
   } else { /* sparse branch :499-537 */
     float *sg = (float *)malloc(inter * sizeof(float));
     uint32_t *act = (uint32_t *)malloc(inter * sizeof(uint32_t));
-    size_t na = or_build_active_mask(g, inter, tau, sg, act);
+    size_t na = or_build_active_mask_mode(g, inter, tau, thresholds, sg, act);
     frac = (float)na / (float)inter;
     or_gemv_rows_subset(expert_flat + off[2], expert_flat + off[3], x, inter, hidden, group,
                         scale_dtype, order, act, na, u);
@@ -336,11 +354,24 @@ float or_ffn_forward_f32(const float *x, size_t hidden, size_t inter, size_t gro
   return frac;
 }
 
-/* ffn_sparsity.rs:756-867 (Global mode). */
-float or_expert_forward_sparse(const uint16_t *x_bf16, size_t hidden, size_t inter,
-                               size_t group, int scale_dtype, int order,
-                               const uint8_t *expert_flat, float tau, uint16_t *out_bf16) {
-  if (tau <= 0.0f) {
+float or_ffn_forward_f32(const float *x, size_t hidden, size_t inter, size_t group,
+                         int scale_dtype, int order, const uint8_t *expert_flat,
+                         float tau, float *out) {
+  return or_ffn_forward_f32_mode(x, hidden, inter, group, scale_dtype, order, expert_flat, tau,
+                                 NULL, out);
+}
+
+/* ffn_sparsity.rs:756-867 (expert_forward_sparse_mode; thresholds as in
+ * or_build_active_mask_mode). */
+float or_expert_forward_sparse_mode(const uint16_t *x_bf16, size_t hidden, size_t inter,
+                                    size_t group, int scale_dtype, int order,
+                                    const uint8_t *expert_flat, float tau,
+                                    const float *thresholds, uint16_t *out_bf16) {
+  int dense = thresholds ? 1 : tau <= 0.0f;
+  if (thresholds)
+    for (size_t i = 0; i < inter; i++)
+      if (!(thresholds[i] <= 0.0f)) dense = 0;
+  if (dense) {
     or_expert_forward(x_bf16, hidden, inter, group, scale_dtype, order, expert_flat,
                       out_bf16);
     return 1.0f;
@@ -348,12 +379,19 @@ float or_expert_forward_sparse(const uint16_t *x_bf16, size_t hidden, size_t int
   float *x = (float *)malloc(hidden * sizeof(float));
   float *o = (float *)malloc(hidden * sizeof(float));
   for (size_t i = 0; i < hidden; i++) x[i] = or_bf16_to_f32(x_bf16[i]);
-  float frac =
-      or_ffn_forward_f32(x, hidden, inter, group, scale_dtype, order, expert_flat, tau, o);
+  float frac = or_ffn_forward_f32_mode(x, hidden, inter, group, scale_dtype, order,
+                                       expert_flat, tau, thresholds, o);
   for (size_t i = 0; i < hidden; i++) out_bf16[i] = or_f32_to_bf16(o[i]);
   free(x);
   free(o);
   return frac;
+}
+
+float or_expert_forward_sparse(const uint16_t *x_bf16, size_t hidden, size_t inter,
+                               size_t group, int scale_dtype, int order,
+                               const uint8_t *expert_flat, float tau, uint16_t *out_bf16) {
+  return or_expert_forward_sparse_mode(x_bf16, hidden, inter, group, scale_dtype, order,
+                                       expert_flat, tau, NULL, out_bf16);
 }
 
 /* ------------------------------------------------------------------ */

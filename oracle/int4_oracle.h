@@ -89,6 +89,18 @@ float or_expert_forward_sparse(const uint16_t *x_bf16, size_t hidden, size_t int
 /* ffn_sparsity.rs:131-179: stable SiLU, mask |silu| >= tau*max; returns count. */
 size_t or_build_active_mask(const float *gate_out, size_t n, float tau, float *silu_out,
                             uint32_t *active_out);
+/* The *_mode variants take per-channel thresholds (SparsityMode::PerChannel,
+ * ffn_sparsity.rs:85-90, 116-179, 407, 785); NULL selects the global tau. */
+size_t or_build_active_mask_mode(const float *gate_out, size_t n, float tau,
+                                 const float *thresholds, float *silu_out,
+                                 uint32_t *active_out);
+float or_ffn_forward_f32_mode(const float *x, size_t hidden, size_t inter, size_t group,
+                              int scale_dtype, int order, const uint8_t *expert_flat,
+                              float tau, const float *thresholds, float *out);
+float or_expert_forward_sparse_mode(const uint16_t *x_bf16, size_t hidden, size_t inter,
+                                    size_t group, int scale_dtype, int order,
+                                    const uint8_t *expert_flat, float tau,
+                                    const float *thresholds, uint16_t *out_bf16);
 
 /* ---- routing ---- */
 /* K2.6 / GLM rule: sigmoid, choose top-k by (sigmoid + bias) with ties to the

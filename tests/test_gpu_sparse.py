@@ -1,0 +1,166 @@
+"""GPU parity of the activation-sparse expert FFN (tau > 0: ffn_sparsity.rs:
+131-179 mask, 187-348 rows-subset up, 438-538 and 756-867 the two forms,
+global and per-channel thresholds) against the oracle, in both weight
+layouts, one and several token rows.
+
+The mask compares |silu(gate)| with a cutoff, so a lane whose value lies
+within the GEMV's rounding of the cutoff may land on either side.  Each case
+checks from the oracle that no lane is that close (relative margin 1e-5 of
+max|silu|; the GPU's gate agrees to ~1e-6), so the active counts must agree
+exactly and the outputs to the usual tolerance."""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_gemm import assert_bf16_close, assert_f32_close
+
+pytestmark = pytest.mark.gpu
+BF16, F16 = 0, 1
+MARGIN = 1e-5
+
+
+@pytest.fixture(scope="module")
+def cl():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import cascadia_amd
+
+    return cascadia_amd
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def make_expert(orc, h, i, g, sdt, seed):
+    flat = orc.fill_bytes(seed, 60, orc.expert_bytes(h, i, g))
+    offs, sizes = orc.expert_offsets(h, i, g)
+    for s_ in (1, 3, 5):
+        flat[offs[s_]:offs[s_] + sizes[s_]] = orc.fill_scales(seed, 61 + s_, sizes[s_] // 2, sdt).view(np.uint8)
+    return flat
+
+
+def margin(orc, flat, x_f32, h, i, g, sdt, tau, thr):
+    """Smallest | |silu_i| - cutoff_i | / max|silu| over lanes (oracle), the
+    max lane aside: it meets tau * itself exactly on both sides."""
+    o, _ = orc.expert_offsets(h, i, g)
+    gate = orc.gemv(flat[o[0]:o[1]], flat[o[1]:o[2]], x_f32, i, h, g, sdt)
+    silu, _ = orc.build_active_mask(gate, tau, thresholds=thr)
+    a = np.abs(silu.astype(np.float64))
+    mx = a.max()
+    cut = (thr.astype(np.float64) if thr is not None else tau) * mx
+    d = np.abs(a - cut) / mx
+    return float(np.min(np.where(a == mx, np.inf, d)))
+
+
+def pick_x(orc, flat, h, i, g, sdt, tau, thr, seed):
+    """The first seeded bf16 row from `seed` on with no lane near its cutoff."""
+    for s in range(seed, seed + 50):
+        xb = orc.fill_normal_bf16(s, 90, h)
+        if margin(orc, flat, orc.bf16_to_f32(xb), h, i, g, sdt, tau, thr) > MARGIN:
+            return xb
+    raise AssertionError("no seed keeps every lane away from the cutoff")
+
+
+CASES = [  # h, i, G, sdt, tiled
+    (512, 256, 32, BF16, False),
+    (7168, 2048, 32, BF16, True),   # the crate's HIDDEN / INTERMEDIATE
+    (7168, 2048, 32, BF16, False),
+    (4096, 1024, 128, F16, True),
+    (3072, 1536, 64, F16, False),
+]
+
+
+@pytest.mark.parametrize("h,i,g,sdt,tiled", CASES)
+@pytest.mark.parametrize("tau", [0.05, 0.3, 1.0])
+def test_expert_forward_sparse_global(cl, orc, h, i, g, sdt, tiled, tau):
+    flat = make_expert(orc, h, i, g, sdt, h + i + g)
+    W = cl.ExpertWeights(dev(flat), h, i, g, sdt)
+    til = cl.TILING_MFMA if tiled else cl.TILING_CRATE
+    if tiled:
+        W = W.tiled()
+    T = 3
+    xb = np.stack([pick_x(orc, flat, h, i, g, sdt, tau, None, 100 * t + int(tau * 100))
+                   for t in range(T)])
+    out = torch.empty(T * h, dtype=torch.int16, device="cuda")
+    fr = cl.expert_forward_sparse(dev(xb.view(np.int16)), *W.slices(), out, tau, group_size=g,
+                                  scale_dtype=sdt, tiling=til)
+    got = host(out).view(np.uint16).reshape(T, h)
+    for t in range(T):
+        want, wf = orc.expert_forward_sparse(xb[t], flat, h, i, g, sdt, tau)
+        assert fr[t] == wf, f"token {t}: active {fr[t]} vs {wf}"
+        assert_bf16_close(got[t], want, f"{h}x{i} G{g} tau {tau} token {t}")
+    if tau == 1.0:
+        assert all(f == float(np.float32(1) / np.float32(i)) for f in fr)  # only the max lane
+    # f32 form on the same rows
+    xf = orc.bf16_to_f32(xb)
+    o32 = torch.empty(T * h, dtype=torch.float32, device="cuda")
+    fr32 = cl.ffn_forward_sparse_f32(dev(xf), h, i, *W.slices(), o32, tau, group_size=g,
+                                     scale_dtype=sdt, tiling=til)
+    got32 = host(o32).reshape(T, h)
+    for t in range(T):
+        want, wf = orc.ffn_forward_f32(xf[t], flat, h, i, g, sdt, tau)
+        assert fr32[t] == wf
+        assert_f32_close(got32[t], want, f"f32 {h}x{i} tau {tau} token {t}")
+
+
+@pytest.mark.parametrize("h,i,g,sdt,tiled", [CASES[0], CASES[1], CASES[3]])
+def test_sparse_per_channel(cl, orc, h, i, g, sdt, tiled):
+    flat = make_expert(orc, h, i, g, sdt, 3 * h + i)
+    W = cl.ExpertWeights(dev(flat), h, i, g, sdt)
+    til = cl.TILING_MFMA if tiled else cl.TILING_CRATE
+    if tiled:
+        W = W.tiled()
+    rng = np.random.default_rng(h + i)
+    thr = rng.uniform(-0.1, 0.6, i).astype(np.float32)  # some lanes always on
+    xb = pick_x(orc, flat, h, i, g, sdt, 0.0, thr, 7)
+    xf = orc.bf16_to_f32(xb)
+    out = torch.empty(h, dtype=torch.int16, device="cuda")
+    f = cl.expert_forward_sparse_per_channel(dev(xb.view(np.int16)), *W.slices(), out, dev(thr),
+                                             group_size=g, scale_dtype=sdt, tiling=til)
+    want, wf = orc.expert_forward_sparse(xb, flat, h, i, g, sdt, 0.0, thresholds=thr)
+    assert f == wf and 0 < wf < 1
+    assert_bf16_close(host(out).view(np.uint16), want, "per-channel bf16")
+    o32 = torch.empty(h, dtype=torch.float32, device="cuda")
+    f = cl.ffn_forward_sparse_f32_per_channel(dev(xf), h, i, *W.slices(), o32, dev(thr),
+                                              group_size=g, scale_dtype=sdt, tiling=til)
+    want32, wf = orc.ffn_forward_f32(xf, flat, h, i, g, sdt, 0.0, thresholds=thr)
+    assert f == wf
+    assert_f32_close(host(o32), want32, "per-channel f32")
+    # every threshold <= 0: the dense FFN (ffn_sparsity.rs:85-90)
+    neg = -np.abs(thr)
+    f = cl.ffn_forward_sparse_f32_per_channel(dev(xf), h, i, *W.slices(), o32, dev(neg),
+                                              group_size=g, scale_dtype=sdt, tiling=til)
+    assert f == 1.0
+    assert_f32_close(host(o32), orc.ffn_forward_f32(xf, flat, h, i, g, sdt, 0.0)[0], "dense pc")
+
+
+def test_sparse_edge_cases(cl, orc):
+    h, i, g = 512, 256, 32
+    flat = make_expert(orc, h, i, g, BF16, 11)
+    W = cl.ExpertWeights(dev(flat), h, i, g, BF16)
+    # x = 0: gate 0, max|silu| = 0, every lane active (ffn_sparsity.rs:151), out 0
+    o32 = torch.full((h,), 7.0, dtype=torch.float32, device="cuda")
+    f = cl.ffn_forward_sparse_f32(dev(np.zeros(h, np.float32)), h, i, *W.slices(), o32, 0.5)
+    assert f == 1.0 and not np.any(host(o32))
+    # tau 0 with a workspace of the sparse size: the dense FFN, fraction 1
+    ws = torch.empty(cl.ffn_sparse_workspace_bytes(h, i, 1), dtype=torch.uint8, device="cuda")
+    xf = orc.fill_normal_f32(1, 92, h)
+    f = cl.ffn_forward_sparse_f32(dev(xf), h, i, *W.slices(), o32, 0.0, workspace=ws)
+    assert f == 1.0
+    assert_f32_close(host(o32), orc.ffn_forward_f32(xf, flat, h, i, g, BF16, 0.0)[0], "tau 0")
+    # a caller workspace on the sparse branch
+    assert margin(orc, flat, xf, h, i, g, BF16, 0.2, None) > MARGIN
+    f = cl.ffn_forward_sparse_f32(dev(xf), h, i, *W.slices(), o32, 0.2, workspace=ws)
+    want, wf = orc.ffn_forward_f32(xf, flat, h, i, g, BF16, 0.2)
+    assert f == wf
+    assert_f32_close(host(o32), want, "caller workspace")
+    # thresholds of the wrong length (ffn_sparsity.rs:117-123 asserts)
+    with pytest.raises(ValueError):
+        cl.ffn_forward_sparse_f32_per_channel(dev(xf), h, i, *W.slices(), o32,
+                                              dev(np.zeros(i - 1, np.float32)))

@@ -511,3 +511,67 @@ def test_generators_deterministic_and_distributed(orc):
     assert abs(z.mean()) < 0.02 and abs(z.std() - 1) < 0.02
     s = orc.fill_scales(0, 4, 100000, F16).view(np.float16).astype(np.float64)
     assert s.min() >= 1e-3 * 0.999 and abs((s - 1e-3).mean() - 0.02 * np.sqrt(2 / np.pi)) < 5e-4
+
+
+def test_mask_per_channel_known_answers(orc):
+    """PerChannel (ffn_sparsity.rs:162-175): cutoff_i = t_i * max|silu|.
+    silu(10) = 9.9995, silu(5) = 4.9665, silu(+-0.001) = +-0.0005."""
+    g = np.array([10.0, 0.001, 5.0, -0.001], np.float32)
+    _, act = orc.build_active_mask(g, 0.0, thresholds=np.array([0.9, 0.0, 0.6, 2.0], np.float32))
+    assert act.tolist() == [0, 1]
+    _, act = orc.build_active_mask(g, 0.0, thresholds=np.array([0.9, 0.0, 0.4, 2.0], np.float32))
+    assert act.tolist() == [0, 1, 2]
+    # every threshold <= 0 is dense (:88): all lanes, whatever the values
+    _, act = orc.build_active_mask(g, 0.0, thresholds=np.array([0, -1, 0, -3], np.float32))
+    assert act.tolist() == [0, 1, 2, 3]
+    # stable SiLU against float64
+    s, _ = orc.build_active_mask(np.array([-30, -3, -0.5, 0, 0.5, 3, 30], np.float32), 0.5)
+    x = np.array([-30, -3, -0.5, 0, 0.5, 3, 30], np.float64)
+    assert np.allclose(s, x / (1 + np.exp(-x)), rtol=1e-6, atol=1e-30)
+
+
+def _random_expert(orc, h, i, seed):
+    flat = orc.fill_bytes(seed, 60, orc.expert_bytes(h, i, 32))
+    offs, sizes = orc.expert_offsets(h, i, 32)
+    for s_ in (1, 3, 5):
+        flat[offs[s_]:offs[s_] + sizes[s_]] = orc.fill_scales(seed, 61 + s_, sizes[s_] // 2, BF16).view(np.uint8)
+    return flat
+
+
+def test_sparse_per_channel_uniform_is_global(orc):
+    """A per-channel vector equal to tau everywhere is the global mode, bitwise;
+    one with every entry <= 0 is the dense FFN, bitwise."""
+    h, i = 256, 128
+    flat = _random_expert(orc, h, i, 5)
+    x = orc.fill_normal_f32(5, 9, h)
+    xb = orc.f32_to_bf16(x)
+    for tau in (0.05, 0.3, 1.0):
+        a, fa = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, tau)
+        b, fb = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, 0.0, thresholds=np.full(i, tau, np.float32))
+        assert fa == fb < 1.0 and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        c, fc = orc.expert_forward_sparse(xb, flat, h, i, 32, BF16, tau)
+        d, fd = orc.expert_forward_sparse(xb, flat, h, i, 32, BF16, 0.0, thresholds=np.full(i, tau, np.float32))
+        assert fc == fd and np.array_equal(c, d)
+    dense, _ = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, 0.0)
+    pc, f = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, 0.0, thresholds=-np.arange(i, dtype=np.float32))
+    assert f == 1.0 and np.array_equal(dense.view(np.uint32), pc.view(np.uint32))
+
+
+def test_sparse_branch_composition(orc):
+    """ffn_sparsity.rs:499-537: the sparse branch is gate in full, the mask,
+    up on the active rows, inter = silu * up there and 0 elsewhere, down in
+    full -- restated from the oracle's GEMV and mask (pinned above)."""
+    h, i = 256, 128
+    flat = _random_expert(orc, h, i, 8)
+    o, _ = orc.expert_offsets(h, i, 32)
+    x = orc.fill_normal_f32(8, 9, h)
+    for tau in (0.1, 0.5):
+        g = orc.gemv(flat[o[0]:o[1]], flat[o[1]:o[2]], x, i, h, 32, BF16)
+        silu, act = orc.build_active_mask(g, tau)
+        u = orc.gemv(flat[o[2]:o[3]], flat[o[3]:o[4]], x, i, h, 32, BF16)
+        m = np.zeros(i, np.float32)
+        m[act] = silu[act] * u[act]
+        want = orc.gemv(flat[o[4]:o[5]], flat[o[5]:], m, h, i, 32, BF16)
+        got, frac = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, tau)
+        assert frac == len(act) / i and 0 < len(act) < i
+        assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
