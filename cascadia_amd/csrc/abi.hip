@@ -269,8 +269,8 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Workspace of the activation-sparse FFN: gate output, SiLU, active lanes and
-// the intermediate ([n_tokens, inter] each), per-token counts, then split-K
+// Workspace of the activation-sparse FFN: gate output, SiLU and the
+// intermediate ([n_tokens, inter] each), two cells per token, then split-K
 // partials of the largest of its GEMMs; at least what the dense branch needs.
 struct SparseWorkspace {
   size_t lanes, counts, partials, total;
@@ -291,9 +291,9 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
   for (const cai4::SkinnyPlan &p : plans) part = p.partial_bytes > part ? p.partial_bytes : part;
   SparseWorkspace w;
   w.lanes = align256((size_t)n_tokens * inter * 4);
-  w.counts = align256((size_t)n_tokens * 4);
+  w.counts = align256((size_t)n_tokens * 8);  // two cells per token
   w.partials = part;
-  w.total = 4 * w.lanes + w.counts + part;
+  w.total = 3 * w.lanes + w.counts + part;
   const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group, n_tokens, true);
   const FfnWorkspace b = ffn_workspace(dev, hidden, inter, group, n_tokens, false);
   const size_t dense = f.planes + (f.partials > b.partials ? f.partials : b.partials);
@@ -334,20 +334,17 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   uint8_t *b = static_cast<uint8_t *>(ws);
   float *gate = reinterpret_cast<float *>(b);
   float *sg = reinterpret_cast<float *>(b + w.lanes);
-  uint32_t *act = reinterpret_cast<uint32_t *>(b + 2 * w.lanes);
-  float *mid = reinterpret_cast<float *>(b + 3 * w.lanes);
-  uint32_t *cnt = reinterpret_cast<uint32_t *>(b + 4 * w.lanes);
-  void *part = w.partials ? b + 4 * w.lanes + w.counts : nullptr;
+  float *mid = reinterpret_cast<float *>(b + 2 * w.lanes);
+  uint32_t *cells = reinterpret_cast<uint32_t *>(b + 3 * w.lanes);
+  void *part = w.partials ? b + 3 * w.lanes + w.counts : nullptr;
   int rc = run_gemm(e->gate_packed, e->gate_scale, nullptr, nullptr, (int)inter, (int)hidden,
                     (int)group, (int)sdt, (int)e->tiling, x, nullptr, amode, (int)n_tokens, gate,
                     nullptr, cai4::EPI_F32, st, part);
   if (rc) return rc;
-  if ((rc = hip_status(cai4::sparse_mask(gate, (int)n_tokens, (int)inter, tau, thr, sg, act, cnt,
-                                         counts, mid, st))))
-    return rc;
-  if ((rc = hip_status(cai4::rows_subset_up(e->up_packed, e->up_scale, (int)inter, (int)hidden,
+  if ((rc = hip_status(cai4::sparse_ffn_mid(e->up_packed, e->up_scale, (int)inter, (int)hidden,
                                             (int)group, (int)sdt, (int)e->tiling, x, x_f32,
-                                            (int)n_tokens, act, cnt, sg, mid, st))))
+                                            (int)n_tokens, gate, tau, thr, sg, cells, mid, counts,
+                                            st))))
     return rc;
   return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
                   (int)group, (int)sdt, (int)e->tiling, mid, nullptr, cai4::A_XF32,

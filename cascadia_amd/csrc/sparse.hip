@@ -3,15 +3,19 @@
 // up GEMV, :499-537 the sparse branch).  The gate and down GEMMs are the
 // ordinary kernels; between them:
 //
-//   sparse_mask_kernel   one workgroup per token: stable SiLU of the gate
-//                        output, max |silu|, the mask |silu| >= cutoff and the
-//                        active lanes compacted in ascending order (a block
-//                        prefix sum per 1024 lanes), inactive lanes of the
-//                        intermediate zeroed.
-//   rows_subset_kernel   one wave per active lane: the up row's dot product
-//                        with x, read from either weight layout, times the
-//                        lane's SiLU -> the intermediate.  Inactive rows are
-//                        never read, which is the point of the sparse path.
+//   sparse_prep_kernel   a lane per thread over many workgroups: stable SiLU
+//                        of the gate output, each workgroup's max |silu| into
+//                        the token's max cell (an unsigned max of the float
+//                        bits: every value is >= 0 and NaN never enters), and
+//                        for per-channel thresholds whether any is > 0.
+//   rows_subset_kernel   one wave per intermediate lane: the mask test
+//                        |silu| >= cutoff * max (every lane when the max is 0
+//                        or the mode is dense), then for an active lane the up
+//                        row's dot product with x, read from either weight
+//                        layout, times the SiLU -> the intermediate; 0 for an
+//                        inactive lane, whose up row is never read.
+//   sparse_count_kernel  the active-lane count of each token, by the same
+//                        test (only when the caller asks for it).
 //
 // HBM traffic per token: gate and down in full, up for the active rows only.
 #include "int4_common.hpp"
@@ -22,6 +26,11 @@ namespace cai4 {
 namespace {
 
 constexpr int kMaskThreads = 1024;
+
+__global__ void fill_u32_kernel(uint32_t *p, int n, uint32_t v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
 constexpr int kMaskWaves = kMaskThreads / 64;
 
 // ffn_sparsity.rs:141-147: the stable form, e^-g for g >= 0, e^g below.
@@ -49,150 +58,72 @@ CAI4_DEV float wave_sum(float v) {
   return v;
 }
 
-__global__ void __launch_bounds__(kMaskThreads)
-    sparse_mask_kernel(const float *__restrict__ gate, int I, float tau,
-                       const float *__restrict__ thr, float *__restrict__ sg,
-                       uint32_t *__restrict__ act, uint32_t *__restrict__ cnt,
-                       uint32_t *__restrict__ counts_out, float *__restrict__ inter) {
-  __shared__ float s_max[kMaskWaves];
-  __shared__ uint32_t s_pos[kMaskWaves];
-  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// cells of a token: [0] max |silu| bits, [1] any per-channel threshold > 0
+__global__ void __launch_bounds__(256)
+    sparse_prep_kernel(const float *__restrict__ gate, int I, const float *__restrict__ thr,
+                       float *__restrict__ sg, uint32_t *__restrict__ cells) {
+  __shared__ float s_max[4];
+  const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const size_t row = (size_t)t * I;
-  const float *g = gate + row;
-  // dense: SparsityMode::is_dense (ffn_sparsity.rs:85-90).  A per-channel
-  // vector with every threshold <= 0 takes the dense branch's SiLU.
-  int sparse_any = thr ? 0 : !(tau <= 0.0f);
-  if (thr)
-    for (int i = tid; i < I; i += kMaskThreads) sparse_any |= !(thr[i] <= 0.0f);
-  sparse_any = __syncthreads_or(sparse_any);
-  float mx = 0.0f;
-  for (int i = tid; i < I; i += kMaskThreads) {
-    const float s = sparse_any ? silu_stable(g[i]) : silu_plain(g[i]);
+  float a = 0.0f;
+  int pos = 0;
+  if (i < I) {
+    const float s = silu_stable(gate[row + i]);
     sg[row + i] = s;
-    const float a = fabsf(s);
-    mx = a > mx ? a : mx;
+    a = fabsf(s);
+    a = a > 0.0f ? a : 0.0f;  // NaN -> 0 (a NaN lane never raises the max)
+    if (thr) pos = !(thr[i] <= 0.0f);
   }
-  mx = wave_max(mx);
-  if (lane == 0) s_max[wave] = mx;
-  __syncthreads();
-  mx = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kMaskWaves; ++w) mx = s_max[w] > mx ? s_max[w] : mx;
-  const bool all = mx == 0.0f || !sparse_any;
-  // compaction, 1024 lanes at a time, ascending
-  uint32_t base = 0;
-  for (int c0 = 0; c0 < I; c0 += kMaskThreads) {
-    const int i = c0 + tid;
-    bool on = false;
-    if (i < I) {
-      const float s = sg[row + i];
-      on = all || fabsf(s) >= (thr ? thr[i] : tau) * mx;
-      if (!on) inter[row + i] = 0.0f;
-    }
-    const uint64_t b = __ballot(on);
-    const uint32_t below = __popcll(b & ((1ull << lane) - 1ull));
-    __syncthreads();  // s_pos of the previous chunk is consumed
-    if (lane == 0) s_pos[wave] = (uint32_t)__popcll(b);
-    __syncthreads();
-    uint32_t off = base;
-    for (int w = 0; w < wave; ++w) off += s_pos[w];
-    if (on) act[row + off + below] = (uint32_t)i;
-    for (int w = 0; w < kMaskWaves; ++w) base += s_pos[w];
-  }
-  if (tid == 0) {
-    cnt[t] = base;
-    if (counts_out) counts_out[t] = base;
+  a = wave_max(a);
+  if (lane == 0) s_max[wave] = a;
+  pos = __syncthreads_or(pos);
+  if (threadIdx.x == 0) {
+    float m = s_max[0];
+    for (int w = 1; w < 4; ++w) m = s_max[w] > m ? s_max[w] : m;
+    if (m > 0.0f) atomicMax(&cells[2 * t], fbits(m));
+    if (pos) atomicOr(&cells[2 * t + 1], 1u);
   }
 }
 
-// The same mask in one pass with each thread's NPT lanes (tid, tid + 1024,
-// ...) held in registers: every load and store coalesced, the ascending
-// compaction from one ballot per 1024-lane chunk and a scan of the 16 x NPT
-// per-wave counts.  I <= 1024 * NPT.
-template <int NPT>
+// The mask test of lane i of token t (ffn_sparsity.rs:131-179); *silu
+// receives the SiLU the intermediate uses: the dense branch's plain form
+// when the per-channel vector is dense (:85-90, 487).
+CAI4_DEV bool lane_active(const float *__restrict__ gate, const float *__restrict__ sg,
+                          const float *__restrict__ thr, float tau,
+                          const uint32_t *__restrict__ cells, int t, size_t at, int i,
+                          float *silu) {
+  const bool sparse = thr ? cells[2 * t + 1] != 0u : !(tau <= 0.0f);
+  const float mx = bitsf(cells[2 * t]);
+  if (!sparse) {
+    *silu = silu_plain(gate[at]);
+    return true;
+  }
+  const float s = sg[at];
+  *silu = s;
+  return mx == 0.0f || fabsf(s) >= (thr ? thr[i] : tau) * mx;
+}
+
 __global__ void __launch_bounds__(kMaskThreads)
-    sparse_mask_reg_kernel(const float *__restrict__ gate, int I, float tau,
-                           const float *__restrict__ thr, float *__restrict__ sg,
-                           uint32_t *__restrict__ act, uint32_t *__restrict__ cnt,
-                           uint32_t *__restrict__ counts_out, float *__restrict__ inter) {
-  __shared__ float s_max[kMaskWaves];
-  __shared__ uint32_t s_off[NPT][kMaskWaves];
-  __shared__ uint32_t s_base[NPT + 1];
+    sparse_count_kernel(const float *__restrict__ gate, int I, float tau,
+                        const float *__restrict__ thr, const float *__restrict__ sg,
+                        const uint32_t *__restrict__ cells, uint32_t *__restrict__ counts) {
+  __shared__ uint32_t s_n[kMaskWaves];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const size_t row = (size_t)t * I;
-  float v[NPT], th[NPT];
-#pragma unroll
-  for (int k = 0; k < NPT; ++k) {
-    const int i = k * kMaskThreads + tid;
-    v[k] = i < I ? gate[row + i] : 0.0f;
-    th[k] = thr && i < I ? thr[i] : 0.0f;
+  uint32_t n = 0;
+  for (int i = tid; i < I; i += kMaskThreads) {
+    float s;
+    n += lane_active(gate, sg, thr, tau, cells, t, row + i, i, &s) ? 1u : 0u;
   }
-  // SparsityMode::is_dense (ffn_sparsity.rs:85-90)
-  int sparse_any = thr ? 0 : !(tau <= 0.0f);
-  if (thr) {
 #pragma unroll
-    for (int k = 0; k < NPT; ++k) sparse_any |= (k * kMaskThreads + tid < I) & !(th[k] <= 0.0f);
-  }
-  sparse_any = __syncthreads_or(sparse_any);
-  float mx = 0.0f;
-#pragma unroll
-  for (int k = 0; k < NPT; ++k) {
-    const int i = k * kMaskThreads + tid;
-    if (i < I) {
-      v[k] = sparse_any ? silu_stable(v[k]) : silu_plain(v[k]);
-      sg[row + i] = v[k];
-      const float a = fabsf(v[k]);
-      mx = a > mx ? a : mx;
-    }
-  }
-  mx = wave_max(mx);
-  if (lane == 0) s_max[wave] = mx;
+  for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o, 64);
+  if (lane == 0) s_n[wave] = n;
   __syncthreads();
-  mx = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kMaskWaves; ++w) mx = s_max[w] > mx ? s_max[w] : mx;
-  const bool all = mx == 0.0f || !sparse_any;
-  uint64_t bal[NPT];
-#pragma unroll
-  for (int k = 0; k < NPT; ++k) {
-    const int i = k * kMaskThreads + tid;
-    const bool on = i < I && (all || fabsf(v[k]) >= (thr ? th[k] : tau) * mx);
-    if (i < I && !on) inter[row + i] = 0.0f;
-    bal[k] = __ballot(on);
-    if (lane == 0) s_off[k][wave] = (uint32_t)__popcll(bal[k]);
-  }
-  __syncthreads();
-  if (tid < NPT) {  // exclusive scan over the waves of chunk tid
-    uint32_t run = 0;
-#pragma unroll
-    for (int w = 0; w < kMaskWaves; ++w) {
-      const uint32_t c = s_off[tid][w];
-      s_off[tid][w] = run;
-      run += c;
-    }
-    s_base[tid + 1] = run;
-  }
-  __syncthreads();
-  if (tid == 0) {  // exclusive scan over the chunks
-    uint32_t run = 0;
-    for (int k = 0; k < NPT; ++k) {
-      const uint32_t c = s_base[k + 1];
-      s_base[k] = run;
-      run += c;
-    }
-    s_base[NPT] = run;
-  }
-  __syncthreads();
-  const uint64_t below = (1ull << lane) - 1ull;
-#pragma unroll
-  for (int k = 0; k < NPT; ++k) {
-    if ((bal[k] >> lane) & 1ull)
-      act[row + s_base[k] + s_off[k][wave] + __popcll(bal[k] & below)] =
-          (uint32_t)(k * kMaskThreads + tid);
-  }
   if (tid == 0) {
-    cnt[t] = s_base[NPT];
-    if (counts_out) counts_out[t] = s_base[NPT];
+    uint32_t tot = 0;
+    for (int w = 0; w < kMaskWaves; ++w) tot += s_n[w];
+    counts[t] = tot;
   }
 }
 
@@ -257,14 +188,19 @@ template <int TILED, int XF32>
 __global__ void __launch_bounds__(256)
     rows_subset_kernel(const uint8_t *__restrict__ w, const uint16_t *__restrict__ s, int I,
                        int K, int G, int sdt, const void *__restrict__ x,
-                       const uint32_t *__restrict__ act, const uint32_t *__restrict__ cnt,
-                       const float *__restrict__ sg, float *__restrict__ inter) {
+                       const float *__restrict__ gate, const float *__restrict__ sg,
+                       const float *__restrict__ thr, float tau,
+                       const uint32_t *__restrict__ cells, float *__restrict__ inter) {
   const int t = blockIdx.y;
-  const int slot = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (slot >= (int)cnt[t]) return;  // wave-uniform
+  if (r >= I) return;  // wave-uniform
   const size_t row = (size_t)t * I;
-  const int r = (int)act[row + slot];
+  float silu;
+  if (!lane_active(gate, sg, thr, tau, cells, t, row + r, r, &silu)) {
+    if (lane == 0) inter[row + r] = 0.0f;
+    return;
+  }
   float acc = 0.0f;
   // two 32-column chunks per pass: both weight loads are issued before
   // either is used
@@ -277,59 +213,41 @@ __global__ void __launch_bounds__(256)
     if (two) acc += row_chunk_dot<TILED>(w, s, r, c + 2048, K, G, sdt, xb);
   }
   acc = wave_sum(acc);
-  if (lane == 0) inter[row + r] = sg[row + r] * acc;
+  if (lane == 0) inter[row + r] = silu * acc;
 }
 
 }  // namespace
 
-hipError_t sparse_mask(const float *gate, int T, int I, float tau, const float *thr, float *sg,
-                       uint32_t *act, uint32_t *cnt, uint32_t *counts_out, float *inter,
-                       hipStream_t st) {
-  const dim3 grid(T), block(kMaskThreads);
-  if (I <= 4 * kMaskThreads)
-    hipLaunchKernelGGL(sparse_mask_reg_kernel<4>, grid, block, 0, st, gate, I, tau, thr, sg, act,
-                       cnt, counts_out, inter);
-  else if (I <= 8 * kMaskThreads)
-    hipLaunchKernelGGL(sparse_mask_reg_kernel<8>, grid, block, 0, st, gate, I, tau, thr, sg, act,
-                       cnt, counts_out, inter);
-  else if (I <= 16 * kMaskThreads)
-    hipLaunchKernelGGL(sparse_mask_reg_kernel<16>, grid, block, 0, st, gate, I, tau, thr, sg,
-                       act, cnt, counts_out, inter);
-  else
-    hipLaunchKernelGGL(sparse_mask_kernel, grid, block, 0, st, gate, I, tau, thr, sg, act, cnt,
-                       counts_out, inter);
-  return hipGetLastError();
-}
-
-hipError_t rows_subset_up(const uint8_t *w, const uint8_t *s, int I, int K, int G, int sdt,
-                          int tiled, const void *x, bool x_f32, int T, const uint32_t *act,
-                          const uint32_t *cnt, const float *sg, float *inter, hipStream_t st) {
+hipError_t sparse_ffn_mid(const uint8_t *w, const uint8_t *s, int I, int K, int G, int sdt,
+                          int tiled, const void *x, bool x_f32, int T, const float *gate,
+                          float tau, const float *thr, float *sg, uint32_t *cells, float *inter,
+                          uint32_t *counts_out, hipStream_t st) {
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((2 * T + 255) / 256), dim3(256), 0, st, cells, 2 * T,
+                     0u);
+  hipLaunchKernelGGL(sparse_prep_kernel, dim3((I + 255) / 256, T), dim3(256), 0, st, gate, I, thr,
+                     sg, cells);
   const dim3 grid((I + 3) / 4, T), block(256);
   const uint16_t *sc = reinterpret_cast<const uint16_t *>(s);
   if (tiled) {
     if (x_f32)
       hipLaunchKernelGGL((rows_subset_kernel<1, 1>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         act, cnt, sg, inter);
+                         gate, sg, thr, tau, cells, inter);
     else
       hipLaunchKernelGGL((rows_subset_kernel<1, 0>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         act, cnt, sg, inter);
+                         gate, sg, thr, tau, cells, inter);
   } else {
     if (x_f32)
       hipLaunchKernelGGL((rows_subset_kernel<0, 1>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         act, cnt, sg, inter);
+                         gate, sg, thr, tau, cells, inter);
     else
       hipLaunchKernelGGL((rows_subset_kernel<0, 0>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         act, cnt, sg, inter);
+                         gate, sg, thr, tau, cells, inter);
   }
+  if (counts_out)
+    hipLaunchKernelGGL(sparse_count_kernel, dim3(T), dim3(kMaskThreads), 0, st, gate, I, tau, thr,
+                       sg, cells, counts_out);
   return hipGetLastError();
 }
-
-namespace {
-__global__ void fill_u32_kernel(uint32_t *p, int n, uint32_t v) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
-}
-}  // namespace
 
 hipError_t fill_u32(uint32_t *p, int n, uint32_t v, hipStream_t st) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, n, v);
