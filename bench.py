@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--extra", action="store_true", help="also time configs 0 and 2, M=4/16")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="launch the config 2 prefill GEMMs eagerly, without timing, for rocprofv3")
+    ap.add_argument("--profile-sparse", action="store_true",
+                    help="launch the config 1 activation-sparse expert (tau 0.3) 50 times "
+                         "eagerly, for rocprofv3")
     ap.add_argument("--profile-moe", action="store_true",
                     help="run configs 3 and 4 at T=--moe-tokens (a few steps), for rocprofv3")
     ap.add_argument("--moe-tokens", type=int, default=1, help="tokens of --profile-moe")
@@ -404,6 +407,18 @@ def main():
             del pre
         print(json.dumps({"profile": "prefill", "shapes": PREFILL_SHAPES, "launches": 5}),
               flush=True)
+        return
+    if args.profile_sparse:
+        copies = Copies(cl, torch, 4096, 14336, 128, sdt, 1)
+        xs1 = cl.fill_normal(torch.empty(4096, dtype=torch.bfloat16, device="cuda"), 0, 23)
+        os1 = torch.empty(4096, dtype=torch.bfloat16, device="cuda")
+        for r in range(50):
+            fr = cl.expert_forward_sparse(xs1.view(torch.int16), *copies.w[0].slices(),
+                                          os1.view(torch.int16), 0.3, group_size=128,
+                                          scale_dtype=sdt, tiling=cl.TILING_MFMA)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": "sparse_expert", "tau": 0.3, "active_frac": fr,
+                          "launches": 50}), flush=True)
         return
     if args.profile_moe:
         T = args.moe_tokens
