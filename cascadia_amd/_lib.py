@@ -87,6 +87,9 @@ SIGNATURES = {
     "cascadia_int4_moe_forward": (_i32, [_MP, _RP, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_debug_dequant": (_i32, [_LP, _vp, _vp, _vp, _vp]),
     "cascadia_int4_fill_synthetic": (_i32, [_u32, _u64, _u64, _sz, _f64, _f64, _u32, _vp, _vp]),
+    "cascadia_int4_transpose_requantize_down": (_i32, [_u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_axpy_workspace_bytes": (_sz, [_u32, _u32]),
+    "cascadia_int4_dequant_axpy_active": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "cascadia_int4_ffn_sparse_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
     "cascadia_int4_ffn_forward_sparse_f32": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, C.c_float,
                                                     _vp, _vp, _vp, _vp, _vp]),

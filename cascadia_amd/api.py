@@ -329,6 +329,52 @@ def _sparse_call(x, weights, out, threshold, thresholds, group_size, scale_dtype
     return frac[0] if x.dim() == 1 else frac
 
 
+def transpose_requantize_down(src_packed, src_scale_bits, n_hidden, n_intermediate,
+                              group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
+    """ffn_axpy.rs:342-440: the down matrix [n_hidden, n_intermediate] (crate
+    layout) -> (packed_t u8 [n_intermediate * n_hidden / 2], scale_t u8
+    [n_intermediate * n_hidden / 32 * 2]), requantised in groups of 32 along
+    hidden with bf16 scales, bit-identical to the crate."""
+    _dev(src_packed, "src_packed"), _dev(src_scale_bits, "src_scale_bits")
+    _expect(n_hidden % 32 == 0 and group_size % 32 == 0 and n_intermediate % group_size == 0,
+            "hidden must be a multiple of 32 and the group a multiple of 32 dividing intermediate")
+    _expect(src_packed.numel() * src_packed.element_size() == n_hidden * n_intermediate // 2,
+            "src_packed length")
+    _expect(src_scale_bits.numel() * src_scale_bits.element_size() ==
+            n_hidden * (n_intermediate // group_size) * 2, "src_scale_bits length")
+    pt = torch.empty(n_intermediate * n_hidden // 2, dtype=torch.uint8, device=src_packed.device)
+    st = torch.empty(n_intermediate * (n_hidden // 32) * 2, dtype=torch.uint8,
+                     device=src_packed.device)
+    check("cascadia_int4_transpose_requantize_down", lib().cascadia_int4_transpose_requantize_down(
+        n_hidden, n_intermediate, group_size, scale_dtype, src_packed.data_ptr(),
+        src_scale_bits.data_ptr(), pt.data_ptr(), st.data_ptr(), _stream()))
+    return pt, st
+
+
+def dequant_axpy_int4_active(packed_t, scale_t_bits, scalars, active, n_intermediate, n_hidden,
+                             y, workspace=None):
+    """ffn_axpy.rs:82-160: y[n_hidden] += sum over r in active of scalars[r] *
+    W_t[r, :] (device tensors; active int32/uint32 row ids)."""
+    for t, n in ((packed_t, "packed_t"), (scale_t_bits, "scale_t_bits"), (scalars, "scalars"),
+                 (active, "active"), (y, "y")):
+        _dev(t, n)
+    _expect(packed_t.numel() * packed_t.element_size() == n_intermediate * n_hidden // 2,
+            "packed_t length")
+    _expect(scale_t_bits.numel() * scale_t_bits.element_size() ==
+            n_intermediate * (n_hidden // 32) * 2, "scale_t_bits length")
+    _expect(scalars.dtype == torch.float32 and scalars.numel() == n_intermediate, "scalars")
+    _expect(y.dtype == torch.float32 and y.numel() == n_hidden, "y")
+    _expect(active.element_size() == 4, "active must hold 32-bit row ids")
+    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
+    check("cascadia_int4_dequant_axpy_active", lib().cascadia_int4_dequant_axpy_active(
+        packed_t.data_ptr(), scale_t_bits.data_ptr(), scalars.data_ptr(), active.data_ptr(),
+        active.numel(), n_intermediate, n_hidden, y.data_ptr(), ws, _stream()))
+    return y
+
+
+dequant_axpy_int4_active_auto = dequant_axpy_int4_active  # ffn_axpy.rs:274
+
+
 def ffn_sparse_workspace_bytes(hidden, inter, n_tokens, group_size=GROUP_SIZE) -> int:
     """Workspace bytes of the sparse entry points for n_tokens rows."""
     return int(lib().cascadia_int4_ffn_sparse_workspace_bytes(hidden, inter, group_size,

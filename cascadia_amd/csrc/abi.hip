@@ -7,6 +7,7 @@
 #include <new>
 
 #include "../../include/cascadia_int4.h"
+#include "axpy.hpp"
 #include "int4_common.hpp"
 #include "layout.hpp"
 #include "moe.hpp"
@@ -862,6 +863,52 @@ int cascadia_int4_ffn_forward_f32(uint32_t hidden, uint32_t inter, uint32_t grou
                                   void *workspace, void *stream) {
   return ffn_common(hidden, inter, group_size, scale_dtype, expert, x, true, n_tokens, out,
                     false, workspace, (hipStream_t)stream);
+}
+
+int cascadia_int4_transpose_requantize_down(uint32_t hidden, uint32_t inter,
+                                            uint32_t group_size, uint32_t scale_dtype,
+                                            const uint8_t *packed, const uint8_t *scale_bits,
+                                            uint8_t *packed_t, uint8_t *scale_t_bits,
+                                            void *stream) {
+  if (!packed || !scale_bits || !packed_t || !scale_t_bits) return CASCADIA_INT4_ERR_NULL;
+  if (hidden == 0 || inter == 0 || group_size == 0 || group_size % 32 || inter % group_size ||
+      hidden % 32 || scale_dtype > 1 || hidden > (1u << 30) || inter > (1u << 30) ||
+      (size_t)hidden * inter > ((size_t)1 << 34))
+    return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(packed_t, 16) || !aligned(scale_bits, 2) || !aligned(scale_t_bits, 2))
+    return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::transpose_requantize(packed, scale_bits, (int)hidden, (int)inter,
+                                               (int)group_size, (int)scale_dtype, packed_t,
+                                               scale_t_bits, (hipStream_t)stream));
+}
+
+size_t cascadia_int4_axpy_workspace_bytes(uint32_t hidden, uint32_t n_active) {
+  return align256(cai4::axpy_plan((int)hidden, (int)n_active).partial_bytes);
+}
+
+int cascadia_int4_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *scale_t_bits,
+                                      const float *scalars, const uint32_t *active,
+                                      uint32_t n_active, uint32_t inter, uint32_t hidden,
+                                      float *y, void *workspace, void *stream) {
+  if (!packed_t || !scale_t_bits || !scalars || !y || (n_active && !active))
+    return CASCADIA_INT4_ERR_NULL;
+  if (hidden == 0 || inter == 0 || hidden % 32 || hidden > (1u << 30) || inter > (1u << 30) ||
+      n_active > (1u << 30))
+    return CASCADIA_INT4_ERR_ARG;
+  if (!aligned(packed_t, 16) || !aligned(scale_t_bits, 2) || !aligned(scalars, 4) ||
+      !aligned(y, 4) || (active && !aligned(active, 4)) || (workspace && !aligned(workspace, 16)))
+    return CASCADIA_INT4_ERR_ARG;
+  if (n_active == 0) return CASCADIA_INT4_OK;
+  const cai4::AxpyPlan p = cai4::axpy_plan((int)hidden, (int)n_active);
+  void *ws = workspace;
+  if (!ws) {
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    if (int rc = lib_workspace(dev, p.partial_bytes, &ws)) return rc;
+  }
+  return hip_status(cai4::axpy_active(packed_t, scale_t_bits, scalars, active, (int)n_active,
+                                      (int)hidden, (int)inter, static_cast<float *>(ws), y,
+                                      (hipStream_t)stream));
 }
 
 size_t cascadia_int4_ffn_sparse_workspace_bytes(uint32_t hidden, uint32_t inter,

@@ -1,0 +1,148 @@
+// axpy.hip -- the AXPY form of the sparse down projection (ffn_axpy.rs).
+//
+// transpose_requantize_kernel  load time: the down matrix [hidden, inter]
+//   (crate layout, groups along inter) dequantised, transposed to
+//   [inter, hidden] and quantised again in groups of 32 along hidden with
+//   bf16 scales, bit-identical to ffn_axpy.rs:342-440.  One thread per
+//   destination group; neighbouring threads take neighbouring source columns,
+//   so the strided source reads share cache lines.
+// axpy_active_kernel  y[hidden] += sum over the active rows r of
+//   scalar[r] * W_t[r, :] (ffn_axpy.rs:82-160): only the active rows are
+//   read, which is what the transposed layout buys.  Grid (column chunk of
+//   2048, row slice); a lane holds 32 columns of f32 sums, the block's four
+//   waves are folded through LDS into one partial row per slice, and
+//   axpy_reduce_kernel adds the slices to y in slice order (deterministic).
+#include "int4_common.hpp"
+#include "axpy.hpp"
+
+namespace cai4 {
+
+namespace {
+
+__global__ void __launch_bounds__(256)
+    transpose_requantize_kernel(const uint8_t *__restrict__ src, const uint16_t *__restrict__ ssc,
+                                int H, int I, int G, int sdt, uint8_t *__restrict__ dst,
+                                uint16_t *__restrict__ dsc) {
+  const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int GD = H / 32;
+  if (tid >= (size_t)I * GD) return;
+  const int r = (int)(tid % I), g = (int)(tid / I);  // r: destination row = source column
+  const int NG = I / G;
+  float v[32];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const size_t h = (size_t)g * 32 + j;
+    const uint32_t b = src[h * (I / 2) + r / 2];
+    const int q = (int)((r & 1) ? (b >> 4) : (b & 15u)) - 8;
+    v[j] = (float)q * scale_bits_f32(ssc[h * NG + r / G], sdt);
+    const float a = fabsf(v[j]);
+    mx = a > mx ? a : mx;
+  }
+  const float scale = mx == 0.0f ? 1.0f : __fdiv_rn(mx, 7.0f);
+  const float inv = mx == 0.0f ? 0.0f : __fdiv_rn(1.0f, scale);
+  dsc[(size_t)r * GD + g] = (uint16_t)f32_to_bf16_rne(scale);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const float qf = roundf(__fmul_rn(v[j], inv));
+    const int q = qf != qf ? 0 : (int)fminf(fmaxf(qf, -8.0f), 7.0f);
+    w[j >> 3] |= (uint32_t)(q + 8) << (4 * (j & 7));
+  }
+  *reinterpret_cast<u32x4_t *>(dst + (size_t)r * (H / 2) + (size_t)g * 16) =
+      u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
+__global__ void __launch_bounds__(256)
+    axpy_active_kernel(const uint8_t *__restrict__ pt, const uint16_t *__restrict__ st,
+                       const float *__restrict__ scalars, const uint32_t *__restrict__ active,
+                       int n_active, int per_slice, int H, int I, float *__restrict__ partial) {
+  __shared__ float s_acc[3][2048];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * 2048 + 32 * lane;  // this lane's 32 columns
+  const int a0 = blockIdx.y * per_slice;
+  const int a1 = min(a0 + per_slice, n_active);
+  const int GD = H / 32;
+  float acc[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) acc[j] = 0.0f;
+  if (c < H) {
+    for (int a = a0 + wave; a < a1; a += 4) {
+      const uint32_t r = active[a];
+      if (r >= (uint32_t)I) continue;  // ids past the intermediate size are ignored
+      const u32x4_t q = *reinterpret_cast<const u32x4_t *>(pt + (size_t)r * (H / 2) + c / 2);
+      const float comb = scalars[r] * bf16_to_f32(st[(size_t)r * GD + c / 32]);
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          acc[8 * d + e] += comb * (float)((int)((q[d] >> (4 * e)) & 15u) - 8);
+    }
+  }
+  // fold waves 1..3 into wave 0 through LDS (column-major per lane)
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) s_acc[wave - 1][j * 64 + lane] = acc[j];
+  }
+  __syncthreads();
+  if (wave == 0 && c < H) {
+    float *out = partial + (size_t)blockIdx.y * H + c;
+#pragma unroll
+    for (int j = 0; j < 32; j += 4) {
+      f32x4_t o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        o[k] = acc[j + k] + s_acc[0][(j + k) * 64 + lane] + s_acc[1][(j + k) * 64 + lane] +
+               s_acc[2][(j + k) * 64 + lane];
+      *reinterpret_cast<f32x4_t *>(out + j) = o;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    axpy_reduce_kernel(const float *__restrict__ partial, int slices, int H, float *__restrict__ y) {
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float s = 0.0f;
+  for (int k = 0; k < slices; ++k) s += partial[(size_t)k * H + h];
+  y[h] += s;
+}
+
+}  // namespace
+
+hipError_t transpose_requantize(const uint8_t *src, const uint8_t *src_scale_bits, int H, int I,
+                                int G, int sdt, uint8_t *dst, uint8_t *dst_scale_bits,
+                                hipStream_t st) {
+  const size_t n = (size_t)I * (H / 32);
+  hipLaunchKernelGGL(transpose_requantize_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     st, src, reinterpret_cast<const uint16_t *>(src_scale_bits), H, I, G, sdt,
+                     dst, reinterpret_cast<uint16_t *>(dst_scale_bits));
+  return hipGetLastError();
+}
+
+AxpyPlan axpy_plan(int H, int n_active) {
+  AxpyPlan p;
+  p.per_slice = 32;  // about eight rows per wave
+  p.slices = n_active > 0 ? (n_active + p.per_slice - 1) / p.per_slice : 0;
+  if (p.slices > 4096) {  // bound the partial rows: longer slices instead
+    p.slices = 4096;
+    p.per_slice = (n_active + 4095) / 4096;
+  }
+  p.partial_bytes = (size_t)p.slices * H * sizeof(float);
+  return p;
+}
+
+hipError_t axpy_active(const uint8_t *pt, const uint8_t *st_bits, const float *scalars,
+                       const uint32_t *active, int n_active, int H, int I, float *partial,
+                       float *y, hipStream_t st) {
+  const AxpyPlan p = axpy_plan(H, n_active);
+  if (p.slices == 0) return hipSuccess;
+  hipLaunchKernelGGL(axpy_active_kernel, dim3((H + 2047) / 2048, p.slices), dim3(256), 0, st, pt,
+                     reinterpret_cast<const uint16_t *>(st_bits), scalars, active, n_active,
+                     p.per_slice, H, I, partial);
+  hipLaunchKernelGGL(axpy_reduce_kernel, dim3((H + 255) / 256), dim3(256), 0, st, partial,
+                     p.slices, H, y);
+  return hipGetLastError();
+}
+
+}  // namespace cai4

@@ -177,6 +177,28 @@ int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_s
                                const void *x, uint32_t x_is_f32, uint32_t n_tokens,
                                float *inter_out, void *stream);
 
+/* The AXPY form of the sparse down projection (src/ffn_axpy.rs).
+ * transpose_requantize_down (ffn_axpy.rs:342-440, load time): the down matrix
+ * [hidden, inter] in the crate layout (groups of group_size along inter,
+ * bf16 or fp16 scales; the crate: 32, bf16) -> packed_t [inter, hidden / 2]
+ * (16-byte aligned) and bf16 scale_t [inter, hidden / 32], requantised in
+ * groups of 32 along hidden exactly as the crate (scale = max|v| / 7, 1.0
+ * for a zero group; codes round(v / scale) clamped to [-8, 7]).
+ * dequant_axpy_active (ffn_axpy.rs:82-160): y[hidden] += sum over a <
+ * n_active of scalars[active[a]] * dequant(packed_t[active[a], :]), only the
+ * active rows read; ids >= inter are skipped.  All pointers device;
+ * workspace >= cascadia_int4_axpy_workspace_bytes or NULL. */
+int cascadia_int4_transpose_requantize_down(uint32_t hidden, uint32_t inter,
+                                            uint32_t group_size, uint32_t scale_dtype,
+                                            const uint8_t *packed, const uint8_t *scale_bits,
+                                            uint8_t *packed_t, uint8_t *scale_t_bits,
+                                            void *stream);
+size_t cascadia_int4_axpy_workspace_bytes(uint32_t hidden, uint32_t n_active);
+int cascadia_int4_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *scale_t_bits,
+                                      const float *scalars, const uint32_t *active,
+                                      uint32_t n_active, uint32_t inter, uint32_t hidden,
+                                      float *y, void *workspace, void *stream);
+
 /* Activation-sparse expert FFN (src/ffn_sparsity.rs:438-538
  * ffn_forward_sparse_f32_mode, :756-867 expert_forward_sparse_mode; the
  * mask :131-179): gate in full, s = stable SiLU(gate), lanes with |s| >=

@@ -64,6 +64,8 @@ def _declare(L):
         "or_ffn_forward_f32": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp]),
         "or_expert_forward_sparse": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp]),
         "or_build_active_mask": (sz, [vp, sz, f32, vp, vp]),
+        "or_transpose_requantize_down": (None, [vp, vp, sz, sz, vp, vp]),
+        "or_dequant_axpy_active": (None, [vp, vp, vp, vp, sz, sz, sz, vp]),
         "or_build_active_mask_mode": (sz, [vp, sz, f32, vp, vp, vp]),
         "or_ffn_forward_f32_mode": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp, vp]),
         "or_expert_forward_sparse_mode": (f32, [vp, sz, sz, sz, i32, i32, vp, f32, vp, vp]),
@@ -202,6 +204,25 @@ def expert_forward_sparse(x_bf16, flat, hidden, inter, group, sdt, tau, order=OR
     frac = lib().or_expert_forward_sparse_mode(_p(x_bf16), hidden, inter, group, sdt, order,
                                                _p(flat), tau, tp, _p(out))
     return out, float(frac)
+
+
+def transpose_requantize_down(packed, scales, hidden, inter):
+    """ffn_axpy.rs:342: -> (packed_t u8[inter * hidden / 2], scale_t u8[inter * hidden / 32 * 2])."""
+    packed, scales = _c(packed, np.uint8), _c(scales, np.uint8)
+    pt = np.empty(inter * hidden // 2, np.uint8)
+    st = np.empty(inter * (hidden // 32) * 2, np.uint8)
+    lib().or_transpose_requantize_down(_p(packed), _p(scales), hidden, inter, _p(pt), _p(st))
+    return pt, st
+
+
+def dequant_axpy_active(packed_t, scale_t, scalars, active, inter, hidden, y=None):
+    """ffn_axpy.rs:82: y (f32 [hidden], default zeros) += sum over active rows."""
+    packed_t, scale_t = _c(packed_t, np.uint8), _c(scale_t, np.uint8)
+    scalars, active = _c(scalars, np.float32), _c(active, np.uint32)
+    y = np.zeros(hidden, np.float32) if y is None else _c(y, np.float32).copy()
+    lib().or_dequant_axpy_active(_p(packed_t), _p(scale_t), _p(scalars), _p(active), active.size,
+                                 inter, hidden, _p(y))
+    return y
 
 
 def build_active_mask(gate_out, tau, thresholds=None):

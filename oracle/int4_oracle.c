@@ -592,3 +592,75 @@ void or_fill_normal_f32(uint64_t seed, uint64_t stream, size_t n, float *out) {
 void or_fill_normal_bf16(uint64_t seed, uint64_t stream, size_t n, uint16_t *out) {
   for (size_t i = 0; i < n; i++) out[i] = or_f32_to_bf16((float)or_rng_normal(seed, stream, i));
 }
+
+/* ------------------------------------------------------------------ */
+/* AXPY-form down (ffn_axpy.rs)                                        */
+/* ------------------------------------------------------------------ */
+
+/* ffn_axpy.rs:342-440: the crate's down matrix [hidden, inter] (bf16 scales,
+ * groups of 32 along inter) dequantised, transposed to [inter, hidden] and
+ * quantised again in groups of 32 along hidden: scale = max|v| / 7 (1.0 for
+ * an all-zero group, whose codes are then 0), stored as bf16, codes
+ * round(v * (1 / scale)) with the f32 scale, half away from zero, clamped to
+ * [-8, 7].  The max ignores NaN (f32::max); a NaN code is 0 (`as i32`). */
+void or_transpose_requantize_down(const uint8_t *src_packed, const uint8_t *src_scale_bits,
+                                  size_t hidden, size_t inter, uint8_t *packed_t,
+                                  uint8_t *scale_t_bits) {
+  const size_t gs = inter / 32, gd = hidden / 32;
+  float *t = (float *)malloc(inter * hidden * sizeof(float));
+  for (size_t h = 0; h < hidden; h++)
+    for (size_t c = 0; c < inter; c++) {
+      const uint8_t b = src_packed[h * (inter / 2) + c / 2];
+      const int q = (int)((c & 1) ? (b >> 4) : (b & 15)) - 8;
+      const uint16_t sb = (uint16_t)(src_scale_bits[(h * gs + c / 32) * 2] |
+                                     (src_scale_bits[(h * gs + c / 32) * 2 + 1] << 8));
+      t[c * hidden + h] = (float)q * or_bf16_to_f32(sb);
+    }
+  for (size_t r = 0; r < inter; r++)
+    for (size_t g = 0; g < gd; g++) {
+      const float *v = t + r * hidden + g * 32;
+      float mx = 0.0f;
+      for (int i = 0; i < 32; i++) {
+        const float a = fabsf(v[i]);
+        if (a > mx) mx = a;
+      }
+      const float scale = mx == 0.0f ? 1.0f : mx / 7.0f;
+      const float inv = mx == 0.0f ? 0.0f : 1.0f / scale;
+      const uint16_t sb = or_f32_to_bf16(scale);
+      scale_t_bits[(r * gd + g) * 2] = (uint8_t)(sb & 0xFF);
+      scale_t_bits[(r * gd + g) * 2 + 1] = (uint8_t)(sb >> 8);
+      for (int i = 0; i < 16; i++) {
+        uint8_t nib[2];
+        for (int e = 0; e < 2; e++) {
+          const float qf = roundf(v[2 * i + e] * inv);
+          int q = qf != qf ? 0 : (qf > 7.0f ? 7 : (qf < -8.0f ? -8 : (int)qf));
+          nib[e] = (uint8_t)(q + 8);
+        }
+        packed_t[r * (hidden / 2) + g * 16 + i] = (uint8_t)(nib[0] | (nib[1] << 4));
+      }
+    }
+  free(t);
+}
+
+/* ffn_axpy.rs:82-160: y[hidden] += sum over r in active (in order) of
+ * scalars[r] * dequant(packed_t[r, :]); per element the product is
+ * (scalar * scale) * q, as the crate forms it. */
+void or_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *scale_t_bits,
+                            const float *scalars, const uint32_t *active, size_t n_active,
+                            size_t inter, size_t hidden, float *y) {
+  const size_t gd = hidden / 32;
+  (void)inter;
+  for (size_t a = 0; a < n_active; a++) {
+    const size_t r = active[a];
+    for (size_t g = 0; g < gd; g++) {
+      const uint16_t sb = (uint16_t)(scale_t_bits[(r * gd + g) * 2] |
+                                     (scale_t_bits[(r * gd + g) * 2 + 1] << 8));
+      const float comb = scalars[r] * or_bf16_to_f32(sb);
+      for (int i = 0; i < 16; i++) {
+        const uint8_t b = packed_t[r * (hidden / 2) + g * 16 + i];
+        y[g * 32 + 2 * i] += comb * (float)((int)(b & 15) - 8);
+        y[g * 32 + 2 * i + 1] += comb * (float)((int)(b >> 4) - 8);
+      }
+    }
+  }
+}

@@ -102,6 +102,15 @@ float or_expert_forward_sparse_mode(const uint16_t *x_bf16, size_t hidden, size_
                                     const uint8_t *expert_flat, float tau,
                                     const float *thresholds, uint16_t *out_bf16);
 
+/* ffn_axpy.rs:342-440 (G = 32, bf16 scales both sides). */
+void or_transpose_requantize_down(const uint8_t *src_packed, const uint8_t *src_scale_bits,
+                                  size_t hidden, size_t inter, uint8_t *packed_t,
+                                  uint8_t *scale_t_bits);
+/* ffn_axpy.rs:82-160: y += sum_{r in active} scalars[r] * W_t[r, :]. */
+void or_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *scale_t_bits,
+                            const float *scalars, const uint32_t *active, size_t n_active,
+                            size_t inter, size_t hidden, float *y);
+
 /* ---- routing ---- */
 /* K2.6 / GLM rule: sigmoid, choose top-k by (sigmoid + bias) with ties to the
  * lower id, weights = sigmoid of the chosen, optionally renormalised (+1e-20),

@@ -575,3 +575,55 @@ def test_sparse_branch_composition(orc):
         got, frac = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, tau)
         assert frac == len(act) / i and 0 < len(act) < i
         assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+def _crate_down(orc, h, i, codes, scale_bits):
+    """Crate bytes of a down matrix [h, i]: codes int [-8, 7], one scale per
+    row-group of 32 (uint16 bits, shape [h, i / 32])."""
+    nib = (codes + 8).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8).reshape(-1)
+    return packed, np.ascontiguousarray(scale_bits, np.uint16).view(np.uint8).reshape(-1)
+
+
+def test_transpose_requantize_closed_forms(orc):
+    """ffn_axpy.rs:342-440.  Codes in [-7, 7] with every destination group
+    holding a +-7, all source scales s (a power of two): each destination
+    group's max is 7 s, so its scale is s exactly and the codes are the
+    transposed source codes; an all-zero group gets scale 1.0 and code 0."""
+    h, i = 96, 64
+    rng = np.random.default_rng(4)
+    codes = rng.integers(-7, 8, (h, i))
+    codes[0::32, :] = 7 * np.where(rng.integers(0, 2, i), 1, -1)  # a +-7 in every (r, g)
+    codes[64:96, 5] = 0  # destination row 5, group 2: all zero
+    for s_bits, s_val in ((0x3F80, 1.0), (0x4000, 2.0), (0x3E00, 0.125)):
+        packed, scales = _crate_down(orc, h, i, codes, np.full((h, i // 32), s_bits))
+        pt, st = orc.transpose_requantize_down(packed, scales, h, i)
+        st = st.view(np.uint16).reshape(i, h // 32)
+        got = np.stack([pt & 15, pt >> 4], -1).reshape(i, h).astype(np.int64) - 8
+        want = codes.T.copy()
+        assert np.array_equal(got, want), s_val
+        exp_s = np.full((i, h // 32), s_bits, np.uint16)
+        exp_s[5, 2] = 0x3F80
+        assert np.array_equal(st, exp_s), s_val
+
+
+def test_axpy_is_transposed_gemv(orc):
+    """ffn_axpy.rs:82-160: with W_t the exact transpose of W (the closed form
+    above), y = sum_{r active} s_r W_t[r, :] is W . m with m = s on the
+    active rows and 0 elsewhere -- the oracle GEMV, pinned independently."""
+    h, i = 96, 64
+    rng = np.random.default_rng(5)
+    codes = rng.integers(-7, 8, (h, i))
+    codes[0::32, :] = 7
+    packed, scales = _crate_down(orc, h, i, codes, np.full((h, i // 32), 0x3F00))  # 0.5
+    pt, st = orc.transpose_requantize_down(packed, scales, h, i)
+    s = rng.normal(0, 1, i).astype(np.float32)
+    active = np.sort(rng.choice(i, 20, replace=False)).astype(np.uint32)
+    y = orc.dequant_axpy_active(pt, st, s, active, i, h)
+    m = np.zeros(i, np.float32)
+    m[active] = s[active]
+    want = orc.gemv(packed, scales, m, h, i, 32, BF16)
+    assert np.allclose(y, want, rtol=1e-5, atol=1e-5)
+    # accumulates onto y
+    y2 = orc.dequant_axpy_active(pt, st, s, active, i, h, y=np.ones(h, np.float32))
+    assert np.allclose(y2, y + 1, rtol=1e-6, atol=1e-6)
