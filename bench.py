@@ -283,6 +283,40 @@ def extra_measurements(cl, torch, args, sdt, copies):
                                              "active_frac": round(fr, 4),
                                              "GB/s": round(b / t / 1e9, 1),
                                              "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+    # the AXPY form of the sparse down (ffn_axpy.rs:82-160): config 1's down
+    # transposed to [inter, hidden], 13.4 % of the rows active (what tau 0.3
+    # selects above), over rotating copies larger than 2x the Infinity Cache
+    I1, H1 = i, h
+    ptb, stb = I1 * H1 // 2, I1 * (H1 // 32) * 2
+    nca = math.ceil(2 * MALL_BYTES / (ptb + stb)) + 1
+    AX = []
+    for c in range(nca):
+        p = cl.fill_bytes(torch.empty(H1 * I1 // 2, dtype=torch.uint8, device="cuda"), 2, 600 + c)
+        sc = cl.fill_scales(torch.empty(H1 * (I1 // 32) * 2, dtype=torch.uint8, device="cuda"),
+                            2, 700 + c, cl.SCALE_BF16)
+        AX.append(cl.transpose_requantize_down(p, sc, H1, I1))
+        del p, sc
+    n_act = int(round(0.1344 * I1))
+    act = torch.sort(torch.randperm(I1, device="cuda")[:n_act])[0].to(torch.int32)
+    sca = cl.fill_normal(torch.empty(I1, dtype=torch.float32, device="cuda"), 2, 11)
+    ya = torch.zeros(H1, dtype=torch.float32, device="cuda")
+    wsa = torch.empty(cl.lib().cascadia_int4_axpy_workspace_bytes(H1, n_act), dtype=torch.uint8,
+                      device="cuda")
+
+    def axpy(r):
+        pt_, st_ = AX[r % nca]
+        cl.dequant_axpy_int4_active(pt_, st_, sca, act, I1, H1, ya, workspace=wsa)
+    for r in range(5):
+        axpy(r)
+    steps = 200
+    w, _ = graph_time(torch, axpy, steps)
+    t = w / steps
+    b = n_act * (H1 // 2 + (H1 // 32) * 2 + 8) + 2 * H1 * 4
+    res["axpy_down_config1_13pct"] = {"us_per_call": round(t * 1e6, 2), "active_rows": n_act,
+                                      "GB/s": round(b / t / 1e9, 1),
+                                      "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+                                      "copies": nca}
+    del AX
     # config 2: prefill GEMM (bf16 in/out)
     for (m, nn) in PREFILL_SHAPES:
         pre = prefill_fn(cl, torch, m, nn, 4096, g, sdt)

@@ -9,7 +9,8 @@
 // axpy_active_kernel  y[hidden] += sum over the active rows r of
 //   scalar[r] * W_t[r, :] (ffn_axpy.rs:82-160): only the active rows are
 //   read, which is what the transposed layout buys.  Grid (column chunk of
-//   2048, row slice); a lane holds 32 columns of f32 sums, the block's four
+//   2048, slice of 64 active rows); a lane holds 32 columns of f32 sums and
+//   each of the block's eight waves keeps eight rows' loads in flight; the
 //   waves are folded through LDS into one partial row per slice, and
 //   axpy_reduce_kernel adds the slices to y in slice order (deterministic).
 #include "int4_common.hpp"
@@ -53,11 +54,13 @@ __global__ void __launch_bounds__(256)
       u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
-__global__ void __launch_bounds__(256)
+constexpr int kAxWaves = 8, kAxRows = 8;  // a slice: 64 active rows, 8 per wave in flight
+
+__global__ void __launch_bounds__(64 * kAxWaves)
     axpy_active_kernel(const uint8_t *__restrict__ pt, const uint16_t *__restrict__ st,
                        const float *__restrict__ scalars, const uint32_t *__restrict__ active,
                        int n_active, int per_slice, int H, int I, float *__restrict__ partial) {
-  __shared__ float s_acc[3][2048];
+  __shared__ float s_acc[kAxWaves - 1][2048];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = blockIdx.x * 2048 + 32 * lane;  // this lane's 32 columns
   const int a0 = blockIdx.y * per_slice;
@@ -67,19 +70,32 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int j = 0; j < 32; ++j) acc[j] = 0.0f;
   if (c < H) {
-    for (int a = a0 + wave; a < a1; a += 4) {
-      const uint32_t r = active[a];
-      if (r >= (uint32_t)I) continue;  // ids past the intermediate size are ignored
-      const u32x4_t q = *reinterpret_cast<const u32x4_t *>(pt + (size_t)r * (H / 2) + c / 2);
-      const float comb = scalars[r] * bf16_to_f32(st[(size_t)r * GD + c / 32]);
+    for (int a = a0 + wave; a < a1; a += kAxWaves * kAxRows) {
+      uint32_t r[kAxRows];
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
+      for (int k = 0; k < kAxRows; ++k) {
+        const int ak = a + k * kAxWaves;
+        r[k] = ak < a1 ? active[ak] : 0xFFFFFFFFu;
+      }
+      u32x4_t q[kAxRows];
+      float comb[kAxRows];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          acc[8 * d + e] += comb * (float)((int)((q[d] >> (4 * e)) & 15u) - 8);
+      for (int k = 0; k < kAxRows; ++k) {
+        const bool ok = r[k] < (uint32_t)I;  // ids past the intermediate size are skipped
+        q[k] = ok ? *reinterpret_cast<const u32x4_t *>(pt + (size_t)r[k] * (H / 2) + c / 2)
+                  : u32x4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+        comb[k] = ok ? scalars[r[k]] * bf16_to_f32(st[(size_t)r[k] * GD + c / 32]) : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < kAxRows; ++k)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            acc[8 * d + e] += comb[k] * (float)((int)((q[k][d] >> (4 * e)) & 15u) - 8);
     }
   }
-  // fold waves 1..3 into wave 0 through LDS (column-major per lane)
+  // fold waves 1.. into wave 0 through LDS (column-major per lane)
   if (wave > 0) {
 #pragma unroll
     for (int j = 0; j < 32; ++j) s_acc[wave - 1][j * 64 + lane] = acc[j];
@@ -91,9 +107,12 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < 32; j += 4) {
       f32x4_t o;
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        o[k] = acc[j + k] + s_acc[0][(j + k) * 64 + lane] + s_acc[1][(j + k) * 64 + lane] +
-               s_acc[2][(j + k) * 64 + lane];
+      for (int k = 0; k < 4; ++k) {
+        float v = acc[j + k];
+#pragma unroll
+        for (int w = 0; w < kAxWaves - 1; ++w) v += s_acc[w][(j + k) * 64 + lane];
+        o[k] = v;
+      }
       *reinterpret_cast<f32x4_t *>(out + j) = o;
     }
   }
@@ -103,8 +122,15 @@ __global__ void __launch_bounds__(256)
     axpy_reduce_kernel(const float *__restrict__ partial, int slices, int H, float *__restrict__ y) {
   const int h = blockIdx.x * 256 + threadIdx.x;
   if (h >= H) return;
+  // eight slices' loads in flight, added in slice order
   float s = 0.0f;
-  for (int k = 0; k < slices; ++k) s += partial[(size_t)k * H + h];
+  for (int k = 0; k < slices; k += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = k + j < slices ? partial[(size_t)(k + j) * H + h] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
+  }
   y[h] += s;
 }
 
@@ -122,7 +148,7 @@ hipError_t transpose_requantize(const uint8_t *src, const uint8_t *src_scale_bit
 
 AxpyPlan axpy_plan(int H, int n_active) {
   AxpyPlan p;
-  p.per_slice = 32;  // about eight rows per wave
+  p.per_slice = kAxWaves * kAxRows;
   p.slices = n_active > 0 ? (n_active + p.per_slice - 1) / p.per_slice : 0;
   if (p.slices > 4096) {  // bound the partial rows: longer slices instead
     p.slices = 4096;
@@ -137,7 +163,8 @@ hipError_t axpy_active(const uint8_t *pt, const uint8_t *st_bits, const float *s
                        float *y, hipStream_t st) {
   const AxpyPlan p = axpy_plan(H, n_active);
   if (p.slices == 0) return hipSuccess;
-  hipLaunchKernelGGL(axpy_active_kernel, dim3((H + 2047) / 2048, p.slices), dim3(256), 0, st, pt,
+  hipLaunchKernelGGL(axpy_active_kernel, dim3((H + 2047) / 2048, p.slices), dim3(64 * kAxWaves), 0,
+                     st, pt,
                      reinterpret_cast<const uint16_t *>(st_bits), scalars, active, n_active,
                      p.per_slice, H, I, partial);
   hipLaunchKernelGGL(axpy_reduce_kernel, dim3((H + 255) / 256), dim3(256), 0, st, partial,
