@@ -9,8 +9,8 @@
 // axpy_active_kernel  y[hidden] += sum over the active rows r of
 //   scalar[r] * W_t[r, :] (ffn_axpy.rs:82-160): only the active rows are
 //   read, which is what the transposed layout buys.  Grid (column chunk of
-//   2048, slice of 64 active rows); a lane holds 32 columns of f32 sums and
-//   each of the block's eight waves keeps eight rows' loads in flight; the
+//   2048, slice of 32 active rows); a lane holds 32 columns of f32 sums and
+//   each of the block's eight waves keeps four rows' loads in flight; the
 //   waves are folded through LDS into one partial row per slice, and
 //   axpy_reduce_kernel adds the slices to y in slice order (deterministic).
 #include "int4_common.hpp"
@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(256)
       u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
-constexpr int kAxWaves = 8, kAxRows = 8;  // a slice: 64 active rows, 8 per wave in flight
+constexpr int kAxWaves = 8, kAxRows = 4;  // a slice: 32 active rows, 4 per wave in flight
 
 __global__ void __launch_bounds__(64 * kAxWaves)
     axpy_active_kernel(const uint8_t *__restrict__ pt, const uint16_t *__restrict__ st,
@@ -118,20 +118,29 @@ __global__ void __launch_bounds__(64 * kAxWaves)
   }
 }
 
+// 64 columns per block; wave w adds slices w, w + 4, ... (eight loads in
+// flight), and the four wave sums are added in wave order: deterministic.
 __global__ void __launch_bounds__(256)
     axpy_reduce_kernel(const float *__restrict__ partial, int slices, int H, float *__restrict__ y) {
-  const int h = blockIdx.x * 256 + threadIdx.x;
-  if (h >= H) return;
-  // eight slices' loads in flight, added in slice order
+  __shared__ float s_sum[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = blockIdx.x * 64 + lane;
   float s = 0.0f;
-  for (int k = 0; k < slices; k += 8) {
-    float v[8];
+  if (h < H) {
+    for (int k = wave; k < slices; k += 32) {
+      float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = k + j < slices ? partial[(size_t)(k + j) * H + h] : 0.0f;
+      for (int j = 0; j < 8; ++j) {
+        const int kk = k + 4 * j;
+        v[j] = kk < slices ? partial[(size_t)kk * H + h] : 0.0f;
+      }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += v[j];
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
   }
-  y[h] += s;
+  s_sum[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && h < H) y[h] += ((s_sum[0][lane] + s_sum[1][lane]) + s_sum[2][lane]) + s_sum[3][lane];
 }
 
 }  // namespace
@@ -167,7 +176,7 @@ hipError_t axpy_active(const uint8_t *pt, const uint8_t *st_bits, const float *s
                      st, pt,
                      reinterpret_cast<const uint16_t *>(st_bits), scalars, active, n_active,
                      p.per_slice, H, I, partial);
-  hipLaunchKernelGGL(axpy_reduce_kernel, dim3((H + 255) / 256), dim3(256), 0, st, partial,
+  hipLaunchKernelGGL(axpy_reduce_kernel, dim3((H + 63) / 64), dim3(256), 0, st, partial,
                      p.slices, H, y);
   return hipGetLastError();
 }
