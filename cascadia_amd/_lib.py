@@ -81,6 +81,7 @@ SIGNATURES = {
     "cascadia_int4_expert_from_flat": (_i32, [_vp, _u32, _u32, _u32, _EP]),
     "cascadia_int4_ffn_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
     "cascadia_int4_expert_forward_device": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
+    "cascadia_int4_expert_forward_noalloc": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp]),
     "cascadia_int4_ffn_forward_f32": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _vp, _vp, _vp]),
     "cascadia_int4_gate_up_silu": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, _u32, _vp, _vp]),
     "cascadia_int4_moe_workspace_bytes": (_sz, [_MP, _u32, _u32]),

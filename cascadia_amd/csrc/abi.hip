@@ -35,6 +35,27 @@ std::mutex g_mu;
 std::mutex g_side_mu;  // held from a fork onto the side stream to the join
 DeviceState g_dev[kMaxDevices];
 
+// Scratch of cascadia_int4_expert_forward_noalloc: a file-scope device array,
+// one copy per GPU, held until the process ends.  In host code `scratch`
+// names a host-side stand-in; its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+constexpr size_t kNoAllocScratchBytes = CASCADIA_INT4_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+void *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on device `dev` (which must be current).
+int noalloc_scratch(int dev, void **out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+      return CASCADIA_INT4_ERR_DEVICE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CASCADIA_INT4_OK;
+}
+
 int current_device(int *dev) {
   if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kMaxDevices)
     return CASCADIA_INT4_ERR_DEVICE;
@@ -136,10 +157,12 @@ bool act_fits(int M, int K, int amode) {
 }
 
 // One skinny GEMM (any M), f32 output or fused epilogue.  `partials` is
-// workspace for split-K partial sums (null: the library's own workspace).
+// workspace for split-K partial sums (null: the library's own workspace,
+// unless `may_alloc` is false, when a plan that needs partials is an error).
 int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint8_t *s1,
              int N, int K, int G, int sdt, int tiled, const void *x, const void *x2, int amode,
-             int M, void *out, void *out2, int epi, hipStream_t st, void *partials = nullptr) {
+             int M, void *out, void *out2, int epi, hipStream_t st, void *partials = nullptr,
+             bool may_alloc = true) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
   if (!act_fits(M, K, amode)) return CASCADIA_INT4_ERR_ARG;
@@ -165,6 +188,7 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   }
   const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, G, M, amode, epi, d);
   if (p.partial_bytes && !partials) {
+    if (!may_alloc) return CASCADIA_INT4_ERR_ARG;
     if (int rc = lib_workspace(dev, p.partial_bytes, &partials)) return rc;
   }
   cai4::SkinnyArgs a{};
@@ -258,14 +282,16 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   uint16_t *hi = reinterpret_cast<uint16_t *>(ws);
   uint16_t *lo = hi + (size_t)n_tokens * inter;
   void *part = need.partials ? static_cast<uint8_t *>(ws) + need.planes : nullptr;
+  // a caller's workspace (or the static scratch) is never supplemented by an allocation
+  const bool may_alloc = workspace == nullptr;
   int rc = run_gemm(e->gate_packed, e->gate_scale, e->up_packed, e->up_scale, (int)inter,
                     (int)hidden, (int)group, (int)sdt, (int)e->tiling, x, nullptr,
                     x_f32 ? cai4::A_XF32 : cai4::A_BF16, (int)n_tokens, hi, lo,
-                    cai4::EPI_SWIGLU_HILO, st, part);
+                    cai4::EPI_SWIGLU_HILO, st, part, may_alloc);
   if (rc) return rc;
   return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
                   (int)group, (int)sdt, (int)e->tiling, hi, lo, cai4::A_HILO, (int)n_tokens,
-                  out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st, part);
+                  out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st, part, may_alloc);
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -855,6 +881,24 @@ int cascadia_int4_expert_forward_device(uint32_t hidden, uint32_t inter, uint32_
                                         uint16_t *out_bf16, void *workspace, void *stream) {
   return ffn_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false,
                     n_tokens, out_bf16, true, workspace, (hipStream_t)stream);
+}
+
+int cascadia_int4_expert_forward_noalloc(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                         uint32_t scale_dtype,
+                                         const cascadia_int4_expert *expert,
+                                         const uint16_t *x_bf16, uint32_t n_tokens,
+                                         uint16_t *out_bf16, void *stream) {
+  if (int rc = check_expert(hidden, inter, group_size, scale_dtype, expert)) return rc;
+  if (!x_bf16 || !out_bf16) return CASCADIA_INT4_ERR_NULL;
+  if (n_tokens == 0) return CASCADIA_INT4_OK;
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const FfnWorkspace need = ffn_workspace(dev, hidden, inter, group_size, n_tokens, false);
+  if (need.planes + need.partials > kNoAllocScratchBytes) return CASCADIA_INT4_ERR_ARG;
+  void *ws = nullptr;
+  if (int rc = noalloc_scratch(dev, &ws)) return rc;
+  return ffn_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false, n_tokens,
+                    out_bf16, true, ws, (hipStream_t)stream);
 }
 
 int cascadia_int4_ffn_forward_f32(uint32_t hidden, uint32_t inter, uint32_t group_size,

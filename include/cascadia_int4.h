@@ -167,6 +167,24 @@ int cascadia_int4_expert_forward_device(uint32_t hidden, uint32_t inter, uint32_
                                         const uint16_t *x_bf16, uint32_t n_tokens,
                                         uint16_t *out_bf16, void *workspace, void *stream);
 
+/* cascadia_int4_expert_forward_device without a workspace argument and
+ * without any allocation: no counterpart in the reference crate.  For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The SwiGLU intermediate
+ * and split-K partials live in a file-scope device array of
+ * CASCADIA_INT4_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends;
+ * a call whose cascadia_int4_ffn_workspace_bytes(hidden, inter, group_size,
+ * n_tokens) exceeds it returns CASCADIA_INT4_ERR_ARG (config 1's Llama-3-8B
+ * FFN fits up to 64 tokens).  Every call on one GPU shares that array, so
+ * calls that overlap on one GPU (different streams, or threads) race;
+ * serialise them.  Same kernels and results as the _device entry point. */
+#define CASCADIA_INT4_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int cascadia_int4_expert_forward_noalloc(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                                         uint32_t scale_dtype,
+                                         const cascadia_int4_expert *expert,
+                                         const uint16_t *x_bf16, uint32_t n_tokens,
+                                         uint16_t *out_bf16, void *stream);
+
 /* First half of the expert FFN: inter[t, i] = silu(W_g·x_t)[i] * (W_u·x_t)[i]
  * in f32 (kernel.rs:96-120; the batched gate/up + swiglu_mul of
  * shell_int4.rs:1112-1130).  x: [n_tokens, hidden], bf16 bits when x_is_f32
