@@ -84,6 +84,7 @@ def _declare(L):
         "or_cpu_threads": (i32, []),
         "or_cpu_gemm": (None, [vp, vp, vp, sz, sz, sz, sz, i32, vp]),
         "or_cpu_expert_forward": (None, [vp, sz, sz, sz, sz, i32, vp, vp]),
+        "or_cpu_moe_layer": (None, [vp, sz, sz, sz, sz, i32, vp, sz, sz, vp, sz, vp, vp, sz, f32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -342,4 +343,22 @@ def cpu_expert_forward(x_bf16, n_tokens, flat, hidden, inter, group, sdt, out=No
     if out is None:
         out = np.empty((n_tokens, hidden), np.uint16)
     lib().or_cpu_expert_forward(_p(x_bf16), n_tokens, hidden, inter, group, sdt, _p(flat), _p(out))
+    return out
+
+
+def cpu_moe_layer(x, experts, n_experts, shared, shared_inter, hidden, inter, group, sdt, ids,
+                  weights, threshold=0.0, stride=None):
+    """The runner's per-(token, slot) MoE loop on the crate-dispatch CPU
+    kernels (timed baseline; bit-identical per token to moe_layer)."""
+    x = _c(x, np.float32)
+    T = x.size // hidden
+    experts = _c(experts, np.uint8)
+    stride = experts.size // n_experts if stride is None else stride
+    ids, weights = _c(ids, np.int64), _c(weights, np.float32)
+    k = ids.size // T
+    sh = None if shared is None else _c(shared, np.uint8)
+    out = np.empty((T, hidden), np.float32)
+    lib().or_cpu_moe_layer(_p(x), T, hidden, inter, group, sdt, _p(experts), stride, n_experts,
+                           None if sh is None else _p(sh), shared_inter, _p(ids), _p(weights), k,
+                           threshold, _p(out))
     return out

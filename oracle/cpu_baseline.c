@@ -252,3 +252,57 @@ void or_cpu_expert_forward(const uint16_t *x_bf16, size_t n_tokens, size_t hidde
   free(u);
   free(o);
 }
+
+/* Dense SwiGLU FFN, f32 in / f32 out (ffn_sparsity.rs:465-496 at tau 0, the
+ * shared expert of shell_int4.rs:629) on the crate-dispatch GEMV. */
+static void cpu_ffn_f32(const float *x, size_t hidden, size_t inter, size_t group, int sdt,
+                        const uint8_t *flat, float *out) {
+  size_t off[6];
+  or_expert_offsets(hidden, inter, group, off);
+  float *g = (float *)malloc(inter * sizeof(float));
+  float *u = (float *)malloc(inter * sizeof(float));
+  gemv_any(flat + off[0], flat + off[1], x, inter, hidden, group, sdt, g);
+  gemv_any(flat + off[2], flat + off[3], x, inter, hidden, group, sdt, u);
+  for (size_t i = 0; i < inter; i++) g[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+  gemv_any(flat + off[4], flat + off[5], g, hidden, inter, group, sdt, out);
+  free(g);
+  free(u);
+}
+
+/* One MoE layer as the runner runs it (runner.rs:1806-1832; multi-token
+ * steps keep the same per-token, per-expert loop, :2079-2108): per token,
+ * per slot in selection order, skip w < threshold (:1811), y =
+ * expert_forward(bf16(x_t)) (:1066-1093), moe += w * y; then
+ * h = (x + shared(x)) + moe with the shared expert f32 in / f32 out.  Each
+ * GEMV is the crate's rayon-parallel AVX-512 kernel; per token the result is
+ * bit-identical to or_moe_layer at OR_ORDER_AVX512 (checked in tests/). */
+void or_cpu_moe_layer(const float *x, size_t n_tokens, size_t hidden, size_t inter,
+                      size_t group, int scale_dtype, const uint8_t *experts_base,
+                      size_t expert_stride, size_t n_experts, const uint8_t *shared_flat,
+                      size_t shared_inter, const int64_t *ids, const float *weights,
+                      size_t top_k, float threshold, float *h_out) {
+  uint16_t *xb = (uint16_t *)malloc(hidden * sizeof(uint16_t));
+  uint16_t *yb = (uint16_t *)malloc(hidden * sizeof(uint16_t));
+  float *moe = (float *)malloc(hidden * sizeof(float));
+  float *sh = (float *)calloc(hidden, sizeof(float));
+  for (size_t t = 0; t < n_tokens; t++) {
+    const float *xt = x + t * hidden;
+    for (size_t j = 0; j < hidden; j++) moe[j] = 0.0f;
+    for (size_t j = 0; j < hidden; j++) xb[j] = or_f32_to_bf16(xt[j]);
+    for (size_t k = 0; k < top_k; k++) {
+      float w = weights[t * top_k + k];
+      if (w < threshold) continue;
+      int64_t e = ids[t * top_k + k];
+      if (e < 0 || (size_t)e >= n_experts) continue;
+      or_cpu_expert_forward(xb, 1, hidden, inter, group, scale_dtype,
+                            experts_base + (size_t)e * expert_stride, yb);
+      for (size_t j = 0; j < hidden; j++) moe[j] += w * or_bf16_to_f32(yb[j]);
+    }
+    if (shared_flat) cpu_ffn_f32(xt, hidden, shared_inter, group, scale_dtype, shared_flat, sh);
+    for (size_t j = 0; j < hidden; j++) h_out[t * hidden + j] = xt[j] + sh[j] + moe[j];
+  }
+  free(xb);
+  free(yb);
+  free(moe);
+  free(sh);
+}

@@ -164,6 +164,11 @@ void or_cpu_gemm(const uint8_t *packed, const uint8_t *scale_bits, const float *
 void or_cpu_expert_forward(const uint16_t *x_bf16, size_t n_tokens, size_t hidden,
                            size_t inter, size_t group, int scale_dtype,
                            const uint8_t *expert_flat, uint16_t *out_bf16);
+void or_cpu_moe_layer(const float *x, size_t n_tokens, size_t hidden, size_t inter,
+                      size_t group, int scale_dtype, const uint8_t *experts_base,
+                      size_t expert_stride, size_t n_experts, const uint8_t *shared_flat,
+                      size_t shared_inter, const int64_t *ids, const float *weights,
+                      size_t top_k, float threshold, float *h_out);
 
 #ifdef __cplusplus
 }

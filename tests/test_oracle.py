@@ -461,6 +461,37 @@ def test_moe_combine_slot_order_and_threshold(orc):
         assert np.array_equal(layer[t], ((x[t] + sh).astype(np.float32) + got[t]).astype(np.float32))
 
 
+@pytest.mark.parametrize("group,sdt,thr", [(32, BF16, 0.1), (128, F16, 0.0)])
+def test_cpu_moe_layer_bit_identical_to_oracle(orc, group, sdt, thr):
+    """The timed per-(token, slot) MoE loop on the AVX-512 kernels (the MoE
+    CPU baseline, and the checker of full-size GPU MoE layers) equals the
+    restatement's layer at the AVX-512 order, bitwise, shared expert included."""
+    if orc.cpu_isa() != 2:
+        pytest.skip("host has no AVX-512; the port then uses another order")
+    h, i, E, k, T, si = 256, 128, 6, 3, 4, 64
+    per = orc.expert_bytes(h, i, group)
+    offs, sizes = orc.expert_offsets(h, i, group)
+    experts = np.concatenate([orc.fill_bytes(3, 10 + e, per) for e in range(E)])
+    for e in range(E):
+        for s_ in (1, 3, 5):
+            o = e * per + offs[s_]
+            experts[o:o + sizes[s_]] = orc.fill_scales(3, 20 + 10 * e + s_, sizes[s_] // 2, sdt).view(np.uint8)
+    shared = orc.fill_bytes(3, 90, orc.expert_bytes(h, si, group))
+    so, ss = orc.expert_offsets(h, si, group)
+    for s_ in (1, 3, 5):
+        shared[so[s_]:so[s_] + ss[s_]] = orc.fill_scales(3, 91 + s_, ss[s_] // 2, sdt).view(np.uint8)
+    x = orc.fill_normal_f32(3, 7, T * h).reshape(T, h)
+    rng = np.random.default_rng(4)
+    ids = rng.integers(0, E, size=(T, k)).astype(np.int64)
+    w = rng.random((T, k)).astype(np.float32)
+    want = orc.moe_layer(x, experts, E, shared, si, h, i, group, sdt, ids, w, thr)
+    got = orc.cpu_moe_layer(x, experts, E, shared, si, h, i, group, sdt, ids, w, thr)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    want0 = orc.moe_layer(x, experts, E, None, 0, h, i, group, sdt, ids, w, thr)
+    got0 = orc.cpu_moe_layer(x, experts, E, None, 0, h, i, group, sdt, ids, w, thr)
+    assert np.array_equal(got0.view(np.uint32), want0.view(np.uint32))
+
+
 # ----------------------------------------------------------------------------
 # a11: load-time quantiser (shell_int4.rs:148-212)
 # ----------------------------------------------------------------------------
