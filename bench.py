@@ -1,7 +1,8 @@
 """Benchmark of the INT4 weight-only matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--extra]
-    python bench.py --profile        # the headline kernels only, for rocprofv3
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--headline-only]
+    python bench.py --profile | --profile-gemv | --profile-prefill | --profile-moe | --profile-sparse
+        (launch one workload eagerly, untimed, for rocprofv3)
 
 Headline: the Llama-3-8B-shaped decode FFN chain,
 gate/up 14336x4096 + down 4096x14336, INT4 group 128 with fp16 scales, bf16
@@ -17,10 +18,18 @@ bracketed by synchronisations, as a server's decode loop would run them.
 `value` = algorithmic bytes per step (3 x (packed + scales) + M*H*2*2: the
 weights read once plus activations in and out) x steps / wall time of the
 timed region -> GB/s.  The roofline object covers the dominant kernel (the
-fused gate/up kernel), timed the same way with HIP events recorded on the
-stream the kernels run on.  The CPU baseline is the oracle's AVX-512 port of
-the crate's kernels on the host cores, on a bounded sample of the same
-workload (same bytes).
+fused gate/up kernel), timed with HIP events recorded on the stream the
+kernels run on.  The CPU baseline is the oracle's AVX-512 port of the crate's
+kernels on the host cores, on a bounded sample of the same workload.
+
+`extra` (unless --headline-only) measures every other BASELINE config the
+same way -- config 0 GEMV, config 1 at M 4 / 16, the four config 2 prefill
+GEMMs, config 3 MoE at T 1 / 32 / 256, config 4 (four stacked layers) at T 1
+/ 8 / 64 / 1024 -- each with event-timed GPU time, algorithmic bytes or flops,
+the roofline fraction, and a CPU baseline of the crate's own dispatch on a
+bounded sample (the per-token loop for seq > 64; the runner's per-(token,
+slot) loop for MoE); plus the box's measured copy / read ceilings and the
+f1 / f3 paths (shell projections, activation-sparse expert, AXPY down).
 """
 from __future__ import annotations
 
@@ -38,6 +47,8 @@ MALL_BYTES = 256 << 20
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "config1_gate_up_traffic.json")
+PREFILL_SHAPES = [(512, 4096), (512, 14336), (2048, 4096), (2048, 14336)]
+CPU_SAMPLE_S = 2.0  # CPU seconds per secondary baseline
 
 
 def parse():
@@ -46,9 +57,12 @@ def parse():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--m", type=int, default=1, help="decode batch (tokens) of the headline")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--extra", action="store_true", help="also time configs 0 and 2, M=4/16")
+    ap.add_argument("--headline-only", action="store_true", help="skip the other configs")
+    ap.add_argument("--extra", action="store_true", help="(default behaviour; kept for scripts)")
+    ap.add_argument("--profile-gemv", action="store_true",
+                    help="launch the config 0 GEMV 200 times over rotating copies, for rocprofv3")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="launch the config 2 prefill GEMMs eagerly, without timing, for rocprofv3")
     ap.add_argument("--profile-sparse", action="store_true",
@@ -63,6 +77,10 @@ def parse():
     return ap.parse_args()
 
 
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
 def ffn_bytes(h, i, g, m):
     w = 3 * (i * h // 2 + i * (h // g) * 2)
     return w + m * h * 2 * 2
@@ -70,6 +88,37 @@ def ffn_bytes(h, i, g, m):
 
 def gate_up_bytes(h, i, g, m):
     return 2 * (i * h // 2 + i * (h // g) * 2) + m * h * 2 + m * i * 4
+
+
+def host_cpu():
+    """nproc, the OpenMP threads the CPU port uses, and the CPU model."""
+    import oracle as orc
+
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "threads": orc.cpu_threads(), "model": model,
+            "isa": {2: "avx512", 1: "avx2", 0: "scalar"}[orc.cpu_isa()]}
+
+
+def cpu_loop(fn, seconds):
+    """Call fn(n) for n = 0, 1, ... for about `seconds` (one untimed warm-up
+    call first); returns (calls, elapsed)."""
+    fn(0)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        fn(n)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            return n, dt
 
 
 class Copies:
@@ -137,7 +186,9 @@ def gate_up_fn(cl, copies, x, inter, sdt):
     return fn
 
 
-def cpu_baseline(torch, copies, x, m, seconds):
+def cpu_chain_baseline(torch, copies, x, m, seconds):
+    """expert_forward chains on the host (the crate's dispatch: a4 at one
+    token, the blocked / multi tiles at 4..64), rotating the host copies."""
     import numpy as np
 
     import oracle as orc
@@ -146,13 +197,10 @@ def cpu_baseline(torch, copies, x, m, seconds):
     host = [c.cpu().numpy() for c in copies.crate]
     xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
     out = np.empty((m, h), np.uint16)
-    orc.cpu_expert_forward(xb, m, host[0], h, i, g, orc.SCALE_F16, out)  # warm-up
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+
+    def run(n):
         orc.cpu_expert_forward(xb, m, host[n % len(host)], h, i, g, orc.SCALE_F16, out)
-        n += 1
-    dt = time.perf_counter() - t0
+    n, dt = cpu_loop(run, seconds)
     isa = {2: "avx512", 1: "avx2", 0: "scalar"}[orc.cpu_isa()]
     return {
         "value": round(ffn_bytes(h, i, g, m) * n / dt / 1e9, 3),
@@ -177,23 +225,46 @@ def read_traffic(m):
         return None
 
 
-def extra_measurements(cl, torch, args, sdt, copies):
-    """Secondary numbers (not the headline): M=4/16 chains, config 0 GEMV, the
-    K2.6 shell projections at one token, config 2 prefill GEMM."""
-    res = {}
-    h, i, g = copies.h, copies.i, copies.g
-    for mm in (4, 16):
-        xm = cl.fill_normal(torch.empty((mm, h), dtype=torch.bfloat16, device="cuda"), 0, 22)
-        om = torch.empty((mm, h), dtype=torch.bfloat16, device="cuda")
-        fn = chain_fn(cl, copies, xm, om, sdt)
-        for k in range(10):
-            fn(k)
-        w2, _ = graph_time(torch, fn, args.steps)
-        res[f"config1_M{mm}"] = {"GB/s": round(ffn_bytes(h, i, g, mm) * args.steps / w2 / 1e9, 1),
-                                 "us_per_chain": round(w2 / args.steps * 1e6, 2),
-                                 "tokens_per_s": round(mm * args.steps / w2, 1)}
-    # config 0: 4096x4096 GEMV, f32 x, rotating > 2x MALL of weight copies
+# ---------------------------------------------------------------------------
+# the other BASELINE configs
+# ---------------------------------------------------------------------------
+
+def hbm_ceiling(torch):
+    """The box's measured streaming ceilings: a 1 GiB device copy (read +
+    write bytes) and a 1 GiB read-only reduction, event-timed."""
+    a = torch.ones(256 << 20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+        a.sum()
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    reps = 20
+    e[0].record()
+    for _ in range(reps):
+        b.copy_(a)
+    e[1].record()
+    for _ in range(reps):
+        a.sum()
+    e[2].record()
+    torch.cuda.synchronize()
+    nb = a.numel() * 4
+    tc = e[0].elapsed_time(e[1]) / 1e3 / reps
+    tr = e[1].elapsed_time(e[2]) / 1e3 / reps
+    del a, b
+    return {"copy_GBps": round(2 * nb / tc / 1e9, 1), "read_GBps": round(nb / tr / 1e9, 1),
+            "bytes": nb, "note": "1 GiB device copy (read + write counted) and 1 GiB sum (read)"}
+
+
+def config0(cl, torch, sdt, cpu):
+    """Config 0: one 4096x4096 GEMV, f32 x, G128 fp16, over > 2x MALL of
+    rotating weight copies."""
+    import numpy as np
+
+    import oracle as orc
+
     n = k = 4096
+    g = 128
     nb, nsb = n * k // 2, n * (k // g) * 2
     ncp = math.ceil(2 * MALL_BYTES / (nb + nsb)) + 1
     PS = []
@@ -212,12 +283,243 @@ def extra_measurements(cl, torch, args, sdt, copies):
     for r in range(10):
         gemv(r)
     steps = 1000
-    w, _ = graph_time(torch, gemv, steps)
-    t = w / steps
+    wall, ev = graph_time(torch, gemv, steps)
+    t = ev / steps
     b = nb + nsb + k * 4 + n * 4
-    res["config0_gemv"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(b / t / 1e9, 1),
-                           "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4), "copies": ncp}
+    res = {"us_per_call": round(t * 1e6, 3), "wall_us_per_call": round(wall / steps * 1e6, 3),
+           "GB/s": round(b / t / 1e9, 1), "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+           "kernel": "gemv_kernel (one token, MFMA-tiled weights)", "algorithmic_bytes": b,
+           "copies": ncp}
     del PS
+    if cpu:
+        hc = 16  # 139 MB of host copies: more than the host's last-level cache
+        hp = [orc.fill_bytes(0, 200 + c, nb) for c in range(hc)]
+        hs = [orc.fill_scales(0, 300 + c, nsb // 2, sdt).view(np.uint8).copy() for c in range(hc)]
+        xh = x.cpu().numpy()
+        yh = np.empty(n, np.float32)
+
+        def run(r):
+            orc.cpu_gemm(hp[r % hc], hs[r % hc], xh, n, k, 1, g, sdt, yh)
+        cnt, dt = cpu_loop(run, CPU_SAMPLE_S)
+        res["cpu_baseline"] = {"value": round(b * cnt / dt / 1e9, 3), "unit": "GB/s",
+                               "us_per_call": round(dt / cnt * 1e6, 2), "cores": orc.cpu_threads(),
+                               "kind": "port",
+                               "sample": f"{cnt} GEMVs over {hc} host copies in {dt:.1f}s "
+                                         "(dequant_gemv_int4_auto, AVX-512, OpenMP)"}
+    return res
+
+
+def config1_batches(cl, torch, sdt, copies, cpu):
+    """Config 1 at M = 4 and 16: chain time, the fused gate/up kernel's
+    event-timed duration and roofline fraction, CPU chains on the host."""
+    res = {}
+    h, i, g = copies.h, copies.i, copies.g
+    for mm in (4, 16):
+        xm = cl.fill_normal(torch.empty((mm, h), dtype=torch.bfloat16, device="cuda"), 0, 22)
+        om = torch.empty((mm, h), dtype=torch.bfloat16, device="cuda")
+        im = torch.empty((mm, i), dtype=torch.float32, device="cuda")
+        fn = chain_fn(cl, copies, xm, om, sdt)
+        gu = gate_up_fn(cl, copies, xm, im, sdt)
+        for k in range(10):
+            fn(k)
+            gu(k)
+        steps = 200
+        wall, ev = graph_time(torch, fn, steps)
+        _, ev_gu = graph_time(torch, gu, steps)
+        t_gu = ev_gu / steps
+        gub = gate_up_bytes(h, i, g, mm)
+        e = {"us_per_chain": round(ev / steps * 1e6, 2),
+             "wall_us_per_chain": round(wall / steps * 1e6, 2),
+             "GB/s": round(ffn_bytes(h, i, g, mm) * steps / ev / 1e9, 1),
+             "hbm_frac": round(ffn_bytes(h, i, g, mm) * steps / ev / 1e9 / HBM_PEAK_GBS, 4),
+             "tokens_per_s": round(mm * steps / ev, 1),
+             "gate_up_kernel": {"name": "skinny_kernel (fused gate/up + SiLU*up)",
+                                "us": round(t_gu * 1e6, 2), "algorithmic_bytes": gub,
+                                "frac": round(gub / t_gu / 1e9 / HBM_PEAK_GBS, 4)}}
+        if cpu:
+            e["cpu_baseline"] = cpu_chain_baseline(torch, copies, xm, mm, CPU_SAMPLE_S)
+        res[f"config1_M{mm}"] = e
+    return res
+
+
+def prefill_setup(cl, torch, m, nn, kk, g, sdt, keep_host=False):
+    """One config 2 prefill GEMM (bf16 x, MFMA-tiled weights, bf16 out)."""
+    pk = cl.fill_bytes(torch.empty(nn * kk // 2, dtype=torch.uint8, device="cuda"), 2, 1)
+    sc = cl.fill_scales(torch.empty(nn * (kk // g) * 2, dtype=torch.uint8, device="cuda"), 2, 2,
+                        sdt)
+    pt, st = cl.tile_weights(pk, sc, nn, kk, g)
+    hostw = (pk.cpu().numpy(), sc.cpu().numpy()) if keep_host else None
+    del pk, sc
+    xb = cl.fill_normal(torch.empty(m * kk, dtype=torch.bfloat16, device="cuda"), 2, 3)
+    yb = torch.empty(m * nn, dtype=torch.bfloat16, device="cuda")
+
+    def pre(r):
+        cl.gemm_int4_bf16(pt, st, xb, nn, kk, m, yb, group_size=g, scale_dtype=sdt,
+                          tiling=cl.TILING_MFMA)
+    return pre, xb, hostw
+
+
+def config2(cl, torch, sdt, cpu):
+    """Config 2 prefill GEMMs: TFLOP/s against the 2.5 PF bf16 dense peak;
+    the CPU runs the crate's per-token GEMV loop (seq > 64) on 128 tokens."""
+    import numpy as np
+
+    import oracle as orc
+
+    res = {}
+    kk, g = 4096, 128
+    for (m, nn) in PREFILL_SHAPES:
+        pre, xb, hostw = prefill_setup(cl, torch, m, nn, kk, g, sdt, keep_host=cpu)
+        pre(0)
+        reps = 20
+        wall, ev = graph_time(torch, pre, reps)
+        t = ev / reps
+        fl = 2.0 * m * nn * kk
+        e = {"us_per_call": round(t * 1e6, 1), "TFLOP/s": round(fl / t / 1e12, 1),
+             "mfma_frac": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": fl,
+             "kernel": "pf_gemm_kernel (+ pf_xsum_kernel, split-K reduce when planned)"}
+        if cpu:
+            ns = 128
+            xs = orc.bf16_to_f32(xb[:ns * kk].view(torch.int16).cpu().numpy().view(np.uint16))
+            ys = np.empty((ns, nn), np.float32)
+
+            def run(r):
+                orc.cpu_gemm(hostw[0], hostw[1], xs, nn, kk, ns, g, sdt, ys)
+            cnt, dt = cpu_loop(run, CPU_SAMPLE_S)
+            cfl = 2.0 * nn * kk * ns * cnt
+            e["cpu_baseline"] = {"value": round(cfl / dt / 1e12, 4), "unit": "TFLOP/s",
+                                 "cores": orc.cpu_threads(), "kind": "port",
+                                 "sample": f"{cnt} x {ns} tokens (the crate's per-token GEMV loop "
+                                           f"for seq > 64) in {dt:.1f}s, AVX-512, OpenMP"}
+        res[f"config2_prefill_M{m}_N{nn}"] = e
+        del pre, xb, hostw
+        torch.cuda.empty_cache()
+    return res
+
+
+def make_experts_dev(cl, torch, E, h, i, g, sdt, seed):
+    """E synthetic experts (crate layout, seeded): (crate blob, stride, tiled)."""
+    per = cl.expert_bytes(h, i, g)
+    stride = (per + 255) // 256 * 256
+    crate = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
+    cl.fill_bytes(crate, seed, 7)
+    for e in range(E):
+        W = cl.ExpertWeights(crate[e * stride:e * stride + per], h, i, g, sdt)
+        for j, s in enumerate((W.gate_scale_bits(), W.up_scale_bits(), W.down_scale_bits())):
+            cl.fill_scales(s, seed, 100000 + 3 * e + j, sdt)
+    ex = cl.MoEExperts.from_crate(crate, E, h, i, g, sdt, stride=stride, tiled=True)
+    torch.cuda.synchronize()
+    return crate, stride, ex
+
+
+def bench_moe(cl, torch, E, h, i, g, k, T, layers, mode, scale, shared_inter, steps,
+              zipf=None, nsets=64, cpu=False, cpu_tokens=4):
+    """MoE layer(s) for T tokens; steps rotate through `nsets` routing-logit
+    sets so that consecutive steps touch different experts.  With `cpu`, the
+    runner's per-(token, slot) loop on the host over the first `cpu_tokens`
+    tokens, through every layer, with the routing the GPU used."""
+    import numpy as np
+
+    import oracle as orc
+
+    sdt = cl.SCALE_F16
+    stacks, crates, shared_host = [], [], []
+    for layer in range(layers):
+        crate, stride, ex = make_experts_dev(cl, torch, E, h, i, g, sdt, 50 + layer)
+        sh_host = None
+        if shared_inter:
+            per = cl.expert_bytes(h, shared_inter, g)
+            f = cl.fill_bytes(torch.empty(per, dtype=torch.uint8, device="cuda"), 60 + layer, 1)
+            W = cl.ExpertWeights(f, h, shared_inter, g, sdt)
+            for j, s in enumerate((W.gate_scale_bits(), W.up_scale_bits(), W.down_scale_bits())):
+                cl.fill_scales(s, 60 + layer, 10 + j, sdt)
+            sh_host = f.cpu().numpy() if cpu else None
+            ex = cl.MoEExperts(ex.blobs, E, h, i, g, sdt, cl.TILING_MFMA, ex.stride, W.tiled())
+        stacks.append(ex)
+        crates.append((crate, stride) if cpu else None)
+        shared_host.append(sh_host)
+        if not cpu:
+            del crate
+    logits = []
+    for sidx in range(nsets):
+        l = cl.fill_normal(torch.empty((T, E), dtype=torch.float32, device="cuda"), 70 + sidx, 1)
+        if zipf is not None:
+            perm = torch.randperm(E, generator=torch.Generator().manual_seed(1))
+            l += (-zipf * torch.log1p(perm.float())).cuda()[None, :]
+        logits.append(l)
+    xb = cl.fill_normal(torch.empty((T, h), dtype=torch.bfloat16, device="cuda"), 80, 1)
+    xs = [xb.float()] + [torch.empty((T, h), dtype=torch.float32, device="cuda") for _ in range(layers)]
+    ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    # unique experts per step and layer (routing only depends on the logits)
+    uniq = []
+    for sidx in range(nsets):
+        cl.moe_forward(stacks[0], xs[0], xs[1], top_k=k, logits=logits[sidx], mode=mode,
+                       scale=scale, residual=xs[0], ids_out=ids)
+        uniq.append(len(set(ids.cpu().flatten().tolist())))
+    u_avg = sum(uniq) / len(uniq)
+
+    def step(r):
+        for layer in range(layers):
+            cl.moe_forward(stacks[layer], xs[layer], xs[layer + 1], top_k=k,
+                           logits=logits[(r + 7 * layer) % nsets], mode=mode, scale=scale,
+                           residual=xs[layer])
+    for r in range(5):
+        step(r)
+    wall, ev = graph_time(torch, step, steps)
+    t = ev / steps
+    per_expert = 3 * (i * h // 2 + i * (h // g) * 2)
+    per_shared = 3 * (shared_inter * h // 2 + shared_inter * (h // g) * 2) if shared_inter else 0
+    byts = layers * (u_avg * per_expert + per_shared + T * h * 6 + T * E * 4 + T * k * 8)
+    flops = layers * 2.0 * T * (k + (1 if shared_inter else 0)) * 3 * h * i
+    res = {"T": T, "layers": layers, "us_per_step": round(t * 1e6, 2),
+           "wall_us_per_step": round(wall / steps * 1e6, 2),
+           "tokens_per_s": round(T / t, 1), "GB/s": round(byts / t / 1e9, 1),
+           "hbm_frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 4),
+           "TFLOP/s": round(flops / t / 1e12, 2),
+           "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4),
+           "unique_experts_avg": round(u_avg, 1), "algorithmic_bytes_per_step": int(byts),
+           "kernels": "cascadia_int4_moe_forward per layer: routing/grouping, grouped gate/up "
+                      "(SwiGLU hi/lo) and down, shared expert, slot-order combine"}
+    if cpu:
+        S = min(T, cpu_tokens)
+        plan = []
+        for layer in range(layers):
+            cl.moe_forward(stacks[layer], xs[0], xs[1], top_k=k, logits=logits[(7 * layer) % nsets],
+                           mode=mode, scale=scale, residual=xs[0], ids_out=ids, weights_out=wts)
+            li = ids.cpu().numpy()[:S].astype(np.int64)
+            lw = wts.cpu().numpy()[:S].copy()
+            crate, stride = crates[layer]
+            used = sorted({int(e) for e in li.ravel()})
+            blob = np.concatenate([crate[e * stride:(e + 1) * stride].cpu().numpy() for e in used])
+            remap = np.vectorize({e: j for j, e in enumerate(used)}.get)(li).astype(np.int64)
+            plan.append((blob, len(used), stride, remap, lw, shared_host[layer]))
+        x0 = xb[:S].float().cpu().numpy()
+
+        def run(r):
+            xr = x0
+            for blob, ne, stride, rid, lw, shh in plan:
+                xr = orc.cpu_moe_layer(xr, blob, ne, shh, shared_inter, h, i, g, sdt, rid, lw,
+                                       0.0, stride=stride)
+        cnt, dt = cpu_loop(run, CPU_SAMPLE_S)
+        res["cpu_baseline"] = {"value": round(S * cnt / dt, 2), "unit": "tokens/s",
+                               "us_per_token": round(dt / (S * cnt) * 1e6, 1),
+                               "cores": orc.cpu_threads(), "kind": "port",
+                               "sample": f"{cnt} x {S} tokens through {layers} layer(s) in "
+                                         f"{dt:.1f}s: the runner's per-(token, slot) "
+                                         "expert_forward loop + serial combine, AVX-512, OpenMP"}
+    del stacks, logits, crates, xs
+    torch.cuda.empty_cache()
+    return res
+
+
+def f_rows(cl, torch, sdt, copies):
+    """f1 / f3 paths at one token: the K2.6 shell projections, the
+    activation-sparse expert at tau 0.1 / 0.3, the AXPY down."""
+    import ctypes as C
+
+    res = {}
+    h, i, g = copies.h, copies.i, copies.g
     # the K2.6 shell projections at one token (q_a, q_b, kv_a, kv_b, o_proj,
     # router; shell_int4.rs:404-660) in the crate's format (G = 32, bf16
     # scales): six one-token GEMVs per step over rotating weight copies
@@ -247,8 +549,8 @@ def extra_measurements(cl, torch, args, sdt, copies):
     for r in range(5):
         shell(r)
     steps = 200
-    w, _ = graph_time(torch, shell, steps)
-    t = w / steps
+    _, ev = graph_time(torch, shell, steps)
+    t = ev / steps
     b = per + sum(kk * 4 + nn * 4 for nn, kk in shapes)
     res["shell_projections_M1"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1),
                                    "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
@@ -257,7 +559,6 @@ def extra_measurements(cl, torch, args, sdt, copies):
     # the activation-sparse expert (tau > 0, ffn_sparsity.rs:756-867) at one
     # token: gate and down in full, up for the active rows only.  Called
     # through the C entry point with no count output, so it captures.
-    import ctypes as C
     xs1 = cl.fill_normal(torch.empty(h, dtype=torch.bfloat16, device="cuda"), 0, 23)
     os1 = torch.empty(h, dtype=torch.bfloat16, device="cuda")
     nc = len(copies.w)
@@ -275,8 +576,8 @@ def extra_measurements(cl, torch, args, sdt, copies):
         for r in range(10):
             sparse(r)
         steps = 200
-        w, _ = graph_time(torch, sparse, steps)
-        t = w / steps
+        _, ev = graph_time(torch, sparse, steps)
+        t = ev / steps
         mat = i * h // 2 + i * (h // g) * 2
         b = 2 * mat + int(round(fr * i)) * (h // 2 + (h // g) * 2) + h * 2 * 2
         res[f"sparse_expert_M1_tau{tau}"] = {"us_per_call": round(t * 1e6, 2),
@@ -309,117 +610,40 @@ def extra_measurements(cl, torch, args, sdt, copies):
     for r in range(5):
         axpy(r)
     steps = 200
-    w, _ = graph_time(torch, axpy, steps)
-    t = w / steps
+    _, ev = graph_time(torch, axpy, steps)
+    t = ev / steps
     b = n_act * (H1 // 2 + (H1 // 32) * 2 + 8) + 2 * H1 * 4
     res["axpy_down_config1_13pct"] = {"us_per_call": round(t * 1e6, 2), "active_rows": n_act,
                                       "GB/s": round(b / t / 1e9, 1),
                                       "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
                                       "copies": nca}
     del AX
-    # config 2: prefill GEMM (bf16 in/out)
-    for (m, nn) in PREFILL_SHAPES:
-        pre = prefill_fn(cl, torch, m, nn, 4096, g, sdt)
-        pre(0)
-        reps = 10
-        w, _ = graph_time(torch, pre, reps)
-        t = w / reps
-        tf = 2.0 * m * nn * 4096 / t / 1e12
-        res[f"config2_prefill_M{m}_N{nn}"] = {"us_per_call": round(t * 1e6, 1),
-                                              "TFLOP/s": round(tf, 1),
-                                              "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
-        del pre
     return res
 
 
-PREFILL_SHAPES = [(512, 4096), (512, 14336), (2048, 4096), (2048, 14336)]
-
-
-def prefill_fn(cl, torch, m, nn, kk, g, sdt):
-    """One config 2 prefill GEMM (bf16 x, MFMA-tiled weights, bf16 out)."""
-    pk = cl.fill_bytes(torch.empty(nn * kk // 2, dtype=torch.uint8, device="cuda"), 2, 1)
-    sc = cl.fill_scales(torch.empty(nn * (kk // g) * 2, dtype=torch.uint8, device="cuda"), 2, 2,
-                        sdt)
-    pt, st = cl.tile_weights(pk, sc, nn, kk, g)
-    del pk, sc
-    xb = cl.fill_normal(torch.empty(m * kk, dtype=torch.bfloat16, device="cuda"), 2, 3)
-    yb = torch.empty(m * nn, dtype=torch.bfloat16, device="cuda")
-
-    def pre(r):
-        cl.gemm_int4_bf16(pt, st, xb, nn, kk, m, yb, group_size=g, scale_dtype=sdt,
-                          tiling=cl.TILING_MFMA)
-    return pre
-
-
-def make_experts_dev(cl, torch, E, h, i, g, sdt, seed):
-    """E synthetic experts (crate layout, seeded) tiled into one HBM blob."""
-    per = cl.expert_bytes(h, i, g)
-    stride = (per + 255) // 256 * 256
-    crate = torch.empty(E * stride, dtype=torch.uint8, device="cuda")
-    cl.fill_bytes(crate, seed, 7)
-    for e in range(E):
-        W = cl.ExpertWeights(crate[e * stride:e * stride + per], h, i, g, sdt)
-        for j, s in enumerate((W.gate_scale_bits(), W.up_scale_bits(), W.down_scale_bits())):
-            cl.fill_scales(s, seed, 100000 + 3 * e + j, sdt)
-    ex = cl.MoEExperts.from_crate(crate, E, h, i, g, sdt, stride=stride, tiled=True)
-    del crate
-    torch.cuda.synchronize()
+def all_configs(cl, torch, sdt, copies, cpu):
+    ex = {"hbm_ceiling": hbm_ceiling(torch)}
+    if cpu:
+        ex["cpu_host"] = host_cpu()
+    ex["config0_gemv"] = config0(cl, torch, sdt, cpu)
+    ex.update(config1_batches(cl, torch, sdt, copies, cpu))
+    ex.update(config2(cl, torch, sdt, cpu))
+    for T in (1, 32, 256):
+        ex[f"config3_moe_T{T}"] = bench_moe(
+            cl, torch, 256, 3072, 1536, 128, 8, T, 1, cl.ROUTE_SOFTMAX_TOPK, 1.0, 0,
+            200 if T < 256 else 40, cpu=cpu, cpu_tokens=8)
+    for T in (1, 8, 64, 1024):
+        ex[f"config4_moe_T{T}"] = bench_moe(
+            cl, torch, 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS, 2.827, 2048,
+            50 if T < 64 else (20 if T == 64 else 5), zipf=1.1, nsets=16 if T == 1024 else 64,
+            cpu=cpu, cpu_tokens=4)
+    ex.update(f_rows(cl, torch, sdt, copies))
     return ex
 
 
-def bench_moe(cl, torch, name, E, h, i, g, k, T, layers, mode, scale, shared_inter, steps,
-              zipf=None, nsets=64):
-    """MoE layer(s) for T tokens; steps rotate through `nsets` routing-logit
-    sets so that consecutive steps touch different experts."""
-    sdt = cl.SCALE_F16
-    stacks = []
-    for layer in range(layers):
-        ex = make_experts_dev(cl, torch, E, h, i, g, sdt, 50 + layer)
-        if shared_inter:
-            per = cl.expert_bytes(h, shared_inter, g)
-            f = cl.fill_bytes(torch.empty(per, dtype=torch.uint8, device="cuda"), 60 + layer, 1)
-            W = cl.ExpertWeights(f, h, shared_inter, g, sdt)
-            for j, s in enumerate((W.gate_scale_bits(), W.up_scale_bits(), W.down_scale_bits())):
-                cl.fill_scales(s, 60 + layer, 10 + j, sdt)
-            ex = cl.MoEExperts(ex.blobs, E, h, i, g, sdt, cl.TILING_MFMA, ex.stride, W.tiled())
-        stacks.append(ex)
-    logits = []
-    for sidx in range(nsets):
-        l = cl.fill_normal(torch.empty((T, E), dtype=torch.float32, device="cuda"), 70 + sidx, 1)
-        if zipf is not None:
-            perm = torch.randperm(E, generator=torch.Generator().manual_seed(1))
-            l += (-zipf * torch.log1p(perm.float())).cuda()[None, :]
-        logits.append(l)
-    xb = cl.fill_normal(torch.empty((T, h), dtype=torch.bfloat16, device="cuda"), 80, 1)
-    xs = [xb.float()] + [torch.empty((T, h), dtype=torch.float32, device="cuda") for _ in range(layers)]
-    ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
-    # unique experts per step and layer (routing only depends on the logits)
-    uniq = []
-    for sidx in range(nsets):
-        cl.moe_forward(stacks[0], xs[0], xs[1], top_k=k, logits=logits[sidx], mode=mode,
-                       scale=scale, residual=xs[0], ids_out=ids)
-        uniq.append(len(set(ids.cpu().flatten().tolist())))
-    u_avg = sum(uniq) / len(uniq)
-
-    def step(r):
-        for layer in range(layers):
-            cl.moe_forward(stacks[layer], xs[layer], xs[layer + 1], top_k=k,
-                           logits=logits[(r + 7 * layer) % nsets], mode=mode, scale=scale,
-                           residual=xs[layer])
-    for r in range(5):
-        step(r)
-    wall, _ = graph_time(torch, step, steps)
-    t = wall / steps
-    per_expert = 3 * (i * h // 2 + i * (h // g) * 2)
-    per_shared = 3 * (shared_inter * h // 2 + shared_inter * (h // g) * 2) if shared_inter else 0
-    byts = layers * (u_avg * per_expert + per_shared + T * h * 6 + T * E * 4 + T * k * 8)
-    res = {"T": T, "layers": layers, "us_per_step": round(t * 1e6, 2),
-           "tokens_per_s": round(T / t, 1), "GB/s": round(byts / t / 1e9, 1),
-           "hbm_frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 4), "unique_experts_avg": round(u_avg, 1)}
-    del stacks, logits
-    torch.cuda.empty_cache()
-    return res
-
+# ---------------------------------------------------------------------------
+# main
+# ---------------------------------------------------------------------------
 
 def main():
     args = parse()
@@ -432,9 +656,28 @@ def main():
     import cascadia_amd as cl
 
     sdt = cl.SCALE_F16
+    if args.profile_gemv:
+        n = k = 4096
+        g = 128
+        nb, nsb = n * k // 2, n * (k // g) * 2
+        ncp = math.ceil(2 * MALL_BYTES / (nb + nsb)) + 1
+        PS = []
+        for c in range(ncp):
+            p = cl.fill_bytes(torch.empty(nb, dtype=torch.uint8, device="cuda"), 0, 200 + c)
+            s = cl.fill_scales(torch.empty(nsb, dtype=torch.uint8, device="cuda"), 0, 300 + c, sdt)
+            PS.append(cl.tile_weights(p, s, n, k, g))
+        x = cl.fill_normal(torch.empty(k, dtype=torch.float32, device="cuda"), 0, 13)
+        y = torch.empty(n, dtype=torch.float32, device="cuda")
+        for r in range(200):
+            pt, st = PS[r % ncp]
+            cl.dequant_gemv_int4(pt, st, x, n, k, y, group_size=g, scale_dtype=sdt,
+                                 tiling=cl.TILING_MFMA)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": "gemv", "launches": 200, "copies": ncp}), flush=True)
+        return
     if args.profile_prefill:
         for (pm, pn) in PREFILL_SHAPES:
-            pre = prefill_fn(cl, torch, pm, pn, 4096, 128, sdt)
+            pre, _, _ = prefill_setup(cl, torch, pm, pn, 4096, 128, sdt)
             for r in range(5):
                 pre(r)
             torch.cuda.synchronize()
@@ -456,10 +699,10 @@ def main():
         return
     if args.profile_moe:
         T = args.moe_tokens
-        r3 = bench_moe(cl, torch, "config3", 256, 3072, 1536, 128, 8, T, 1,
-                       cl.ROUTE_SOFTMAX_TOPK, 1.0, 0, 50, nsets=16)
-        r4 = bench_moe(cl, torch, "config4", 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS,
-                       2.827, 2048, 20, zipf=1.1, nsets=16)
+        r3 = bench_moe(cl, torch, 256, 3072, 1536, 128, 8, T, 1, cl.ROUTE_SOFTMAX_TOPK, 1.0, 0,
+                       50 if T < 256 else 10, nsets=16)
+        r4 = bench_moe(cl, torch, 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS, 2.827,
+                       2048, 20 if T < 256 else 3, zipf=1.1, nsets=16)
         print(json.dumps({"profile": "moe", f"config3_T{T}": r3, f"config4_T{T}": r4}),
               flush=True)
         return
@@ -526,17 +769,9 @@ def main():
                      "avg_launch_us": round(t_gu * 1e6, 3)},
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(torch, copies, x, m, args.cpu_seconds)
-    if args.extra:
-        line["extra"] = extra_measurements(cl, torch, args, sdt, copies)
-        for T in (1, 32, 256):
-            line["extra"][f"config3_moe_T{T}"] = bench_moe(
-                cl, torch, "config3", 256, 3072, 1536, 128, 8, T, 1, cl.ROUTE_SOFTMAX_TOPK, 1.0, 0,
-                200 if T < 256 else 40)
-        for T in (1, 8, 64):
-            line["extra"][f"config4_moe_T{T}"] = bench_moe(
-                cl, torch, "config4", 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS, 2.827,
-                2048, 50 if T < 64 else 20, zipf=1.1)
+        line["cpu_baseline"] = cpu_chain_baseline(torch, copies, x, m, args.cpu_seconds)
+    if not args.headline_only:
+        line["extra"] = all_configs(cl, torch, sdt, copies, not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 
