@@ -3,6 +3,8 @@
 // Argument validation mirrors the crate's assert_eq! length checks
 // (kernel.rs:39-43, kernel_avx512_multi.rs:75-80) but returns
 // CASCADIA_INT4_ERR_ARG instead of panicking; nothing throws across the ABI.
+#include <stdlib.h>
+
 #include <mutex>
 #include <new>
 
@@ -12,6 +14,7 @@
 #include "layout.hpp"
 #include "moe.hpp"
 #include "gemv.hpp"
+#include "grouped.hpp"
 #include "prefill.hpp"
 #include "quant.hpp"
 #include "skinny.hpp"
@@ -213,22 +216,100 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   return hip_status(cai4::skinny_launch(a, p, amode, epi, st));
 }
 
+// Tokens from which an expert FFN runs on the MFMA-tile GEMMs (grouped.hip)
+// rather than the skinny kernel's 64-row passes (measured: the tiles win from
+// 512 rows at the K2.6 and Llama-3-8B FFN shapes; below, too few workgroups).
+// CASCADIA_INT4_FFN_TILE_TOKENS overrides.
+uint32_t ffn_tile_tokens() {
+  const char *e = getenv("CASCADIA_INT4_FFN_TILE_TOKENS");
+  const int n = e ? atoi(e) : 0;
+  return n > 0 ? (uint32_t)n : 512u;
+}
+
+bool ffn_tile_shape(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t n_tokens) {
+  return n_tokens >= ffn_tile_tokens() && cai4::gg_supported((int)hidden, (int)group, 1) &&
+         cai4::gg_supported((int)inter, (int)group, 1);
+}
+
 // Workspace of an expert FFN: the SwiGLU intermediate as two bf16 planes,
-// then the split-K partials of whichever of its two GEMMs needs more.
+// then the split-K partials of whichever of its two GEMMs needs more; or, for
+// many tokens, the planes and the MFMA-tile GEMMs' seeds / split activations.
 struct FfnWorkspace {
-  size_t planes, partials;
+  size_t planes, partials, tile;
+  size_t total() const { return planes + partials > tile ? planes + partials : tile; }
 };
+size_t ffn_tile_workspace(int num_cus, uint32_t hidden, uint32_t inter, uint32_t group,
+                          uint32_t n_tokens, bool x_f32, bool out_bf16) {
+  const size_t planes = 2 * (((size_t)n_tokens * inter * 2 + 255) & ~(size_t)255);
+  const size_t a = cai4::gg_dense_workspace((int)n_tokens, (int)inter, (int)hidden, (int)group,
+                                            x_f32 ? cai4::GG_A_F32 : cai4::GG_A_BF16,
+                                            cai4::GG_SWIGLU_HILO, num_cus);
+  const size_t b = cai4::gg_dense_workspace((int)n_tokens, (int)hidden, (int)inter, (int)group,
+                                            cai4::GG_A_PLANES,
+                                            out_bf16 ? cai4::GG_BF16 : cai4::GG_F32, num_cus);
+  return planes + (a > b ? a : b);
+}
 FfnWorkspace ffn_workspace(int dev, uint32_t hidden, uint32_t inter, uint32_t group,
                            uint32_t n_tokens, bool x_f32) {
   const cai4::SkinnyDevice d = device_props(dev);
+  size_t tile = 0;
+  if (ffn_tile_shape(hidden, inter, group, n_tokens)) {
+    const size_t t0 = ffn_tile_workspace(d.num_cus, hidden, inter, group, n_tokens, x_f32, false);
+    const size_t t1 = ffn_tile_workspace(d.num_cus, hidden, inter, group, n_tokens, x_f32, true);
+    tile = t0 > t1 ? t0 : t1;
+  }
   const cai4::SkinnyPlan gu =
       cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens,
                         x_f32 ? cai4::A_XF32 : cai4::A_BF16, cai4::EPI_SWIGLU_HILO, d);
   const cai4::SkinnyPlan dn = cai4::skinny_plan((int)hidden, (int)inter, (int)group,
                                                 (int)n_tokens, cai4::A_HILO, cai4::EPI_F32, d);
   const size_t planes = ((size_t)n_tokens * inter * 2 * sizeof(uint16_t) + 255) & ~(size_t)255;
-  return FfnWorkspace{planes, gu.partial_bytes > dn.partial_bytes ? gu.partial_bytes
-                                                                  : dn.partial_bytes};
+  return FfnWorkspace{planes,
+                      gu.partial_bytes > dn.partial_bytes ? gu.partial_bytes : dn.partial_bytes,
+                      tile};
+}
+
+// The expert FFN on the MFMA-tile GEMMs: gate/up with the SwiGLU epilogue
+// into hi / lo planes, then down over the planes (grouped.hip, dense mode).
+int ffn_tiles(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
+              const cascadia_int4_expert *e, const void *x, bool x_f32, uint32_t n_tokens,
+              void *out, bool out_bf16, void *ws, int num_cus, hipStream_t st) {
+  const size_t plane = ((size_t)n_tokens * inter * 2 + 255) & ~(size_t)255;
+  uint16_t *hi = static_cast<uint16_t *>(ws);
+  uint16_t *lo = reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(ws) + plane);
+  void *rest = static_cast<uint8_t *>(ws) + 2 * plane;
+  cai4::GgArgs g{};
+  g.w0 = e->gate_packed;
+  g.s0 = e->gate_scale;
+  g.w1 = e->up_packed;
+  g.s1 = e->up_scale;
+  g.x = static_cast<const uint16_t *>(x);
+  g.y = hi;
+  g.y2 = lo;
+  g.M = (int)n_tokens;
+  g.N = (int)inter;
+  g.K = (int)hidden;
+  g.G = (int)group;
+  g.sdt = (int)sdt;
+  g.ldy = (int)inter;
+  g.epi = cai4::GG_SWIGLU_HILO;
+  if (hipError_t err =
+          cai4::gg_dense(g, x_f32 ? cai4::GG_A_F32 : cai4::GG_A_BF16, rest, num_cus, st))
+    return hip_status(err);
+  cai4::GgArgs dn{};
+  dn.w0 = e->down_packed;
+  dn.s0 = e->down_scale;
+  dn.x = hi;
+  dn.x2 = lo;
+  dn.y = out;
+  dn.M = (int)n_tokens;
+  dn.N = (int)hidden;
+  dn.K = (int)inter;
+  dn.G = (int)group;
+  dn.sdt = (int)sdt;
+  dn.ldy = (int)hidden;
+  dn.epi = out_bf16 ? cai4::GG_BF16 : cai4::GG_F32;
+  return hip_status(cai4::gg_dense(dn, cai4::GG_A_PLANES, rest, num_cus, st));
 }
 
 void expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[6]) {
@@ -274,9 +355,13 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   const FfnWorkspace need = ffn_workspace(dev, hidden, inter, group, n_tokens, x_f32);
   void *ws = workspace;
   if (!ws) {
-    if (int rc = lib_workspace(dev, need.planes + need.partials, &ws)) return rc;
+    if (int rc = lib_workspace(dev, need.total(), &ws)) return rc;
   } else if (!aligned(ws, 16)) {
     return CASCADIA_INT4_ERR_ARG;
+  }
+  if (need.tile && e->tiling == CASCADIA_INT4_TILING_MFMA) {
+    return ffn_tiles(hidden, inter, group, sdt, e, x, x_f32, n_tokens, out, out_bf16, ws,
+                     device_props(dev).num_cus, st);
   }
   // the SwiGLU intermediate as two bf16 planes (hi, lo): [n_tokens, inter] each
   uint16_t *hi = reinterpret_cast<uint16_t *>(ws);
@@ -323,7 +408,7 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
   w.total = 3 * w.lanes + w.counts + part;
   const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group, n_tokens, true);
   const FfnWorkspace b = ffn_workspace(dev, hidden, inter, group, n_tokens, false);
-  const size_t dense = f.planes + (f.partials > b.partials ? f.partials : b.partials);
+  const size_t dense = f.total() > b.total() ? f.total() : b.total();
   if (dense > w.total) w.total = dense;
   return w;
 }
@@ -409,12 +494,43 @@ void expert_blob_sections(uint32_t hidden, uint32_t inter, uint32_t group, uint3
   }
 }
 
-// Prefill GEMM (M >= 64 tokens, MFMA-tiled weights, K and G multiples of 128).
+// Which prefill kernel: prefill.hip's (K and G multiples of 128), or the
+// MFMA-tile GEMM of grouped.hip (any G of 32, 64, 128k; CASCADIA_INT4_PREFILL_TILES=1
+// takes it for every shape).
+bool prefill_tiles(const cascadia_int4_layout *L) {
+  const char *e = getenv("CASCADIA_INT4_PREFILL_TILES");
+  return (e && atoi(e) > 0) || L->group_size % 128 != 0;
+}
+
+// Prefill GEMM (M >= 64 tokens, MFMA-tiled weights).
 int run_prefill(const cascadia_int4_layout *L, const uint8_t *packed, const uint8_t *scales,
                 const uint16_t *x, uint32_t M, void *y, bool out_f32, hipStream_t st) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
   if ((size_t)M * L->k_cols * 2 >= 0x7FFFFFFFu) return CASCADIA_INT4_ERR_ARG;
+  if (prefill_tiles(L)) {
+    const int cus = device_props(dev).num_cus;
+    void *ws = nullptr;
+    if (int rc = lib_workspace(
+            dev,
+            cai4::gg_dense_workspace((int)M, (int)L->n_rows, (int)L->k_cols, (int)L->group_size,
+                                     cai4::GG_A_BF16, out_f32 ? cai4::GG_F32 : cai4::GG_BF16, cus),
+            &ws))
+      return rc;
+    cai4::GgArgs a{};
+    a.w0 = packed;
+    a.s0 = scales;
+    a.x = x;
+    a.y = y;
+    a.M = (int)M;
+    a.N = (int)L->n_rows;
+    a.K = (int)L->k_cols;
+    a.G = (int)L->group_size;
+    a.sdt = (int)L->scale_dtype;
+    a.ldy = (int)L->n_rows;
+    a.epi = out_f32 ? cai4::GG_F32 : cai4::GG_BF16;
+    return hip_status(cai4::gg_dense(a, cai4::GG_A_BF16, ws, cus, st));
+  }
   void *ws = nullptr;
   if (int rc = lib_workspace(dev,
                              cai4::prefill_workspace_bytes((int)M, (int)L->n_rows, (int)L->k_cols,
@@ -424,6 +540,15 @@ int run_prefill(const cascadia_int4_layout *L, const uint8_t *packed, const uint
   return hip_status(cai4::prefill_gemm(packed, scales, x, y, (int)M, (int)L->n_rows,
                                        (int)L->k_cols, (int)L->group_size, (int)L->scale_dtype,
                                        out_f32 ? 1 : 0, ws, device_props(dev).num_cus, st));
+}
+
+// Many tokens over MFMA-tiled weights: one of the prefill GEMMs.
+bool prefill_shape(const cascadia_int4_layout *L, uint32_t seq) {
+  if (!L->tiling || seq < 64 || L->n_rows < 16) return false;
+  if (L->group_size % 128 == 0 && !prefill_tiles(L))
+    return cai4::prefill_supported((int)seq, (int)L->n_rows, (int)L->k_cols, (int)L->group_size,
+                                   (int)L->tiling);
+  return cai4::gg_supported((int)L->k_cols, (int)L->group_size, 1);
 }
 
 // ---- sparse-MoE layer ----
@@ -460,26 +585,55 @@ int moe_check(const cascadia_int4_moe_layer *L, uint32_t top_k, uint32_t T) {
 struct MoePlan {
   cai4::SkinnyPlan gu, dn;
   cai4::MoeWorkspace ws;
+  bool tiles;  // the MFMA-tile GEMMs (grouped.hip) over 128-row chunks
+  int rows_pad;
 };
+
+// Many tokens per layer: experts receive enough rows that 16-row chunks would
+// stream each hot expert's weights many times over; 128-row MFMA tiles read
+// them about once per 128 rows.
+bool moe_tiles(const cascadia_int4_moe_layer *L, uint32_t T) {
+  return L->tiling == CASCADIA_INT4_TILING_MFMA && T >= (uint32_t)cai4::moe_tile_tokens() &&
+         cai4::gg_supported((int)L->hidden, (int)L->group_size, 1) &&
+         cai4::gg_supported((int)L->inter, (int)L->group_size, 1);
+}
 
 MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint32_t T,
                  bool given_ids) {
   const cai4::SkinnyDevice d = device_props(dev);
   const int H = (int)L->hidden, I = (int)L->inter, G = (int)L->group_size;
-  // routing picks distinct experts per token; given ids may repeat one
-  const int C = cai4::moe_chunk_rows((int)T, given_ids ? (int)(T * top_k) : (int)T);
-  const int maxc = cai4::moe_max_chunks((int)T, (int)L->n_experts, (int)top_k, C);
   MoePlan m{};
-  m.gu = cai4::skinny_plan_grouped(I, H, G, C, maxc, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d);
-  m.dn = cai4::skinny_plan_grouped(H, I, G, C, maxc, cai4::A_HILO, cai4::EPI_BF16, d);
-  const size_t part = m.gu.partial_bytes > m.dn.partial_bytes ? m.gu.partial_bytes
-                                                              : m.dn.partial_bytes;
+  m.tiles = moe_tiles(L, T);
   size_t sh = 0, sh_ws = 0;
   if (has_shared(L)) {
     const FfnWorkspace f = ffn_workspace(dev, L->hidden, L->shared_inter, L->group_size, T, true);
     sh = (size_t)T * H * sizeof(float);
-    sh_ws = f.planes + f.partials;
+    sh_ws = f.total();
   }
+  if (m.tiles) {
+    // hot experts in 128-row MFMA tiles; the others in 16-row skinny chunks
+    const int C = cai4::kGgChunkRows, C2 = 16;
+    const int n = (int)(T * top_k);
+    m.rows_pad = cai4::gg_rows_pad(n);
+    const int gw = cai4::gg_group_width(G);
+    const int maxc2 = cai4::moe_max_chunks((int)T, (int)L->n_experts, (int)top_k, C2);
+    m.gu = cai4::skinny_plan_grouped(I, H, G, C2, maxc2, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO,
+                                     d);
+    m.dn = cai4::skinny_plan_grouped(H, I, G, C2, maxc2, cai4::A_HILO, cai4::EPI_BF16, d);
+    const size_t part =
+        m.gu.partial_bytes > m.dn.partial_bytes ? m.gu.partial_bytes : m.dn.partial_bytes;
+    m.ws = cai4::moe_workspace((int)T, H, I, (int)L->n_experts, (int)top_k, C, part, sh, sh_ws,
+                               (size_t)n * H * 2, (size_t)(H / gw) * m.rows_pad * 4,
+                               (size_t)(I / gw) * m.rows_pad * 4, C2);
+    return m;
+  }
+  // routing picks distinct experts per token; given ids may repeat one
+  const int C = cai4::moe_chunk_rows((int)T, given_ids ? (int)(T * top_k) : (int)T);
+  const int maxc = cai4::moe_max_chunks((int)T, (int)L->n_experts, (int)top_k, C);
+  m.gu = cai4::skinny_plan_grouped(I, H, G, C, maxc, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d);
+  m.dn = cai4::skinny_plan_grouped(H, I, G, C, maxc, cai4::A_HILO, cai4::EPI_BF16, d);
+  const size_t part = m.gu.partial_bytes > m.dn.partial_bytes ? m.gu.partial_bytes
+                                                              : m.dn.partial_bytes;
   m.ws = cai4::moe_workspace((int)T, H, I, (int)L->n_experts, (int)top_k, C, part, sh, sh_ws);
   return m;
 }
@@ -644,6 +798,112 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     return hip_status(cai4::moe_combine(residual, sh, y, pos, wts, 1, H, k, out, st));
   }
   hipError_t e = hipSuccess;
+  if (m.tiles) {
+    // many tokens: route, group into 128-row chunks, gather the rows as bf16
+    // with their seeds, then the grouped MFMA-tile gate/up (SwiGLU -> hi / lo
+    // planes) and down (-> bf16 per (token, slot)) over all experts at once
+    if (R->mode == CASCADIA_INT4_ROUTE_IDS) {
+      e = hipMemcpyAsync(ids, R->ids, n * 4, hipMemcpyDeviceToDevice, st);
+      if (e == hipSuccess) e = hipMemcpyAsync(wts, R->weights, n * 4, hipMemcpyDeviceToDevice, st);
+    } else {
+      e = cai4::moe_route(r, (int)T, E, ids, wts, st);
+    }
+    cai4::SkinnyChunk *chunks2 = reinterpret_cast<cai4::SkinnyChunk *>(W + m.ws.chunks2);
+    if (e == hipSuccess)
+      e = cai4::moe_group(ids, wts, R->threshold, (int)T, E, k, m.ws.chunk_rows,
+                          m.ws.max_chunks, pos, row_map, chunks, counts, st, m.ws.chunk_rows2,
+                          cai4::moe_tile_rows(), chunks2, m.ws.max_chunks2);
+    // the skinny kernels' share: experts with few rows, 16-row chunks
+    cai4::SkinnyArgs sk{};
+    sk.partials = part;
+    sk.chunks = chunks2;
+    sk.expert_stride = L->expert_stride;
+    sk.M = (int)n;
+    sk.G = G;
+    sk.sdt = (int)L->scale_dtype;
+    sk.glog2 = glog2_of(G);
+    sk.tiled = (int)L->tiling;
+    uint16_t *xg = reinterpret_cast<uint16_t *>(W + m.ws.xg);
+    float *sx = reinterpret_cast<float *>(W + m.ws.seeds_x);
+    float *si = reinterpret_cast<float *>(W + m.ws.seeds_i);
+    if (e == hipSuccess)  // grouped row r <- bf16(x[row_map[r]]), the row count from the grouping
+      e = cai4::gg_prep(2, x, nullptr, row_map, xg, nullptr, sx, (int)n, m.rows_pad, H, G, counts,
+                        st);
+    cai4::GgArgs a{};
+    a.estride = L->expert_stride;
+    a.tiles = chunks;
+    a.M = (int)n;
+    a.G = G;
+    a.sdt = (int)L->scale_dtype;
+    a.rows_pad = m.rows_pad;
+    if (e == hipSuccess) {
+      cai4::GgArgs g = a;
+      g.w0 = L->experts + off[0];
+      g.s0 = L->experts + off[1];
+      g.w1 = L->experts + off[2];
+      g.s1 = L->experts + off[3];
+      g.x = xg;
+      g.seeds = sx;
+      g.y = hi;
+      g.y2 = lo;
+      g.N = I;
+      g.K = H;
+      g.ldy = I;
+      g.epi = cai4::GG_SWIGLU_HILO;
+      e = cai4::gg_grouped(g, m.ws.max_chunks, st);
+    }
+    if (e == hipSuccess) {
+      cai4::SkinnyArgs a2 = sk;
+      a2.w0 = L->experts + off[0];
+      a2.s0 = L->experts + off[1];
+      a2.w1 = L->experts + off[2];
+      a2.s1 = L->experts + off[3];
+      a2.x = x;
+      a2.row_map = row_map;
+      a2.x_rows = (int)T;
+      a2.out = hi;
+      a2.out2 = lo;
+      a2.N = I;
+      a2.K = H;
+      a2.ldx = H;
+      a2.ldo = I;
+      e = cai4::skinny_launch(a2, m.gu, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, st);
+    }
+    if (e == hipSuccess)
+      e = cai4::gg_prep(1, hi, lo, nullptr, nullptr, nullptr, si, (int)n, m.rows_pad, I, G, counts,
+                        st);
+    if (e == hipSuccess) {
+      cai4::GgArgs dn = a;
+      dn.w0 = L->experts + off[4];
+      dn.s0 = L->experts + off[5];
+      dn.x = hi;
+      dn.x2 = lo;
+      dn.hilo = 1;
+      dn.seeds = si;
+      dn.y = y;
+      dn.N = H;
+      dn.K = I;
+      dn.ldy = H;
+      dn.epi = cai4::GG_BF16;
+      e = cai4::gg_grouped(dn, m.ws.max_chunks, st);
+    }
+    if (e == hipSuccess) {
+      cai4::SkinnyArgs a2 = sk;
+      a2.w0 = L->experts + off[4];
+      a2.s0 = L->experts + off[5];
+      a2.x = hi;
+      a2.x2 = lo;
+      a2.out = y;
+      a2.N = H;
+      a2.K = I;
+      a2.ldx = I;
+      a2.ldo = H;
+      e = cai4::skinny_launch(a2, m.dn, cai4::A_HILO, cai4::EPI_BF16, st);
+    }
+    if (e != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+    if (join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+    return hip_status(cai4::moe_combine(residual, sh, y, pos, wts, (int)T, H, k, out, st));
+  }
   if (T <= (uint32_t)cai4::kMoePrepMaxTokens) {
     // small decode batches: routing and grouping in one launch
     e = cai4::moe_prep(r, (int)T, E, k, m.ws.chunk_rows, m.ws.max_chunks, ids, wts, pos, row_map,
@@ -757,8 +1017,7 @@ int cascadia_int4_dequant_gemm_bf16in(const cascadia_int4_layout *L, const uint8
   if (!xs_bf16 || !ys) return CASCADIA_INT4_ERR_NULL;
   if (seq == 0) return CASCADIA_INT4_ERR_ARG;
   if (!aligned(xs_bf16, 16) || !aligned(ys, 4)) return CASCADIA_INT4_ERR_ARG;
-  if (cai4::prefill_supported((int)seq, (int)L->n_rows, (int)L->k_cols, (int)L->group_size,
-                              (int)L->tiling))
+  if (prefill_shape(L, seq))
     return run_prefill(L, packed, scale_bits, xs_bf16, seq, ys, true, (hipStream_t)stream);
   return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
                   (int)L->group_size, (int)L->scale_dtype, (int)L->tiling, xs_bf16, nullptr,
@@ -774,8 +1033,7 @@ int cascadia_int4_gemm_bf16(const cascadia_int4_layout *L, const uint8_t *packed
   if (!xs_bf16 || !ys_bf16) return CASCADIA_INT4_ERR_NULL;
   if (seq == 0) return CASCADIA_INT4_ERR_ARG;
   if (!aligned(xs_bf16, 16) || !aligned(ys_bf16, 2)) return CASCADIA_INT4_ERR_ARG;
-  if (cai4::prefill_supported((int)seq, (int)L->n_rows, (int)L->k_cols, (int)L->group_size,
-                              (int)L->tiling))
+  if (prefill_shape(L, seq))
     return run_prefill(L, packed, scale_bits, xs_bf16, seq, ys_bf16, false, (hipStream_t)stream);
   return run_gemm(packed, scale_bits, nullptr, nullptr, (int)L->n_rows, (int)L->k_cols,
                   (int)L->group_size, (int)L->scale_dtype, (int)L->tiling, xs_bf16, nullptr,
@@ -872,7 +1130,7 @@ size_t cascadia_int4_ffn_workspace_bytes(uint32_t hidden, uint32_t inter, uint32
   if (group_size == 0 || group_size % 32) return 0;
   const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group_size, n_tokens, true);
   const FfnWorkspace b = ffn_workspace(dev, hidden, inter, group_size, n_tokens, false);
-  return f.planes + (f.partials > b.partials ? f.partials : b.partials);
+  return f.total() > b.total() ? f.total() : b.total();
 }
 
 int cascadia_int4_expert_forward_device(uint32_t hidden, uint32_t inter, uint32_t group_size,
@@ -894,7 +1152,7 @@ int cascadia_int4_expert_forward_noalloc(uint32_t hidden, uint32_t inter, uint32
   int dev;
   if (int rc = current_device(&dev)) return rc;
   const FfnWorkspace need = ffn_workspace(dev, hidden, inter, group_size, n_tokens, false);
-  if (need.planes + need.partials > kNoAllocScratchBytes) return CASCADIA_INT4_ERR_ARG;
+  if (need.total() > kNoAllocScratchBytes) return CASCADIA_INT4_ERR_ARG;
   void *ws = nullptr;
   if (int rc = noalloc_scratch(dev, &ws)) return rc;
   return ffn_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false, n_tokens,

@@ -17,6 +17,7 @@
 // deterministic, because each token row of a grouped GEMM is computed
 // independently of its position and the combine reads slots in order.
 #include <math.h>
+#include <stdlib.h>
 
 #include "int4_common.hpp"
 #include "moe.hpp"
@@ -39,6 +40,18 @@ int moe_chunk_rows(int T, int per_expert_max) {
   return per_expert_max < c ? per_expert_max : c;
 }
 
+int moe_tile_tokens() {
+  const char *e = getenv("CASCADIA_INT4_MOE_TILE_TOKENS");
+  const int n = e ? atoi(e) : 0;
+  return n > 0 ? n : 512;
+}
+
+int moe_tile_rows() {
+  const char *e = getenv("CASCADIA_INT4_MOE_TILE_ROWS");
+  const int n = e ? atoi(e) : 0;
+  return n > 0 ? n : 48;
+}
+
 int moe_max_chunks(int T, int E, int top_k, int chunk_rows) {
   // sum_e ceil(c_e / C) <= A + (n - A) / C for A active experts, largest at
   // A = min(n, E)
@@ -47,11 +60,15 @@ int moe_max_chunks(int T, int E, int top_k, int chunk_rows) {
 }
 
 MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows,
-                           size_t part_bytes, size_t shared_bytes, size_t shared_ws_bytes) {
+                           size_t part_bytes, size_t shared_bytes, size_t shared_ws_bytes,
+                           size_t xg_bytes, size_t seeds_x_bytes, size_t seeds_i_bytes,
+                           int chunk_rows2) {
   MoeWorkspace w{};
   const size_t n = (size_t)T * top_k;
   w.chunk_rows = chunk_rows;
   w.max_chunks = moe_max_chunks(T, E, top_k, w.chunk_rows);
+  w.chunk_rows2 = chunk_rows2;
+  w.max_chunks2 = chunk_rows2 ? moe_max_chunks(T, E, top_k, chunk_rows2) : 0;
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -70,6 +87,10 @@ MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows
   w.shared = take(shared_bytes);
   w.part = take(part_bytes);
   w.shared_ws = take(shared_ws_bytes);
+  w.xg = take(xg_bytes);
+  w.seeds_x = take(seeds_x_bytes);
+  w.seeds_i = take(seeds_i_bytes);
+  w.chunks2 = take((size_t)w.max_chunks2 * sizeof(SkinnyChunk));
   w.total = o;
   return w;
 }
@@ -147,8 +168,8 @@ CAI4_DEV int wave_exclusive_scan(int x, int *total) {
 // not be waited for (__syncthreads would wait for every store to complete).
 CAI4_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// ceil(a / C) for 0 <= a < 2^20 and 1 <= C <= 64: a float estimate, then one
-// correction step each way (exact; no integer division).
+// ceil(a / C) for 0 <= a < 2^20 and 1 <= C <= 256: a float estimate (off by
+// at most one), then one correction step each way (exact; no integer division).
 CAI4_DEV int ceil_div_small(int a, int C, float invC) {
   const int n = a + C - 1;
   int q = (int)((float)n * invC);
@@ -162,11 +183,15 @@ struct GroupLds {
   int total, nchunks;
 };
 
+// Two tables (chunks2 not null): experts with at least hot_min rows are cut
+// into chunks of C rows in `chunks`, the others into chunks of C2 rows in
+// `chunks2`; counts[1] / counts[2] get the two chunk counts.
 template <int PMAX>  // PMAX >= ceil(E / 64)
 CAI4_DEV void group_assignments(const int32_t *ids, const float *w, float thr, int T, int E,
                                 int k, int C, int max_chunks, int *rank, GroupLds &g,
                                 int32_t *pos, int *rowmap, SkinnyChunk *chunks,
-                                int32_t *counts) {
+                                int32_t *counts, int C2 = 0, int hot_min = 0,
+                                SkinnyChunk *chunks2 = nullptr, int max_chunks2 = 0) {
   const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63;
   const int n = T * k;
   for (int e = tid; e < E; e += nth) g.cnt[e] = 0;
@@ -181,18 +206,22 @@ CAI4_DEV void group_assignments(const int32_t *ids, const float *w, float thr, i
     // lane l scans experts l * per .. l * per + per - 1 (all its counts read
     // at once: the loop carries no LDS latency)
     const int per = (E + 63) >> 6, e0 = lane * per;
-    const float invC = 1.0f / (float)C;
-    int c[PMAX], nc[PMAX];
-    int rows = 0, chs = 0;
+    const float invC = 1.0f / (float)C, invC2 = chunks2 ? 1.0f / (float)C2 : 0.f;
+    int c[PMAX], nc[PMAX], nc2[PMAX];
+    int rows = 0, chs = 0, chs2 = 0;
 #pragma unroll
     for (int q = 0; q < PMAX; ++q) {
       c[q] = q < per && e0 + q < E ? g.cnt[e0 + q] : 0;
-      nc[q] = ceil_div_small(c[q], C, invC);
+      const bool hot = !chunks2 || c[q] >= hot_min;
+      nc[q] = hot ? ceil_div_small(c[q], C, invC) : 0;
+      nc2[q] = hot ? 0 : ceil_div_small(c[q], C2, invC2);
       rows += c[q];
       chs += nc[q];
+      chs2 += nc2[q];
     }
-    int total, total_chunks;
+    int total, total_chunks, total_chunks2;
     int ro = wave_exclusive_scan(rows, &total), co = wave_exclusive_scan(chs, &total_chunks);
+    int co2 = wave_exclusive_scan(chs2, &total_chunks2);
 #pragma unroll
     for (int q = 0; q < PMAX; ++q) {
       if (q < per && e0 + q < E) {
@@ -202,16 +231,25 @@ CAI4_DEV void group_assignments(const int32_t *ids, const float *w, float thr, i
           const int left = c[q] - h * C;
           chunks[co + h] = SkinnyChunk{e, ro + h * C, left < C ? left : C, 0};
         }
+        for (int h = 0; h < nc2[q]; ++h) {
+          const int left = c[q] - h * C2;
+          chunks2[co2 + h] = SkinnyChunk{e, ro + h * C2, left < C2 ? left : C2, 0};
+        }
       }
       ro += c[q];
       co += nc[q];
+      co2 += nc2[q];
     }
     for (int j = total_chunks + lane; j < max_chunks; j += 64) chunks[j] = SkinnyChunk{0, 0, 0, 0};
+    if (chunks2)
+      for (int j = total_chunks2 + lane; j < max_chunks2; j += 64)
+        chunks2[j] = SkinnyChunk{0, 0, 0, 0};
     if (lane == 0) {
       g.total = total;
       g.nchunks = total_chunks;
       counts[0] = total;
       counts[1] = total_chunks;
+      counts[2] = total_chunks2;
     }
   }
   lds_barrier();
@@ -235,19 +273,22 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *ids, con
                                                        float thr, int T, int E, int k, int C,
                                                        int max_chunks, int32_t *pos,
                                                        int32_t *row_map, SkinnyChunk *chunks,
-                                                       int32_t *counts) {
+                                                       int32_t *counts, int C2, int hot_min,
+                                                       SkinnyChunk *chunks2, int max_chunks2) {
   __shared__ GroupLds g;
   // pos doubles as the rank array: each slot is read before it is written
   group_assignments<R>(ids, w, thr, T, E, k, C, max_chunks, pos, g, pos, row_map, chunks,
-                      counts);
+                       counts, C2, hot_min, chunks2, max_chunks2);
 }
 
 hipError_t moe_group(const int32_t *ids, const float *w, float threshold, int T, int E,
                      int top_k, int chunk_rows, int max_chunks, int32_t *pos, int32_t *row_map,
-                     SkinnyChunk *chunks, int32_t *counts, hipStream_t st) {
+                     SkinnyChunk *chunks, int32_t *counts, hipStream_t st, int chunk_rows2,
+                     int hot_min, SkinnyChunk *chunks2, int max_chunks2) {
   CAI4_MOE_DISPATCH(E, hipLaunchKernelGGL(moe_group_kernel<R>, dim3(1), dim3(1024), 0, st, ids, w,
                                           threshold, T, E, top_k, chunk_rows, max_chunks, pos,
-                                          row_map, chunks, counts));
+                                          row_map, chunks, counts, chunk_rows2, hot_min, chunks2,
+                                          max_chunks2));
   return hipGetLastError();
 }
 
