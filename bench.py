@@ -584,6 +584,46 @@ def f_rows(cl, torch, sdt, copies):
                                              "active_frac": round(fr, 4),
                                              "GB/s": round(b / t / 1e9, 1),
                                              "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+    # the composed AXPY-form sparse FFN (ffn_sparsity.rs:638-740): f32 in /
+    # out, gate + mask + rows-subset up + AXPY down over config 1's
+    # transposed down, one token, tau 0.1 / 0.3
+    src = cl.ExpertWeights(copies.crate[0], h, i, g, sdt)
+    ptc, stc = cl.transpose_requantize_down(src.down_packed_bytes(), src.down_scale_bits(), h, i,
+                                            group_size=g, scale_dtype=sdt)
+    xf1 = xs1.float()
+    of1 = torch.empty(h, dtype=torch.float32, device="cuda")
+    wsx = torch.empty(cl.ffn_sparse_axpy_workspace_bytes(h, i, 1, g), dtype=torch.uint8,
+                      device="cuda")
+    for tau in (0.1, 0.3):
+        W0 = copies.w[0]
+        fr = cl.ffn_forward_sparse_axpy_f32(xf1, h, i, W0.gate_packed_bytes(), W0.gate_scale_bits(),
+                                            W0.up_packed_bytes(), W0.up_scale_bits(), ptc, stc,
+                                            of1, tau, group_size=g, scale_dtype=sdt,
+                                            workspace=wsx, tiling=cl.TILING_MFMA)
+        exa = [cl._lib.Expert(*(t.data_ptr() for t in (W.gate_packed_bytes(), W.gate_scale_bits(),
+                                                        W.up_packed_bytes(), W.up_scale_bits())),
+                              ptc.data_ptr(), stc.data_ptr(), cl.TILING_MFMA) for W in copies.w]
+
+        def axffn(r, tau=tau):
+            cl.check("cascadia_int4_ffn_forward_sparse_axpy_f32",
+                     cl.lib().cascadia_int4_ffn_forward_sparse_axpy_f32(
+                         h, i, g, sdt, C.byref(exa[r % nc]), xf1.data_ptr(), 1, tau, None,
+                         of1.data_ptr(), None, wsx.data_ptr(),
+                         torch.cuda.current_stream().cuda_stream))
+        for r in range(10):
+            axffn(r)
+        steps = 200
+        _, ev = graph_time(torch, axffn, steps)
+        t = ev / steps
+        mat = i * h // 2 + i * (h // g) * 2
+        na = int(round(fr * i))
+        b = mat + na * (h // 2 + (h // g) * 2) + na * (h // 2 + (h // 32) * 2) + h * 4 * 2
+        res[f"sparse_axpy_ffn_M1_tau{tau}"] = {"us_per_call": round(t * 1e6, 2),
+                                               "active_frac": round(fr, 4),
+                                               "GB/s": round(b / t / 1e9, 1),
+                                               "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+                                               "note": "gate copies rotate; one transposed down"}
+    del ptc, stc, wsx
     # the AXPY form of the sparse down (ffn_axpy.rs:82-160): config 1's down
     # transposed to [inter, hidden], 13.4 % of the rows active (what tau 0.3
     # selects above), over rotating copies larger than 2x the Infinity Cache

@@ -17,6 +17,8 @@ from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertSou
                   dequant_gemv_int4_auto, expert_bytes, expert_forward, expert_forward_sparse,
                   expert_forward_sparse_per_channel, ffn_forward_sparse_f32,
                   ffn_forward_sparse_f32_per_channel, ffn_sparse_workspace_bytes,
+                  ffn_forward_sparse_axpy_f32, ffn_forward_sparse_axpy_f32_mode,
+                  ffn_forward_sparse_axpy_f32_per_channel, ffn_sparse_axpy_workspace_bytes,
                   ffn_workspace_bytes, transpose_requantize_down, dequant_axpy_int4_active,
                   dequant_axpy_int4_active_auto, fill_bytes, fill_normal,
                   fill_scales, gate_up_silu, gemm_int4_bf16, MoEExperts, moe_forward,
@@ -29,6 +31,8 @@ __all__ = [
     "dequant_gemv_int4", "dequant_gemv_int4_auto", "expert_bytes", "expert_forward",
     "expert_forward_sparse", "expert_forward_sparse_per_channel", "ffn_forward_sparse_f32",
     "ffn_forward_sparse_f32_per_channel", "ffn_sparse_workspace_bytes", "ffn_workspace_bytes",
+    "ffn_forward_sparse_axpy_f32", "ffn_forward_sparse_axpy_f32_mode",
+    "ffn_forward_sparse_axpy_f32_per_channel", "ffn_sparse_axpy_workspace_bytes",
     "transpose_requantize_down", "dequant_axpy_int4_active", "dequant_axpy_int4_active_auto", "fill_bytes",
     "fill_normal", "fill_scales", "gate_up_silu", "gemm_int4_bf16", "tile_weights",
     "tiled_sizes", "TILING_CRATE", "TILING_MFMA", "MoEExperts", "moe_forward",

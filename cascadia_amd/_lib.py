@@ -96,6 +96,9 @@ SIGNATURES = {
                                                     _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_expert_forward_sparse": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32, C.c_float,
                                                    _vp, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_ffn_sparse_axpy_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
+    "cascadia_int4_ffn_forward_sparse_axpy_f32": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32,
+                                                         C.c_float, _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_quantize_bf16": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "cascadia_int4_open_source": (_i32, [C.c_char_p, C.POINTER(_vp)]),
     "cascadia_int4_destroy_source": (None, [_vp]),

@@ -329,6 +329,79 @@ def _sparse_call(x, weights, out, threshold, thresholds, group_size, scale_dtype
     return frac[0] if x.dim() == 1 else frac
 
 
+def ffn_sparse_axpy_workspace_bytes(hidden, inter, n_tokens, group_size=GROUP_SIZE) -> int:
+    return int(lib().cascadia_int4_ffn_sparse_axpy_workspace_bytes(hidden, inter, group_size,
+                                                                    n_tokens))
+
+
+def ffn_forward_sparse_axpy_f32_mode(x_f32, hidden, intermediate, gate_packed, gate_scale,
+                                     up_packed, up_scale, down_packed_t, down_scale_t_bits,
+                                     out_f32, mode, group_size=GROUP_SIZE,
+                                     scale_dtype=SCALE_BF16, workspace=None,
+                                     tiling=TILING_CRATE):
+    """ffn_sparsity.rs:638-740: the AXPY-form sparse SwiGLU FFN, f32 in / out.
+    down_packed_t / down_scale_t_bits: transpose_requantize_down's layout
+    ([intermediate, hidden] codes, bf16 scales in groups of 32 along hidden).
+    mode: a float (SparsityMode::Global) or a device f32 tensor of one
+    threshold per intermediate lane (SparsityMode::PerChannel).  `workspace`
+    plays the crate's FfnScratch (ffn_axpy.rs:452).  Returns the active
+    fraction (a float for a 1-D x, else one per row)."""
+    _dev(x_f32, "x"), _dev(out_f32, "out")
+    _expect(x_f32.dtype == torch.float32 and out_f32.dtype == torch.float32, "f32 in/out")
+    _expect(hidden % 32 == 0 and hidden % group_size == 0, "hidden: a multiple of 32 and of G")
+    _check_weights(gate_packed, gate_scale, intermediate, hidden, group_size, tiling)
+    _check_weights(up_packed, up_scale, intermediate, hidden, group_size, tiling)
+    _dev(down_packed_t, "down_packed_t"), _dev(down_scale_t_bits, "down_scale_t_bits")
+    _expect(_nbytes(down_packed_t) == intermediate * hidden // 2, "down_packed_t length")
+    _expect(_nbytes(down_scale_t_bits) == intermediate * (hidden // 32) * 2,
+            "down_scale_t_bits length")
+    T = x_f32.numel() // hidden
+    _expect(x_f32.numel() == T * hidden and out_f32.numel() == T * hidden and T >= 1,
+            "x and out must be [n_tokens, hidden]")
+    thr, tau = 0, 0.0
+    if isinstance(mode, torch.Tensor):
+        _dev(mode, "thresholds")
+        _expect(mode.dtype == torch.float32 and mode.numel() == intermediate,
+                f"per-channel thresholds length {mode.numel()} != intermediate {intermediate}")
+        thr = mode.contiguous().data_ptr()
+    else:
+        tau = float(mode)
+    e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed_t,
+                       down_scale_t_bits, tiling)
+    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
+    counts = torch.empty(T, dtype=torch.int32, device=x_f32.device)
+    check("cascadia_int4_ffn_forward_sparse_axpy_f32",
+          lib().cascadia_int4_ffn_forward_sparse_axpy_f32(
+              hidden, intermediate, group_size, scale_dtype, C.byref(e), x_f32.data_ptr(), T,
+              tau, thr, out_f32.data_ptr(), counts.data_ptr(), ws, _stream()))
+    # count / intermediate in f32 (ffn_sparsity.rs:703)
+    frac = [float(np.float32(c) / np.float32(intermediate)) for c in counts.cpu().tolist()]
+    return frac[0] if x_f32.dim() == 1 else frac
+
+
+def ffn_forward_sparse_axpy_f32(x_f32, hidden, intermediate, gate_packed, gate_scale, up_packed,
+                                up_scale, down_packed_t, down_scale_t_bits, out_f32, threshold,
+                                group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, workspace=None,
+                                tiling=TILING_CRATE):
+    """ffn_sparsity.rs:569-600 (SparsityMode::Global)."""
+    return ffn_forward_sparse_axpy_f32_mode(x_f32, hidden, intermediate, gate_packed, gate_scale,
+                                            up_packed, up_scale, down_packed_t,
+                                            down_scale_t_bits, out_f32, float(threshold),
+                                            group_size, scale_dtype, workspace, tiling)
+
+
+def ffn_forward_sparse_axpy_f32_per_channel(x_f32, hidden, intermediate, gate_packed,
+                                            gate_scale, up_packed, up_scale, down_packed_t,
+                                            down_scale_t_bits, out_f32, thresholds,
+                                            group_size=GROUP_SIZE, scale_dtype=SCALE_BF16,
+                                            workspace=None, tiling=TILING_CRATE):
+    """ffn_sparsity.rs:605-633 (SparsityMode::PerChannel)."""
+    return ffn_forward_sparse_axpy_f32_mode(x_f32, hidden, intermediate, gate_packed, gate_scale,
+                                            up_packed, up_scale, down_packed_t,
+                                            down_scale_t_bits, out_f32, thresholds, group_size,
+                                            scale_dtype, workspace, tiling)
+
+
 def transpose_requantize_down(src_packed, src_scale_bits, n_hidden, n_intermediate,
                               group_size=GROUP_SIZE, scale_dtype=SCALE_BF16):
     """ffn_axpy.rs:342-440: the down matrix [n_hidden, n_intermediate] (crate

@@ -463,6 +463,83 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
                   (int)n_tokens, out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st,
                   part);
 }
+// Workspace of the AXPY-form sparse FFN: gate, SiLU and the intermediate
+// ([n_tokens, inter] f32 each), active lane ids [n_tokens, inter], two cells
+// and a count per token, the gate GEMM's split-K partials, the AXPY's slice
+// partials (one token at a time, sized for every lane active).
+struct AxpyFfnWorkspace {
+  size_t lanes, cells, counts, part_gemm, part_axpy, total;
+};
+AxpyFfnWorkspace axpy_ffn_workspace(int dev, uint32_t hidden, uint32_t inter, uint32_t group,
+                                    uint32_t n_tokens) {
+  const cai4::SkinnyDevice d = device_props(dev);
+  AxpyFfnWorkspace w;
+  w.lanes = align256((size_t)n_tokens * inter * 4);
+  w.cells = align256((size_t)n_tokens * 8);
+  w.counts = align256((size_t)n_tokens * 4);
+  w.part_gemm = align256(cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens,
+                                           cai4::A_XF32, cai4::EPI_F32, d)
+                             .partial_bytes);
+  w.part_axpy = align256(cai4::axpy_plan((int)hidden, (int)inter).partial_bytes);
+  w.total = 4 * w.lanes + w.cells + w.counts + w.part_gemm + w.part_axpy;
+  return w;
+}
+
+// ffn_forward_sparse_axpy_f32_mode (ffn_sparsity.rs:638-740) for n_tokens
+// rows: gate GEMM (f32 x), plain SiLU + max, the mask and rows-subset up
+// (inter = silu * up on the active lanes), the active lanes compacted in
+// ascending order, then per token out = AXPY of those rows of the transposed
+// down (e->down_* hold transpose_requantize_down's codes and bf16 scales).
+int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
+             const cascadia_int4_expert *e, const float *x, uint32_t n_tokens, float tau,
+             const float *thr, float *out, uint32_t *counts_out, void *workspace,
+             hipStream_t st) {
+  if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
+  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
+  if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (hidden % 32 || n_tokens > 65535 || !aligned(x, 16) || !aligned(out, 16) ||
+      (thr && !aligned(thr, 4)) || (counts_out && !aligned(counts_out, 4)) ||
+      (workspace && !aligned(workspace, 16)))
+    return CASCADIA_INT4_ERR_ARG;
+  if (!act_fits((int)n_tokens, (int)hidden, cai4::A_XF32) ||
+      !act_fits((int)n_tokens, (int)inter, cai4::A_XF32))
+    return CASCADIA_INT4_ERR_ARG;
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const AxpyFfnWorkspace w = axpy_ffn_workspace(dev, hidden, inter, group, n_tokens);
+  void *ws = workspace;
+  if (!ws) {
+    if (int rc = lib_workspace(dev, w.total, &ws)) return rc;
+  }
+  uint8_t *b = static_cast<uint8_t *>(ws);
+  float *gate = reinterpret_cast<float *>(b);
+  float *sg = reinterpret_cast<float *>(b + w.lanes);
+  float *mid = reinterpret_cast<float *>(b + 2 * w.lanes);
+  uint32_t *active = reinterpret_cast<uint32_t *>(b + 3 * w.lanes);
+  uint32_t *cells = reinterpret_cast<uint32_t *>(b + 4 * w.lanes);
+  uint32_t *counts = counts_out ? counts_out
+                                : reinterpret_cast<uint32_t *>(b + 4 * w.lanes + w.cells);
+  void *part_gemm = w.part_gemm ? b + 4 * w.lanes + w.cells + w.counts : nullptr;
+  float *part_axpy =
+      reinterpret_cast<float *>(b + 4 * w.lanes + w.cells + w.counts + w.part_gemm);
+  int rc = run_gemm(e->gate_packed, e->gate_scale, nullptr, nullptr, (int)inter, (int)hidden,
+                    (int)group, (int)sdt, (int)e->tiling, x, nullptr, cai4::A_XF32,
+                    (int)n_tokens, gate, nullptr, cai4::EPI_F32, st, part_gemm, workspace == nullptr);
+  if (rc) return rc;
+  hipError_t err = cai4::sparse_ffn_mid(e->up_packed, e->up_scale, (int)inter, (int)hidden,
+                                        (int)group, (int)sdt, (int)e->tiling, x, true,
+                                        (int)n_tokens, gate, tau, thr, sg, cells, mid, nullptr,
+                                        st, true);
+  if (err == hipSuccess)
+    err = cai4::sparse_compact(gate, (int)inter, (int)n_tokens, tau, thr, sg, cells, active,
+                               counts, st);
+  for (uint32_t t = 0; t < n_tokens && err == hipSuccess; ++t)
+    err = cai4::axpy_active(e->down_packed, e->down_scale, mid + (size_t)t * inter,
+                            active + (size_t)t * inter, (int)inter, (int)hidden, (int)inter,
+                            part_axpy, out + (size_t)t * hidden, st, counts + t, true);
+  return hip_status(err);
+}
+
 // offsets of the six sections of a tiled expert blob
 void tiled_expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off[7]) {
   size_t gp, gs, dp, ds;
@@ -1242,6 +1319,25 @@ int cascadia_int4_expert_forward_sparse(uint32_t hidden, uint32_t inter, uint32_
   return sparse_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false, n_tokens,
                        threshold, thresholds, out_bf16, true, active_counts, workspace,
                        (hipStream_t)stream);
+}
+
+size_t cascadia_int4_ffn_sparse_axpy_workspace_bytes(uint32_t hidden, uint32_t inter,
+                                                     uint32_t group_size, uint32_t n_tokens) {
+  int dev;
+  if (current_device(&dev)) return 0;
+  if (group_size == 0 || group_size % 32) return 0;
+  return axpy_ffn_workspace(dev, hidden, inter, group_size, n_tokens).total;
+}
+
+int cascadia_int4_ffn_forward_sparse_axpy_f32(uint32_t hidden, uint32_t inter,
+                                              uint32_t group_size, uint32_t scale_dtype,
+                                              const cascadia_int4_expert *expert, const float *x,
+                                              uint32_t n_tokens, float threshold,
+                                              const float *thresholds, float *out,
+                                              uint32_t *active_counts, void *workspace,
+                                              void *stream) {
+  return axpy_ffn(hidden, inter, group_size, scale_dtype, expert, x, n_tokens, threshold,
+                  thresholds, out, active_counts, workspace, (hipStream_t)stream);
 }
 
 int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_size,

@@ -59,11 +59,14 @@ constexpr int kAxWaves = 8, kAxRows = 4;  // a slice: 32 active rows, 4 per wave
 __global__ void __launch_bounds__(64 * kAxWaves)
     axpy_active_kernel(const uint8_t *__restrict__ pt, const uint16_t *__restrict__ st,
                        const float *__restrict__ scalars, const uint32_t *__restrict__ active,
-                       int n_active, int per_slice, int H, int I, float *__restrict__ partial) {
+                       int n_active, const uint32_t *__restrict__ n_dev, int per_slice, int H,
+                       int I, float *__restrict__ partial) {
   __shared__ float s_acc[kAxWaves - 1][2048];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = blockIdx.x * 2048 + 32 * lane;  // this lane's 32 columns
+  if (n_dev) n_active = min(n_active, (int)*n_dev);  // the count the device found
   const int a0 = blockIdx.y * per_slice;
+  if (a0 >= n_active) return;  // uniform: a slice past the count (its partial is never read)
   const int a1 = min(a0 + per_slice, n_active);
   const int GD = H / 32;
   float acc[32];
@@ -121,10 +124,12 @@ __global__ void __launch_bounds__(64 * kAxWaves)
 // 64 columns per block; wave w adds slices w, w + 4, ... (eight loads in
 // flight), and the four wave sums are added in wave order: deterministic.
 __global__ void __launch_bounds__(256)
-    axpy_reduce_kernel(const float *__restrict__ partial, int slices, int H, float *__restrict__ y) {
+    axpy_reduce_kernel(const float *__restrict__ partial, int slices, int H, float *__restrict__ y,
+                       const uint32_t *__restrict__ n_dev, int per_slice, int overwrite) {
   __shared__ float s_sum[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = blockIdx.x * 64 + lane;
+  if (n_dev) slices = min(slices, (int)((*n_dev + per_slice - 1) / per_slice));
   float s = 0.0f;
   if (h < H) {
     for (int k = wave; k < slices; k += 32) {
@@ -140,7 +145,10 @@ __global__ void __launch_bounds__(256)
   }
   s_sum[wave][lane] = s;
   __syncthreads();
-  if (wave == 0 && h < H) y[h] += ((s_sum[0][lane] + s_sum[1][lane]) + s_sum[2][lane]) + s_sum[3][lane];
+  if (wave == 0 && h < H) {
+    const float v = ((s_sum[0][lane] + s_sum[1][lane]) + s_sum[2][lane]) + s_sum[3][lane];
+    y[h] = overwrite ? v : y[h] + v;
+  }
 }
 
 }  // namespace
@@ -169,15 +177,15 @@ AxpyPlan axpy_plan(int H, int n_active) {
 
 hipError_t axpy_active(const uint8_t *pt, const uint8_t *st_bits, const float *scalars,
                        const uint32_t *active, int n_active, int H, int I, float *partial,
-                       float *y, hipStream_t st) {
+                       float *y, hipStream_t st, const uint32_t *n_dev, bool overwrite) {
   const AxpyPlan p = axpy_plan(H, n_active);
   if (p.slices == 0) return hipSuccess;
   hipLaunchKernelGGL(axpy_active_kernel, dim3((H + 2047) / 2048, p.slices), dim3(64 * kAxWaves), 0,
                      st, pt,
                      reinterpret_cast<const uint16_t *>(st_bits), scalars, active, n_active,
-                     p.per_slice, H, I, partial);
+                     n_dev, p.per_slice, H, I, partial);
   hipLaunchKernelGGL(axpy_reduce_kernel, dim3((H + 63) / 64), dim3(256), 0, st, partial,
-                     p.slices, H, y);
+                     p.slices, H, y, n_dev, p.per_slice, overwrite ? 1 : 0);
   return hipGetLastError();
 }
 

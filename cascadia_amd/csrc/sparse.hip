@@ -58,7 +58,10 @@ CAI4_DEV float wave_sum(float v) {
   return v;
 }
 
-// cells of a token: [0] max |silu| bits, [1] any per-channel threshold > 0
+// cells of a token: [0] max |silu| bits, [1] any per-channel threshold > 0.
+// PLAIN: the AXPY form's SiLU g / (1 + e^-g) (ffn_sparsity.rs:667-678), else
+// the stable one of build_active_mask_mode.
+template <bool PLAIN>
 __global__ void __launch_bounds__(256)
     sparse_prep_kernel(const float *__restrict__ gate, int I, const float *__restrict__ thr,
                        float *__restrict__ sg, uint32_t *__restrict__ cells) {
@@ -69,7 +72,7 @@ __global__ void __launch_bounds__(256)
   float a = 0.0f;
   int pos = 0;
   if (i < I) {
-    const float s = silu_stable(gate[row + i]);
+    const float s = PLAIN ? silu_plain(gate[row + i]) : silu_stable(gate[row + i]);
     sg[row + i] = s;
     a = fabsf(s);
     a = a > 0.0f ? a : 0.0f;  // NaN -> 0 (a NaN lane never raises the max)
@@ -218,14 +221,53 @@ __global__ void __launch_bounds__(256)
 
 }  // namespace
 
+// Active lanes of each token in ascending order (active[t * I ..]) and their
+// count, by the mask test of rows_subset_kernel: one workgroup per token, a
+// chunk of 1024 lanes per pass, ranks by ballot within waves and a scan of
+// the wave totals.
+__global__ void __launch_bounds__(kMaskThreads)
+    sparse_compact_kernel(const float *__restrict__ gate, int I, float tau,
+                          const float *__restrict__ thr, const float *__restrict__ sg,
+                          const uint32_t *__restrict__ cells, uint32_t *__restrict__ active,
+                          uint32_t *__restrict__ counts) {
+  __shared__ uint32_t s_w[kMaskWaves];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t row = (size_t)t * I;
+  uint32_t base = 0;
+  for (int c0 = 0; c0 < I; c0 += kMaskThreads) {
+    const int i = c0 + tid;
+    float s;
+    const bool on = i < I && lane_active(gate, sg, thr, tau, cells, t, row + i, i, &s);
+    const uint64_t b = __ballot(on);
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+    if (lane == 0) s_w[wave] = (uint32_t)__popcll(b);
+    __syncthreads();
+    uint32_t off = base, tot = 0;
+    for (int w = 0; w < kMaskWaves; ++w) {
+      const uint32_t n = s_w[w];
+      if (w < wave) off += n;
+      tot += n;
+    }
+    if (on) active[row + off + rank] = (uint32_t)i;
+    base += tot;
+    __syncthreads();  // s_w is rewritten by the next pass
+  }
+  if (tid == 0) counts[t] = base;
+}
+
 hipError_t sparse_ffn_mid(const uint8_t *w, const uint8_t *s, int I, int K, int G, int sdt,
                           int tiled, const void *x, bool x_f32, int T, const float *gate,
                           float tau, const float *thr, float *sg, uint32_t *cells, float *inter,
-                          uint32_t *counts_out, hipStream_t st) {
+                          uint32_t *counts_out, hipStream_t st, bool plain_silu) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((2 * T + 255) / 256), dim3(256), 0, st, cells, 2 * T,
                      0u);
-  hipLaunchKernelGGL(sparse_prep_kernel, dim3((I + 255) / 256, T), dim3(256), 0, st, gate, I, thr,
-                     sg, cells);
+  if (plain_silu)
+    hipLaunchKernelGGL(sparse_prep_kernel<true>, dim3((I + 255) / 256, T), dim3(256), 0, st, gate,
+                       I, thr, sg, cells);
+  else
+    hipLaunchKernelGGL(sparse_prep_kernel<false>, dim3((I + 255) / 256, T), dim3(256), 0, st,
+                       gate, I, thr, sg, cells);
   const dim3 grid((I + 3) / 4, T), block(256);
   const uint16_t *sc = reinterpret_cast<const uint16_t *>(s);
   if (tiled) {
@@ -246,6 +288,14 @@ hipError_t sparse_ffn_mid(const uint8_t *w, const uint8_t *s, int I, int K, int 
   if (counts_out)
     hipLaunchKernelGGL(sparse_count_kernel, dim3(T), dim3(kMaskThreads), 0, st, gate, I, tau, thr,
                        sg, cells, counts_out);
+  return hipGetLastError();
+}
+
+hipError_t sparse_compact(const float *gate, int I, int T, float tau, const float *thr,
+                          const float *sg, const uint32_t *cells, uint32_t *active,
+                          uint32_t *counts, hipStream_t st) {
+  hipLaunchKernelGGL(sparse_compact_kernel, dim3(T), dim3(kMaskThreads), 0, st, gate, I, tau, thr,
+                     sg, cells, active, counts);
   return hipGetLastError();
 }
 

@@ -246,6 +246,31 @@ int cascadia_int4_expert_forward_sparse(uint32_t hidden, uint32_t inter, uint32_
                                         uint16_t *out_bf16, uint32_t *active_counts,
                                         void *workspace, void *stream);
 
+/* The AXPY form of the activation-sparse FFN, f32 in / f32 out: replaces
+ * ffn_forward_sparse_axpy_f32 / _per_channel / _mode
+ * (src/ffn_sparsity.rs:569-740; called per routed expert by
+ * crates/cascadia-engine-sparse-moe/src/runner.rs:1043, :1162).  gate in
+ * full, s = g / (1 + e^-g), lanes with |s| >= cutoff * max|s| active (every
+ * lane when max|s| is 0, threshold <= 0 with thresholds NULL, or every
+ * per-channel threshold <= 0), up for the active rows only, inter = s * up
+ * on them, then out = sum over the active lanes r (ascending) of inter[r] *
+ * dequant(down_t[r, :]) -- the down matrix in the transposed layout of
+ * cascadia_int4_transpose_requantize_down, given in expert->down_packed /
+ * down_scale (as the crate passes down_packed_t / down_scale_t_bits in the
+ * down slots); gate/up in expert->tiling.  x, out: f32 [n_tokens, hidden]
+ * (out fully overwritten); active_counts (device u32 [n_tokens], may be NULL)
+ * receives each row's active-lane count (the crate returns count / inter).
+ * workspace: >= cascadia_int4_ffn_sparse_axpy_workspace_bytes or NULL. */
+size_t cascadia_int4_ffn_sparse_axpy_workspace_bytes(uint32_t hidden, uint32_t inter,
+                                                     uint32_t group_size, uint32_t n_tokens);
+int cascadia_int4_ffn_forward_sparse_axpy_f32(uint32_t hidden, uint32_t inter,
+                                              uint32_t group_size, uint32_t scale_dtype,
+                                              const cascadia_int4_expert *expert, const float *x,
+                                              uint32_t n_tokens, float threshold,
+                                              const float *thresholds, float *out,
+                                              uint32_t *active_counts, void *workspace,
+                                              void *stream);
+
 /* Dense SwiGLU FFN, f32 in / f32 out, no rounding: ffn_forward_sparse_f32 at
  * tau = 0 (src/ffn_sparsity.rs:373-496), used for the shared expert
  * (shell_int4.rs:629).  x, out: [n_tokens, hidden] f32. */

@@ -85,6 +85,8 @@ def _declare(L):
         "or_cpu_gemm": (None, [vp, vp, vp, sz, sz, sz, sz, i32, vp]),
         "or_cpu_expert_forward": (None, [vp, sz, sz, sz, sz, i32, vp, vp]),
         "or_cpu_moe_layer": (None, [vp, sz, sz, sz, sz, i32, vp, sz, sz, vp, sz, vp, vp, sz, f32, vp]),
+        "or_ffn_forward_sparse_axpy_f32_mode": (f32, [vp, sz, sz, sz, i32, i32, vp, vp, vp, vp, vp,
+                                                      vp, f32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -224,6 +226,24 @@ def dequant_axpy_active(packed_t, scale_t, scalars, active, inter, hidden, y=Non
     lib().or_dequant_axpy_active(_p(packed_t), _p(scale_t), _p(scalars), _p(active), active.size,
                                  inter, hidden, _p(y))
     return y
+
+
+def ffn_forward_sparse_axpy_f32(x, flat, down_pt, down_st, hidden, inter, group, sdt, tau,
+                                thresholds=None, order=ORDER_AVX512):
+    """ffn_sparsity.rs:638-740: gate / up from the crate-layout expert blob
+    `flat`, down from transpose_requantize_down's (down_pt, down_st);
+    returns (out f32 [hidden], active fraction)."""
+    x, flat = _c(x, np.float32), _c(flat, np.uint8)
+    pt, st = _c(down_pt, np.uint8), _c(down_st, np.uint8)
+    t, tp = _thr(thresholds, inter)
+    offs, _ = expert_offsets(hidden, inter, group)
+    base = flat.ctypes.data
+    out = np.empty(hidden, np.float32)
+    frac = lib().or_ffn_forward_sparse_axpy_f32_mode(
+        _p(x), hidden, inter, group, sdt, order, C.c_void_p(base + offs[0]),
+        C.c_void_p(base + offs[1]), C.c_void_p(base + offs[2]), C.c_void_p(base + offs[3]),
+        _p(pt), _p(st), tau, tp, _p(out))
+    return out, float(frac)
 
 
 def build_active_mask(gate_out, tau, thresholds=None):

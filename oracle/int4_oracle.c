@@ -664,3 +664,54 @@ void or_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *scale_t_bits
     }
   }
 }
+
+/* ------------------------------------------------------------------ */
+/* AXPY-form sparse FFN (ffn_sparsity.rs:638-740)                      */
+/* ------------------------------------------------------------------ */
+
+/* ffn_forward_sparse_axpy_f32_mode: gate in full (f32 x), plain SiLU
+ * g / (1 + e^-g) and its max |.| (:667-678); every lane active when the max
+ * is 0 or the mode is dense (tau <= 0, or every per-channel threshold <= 0,
+ * :679-681), else |silu| >= tau * max (:682-700); up for the active rows
+ * (:704-714), inter = silu * up on them (:717-722), out = 0 then the AXPY of
+ * the active rows of the transposed down (:730-738).  down_pt / down_st:
+ * transpose_requantize_down's [inter, hidden] codes and bf16 scales.
+ * Returns the active fraction. */
+float or_ffn_forward_sparse_axpy_f32_mode(const float *x, size_t hidden, size_t inter,
+                                          size_t group, int scale_dtype, int order,
+                                          const uint8_t *gate_p, const uint8_t *gate_s,
+                                          const uint8_t *up_p, const uint8_t *up_s,
+                                          const uint8_t *down_pt, const uint8_t *down_st,
+                                          float tau, const float *thresholds, float *out) {
+  float *g = (float *)malloc(inter * sizeof(float));
+  float *sg = (float *)malloc(inter * sizeof(float));
+  float *u = (float *)calloc(inter, sizeof(float));
+  float *m = (float *)calloc(inter, sizeof(float));
+  uint32_t *act = (uint32_t *)malloc(inter * sizeof(uint32_t));
+  or_gemv(gate_p, gate_s, x, inter, hidden, group, scale_dtype, order, g);
+  float max_abs = 0.0f;
+  for (size_t i = 0; i < inter; i++) {
+    sg[i] = silu_plain(g[i]);
+    const float a = fabsf(sg[i]);
+    if (a > max_abs) max_abs = a;
+  }
+  int dense = thresholds ? 1 : !(tau > 0.0f);
+  if (thresholds)
+    for (size_t i = 0; i < inter; i++)
+      if (!(thresholds[i] <= 0.0f)) dense = 0;
+  size_t na = 0;
+  for (size_t i = 0; i < inter; i++) {
+    const float cut = (thresholds ? thresholds[i] : tau) * max_abs;
+    if (max_abs == 0.0f || dense || fabsf(sg[i]) >= cut) act[na++] = (uint32_t)i;
+  }
+  or_gemv_rows_subset(up_p, up_s, x, inter, hidden, group, scale_dtype, order, act, na, u);
+  for (size_t a = 0; a < na; a++) m[act[a]] = sg[act[a]] * u[act[a]];
+  for (size_t j = 0; j < hidden; j++) out[j] = 0.0f;
+  or_dequant_axpy_active(down_pt, down_st, m, act, na, inter, hidden, out);
+  free(g);
+  free(sg);
+  free(u);
+  free(m);
+  free(act);
+  return (float)na / (float)inter;
+}

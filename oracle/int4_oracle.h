@@ -110,6 +110,12 @@ void or_transpose_requantize_down(const uint8_t *src_packed, const uint8_t *src_
 void or_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *scale_t_bits,
                             const float *scalars, const uint32_t *active, size_t n_active,
                             size_t inter, size_t hidden, float *y);
+float or_ffn_forward_sparse_axpy_f32_mode(const float *x, size_t hidden, size_t inter,
+                                          size_t group, int scale_dtype, int order,
+                                          const uint8_t *gate_p, const uint8_t *gate_s,
+                                          const uint8_t *up_p, const uint8_t *up_s,
+                                          const uint8_t *down_pt, const uint8_t *down_st,
+                                          float tau, const float *thresholds, float *out);
 
 /* ---- routing ---- */
 /* K2.6 / GLM rule: sigmoid, choose top-k by (sigmoid + bias) with ties to the

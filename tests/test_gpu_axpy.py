@@ -85,3 +85,40 @@ def test_axpy_order_empty_and_bad_ids(cl, orc):
     assert_f32_close(host(y2), orc.dequant_axpy_active(want_p, want_s, s, act[:10], i, h), "bad ids")
     with pytest.raises(ValueError):
         cl.transpose_requantize_down(dev(packed), dev(scales), h + 16, i)
+
+
+def test_transpose_requantize_f32_inverse(cl, orc):
+    """The closed form of test_oracle's f32-inverse pin on the GPU: a group
+    holding -8 and 4 at source scale 0.125 transposes to codes -7 and 3 (not
+    4, which 1 / bf16(scale) would give), scale bits 0x3E12."""
+    from test_oracle import _crate_down
+    h, i = 64, 32
+    codes = np.zeros((h, i), np.int64)
+    codes[0, :] = -8
+    codes[1, :] = 4
+    codes[2, :] = 3
+    packed, scales = _crate_down(orc, h, i, codes, np.full((h, i // 32), 0x3E00))
+    pt, st = cl.transpose_requantize_down(dev(packed), dev(scales), h, i)
+    pt, st = host(pt), host(st)
+    got = np.stack([pt & 15, pt >> 4], -1).reshape(i, h).astype(np.int64) - 8
+    assert np.all(got[:, 0] == -7) and np.all(got[:, 1] == 3) and np.all(got[:, 2] == 3)
+    assert np.all(st.view(np.uint16).reshape(i, h // 32)[:, 0] == 0x3E12)
+
+
+def test_transpose_requantize_g128_f16(cl, orc):
+    """The generalised source format (G 128 along intermediate, fp16 scales:
+    config 1's down, which the crate's G 32 / bf16 function does not take):
+    the GPU codes and scales equal the crate's re-quantisation (restated in
+    numpy above) applied to the source dequantised bit-exactly."""
+    h, i, g = 512, 1024, 128
+    packed = orc.fill_bytes(4, 80, h * i // 2)
+    scales = orc.fill_scales(4, 81, h * (i // g), 1).view(np.uint8).copy()
+    from test_oracle import np_requantize
+    w = orc.dequant(packed, scales, h, i, g, 1)  # pinned bit-exact dequantisation
+    want_q, want_s = np_requantize(w)
+    pt, st = cl.transpose_requantize_down(dev(packed), dev(scales), h, i, group_size=g,
+                                          scale_dtype=1)
+    pt, st = host(pt), host(st)
+    got_q = np.stack([pt & 15, pt >> 4], -1).reshape(i, h).astype(np.int64) - 8
+    assert np.array_equal(st.view(np.uint16).reshape(i, h // 32), want_s)
+    assert np.array_equal(got_q, want_q)

@@ -164,3 +164,73 @@ def test_sparse_edge_cases(cl, orc):
     with pytest.raises(ValueError):
         cl.ffn_forward_sparse_f32_per_channel(dev(xf), h, i, *W.slices(), o32,
                                               dev(np.zeros(i - 1, np.float32)))
+
+
+# ----------------------------------------------------------------------------
+# the AXPY form (ffn_sparsity.rs:569-740): f32 in / out, plain SiLU, down as
+# an AXPY over the active rows of transpose_requantize_down's matrix
+# ----------------------------------------------------------------------------
+
+def _axpy_case(cl, orc, h, i, g, sdt, tiled, seed):
+    flat = make_expert(orc, h, i, g, sdt, seed)
+    offs, sizes = orc.expert_offsets(h, i, g)
+    W = cl.ExpertWeights(dev(flat), h, i, g, sdt)
+    pt, st = cl.transpose_requantize_down(W.down_packed_bytes(), W.down_scale_bits(), h, i,
+                                          group_size=g, scale_dtype=sdt)
+    Wt = W.tiled() if tiled else W
+    return flat, Wt, pt, st
+
+
+@pytest.mark.parametrize("tau", [0.0, 0.1, 0.3])
+@pytest.mark.parametrize("h,i,g,sdt,tiled", [(512, 256, 32, BF16, False),
+                                             (7168, 2048, 32, BF16, True),
+                                             (4096, 14336, 128, F16, True)])
+def test_axpy_ffn_matches_oracle(cl, orc, h, i, g, sdt, tiled, tau):
+    """One token: output within rel-L2 1e-3 / max-abs 2e-2 of the oracle fed
+    the same transposed down (bit-identical to the crate's for G 32 bf16; for
+    config 1's G 128 fp16 source, pinned by test_transpose_requantize_g128_f16),
+    the active fraction exact."""
+    flat, W, pt, st = _axpy_case(cl, orc, h, i, g, sdt, tiled, h + i + g)
+    x = orc.fill_normal_f32(91, h, h)
+    if tau > 0:
+        assert margin(orc, flat, x, h, i, g, sdt, tau, None) > MARGIN
+    out = torch.empty(h, dtype=torch.float32, device="cuda")
+    frac = cl.ffn_forward_sparse_axpy_f32(dev(x), h, i, W.gate_packed_bytes(), W.gate_scale_bits(),
+                                          W.up_packed_bytes(), W.up_scale_bits(), pt, st, out, tau,
+                                          group_size=g, scale_dtype=sdt,
+                                          tiling=cl.TILING_MFMA if tiled else cl.TILING_CRATE)
+    want, wfrac = orc.ffn_forward_sparse_axpy_f32(x, flat, host(pt), host(st), h, i, g, sdt, tau)
+    assert frac == wfrac, f"active fraction {frac} != {wfrac}"
+    assert_f32_close(host(out), want, f"axpy ffn {h}x{i} G{g} tau={tau}")
+
+
+def test_axpy_ffn_rows_and_per_channel(cl, orc):
+    """Three token rows, each against the oracle; per-channel thresholds of one
+    value equal the global tau bit for bit (ffn_sparsity.rs:1497-1560);
+    mixed per-channel thresholds against the oracle."""
+    h, i, g, sdt, T = 1024, 768, 64, F16, 3
+    flat, W, pt, st = _axpy_case(cl, orc, h, i, g, sdt, True, 5)
+    x = orc.fill_normal_f32(92, T, T * h).reshape(T, h)
+    args = (W.gate_packed_bytes(), W.gate_scale_bits(), W.up_packed_bytes(), W.up_scale_bits(),
+            pt, st)
+    kw = dict(group_size=g, scale_dtype=sdt, tiling=cl.TILING_MFMA)
+    o1 = torch.empty((T, h), dtype=torch.float32, device="cuda")
+    f1 = cl.ffn_forward_sparse_axpy_f32(dev(x), h, i, *args, o1, 0.2, **kw)
+    o2 = torch.empty((T, h), dtype=torch.float32, device="cuda")
+    f2 = cl.ffn_forward_sparse_axpy_f32_per_channel(dev(x), h, i, *args, o2,
+                                                    torch.full((i,), 0.2, device="cuda"), **kw)
+    assert np.array_equal(host(o1).view(np.uint32), host(o2).view(np.uint32)) and f1 == f2
+    ptn, stn = host(pt), host(st)
+    for t in range(T):
+        want, wf = orc.ffn_forward_sparse_axpy_f32(x[t], flat, ptn, stn, h, i, g, sdt, 0.2)
+        assert f1[t] == wf
+        assert_f32_close(host(o1)[t], want, f"row {t}")
+    thr = (np.random.default_rng(3).random(i) * 0.4).astype(np.float32)
+    o3 = torch.empty((T, h), dtype=torch.float32, device="cuda")
+    f3 = cl.ffn_forward_sparse_axpy_f32_per_channel(dev(x), h, i, *args, o3, dev(thr), **kw)
+    for t in range(T):
+        assert margin(orc, flat, x[t], h, i, g, sdt, 0.0, thr) > MARGIN
+        want, wf = orc.ffn_forward_sparse_axpy_f32(x[t], flat, ptn, stn, h, i, g, sdt, 0.0,
+                                                   thresholds=thr)
+        assert f3[t] == wf
+        assert_f32_close(host(o3)[t], want, f"per-channel row {t}")

@@ -658,3 +658,136 @@ def test_axpy_is_transposed_gemv(orc):
     # accumulates onto y
     y2 = orc.dequant_axpy_active(pt, st, s, active, i, h, y=np.ones(h, np.float32))
     assert np.allclose(y2, y + 1, rtol=1e-6, atol=1e-6)
+
+
+# ----------------------------------------------------------------------------
+# f3: the AXPY-form sparse FFN (ffn_sparsity.rs:569-740)
+# ----------------------------------------------------------------------------
+
+def _axpy_fixture():
+    """ffn_sparsity.rs:1196-1217: constant gate/up/down bytes, unit bf16
+    scales, x = 0.05 i - 0.5, hidden = intermediate = 64."""
+    h = i = 64
+    flat = fake_expert(h, i)
+    offs, _ = _offsets(h, i, 32)
+    down = flat[offs[4]:offs[5]]
+    down_s = flat[offs[5]:]
+    x = (np.arange(h, dtype=np.float32) * np.float32(0.05) - np.float32(0.5)).astype(np.float32)
+    return h, i, flat, down, down_s, x
+
+
+def _offsets(h, i, g):
+    gp, gs, dp = i * h // 2, i * (h // g) * 2, h * i // 2
+    return [0, gp, gp + gs, 2 * gp + gs, 2 * (gp + gs), 2 * (gp + gs) + dp], None
+
+
+def test_axpy_ffn_close_to_dense_at_zero(orc):
+    """ffn_sparsity.rs:1196-1267: at tau 0 the AXPY form (re-quantised
+    transposed down) stays within 20 % of the dense FFN's max."""
+    h, i, flat, down, down_s, x = _axpy_fixture()
+    dense, _ = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, 0.0)
+    pt, st = orc.transpose_requantize_down(down, down_s, h, i)
+    axpy, frac = orc.ffn_forward_sparse_axpy_f32(x, flat, pt, st, h, i, 32, BF16, 0.0)
+    assert frac == 1.0
+    assert np.max(np.abs(dense - axpy)) <= max(float(np.max(np.abs(dense))), 1.0) * 0.20
+
+
+def test_axpy_ffn_matches_sparse_at_small_tau(orc):
+    """ffn_sparsity.rs:1273-1345: at tau 0.1 the two sparse formulations agree
+    within 2x the dense max, with a fraction in (0, 1]."""
+    h, i, flat, down, down_s, x = _axpy_fixture()
+    sparse, _ = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, 0.10)
+    pt, st = orc.transpose_requantize_down(down, down_s, h, i)
+    axpy, frac = orc.ffn_forward_sparse_axpy_f32(x, flat, pt, st, h, i, 32, BF16, 0.10)
+    assert 0.0 < frac <= 1.0
+    assert np.max(np.abs(sparse - axpy)) <= max(float(np.max(np.abs(sparse))), 1.0) * 2.0
+
+
+def test_axpy_per_channel_uniform_matches_global(orc):
+    """ffn_sparsity.rs:1497-1560: a per-channel vector of one value tau0 is
+    bit-identical to the global tau0 (output and fraction)."""
+    h, i, flat, down, down_s, x = _axpy_fixture()
+    pt, st = orc.transpose_requantize_down(down, down_s, h, i)
+    for tau in (0.0, 0.05, 0.10, 0.30):
+        a, fa = orc.ffn_forward_sparse_axpy_f32(x, flat, pt, st, h, i, 32, BF16, tau)
+        b, fb = orc.ffn_forward_sparse_axpy_f32(x, flat, pt, st, h, i, 32, BF16, 0.0,
+                                                thresholds=np.full(i, tau, np.float32))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and fa == fb, tau
+
+
+@pytest.mark.parametrize("tau", [0.0, 0.2, 0.5])
+def test_axpy_ffn_closed_form_exact_transpose(orc, tau):
+    """With a down matrix the transpose-requantisation keeps exactly (codes in
+    [-7, 7], a +-7 in every group, power-of-two scales), the AXPY FFN is the
+    f32 FFN whose intermediate is silu * up on the lanes |silu| >= tau * max
+    and 0 elsewhere -- computed here with numpy from the pinned GEMVs; the
+    active fraction is that lane count."""
+    h, i, g = 96, 64, 32
+    rng = np.random.default_rng(9)
+    gate_p, gate_s = rand_layout(rng, i, h, g, BF16)
+    up_p, up_s = rand_layout(rng, i, h, g, BF16)
+    codes = rng.integers(-7, 8, (h, i))
+    codes[0::32, :] = 7
+    down_p, down_s = _crate_down(orc, h, i, codes, np.full((h, i // 32), 0x3E80))  # 0.25
+    flat = np.concatenate([gate_p, gate_s, up_p, up_s, down_p, down_s])
+    pt, st = orc.transpose_requantize_down(down_p, down_s, h, i)
+    x = rng.normal(0, 1, h).astype(np.float32)
+    got, frac = orc.ffn_forward_sparse_axpy_f32(x, flat, pt, st, h, i, g, BF16, tau)
+    gate = orc.gemv(gate_p, gate_s, x, i, h, g, BF16).astype(np.float64)
+    up = orc.gemv(up_p, up_s, x, i, h, g, BF16).astype(np.float64)
+    silu = gate / (1.0 + np.exp(-gate))
+    mask = np.abs(silu) >= tau * np.max(np.abs(silu)) if tau > 0 else np.ones(i, bool)
+    m = np.where(mask, silu * up, 0.0)
+    w_down = codes.astype(np.float64) * 0.25
+    want = w_down @ m
+    assert frac == mask.sum() / i
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-4 * np.max(np.abs(want)))
+
+
+def test_transpose_requantize_uses_f32_inverse(orc):
+    """ffn_axpy.rs:406-419: codes are round(v * (1 / scale)) with the f32
+    scale max|v| / 7, and the bf16 rounding of the scale is only what is
+    stored.  Source scale 0.125 with a -8 and a 4 in the destination group:
+    scale = 1/7 in f32, v = 0.5 -> 0.5 * 6.9999995 = 3.4999998 -> code 3;
+    with 1 / bf16(scale) = 1 / 0.142578125 it would be 3.507 -> code 4."""
+    h, i = 64, 32
+    codes = np.zeros((h, i), np.int64)
+    codes[0, :] = -8   # the group max: |-8 * 0.125| = 1.0
+    codes[1, :] = 4    # v = 0.5
+    codes[2, :] = 3    # v = 0.375 -> 2.6249998 -> 3 either way
+    packed, scales = _crate_down(orc, h, i, codes, np.full((h, i // 32), 0x3E00))  # 0.125
+    pt, st = orc.transpose_requantize_down(packed, scales, h, i)
+    got = (np.stack([pt & 15, pt >> 4], -1).reshape(i, h).astype(np.int64) - 8)
+    assert np.all(got[:, 0] == -7) and np.all(got[:, 1] == 3) and np.all(got[:, 2] == 3)
+    st16 = st.view(np.uint16).reshape(i, h // 32)
+    assert np.all(st16[:, 0] == 0x3E12)  # bf16(1/7) = 0.142578125
+
+
+def np_requantize(w):
+    """ffn_axpy.rs:393-432 on an exactly dequantised source w [h, i] (f32):
+    groups of 32 along h of w^T, scale = max|v| / 7 (f32; 1.0 when 0), codes
+    round-half-away(v * f32(1 / scale)) clamped to [-8, 7], stored scale bf16
+    (RNE)."""
+    h, i = w.shape
+    g = np.ascontiguousarray(w.T).reshape(i, h // 32, 32).astype(np.float32)
+    m = np.max(np.abs(g), axis=2)
+    scale = np.where(m == 0, np.float32(1.0), m / np.float32(7.0)).astype(np.float32)
+    inv = np.where(m == 0, np.float32(0.0), np.float32(1.0) / scale).astype(np.float32)
+    q = (g * inv[..., None]).astype(np.float32).astype(np.float64)
+    q = np.clip(np.sign(q) * np.floor(np.abs(q) + 0.5), -8, 7).astype(np.int64)
+    b = scale.view(np.uint32).astype(np.uint64)
+    sbits = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    return q.reshape(i, h), sbits
+
+
+def test_np_requantize_matches_oracle(orc):
+    """The numpy restatement above (used for the GPU's generalised formats)
+    equals the oracle's transpose_requantize_down on the crate's format."""
+    h, i = 256, 128
+    rng = np.random.default_rng(21)
+    packed, scales = rand_layout(rng, h, i, 32, BF16)
+    pt, st = orc.transpose_requantize_down(packed, scales, h, i)
+    q, sb = np_requantize(orc.dequant(packed, scales, h, i, 32, BF16))
+    got = np.stack([pt & 15, pt >> 4], -1).reshape(i, h).astype(np.int64) - 8
+    assert np.array_equal(got, q)
+    assert np.array_equal(st.view(np.uint16).reshape(i, h // 32), sb)
