@@ -661,11 +661,13 @@ def quantize_int4_group(weight_bf16: torch.Tensor, n_rows: int, k_cols: int,
 
 class ExpertSource:
     """The crate's C handle API (c_ffi.rs:35-341) as its ctypes callers use it:
-    a safetensors model directory, experts run one f32 vector at a time on
-    host arrays of the model's hidden size.  Experts are uploaded and tiled
-    into HBM on first use (or by prewarm) and stay resident until close.
-    Errors raise CascadiaInt4Error with the crate's code (-1 null, -2 path
-    or expert, -3 directory or HIP)."""
+    a safetensors model directory, or an int4_bin one (manifest.json
+    "experts_format": "int4_bin", experts/layer_LL/expert_EEE.bin), experts
+    run one f32 vector at a time on host arrays of the model's hidden size.
+    Experts are uploaded and tiled into HBM on first use (or by prewarm) and
+    stay resident in an LRU cache (set_cache_limits; runner.rs:142-258) until
+    evicted or close.  Errors raise CascadiaInt4Error with the crate's code
+    (-1 null, -2 path or expert, -3 directory or HIP)."""
 
     def __init__(self, model_dir: str):
         h = C.c_void_p()
@@ -687,6 +689,19 @@ class ExpertSource:
                 "out_f32 must be a contiguous float32 numpy array of x's size")
         check("cascadia_int4_expert_forward", lib().cascadia_int4_expert_forward(
             self._h, layer, expert, x_f32.ctypes.data, out_f32.ctypes.data))
+
+    def set_cache_limits(self, max_experts: int = 0, max_bytes: int = 0) -> None:
+        """Bound the resident experts (0 = unbounded); lowering evicts at once."""
+        check("cascadia_int4_source_set_cache_limits",
+              lib().cascadia_int4_source_set_cache_limits(self._h, max_experts, max_bytes))
+
+    def cache_stats(self):
+        """(resident experts, evictions so far, resident bytes) -- lru_stats
+        (runner.rs:148-158) plus the bytes."""
+        a, b, c = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        check("cascadia_int4_source_cache_stats", lib().cascadia_int4_source_cache_stats(
+            self._h, C.byref(a), C.byref(b), C.byref(c)))
+        return a.value, b.value, c.value
 
     def close(self) -> None:
         if self._h:

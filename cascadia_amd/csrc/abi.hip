@@ -110,11 +110,18 @@ int side_stream(int dev, hipStream_t *side, hipEvent_t *fork, hipEvent_t *join) 
   return CASCADIA_INT4_OK;
 }
 
-// Library workspace of at least `bytes` on the current device.
-int lib_workspace(int dev, size_t bytes, void **out) {
+// Library workspace of at least `bytes` on the current device.  Growing it
+// synchronises the device and frees the old buffer, which a stream capture
+// cannot record (and a captured graph may still use the old buffer): while
+// `st` is capturing, a call that would grow it is refused with ERR_ARG (pass
+// a workspace of the *_workspace_bytes size instead).
+int lib_workspace(int dev, size_t bytes, void **out, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState &d = g_dev[dev];
   if (d.ws_bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return CASCADIA_INT4_ERR_ARG;
     if (d.ws) {
       if (hipDeviceSynchronize() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
       (void)hipFree(d.ws);
@@ -192,7 +199,7 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, G, M, amode, epi, d);
   if (p.partial_bytes && !partials) {
     if (!may_alloc) return CASCADIA_INT4_ERR_ARG;
-    if (int rc = lib_workspace(dev, p.partial_bytes, &partials)) return rc;
+    if (int rc = lib_workspace(dev, p.partial_bytes, &partials, st)) return rc;
   }
   cai4::SkinnyArgs a{};
   a.partials = partials;
@@ -355,7 +362,7 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   const FfnWorkspace need = ffn_workspace(dev, hidden, inter, group, n_tokens, x_f32);
   void *ws = workspace;
   if (!ws) {
-    if (int rc = lib_workspace(dev, need.total(), &ws)) return rc;
+    if (int rc = lib_workspace(dev, need.total(), &ws, st)) return rc;
   } else if (!aligned(ws, 16)) {
     return CASCADIA_INT4_ERR_ARG;
   }
@@ -441,7 +448,7 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   const SparseWorkspace w = sparse_workspace(dev, hidden, inter, group, n_tokens);
   void *ws = workspace;
   if (!ws) {
-    if (int rc = lib_workspace(dev, w.total, &ws)) return rc;
+    if (int rc = lib_workspace(dev, w.total, &ws, st)) return rc;
   }
   uint8_t *b = static_cast<uint8_t *>(ws);
   float *gate = reinterpret_cast<float *>(b);
@@ -509,7 +516,7 @@ int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   const AxpyFfnWorkspace w = axpy_ffn_workspace(dev, hidden, inter, group, n_tokens);
   void *ws = workspace;
   if (!ws) {
-    if (int rc = lib_workspace(dev, w.total, &ws)) return rc;
+    if (int rc = lib_workspace(dev, w.total, &ws, st)) return rc;
   }
   uint8_t *b = static_cast<uint8_t *>(ws);
   float *gate = reinterpret_cast<float *>(b);
@@ -592,7 +599,7 @@ int run_prefill(const cascadia_int4_layout *L, const uint8_t *packed, const uint
             dev,
             cai4::gg_dense_workspace((int)M, (int)L->n_rows, (int)L->k_cols, (int)L->group_size,
                                      cai4::GG_A_BF16, out_f32 ? cai4::GG_F32 : cai4::GG_BF16, cus),
-            &ws))
+            &ws, st))
       return rc;
     cai4::GgArgs a{};
     a.w0 = packed;
@@ -612,7 +619,7 @@ int run_prefill(const cascadia_int4_layout *L, const uint8_t *packed, const uint
   if (int rc = lib_workspace(dev,
                              cai4::prefill_workspace_bytes((int)M, (int)L->n_rows, (int)L->k_cols,
                                                            device_props(dev).num_cus),
-                             &ws))
+                             &ws, st))
     return rc;
   return hip_status(cai4::prefill_gemm(packed, scales, x, y, (int)M, (int)L->n_rows,
                                        (int)L->k_cols, (int)L->group_size, (int)L->scale_dtype,
@@ -732,7 +739,7 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   const MoePlan m = moe_plan(dev, L, R->top_k, T, R->mode == CASCADIA_INT4_ROUTE_IDS);
   void *ws = workspace;
   if (!ws) {
-    if (int rc = lib_workspace(dev, m.ws.total, &ws)) return rc;
+    if (int rc = lib_workspace(dev, m.ws.total, &ws, st)) return rc;
   } else if (!aligned(ws, 256)) {
     return CASCADIA_INT4_ERR_ARG;
   }
@@ -1283,7 +1290,7 @@ int cascadia_int4_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *sc
   if (!ws) {
     int dev;
     if (int rc = current_device(&dev)) return rc;
-    if (int rc = lib_workspace(dev, p.partial_bytes, &ws)) return rc;
+    if (int rc = lib_workspace(dev, p.partial_bytes, &ws, (hipStream_t)stream)) return rc;
   }
   return hip_status(cai4::axpy_active(packed_t, scale_t_bits, scalars, active, (int)n_active,
                                       (int)hidden, (int)inter, static_cast<float *>(ws), y,

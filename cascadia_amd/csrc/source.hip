@@ -16,10 +16,22 @@
 // (compressed-tensors: packed int32 [rows, cols / 8], whose little-endian
 // bytes are the crate layout; scales bf16 or f16 [rows, cols / G]).
 //
-// Where the crate mmaps the shards and lets the OS page an expert in
-// (prewarm touches its pages), here an expert is read from the shards once,
-// uploaded, tiled into the MFMA layout and kept resident in HBM for the life
-// of the handle: prewarm does that load.  expert_forward converts x to bf16
+// A directory whose manifest.json says "experts_format": "int4_bin" is read
+// as the runners' flat-expert layout instead (manifest.rs:137-142,
+// ov_moe.rs:786-806): experts/layer_LL/expert_EEE.bin, each the six sections
+// gate_p, gate_s, up_p, up_s, down_p, down_s of format.rs:35-47 with groups
+// of 32 and bf16 scales; hidden = "hidden_size", intermediate =
+// "expert_intermediate" (0 or absent: the crate's 2048, format.rs:51-126).
+//
+// Where the crate mmaps the files and lets the OS page an expert in and out
+// (prewarm touches its pages), here an expert is read once, uploaded, tiled
+// into the MFMA layout and kept in HBM, in an LRU cache modelled on the
+// runner's (runner.rs:142-258): bounded by a count of experts and a byte
+// budget (cascadia_int4_source_set_cache_limits, or the environment variables
+// CASCADIA_INT4_MAX_CACHED_EXPERTS / CASCADIA_INT4_EXPERT_CACHE_BYTES at open;
+// 0 = unbounded), the least recently used expert evicted once the handle's
+// stream has drained; a device allocation that fails evicts and retries
+// before it is reported.  prewarm does the load.  expert_forward converts x to bf16
 // as the crate does (bf16::from_f32: RNE, NaN made quiet), runs
 // cascadia_int4_expert_forward_device and widens the bf16 result to f32; it
 // is synchronous, like the crate's.  The hidden size is the model's (7168 in
@@ -31,8 +43,12 @@
 #include <fcntl.h>
 #include <unistd.h>
 
+#include <sys/stat.h>
+
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <list>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -269,6 +285,7 @@ struct TensorRef {
 
 struct Shard {
   int fd = -1;
+  size_t file_bytes = 0;
   std::unordered_map<std::string, TensorRef> tensors;
   ~Shard() {
     if (fd >= 0) close(fd);
@@ -277,18 +294,35 @@ struct Shard {
 
 struct DeviceExpert {
   void *blob = nullptr;  // the tiled sections
+  size_t bytes = 0;
   cascadia_int4_expert e{};
   uint32_t hidden = 0, inter = 0, group = 0, sdt = 0;
 };
+
+using ExpertKey = std::pair<uint32_t, uint32_t>;
+
+size_t env_size(const char *name) {
+  const char *v = getenv(name);
+  if (!v || !*v) return 0;
+  char *end = nullptr;
+  const unsigned long long n = strtoull(v, &end, 10);
+  return end && *end == '\0' ? (size_t)n : 0;
+}
 
 }  // namespace
 
 struct CascadiaInt4Source {
   std::string dir;
   int device = 0;
+  bool int4_bin = false;  // flat expert files (manifest experts_format "int4_bin")
+  uint32_t bin_hidden = 0, bin_inter = 0;
   std::unordered_map<std::string, std::string> weight_map;  // tensor -> shard file
   std::unordered_map<std::string, std::unique_ptr<Shard>> shards;
-  std::map<std::pair<uint32_t, uint32_t>, DeviceExpert> experts;
+  // the resident experts, most recently used first
+  std::list<std::pair<ExpertKey, DeviceExpert>> lru;
+  std::map<ExpertKey, std::list<std::pair<ExpertKey, DeviceExpert>>::iterator> experts;
+  size_t max_experts = 0, max_bytes = 0, resident_bytes = 0;  // limits 0: unbounded
+  uint64_t evictions = 0;
   hipStream_t stream = nullptr;
   uint16_t *x_dev = nullptr, *out_dev = nullptr;
   void *ws = nullptr;
@@ -304,11 +338,15 @@ Shard *shard_of(CascadiaInt4Source *s, const std::string &file) {
   auto sh = std::make_unique<Shard>();
   sh->fd = open((s->dir + "/" + file).c_str(), O_RDONLY);
   if (sh->fd < 0) return nullptr;
+  struct stat stt;
+  if (fstat(sh->fd, &stt) != 0) return nullptr;
+  sh->file_bytes = (size_t)stt.st_size;
   uint8_t hl[8];
   if (!pread_all(sh->fd, hl, 8, 0)) return nullptr;
   uint64_t n = 0;
   for (int i = 7; i >= 0; --i) n = (n << 8) | hl[i];
-  if (n > (1ull << 30)) return nullptr;
+  // a header longer than the file is malformed (safetensors_source.rs:85-95)
+  if (n > (1ull << 30) || n > sh->file_bytes - 8) return nullptr;
   std::string hdr(n, '\0');
   if (!pread_all(sh->fd, &hdr[0], n, 8)) return nullptr;
   Json j;
@@ -318,8 +356,17 @@ Shard *shard_of(CascadiaInt4Source *s, const std::string &file) {
     if (kv.first == "__metadata__") continue;
     const Json *off = kv.second.get("data_offsets");
     if (!off || off->kind != Json::ARR || off->arr.size() != 2) return nullptr;
-    const double a = off->arr[0].num, b = off->arr[1].num;
+    // as_u64().unwrap_or(0) (safetensors_source.rs:100-106): a negative,
+    // fractional or non-numeric offset, or one past 2^53, reads as 0
+    auto u64_or_0 = [](const Json &v) -> uint64_t {
+      if (v.kind != Json::NUM || !(v.num >= 0.0) || v.num > 9007199254740992.0 ||
+          v.num != (double)(uint64_t)v.num)
+        return 0;
+      return (uint64_t)v.num;
+    };
+    const uint64_t a = u64_or_0(off->arr[0]), b = u64_or_0(off->arr[1]);
     if (b < a) continue;  // safetensors_source.rs:107-109
+    if (b > sh->file_bytes - data0) continue;  // past the end of the file: unreadable
     TensorRef t;
     t.offset = data0 + (size_t)a;
     t.bytes = (size_t)(b - a);
@@ -344,14 +391,43 @@ bool tensor(CascadiaInt4Source *s, const std::string &name, Shard **sh, const Te
   return true;
 }
 
-// 0, -2 (the expert's tensors missing or inconsistent), -3 (HIP failure)
-int load_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, DeviceExpert **out) {
-  const auto key = std::make_pair(layer, expert);
-  auto it = s->experts.find(key);
-  if (it != s->experts.end()) {
-    *out = &it->second;
-    return 0;
+// Drop the least recently used resident expert (after the handle's stream
+// has drained: nothing in flight may still read it).  False when none is left.
+bool evict_one(CascadiaInt4Source *s) {
+  if (s->lru.empty()) return false;
+  if (hipStreamSynchronize(s->stream) != hipSuccess) return false;
+  auto &victim = s->lru.back();
+  (void)hipFree(victim.second.blob);
+  s->resident_bytes -= victim.second.bytes;
+  s->experts.erase(victim.first);
+  s->lru.pop_back();
+  ++s->evictions;
+  return true;
+}
+
+// Evict until one more expert of `bytes` fits the limits.
+void make_room(CascadiaInt4Source *s, size_t bytes) {
+  while (!s->lru.empty() &&
+         ((s->max_experts && s->lru.size() + 1 > s->max_experts) ||
+          (s->max_bytes && s->resident_bytes + bytes > s->max_bytes)))
+    if (!evict_one(s)) break;
+}
+
+// hipMalloc that evicts resident experts and retries when HBM is full.
+bool malloc_evicting(CascadiaInt4Source *s, void **p, size_t bytes) {
+  for (;;) {
+    if (hipMalloc(p, bytes) == hipSuccess) return true;
+    (void)hipGetLastError();  // clear the failed allocation's error
+    *p = nullptr;
+    if (!evict_one(s)) return false;
   }
+}
+
+// The six sections of expert (L, E) from the safetensors shards into the
+// pinned host buffer *host (allocated here): 0, or -2.
+int read_safetensors_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, void **host,
+                            uint32_t *hidden_o, uint32_t *inter_o, uint32_t *group_o,
+                            uint32_t *sdt_o) {
   const std::string base = "language_model.model.layers." + std::to_string(layer) +
                            ".mlp.experts." + std::to_string(expert) + ".";
   static const char *kNames[6] = {"gate_proj.weight_packed", "gate_proj.weight_scale",
@@ -371,40 +447,91 @@ int load_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, DeviceEx
       hidden % t[1]->shape[1])
     return -2;
   const int64_t group = hidden / t[1]->shape[1];
-  const uint32_t sdt = t[1]->dtype == "F16" ? CASCADIA_INT4_SCALE_F16 : CASCADIA_INT4_SCALE_BF16;
   const size_t pin = (size_t)inter * hidden / 2, sin = (size_t)inter * (hidden / group) * 2;
   const size_t pdn = (size_t)hidden * inter / 2, sdn = (size_t)hidden * (inter / group) * 2;
   const size_t want[6] = {pin, sin, pin, sin, pdn, sdn};
   for (int i = 0; i < 6; ++i)
     if (t[i]->bytes != want[i]) return -2;
   if (group % 32 || inter % group || inter > (1 << 30) || hidden > (1 << 30)) return -2;
-
-  const size_t flat = cascadia_int4_expert_bytes((uint32_t)hidden, (uint32_t)inter, (uint32_t)group);
-  const size_t tiled =
-      cascadia_int4_expert_tiled_bytes((uint32_t)hidden, (uint32_t)inter, (uint32_t)group);
-  if (!flat || !tiled) return -2;
-  void *host = nullptr, *dflat = nullptr, *dtiled = nullptr;
-  int rc = 0;
-  if (hipHostMalloc(&host, flat, hipHostMallocDefault) != hipSuccess) return -3;
-  {  // the six tensors in flat-blob order (format.rs:35-47)
-    size_t off = 0;
-    for (int i = 0; i < 6 && !rc; ++i) {
-      if (!pread_all(sh[i]->fd, static_cast<uint8_t *>(host) + off, want[i], t[i]->offset))
-        rc = -2;
-      off += want[i];
+  const size_t flat = pin * 2 + sin * 2 + pdn + sdn;
+  if (hipHostMalloc(host, flat, hipHostMallocDefault) != hipSuccess) return -3;
+  size_t off = 0;
+  for (int i = 0; i < 6; ++i) {  // flat-blob order (format.rs:35-47)
+    if (!pread_all(sh[i]->fd, static_cast<uint8_t *>(*host) + off, want[i], t[i]->offset)) {
+      (void)hipHostFree(*host);
+      *host = nullptr;
+      return -2;
     }
+    off += want[i];
   }
+  *hidden_o = (uint32_t)hidden;
+  *inter_o = (uint32_t)inter;
+  *group_o = (uint32_t)group;
+  *sdt_o = t[1]->dtype == "F16" ? CASCADIA_INT4_SCALE_F16 : CASCADIA_INT4_SCALE_BF16;
+  return 0;
+}
+
+// experts/layer_LL/expert_EEE.bin (manifest.rs:137-142): the flat blob of
+// format.rs:35-47 at the manifest's dims, G 32, bf16 scales: 0, or -2.
+int read_bin_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, void **host,
+                    uint32_t *hidden_o, uint32_t *inter_o, uint32_t *group_o, uint32_t *sdt_o) {
+  char name[64];
+  snprintf(name, sizeof name, "/experts/layer_%02u/expert_%03u.bin", layer, expert);
+  const int fd = open((s->dir + name).c_str(), O_RDONLY);
+  if (fd < 0) return -2;
+  const size_t flat = cascadia_int4_expert_bytes(s->bin_hidden, s->bin_inter, 32);
+  struct stat stt;
+  int rc = 0;
+  if (fstat(fd, &stt) != 0 || (size_t)stt.st_size != flat) rc = -2;
+  if (!rc && hipHostMalloc(host, flat, hipHostMallocDefault) != hipSuccess) rc = -3;
+  if (!rc && !pread_all(fd, *host, flat, 0)) {
+    (void)hipHostFree(*host);
+    *host = nullptr;
+    rc = -2;
+  }
+  close(fd);
+  if (rc) return rc;
+  *hidden_o = s->bin_hidden;
+  *inter_o = s->bin_inter;
+  *group_o = 32;
+  *sdt_o = CASCADIA_INT4_SCALE_BF16;
+  return 0;
+}
+
+// 0, -2 (the expert's data missing or inconsistent), -3 (HIP failure or no
+// room in HBM even with every other expert evicted)
+int load_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, DeviceExpert **out) {
+  const ExpertKey key = std::make_pair(layer, expert);
+  auto it = s->experts.find(key);
+  if (it != s->experts.end()) {
+    s->lru.splice(s->lru.begin(), s->lru, it->second);  // most recently used
+    *out = &it->second->second;
+    return 0;
+  }
+  void *host = nullptr;
+  uint32_t hidden = 0, inter = 0, group = 0, sdt = 0;
+  int rc = s->int4_bin ? read_bin_expert(s, layer, expert, &host, &hidden, &inter, &group, &sdt)
+                       : read_safetensors_expert(s, layer, expert, &host, &hidden, &inter, &group,
+                                                 &sdt);
+  if (rc) return rc;
+  const size_t flat = cascadia_int4_expert_bytes(hidden, inter, group);
+  const size_t tiled = cascadia_int4_expert_tiled_bytes(hidden, inter, group);
+  if (!flat || !tiled) {
+    (void)hipHostFree(host);
+    return -2;
+  }
+  make_room(s, tiled);
+  void *dflat = nullptr, *dtiled = nullptr;
   DeviceExpert de;
   cascadia_int4_expert src{};
-  if (!rc && (hipMalloc(&dflat, flat) != hipSuccess || hipMalloc(&dtiled, tiled) != hipSuccess))
-    rc = -3;
+  if (!malloc_evicting(s, &dtiled, tiled) || !malloc_evicting(s, &dflat, flat)) rc = -3;
   if (!rc && hipMemcpyAsync(dflat, host, flat, hipMemcpyHostToDevice, s->stream) != hipSuccess)
     rc = -3;
-  if (!rc && cascadia_int4_expert_from_flat(static_cast<uint8_t *>(dflat), (uint32_t)hidden,
-                                            (uint32_t)inter, (uint32_t)group, &src) != 0)
+  if (!rc && cascadia_int4_expert_from_flat(static_cast<uint8_t *>(dflat), hidden, inter, group,
+                                            &src) != 0)
     rc = -2;
-  if (!rc && cascadia_int4_tile_expert((uint32_t)hidden, (uint32_t)inter, (uint32_t)group, &src,
-                                       static_cast<uint8_t *>(dtiled), &de.e, s->stream) != 0)
+  if (!rc && cascadia_int4_tile_expert(hidden, inter, group, &src, static_cast<uint8_t *>(dtiled),
+                                       &de.e, s->stream) != 0)
     rc = -3;
   if (!rc && hipStreamSynchronize(s->stream) != hipSuccess) rc = -3;
   (void)hipHostFree(host);
@@ -414,11 +541,15 @@ int load_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, DeviceEx
     return rc;
   }
   de.blob = dtiled;
-  de.hidden = (uint32_t)hidden;
-  de.inter = (uint32_t)inter;
-  de.group = (uint32_t)group;
+  de.bytes = tiled;
+  de.hidden = hidden;
+  de.inter = inter;
+  de.group = group;
   de.sdt = sdt;
-  *out = &s->experts.emplace(key, de).first->second;
+  s->lru.emplace_front(key, de);
+  s->experts[key] = s->lru.begin();
+  s->resident_bytes += tiled;
+  *out = &s->lru.front().second;
   return 0;
 }
 
@@ -445,13 +576,29 @@ int cascadia_int4_open_source(const char *model_dir, CascadiaInt4Source **out_ha
   auto s = std::make_unique<CascadiaInt4Source>();
   s->dir = model_dir;
   std::string text;
-  Json idx;
-  if (!read_file(s->dir + "/model.safetensors.index.json", text) || !parse_json(text, idx))
-    return -3;
-  const Json *wm = idx.get("weight_map");
-  if (!wm || wm->kind != Json::OBJ) return -3;
-  for (const auto &kv : wm->obj)
-    if (kv.second.kind == Json::STR) s->weight_map.emplace(kv.first, kv.second.str);
+  Json man;
+  const Json *fmt = nullptr;
+  if (read_file(s->dir + "/manifest.json", text) && parse_json(text, man) &&
+      (fmt = man.get("experts_format")) && fmt->kind == Json::STR && fmt->str == "int4_bin") {
+    // the flat-expert layout (manifest.rs:21-80: hidden_size, expert_intermediate)
+    const Json *hs = man.get("hidden_size"), *ei = man.get("expert_intermediate");
+    if (!hs || hs->kind != Json::NUM || !(hs->num >= 32) || hs->num > (double)(1 << 20))
+      return -3;
+    s->int4_bin = true;
+    s->bin_hidden = (uint32_t)hs->num;
+    s->bin_inter = ei && ei->kind == Json::NUM && ei->num > 0 ? (uint32_t)ei->num : 2048u;
+    if (s->bin_hidden % 32 || s->bin_inter % 32 || s->bin_inter > (1u << 20)) return -3;
+  } else {
+    Json idx;
+    if (!read_file(s->dir + "/model.safetensors.index.json", text) || !parse_json(text, idx))
+      return -3;
+    const Json *wm = idx.get("weight_map");
+    if (!wm || wm->kind != Json::OBJ) return -3;
+    for (const auto &kv : wm->obj)
+      if (kv.second.kind == Json::STR) s->weight_map.emplace(kv.first, kv.second.str);
+  }
+  s->max_experts = env_size("CASCADIA_INT4_MAX_CACHED_EXPERTS");
+  s->max_bytes = env_size("CASCADIA_INT4_EXPERT_CACHE_BYTES");
   if (hipGetDevice(&s->device) != hipSuccess) return -3;
   if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) return -3;
   *out_handle = s.release();
@@ -463,7 +610,7 @@ void cascadia_int4_destroy_source(CascadiaInt4Source *handle) {
   {
     DeviceScope ds(handle->device);
     if (handle->stream) (void)hipStreamSynchronize(handle->stream);
-    for (auto &kv : handle->experts) (void)hipFree(kv.second.blob);
+    for (auto &kv : handle->lru) (void)hipFree(kv.second.blob);
     if (handle->x_dev) (void)hipFree(handle->x_dev);
     if (handle->out_dev) (void)hipFree(handle->out_dev);
     if (handle->ws) (void)hipFree(handle->ws);
@@ -496,8 +643,8 @@ int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uin
     if (handle->out_dev) (void)hipFree(handle->out_dev);
     handle->x_dev = handle->out_dev = nullptr;
     handle->io_elems = 0;
-    if (hipMalloc(&handle->x_dev, (size_t)h * 2) != hipSuccess ||
-        hipMalloc(&handle->out_dev, (size_t)h * 2) != hipSuccess)
+    if (!malloc_evicting(handle, reinterpret_cast<void **>(&handle->x_dev), (size_t)h * 2) ||
+        !malloc_evicting(handle, reinterpret_cast<void **>(&handle->out_dev), (size_t)h * 2))
       return -3;
     handle->io_elems = h;
   }
@@ -505,9 +652,11 @@ int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uin
     if (handle->ws) (void)hipFree(handle->ws);
     handle->ws = nullptr;
     handle->ws_bytes = 0;
-    if (hipMalloc(&handle->ws, need_ws) != hipSuccess) return -3;
+    if (!malloc_evicting(handle, &handle->ws, need_ws)) return -3;
     handle->ws_bytes = need_ws;
   }
+  // the expert may have been evicted to make room for the buffers: reload
+  if (int rc = load_expert(handle, layer, expert, &de)) return rc;
   std::vector<uint16_t> xb(h), ob(h);
   for (uint32_t i = 0; i < h; ++i) xb[i] = f32_to_bf16_host(x_f32[i]);  // c_ffi.rs:323
   if (hipMemcpyAsync(handle->x_dev, xb.data(), (size_t)h * 2, hipMemcpyHostToDevice,
@@ -524,6 +673,31 @@ int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uin
     const uint32_t b = (uint32_t)ob[i] << 16;
     memcpy(&out_f32[i], &b, 4);
   }
+  return 0;
+}
+
+int cascadia_int4_source_set_cache_limits(CascadiaInt4Source *handle, uint64_t max_experts,
+                                          uint64_t max_bytes) {
+  if (!handle) return -1;
+  std::lock_guard<std::mutex> lk(handle->mu);
+  DeviceScope ds(handle->device);
+  if (!ds.ok) return -3;
+  handle->max_experts = (size_t)max_experts;
+  handle->max_bytes = (size_t)max_bytes;
+  while (!handle->lru.empty() &&
+         ((handle->max_experts && handle->lru.size() > handle->max_experts) ||
+          (handle->max_bytes && handle->resident_bytes > handle->max_bytes)))
+    if (!evict_one(handle)) return -3;
+  return 0;
+}
+
+int cascadia_int4_source_cache_stats(CascadiaInt4Source *handle, uint64_t *cached,
+                                     uint64_t *evictions, uint64_t *resident_bytes) {
+  if (!handle) return -1;
+  std::lock_guard<std::mutex> lk(handle->mu);
+  if (cached) *cached = handle->lru.size();
+  if (evictions) *evictions = handle->evictions;
+  if (resident_bytes) *resident_bytes = handle->resident_bytes;
   return 0;
 }
 

@@ -21,6 +21,12 @@
  *   - Outputs are fully overwritten, as in the crate.  Calls are reentrant
  *     for distinct output buffers; a shared workspace (workspace == NULL, the
  *     library's own) makes concurrent calls on different streams race.
+ *   - HIP graph capture: the library's own workspace grows by a device
+ *     synchronisation and a reallocation, which a capture cannot record; a
+ *     call on a capturing stream that would grow it returns
+ *     CASCADIA_INT4_ERR_ARG.  Callers that capture pass a workspace of the
+ *     matching *_workspace_bytes size (or warm the library's up first, or use
+ *     cascadia_int4_expert_forward_noalloc).
  */
 #ifndef CASCADIA_INT4_H
 #define CASCADIA_INT4_H
@@ -343,9 +349,13 @@ int cascadia_int4_debug_dequant(const cascadia_int4_layout *layout, const uint8_
  * and codes.  A source is a safetensors model directory
  * (model.safetensors.index.json + shards; expert tensors
  * language_model.model.layers.L.mlp.experts.E.{gate,up,down}_proj.weight_{packed,scale},
- * packed int32 = the crate's bytes, scales bf16 or f16).  Experts are read
+ * packed int32 = the crate's bytes, scales bf16 or f16), or a directory whose
+ * manifest.json has "experts_format": "int4_bin" (flat expert files
+ * experts/layer_LL/expert_EEE.bin, manifest.rs:137-142, groups of 32, bf16
+ * scales, dims "hidden_size" / "expert_intermediate").  Experts are read
  * once, uploaded and tiled into HBM on first use (prewarm does that load, the
- * analogue of the crate's page-in) and stay resident until destroy.
+ * analogue of the crate's page-in) and stay resident in an LRU cache
+ * (cascadia_int4_source_set_cache_limits) until evicted or destroy.
  * expert_forward is synchronous and takes host arrays of the model's hidden
  * size (the crate's HIDDEN = 7168): x f32 -> bf16 (RNE, NaN quiet), the
  * expert FFN, bf16 -> f32.  Codes: 0 OK; -1 null; -2 invalid UTF-8 path
@@ -358,6 +368,19 @@ void cascadia_int4_destroy_source(CascadiaInt4Source *handle);
 int cascadia_int4_prewarm(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert);
 int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert,
                                  const float *x_f32, float *out_f32);
+
+/* A handle's expert cache (no counterpart in c_ffi.rs; the runner's
+ * RunnerOptions.max_cached_experts and lru_stats, runner.rs:148-170,
+ * 368-416).  Resident experts form an LRU bounded by max_experts and by
+ * max_bytes of HBM (0 = unbounded; the defaults come from the environment
+ * variables CASCADIA_INT4_MAX_CACHED_EXPERTS / CASCADIA_INT4_EXPERT_CACHE_BYTES
+ * at open).  Lowering a limit evicts at once.  A device allocation that
+ * fails evicts the least recently used experts and retries before a call
+ * reports -3.  Codes: 0, -1 null handle, -3 HIP failure. */
+int cascadia_int4_source_set_cache_limits(CascadiaInt4Source *handle, uint64_t max_experts,
+                                          uint64_t max_bytes);
+int cascadia_int4_source_cache_stats(CascadiaInt4Source *handle, uint64_t *cached,
+                                     uint64_t *evictions, uint64_t *resident_bytes);
 
 /* Load-time quantiser: bf16 weights [n_rows, k_cols] (device, 16-byte
  * aligned) -> packed nibbles [n_rows, k_cols/2] and bf16 group scales

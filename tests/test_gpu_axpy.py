@@ -122,3 +122,44 @@ def test_transpose_requantize_g128_f16(cl, orc):
     got_q = np.stack([pt & 15, pt >> 4], -1).reshape(i, h).astype(np.int64) - 8
     assert np.array_equal(st.view(np.uint16).reshape(i, h // 32), want_s)
     assert np.array_equal(got_q, want_q)
+
+
+def test_capture_refuses_library_workspace_growth(cl, orc):
+    """Inside a HIP graph capture, a call that would grow the library's own
+    workspace (a device synchronisation and a reallocation) is refused with
+    ERR_ARG before anything is launched; with a caller workspace the same
+    call captures, and its replays give the eager result."""
+    h, i, n = 32768, 32, 131072  # 4096 slices x 32768 x 4 B = 512 MiB of partials
+    pt = torch.full((i * h // 2,), 0x99, dtype=torch.uint8, device="cuda")
+    st = dev(np.full(i * (h // 32), 0x3F80, np.uint16).view(np.uint8))
+    s = torch.ones(i, dtype=torch.float32, device="cuda")
+    act = torch.zeros(n, dtype=torch.int32, device="cuda")  # row 0, n times
+    y = torch.zeros(h, dtype=torch.float32, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with pytest.raises(cl.CascadiaInt4Error) as ei:
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                cl.dequant_axpy_int4_active(pt, st, s, act, i, h, y)
+    assert ei.value.rc == -2
+    del g
+    torch.cuda.synchronize()
+    small = act[:100]
+    ws = torch.empty(cl.lib().cascadia_int4_axpy_workspace_bytes(h, 100), dtype=torch.uint8,
+                     device="cuda")
+    y_eager = torch.zeros(h, dtype=torch.float32, device="cuda")
+    cl.dequant_axpy_int4_active(pt, st, s, small, i, h, y_eager, workspace=ws)
+    g = torch.cuda.CUDAGraph()
+    y.zero_()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            cl.dequant_axpy_int4_active(pt, st, s, small, i, h, y, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager), f"replay {rep}"
+    # 0x99: codes 1, scale 1.0, each of 100 active rows adds 1
+    assert float(y_eager[0]) == 100.0

@@ -111,3 +111,137 @@ def test_handle_api_error_codes(tmp_path):
     assert L.cascadia_int4_prewarm(None, 0, 0) == -1
     assert L.cascadia_int4_expert_forward(None, 0, 0, None, None) == -1
     L.cascadia_int4_destroy_source(None)  # null-safe
+
+
+def write_int4_bin(path, hidden, inter, experts, with_inter=True):
+    """An int4_bin model directory (manifest.rs:21-80, :137-142): manifest.json
+    and experts/layer_LL/expert_EEE.bin flat blobs (format.rs:35-47, G 32,
+    bf16 scales).  experts: {(layer, expert): flat bytes}."""
+    man = {"arch": "test", "num_layers": 4, "dense_layers": [], "num_experts": 8, "top_k": 2,
+           "hidden_size": hidden, "num_kv_heads": 1, "qk_head_dim": 1, "v_head_dim": 1,
+           "vocab_size": 1, "eos_token_ids": [], "experts_format": "int4_bin"}
+    if with_inter:
+        man["expert_intermediate"] = inter
+    with open(os.path.join(path, "manifest.json"), "w") as f:
+        json.dump(man, f)
+    for (layer, e), flat in experts.items():
+        d = os.path.join(path, "experts", f"layer_{layer:02d}")
+        os.makedirs(d, exist_ok=True)
+        with open(os.path.join(d, f"expert_{e:03d}.bin"), "wb") as f:
+            f.write(bytes(flat))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hidden,inter,with_inter", [(3072, 1536, True), (7168, 2048, False)])
+def test_int4_bin_directory(orc, tmp_path, hidden, inter, with_inter):
+    """The runners' int4_bin layout through the handle API: M2 dims from the
+    manifest's expert_intermediate, and K2.6 dims from the crate's defaults
+    (no expert_intermediate); a missing or truncated file is -2."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import cascadia_amd as cl
+
+    data = {(1, 5): make_expert(orc, hidden, inter, 32, BF16, 31),
+            (2, 0): make_expert(orc, hidden, inter, 32, BF16, 32)}
+    write_int4_bin(str(tmp_path), hidden, inter, data, with_inter)
+    d = os.path.join(str(tmp_path), "experts", "layer_03")
+    os.makedirs(d)
+    with open(os.path.join(d, "expert_000.bin"), "wb") as f:
+        f.write(bytes(data[(1, 5)][:-2]))  # two bytes short
+    src = cl.ExpertSource(str(tmp_path))
+    for (layer, e), flat in data.items():
+        x = orc.fill_normal_f32(layer, e, hidden)
+        out = np.empty(hidden, np.float32)
+        src.expert_forward(layer, e, x, out)
+        want = orc.cpu_expert_forward(orc.f32_to_bf16(x), 1, flat, hidden, inter, 32, BF16).reshape(-1)
+        assert_bf16_close((out.view(np.uint32) >> 16).astype(np.uint16), want, f"bin ({layer}, {e})")
+    for layer, e in ((1, 6), (3, 0)):
+        with pytest.raises(cl.CascadiaInt4Error) as ei:
+            src.prewarm(layer, e)
+        assert ei.value.rc == -2
+    src.close()
+
+
+@pytest.mark.gpu
+def test_expert_cache_lru(orc, tmp_path, monkeypatch):
+    """The LRU of runner.rs:142-258: a two-expert cap evicts the least recently
+    used (stats count them), an evicted expert reloads with the same result, a
+    byte budget of one expert keeps one, and the environment variable sets the
+    cap at open."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import cascadia_amd as cl
+
+    h, i, g = 512, 256, 32
+    keys = [(0, 0), (0, 1), (1, 0), (1, 1)]
+    data = {k: (h, i, g, BF16, make_expert(orc, h, i, g, BF16, 40 + 2 * k[0] + k[1])) for k in keys}
+    write_model(str(tmp_path), data)
+    x = orc.fill_normal_f32(5, 5, h)
+
+    def run(src, k):
+        out = np.empty(h, np.float32)
+        src.expert_forward(*k, x, out)
+        return out
+
+    src = cl.ExpertSource(str(tmp_path))
+    first = {k: run(src, k) for k in keys}
+    assert src.cache_stats()[:2] == (4, 0)
+    src.set_cache_limits(max_experts=2)  # lowering evicts the two least recently used
+    n, ev, b = src.cache_stats()
+    assert (n, ev) == (2, 2)
+    per = b // 2
+    run(src, keys[0])  # evicted: reloads, evicting (1, 0)
+    assert src.cache_stats()[:2] == (2, 3)
+    run(src, keys[3])  # resident: no eviction
+    assert src.cache_stats()[:2] == (2, 3)
+    for k in keys:
+        assert np.array_equal(run(src, k), first[k]), f"reloaded expert {k} differs"
+    src.set_cache_limits(max_experts=0, max_bytes=per + per // 2)
+    assert src.cache_stats()[0] == 1
+    run(src, keys[1])
+    n, _, b = src.cache_stats()
+    assert n == 1 and b == per
+    src.close()
+    monkeypatch.setenv("CASCADIA_INT4_MAX_CACHED_EXPERTS", "1")
+    src = cl.ExpertSource(str(tmp_path))
+    for k in keys:
+        run(src, k)
+    assert src.cache_stats()[:2] == (1, 3)
+    src.close()
+
+
+@pytest.mark.gpu
+def test_corrupt_shard_headers(orc, tmp_path):
+    """Safetensors headers the crate rejects or reads as 0 (safetensors_source.rs
+    :85-109): a header length past the file, and negative or fractional data
+    offsets (as_u64().unwrap_or(0): the tensor's length comes out wrong) make
+    the expert unreadable, -2; nothing is read out of bounds."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import cascadia_amd as cl
+
+    h, i, g = 512, 256, 32
+    write_model(str(tmp_path), {(0, 0): (h, i, g, BF16, make_expert(orc, h, i, g, BF16, 9)),
+                                (1, 0): (h, i, g, BF16, make_expert(orc, h, i, g, BF16, 10))})
+    shard0 = os.path.join(str(tmp_path), "model-00001-of-00002.safetensors")
+    raw = bytearray(open(shard0, "rb").read())
+    n = int.from_bytes(raw[:8], "little")
+    hdr = json.loads(raw[8:8 + n])
+    name = "language_model.model.layers.0.mlp.experts.0.gate_proj.weight_scale"
+    a, b = hdr[name]["data_offsets"]
+    for bad in ([-4, b], [a + 0.5, b], [a, 1e30]):
+        hdr[name]["data_offsets"] = bad
+        hj = json.dumps(hdr).encode()
+        open(shard0, "wb").write(len(hj).to_bytes(8, "little") + hj + raw[8 + n:])
+        src = cl.ExpertSource(str(tmp_path))
+        with pytest.raises(cl.CascadiaInt4Error) as ei:
+            src.prewarm(0, 0)
+        assert ei.value.rc == -2, bad
+        src.prewarm(1, 0)  # the other shard is intact
+        src.close()
+    open(shard0, "wb").write((len(raw) * 4).to_bytes(8, "little") + raw[8:])  # length past EOF
+    src = cl.ExpertSource(str(tmp_path))
+    with pytest.raises(cl.CascadiaInt4Error) as ei:
+        src.prewarm(0, 0)
+    assert ei.value.rc == -2
+    src.close()
