@@ -22,7 +22,8 @@ from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertSou
                   ffn_workspace_bytes, transpose_requantize_down, dequant_axpy_int4_active,
                   dequant_axpy_int4_active_auto, fill_bytes, fill_normal,
                   fill_scales, gate_up_silu, gemm_int4_bf16, MoEExperts, moe_forward,
-                  moe_workspace_bytes, quantize_int4_group, tile_weights, tiled_sizes)
+                  moe_workspace_bytes, ov_gemv, ov_to_crate, quantize_int4_group, tile_weights,
+                  tiled_sizes)
 
 __all__ = [
     "CascadiaInt4Error", "LIB_PATH", "SCALE_BF16", "SCALE_F16", "SIGNATURES", "check", "lib",
@@ -36,6 +37,7 @@ __all__ = [
     "transpose_requantize_down", "dequant_axpy_int4_active", "dequant_axpy_int4_active_auto", "fill_bytes",
     "fill_normal", "fill_scales", "gate_up_silu", "gemm_int4_bf16", "tile_weights",
     "tiled_sizes", "TILING_CRATE", "TILING_MFMA", "MoEExperts", "moe_forward",
-    "moe_workspace_bytes", "quantize_int4_group", "ROUTE_IDS", "ROUTE_SIGMOID_BIAS",
+    "moe_workspace_bytes", "ov_gemv", "ov_to_crate", "quantize_int4_group", "ROUTE_IDS",
+    "ROUTE_SIGMOID_BIAS",
     "ROUTE_SOFTMAX_TOPK",
 ]

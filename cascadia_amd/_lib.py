@@ -55,6 +55,11 @@ class MoeLayer(C.Structure):
                 ("shared_inter", C.c_uint32)]
 
 
+class OvSegment(C.Structure):
+    _fields_ = [("packed", C.c_void_p), ("scale_f16", C.c_void_p), ("n_rows", C.c_uint32),
+                ("tiling", C.c_uint32)]
+
+
 class Routing(C.Structure):
     _fields_ = [("mode", C.c_uint32), ("top_k", C.c_uint32), ("logits", C.c_void_p),
                 ("bias", C.c_void_p), ("scale", C.c_float), ("normalize", C.c_uint32),
@@ -99,6 +104,10 @@ SIGNATURES = {
     "cascadia_int4_ffn_sparse_axpy_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
     "cascadia_int4_ffn_forward_sparse_axpy_f32": (_i32, [_u32, _u32, _u32, _u32, _EP, _vp, _u32,
                                                          C.c_float, _vp, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_ov_to_crate": (_i32, [_vp, _sz, _vp, _vp]),
+    "cascadia_int4_ov_gemv_workspace_bytes": (_sz, [C.POINTER(OvSegment), _u32, _u32, _u32, _u32]),
+    "cascadia_int4_ov_gemv": (_i32, [C.POINTER(OvSegment), _u32, _u32, _u32, _vp, _u32, _u32, _vp,
+                                     _u32, _vp, _vp]),
     "cascadia_int4_quantize_bf16": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "cascadia_int4_open_source": (_i32, [C.c_char_p, C.POINTER(_vp)]),
     "cascadia_int4_destroy_source": (None, [_vp]),

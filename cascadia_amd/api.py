@@ -18,7 +18,8 @@ import numpy as np
 import torch
 
 from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, Expert, Layout, MoeLayer,
-                   Routing, SCALE_BF16, SCALE_F16, TILING_CRATE, TILING_MFMA, check, lib)
+                   OvSegment, Routing, SCALE_BF16, SCALE_F16, TILING_CRATE, TILING_MFMA, check,
+                   lib)
 
 # K2.6 constants of the crate (lib.rs:71-78)
 HIDDEN = 7168
@@ -618,6 +619,47 @@ def moe_forward(experts: MoEExperts, x, out, *, top_k: int, logits=None, bias=No
     check("cascadia_int4_moe_forward", lib().cascadia_int4_moe_forward(
         C.byref(experts._struct()), C.byref(R), x.data_ptr(), res, T, out.data_ptr(), io, wo, ws,
         _stream()))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the OpenVINO CascadiaInt4Gemv format (cascadia-ov-genai-shim/cpp/gemv_offload.cpp)
+# ---------------------------------------------------------------------------
+
+def ov_to_crate(packed_ov: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The op's two's-complement nibbles -> the crate's offset nibbles (every
+    byte XOR 0x88; the same products).  out may be packed_ov (in place)."""
+    _dev(packed_ov, "packed_ov")
+    out = torch.empty_like(packed_ov) if out is None else _dev(out, "out")
+    _expect(_nbytes(out) == _nbytes(packed_ov), "out size")
+    check("cascadia_int4_ov_to_crate", lib().cascadia_int4_ov_to_crate(
+        packed_ov.data_ptr(), _nbytes(packed_ov), out.data_ptr(), _stream()))
+    return out
+
+
+def ov_gemv(segments, k_cols: int, group_size: int, act, out, workspace=None):
+    """The op's evaluate() (gemv_offload.cpp:413-660).  segments: a list of
+    (packed, scale_f16, n_rows, tiling) with packed converted by ov_to_crate
+    (and tiled, for TILING_MFMA); act: f16 or f32 [rows, k_cols]; out: f16 or
+    f32 [rows, sum n_rows], the segments' outputs concatenated per row."""
+    _dev(act, "act"), _dev(out, "out")
+    _expect(act.dtype in (torch.float16, torch.float32) and out.dtype in (torch.float16,
+                                                                          torch.float32),
+            "act and out: f16 or f32")
+    segs = (OvSegment * len(segments))()
+    n_total = 0
+    for j, (p, sc, n, tiling) in enumerate(segments):
+        _check_weights(p, sc, n, k_cols, group_size, tiling)
+        segs[j] = OvSegment(p.data_ptr(), sc.data_ptr(), n, tiling)
+        n_total += n
+    rows = act.numel() // k_cols
+    _expect(act.numel() == rows * k_cols and rows >= 1, "act must be [rows, k_cols]")
+    _expect(out.numel() == rows * n_total, "out must be [rows, sum of n_rows]")
+    ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
+    check("cascadia_int4_ov_gemv", lib().cascadia_int4_ov_gemv(
+        segs, len(segments), k_cols, group_size, act.data_ptr(),
+        int(act.dtype == torch.float16), rows, out.data_ptr(), int(out.dtype == torch.float16),
+        ws, _stream()))
     return out
 
 

@@ -13,6 +13,7 @@
 #include "int4_common.hpp"
 #include "layout.hpp"
 #include "moe.hpp"
+#include "ov.hpp"
 #include "gemv.hpp"
 #include "grouped.hpp"
 #include "prefill.hpp"
@@ -172,7 +173,7 @@ bool act_fits(int M, int K, int amode) {
 int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint8_t *s1,
              int N, int K, int G, int sdt, int tiled, const void *x, const void *x2, int amode,
              int M, void *out, void *out2, int epi, hipStream_t st, void *partials = nullptr,
-             bool may_alloc = true) {
+             bool may_alloc = true, int ldo = 0) {
   int dev;
   if (int rc = current_device(&dev)) return rc;
   if (!act_fits(M, K, amode)) return CASCADIA_INT4_ERR_ARG;
@@ -193,7 +194,7 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
     g.M = M;
     g.sdt = sdt;
     g.tiled = tiled;
-    if (cai4::gemv_supported(g, amode, epi, d.num_cus))
+    if ((M == 1 || ldo == 0 || ldo == N) && cai4::gemv_supported(g, amode, epi, d.num_cus))
       return hip_status(cai4::gemv_launch(g, amode, epi, d.num_cus, 0, st));
   }
   const cai4::SkinnyPlan p = cai4::skinny_plan(N, K, G, M, amode, epi, d);
@@ -216,7 +217,7 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
   a.G = G;
   a.M = M;
   a.ldx = K;
-  a.ldo = N;
+  a.ldo = ldo ? ldo : N;
   a.sdt = sdt;
   a.glog2 = glog2_of(G);
   a.tiled = tiled;
@@ -1326,6 +1327,88 @@ int cascadia_int4_expert_forward_sparse(uint32_t hidden, uint32_t inter, uint32_
   return sparse_common(hidden, inter, group_size, scale_dtype, expert, x_bf16, false, n_tokens,
                        threshold, thresholds, out_bf16, true, active_counts, workspace,
                        (hipStream_t)stream);
+}
+
+int cascadia_int4_ov_to_crate(const uint8_t *packed_ov, size_t n_bytes, uint8_t *packed_crate,
+                              void *stream) {
+  if (!packed_ov || !packed_crate) return CASCADIA_INT4_ERR_NULL;
+  if (n_bytes == 0) return CASCADIA_INT4_OK;
+  if (!aligned(packed_ov, 4) || !aligned(packed_crate, 4)) return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::ov_to_crate(packed_ov, n_bytes, packed_crate, (hipStream_t)stream));
+}
+
+size_t cascadia_int4_ov_gemv_workspace_bytes(const cascadia_int4_ov_segment *segs,
+                                             uint32_t n_segs, uint32_t k_cols,
+                                             uint32_t group_size, uint32_t rows) {
+  int dev;
+  if (!segs || current_device(&dev) || group_size == 0 || group_size % 32) return 0;
+  const cai4::SkinnyDevice d = device_props(dev);
+  size_t n_total = 0, part = 0;
+  for (uint32_t i = 0; i < n_segs; ++i) {
+    n_total += segs[i].n_rows;
+    const size_t pb = cai4::skinny_plan((int)segs[i].n_rows, (int)k_cols, (int)group_size,
+                                        (int)rows, cai4::A_XF32, cai4::EPI_F32, d)
+                          .partial_bytes;
+    part = pb > part ? pb : part;
+  }
+  return align256((size_t)rows * k_cols * 4) + align256((size_t)rows * n_total * 4) + part;
+}
+
+int cascadia_int4_ov_gemv(const cascadia_int4_ov_segment *segs, uint32_t n_segs,
+                          uint32_t k_cols, uint32_t group_size, const void *act,
+                          uint32_t act_f16, uint32_t rows, void *out, uint32_t out_f16,
+                          void *workspace, void *stream) {
+  if (!segs || !act || !out) return CASCADIA_INT4_ERR_NULL;
+  if (n_segs == 0 || rows == 0 || k_cols == 0 || group_size == 0 || group_size % 32 ||
+      k_cols % group_size || act_f16 > 1 || out_f16 > 1 || k_cols > (1u << 30))
+    return CASCADIA_INT4_ERR_ARG;
+  size_t n_total = 0;
+  for (uint32_t i = 0; i < n_segs; ++i) {
+    if (int rc = check_weights(segs[i].packed, segs[i].scale_f16)) return rc;
+    if (segs[i].n_rows == 0 || segs[i].tiling > CASCADIA_INT4_TILING_MFMA)
+      return CASCADIA_INT4_ERR_ARG;
+    n_total += segs[i].n_rows;
+  }
+  if (n_total > (1u << 30) || !aligned(act, act_f16 ? 2 : 16) || !aligned(out, out_f16 ? 2 : 4) ||
+      (workspace && !aligned(workspace, 256)))
+    return CASCADIA_INT4_ERR_ARG;
+  if (!act_fits((int)rows, (int)k_cols, cai4::A_XF32)) return CASCADIA_INT4_ERR_ARG;
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const size_t need =
+      cascadia_int4_ov_gemv_workspace_bytes(segs, n_segs, k_cols, group_size, rows);
+  void *ws = workspace;
+  if (!ws) {
+    if (int rc = lib_workspace(dev, need, &ws, st)) return rc;
+  }
+  uint8_t *b = static_cast<uint8_t *>(ws);
+  const size_t act_b = align256((size_t)rows * k_cols * 4);
+  const size_t out_b = align256((size_t)rows * n_total * 4);
+  const float *x = static_cast<const float *>(act);
+  if (act_f16) {  // the op's f16 activations (gemv_offload.cpp:485-488), exactly in f32
+    float *xf = reinterpret_cast<float *>(b);
+    if (hipError_t e = cai4::f16_to_f32(static_cast<const uint16_t *>(act),
+                                        (size_t)rows * k_cols, xf, st))
+      return hip_status(e);
+    x = xf;
+  }
+  float *y = out_f16 ? reinterpret_cast<float *>(b + act_b) : static_cast<float *>(out);
+  void *part = b + act_b + out_b;
+  size_t start = 0;
+  for (uint32_t i = 0; i < n_segs; ++i) {  // the segments' rows concatenated (:434-452)
+    if (int rc = run_gemm(segs[i].packed, segs[i].scale_f16, nullptr, nullptr,
+                          (int)segs[i].n_rows, (int)k_cols, (int)group_size,
+                          CASCADIA_INT4_SCALE_F16, (int)segs[i].tiling, x, nullptr, cai4::A_XF32,
+                          (int)rows, y + start, nullptr, cai4::EPI_F32, st, part, false,
+                          (int)n_total))
+      return rc;
+    start += segs[i].n_rows;
+  }
+  if (out_f16)  // ov::float16(acc): round to nearest even
+    return hip_status(cai4::f32_to_f16(y, (size_t)rows * n_total, static_cast<uint16_t *>(out),
+                                       st));
+  return CASCADIA_INT4_OK;
 }
 
 size_t cascadia_int4_ffn_sparse_axpy_workspace_bytes(uint32_t hidden, uint32_t inter,

@@ -382,6 +382,44 @@ int cascadia_int4_source_set_cache_limits(CascadiaInt4Source *handle, uint64_t m
 int cascadia_int4_source_cache_stats(CascadiaInt4Source *handle, uint64_t *cached,
                                      uint64_t *evictions, uint64_t *resident_bytes);
 
+/* ---- the OpenVINO CascadiaInt4Gemv format (crates/cascadia-ov-genai-shim/
+ *      cpp/gemv_offload.cpp) ---- */
+
+/* Convert that op's packed weights -- two per byte, element 0 in the low
+ * nibble, each nibble a two's-complement int4, q = (x ^ 8) - 8
+ * (gemv_offload.cpp:425-429, 630-632) -- to the crate's offset nibbles
+ * (q = x' - 8): every byte XOR 0x88, so the products are unchanged bit for
+ * bit.  Done once at upload; packed_crate may equal packed_ov.  Its f16
+ * scales [n, k / group] are already the crate layout with
+ * CASCADIA_INT4_SCALE_F16; tile the result with cascadia_int4_tile_weights as
+ * any crate-layout matrix. */
+int cascadia_int4_ov_to_crate(const uint8_t *packed_ov, size_t n_bytes, uint8_t *packed_crate,
+                              void *stream);
+
+/* One weight segment of the op (gemv_offload.cpp:334-341): n_rows output rows,
+ * packed already converted by cascadia_int4_ov_to_crate (tiling CRATE, or
+ * MFMA after cascadia_int4_tile_weights), f16 scales. */
+typedef struct cascadia_int4_ov_segment {
+  const uint8_t *packed;
+  const uint8_t *scale_f16;
+  uint32_t n_rows;
+  uint32_t tiling;
+} cascadia_int4_ov_segment;
+
+/* The op's evaluate() (gemv_offload.cpp:413-660): out[r, :] = the segments'
+ * GEMVs of activation row r, concatenated in segment order, for rows rows;
+ * act f16 (act_f16 = 1) or f32 [rows, k_cols], out f16 (RNE) or f32
+ * [rows, sum of n_rows]; any group size that is a multiple of 32 dividing
+ * k_cols (the op: any even size).  f32 accumulation.  workspace: >=
+ * cascadia_int4_ov_gemv_workspace_bytes (256-byte aligned) or NULL. */
+size_t cascadia_int4_ov_gemv_workspace_bytes(const cascadia_int4_ov_segment *segs,
+                                             uint32_t n_segs, uint32_t k_cols,
+                                             uint32_t group_size, uint32_t rows);
+int cascadia_int4_ov_gemv(const cascadia_int4_ov_segment *segs, uint32_t n_segs,
+                          uint32_t k_cols, uint32_t group_size, const void *act,
+                          uint32_t act_f16, uint32_t rows, void *out, uint32_t out_f16,
+                          void *workspace, void *stream);
+
 /* Load-time quantiser: bf16 weights [n_rows, k_cols] (device, 16-byte
  * aligned) -> packed nibbles [n_rows, k_cols/2] and bf16 group scales
  * [n_rows, k_cols/group_size], the crate layout.  Replaces

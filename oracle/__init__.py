@@ -87,6 +87,7 @@ def _declare(L):
         "or_cpu_moe_layer": (None, [vp, sz, sz, sz, sz, i32, vp, sz, sz, vp, sz, vp, vp, sz, f32, vp]),
         "or_ffn_forward_sparse_axpy_f32_mode": (f32, [vp, sz, sz, sz, i32, i32, vp, vp, vp, vp, vp,
                                                       vp, f32, vp, vp]),
+        "or_ov_gemv": (None, [vp, vp, vp, sz, sz, sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -381,4 +382,15 @@ def cpu_moe_layer(x, experts, n_experts, shared, shared_inter, hidden, inter, gr
     lib().or_cpu_moe_layer(_p(x), T, hidden, inter, group, sdt, _p(experts), stride, n_experts,
                            None if sh is None else _p(sh), shared_inter, _p(ids), _p(weights), k,
                            threshold, _p(out))
+    return out
+
+
+def ov_gemv(packed, scale_f16_bits, act, n, k, gsize):
+    """gemv_offload.cpp:623-638: the CascadiaInt4Gemv op's scalar path, one
+    activation row; two's-complement nibbles, f16 scales, any even group."""
+    packed = _c(packed, np.uint8)
+    sc = _c(scale_f16_bits, np.uint16)
+    act = _c(act, np.float32)
+    out = np.empty(n, np.float32)
+    lib().or_ov_gemv(_p(packed), _p(sc), _p(act), n, k, gsize, _p(out))
     return out

@@ -715,3 +715,35 @@ float or_ffn_forward_sparse_axpy_f32_mode(const float *x, size_t hidden, size_t 
   free(act);
   return (float)na / (float)inter;
 }
+
+/* ------------------------------------------------------------------ */
+/* OpenVINO CascadiaInt4Gemv (cascadia-ov-genai-shim/cpp/gemv_offload.cpp) */
+/* ------------------------------------------------------------------ */
+
+/* The op's scalar evaluate path (gemv_offload.cpp:623-638) for one row of
+ * activations: packed [n, k/2], element 0 in the low nibble, each nibble a
+ * two's-complement int4 (sign-extended: (b << 4) >> 4 and b >> 4 of the int8
+ * byte, :630-632); f16 scales [n, k / gsize]; per group dot += lo * a[2j],
+ * dot += hi * a[2j + 1] in order, then acc += f32(scale) * dot. */
+void or_ov_gemv(const uint8_t *packed, const uint16_t *scale_f16, const float *act, size_t n,
+                size_t k, size_t gsize, float *out) {
+  const size_t groups = k / gsize;
+  for (size_t r = 0; r < n; r++) {
+    const uint8_t *wrow = packed + r * (k / 2);
+    float acc = 0.0f;
+    for (size_t gi = 0; gi < groups; gi++) {
+      const uint8_t *gw = wrow + gi * (gsize / 2);
+      const float *ga = act + gi * gsize;
+      float dot = 0.0f;
+      for (size_t j = 0; j < gsize / 2; j++) {
+        const uint8_t b = gw[j];
+        const int lo = (int)(int8_t)(uint8_t)(b << 4) >> 4;
+        const int hi = (int)(int8_t)b >> 4;
+        dot += (float)lo * ga[2 * j];
+        dot += (float)hi * ga[2 * j + 1];
+      }
+      acc += or_f16_to_f32(scale_f16[r * groups + gi]) * dot;
+    }
+    out[r] = acc;
+  }
+}

@@ -110,6 +110,8 @@ void or_transpose_requantize_down(const uint8_t *src_packed, const uint8_t *src_
 void or_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *scale_t_bits,
                             const float *scalars, const uint32_t *active, size_t n_active,
                             size_t inter, size_t hidden, float *y);
+void or_ov_gemv(const uint8_t *packed, const uint16_t *scale_f16, const float *act, size_t n,
+                size_t k, size_t gsize, float *out);
 float or_ffn_forward_sparse_axpy_f32_mode(const float *x, size_t hidden, size_t inter,
                                           size_t group, int scale_dtype, int order,
                                           const uint8_t *gate_p, const uint8_t *gate_s,

@@ -791,3 +791,44 @@ def test_np_requantize_matches_oracle(orc):
     got = np.stack([pt & 15, pt >> 4], -1).reshape(i, h).astype(np.int64) - 8
     assert np.array_equal(got, q)
     assert np.array_equal(st.view(np.uint16).reshape(i, h // 32), sb)
+
+
+# ----------------------------------------------------------------------------
+# f4: the OpenVINO CascadiaInt4Gemv format (gemv_offload.cpp:150-340, 623-638)
+# ----------------------------------------------------------------------------
+
+def test_ov_gemv_sign_extension_closed_form(orc):
+    """Two's-complement nibbles: byte 0x8F holds lo = 0xF -> -1 and hi = 0x8
+    -> -8 (the crate's offset form would read 7 and 0); with unit scales and a
+    one-hot activation the output is that code exactly."""
+    n, k, g = 2, 64, 32
+    packed = np.full((n, k // 2), 0x8F, np.uint8)
+    packed[1] = 0x70  # lo 0, hi 7
+    sc = np.full(n * (k // g), 0x3C00, np.uint16)  # f16 1.0
+    for col, want in ((0, (-1.0, 0.0)), (1, (-8.0, 7.0)), (34, (-1.0, 0.0)), (63, (-8.0, 7.0))):
+        a = np.zeros(k, np.float32)
+        a[col] = 1.0
+        assert tuple(orc.ov_gemv(packed, sc, a, n, k, g)) == want, col
+
+
+@pytest.mark.parametrize("g", [32, 64, 128, 48])
+def test_ov_gemv_is_crate_gemv_of_xored_bytes(orc, g):
+    """(x ^ 8) - 8 == (x ^ 8) - 8 with x ^ 8 the crate's offset nibble: the
+    OV bytes XOR 0x88 in the crate layout give the same products, so the
+    crate's GEMV over them (f16 scales) matches to f32 summation rounding;
+    and an f64 brute force of the two's-complement decode pins both."""
+    n, k = 24, 384
+    rng = np.random.default_rng(g)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    sc = orc.fill_scales(g, 3, n * (k // g), F16)
+    a = rng.normal(0, 1, k).astype(np.float32)
+    got = orc.ov_gemv(packed, sc, a, n, k, g)
+    lo = ((packed & 15).astype(np.int64) ^ 8) - 8
+    hi = ((packed >> 4).astype(np.int64) ^ 8) - 8
+    q = np.stack([lo, hi], -1).reshape(n, k)
+    s = np.repeat(np.frombuffer(sc.tobytes(), np.float16).astype(np.float64).reshape(n, k // g), g, 1)
+    want64 = (q * s) @ a.astype(np.float64)
+    assert np.allclose(got, want64, rtol=1e-5, atol=1e-5 * np.max(np.abs(want64)))
+    if g % 32 == 0:
+        crate = orc.gemv((packed ^ 0x88).reshape(-1), sc.view(np.uint8), a, n, k, g, F16)
+        assert np.allclose(got, crate, rtol=1e-5, atol=1e-5 * np.max(np.abs(want64)))
