@@ -660,6 +660,28 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
     rw *= 2;
   }
   if (rw > maxw) rw = maxw;
+  // Dense plans without a SwiGLU pair (the down projection, plain GEMMs): one
+  // workgroup per CU, from the fewest row groups per workgroup whose staging
+  // of its k-range stays within kDenseStageBytes, K split across workgroups as
+  // needed.  Measured on config 1's down projection (4096 x 14336, two
+  // activation planes) at 2, 4, 8 and 16 tokens: 11.0, 13.6, 13.8 and 17.8 us
+  // against 14.4, 16.0, 16.5 and 22.3 us for the rule above, whose fewer,
+  // fuller workgroups left half the CUs idle.
+  constexpr double kDenseStageBytes = 120.0 * 1024;
+  int ks_min = 0;
+  if (!sw && m_chunks <= 0 && !env_int("CASCADIA_INT4_SKINNY_RW", 1, 16) &&
+      !env_int("CASCADIA_INT4_SKINNY_KSPLIT", 1, 64)) {
+    for (int r = 1; r <= maxw && r <= units; r *= 2) {
+      const long per = (units + r - 1) / r * p.m_chunks;
+      const int ks = (int)(per >= d.num_cus ? 1 : (d.num_cus + per - 1) / per);
+      if (ks > kb_total) continue;
+      const double stage = (double)planes * p.act_rows * 256.0 * ((kb_total + ks - 1) / ks);
+      if (stage > kDenseStageBytes) continue;
+      rw = r;
+      ks_min = ks;
+      break;
+    }
+  }
   if (int v = env_int("CASCADIA_INT4_SKINNY_RW", 1, 16)) rw = v <= maxw ? v : maxw;
   p.rw = rw;
   p.row_blocks = (int)((units + rw - 1) / rw);
@@ -687,7 +709,7 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   };
   auto plan_k = [&](bool sliced) {
     KPlan q{1, kb_total, kb_total, 1};
-    for (int ks = ks_env ? ks_env : 1; ks <= kb_total; ++ks) {
+    for (int ks = ks_env ? ks_env : (ks_min ? ks_min : 1); ks <= kb_total; ++ks) {
       q.kper = (kb_total + ks - 1) / ks;
       q.ksplit = (kb_total + q.kper - 1) / q.kper;
       const long wgs = wgs0 * q.ksplit;
