@@ -36,7 +36,11 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // (-6 %) but lost 16 % at 64 tokens on config 4, whose skewed routing gives
 // its hot experts many rows -- so 16 from 9 tokens up.
 int moe_chunk_rows(int T, int per_expert_max) {
-  const int c = T <= 8 ? 8 : 16;
+  // override 1 .. 32 (a 32-row chunk is the most one pass of the two-plane
+  // down projection holds)
+  const char *e = getenv("CASCADIA_INT4_MOE_CHUNK_ROWS");
+  const int ev = e ? atoi(e) : 0;
+  const int c = ev >= 1 && ev <= 32 ? ev : T <= 8 ? 8 : 16;
   return per_expert_max < c ? per_expert_max : c;
 }
 

@@ -46,6 +46,7 @@
 //   A_XF32 / A_HILO: slots 0-7 = hi plane of tokens 0-7, slots 8-15 = lo plane
 //   (hi = f32 truncated to bf16, lo = bf16 of the exact remainder); the two
 //   halves of the MFMA result are added: y = D[hi] + D[lo].
+#include <stdio.h>
 #include <stdlib.h>
 
 #include "int4_common.hpp"
@@ -565,13 +566,16 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
 }
 
 // Split-K: add the ksplit partials of each row unit in split order, then the
-// epilogue.  One wave per row unit.
+// epilogue.  One wave per row unit and M-tile (blockIdx.z), so that large row
+// groups or M-tile counts still spread over many waves; the loads of four
+// splits are in flight before their (ordered) adds.
 template <int NT, int MT, bool SW>
 __global__ __launch_bounds__(1024) void splitk_reduce_kernel(KParams a, int ksplit) {
   constexpr int NI = MT * NT;
   const int lane = threadIdx.x & 63;
   const int rwi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tpm = amode_single_plane(a.amode) ? 16 : 8;
+  const int mt = blockIdx.z;
   int m0 = blockIdx.y * tpm * MT;
   int mcount = min(a.M - m0, tpm * MT);
   if (a.chunks) {
@@ -579,23 +583,30 @@ __global__ __launch_bounds__(1024) void splitk_reduce_kernel(KParams a, int kspl
     m0 = c.row0;
     mcount = min(c.count, tpm * MT);
   }
+  mcount -= mt * tpm;  // rows of this M-tile
   if (mcount <= 0) return;
   const size_t zstride = (size_t)gridDim.y * gridDim.x * a.rw * NI * 64;
-  const size_t base =
-      (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * a.rw + rwi) * NI * 64 + lane;
-  f32x4_t acc[MT][NT];
+  const size_t base = (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * a.rw + rwi) * NI * 64 +
+                      (size_t)mt * NT * 64 + lane;
+  f32x4_t acc[1][NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int nt = 0; nt < NT; ++nt) acc[0][nt] = a.part[base + nt * 64];
+  for (int z0 = 1; z0 < ksplit; z0 += 4) {
+    f32x4_t v[4][NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = a.part[base + (mt * NT + nt) * 64];
-  for (int z = 1; z < ksplit; ++z) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
-        acc[mt][nt] += a.part[z * zstride + base + (mt * NT + nt) * 64];
+        v[j][nt] = z0 + j < ksplit ? a.part[(size_t)(z0 + j) * zstride + base + nt * 64]
+                                   : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (z0 + j < ksplit) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[0][nt] += v[j][nt];
+      }
   }
-  epilogue<NT, MT, SW>(a, acc, blockIdx.x * a.rw + rwi, m0, mcount);
+  epilogue<NT, 1, SW>(a, acc, blockIdx.x * a.rw + rwi, m0 + mt * tpm, min(mcount, tpm));
 }
 
 // ---------------------------------------------------------------------------
@@ -613,6 +624,19 @@ int env_int(const char *name, int lo, int hi) {
 }
 
 size_t round16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+// Plan overrides: CASCADIA_INT4_SKINNY_{RW,KSPLIT,WAVES} for every plan,
+// CASCADIA_INT4_GROUPED_{RW,KSPLIT,WAVES} for grouped (MoE) plans only, taking
+// precedence there.
+int plan_env(const char *what, bool grouped, int lo, int hi) {
+  char name[64];
+  if (grouped) {
+    snprintf(name, sizeof name, "CASCADIA_INT4_GROUPED_%s", what);
+    if (int v = env_int(name, lo, hi)) return v;
+  }
+  snprintf(name, sizeof name, "CASCADIA_INT4_SKINNY_%s", what);
+  return env_int(name, lo, hi);
+}
 
 }  // namespace
 
@@ -669,8 +693,8 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   // fuller workgroups left half the CUs idle.
   constexpr double kDenseStageBytes = 120.0 * 1024;
   int ks_min = 0;
-  if (!sw && m_chunks <= 0 && !env_int("CASCADIA_INT4_SKINNY_RW", 1, 16) &&
-      !env_int("CASCADIA_INT4_SKINNY_KSPLIT", 1, 64)) {
+  const bool grouped = m_chunks > 0;
+  if (!sw && !grouped && !plan_env("RW", false, 1, 16) && !plan_env("KSPLIT", false, 1, 64)) {
     for (int r = 1; r <= maxw && r <= units; r *= 2) {
       const long per = (units + r - 1) / r * p.m_chunks;
       const int ks = (int)(per >= d.num_cus ? 1 : (d.num_cus + per - 1) / per);
@@ -682,7 +706,7 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
       break;
     }
   }
-  if (int v = env_int("CASCADIA_INT4_SKINNY_RW", 1, 16)) rw = v <= maxw ? v : maxw;
+  if (int v = plan_env("RW", grouped, 1, 16)) rw = v <= maxw ? v : maxw;
   p.rw = rw;
   p.row_blocks = (int)((units + rw - 1) / rw);
   const long wgs0 = (long)p.row_blocks * p.m_chunks;
@@ -695,8 +719,8 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
     const size_t st = round16(act) + sc;
     return st > red ? st : red;
   };
-  const int ks_env = env_int("CASCADIA_INT4_SKINNY_KSPLIT", 1, 64);
-  const int kw_env = env_int("CASCADIA_INT4_SKINNY_WAVES", 1, 16);
+  const int ks_env = plan_env("KSPLIT", grouped, 1, 64);
+  const int kw_env = plan_env("WAVES", grouped, 1, 16);
   // K decomposition.  Split K across workgroups when fewer than half the CUs
   // would get a workgroup (the reduce launch costs more than that), and --
   // unsliced -- also when the staging does not fit in LDS; or (sliced) stage
@@ -776,7 +800,7 @@ hipError_t launch_one(const KParams &k, const SkinnyPlan &p, hipStream_t st) {
     hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, false>), grid, block, p.lds_bytes, st, k);
   if (hipError_t e = hipGetLastError()) return e;
   if (p.ksplit > 1) {
-    dim3 g2(p.row_blocks, p.m_chunks, 1), b2(64 * p.rw, 1, 1);
+    dim3 g2(p.row_blocks, p.m_chunks, p.mt), b2(64 * p.rw, 1, 1);
     hipLaunchKernelGGL((splitk_reduce_kernel<NT, MT, SW>), g2, b2, 0, st, k, p.ksplit);
     return hipGetLastError();
   }
