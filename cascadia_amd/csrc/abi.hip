@@ -767,9 +767,10 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   uint16_t *lo = reinterpret_cast<uint16_t *>(W + m.ws.lo);
   uint16_t *y = reinterpret_cast<uint16_t *>(W + m.ws.y);
   void *part = W + m.ws.part;  // used only when a grouped GEMM splits K
-  // The shared expert depends only on x: it runs on the side stream, forked
-  // here and joined before the combine, so it fills the routed path's gaps.
-  // The guard enqueues the join on every return path once the fork is made.
+  // The shared expert depends only on x: unless it runs as a slot of the
+  // one-token launches, it runs on the side stream, forked below and joined
+  // before the combine, so it fills the routed path's gaps.  The guard
+  // enqueues the join on every return path once the fork is made.
   struct Join {
     hipStream_t st = nullptr;
     hipEvent_t ev = nullptr;
@@ -783,27 +784,6 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     }
     ~Join() { (void)wait(); }
   } join_guard;
-  float *sh = nullptr;
-  if (has_shared(L)) {
-    sh = reinterpret_cast<float *>(W + m.ws.shared);
-    hipStream_t side = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-    if (side_stream(dev, &side, &fork, &join) == CASCADIA_INT4_OK) {
-      join_guard.lk = std::unique_lock<std::mutex>(g_side_mu);
-      if (hipEventRecord(fork, st) != hipSuccess ||
-          hipStreamWaitEvent(side, fork, 0) != hipSuccess)
-        return CASCADIA_INT4_ERR_DEVICE;
-      const int rc = ffn_common(L->hidden, L->shared_inter, L->group_size, L->scale_dtype,
-                                &L->shared, x, true, T, sh, false, W + m.ws.shared_ws, side);
-      if (hipEventRecord(join, side) != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
-      join_guard.st = st;
-      join_guard.ev = join;
-      if (rc) return rc;
-    } else if (int rc = ffn_common(L->hidden, L->shared_inter, L->group_size, L->scale_dtype,
-                                   &L->shared, x, true, T, sh, false, W + m.ws.shared_ws, st)) {
-      return rc;  // no side stream (e.g. first call inside a stream capture): in order on st
-    }
-  }
   size_t off[6];
   expert_blob_sections(L->hidden, L->inter, L->group_size, L->tiling, off);
   const int G = (int)L->group_size;
@@ -828,9 +808,55 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   dn1.glog2 = glog2_of(G);
   dn1.tiled = (int)L->tiling;
   const bool fused1 = T == 1 && cai4::gemv_moe1_down_fused(H, I, G, k, d.num_cus);
-  if (T == 1 && L->tiling == CASCADIA_INT4_TILING_MFMA &&
+  const bool one_tok =
+      T == 1 && L->tiling == CASCADIA_INT4_TILING_MFMA &&
       cai4::gemv_moe1_supported(H, I, G, k, E, d.num_cus) &&
-      (fused1 || cai4::gemv_supported(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, 1, k))) {
+      (fused1 || cai4::gemv_supported(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, 1, k));
+  // One token whose shared expert has the routed experts' shape (and layout):
+  // its down runs as an always-on slot (f32 out) of the grouped down launch,
+  // its gate/up as a GEMV beside the routed one writing the spare hi / lo row
+  // (sh_mode 2), or as a slot of the routed gate/up launch too (1; its f32
+  // activations then set that launch's register budget);
+  // CASCADIA_INT4_MOE1_SHARED = 0 / 1 / 2 chooses, 0 = its own FFN beside.
+  int sh_mode = 0;
+  if (one_tok && !fused1 && has_shared(L) && L->shared_inter == L->inter &&
+      L->shared.tiling == CASCADIA_INT4_TILING_MFMA &&
+      cai4::gemv_supported(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, 1, k + 1)) {
+    const char *ev = getenv("CASCADIA_INT4_MOE1_SHARED");
+    sh_mode = ev ? atoi(ev) : 2;
+    if (sh_mode < 0 || sh_mode > 2) sh_mode = 2;
+  }
+  const bool sh_slot = sh_mode != 0;
+  float *sh = nullptr;
+  if (has_shared(L)) sh = reinterpret_cast<float *>(W + m.ws.shared);
+  if (has_shared(L) && sh_mode != 1) {
+    // the shared FFN (or, sh_mode 2, its gate/up into the spare hi / lo row)
+    auto shared_work = [&](hipStream_t on) {
+      if (sh_mode == 2)
+        return run_gemm(L->shared.gate_packed, L->shared.gate_scale, L->shared.up_packed,
+                        L->shared.up_scale, I, H, (int)L->group_size, (int)L->scale_dtype,
+                        (int)L->shared.tiling, x, nullptr, cai4::A_XF32, 1,
+                        hi + (size_t)k * I, lo + (size_t)k * I, cai4::EPI_SWIGLU_HILO, on);
+      return ffn_common(L->hidden, L->shared_inter, L->group_size, L->scale_dtype, &L->shared,
+                        x, true, T, sh, false, W + m.ws.shared_ws, on);
+    };
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    if (side_stream(dev, &side, &fork, &join) == CASCADIA_INT4_OK) {
+      join_guard.lk = std::unique_lock<std::mutex>(g_side_mu);
+      if (hipEventRecord(fork, st) != hipSuccess ||
+          hipStreamWaitEvent(side, fork, 0) != hipSuccess)
+        return CASCADIA_INT4_ERR_DEVICE;
+      const int rc = shared_work(side);
+      if (hipEventRecord(join, side) != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+      join_guard.st = st;
+      join_guard.ev = join;
+      if (rc) return rc;
+    } else if (int rc = shared_work(st)) {
+      return rc;  // no side stream (e.g. first call inside a stream capture): in order on st
+    }
+  }
+  if (one_tok) {
     // one token: routing inside the gate/up GEMV, the combine inside the down GEMV
     cai4::Moe1Args q{};
     q.gate = L->experts + off[0];
@@ -856,6 +882,13 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     q.I = I;
     q.G = G;
     q.sdt = (int)L->scale_dtype;
+    if (sh_slot) {
+      q.sh = sh_mode;
+      q.sh_gate = L->shared.gate_packed;
+      q.sh_gate_s = L->shared.gate_scale;
+      q.sh_up = L->shared.up_packed;
+      q.sh_up_s = L->shared.up_scale;
+    }
     if (R->mode != CASCADIA_INT4_ROUTE_IDS && !cai4::gemv_moe1_routes(r, E)) {
       // many experts: route in a launch of its own, the GEMV reads the result
       if (cai4::moe_route(r, 1, E, ids, wts, st) != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
@@ -877,7 +910,12 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       if (join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
       return hip_status(cai4::moe_finish(residual, sh, q.moe_sum, H, out, st));
     }
-    if (cai4::gemv_launch(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, k, st) != hipSuccess)
+    // the grouped down over the slots' one-row chunks (and the shared slot's,
+    // f32 into sh; its gate/up rows joined first), then the combine
+    if (sh_mode == 2 && join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
+    const cai4::GemvSharedSlot shs{L->shared.down_packed, L->shared.down_scale, sh};
+    if (cai4::gemv_launch(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, k + (sh_slot ? 1 : 0),
+                          st, sh_slot ? &shs : nullptr) != hipSuccess)
       return CASCADIA_INT4_ERR_DEVICE;
     if (join_guard.wait() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
     return hip_status(cai4::moe_combine(residual, sh, y, pos, wts, 1, H, k, out, st));

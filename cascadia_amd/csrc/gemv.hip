@@ -73,6 +73,14 @@ struct GvParams {
   int moe_partial;                 // MODE 2: out = sum_k w_k y_k only
   SkinnyChunk *chunks_out;         // MODE 1: [top_k] chunk table of one row per slot, or null
   int32_t *row_map_out;            // MODE 1: [top_k] (all token 0), or null
+  // the token's shared expert as an always-on slot (sh_slot = top_k; -1: none):
+  // MODE 1 workgroup row sh_slot runs its gate/up over the f32 x split into hi /
+  // lo planes (routed slots round x to bf16) and records chunk sh_slot with
+  // pad = 1; a grouped launch reads such a chunk's matrix at sh_w0 / sh_s0 and
+  // writes its f32 output row to sh_out (no bf16 rounding)
+  const uint8_t *sh_w0, *sh_s0, *sh_w1, *sh_s1;
+  float *sh_out;
+  int sh_slot;
 };
 
 // Slot kk of the one token: its expert, weight, position (kk, or -1 when
@@ -84,6 +92,15 @@ CAI4_DEV void moe1_record(const GvParams &a, int kk, int id, float w, bool keep)
   if (a.chunks_out) {
     a.chunks_out[kk] = SkinnyChunk{keep ? id : 0, kk, keep ? 1 : 0, 0};
     a.row_map_out[kk] = 0;
+  }
+}
+
+// The shared-expert slot's chunk (one row, flagged pad = 1) for the grouped
+// down launch.
+CAI4_DEV void moe1_record_shared(const GvParams &a) {
+  if (a.sh_slot >= 0 && a.chunks_out) {
+    a.chunks_out[a.sh_slot] = SkinnyChunk{0, a.sh_slot, 1, 1};
+    a.row_map_out[a.sh_slot] = 0;
   }
 }
 
@@ -106,7 +123,7 @@ constexpr int kGvWavesPerCu = 28;  // planned waves per CU
 // (step s then holds columns 32 s .. 32 s + 31) and the activations are read
 // to match; every group gets its own seed and scale.  MODE: GvMode; R: routing
 // registers per lane (GV_MOE_GATE_UP; 0: given ids and weights only).
-template <int NT, int AM, int RING, int KPWM, int GPB, int MODE, int R>
+template <int NT, int AM, int RING, int KPWM, int GPB, int MODE, int R, bool SHWG = false>
 CAI4_DEV void gemv_body(const GvParams &a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr bool two = AM == A_XF32 || AM == A_HILO;  // hi/lo planes
@@ -128,13 +145,16 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   const uint8_t *w0 = a.w0, *w1 = a.w1, *s0 = a.s0, *s1 = a.s1;
   const uint8_t *xp = static_cast<const uint8_t *>(a.x), *xp2 = static_cast<const uint8_t *>(a.x2);
   size_t orow = 0;
+  bool sh_chunk = false;  // grouped: this chunk is the shared-expert slot
   bool live = true;  // false: this wave's slot is skipped, all its loads read nothing
   const int nw = blockDim.x >> 6;
   float *red = reinterpret_cast<float *>(lds + (size_t)nw * wbytes);  // partials [nw - 1][NT][16]
   if constexpr (MODE == GV_MOE_GATE_UP) {
     const int k = a.top_k;
     int e;
-    if constexpr (R == 0) {  // given ids and weights (or another launch's routing)
+    if constexpr (SHWG) {  // the shared expert: always on, its own matrices
+      e = 0;
+    } else if constexpr (R == 0) {  // given ids and weights (or another launch's routing)
       const int kk = blockIdx.y;
       const int id = a.route.ids[kk];
       const float w = a.route.weights[kk];
@@ -146,6 +166,7 @@ CAI4_DEV void gemv_body(const GvParams &a) {
         const bool keep = !(lw < a.route.threshold) && li >= 0 && li < a.E;
         moe1_record(a, lane, li, lw, keep);
       }
+      if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0 && lane == k) moe1_record_shared(a);
     } else {  // every workgroup routes the token itself (wave 0), then broadcasts its slot
       int *bcast = reinterpret_cast<int *>(red + (nw - 1) * NT * 16);  // past the partials
       if (wave == 0) {
@@ -161,17 +182,25 @@ CAI4_DEV void gemv_body(const GvParams &a) {
         }
         const bool keep = !(w < a.route.threshold) && id >= 0 && id < a.E;
         if (blockIdx.x == 0 && blockIdx.y == 0 && lane < k) moe1_record(a, lane, id, w, keep);
+        if (blockIdx.x == 0 && blockIdx.y == 0 && lane == k) moe1_record_shared(a);
         if (lane == (int)blockIdx.y) *bcast = keep ? id : -1;
       }
       __syncthreads();
       e = *bcast;
     }
     if (e < 0) return;  // the whole workgroup
-    const size_t eo = (size_t)e * a.expert_stride;
-    w0 += eo;
-    s0 += eo;
-    w1 += eo;
-    s1 += eo;
+    if constexpr (SHWG) {
+      w0 = a.sh_w0;
+      s0 = a.sh_s0;
+      w1 = a.sh_w1;
+      s1 = a.sh_s1;
+    } else {
+      const size_t eo = (size_t)e * a.expert_stride;
+      w0 += eo;
+      s0 += eo;
+      w1 += eo;
+      s1 += eo;
+    }
     orow = (size_t)blockIdx.y * a.ldo;
   } else if constexpr (MODE == GV_MOE_DOWN) {
     live = a.pos[slot] >= 0;
@@ -183,12 +212,18 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   } else if (a.chunks) {
     const SkinnyChunk c = a.chunks[blockIdx.y];
     if (c.count == 0) return;  // the whole workgroup
-    const size_t eo = (size_t)c.expert * a.expert_stride;
-    w0 += eo;
-    s0 += eo;
-    if (NT == 2) {
-      w1 += eo;
-      s1 += eo;
+    if (NT == 1 && c.pad == 1 && a.sh_out) {  // the shared-expert slot: f32 out
+      w0 = a.sh_w0;
+      s0 = a.sh_s0;
+      sh_chunk = true;
+    } else {
+      const size_t eo = (size_t)c.expert * a.expert_stride;
+      w0 += eo;
+      s0 += eo;
+      if (NT == 2) {
+        w1 += eo;
+        s1 += eo;
+      }
     }
     const size_t xr = (size_t)(a.row_map ? a.row_map[c.row0] : c.row0) * a.ldx;
     xp += xr * (xf32 ? 4 : 2);
@@ -400,6 +435,8 @@ CAI4_DEV void gemv_body(const GvParams &a) {
       reinterpret_cast<uint16_t *>(a.out)[row] = (uint16_t)hb;
       reinterpret_cast<uint16_t *>(a.out2)[row] = (uint16_t)f32_to_bf16_rne(h - bitsf(hb << 16));
     }
+  } else if (sh_chunk) {
+    a.sh_out[r16] = y;
   } else if (a.epi == EPI_BF16) {
     reinterpret_cast<uint16_t *>(a.out)[row] = (uint16_t)f32_to_bf16_rne(y);
   } else {
@@ -422,10 +459,27 @@ constexpr int gv_waves_per_simd() {
   return two && NT == 2 ? 5 : 6;
 }
 
-template <int NT, int AM, int KPWM, int GPB, int MODE = GV_PLAIN, int R = 1>
-__global__ __launch_bounds__(1024) __attribute__((
-    amdgpu_waves_per_eu(gv_waves_per_simd<NT, AM, KPWM, GPB, MODE, R>()))) void gemv_kernel(GvParams a) {
-  gemv_body<NT, AM, NT == 2 ? kGvRing2 : kGvRing1, KPWM, GPB, MODE, R>(a);
+// SH (routed gate/up only): workgroup row a.sh_slot runs the shared expert's
+// body (f32 x as hi / lo planes); the kernel then takes the smaller register
+// budget of the two bodies.
+template <int NT, int AM, int KPWM, int GPB, int MODE, int R, bool SH>
+constexpr int gv_waves_per_simd_sh() {
+  constexpr int a = gv_waves_per_simd<NT, AM, KPWM, GPB, MODE, R>();
+  constexpr int b = gv_waves_per_simd<NT, A_XF32, KPWM, GPB, MODE, 0>();
+  return SH && b < a ? b : a;
+}
+
+template <int NT, int AM, int KPWM, int GPB, int MODE = GV_PLAIN, int R = 1, bool SH = false>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(
+    gv_waves_per_simd_sh<NT, AM, KPWM, GPB, MODE, R, SH>()))) void gemv_kernel(GvParams a) {
+  constexpr int RING = NT == 2 ? kGvRing2 : kGvRing1;
+  if constexpr (SH) {
+    if ((int)blockIdx.y == a.sh_slot) {  // uniform per workgroup
+      gemv_body<NT, A_XF32, RING, KPWM, GPB, MODE, 0, true>(a);
+      return;
+    }
+  }
+  gemv_body<NT, AM, RING, KPWM, GPB, MODE, R>(a);
 }
 
 }  // namespace
@@ -484,7 +538,7 @@ size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt, int gpb) {
 }
 
 hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int max_chunks,
-                       hipStream_t st) {
+                       hipStream_t st, const GemvSharedSlot *sh) {
   const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
   const int nch = a.chunks ? max_chunks : 1;
   const GemvPlan p = gemv_plan(a.N * nch, a.K, num_cus);
@@ -509,6 +563,12 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int
   k.expert_stride = a.expert_stride;
   k.ldx = a.ldx;
   k.ldo = a.ldo;
+  k.sh_slot = -1;
+  if (sh && a.chunks && !sw) {
+    k.sh_w0 = sh->w;
+    k.sh_s0 = sh->s;
+    k.sh_out = sh->out;
+  }
   const int gpb = gemv_gpb(a.G);
   const size_t lds = gemv_lds_bytes(p, amode, sw ? 2 : 1, gpb);
   const dim3 grid((a.N + 15) / 16, nch), block(64 * p.kw);
@@ -564,9 +624,13 @@ bool gemv_moe1_supported(int H, int I, int G, int top_k, int E, int num_cus) {
   if (!gpb || H % 128 || I % 128 || H % G || I % G) return false;
   if (top_k < 1 || top_k > kMoeMaxTopK || E < 1 || E > kMoeMaxExperts) return false;
   if ((long)I * top_k > (1L << 30)) return false;
-  const GemvPlan gu = gemv_plan(I * top_k, H, num_cus);
+  // with a shared-expert slot: top_k + 1 rows of two activation planes
+  const GemvPlan gu = gemv_plan(I * (top_k + 1), H, num_cus);
   if (gu.kw < 1 || gu.kw > 16 || gu.kpw > 8) return false;
-  return gemv_lds_bytes(gu, A_GATHER, 2, gpb) <= kGvMaxLds;
+  const GemvPlan gu0 = gemv_plan(I * top_k, H, num_cus);
+  if (gu0.kw < 1 || gu0.kw > 16 || gu0.kpw > 8) return false;
+  return gemv_lds_bytes(gu, A_XF32, 2, gpb) <= kGvMaxLds &&
+         gemv_lds_bytes(gu0, A_GATHER, 2, gpb) <= kGvMaxLds;
 }
 
 bool gemv_moe1_down_fused(int H, int I, int G, int top_k, int num_cus) {
@@ -580,7 +644,8 @@ bool gemv_moe1_down_fused(int H, int I, int G, int top_k, int num_cus) {
 
 hipError_t gemv_moe1_gate_up(const Moe1Args &m, int num_cus, hipStream_t st) {
   const int gpb = gemv_gpb(m.G);
-  const GemvPlan p = gemv_plan(m.I * m.top_k, m.H, num_cus);
+  const int rows = m.top_k + (m.sh == 1 ? 1 : 0);
+  const GemvPlan p = gemv_plan(m.I * rows, m.H, num_cus);
   GvParams k{};
   k.w0 = m.gate;
   k.s0 = m.gate_s;
@@ -608,10 +673,23 @@ hipError_t gemv_moe1_gate_up(const Moe1Args &m, int num_cus, hipStream_t st) {
   k.pos = m.pos;
   k.chunks_out = m.chunks;
   k.row_map_out = m.row_map;
-  const size_t lds = gemv_lds_bytes(p, A_GATHER, 2, gpb);
-  const dim3 grid((m.I + 15) / 16, m.top_k), block(64 * p.kw);
-#define CAI4_GVR(KP, GP, R) \
-  hipLaunchKernelGGL((gemv_kernel<2, A_GATHER, KP, GP, GV_MOE_GATE_UP, R>), grid, block, lds, st, k)
+  k.sh_slot = m.sh ? m.top_k : -1;
+  k.sh_w0 = m.sh_gate;
+  k.sh_s0 = m.sh_gate_s;
+  k.sh_w1 = m.sh_up;
+  k.sh_s1 = m.sh_up_s;
+  // the shared slot stages two activation planes
+  const size_t lds = gemv_lds_bytes(p, m.sh == 1 ? A_XF32 : A_GATHER, 2, gpb);
+  const dim3 grid((m.I + 15) / 16, rows), block(64 * p.kw);
+#define CAI4_GVR(KP, GP, R)                                                                   \
+  do {                                                                                        \
+    if (m.sh == 1)                                                                            \
+      hipLaunchKernelGGL((gemv_kernel<2, A_GATHER, KP, GP, GV_MOE_GATE_UP, R, true>), grid,   \
+                         block, lds, st, k);                                                  \
+    else                                                                                      \
+      hipLaunchKernelGGL((gemv_kernel<2, A_GATHER, KP, GP, GV_MOE_GATE_UP, R>), grid, block, \
+                         lds, st, k);                                                         \
+  } while (0)
 #define CAI4_GVR_E(KP, GP)                                    \
   do {                                                        \
     if (m.route.mode != ROUTE_IDS && m.E <= 256) CAI4_GVR(KP, GP, 4); \

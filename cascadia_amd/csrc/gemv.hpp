@@ -20,8 +20,14 @@ struct GemvPlan {
 bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int chunk_rows = 0,
                     int max_chunks = 0);
 GemvPlan gemv_plan(int N, int K, int num_cus);
+// The shared expert of one MoE token as an always-on slot of a grouped launch:
+// the chunk flagged pad = 1 reads its matrix w / s and writes f32 to out.
+struct GemvSharedSlot {
+  const uint8_t *w, *s;
+  float *out;
+};
 hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int max_chunks,
-                       hipStream_t st);
+                       hipStream_t st, const GemvSharedSlot *sh = nullptr);
 
 // One MoE token (T = 1) over MFMA-tiled experts, in two launches: the gate/up
 // of every slot (each workgroup recomputes the token's routing for up to 256
@@ -47,6 +53,12 @@ struct Moe1Args {
   SkinnyChunk *chunks;             // [top_k] one-row chunks for a grouped down launch, or null
   int32_t *row_map;                // [top_k], with chunks
   int H, I, G, sdt;
+  // the shared expert (its inter size I): sh = 1 runs its gate/up as slot
+  // top_k of this launch (rows hi / lo [top_k]); sh = 2 only records chunk
+  // top_k (pad = 1) for the grouped down, the rows coming from another launch;
+  // 0: none.  With sh, chunks / row_map hold top_k + 1 entries.
+  int sh;
+  const uint8_t *sh_gate, *sh_gate_s, *sh_up, *sh_up_s;
 };
 // Whether the gate/up launch routes in-kernel (else route must hold ids).
 inline bool gemv_moe1_routes(const MoeRouting &r, int E) { return r.mode != ROUTE_IDS && E <= 256; }

@@ -79,14 +79,16 @@ MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows
     o += align256(bytes);
     return at;
   };
+  // one spare row map entry, chunk and hi / lo row: a one-token layer's
+  // shared expert as an always-on slot
   w.ids = take(n * 4);
   w.weights = take(n * 4);
   w.pos = take(n * 4);
-  w.row_map = take(n * 4);
-  w.chunks = take((size_t)w.max_chunks * sizeof(SkinnyChunk));
+  w.row_map = take((n + 1) * 4);
+  w.chunks = take((size_t)(w.max_chunks + 1) * sizeof(SkinnyChunk));
   w.counts = take(16);
-  w.hi = take(n * I * 2);
-  w.lo = take(n * I * 2);
+  w.hi = take((n + 1) * I * 2);
+  w.lo = take((n + 1) * I * 2);
   w.y = take(n * H * 2);
   w.shared = take(shared_bytes);
   w.part = take(part_bytes);

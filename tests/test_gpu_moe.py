@@ -243,13 +243,24 @@ def test_moe_one_token_routing_launch(cl, orc, E, shared_inter, mode):
                 f"one token E={E} shared={shared_inter} mode={mode}")
 
 
-@pytest.mark.parametrize("E,h,i,g,mode", [(24, 7168, 2048, 32, 1), (260, 4608, 128, 128, 1)])
-def test_moe_one_token_wide_hidden(cl, orc, E, h, i, g, mode):
+@pytest.mark.parametrize("sh_mode", ["0", "1", "2"])
+@pytest.mark.parametrize("E,h,i,g,mode,si", [(24, 7168, 2048, 32, 1, 256), (260, 4608, 128, 128, 1, 256),
+                                             (24, 7168, 2048, 32, 1, 2048), (260, 4608, 128, 128, 1, 128)])
+def test_moe_one_token_wide_hidden(cl, orc, monkeypatch, E, h, i, g, mode, si, sh_mode):
     """One token with more 16-row output tiles than CUs (hidden > 4096): the
     gate/up launch leaves a chunk table of one row per slot, the grouped down
     and the combine kernel follow; config 4 dims (G32, shared expert) on a
-    24-expert subset, and 260 experts (routing in a launch of its own)."""
-    k, T, si = 8, 1, 256
+    24-expert subset, and 260 experts (routing in a launch of its own).  A
+    shared expert of the routed experts' inter size runs as an always-on slot
+    of both launches (f32 x as hi / lo planes, f32 out); another size runs as
+    its own FFN beside them.  CASCADIA_INT4_MOE1_SHARED picks how a shared
+    expert of the routed shape runs: 1 both halves as slots, 2 (default) the
+    gate/up as a GEMV beside the routed one and the down as a slot, 0 its own
+    FFN."""
+    if si != i and sh_mode != "2":
+        pytest.skip("the mode applies to a shared expert of the routed shape")
+    monkeypatch.setenv("CASCADIA_INT4_MOE1_SHARED", sh_mode)
+    k, T = 8, 1
     blob, shared, ex = build(cl, orc, E, h, i, g, F16, 33, si, True)
     logits = orc.fill_normal_f32(34, T, T * E).reshape(T, E)
     bias = orc.fill_normal_f32(35, 1, E) * np.float32(0.1)
@@ -261,7 +272,7 @@ def test_moe_one_token_wide_hidden(cl, orc, E, h, i, g, mode):
     cl.moe_forward(ex, xd, out, top_k=k, logits=dev(logits), bias=dev(bias), mode=mode,
                    scale=2.827, normalize=True, residual=xd, ids_out=ids_o, weights_out=w_o)
     check_layer(orc, host(out), x, blob, shared, si, E, h, i, g, F16, host(ids_o), host(w_o),
-                0.0, f"one token E={E} h={h}")
+                0.0, f"one token E={E} h={h} shared={si}")
 
 
 @pytest.mark.parametrize("T", [24, 70])
