@@ -4,6 +4,12 @@ weight-only matmul hot path, behind the C ABI of include/cascadia_int4.h.
 Importing the package loads libcascadia_int4_hip.so; it raises if the library
 was not built (``python cascadia_amd/build.py``).  There is no CPU fallback.
 """
+# torch first: its HIP runtime must be the process's one before the library
+# (linked against libamdhip64) is loaded, or a program importing this package
+# before torch would hold two HIP runtimes and device pointers from one would be
+# invalid in the other.
+import torch  # noqa: F401
+
 from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, CascadiaInt4Error,
                    LIB_PATH, SCALE_BF16, SCALE_F16, SIGNATURES, TILING_CRATE, TILING_MFMA, check,
                    lib)

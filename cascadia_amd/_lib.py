@@ -8,7 +8,9 @@ import ctypes as C
 import os
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "lib", "libcascadia_int4_hip.so")
+# the in-tree build; CASCADIA_INT4_LIB names another build of the same ABI
+LIB_PATH = os.environ.get("CASCADIA_INT4_LIB") or os.path.join(PKG, "lib",
+                                                               "libcascadia_int4_hip.so")
 
 OK = 0
 ERR_NULL = -1
