@@ -684,32 +684,54 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
     rw *= 2;
   }
   if (rw > maxw) rw = maxw;
-  // Dense plans without a SwiGLU pair (the down projection, plain GEMMs): one
-  // workgroup per CU, from the fewest row groups per workgroup whose staging
-  // of its k-range stays within kDenseStageBytes, K split across workgroups as
-  // needed.  Measured on config 1's down projection (4096 x 14336, two
-  // activation planes) at 2, 4, 8 and 16 tokens: 11.0, 13.6, 13.8 and 17.8 us
-  // against 14.4, 16.0, 16.5 and 22.3 us for the rule above, whose fewer,
-  // fuller workgroups left half the CUs idle.
-  constexpr double kDenseStageBytes = 120.0 * 1024;
-  int ks_min = 0;
+  // Dense plans: one round of workgroups, between 7/8 of the CUs and all of
+  // them, each staging at most kDenseStageBytes of its k-range, K split across
+  // workgroups as needed (dense_window).  Without a SwiGLU pair (the down
+  // projection, plain GEMMs) from the fewest row groups per workgroup; with
+  // one only when the rule above leaves CUs idle, and then the split with the
+  // fewest staged plus partial bytes.  Measured on config 1's down (4096 x
+  // 14336) at 2 / 4 / 8 / 16 tokens: 11.0 / 13.6 / 13.8 / 17.8 us against 14.4
+  // / 16.0 / 16.5 / 22.3 us; config 4's shared expert (f32 x, 7168 / 2048) at 8
+  // / 32 / 64 tokens: gate/up 13.1 / 19.9 / 27.9 us against 15.2 / 26.8 / 44.2,
+  // down 8.3 / 14.3 / 21.0 against 9.5 / 20.5 / 27.3.
   const bool grouped = m_chunks > 0;
-  if (!sw && !grouped && !plan_env("RW", false, 1, 16) && !plan_env("KSPLIT", false, 1, 64)) {
+  int ks_min = 0;
+  const bool dense_auto =
+      !grouped && !plan_env("RW", false, 1, 16) && !plan_env("KSPLIT", false, 1, 64);
+  auto dense_window = [&](bool fewest_rows, int *rw_out, int *ks_out) {
+    constexpr double kDenseStageBytes = 132.0 * 1024;
+    const long lo = (long)d.num_cus * 7 / 8, hi = d.num_cus;
+    double best = -1.0;
     for (int r = 1; r <= maxw && r <= units; r *= 2) {
       const long per = (units + r - 1) / r * p.m_chunks;
-      const int ks = (int)(per >= d.num_cus ? 1 : (d.num_cus + per - 1) / per);
-      if (ks > kb_total) continue;
-      const double stage = (double)planes * p.act_rows * 256.0 * ((kb_total + ks - 1) / ks);
+      const int ks = (int)(hi / per);  // the most splits that stay in one round
+      if (ks < 1 || per * ks < lo || ks > kb_total) continue;
+      const int kper = (kb_total + ks - 1) / ks;
+      const double stage = (double)planes * p.act_rows * 256.0 * kper;
       if (stage > kDenseStageBytes) continue;
+      // bytes beyond the weights: staged activations, split-K partials written and read
+      const double extra = stage * per * ks +
+                           (ks > 1 ? 2.0 * ks * per * r * mt * p.nt * 1024.0 : 0.0);
+      if (best < 0 || (!fewest_rows && extra < best)) {
+        best = extra;
+        *rw_out = r;
+        *ks_out = ks;
+        if (fewest_rows) break;
+      }
+    }
+    return best >= 0;
+  };
+  if (dense_auto && !sw) {
+    int r, ks;
+    if (dense_window(true, &r, &ks)) {
       rw = r;
       ks_min = ks;
-      break;
     }
   }
   if (int v = plan_env("RW", grouped, 1, 16)) rw = v <= maxw ? v : maxw;
   p.rw = rw;
   p.row_blocks = (int)((units + rw - 1) / rw);
-  const long wgs0 = (long)p.row_blocks * p.m_chunks;
+  long wgs0 = (long)p.row_blocks * p.m_chunks;
   auto lds_need = [&](int kper, int kw) {
     const size_t stride = (size_t)kper * 256 + 16;
     const size_t act = (size_t)planes * p.act_rows * stride;
@@ -765,6 +787,18 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   // tokens: 7 %) the split ran faster.
   KPlan q = plan_k(false);
   if (2.0 * partials(q) > 0.2 * wbytes) q = plan_k(true);
+  if (dense_auto && sw && (long)q.ksplit * wgs0 < (long)d.num_cus * 7 / 8) {
+    int r, ks;
+    if (dense_window(false, &r, &ks)) {
+      rw = r;
+      p.rw = rw;
+      p.row_blocks = (int)((units + rw - 1) / rw);
+      wgs0 = (long)p.row_blocks * p.m_chunks;
+      ks_min = ks;
+      q = plan_k(false);
+      if (2.0 * partials(q) > 0.2 * wbytes) q = plan_k(true);
+    }
+  }
   const int ksplit = q.ksplit, kper = q.kper, kslice = q.kslice, kw = q.kw;
   p.ksplit = ksplit;
   p.kper = kper;
