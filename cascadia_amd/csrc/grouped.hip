@@ -271,9 +271,7 @@ CAI4_DEV void gg_stage(uint8_t *cur, uint8_t *nxt2, const GgLd &d, int kb, int K
 template <int MS, int NT, int WM, int WN, int GPK, bool HILO, bool SW>
 __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
   using P = Gg<MS, NT, WM, WN, GPK, HILO, SW>;
-  __shared__ __attribute__((aligned(16))) uint8_t st0[P::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t st1[P::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t st2[P::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t stages[3 * P::BYTES];
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave % WM, wn = wave / WM;
   // this workgroup's rows
@@ -327,15 +325,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
 
   const int kb0 = blockIdx.z * a.kper, KE = min(KB, kb0 + a.kper);
 #pragma unroll
-  for (int l = 0; l < P::LOADS; ++l) gg_load<P, GPK, SW>(l, st0, d, kb0);
+  for (int l = 0; l < P::LOADS; ++l) gg_load<P, GPK, SW>(l, stages, d, kb0);
   if (kb0 + 1 < KE) {
 #pragma unroll
-    for (int l = 0; l < P::LOADS; ++l) gg_load<P, GPK, SW>(l, st1, d, kb0 + 1);
+    for (int l = 0; l < P::LOADS; ++l) gg_load<P, GPK, SW>(l, stages + P::BYTES, d, kb0 + 1);
   }
-  for (int kb = kb0; kb < KE; kb += 3) {
-    gg_stage<P, MS, NT, GPK, HILO, SW>(st0, st2, d, kb, KE, wm, wn, a.sdt, mt_live, acc);
-    gg_stage<P, MS, NT, GPK, HILO, SW>(st1, st0, d, kb + 1, KE, wm, wn, a.sdt, mt_live, acc);
-    gg_stage<P, MS, NT, GPK, HILO, SW>(st2, st1, d, kb + 2, KE, wm, wn, a.sdt, mt_live, acc);
+  // one stage per iteration, not unrolled: the stage buffers rotate at run
+  // time, so the compiler cannot hoist one stage's work into another's
+  int cur = 0;
+#pragma unroll 1
+  for (int kb = kb0; kb < KE; ++kb) {
+    const int nx2 = cur == 0 ? 2 : cur - 1;  // (cur + 2) % 3
+    gg_stage<P, MS, NT, GPK, HILO, SW>(stages + cur * P::BYTES, stages + nx2 * P::BYTES, d, kb,
+                                       KE, wm, wn, a.sdt, mt_live, acc);
+    cur = cur == 2 ? 0 : cur + 1;
   }
 
   // epilogue: D lane l holds column l % 16 and rows 4 (l / 16) + v
