@@ -357,7 +357,7 @@ def ffn_forward_sparse_axpy_f32_mode(x_f32, hidden, intermediate, gate_packed, g
     _expect(_nbytes(down_scale_t_bits) == intermediate * (hidden // 32) * 2,
             "down_scale_t_bits length")
     T = x_f32.numel() // hidden
-    _expect(x_f32.numel() == T * hidden and out_f32.numel() == T * hidden and T >= 1,
+    _expect(x_f32.numel() == T * hidden and out_f32.numel() == T * hidden,
             "x and out must be [n_tokens, hidden]")
     thr, tau = 0, 0.0
     if isinstance(mode, torch.Tensor):

@@ -352,8 +352,8 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
                const cascadia_int4_expert *e, const void *x, bool x_f32, uint32_t n_tokens,
                void *out, bool out_bf16, void *workspace, hipStream_t st) {
   if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
-  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (!aligned(x, 16)) return CASCADIA_INT4_ERR_ARG;
   int dev;
   if (int rc = current_device(&dev)) return rc;
@@ -429,8 +429,8 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
                   float tau, const float *thr, void *out, bool out_bf16, uint32_t *counts,
                   void *workspace, hipStream_t st) {
   if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
-  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (n_tokens > 65535 || !aligned(x, 16) || (thr && !aligned(thr, 4)) ||
       (counts && !aligned(counts, 4)) || (workspace && !aligned(workspace, 16)))
     return CASCADIA_INT4_ERR_ARG;
@@ -503,8 +503,8 @@ int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
              const float *thr, float *out, uint32_t *counts_out, void *workspace,
              hipStream_t st) {
   if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
-  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (hidden % 32 || n_tokens > 65535 || !aligned(x, 16) || !aligned(out, 16) ||
       (thr && !aligned(thr, 4)) || (counts_out && !aligned(counts_out, 4)) ||
       (workspace && !aligned(workspace, 16)))
@@ -1270,8 +1270,8 @@ int cascadia_int4_expert_forward_noalloc(uint32_t hidden, uint32_t inter, uint32
                                          const uint16_t *x_bf16, uint32_t n_tokens,
                                          uint16_t *out_bf16, void *stream) {
   if (int rc = check_expert(hidden, inter, group_size, scale_dtype, expert)) return rc;
-  if (!x_bf16 || !out_bf16) return CASCADIA_INT4_ERR_NULL;
   if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (!x_bf16 || !out_bf16) return CASCADIA_INT4_ERR_NULL;
   int dev;
   if (int rc = current_device(&dev)) return rc;
   const FfnWorkspace need = ffn_workspace(dev, hidden, inter, group_size, n_tokens, false);
@@ -1369,8 +1369,8 @@ int cascadia_int4_expert_forward_sparse(uint32_t hidden, uint32_t inter, uint32_
 
 int cascadia_int4_ov_to_crate(const uint8_t *packed_ov, size_t n_bytes, uint8_t *packed_crate,
                               void *stream) {
-  if (!packed_ov || !packed_crate) return CASCADIA_INT4_ERR_NULL;
   if (n_bytes == 0) return CASCADIA_INT4_OK;
+  if (!packed_ov || !packed_crate) return CASCADIA_INT4_ERR_NULL;
   if (!aligned(packed_ov, 4) || !aligned(packed_crate, 4)) return CASCADIA_INT4_ERR_ARG;
   return hip_status(cai4::ov_to_crate(packed_ov, n_bytes, packed_crate, (hipStream_t)stream));
 }
@@ -1473,8 +1473,8 @@ int cascadia_int4_gate_up_silu(uint32_t hidden, uint32_t inter, uint32_t group_s
                                const void *x, uint32_t x_is_f32, uint32_t n_tokens,
                                float *inter_out, void *stream) {
   if (int rc = check_expert(hidden, inter, group_size, scale_dtype, expert)) return rc;
-  if (!x || !inter_out) return CASCADIA_INT4_ERR_NULL;
   if (n_tokens == 0) return CASCADIA_INT4_OK;
+  if (!x || !inter_out) return CASCADIA_INT4_ERR_NULL;
   if (!aligned(x, 16) || !aligned(inter_out, 4)) return CASCADIA_INT4_ERR_ARG;
   return run_gemm(expert->gate_packed, expert->gate_scale, expert->up_packed, expert->up_scale,
                   (int)inter, (int)hidden, (int)group_size, (int)scale_dtype,

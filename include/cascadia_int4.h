@@ -18,6 +18,11 @@
  *     and return without waiting; outputs are complete once the stream is
  *     synchronised (cascadia_int4_synchronize).  The crate's calls are
  *     synchronous; a caller that needs that calls cascadia_int4_synchronize.
+ *   - A call over zero token rows (n_tokens == 0, n_active == 0,
+ *     n_bytes == 0) reads and writes nothing and returns CASCADIA_INT4_OK;
+ *     the buffers whose length is that count may then be NULL.  The exceptions follow the crate's asserts:
+ *     the seq-major GEMMs (seq >= 1, kernel_avx512_multi.rs:80) and
+ *     cascadia_int4_moe_forward return CASCADIA_INT4_ERR_ARG for zero rows.
  *   - Outputs are fully overwritten, as in the crate.  Calls are reentrant
  *     for distinct output buffers; a shared workspace (workspace == NULL, the
  *     library's own) makes concurrent calls on different streams race.

@@ -376,7 +376,7 @@ float or_expert_forward_sparse_mode(const uint16_t *x_bf16, size_t hidden, size_
                       out_bf16);
     return 1.0f;
   }
-  float *x = (float *)malloc(hidden * sizeof(float));
+  float *x = (float *)calloc(hidden, sizeof(float));
   float *o = (float *)malloc(hidden * sizeof(float));
   for (size_t i = 0; i < hidden; i++) x[i] = or_bf16_to_f32(x_bf16[i]);
   float frac = or_ffn_forward_f32_mode(x, hidden, inter, group, scale_dtype, order,

@@ -97,6 +97,40 @@ def test_argument_errors_before_device_work(cl):
     assert L.cascadia_int4_moe_workspace_bytes(C.byref(layer(n_experts=0)), 8, 1) == 0
 
 
+def test_zero_rows_return_ok_before_device_work(cl):
+    """Zero token rows read and write nothing: OK with NULL row buffers, no
+    HIP call made (this runs without a device).  The weights are still
+    validated; the seq-major GEMMs keep the crate's seq >= 1 assert
+    (kernel_avx512_multi.rs:80)."""
+    L = cl.lib()
+    e = cl._lib.Expert()
+    assert L.cascadia_int4_expert_from_flat(1 << 20, 64, 32, 32, C.byref(e)) == 0
+    OK, NUL = 0, cl._lib.ERR_NULL
+    assert L.cascadia_int4_expert_forward_device(64, 32, 32, 0, C.byref(e), None, 0, None, None,
+                                                 None) == OK
+    assert L.cascadia_int4_expert_forward_noalloc(64, 32, 32, 0, C.byref(e), None, 0, None,
+                                                  None) == OK
+    assert L.cascadia_int4_gate_up_silu(64, 32, 32, 0, C.byref(e), None, 1, 0, None, None) == OK
+    assert L.cascadia_int4_ffn_forward_sparse_f32(64, 32, 32, 0, C.byref(e), None, 0, 0.3, None,
+                                                  None, None, None, None) == OK
+    assert L.cascadia_int4_expert_forward_sparse(64, 32, 32, 0, C.byref(e), None, 0, 0.3, None,
+                                                 None, None, None, None) == OK
+    assert L.cascadia_int4_ffn_forward_sparse_axpy_f32(64, 32, 32, 0, C.byref(e), None, 0, 0.3,
+                                                       None, None, None, None, None) == OK
+    assert L.cascadia_int4_dequant_axpy_active(16, 16, 16, None, 0, 32, 64, 16, None, None) == OK
+    assert L.cascadia_int4_ov_to_crate(None, 0, None, None) == OK
+    # weights are still checked, and one row needs its buffers
+    assert L.cascadia_int4_expert_forward_device(64, 32, 32, 0, None, None, 0, None, None,
+                                                 None) == NUL
+    assert L.cascadia_int4_expert_forward_device(64, 32, 48, 0, C.byref(e), None, 0, None, None,
+                                                 None) == cl._lib.ERR_ARG
+    assert L.cascadia_int4_expert_forward_device(64, 32, 32, 0, C.byref(e), None, 1, None, None,
+                                                 None) == NUL
+    lay = cl._lib.Layout(64, 128, 32, 0)
+    assert L.cascadia_int4_dequant_gemm_multi(C.byref(lay), 16, 16, 16, 0, 16,
+                                              None) == cl._lib.ERR_ARG
+
+
 def test_python_mirror_rejects_host_tensors(cl):
     import torch
 

@@ -234,3 +234,32 @@ def test_axpy_ffn_rows_and_per_channel(cl, orc):
                                                    thresholds=thr)
         assert f3[t] == wf
         assert_f32_close(host(o3)[t], want, f"per-channel row {t}")
+
+
+def test_zero_token_rows(cl, orc):
+    """Zero token rows: the crate's forwards loop over no rows and return an
+    empty output (kernel.rs:75-136, ffn_sparsity.rs:438-538 iterate over
+    x.len() / hidden rows).  Every FFN entry point returns OK without reading
+    or writing, even with the NULL buffers of empty tensors, and the sparse
+    forms report no fractions."""
+    h, i, g = 512, 256, 32
+    flat = make_expert(orc, h, i, g, BF16, 12)
+    W0 = cl.ExpertWeights(dev(flat), h, i, g, BF16)
+    pt, st = cl.transpose_requantize_down(W0.down_packed_bytes(), W0.down_scale_bits(), h, i,
+                                          group_size=g, scale_dtype=BF16)
+    xb = torch.empty((0, h), dtype=torch.int16, device="cuda")
+    xf = torch.empty((0, h), dtype=torch.float32, device="cuda")
+    ob = torch.empty((0, h), dtype=torch.int16, device="cuda")
+    of = torch.empty((0, h), dtype=torch.float32, device="cuda")
+    inter = torch.empty((0, i), dtype=torch.float32, device="cuda")
+    for W in (W0, W0.tiled()):
+        kw = dict(group_size=g, scale_dtype=BF16,
+                  tiling=cl.TILING_MFMA if W is not W0 else cl.TILING_CRATE)
+        cl.expert_forward(xb, *W.slices(), ob, **kw)
+        cl.gate_up_silu(xf, *W.slices()[:4], inter, **kw)
+        assert cl.expert_forward_sparse(xb, *W.slices(), ob, 0.3, **kw) == []
+        assert cl.ffn_forward_sparse_f32(xf, h, i, *W.slices(), of, 0.3, **kw) == []
+        assert cl.ffn_forward_sparse_f32(xf, h, i, *W.slices(), of, 0.0, **kw) == []
+        assert cl.ffn_forward_sparse_axpy_f32(xf, h, i, *W.slices()[:4], pt, st, of, 0.3,
+                                              **kw) == []
+    torch.cuda.synchronize()
