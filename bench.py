@@ -557,7 +557,8 @@ def f_rows(cl, torch, sdt, copies):
                                    "bytes_per_step": b, "copies": ncs}
     del SH
     # the activation-sparse expert (tau > 0, ffn_sparsity.rs:756-867) at one
-    # token: gate and down in full, up for the active rows only.  Called
+    # token: algorithmic bytes gate and down in full, up for the active rows
+    # (this path reads up in full too: the fused gate/up GEMV).  Called
     # through the C entry point with no count output, so it captures.
     xs1 = cl.fill_normal(torch.empty(h, dtype=torch.bfloat16, device="cuda"), 0, 23)
     os1 = torch.empty(h, dtype=torch.bfloat16, device="cuda")
@@ -590,6 +591,14 @@ def f_rows(cl, torch, sdt, copies):
     src = cl.ExpertWeights(copies.crate[0], h, i, g, sdt)
     ptc, stc = cl.transpose_requantize_down(src.down_packed_bytes(), src.down_scale_bits(), h, i,
                                             group_size=g, scale_dtype=sdt)
+    # one transposed down per weight copy, so that the active rows rotate too
+    # (synthetic codes and bf16 scales of the transposed shape; the first is
+    # copy 0's true transpose, used for the active fraction)
+    PTS = [(ptc, stc)] + [
+        (cl.fill_bytes(torch.empty(i * h // 2, dtype=torch.uint8, device="cuda"), 2, 600 + c),
+         cl.fill_scales(torch.empty(i * (h // 32) * 2, dtype=torch.uint8, device="cuda"), 2,
+                        700 + c, cl.SCALE_BF16))
+        for c in range(1, nc)]
     xf1 = xs1.float()
     of1 = torch.empty(h, dtype=torch.float32, device="cuda")
     wsx = torch.empty(cl.ffn_sparse_axpy_workspace_bytes(h, i, 1, g), dtype=torch.uint8,
@@ -602,7 +611,8 @@ def f_rows(cl, torch, sdt, copies):
                                             workspace=wsx, tiling=cl.TILING_MFMA)
         exa = [cl._lib.Expert(*(t.data_ptr() for t in (W.gate_packed_bytes(), W.gate_scale_bits(),
                                                         W.up_packed_bytes(), W.up_scale_bits())),
-                              ptc.data_ptr(), stc.data_ptr(), cl.TILING_MFMA) for W in copies.w]
+                              PTS[c][0].data_ptr(), PTS[c][1].data_ptr(), cl.TILING_MFMA)
+               for c, W in enumerate(copies.w)]
 
         def axffn(r, tau=tau):
             cl.check("cascadia_int4_ffn_forward_sparse_axpy_f32",
@@ -617,13 +627,18 @@ def f_rows(cl, torch, sdt, copies):
         t = ev / steps
         mat = i * h // 2 + i * (h // g) * 2
         na = int(round(fr * i))
+        # algorithmic: the crate's reads (gate, the active up and transposed-down
+        # rows); read: this path's (gate and up in full -- the fused GEMV)
         b = mat + na * (h // 2 + (h // g) * 2) + na * (h // 2 + (h // 32) * 2) + h * 4 * 2
+        rd = 2 * mat + na * (h // 2 + (h // 32) * 2) + h * 4 * 2
         res[f"sparse_axpy_ffn_M1_tau{tau}"] = {"us_per_call": round(t * 1e6, 2),
                                                "active_frac": round(fr, 4),
                                                "GB/s": round(b / t / 1e9, 1),
                                                "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
-                                               "note": "gate copies rotate; one transposed down"}
-    del ptc, stc, wsx
+                                               "bytes_read": rd,
+                                               "read_GB/s": round(rd / t / 1e9, 1),
+                                               "note": "every copy rotates, transposed downs too"}
+    del ptc, stc, wsx, PTS
     # the AXPY form of the sparse down (ffn_axpy.rs:82-160): config 1's down
     # transposed to [inter, hidden], 13.4 % of the rows active (what tau 0.3
     # selects above), over rotating copies larger than 2x the Infinity Cache

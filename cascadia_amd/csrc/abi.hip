@@ -389,11 +389,20 @@ int ffn_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Workspace of the activation-sparse FFN: gate output, SiLU and the
-// intermediate ([n_tokens, inter] each), two cells per token, then split-K
-// partials of the largest of its GEMMs; at least what the dense branch needs.
+// Max-|silu| slot words of n_tokens tokens: the one-token GEMV writes one per
+// 16-row tile, sparse_slots one per 256 lanes of each token.
+size_t sparse_slot_bytes(uint32_t inter, uint32_t n_tokens) {
+  const size_t a = (size_t)cai4::sparse_slots_per_token((int)inter, true);
+  const size_t b = (size_t)n_tokens * cai4::sparse_slots_per_token((int)inter, false);
+  return align256((a > b ? a : b) * 4);
+}
+
+// Workspace of the activation-sparse FFN (GEMV form): gate, up and the
+// intermediate ([n_tokens, inter] f32 each), the slots, the groups' active
+// counts, then split-K partials of the largest of its GEMMs; at least what the
+// dense branch needs.
 struct SparseWorkspace {
-  size_t lanes, counts, partials, total;
+  size_t lanes, slots, cnt, partials, total;
 };
 SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint32_t group,
                                  uint32_t n_tokens) {
@@ -401,9 +410,9 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
   size_t part = 0;
   const cai4::SkinnyPlan plans[4] = {
       cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_XF32,
-                        cai4::EPI_F32, d),
+                        cai4::EPI_PAIR_F32, d),
       cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_BF16,
-                        cai4::EPI_F32, d),
+                        cai4::EPI_PAIR_F32, d),
       cai4::skinny_plan((int)hidden, (int)inter, (int)group, (int)n_tokens, cai4::A_XF32,
                         cai4::EPI_F32, d),
       cai4::skinny_plan((int)hidden, (int)inter, (int)group, (int)n_tokens, cai4::A_XF32,
@@ -411,9 +420,10 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
   for (const cai4::SkinnyPlan &p : plans) part = p.partial_bytes > part ? p.partial_bytes : part;
   SparseWorkspace w;
   w.lanes = align256((size_t)n_tokens * inter * 4);
-  w.counts = align256((size_t)n_tokens * 8);  // two cells per token
+  w.slots = sparse_slot_bytes(inter, n_tokens);
+  w.cnt = align256((size_t)n_tokens * cai4::sparse_groups((int)inter) * 4);
   w.partials = part;
-  w.total = 3 * w.lanes + w.counts + part;
+  w.total = 3 * w.lanes + w.slots + w.cnt + part;
   const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group, n_tokens, true);
   const FfnWorkspace b = ffn_workspace(dev, hidden, inter, group, n_tokens, false);
   const size_t dense = f.total() > b.total() ? f.total() : b.total();
@@ -421,9 +431,50 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
   return w;
 }
 
+// The gate and up GEMMs of a sparse form, f32 out (not combined), with the
+// mask's max-|silu| slots: one fused gate/up GEMV whose epilogue writes them
+// when it serves the shape, else the skinny kernel's gate/up pair and
+// sparse_slots.  *n_slots: slot words per token.
+int sparse_gate_up(const cascadia_int4_expert *e, uint32_t hidden, uint32_t inter,
+                   uint32_t group, uint32_t sdt, const void *x, int amode, uint32_t n_tokens,
+                   float *gate, float *up, const float *thr, bool stable, uint32_t *slots,
+                   int *n_slots, void *part, bool may_alloc, hipStream_t st) {
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const cai4::SkinnyDevice d = device_props(dev);
+  cai4::SkinnyArgs g{};
+  g.w0 = e->gate_packed;
+  g.s0 = e->gate_scale;
+  g.w1 = e->up_packed;
+  g.s1 = e->up_scale;
+  g.x = x;
+  g.out = gate;
+  g.out2 = up;
+  g.N = (int)inter;
+  g.K = (int)hidden;
+  g.G = (int)group;
+  g.M = (int)n_tokens;
+  g.sdt = (int)sdt;
+  g.tiled = (int)e->tiling;
+  g.slots = slots;
+  g.thr = thr;
+  g.silu_slot = stable ? 2 : 1;
+  if (n_tokens == 1 && cai4::gemv_supported(g, amode, cai4::EPI_SWIGLU, d.num_cus)) {
+    *n_slots = cai4::sparse_slots_per_token((int)inter, true);
+    return hip_status(cai4::gemv_launch(g, amode, cai4::EPI_SWIGLU, d.num_cus, 0, st));
+  }
+  int rc = run_gemm(e->gate_packed, e->gate_scale, e->up_packed, e->up_scale, (int)inter,
+                    (int)hidden, (int)group, (int)sdt, (int)e->tiling, x, nullptr, amode,
+                    (int)n_tokens, gate, up, cai4::EPI_PAIR_F32, st, part, may_alloc);
+  if (rc) return rc;
+  *n_slots = cai4::sparse_slots_per_token((int)inter, false);
+  return hip_status(cai4::sparse_slots(gate, (int)inter, (int)n_tokens, thr, stable, slots, st));
+}
+
 // ffn_forward_sparse_f32_mode / expert_forward_sparse_mode
 // (ffn_sparsity.rs:438-538, 756-867): thresholds == nullptr is the global
-// tau, dense (the ordinary FFN) when tau <= 0.
+// tau, dense (the ordinary FFN) when tau <= 0.  Gate/up GEMM with the slots ->
+// the mask and the intermediate -> the down GEMM over it.
 int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
                   const cascadia_int4_expert *e, const void *x, bool x_f32, uint32_t n_tokens,
                   float tau, const float *thr, void *out, bool out_bf16, uint32_t *counts,
@@ -453,51 +504,68 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   }
   uint8_t *b = static_cast<uint8_t *>(ws);
   float *gate = reinterpret_cast<float *>(b);
-  float *sg = reinterpret_cast<float *>(b + w.lanes);
+  float *upv = reinterpret_cast<float *>(b + w.lanes);
   float *mid = reinterpret_cast<float *>(b + 2 * w.lanes);
-  uint32_t *cells = reinterpret_cast<uint32_t *>(b + 3 * w.lanes);
-  void *part = w.partials ? b + 3 * w.lanes + w.counts : nullptr;
-  int rc = run_gemm(e->gate_packed, e->gate_scale, nullptr, nullptr, (int)inter, (int)hidden,
-                    (int)group, (int)sdt, (int)e->tiling, x, nullptr, amode, (int)n_tokens, gate,
-                    nullptr, cai4::EPI_F32, st, part);
+  uint32_t *slots = reinterpret_cast<uint32_t *>(b + 3 * w.lanes);
+  uint32_t *cnt = reinterpret_cast<uint32_t *>(b + 3 * w.lanes + w.slots);
+  void *part = w.partials ? b + 3 * w.lanes + w.slots + w.cnt : nullptr;
+  int n_slots = 0;
+  int rc = sparse_gate_up(e, hidden, inter, group, sdt, x, amode, n_tokens, gate, upv, thr, true,
+                          slots, &n_slots, part, true, st);
   if (rc) return rc;
-  if ((rc = hip_status(cai4::sparse_ffn_mid(e->up_packed, e->up_scale, (int)inter, (int)hidden,
-                                            (int)group, (int)sdt, (int)e->tiling, x, x_f32,
-                                            (int)n_tokens, gate, tau, thr, sg, cells, mid, counts,
-                                            st))))
+  cai4::SparseMaskArgs m{};
+  m.gate = gate;
+  m.up = upv;
+  m.slots = slots;
+  m.thr = thr;
+  m.tau = tau;
+  m.n_slots = n_slots;
+  m.I = (int)inter;
+  m.H = (int)hidden;
+  m.cnt = cnt;
+  m.inter = mid;
+  if ((rc = hip_status(cai4::sparse_mask(m, (int)n_tokens, true, st)))) return rc;
+  if (counts && (rc = hip_status(cai4::sparse_counts(cnt, cai4::sparse_groups((int)inter),
+                                                     (int)n_tokens, counts, st))))
     return rc;
   return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
                   (int)group, (int)sdt, (int)e->tiling, mid, nullptr, cai4::A_XF32,
                   (int)n_tokens, out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st,
                   part);
 }
-// Workspace of the AXPY-form sparse FFN: gate, SiLU and the intermediate
-// ([n_tokens, inter] f32 each), active lane ids [n_tokens, inter], two cells
-// and a count per token, the gate GEMM's split-K partials, the AXPY's slice
-// partials (one token at a time, sized for every lane active).
+
+// Workspace of the AXPY-form sparse FFN: gate and up ([n_tokens, inter] f32
+// each), the slots, the groups' counts [n_tokens, groups], the GEMMs' split-K
+// partials, then the groups' partial output rows of up to `chunk` tokens.
 struct AxpyFfnWorkspace {
-  size_t lanes, cells, counts, part_gemm, part_axpy, total;
+  size_t lanes, slots, cnt, part_gemm, rows, total;
+  uint32_t chunk;  // tokens per AXPY launch pair
 };
 AxpyFfnWorkspace axpy_ffn_workspace(int dev, uint32_t hidden, uint32_t inter, uint32_t group,
                                     uint32_t n_tokens) {
   const cai4::SkinnyDevice d = device_props(dev);
   AxpyFfnWorkspace w;
+  const size_t row_set = (size_t)cai4::sparse_groups((int)inter) * hidden * 4;  // one token's
+  // at most ~32 MB of partial rows per launch pair
+  const size_t fit = ((size_t)32 << 20) / row_set;
+  w.chunk = (uint32_t)(fit < 1 ? 1 : fit < n_tokens ? fit : n_tokens);
   w.lanes = align256((size_t)n_tokens * inter * 4);
-  w.cells = align256((size_t)n_tokens * 8);
-  w.counts = align256((size_t)n_tokens * 4);
+  w.slots = sparse_slot_bytes(inter, n_tokens);
+  w.cnt = align256((size_t)n_tokens * cai4::sparse_groups((int)inter) * 4);
   w.part_gemm = align256(cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens,
-                                           cai4::A_XF32, cai4::EPI_F32, d)
+                                           cai4::A_XF32, cai4::EPI_PAIR_F32, d)
                              .partial_bytes);
-  w.part_axpy = align256(cai4::axpy_plan((int)hidden, (int)inter).partial_bytes);
-  w.total = 4 * w.lanes + w.cells + w.counts + w.part_gemm + w.part_axpy;
+  w.rows = align256((size_t)w.chunk * row_set);
+  w.total = 2 * w.lanes + w.slots + w.cnt + w.part_gemm + w.rows;
   return w;
 }
 
 // ffn_forward_sparse_axpy_f32_mode (ffn_sparsity.rs:638-740) for n_tokens
-// rows: gate GEMM (f32 x), plain SiLU + max, the mask and rows-subset up
-// (inter = silu * up on the active lanes), the active lanes compacted in
-// ascending order, then per token out = AXPY of those rows of the transposed
-// down (e->down_* hold transpose_requantize_down's codes and bf16 scales).
+// rows: gate/up GEMM (f32 x) with the slots, then per chunk of tokens the
+// mask (plain SiLU) and the AXPY of the transposed down's active rows (e->
+// down_* hold transpose_requantize_down's codes and bf16 scales) into the
+// groups' partial rows, and their reduction into out (overwritten) with the
+// active counts.
 int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
              const cascadia_int4_expert *e, const float *x, uint32_t n_tokens, float tau,
              const float *thr, float *out, uint32_t *counts_out, void *workspace,
@@ -521,30 +589,38 @@ int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   }
   uint8_t *b = static_cast<uint8_t *>(ws);
   float *gate = reinterpret_cast<float *>(b);
-  float *sg = reinterpret_cast<float *>(b + w.lanes);
-  float *mid = reinterpret_cast<float *>(b + 2 * w.lanes);
-  uint32_t *active = reinterpret_cast<uint32_t *>(b + 3 * w.lanes);
-  uint32_t *cells = reinterpret_cast<uint32_t *>(b + 4 * w.lanes);
-  uint32_t *counts = counts_out ? counts_out
-                                : reinterpret_cast<uint32_t *>(b + 4 * w.lanes + w.cells);
-  void *part_gemm = w.part_gemm ? b + 4 * w.lanes + w.cells + w.counts : nullptr;
-  float *part_axpy =
-      reinterpret_cast<float *>(b + 4 * w.lanes + w.cells + w.counts + w.part_gemm);
-  int rc = run_gemm(e->gate_packed, e->gate_scale, nullptr, nullptr, (int)inter, (int)hidden,
-                    (int)group, (int)sdt, (int)e->tiling, x, nullptr, cai4::A_XF32,
-                    (int)n_tokens, gate, nullptr, cai4::EPI_F32, st, part_gemm, workspace == nullptr);
+  float *upv = reinterpret_cast<float *>(b + w.lanes);
+  b += 2 * w.lanes;
+  uint32_t *slots = reinterpret_cast<uint32_t *>(b);
+  b += w.slots;
+  uint32_t *cnt = reinterpret_cast<uint32_t *>(b);
+  b += w.cnt;
+  void *part_gemm = w.part_gemm ? b : nullptr;
+  b += w.part_gemm;
+  float *rows = reinterpret_cast<float *>(b);
+  int n_slots = 0;
+  int rc = sparse_gate_up(e, hidden, inter, group, sdt, x, cai4::A_XF32, n_tokens, gate, upv,
+                          thr, false, slots, &n_slots, part_gemm, workspace == nullptr, st);
   if (rc) return rc;
-  hipError_t err = cai4::sparse_ffn_mid(e->up_packed, e->up_scale, (int)inter, (int)hidden,
-                                        (int)group, (int)sdt, (int)e->tiling, x, true,
-                                        (int)n_tokens, gate, tau, thr, sg, cells, mid, nullptr,
-                                        st, true);
-  if (err == hipSuccess)
-    err = cai4::sparse_compact(gate, (int)inter, (int)n_tokens, tau, thr, sg, cells, active,
-                               counts, st);
-  for (uint32_t t = 0; t < n_tokens && err == hipSuccess; ++t)
-    err = cai4::axpy_active(e->down_packed, e->down_scale, mid + (size_t)t * inter,
-                            active + (size_t)t * inter, (int)inter, (int)hidden, (int)inter,
-                            part_axpy, out + (size_t)t * hidden, st, counts + t, true);
+  cai4::SparseMaskArgs m{};
+  m.gate = gate;
+  m.up = upv;
+  m.slots = slots;
+  m.thr = thr;
+  m.tau = tau;
+  m.n_slots = n_slots;
+  m.I = (int)inter;
+  m.H = (int)hidden;
+  m.cnt = cnt;
+  m.dt = e->down_packed;
+  m.dt_s = reinterpret_cast<const uint16_t *>(e->down_scale);
+  m.partial = rows;
+  hipError_t err = hipSuccess;
+  for (uint32_t t0 = 0; t0 < n_tokens && err == hipSuccess; t0 += w.chunk) {
+    const uint32_t nt = n_tokens - t0 < w.chunk ? n_tokens - t0 : w.chunk;
+    m.t0 = (int)t0;
+    err = cai4::sparse_axpy_ffn(m, (int)nt, out, counts_out, st);
+  }
   return hip_status(err);
 }
 

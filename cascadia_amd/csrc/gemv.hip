@@ -81,6 +81,10 @@ struct GvParams {
   const uint8_t *sh_w0, *sh_s0, *sh_w1, *sh_s1;
   float *sh_out;
   int sh_slot;
+  // the sparse-mask epilogue (SkinnyArgs::slots)
+  uint32_t *slots;
+  const float *thr;
+  int silu_slot;
 };
 
 // Slot kk of the one token: its expert, weight, position (kk, or -1 when
@@ -423,6 +427,21 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   }
   if (lg != 0) return;  // D row 0 = the token: lanes 0-15, component 0
   const int r16 = 16 * T + lr;
+  if (MODE == GV_PLAIN && a.slots) {  // uniform: the sparse-mask epilogue
+    float m = 0.f, pos = 0.f;
+    if (r16 < a.N) {
+      reinterpret_cast<float *>(a.out)[r16] = acc[0];
+      if (NT == 2) reinterpret_cast<float *>(a.out2)[r16] = acc[NT - 1];  // up, unfused
+      const float sv = a.silu_slot == 2 ? silu_stable(acc[0]) : silu_plain(acc[0]);
+      m = fabsf(sv);
+      m = m > 0.f ? m : 0.f;  // NaN -> 0: a NaN lane never raises the max
+      if (a.thr) pos = a.thr[r16] <= 0.f ? 0.f : 1.f;
+    }
+    m = row16_max(m);  // lanes 0-15: one DPP row, all live
+    pos = row16_max(pos);
+    if (lr == 0) a.slots[T] = fbits(m) | (pos > 0.f ? 0x80000000u : 0u);
+    return;
+  }
   if (r16 >= a.N) return;
   const size_t row = orow + r16;
   const float y = acc[0];
@@ -558,6 +577,9 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int
   k.epi = epi;
   k.kw = p.kw;
   k.kpw = p.kpw;
+  k.slots = a.slots;
+  k.thr = a.thr;
+  k.silu_slot = a.silu_slot;
   k.chunks = a.chunks;
   k.row_map = a.row_map;
   k.expert_stride = a.expert_stride;

@@ -129,6 +129,18 @@ CAI4_DEV u32x4_t xpose_rows(u32x4_t v) {
 
 CAI4_DEV float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
+// The two SiLU forms of the activation-sparse FFN, correctly rounded
+// division: the plain g / (1 + e^-g) (ffn_sparsity.rs:487, 667-678) and the
+// stable one of build_active_mask_mode (ffn_sparsity.rs:141-147: e^-g for
+// g >= 0, e^g below).  The mask's max and its per-lane test must see the same
+// bits, so every kernel computes them through these.
+CAI4_DEV float silu_plain(float g) { return __fdiv_rn(g, 1.0f + expf(-g)); }
+CAI4_DEV float silu_stable(float g) {
+  if (g >= 0.0f) return __fdiv_rn(g, 1.0f + expf(-g));
+  const float eg = expf(g);
+  return __fdiv_rn(g * eg, 1.0f + eg);
+}
+
 // 8 consecutive f32 -> hi / lo bf16 in natural column order.
 CAI4_DEV u32x4_t act_split_f32_nat(const f32x4_t &a, const f32x4_t &b, bool lo) {
   const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -178,6 +190,15 @@ CAI4_DEV float row16_sum(float t) {
   t += dpp_f32<0x4E>(t);   // quad_perm 2,3,0,1
   t += dpp_f32<0x124>(t);  // row_ror 4
   t += dpp_f32<0x128>(t);  // row_ror 8
+  return t;
+}
+
+// Max over a 16-lane DPP row (every lane of the row gets it).
+CAI4_DEV float row16_max(float t) {
+  t = fmaxf(t, dpp_f32<0xB1>(t));
+  t = fmaxf(t, dpp_f32<0x4E>(t));
+  t = fmaxf(t, dpp_f32<0x124>(t));
+  t = fmaxf(t, dpp_f32<0x128>(t));
   return t;
 }
 

@@ -376,7 +376,10 @@ CAI4_DEV void epilogue(const KParams &a, f32x4_t (&acc)[MT][NT], int unit, int m
         const float y = acc[mt][nt][v];
         if constexpr (SW) {
           const float h = silu_f32(y) * acc[mt][nt + NOUT][v];
-          if (a.epi == EPI_SWIGLU) {
+          if (a.epi == EPI_PAIR_F32) {
+            reinterpret_cast<float *>(a.out)[o] = y;
+            reinterpret_cast<float *>(a.out2)[o] = acc[mt][nt + NOUT][v];
+          } else if (a.epi == EPI_SWIGLU) {
             reinterpret_cast<float *>(a.out)[o] = h;
           } else {
             // hi = h truncated to bf16, lo = bf16(h - hi): the A_HILO planes
@@ -655,7 +658,7 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   p.mt = mt;
   p.m_chunks = m_chunks > 0 ? m_chunks : (m_rows + tpm * mt - 1) / (tpm * mt);
   p.act_rows = m_rows < tpm * mt ? m_rows : tpm * mt;
-  const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
+  const bool sw = epi_pair(epi);
   const int kb_total = (K + 127) / 128;
   const int maxw = skinny_max_threads(mt) / 64;
   const long target = 16L * d.num_cus;  // about 4 resident waves per SIMD
@@ -894,7 +897,7 @@ hipError_t skinny_launch(const SkinnyArgs &a, const SkinnyPlan &p, int amode, in
   k.act_rows = p.act_rows;
   k.act_stride = p.act_stride;
   k.scale_off = p.scale_off;
-  const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
+  const bool sw = epi_pair(epi);
   const bool tr = (a.G % 128) != 0;
   return tr ? launch_nt<true>(k, p, sw, st) : launch_nt<false>(k, p, sw, st);
 }

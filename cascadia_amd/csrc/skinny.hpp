@@ -7,8 +7,13 @@
 namespace cai4 {
 
 // Epilogues: f32 out, bf16 (RNE) out, SwiGLU of a gate/up tile pair as f32,
-// or as the two bf16 planes (hi, lo) that A_HILO consumes.
-enum Epilogue { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_BF16 = 2, EPI_SWIGLU_HILO = 3 };
+// or as the two bf16 planes (hi, lo) that A_HILO consumes; a gate/up pair's
+// two rows as f32, not combined (out = gate, out2 = up: the skinny kernel).
+enum Epilogue { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_BF16 = 2, EPI_SWIGLU_HILO = 3, EPI_PAIR_F32 = 4 };
+
+__host__ __device__ inline bool epi_pair(int epi) {
+  return epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO || epi == EPI_PAIR_F32;
+}
 
 // Activation modes: bf16; f32 (split into hi/lo bf16 planes while staged);
 // precomputed hi/lo bf16 planes (x = hi plane, x2 = lo plane); f32 rows
@@ -36,7 +41,7 @@ struct SkinnyArgs {
   const void *x;      // activations [M, ldx]: bf16 bits, f32, or the hi plane
   const void *x2;     // A_HILO: the lo plane [M, ldx]
   void *out;          // [M, ldo]: f32, bf16 bits, or the hi plane (EPI_SWIGLU_HILO)
-  void *out2;         // EPI_SWIGLU_HILO: the lo plane
+  void *out2;         // EPI_SWIGLU_HILO: the lo plane; EPI_PAIR_F32: up
   void *partials;     // split-K partial sums (SkinnyPlan::partial_bytes), or null
   const SkinnyChunk *chunks;  // grouped mode: [max_chunks] (device), else null
   const int32_t *row_map;     // A_GATHER: x row of each grouped row [M] (device)
@@ -45,6 +50,15 @@ struct SkinnyArgs {
   int N, K, G, M, ldx, ldo, sdt;
   int glog2;  // log2(G) when G is a power of two, else -1
   int tiled;  // weights/scales in the MFMA-tiled device layout (layout.hip)
+  // The one-token GEMV's sparse-mask epilogue: y (the gate) goes to out as
+  // f32 -- with a gate/up pair (EPI_SWIGLU) the up row to out2 as f32, not
+  // combined -- and each 16-row tile writes slots[tile] = max |silu(y)| over
+  // its rows (bits; NaN counts as 0) | (any thr[row] > 0) << 31; silu_slot
+  // 1 = the plain SiLU, 2 = the stable one; thr may be null.  Null slots: the
+  // ordinary epilogue.
+  uint32_t *slots;
+  const float *thr;
+  int silu_slot;
 };
 
 // Launch plan.  A workgroup has rw x kw waves: rw row groups (each nt weight

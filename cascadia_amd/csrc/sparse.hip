@@ -1,23 +1,34 @@
-// sparse.hip -- the activation-sparse (tau > 0) pieces of the expert FFN
-// (ffn_sparsity.rs:131-179 build_active_mask_mode, :187-348 the rows-subset
-// up GEMV, :499-537 the sparse branch).  The gate and down GEMMs are the
-// ordinary kernels; between them:
+// sparse.hip -- the activation-sparse (tau > 0) expert FFN after its gate/up
+// GEMM (ffn_sparsity.rs:131-179 build_active_mask_mode, :499-537 the sparse
+// branch of the GEMV form, :638-740 the AXPY form; ffn_axpy.rs:82-160).
 //
-//   sparse_prep_kernel   a lane per thread over many workgroups: stable SiLU
-//                        of the gate output, each workgroup's max |silu| into
-//                        the token's max cell (an unsigned max of the float
-//                        bits: every value is >= 0 and NaN never enters), and
-//                        for per-channel thresholds whether any is > 0.
-//   rows_subset_kernel   one wave per intermediate lane: the mask test
-//                        |silu| >= cutoff * max (every lane when the max is 0
-//                        or the mode is dense), then for an active lane the up
-//                        row's dot product with x, read from either weight
-//                        layout, times the SiLU -> the intermediate; 0 for an
-//                        inactive lane, whose up row is never read.
-//   sparse_count_kernel  the active-lane count of each token, by the same
-//                        test (only when the caller asks for it).
+// Per token the mask needs the max |silu| over every intermediate lane, so the
+// gate/up GEMM comes first and leaves, next to its f32 gate and up rows, one
+// slot per workgroup: that workgroup's max |silu| (the f32 bits; every value
+// is >= 0 and a NaN counts as 0) with bit 31 set when one of its lanes has a
+// per-channel threshold > 0.  The one-token GEMV writes them from its
+// epilogue (one per 16-row tile); after any other GEMM sparse_slots_kernel
+// does (one per 256 lanes).  Every slot is written on every call, so nothing
+// has to be cleared first.
 //
-// HBM traffic per token: gate and down in full, up for the active rows only.
+// The up GEMM reads every row, as the dense FFN does: at one token on MI355X a
+// rows-subset pass costs two dependent memory round trips and a launch more
+// than the fused gate/up stream takes to read the inactive rows, and the
+// intermediate of the active lanes is the same either way.  What the mask
+// saves is the AXPY form's down: only the active rows of the transposed down
+// are read.
+//
+//   sparse_mask_kernel   (GEMV form) a lane per thread: the token's max and
+//                        flag from its slots, the test |silu| >= cutoff * max
+//                        (every lane when the max is 0 or the mode is dense),
+//                        inter = silu * up or 0, and the group's count.
+//   sparse_axpy_kernel   (AXPY form) workgroup (512-column block, group of
+//                        256 lanes, token): the same test, the active lanes
+//                        listed in ascending order (ballot + mbcnt), then
+//                        sum over them of inter * W_t[lane, block] into the
+//                        group's partial output row.
+//   sparse_axpy_reduce_kernel  the partial rows added in group order
+//                        (deterministic), and the groups' counts.
 #include "int4_common.hpp"
 #include "sparse.hpp"
 
@@ -25,23 +36,10 @@ namespace cai4 {
 
 namespace {
 
-constexpr int kMaskThreads = 1024;
-
 __global__ void fill_u32_kernel(uint32_t *p, int n, uint32_t v) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
 }
-constexpr int kMaskWaves = kMaskThreads / 64;
-
-// ffn_sparsity.rs:141-147: the stable form, e^-g for g >= 0, e^g below.
-CAI4_DEV float silu_stable(float g) {
-  if (g >= 0.0f) return __fdiv_rn(g, 1.0f + expf(-g));
-  const float eg = expf(g);
-  return __fdiv_rn(g * eg, 1.0f + eg);
-}
-
-// ffn_sparsity.rs:487 (the dense branch): g / (1 + e^-g).
-CAI4_DEV float silu_plain(float g) { return __fdiv_rn(g, 1.0f + expf(-g)); }
 
 CAI4_DEV float wave_max(float v) {
 #pragma unroll
@@ -52,250 +50,305 @@ CAI4_DEV float wave_max(float v) {
   return v;
 }
 
-CAI4_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+CAI4_DEV uint32_t wave_rank(uint64_t b) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
 }
 
-// cells of a token: [0] max |silu| bits, [1] any per-channel threshold > 0.
-// PLAIN: the AXPY form's SiLU g / (1 + e^-g) (ffn_sparsity.rs:667-678), else
-// the stable one of build_active_mask_mode.
-template <bool PLAIN>
+// |silu| of one lane as a slot contribution (NaN -> 0).
+CAI4_DEV float slot_mag(float s) {
+  const float m = fabsf(s);
+  return m > 0.0f ? m : 0.0f;
+}
+
+// The slots of a gate [T, I] computed by any GEMM: one per 256 lanes.
+template <bool STABLE>
 __global__ void __launch_bounds__(256)
-    sparse_prep_kernel(const float *__restrict__ gate, int I, const float *__restrict__ thr,
-                       float *__restrict__ sg, uint32_t *__restrict__ cells) {
-  __shared__ float s_max[4];
+    sparse_slots_kernel(const float *__restrict__ gate, int I, const float *__restrict__ thr,
+                        uint32_t *__restrict__ slots, int n_slots) {
+  __shared__ float s_m[4], s_p[4];
   const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const size_t row = (size_t)t * I;
-  float a = 0.0f;
-  int pos = 0;
+  float m = 0.0f, pos = 0.0f;
   if (i < I) {
-    const float s = PLAIN ? silu_plain(gate[row + i]) : silu_stable(gate[row + i]);
-    sg[row + i] = s;
-    a = fabsf(s);
-    a = a > 0.0f ? a : 0.0f;  // NaN -> 0 (a NaN lane never raises the max)
-    if (thr) pos = !(thr[i] <= 0.0f);
+    const float g = gate[(size_t)t * I + i];
+    m = slot_mag(STABLE ? silu_stable(g) : silu_plain(g));
+    if (thr) pos = thr[i] <= 0.0f ? 0.0f : 1.0f;
   }
-  a = wave_max(a);
-  if (lane == 0) s_max[wave] = a;
-  pos = __syncthreads_or(pos);
-  if (threadIdx.x == 0) {
-    float m = s_max[0];
-    for (int w = 1; w < 4; ++w) m = s_max[w] > m ? s_max[w] : m;
-    if (m > 0.0f) atomicMax(&cells[2 * t], fbits(m));
-    if (pos) atomicOr(&cells[2 * t + 1], 1u);
+  m = wave_max(m);
+  pos = wave_max(pos);
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_p[wave] = pos;
   }
-}
-
-// The mask test of lane i of token t (ffn_sparsity.rs:131-179); *silu
-// receives the SiLU the intermediate uses: the dense branch's plain form
-// when the per-channel vector is dense (:85-90, 487).
-CAI4_DEV bool lane_active(const float *__restrict__ gate, const float *__restrict__ sg,
-                          const float *__restrict__ thr, float tau,
-                          const uint32_t *__restrict__ cells, int t, size_t at, int i,
-                          float *silu) {
-  const bool sparse = thr ? cells[2 * t + 1] != 0u : !(tau <= 0.0f);
-  const float mx = bitsf(cells[2 * t]);
-  if (!sparse) {
-    *silu = silu_plain(gate[at]);
-    return true;
-  }
-  const float s = sg[at];
-  *silu = s;
-  return mx == 0.0f || fabsf(s) >= (thr ? thr[i] : tau) * mx;
-}
-
-__global__ void __launch_bounds__(kMaskThreads)
-    sparse_count_kernel(const float *__restrict__ gate, int I, float tau,
-                        const float *__restrict__ thr, const float *__restrict__ sg,
-                        const uint32_t *__restrict__ cells, uint32_t *__restrict__ counts) {
-  __shared__ uint32_t s_n[kMaskWaves];
-  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const size_t row = (size_t)t * I;
-  uint32_t n = 0;
-  for (int i = tid; i < I; i += kMaskThreads) {
-    float s;
-    n += lane_active(gate, sg, thr, tau, cells, t, row + i, i, &s) ? 1u : 0u;
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o, 64);
-  if (lane == 0) s_n[wave] = n;
   __syncthreads();
-  if (tid == 0) {
-    uint32_t tot = 0;
-    for (int w = 0; w < kMaskWaves; ++w) tot += s_n[w];
-    counts[t] = tot;
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) {
+      m = fmaxf(m, s_m[w]);
+      pos = fmaxf(pos, s_p[w]);
+    }
+    slots[(size_t)t * n_slots + blockIdx.x] = fbits(m) | (pos > 0.0f ? 0x80000000u : 0u);
   }
 }
 
-// Weight reads of one lane: 16 bytes = 32 consecutive columns [c, c + 32) of
-// row r, in either layout (layout.hip: the tiled byte b holds columns b and
-// b + 4 of its dword, the crate byte b columns 2b and 2b + 1).
-template <int TILED>
-CAI4_DEV float row_chunk_dot(const uint8_t *__restrict__ w, const uint16_t *__restrict__ s,
-                             int r, int c, int K, int G, int sdt, const float *xs) {
-  u32x4_t v;
-  uint32_t sb;
-  const int NG = K / G;
-  if (TILED) {
-    const size_t KB = (size_t)(K + 127) / 128;
-    v = *reinterpret_cast<const u32x4_t *>(
-        w + ((size_t)(r >> 4) * KB + (c >> 7)) * 1024 + 16 * ((r & 15) + 16 * ((c & 127) >> 5)));
-    sb = s[((size_t)(r >> 4) * NG + c / G) * 16 + (r & 15)];
-  } else {
-    v = *reinterpret_cast<const u32x4_t *>(w + (size_t)r * (K / 2) + c / 2);
-    sb = s[(size_t)r * NG + c / G];
-  }
-  float p = 0.0f;
+constexpr int kSlotLoads = 8;  // slot words per thread in one round of loads
+
+// The mask of lane i (this thread) of token t: every independent load issued
+// first (the token's slots, the lane's gate / up / threshold), the slots
+// folded across the workgroup (one barrier).  Returns whether the lane is
+// active; *v = silu * up.  STABLE && sparse: build_active_mask_mode's SiLU.
+template <bool STABLE>
+CAI4_DEV bool lane_mask(const SparseMaskArgs &a, int t, int i, float *v, float *s_red,
+                        uint32_t *s_flag) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t *sl = a.slots + (size_t)t * a.n_slots;
+  uint32_t sv[kSlotLoads];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const uint32_t q = v[d];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int sh = TILED ? (e < 4 ? 8 * e : 8 * (e - 4) + 4) : 4 * e;
-      p += (float)((int)((q >> sh) & 15u) - 8) * xs[8 * d + e];
-    }
+  for (int u = 0; u < kSlotLoads; ++u) {
+    const int k = tid + 256 * u;
+    sv[u] = k < a.n_slots ? sl[k] : 0u;
   }
-  return p * scale_bits_f32(sb, sdt);
+  const bool in = i < a.I;
+  const float g = in ? a.gate[(size_t)t * a.I + i] : 0.0f;
+  const float up = in ? a.up[(size_t)t * a.I + i] : 0.0f;
+  const float th = in && a.thr ? a.thr[i] : 0.0f;
+  float m = 0.0f;
+  uint32_t f = 0u;
+#pragma unroll
+  for (int u = 0; u < kSlotLoads; ++u) {
+    m = fmaxf(m, bitsf(sv[u] & 0x7FFFFFFFu));
+    f |= sv[u] >> 31;
+  }
+  for (int k = tid + 256 * kSlotLoads; k < a.n_slots; k += 256) {  // past 2048 slots
+    const uint32_t u = sl[k];
+    m = fmaxf(m, bitsf(u & 0x7FFFFFFFu));
+    f |= u >> 31;
+  }
+  m = wave_max(m);
+  const bool fw = __ballot(f != 0u) != 0ull;
+  if (lane == 0) {
+    s_red[wave] = m;
+    s_flag[wave] = fw ? 1u : 0u;
+  }
+  __syncthreads();
+  float mx = 0.0f;
+  bool any = false;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mx = fmaxf(mx, s_red[w]);
+    any = any || s_flag[w] != 0u;
+  }
+  // SparsityMode::is_dense (ffn_sparsity.rs:85-90): tau <= 0, or no
+  // per-channel threshold > 0; then, or when the max is 0, every lane is on
+  const bool sparse = a.thr ? any : !(a.tau <= 0.0f);
+  const bool all = !sparse || mx == 0.0f;
+  const float s = STABLE && sparse ? silu_stable(g) : silu_plain(g);
+  // inter[r] = silu_gate[r] * up[r] (ffn_sparsity.rs:527, 711-716)
+  *v = s * up;
+  return in && (all || fabsf(s) >= (a.thr ? th : a.tau) * mx);
 }
 
-template <int XF32>
-CAI4_DEV void load_x(const void *__restrict__ x, size_t at, float *xs) {
-  if (XF32) {
-    const f32x4_t *xp = reinterpret_cast<const f32x4_t *>(static_cast<const float *>(x) + at);
+template <bool STABLE>
+__global__ void __launch_bounds__(256) sparse_mask_kernel(SparseMaskArgs a) {
+  __shared__ float s_red[4];
+  __shared__ uint32_t s_flag[4], s_wn[4];
+  const int t = blockIdx.y, i = blockIdx.x * kSparseGroup + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float v;
+  const bool on = lane_mask<STABLE>(a, t, i, &v, s_red, s_flag);
+  if (i < a.I) a.inter[(size_t)t * a.I + i] = on ? v : 0.0f;
+  const uint64_t b = __ballot(on);
+  if (lane == 0) s_wn[wave] = (uint32_t)__popcll(b);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    a.cnt[(size_t)t * gridDim.x + blockIdx.x] = ((s_wn[0] + s_wn[1]) + s_wn[2]) + s_wn[3];
+}
+
+// The AXPY form: workgroup (column block, group, token).  The group's active
+// lanes are listed in ascending order; wave w takes entries w, w + 4, ...
+// kAxBatch at a time, all of a batch's loads issued before any is used
+// (entries past the list read its first row with weight 0); a lane owns 8
+// columns (4 bytes of each transposed-down row, one bf16 scale);
+// combined = inter * scale, acc += combined * n, the -8 of q = n - 8 applied
+// once at the end (ffn_axpy.rs:118-134); the four waves' sums are added in
+// wave order.
+constexpr int kAxBatch = 16;
+
+__global__ void __launch_bounds__(256) sparse_axpy_kernel(SparseMaskArgs a) {
+  __shared__ float s_red[4];
+  __shared__ uint32_t s_flag[4], s_wn[4];
+  __shared__ uint32_t s_id[kSparseGroup];
+  __shared__ float s_val[kSparseGroup];
+  __shared__ float s_acc[3][8][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y, tl = blockIdx.z, t = a.t0 + tl;
+  const int i = g * kSparseGroup + tid;
+  float v;
+  const bool on = lane_mask<false>(a, t, i, &v, s_red, s_flag);
+  const uint64_t b = __ballot(on);
+  const uint32_t rank = wave_rank(b);
+  if (lane == 0) s_wn[wave] = (uint32_t)__popcll(b);
+  __syncthreads();
+  uint32_t off = 0u, n = 0u;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const f32x4_t q = xp[j];
-      xs[4 * j] = q.x;
-      xs[4 * j + 1] = q.y;
-      xs[4 * j + 2] = q.z;
-      xs[4 * j + 3] = q.w;
+  for (int w = 0; w < 4; ++w) {
+    if (w < wave) off += s_wn[w];
+    n += s_wn[w];
+  }
+  if (on) {
+    s_id[off + rank] = (uint32_t)i;
+    s_val[off + rank] = v;
+  }
+  if (blockIdx.x == 0 && tid == 0) a.cnt[(size_t)t * gridDim.y + g] = n;
+  __syncthreads();
+
+  const int c0 = blockIdx.x * kSparseAxCols + 8 * lane;  // this lane's 8 columns
+  const bool cok = c0 < a.H;
+  const int cc = cok ? c0 : 0;  // a lane past the columns reads column 0 and adds nothing
+  const int GD = a.H / 32;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  float csum = 0.0f;
+  for (int f0 = wave; f0 < (int)n; f0 += 4 * kAxBatch) {
+    uint32_t q[kAxBatch], sc[kAxBatch];
+#pragma unroll
+    for (int u = 0; u < kAxBatch; ++u) {
+      const int f = f0 + 4 * u;
+      const uint32_t r = s_id[f < (int)n ? f : f0];
+      q[u] = *reinterpret_cast<const uint32_t *>(a.dt + (size_t)r * (a.H / 2) + cc / 2);
+      sc[u] = a.dt_s[(size_t)r * GD + cc / 32];
     }
-  } else {
-    const u32x4_t *xp = reinterpret_cast<const u32x4_t *>(static_cast<const uint16_t *>(x) + at);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x4_t q = xp[j];
+    for (int u = 0; u < kAxBatch; ++u) {
+      const int f = f0 + 4 * u;
+      const float comb = f < (int)n && cok ? s_val[f] * bf16_to_f32(sc[u]) : 0.0f;
+      const uint32_t lo = q[u] & 0x0F0F0F0Fu, hi = (q[u] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        xs[8 * j + 2 * h] = bitsf(q[h] << 16);
-        xs[8 * j + 2 * h + 1] = bitsf(q[h] & 0xFFFF0000u);
+      for (int k = 0; k < 4; ++k) {  // byte k: columns 2k (low nibble) and 2k + 1
+        acc[2 * k] = fmaf(comb, (float)((lo >> (8 * k)) & 0xFFu), acc[2 * k]);
+        acc[2 * k + 1] = fmaf(comb, (float)((hi >> (8 * k)) & 0xFFu), acc[2 * k + 1]);
       }
+      csum += comb;
     }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = fmaf(-8.0f, csum, acc[e]);
+  if (wave > 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_acc[wave - 1][e][lane] = acc[e];
+  }
+  __syncthreads();
+  if (wave == 0 && cok) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      acc[e] = ((acc[e] + s_acc[0][e][lane]) + s_acc[1][e][lane]) + s_acc[2][e][lane];
+    float *prow = a.partial + ((size_t)tl * gridDim.y + g) * a.H + c0;
+    *reinterpret_cast<f32x4_t *>(prow) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4_t *>(prow + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
   }
 }
 
-template <int TILED, int XF32>
-__global__ void __launch_bounds__(256)
-    rows_subset_kernel(const uint8_t *__restrict__ w, const uint16_t *__restrict__ s, int I,
-                       int K, int G, int sdt, const void *__restrict__ x,
-                       const float *__restrict__ gate, const float *__restrict__ sg,
-                       const float *__restrict__ thr, float tau,
-                       const uint32_t *__restrict__ cells, float *__restrict__ inter) {
-  const int t = blockIdx.y;
-  const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (r >= I) return;  // wave-uniform
-  const size_t row = (size_t)t * I;
-  float silu;
-  if (!lane_active(gate, sg, thr, tau, cells, t, row + r, r, &silu)) {
-    if (lane == 0) inter[row + r] = 0.0f;
-    return;
+// Sum of the token's n group counts, by one wave (eight loads in flight).
+CAI4_DEV uint32_t wave_count_sum(const uint32_t *__restrict__ cnt, int n, int lane) {
+  uint32_t s = 0u;
+  for (int k0 = lane; k0 < n; k0 += 64 * 8) {
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = k0 + 64 * j < n ? cnt[k0 + 64 * j] : 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
   }
-  float acc = 0.0f;
-  // two 32-column chunks per pass: both weight loads are issued before
-  // either is used
-  for (int c = 32 * lane; c < K; c += 4096) {
-    const bool two = c + 2048 < K;
-    float xa[32], xb[32];
-    load_x<XF32>(x, (size_t)t * K + c, xa);
-    if (two) load_x<XF32>(x, (size_t)t * K + c + 2048, xb);
-    acc += row_chunk_dot<TILED>(w, s, r, c, K, G, sdt, xa);
-    if (two) acc += row_chunk_dot<TILED>(w, s, r, c + 2048, K, G, sdt, xb);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  return s;
+}
+
+// out[t0 + y][h] = sum over groups of partial[y][group][h], in group order
+// per wave (groups w, w + 16, ...; eight loads in flight) and the sixteen
+// wave sums in wave order: deterministic.  Block (0, y) also sums the token's
+// group counts.
+__global__ void __launch_bounds__(1024)
+    sparse_axpy_reduce_kernel(const float *__restrict__ partial, int n_groups, int H,
+                              float *__restrict__ out, const uint32_t *__restrict__ cnt,
+                              uint32_t *__restrict__ counts, int t0) {
+  __shared__ float s_sum[16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tl = blockIdx.y, t = t0 + tl, h = blockIdx.x * 64 + lane;
+  const float *p = partial + (size_t)tl * n_groups * H;
+  float s = 0.0f;
+  if (h < H) {
+    for (int k = wave; k < n_groups; k += 16 * 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int kk = k + 16 * j;
+        v[j] = kk < n_groups ? p[(size_t)kk * H + h] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
   }
-  acc = wave_sum(acc);
-  if (lane == 0) inter[row + r] = silu * acc;
+  s_sum[wave][lane] = s;
+  if (counts && blockIdx.x == 0 && wave == 15) {
+    const uint32_t c = wave_count_sum(cnt + (size_t)t * n_groups, n_groups, lane);
+    if (lane == 0) counts[t] = c;
+  }
+  __syncthreads();
+  if (wave == 0 && h < H) {
+    float v = s_sum[0][lane];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) v += s_sum[w][lane];
+    out[(size_t)t * H + h] = v;
+  }
+}
+
+__global__ void __launch_bounds__(64)
+    sparse_counts_kernel(const uint32_t *__restrict__ cnt, int n_groups,
+                         uint32_t *__restrict__ counts) {
+  const uint32_t c = wave_count_sum(cnt + (size_t)blockIdx.x * n_groups, n_groups, threadIdx.x);
+  if (threadIdx.x == 0) counts[blockIdx.x] = c;
 }
 
 }  // namespace
 
-// Active lanes of each token in ascending order (active[t * I ..]) and their
-// count, by the mask test of rows_subset_kernel: one workgroup per token, a
-// chunk of 1024 lanes per pass, ranks by ballot within waves and a scan of
-// the wave totals.
-__global__ void __launch_bounds__(kMaskThreads)
-    sparse_compact_kernel(const float *__restrict__ gate, int I, float tau,
-                          const float *__restrict__ thr, const float *__restrict__ sg,
-                          const uint32_t *__restrict__ cells, uint32_t *__restrict__ active,
-                          uint32_t *__restrict__ counts) {
-  __shared__ uint32_t s_w[kMaskWaves];
-  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const size_t row = (size_t)t * I;
-  uint32_t base = 0;
-  for (int c0 = 0; c0 < I; c0 += kMaskThreads) {
-    const int i = c0 + tid;
-    float s;
-    const bool on = i < I && lane_active(gate, sg, thr, tau, cells, t, row + i, i, &s);
-    const uint64_t b = __ballot(on);
-    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-    if (lane == 0) s_w[wave] = (uint32_t)__popcll(b);
-    __syncthreads();
-    uint32_t off = base, tot = 0;
-    for (int w = 0; w < kMaskWaves; ++w) {
-      const uint32_t n = s_w[w];
-      if (w < wave) off += n;
-      tot += n;
-    }
-    if (on) active[row + off + rank] = (uint32_t)i;
-    base += tot;
-    __syncthreads();  // s_w is rewritten by the next pass
-  }
-  if (tid == 0) counts[t] = base;
-}
-
-hipError_t sparse_ffn_mid(const uint8_t *w, const uint8_t *s, int I, int K, int G, int sdt,
-                          int tiled, const void *x, bool x_f32, int T, const float *gate,
-                          float tau, const float *thr, float *sg, uint32_t *cells, float *inter,
-                          uint32_t *counts_out, hipStream_t st, bool plain_silu) {
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((2 * T + 255) / 256), dim3(256), 0, st, cells, 2 * T,
-                     0u);
-  if (plain_silu)
-    hipLaunchKernelGGL(sparse_prep_kernel<true>, dim3((I + 255) / 256, T), dim3(256), 0, st, gate,
-                       I, thr, sg, cells);
+hipError_t sparse_slots(const float *gate, int I, int T, const float *thr, bool stable,
+                        uint32_t *slots, hipStream_t st) {
+  const int n = sparse_slots_per_token(I, false);
+  const dim3 grid((unsigned)n, (unsigned)T);
+  if (stable)
+    hipLaunchKernelGGL(sparse_slots_kernel<true>, grid, dim3(256), 0, st, gate, I, thr, slots, n);
   else
-    hipLaunchKernelGGL(sparse_prep_kernel<false>, dim3((I + 255) / 256, T), dim3(256), 0, st,
-                       gate, I, thr, sg, cells);
-  const dim3 grid((I + 3) / 4, T), block(256);
-  const uint16_t *sc = reinterpret_cast<const uint16_t *>(s);
-  if (tiled) {
-    if (x_f32)
-      hipLaunchKernelGGL((rows_subset_kernel<1, 1>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         gate, sg, thr, tau, cells, inter);
-    else
-      hipLaunchKernelGGL((rows_subset_kernel<1, 0>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         gate, sg, thr, tau, cells, inter);
-  } else {
-    if (x_f32)
-      hipLaunchKernelGGL((rows_subset_kernel<0, 1>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         gate, sg, thr, tau, cells, inter);
-    else
-      hipLaunchKernelGGL((rows_subset_kernel<0, 0>), grid, block, 0, st, w, sc, I, K, G, sdt, x,
-                         gate, sg, thr, tau, cells, inter);
-  }
-  if (counts_out)
-    hipLaunchKernelGGL(sparse_count_kernel, dim3(T), dim3(kMaskThreads), 0, st, gate, I, tau, thr,
-                       sg, cells, counts_out);
+    hipLaunchKernelGGL(sparse_slots_kernel<false>, grid, dim3(256), 0, st, gate, I, thr, slots,
+                       n);
   return hipGetLastError();
 }
 
-hipError_t sparse_compact(const float *gate, int I, int T, float tau, const float *thr,
-                          const float *sg, const uint32_t *cells, uint32_t *active,
-                          uint32_t *counts, hipStream_t st) {
-  hipLaunchKernelGGL(sparse_compact_kernel, dim3(T), dim3(kMaskThreads), 0, st, gate, I, tau, thr,
-                     sg, cells, active, counts);
+hipError_t sparse_mask(const SparseMaskArgs &a, int T, bool stable, hipStream_t st) {
+  const dim3 grid((unsigned)sparse_groups(a.I), (unsigned)T);
+  if (stable)
+    hipLaunchKernelGGL(sparse_mask_kernel<true>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(sparse_mask_kernel<false>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t sparse_axpy_ffn(const SparseMaskArgs &a, int n_tokens, float *out, uint32_t *counts,
+                           hipStream_t st) {
+  const int ng = sparse_groups(a.I);
+  hipLaunchKernelGGL(sparse_axpy_kernel,
+                     dim3((unsigned)((a.H + kSparseAxCols - 1) / kSparseAxCols), (unsigned)ng,
+                          (unsigned)n_tokens),
+                     dim3(256), 0, st, a);
+  hipLaunchKernelGGL(sparse_axpy_reduce_kernel,
+                     dim3((unsigned)((a.H + 63) / 64), (unsigned)n_tokens), dim3(1024), 0, st,
+                     a.partial, ng, a.H, out, a.cnt, counts, a.t0);
+  return hipGetLastError();
+}
+
+hipError_t sparse_counts(const uint32_t *cnt, int n_groups, int T, uint32_t *counts,
+                         hipStream_t st) {
+  hipLaunchKernelGGL(sparse_counts_kernel, dim3((unsigned)T), dim3(64), 0, st, cnt, n_groups,
+                     counts);
   return hipGetLastError();
 }
 
