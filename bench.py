@@ -741,16 +741,38 @@ def main():
               flush=True)
         return
     if args.profile_sparse:
-        copies = Copies(cl, torch, 4096, 14336, 128, sdt, 1)
-        xs1 = cl.fill_normal(torch.empty(4096, dtype=torch.bfloat16, device="cuda"), 0, 23)
-        os1 = torch.empty(4096, dtype=torch.bfloat16, device="cuda")
+        # 50 calls each of the GEMV form (expert_forward_sparse) and the AXPY
+        # form (ffn_forward_sparse_axpy_f32) at tau 0.3, weight copies rotating
+        # past the Infinity Cache
+        h, i, g = 4096, 14336, 128
+        nc = math.ceil(2 * MALL_BYTES / cl.expert_bytes(h, i, g)) + 1
+        copies = Copies(cl, torch, h, i, g, sdt, nc, keep_crate=1)
+        xs1 = cl.fill_normal(torch.empty(h, dtype=torch.bfloat16, device="cuda"), 0, 23)
+        os1 = torch.empty(h, dtype=torch.bfloat16, device="cuda")
         for r in range(50):
-            fr = cl.expert_forward_sparse(xs1.view(torch.int16), *copies.w[0].slices(),
-                                          os1.view(torch.int16), 0.3, group_size=128,
+            fr = cl.expert_forward_sparse(xs1.view(torch.int16), *copies.w[r % nc].slices(),
+                                          os1.view(torch.int16), 0.3, group_size=g,
                                           scale_dtype=sdt, tiling=cl.TILING_MFMA)
+        src = cl.ExpertWeights(copies.crate[0], h, i, g, sdt)
+        pts = [cl.transpose_requantize_down(src.down_packed_bytes(), src.down_scale_bits(), h, i,
+                                            group_size=g, scale_dtype=sdt)]
+        pts += [(cl.fill_bytes(torch.empty(i * h // 2, dtype=torch.uint8, device="cuda"), 2, 600 + c),
+                 cl.fill_scales(torch.empty(i * (h // 32) * 2, dtype=torch.uint8, device="cuda"), 2,
+                                700 + c, cl.SCALE_BF16)) for c in range(1, nc)]
+        xf1, of1 = xs1.float(), torch.empty(h, dtype=torch.float32, device="cuda")
+        ws = torch.empty(cl.ffn_sparse_axpy_workspace_bytes(h, i, 1, g), dtype=torch.uint8,
+                         device="cuda")
+        for r in range(50):
+            W = copies.w[r % nc]
+            fa = cl.ffn_forward_sparse_axpy_f32(xf1, h, i, W.gate_packed_bytes(), W.gate_scale_bits(),
+                                                W.up_packed_bytes(), W.up_scale_bits(),
+                                                *pts[r % nc], of1, 0.3, group_size=g,
+                                                scale_dtype=sdt, workspace=ws,
+                                                tiling=cl.TILING_MFMA)
         torch.cuda.synchronize()
-        print(json.dumps({"profile": "sparse_expert", "tau": 0.3, "active_frac": fr,
-                          "launches": 50}), flush=True)
+        print(json.dumps({"profile": "sparse_expert+sparse_axpy_ffn", "tau": 0.3,
+                          "active_frac": fr, "active_frac_axpy_copy": fa, "launches": 50,
+                          "copies": nc}), flush=True)
         return
     if args.profile_moe:
         T = args.moe_tokens
