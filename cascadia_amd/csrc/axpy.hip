@@ -8,11 +8,10 @@
 //   so the strided source reads share cache lines.
 // axpy_active_kernel  y[hidden] += sum over the active rows r of
 //   scalar[r] * W_t[r, :] (ffn_axpy.rs:82-160): only the active rows are
-//   read, which is what the transposed layout buys.  Grid (column chunk of
-//   2048, slice of 32 active rows); a lane holds 32 columns of f32 sums and
-//   each of the block's eight waves keeps four rows' loads in flight; the
-//   waves are folded through LDS into one partial row per slice, and
-//   axpy_reduce_kernel adds the slices to y in slice order (deterministic).
+//   read, which is what the transposed layout buys.  Grid (512-column block,
+//   slice of 32 ids): enough workgroups to fill the chip, each wave's ids and
+//   then its rows loaded in one round trip each; one partial row per slice,
+//   which axpy_reduce_kernel adds to y in slice order (deterministic).
 #include "int4_common.hpp"
 #include "axpy.hpp"
 
@@ -54,89 +53,91 @@ __global__ void __launch_bounds__(256)
       u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
-constexpr int kAxWaves = 8, kAxRows = 4;  // a slice: 32 active rows, 4 per wave in flight
+// axpy_active_kernel: workgroup (512-column block, slice of kAxSlice ids);
+// wave w takes the slice's ids w, w + 4, ... kAxBatch at a time, every load
+// of a batch (ids first, then the rows) issued before any is used; a lane
+// owns 8 columns (4 bytes of each row, one bf16 scale); combined = scalar *
+// scale, acc += combined * n, the -8 of q = n - 8 applied once at the end
+// (ffn_axpy.rs:118-134); the four waves' sums are added in wave order into
+// the slice's partial row.
+constexpr int kAxSlice = 32, kAxBatch = 8, kAxCols = 512;
 
-__global__ void __launch_bounds__(64 * kAxWaves)
+__global__ void __launch_bounds__(256)
     axpy_active_kernel(const uint8_t *__restrict__ pt, const uint16_t *__restrict__ st,
                        const float *__restrict__ scalars, const uint32_t *__restrict__ active,
-                       int n_active, const uint32_t *__restrict__ n_dev, int per_slice, int H,
-                       int I, float *__restrict__ partial) {
-  __shared__ float s_acc[kAxWaves - 1][2048];
+                       int n_active, int per_slice, int H, int I, float *__restrict__ partial) {
+  __shared__ float s_acc[3][8][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int c = blockIdx.x * 2048 + 32 * lane;  // this lane's 32 columns
-  if (n_dev) n_active = min(n_active, (int)*n_dev);  // the count the device found
-  const int a0 = blockIdx.y * per_slice;
-  if (a0 >= n_active) return;  // uniform: a slice past the count (its partial is never read)
-  const int a1 = min(a0 + per_slice, n_active);
+  const int c0 = blockIdx.x * kAxCols + 8 * lane;  // this lane's 8 columns
+  const bool cok = c0 < H;
+  const int cc = cok ? c0 : 0;  // a lane past the columns reads column 0 and adds nothing
+  const int a0 = blockIdx.y * per_slice, a1 = min(a0 + per_slice, n_active);
   const int GD = H / 32;
-  float acc[32];
+  float acc[8];
 #pragma unroll
-  for (int j = 0; j < 32; ++j) acc[j] = 0.0f;
-  if (c < H) {
-    for (int a = a0 + wave; a < a1; a += kAxWaves * kAxRows) {
-      uint32_t r[kAxRows];
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  float csum = 0.0f;
+  for (int f0 = a0 + wave; f0 < a1; f0 += 4 * kAxBatch) {
+    uint32_t id[kAxBatch], q[kAxBatch], sc[kAxBatch];
+    float sv[kAxBatch];
 #pragma unroll
-      for (int k = 0; k < kAxRows; ++k) {
-        const int ak = a + k * kAxWaves;
-        r[k] = ak < a1 ? active[ak] : 0xFFFFFFFFu;
+    for (int u = 0; u < kAxBatch; ++u) {
+      const int f = f0 + 4 * u;
+      id[u] = active[f < a1 ? f : f0];
+    }
+#pragma unroll
+    for (int u = 0; u < kAxBatch; ++u) {
+      const uint32_t r = id[u] < (uint32_t)I ? id[u] : 0u;  // ids past inter: skipped
+      q[u] = *reinterpret_cast<const uint32_t *>(pt + (size_t)r * (H / 2) + cc / 2);
+      sc[u] = st[(size_t)r * GD + cc / 32];
+      sv[u] = scalars[r];
+    }
+#pragma unroll
+    for (int u = 0; u < kAxBatch; ++u) {
+      const bool ok = f0 + 4 * u < a1 && id[u] < (uint32_t)I && cok;
+      const float comb = ok ? sv[u] * bf16_to_f32(sc[u]) : 0.0f;
+      const uint32_t lo = q[u] & 0x0F0F0F0Fu, hi = (q[u] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {  // byte k: columns 2k (low nibble) and 2k + 1
+        acc[2 * k] = fmaf(comb, (float)((lo >> (8 * k)) & 0xFFu), acc[2 * k]);
+        acc[2 * k + 1] = fmaf(comb, (float)((hi >> (8 * k)) & 0xFFu), acc[2 * k + 1]);
       }
-      u32x4_t q[kAxRows];
-      float comb[kAxRows];
-#pragma unroll
-      for (int k = 0; k < kAxRows; ++k) {
-        const bool ok = r[k] < (uint32_t)I;  // ids past the intermediate size are skipped
-        q[k] = ok ? *reinterpret_cast<const u32x4_t *>(pt + (size_t)r[k] * (H / 2) + c / 2)
-                  : u32x4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-        comb[k] = ok ? scalars[r[k]] * bf16_to_f32(st[(size_t)r[k] * GD + c / 32]) : 0.0f;
-      }
-#pragma unroll
-      for (int k = 0; k < kAxRows; ++k)
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            acc[8 * d + e] += comb[k] * (float)((int)((q[k][d] >> (4 * e)) & 15u) - 8);
+      csum += comb;
     }
   }
-  // fold waves 1.. into wave 0 through LDS (column-major per lane)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = fmaf(-8.0f, csum, acc[e]);
   if (wave > 0) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) s_acc[wave - 1][j * 64 + lane] = acc[j];
+    for (int e = 0; e < 8; ++e) s_acc[wave - 1][e][lane] = acc[e];
   }
   __syncthreads();
-  if (wave == 0 && c < H) {
-    float *out = partial + (size_t)blockIdx.y * H + c;
+  if (wave == 0 && cok) {
 #pragma unroll
-    for (int j = 0; j < 32; j += 4) {
-      f32x4_t o;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float v = acc[j + k];
-#pragma unroll
-        for (int w = 0; w < kAxWaves - 1; ++w) v += s_acc[w][(j + k) * 64 + lane];
-        o[k] = v;
-      }
-      *reinterpret_cast<f32x4_t *>(out + j) = o;
-    }
+    for (int e = 0; e < 8; ++e)
+      acc[e] = ((acc[e] + s_acc[0][e][lane]) + s_acc[1][e][lane]) + s_acc[2][e][lane];
+    float *prow = partial + (size_t)blockIdx.y * H + c0;
+    *reinterpret_cast<f32x4_t *>(prow) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4_t *>(prow + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
   }
 }
 
-// 64 columns per block; wave w adds slices w, w + 4, ... (eight loads in
-// flight), and the four wave sums are added in wave order: deterministic.
-__global__ void __launch_bounds__(256)
-    axpy_reduce_kernel(const float *__restrict__ partial, int slices, int H, float *__restrict__ y,
-                       const uint32_t *__restrict__ n_dev, int per_slice, int overwrite) {
-  __shared__ float s_sum[4][64];
+// y[h] += sum over slices of partial[slice][h]: 64 columns per block, wave w
+// adds slices w, w + 16, ... (eight loads in flight), the sixteen wave sums
+// added in wave order: deterministic.
+__global__ void __launch_bounds__(1024)
+    axpy_reduce_kernel(const float *__restrict__ partial, int slices, int H,
+                       float *__restrict__ y) {
+  __shared__ float s_sum[16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = blockIdx.x * 64 + lane;
-  if (n_dev) slices = min(slices, (int)((*n_dev + per_slice - 1) / per_slice));
   float s = 0.0f;
   if (h < H) {
-    for (int k = wave; k < slices; k += 32) {
+    for (int k = wave; k < slices; k += 16 * 8) {
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int kk = k + 4 * j;
+        const int kk = k + 16 * j;
         v[j] = kk < slices ? partial[(size_t)kk * H + h] : 0.0f;
       }
 #pragma unroll
@@ -146,8 +147,10 @@ __global__ void __launch_bounds__(256)
   s_sum[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && h < H) {
-    const float v = ((s_sum[0][lane] + s_sum[1][lane]) + s_sum[2][lane]) + s_sum[3][lane];
-    y[h] = overwrite ? v : y[h] + v;
+    float v = s_sum[0][lane];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) v += s_sum[w][lane];
+    y[h] += v;
   }
 }
 
@@ -165,7 +168,7 @@ hipError_t transpose_requantize(const uint8_t *src, const uint8_t *src_scale_bit
 
 AxpyPlan axpy_plan(int H, int n_active) {
   AxpyPlan p;
-  p.per_slice = kAxWaves * kAxRows;
+  p.per_slice = kAxSlice;
   p.slices = n_active > 0 ? (n_active + p.per_slice - 1) / p.per_slice : 0;
   if (p.slices > 4096) {  // bound the partial rows: longer slices instead
     p.slices = 4096;
@@ -177,15 +180,14 @@ AxpyPlan axpy_plan(int H, int n_active) {
 
 hipError_t axpy_active(const uint8_t *pt, const uint8_t *st_bits, const float *scalars,
                        const uint32_t *active, int n_active, int H, int I, float *partial,
-                       float *y, hipStream_t st, const uint32_t *n_dev, bool overwrite) {
+                       float *y, hipStream_t st) {
   const AxpyPlan p = axpy_plan(H, n_active);
   if (p.slices == 0) return hipSuccess;
-  hipLaunchKernelGGL(axpy_active_kernel, dim3((H + 2047) / 2048, p.slices), dim3(64 * kAxWaves), 0,
-                     st, pt,
-                     reinterpret_cast<const uint16_t *>(st_bits), scalars, active, n_active,
-                     n_dev, p.per_slice, H, I, partial);
-  hipLaunchKernelGGL(axpy_reduce_kernel, dim3((H + 63) / 64), dim3(256), 0, st, partial,
-                     p.slices, H, y, n_dev, p.per_slice, overwrite ? 1 : 0);
+  hipLaunchKernelGGL(axpy_active_kernel, dim3((H + kAxCols - 1) / kAxCols, p.slices), dim3(256),
+                     0, st, pt, reinterpret_cast<const uint16_t *>(st_bits), scalars, active,
+                     n_active, p.per_slice, H, I, partial);
+  hipLaunchKernelGGL(axpy_reduce_kernel, dim3((H + 63) / 64), dim3(1024), 0, st, partial,
+                     p.slices, H, y);
   return hipGetLastError();
 }
 

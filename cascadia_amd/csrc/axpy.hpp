@@ -22,12 +22,8 @@ AxpyPlan axpy_plan(int H, int n_active);
 // y[H] += sum over a < n_active of scalars[active[a]] * W_t[active[a], :]
 // (ffn_axpy.rs:82-160); ids >= I are skipped; partial:
 // axpy_plan(H, n_active).partial_bytes.
-// n_dev (device, may be null): the active count when only the device knows it
-// (n_active is then its upper bound, which sizes the launch and `partial`);
-// overwrite: y = the sum instead of y += it.
 hipError_t axpy_active(const uint8_t *pt, const uint8_t *st_bits, const float *scalars,
                        const uint32_t *active, int n_active, int H, int I, float *partial,
-                       float *y, hipStream_t st, const uint32_t *n_dev = nullptr,
-                       bool overwrite = false);
+                       float *y, hipStream_t st);
 
 }  // namespace cai4
