@@ -259,6 +259,65 @@ def test_expert_forward_config1_llama_ffn(cl, orc, M):
     assert_bf16_close(got, want, f"config1 M={M}")
 
 
+FEW_SHAPES = [  # n, k, group, sdt, seq: 2..16 tokens over tiled weights, G % 128 == 0
+    (16, 128, 128, F16, 2), (130, 384, 128, F16, 5), (33, 1024, 256, BF16, 3),
+    (200, 2048, 128, BF16, 16), (50, 640, 128, F16, 7), (64, 4096, 128, F16, 8),
+    (300, 14336, 128, F16, 4), (40, 384, 128, BF16, 12),
+]
+
+
+@pytest.mark.parametrize("n,k,group,sdt,seq", FEW_SHAPES)
+def test_gemm_few_tokens_tiled(cl, orc, n, k, group, sdt, seq):
+    """2-16 token rows over MFMA-tiled weights (the skinny kernel's decode
+    path): f32 and bf16 inputs, f32 and bf16 outputs against the oracle;
+    ragged N, 1 to 112 k-blocks, groups of 128 and 256."""
+    packed, scales = weights(orc, n, k, group, sdt, 5 * n + seq)
+    pt, st = cl.tile_weights(dev(packed), dev(scales), n, k, group)
+    ys = torch.empty(seq * n, dtype=torch.float32, device="cuda")
+    xs = orc.fill_normal_f32(seq, 18, seq * k)
+    cl.dequant_gemm_int4_multi_auto(pt, st, dev(xs), n, k, seq, ys, group_size=group,
+                                    scale_dtype=sdt, tiling=cl.TILING_MFMA)
+    assert_f32_close(host(ys).reshape(seq, n),
+                     orc.gemm_multi(packed, scales, xs, n, k, seq, group, sdt),
+                     f"f32 in {n}x{k} G{group} seq{seq}")
+    xb = orc.fill_normal_bf16(seq, 19, seq * k)
+    want_b = orc.gemm_multi(packed, scales, orc.bf16_to_f32(xb), n, k, seq, group, sdt)
+    cl.dequant_gemm_int4_multi_auto(pt, st, dev(xb.view(np.int16)), n, k, seq, ys,
+                                    group_size=group, scale_dtype=sdt, tiling=cl.TILING_MFMA)
+    assert_f32_close(host(ys).reshape(seq, n), want_b, f"bf16 in {n}x{k} G{group} seq{seq}")
+    yb = torch.empty(seq * n, dtype=torch.int16, device="cuda")
+    cl.gemm_int4_bf16(pt, st, dev(xb.view(np.int16)), n, k, seq, yb, group_size=group,
+                      scale_dtype=sdt, tiling=cl.TILING_MFMA)
+    assert_bf16_close(host(yb).view(np.uint16).reshape(seq, n), orc.f32_to_bf16(want_b),
+                      f"bf16 out {n}x{k} G{group} seq{seq}")
+
+
+@pytest.mark.parametrize("M", [2, 3, 8, 16])
+def test_expert_forward_few_tokens_tiled(cl, orc, M):
+    """A tiled G128 expert at 2-16 tokens: the fused gate/up (SwiGLU into hi/lo
+    planes) and the down over those planes.  bf16 x against the crate's
+    forward (cpu_expert_forward), f32 x (the dense ffn_forward) against the
+    oracle per row."""
+    h, i, g = 512, 1024, 128
+    flat = orc.fill_bytes(4, 26, orc.expert_bytes(h, i, g))
+    offs, sizes = orc.expert_offsets(h, i, g)
+    for s_ in (1, 3, 5):
+        flat[offs[s_]:offs[s_] + sizes[s_]] = orc.fill_scales(4, 27 + s_, sizes[s_] // 2, F16).view(np.uint8)
+    W = cl.ExpertWeights(dev(flat), h, i, g, F16).tiled()
+    kw = dict(group_size=g, scale_dtype=F16, tiling=cl.TILING_MFMA)
+    xb = orc.fill_normal_bf16(M, 24, M * h)
+    out = torch.empty(M * h, dtype=torch.int16, device="cuda")
+    cl.expert_forward(dev(xb.view(np.int16).reshape(M, h)), *W.slices(), out, **kw)
+    assert_bf16_close(host(out).view(np.uint16).reshape(M, h),
+                      orc.cpu_expert_forward(xb, M, flat, h, i, g, F16), f"bf16 x M={M}")
+    xf = orc.fill_normal_f32(M, 25, M * h).reshape(M, h)
+    o32 = torch.empty((M, h), dtype=torch.float32, device="cuda")
+    cl.ffn_forward_sparse_f32(dev(xf), h, i, *W.slices(), o32, 0.0, **kw)
+    for t in range(M):
+        assert_f32_close(host(o32)[t], orc.ffn_forward_f32(xf[t], flat, h, i, g, F16, 0.0)[0],
+                         f"f32 x M={M} row {t}")
+
+
 GEMV_SHAPES = [  # n, k, group, sdt: one token, tiled weights (the one-token GEMV kernel)
     (16, 128, 128, F16), (40, 384, 128, BF16), (130, 1024, 256, F16), (33, 2304, 128, F16),
     (4096, 4096, 128, F16), (300, 14336, 128, F16), (64, 32768, 128, BF16),
