@@ -49,6 +49,20 @@ CAI4_DEV float group_sum(float t) {
   }
 }
 
+// n consecutive f32 from LDS (n * 4-byte aligned) in one read.
+template <int n>
+CAI4_DEV void lds_read_f32(const float *p, float *v) {
+  if constexpr (n == 4) {
+    const f32x4_t t = *reinterpret_cast<const f32x4_t *>(p);
+    v[0] = t[0], v[1] = t[1], v[2] = t[2], v[3] = t[3];
+  } else if constexpr (n == 2) {
+    const float2 t = *reinterpret_cast<const float2 *>(p);
+    v[0] = t.x, v[1] = t.y;
+  } else {
+    v[0] = p[0];
+  }
+}
+
 struct GvParams {
   const uint8_t *w0, *w1, *s0, *s1;
   const void *x, *x2;
@@ -113,10 +127,16 @@ CAI4_DEV void moe1_record_shared(const GvParams &a) {
 // token's down projections of all its slots with the combine.
 enum GvMode { GV_PLAIN = 0, GV_MOE_GATE_UP = 1, GV_MOE_DOWN = 2 };
 
-constexpr int kGvMaxKpw = 16;
 constexpr int kGvRing1 = 4;  // k-blocks in flight per wave: single tiles
 constexpr int kGvRing2 = 2;  // gate/up tile pairs
 constexpr int kGvWavesPerCu = 28;  // planned waves per CU
+
+// One wave's LDS region: its activation planes [planes][kpw * 128] bf16, its
+// scales as f32 [nt][kpw][16 rows][gpb] and its zero-point seeds, f32
+// [planes][kpw][gpb] (rounded up to 16 bytes).
+__host__ __device__ inline int gv_wave_bytes(int planes, int nt, int kpw, int gpb) {
+  return planes * kpw * 256 + nt * kpw * gpb * 64 + ((planes * kpw * gpb * 4 + 15) & ~15);
+}
 
 // NT: weight tiles per wave (2 = a gate/up pair, SW epilogue); AM: activation
 // mode (A_BF16, A_XF32, A_HILO; A_GATHER: f32 x rounded to bf16); RING: k-blocks in flight per wave; KPWM: most
@@ -142,8 +162,10 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   const int wis = MODE == GV_MOE_DOWN ? wave - slot * a.kw : wave;
   const int kb0 = min(wis * a.kpw, KB), kb1 = min(kb0 + a.kpw, KB), nkb = kb1 - kb0;
   const int rbytes = a.kpw * 256;                // one plane of a wave's slice
-  const int wbytes = PL * rbytes + NT * a.kpw * GPB * 32;  // + scales [NT][kpw][GPB][16] u16
-  uint8_t *reg = lds + (size_t)wave * wbytes;       // this wave's region
+  const int wbytes = gv_wave_bytes(PL, NT, a.kpw, GPB);
+  uint8_t *reg = lds + (size_t)wave * wbytes;  // this wave's region
+  float *sreg = reinterpret_cast<float *>(reg + PL * rbytes);        // scales
+  float *seeds = sreg + NT * a.kpw * 16 * GPB;                        // seeds
 
   // ---- the matrices, the x row and the output row of this workgroup ----
   const uint8_t *w0 = a.w0, *w1 = a.w1, *s0 = a.s0, *s1 = a.s1;
@@ -258,23 +280,27 @@ CAI4_DEV void gemv_body(const GvParams &a) {
     }
   }
 
-  // ---- scales of the slice: 4-byte pieces, 8 GPB per k-block and tile ----
-  constexpr int kSv = (NT * KPWM * 8 * GPB + 63) / 64;  // pieces per lane at most
-  uint32_t sv[kSv];
-  const int nsv = NT * a.kpw * 8 * GPB;
+  // ---- scales of the slice: 4-byte pieces, 8 GPB per k-block, per tile ----
+  // (a loop per tile keeps each load's descriptor uniform: a per-lane choice
+  // of descriptor would loop over its values)
+  constexpr int kSv = (KPWM * 8 * GPB + 63) / 64;  // pieces per lane and tile at most
+  uint32_t sv[NT][kSv];
+  const int per = a.kpw * 8 * GPB;  // pieces per tile
   {
     const size_t sbytes = live ? (size_t)NG * 32 : 0;
-    const buf_rsrc_t sr0 = buf_rsrc(s0 + (size_t)T * NG * 32, sbytes);
-    const buf_rsrc_t sr1 = buf_rsrc(NT == 2 ? s1 + (size_t)T * NG * 32 : s0, sbytes);
-    const int per = a.kpw * 8 * GPB;  // pieces per tile
+    const buf_rsrc_t sr[2] = {buf_rsrc(s0 + (size_t)T * NG * 32, sbytes),
+                              buf_rsrc(NT == 2 ? s1 + (size_t)T * NG * 32 : s0, sbytes)};
 #pragma unroll
-    for (int i = 0; i < kSv; ++i) {
-      const int e = lane + 64 * i, nt = e / per, q = e - nt * per, j = q / (8 * GPB);
-      const bool ok = e < nsv && j < nkb;
-      // the k-block's first group, then its GPB groups' 32-byte rows in turn
-      const uint32_t off =
-          ok ? (uint32_t)((((kb0 + j) * 128) / a.G) * 32 + 4 * (q - j * 8 * GPB)) : kBufOOB;
-      sv[i] = __builtin_amdgcn_raw_buffer_load_b32(nt == 0 ? sr0 : sr1, off, 0, 0);
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int i = 0; i < kSv; ++i) {
+        const int q = lane + 64 * i, j = q / (8 * GPB);
+        const bool ok = q < per && j < nkb;
+        // the k-block's first group, then its GPB groups' 32-byte rows in turn
+        const uint32_t off =
+            ok ? (uint32_t)((((kb0 + j) * 128) / a.G) * 32 + 4 * (q - j * 8 * GPB)) : kBufOOB;
+        sv[nt][i] = __builtin_amdgcn_raw_buffer_load_b32(sr[nt], off, 0, 0);
+      }
     }
   }
 
@@ -291,8 +317,7 @@ CAI4_DEV void gemv_body(const GvParams &a) {
 #pragma unroll
   for (int u = 0; u < RING; ++u) issue(u, kb0 + u);
 
-  // ---- activation slice -> this wave's LDS region, seeds ----
-  float seed_hi[KPWM / 4], seed_lo[KPWM / 4];
+  // ---- activation slice, its seeds and the scales -> this wave's LDS region ----
 #pragma unroll
   for (int i = 0; i < KPWM / 4; ++i) {
     const int c = lane + 64 * i;
@@ -311,18 +336,33 @@ CAI4_DEV void gemv_body(const GvParams &a) {
       hi.z = f32_to_bf16_rne(bitsf(f1.x)) | (f32_to_bf16_rne(bitsf(f1.y)) << 16);
       hi.w = f32_to_bf16_rne(bitsf(f1.z)) | (f32_to_bf16_rne(bitsf(f1.w)) << 16);
     }
+    // group of chunk c: 16 / GPB consecutive chunks (lanes) of k-block c / 16,
+    // its seed at [plane][c / (16 / GPB)]
+    const float sh = -136.f * group_sum<GPB>(sum8_bf16(hi));
+    const float sl = two ? -136.f * group_sum<GPB>(sum8_bf16(lo)) : 0.f;
     if (i * 64 < nch && c < nch) {
       *reinterpret_cast<u32x4_t *>(reg + 16 * c) = hi;
       if (two) *reinterpret_cast<u32x4_t *>(reg + rbytes + 16 * c) = lo;
+      if ((c & (16 / GPB - 1)) == 0) {
+        seeds[c / (16 / GPB)] = sh;
+        if (two) seeds[a.kpw * GPB + c / (16 / GPB)] = sl;
+      }
     }
-    // group of chunk c: 16 / GPB consecutive chunks (lanes) of k-block c / 16
-    seed_hi[i] = -136.f * group_sum<GPB>(sum8_bf16(hi));
-    seed_lo[i] = two ? -136.f * group_sum<GPB>(sum8_bf16(lo)) : 0.f;
   }
-  uint16_t *sreg = reinterpret_cast<uint16_t *>(reg + PL * rbytes);
+  // piece q of tile nt: rows 2 r, 2 r + 1 of group g of k-block j
 #pragma unroll
-  for (int i = 0; i < kSv; ++i)
-    if (lane + 64 * i < nsv) reinterpret_cast<uint32_t *>(sreg)[lane + 64 * i] = sv[i];
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int i = 0; i < kSv; ++i) {
+      const int q = lane + 64 * i, j = q / (8 * GPB);
+      const int r = q - j * 8 * GPB, g = r >> 3, row = 2 * (r & 7);
+      if (q < per) {
+        float *d = sreg + ((nt * a.kpw + j) * 16 + row) * GPB + g;
+        d[0] = scale_bits_f32(sv[nt][i], a.sdt);
+        d[GPB] = scale_bits_f32(sv[nt][i] >> 16, a.sdt);
+      }
+    }
+  }
   // own region only: no barrier, just this wave's LDS writes
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
@@ -333,51 +373,52 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   // step s of lane group lg: columns 32 lg + 8 s (GPB 1) or 32 s + 8 lg (GPB > 1)
   const uint8_t *arow = reg + (GPB > 1 ? 16 : 64) * lg + (two && lr >= 8 ? rbytes : 0);
   const bool lo_slot = two && lg >= 2;  // D rows 8-15: the lo plane
-  for (int k0 = 0; k0 < nkb; k0 += RING) {
+  const float *sdp = seeds + (lo_slot ? a.kpw * GPB : 0);
+  const float *scp = sreg + lr * GPB;
+  // Unrolled over runs of up to 8 k-blocks (one run unless KPWM is 16),
+  // leaving at the slice's end, each refill unconditional (dead past the
+  // slice): every ring load is then a value of its own.  A rolled loop, or a
+  // refill under a branch, merges ring registers at a join, and the copies
+  // that takes wait for the refill just issued.
+  constexpr int KU = KPWM < 8 ? KPWM : 8;
+#pragma nounroll
+  for (int j0 = 0; j0 < (KU < KPWM ? nkb : 1); j0 += KU) {
 #pragma unroll
-    for (int u = 0; u < RING; ++u) {
-      const int j = k0 + u;  // k-block within the slice
-      if (j < nkb) {
-        u32x4_t af[4];
+    for (int jj = 0; jj < KU; ++jj) {
+      const int j = j0 + jj;  // k-block within the slice
+      if (j >= nkb) break;    // uniform
+      const int u = jj % RING;
+      u32x4_t af[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          af[s] = *reinterpret_cast<const u32x4_t *>(arow + j * 256 + (GPB > 1 ? 64 : 16) * s);
-        // seed of group q of k-block j: lane 16 (j % 4) + q 16 / GPB of register
-        // j / 4 (uniform selection)
-        float sd[GPB];
+      for (int s = 0; s < 4; ++s)
+        af[s] = *reinterpret_cast<const u32x4_t *>(arow + j * 256 + (GPB > 1 ? 64 : 16) * s);
+      // the k-block's GPB seeds of this lane's plane, one LDS read
+      float sd[GPB];
+      lds_read_f32<GPB>(sdp + j * GPB, sd);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const u32x4_t b = GPB > 1 ? xpose_rows(ring[u][nt]) : ring[u][nt];
+        const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+        float sc[GPB];  // row lr's scales of the k-block's groups
+        lds_read_f32<GPB>(scp + (nt * a.kpw + j) * 16 * GPB, sc);
 #pragma unroll
         for (int q = 0; q < GPB; ++q) {
-          float sh = 0.f, sl = 0.f;
+          // only D row 0 (and row 8) is read: C's other rows may hold anything
+          f32x4_t p = __builtin_nondeterministic_value(f32x4_t{});
+          p[0] = sd[q];
 #pragma unroll
-          for (int i = 0; i < KPWM / 4; ++i)
-            if (i == (j >> 2)) {
-              const int ln = 16 * (j & 3) + q * (16 / GPB);
-              sh = bitsf(__builtin_amdgcn_readlane(fbits(seed_hi[i]), ln));
-              if (two) sl = bitsf(__builtin_amdgcn_readlane(fbits(seed_lo[i]), ln));
-            }
-          sd[q] = lo_slot ? sl : sh;
+          for (int s = q * (4 / GPB); s < (q + 1) * (4 / GPB); ++s)
+            p = mfma_bf16(af[s], decode8(bw[s]), p);
+          // only D row 0 (and row 8, the lo plane) is the token
+          acc[nt] += sc[q] * p[0];
         }
-        // take the slot's data, then refill it before the arithmetic: the next
-        // load is in flight while this k-block is decoded
-        u32x4_t bc[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) bc[nt] = ring[u][nt];
+      }
+      // refill the slot just decoded (its registers are free again)
+      if (KU < KPWM || jj + RING < KU) {
         issue(u, kb0 + j + RING);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const u32x4_t b = GPB > 1 ? xpose_rows(bc[nt]) : bc[nt];
-          const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-          for (int q = 0; q < GPB; ++q) {
-            const float sc = scale_bits_f32(sreg[((nt * a.kpw + j) * GPB + q) * 16 + lr], a.sdt);
-            f32x4_t p = f32x4_t{sd[q], sd[q], sd[q], sd[q]};
-#pragma unroll
-            for (int s = q * (4 / GPB); s < (q + 1) * (4 / GPB); ++s)
-              p = mfma_bf16(af[s], decode8(bw[s]), p);
-            // only D row 0 (and row 8, the lo plane) is the token
-            acc[nt] += sc * p[0];
-          }
-        }
+        // keeps the refill here: its only use is past a later exit, and a load
+        // sunk to its use is issued just before it is waited for
+        asm volatile("" ::: "memory");
       }
     }
   }
@@ -526,12 +567,12 @@ bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int ch
   const int nt = sw ? 2 : 1;
   const long n_eff = (long)a.N * (a.chunks ? max_chunks : 1);
   if (n_eff > (1L << 30)) return false;
-  const GemvPlan p = gemv_plan((int)n_eff, a.K, num_cus);  // K > 256 KB blocks: kw > 16
-  if (gpb > 1 && p.kpw > 8) return false;  // no 16-k-block instantiation for small groups
+  // K > 256 k-blocks (128 for small groups): kw > 16
+  const GemvPlan p = gemv_plan((int)n_eff, a.K, num_cus, gemv_max_kpw(gpb));
   return p.kw >= 1 && p.kw <= 16 && gemv_lds_bytes(p, amode, nt, gpb) <= kGvMaxLds;
 }
 
-GemvPlan gemv_plan(int N, int K, int num_cus) {
+GemvPlan gemv_plan(int N, int K, int num_cus, int max_kpw) {
   const int tiles = (N + 15) / 16, KB = K / 128;
   if (KB < 1 || tiles < 1 || num_cus < 1) return GemvPlan{0, 0};  // not supported
   // kGvWavesPerCu waves per CU, all resident at once (the register arrays are
@@ -542,7 +583,7 @@ GemvPlan gemv_plan(int N, int K, int num_cus) {
   if (kw < 1) kw = 1;
   if (kw > KB) kw = KB;
   int kpw = (KB + kw - 1) / kw;
-  while (kpw > kGvMaxKpw) {
+  while (kpw > max_kpw) {
     ++kw;
     kpw = (KB + kw - 1) / kw;
   }
@@ -552,15 +593,16 @@ GemvPlan gemv_plan(int N, int K, int num_cus) {
 
 size_t gemv_lds_bytes(const GemvPlan &p, int amode, int nt, int gpb) {
   const int planes = amode == A_XF32 || amode == A_HILO ? 2 : 1;
-  return (size_t)p.kw * (planes * p.kpw * 256 + nt * p.kpw * gpb * 32) +
-         (size_t)(p.kw - 1) * nt * 16 * 4 + 16;
+  return (size_t)p.kw * gv_wave_bytes(planes, nt, p.kpw, gpb) + (size_t)(p.kw - 1) * nt * 16 * 4 +
+         16;
 }
 
 hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int max_chunks,
                        hipStream_t st, const GemvSharedSlot *sh) {
   const bool sw = epi == EPI_SWIGLU || epi == EPI_SWIGLU_HILO;
   const int nch = a.chunks ? max_chunks : 1;
-  const GemvPlan p = gemv_plan(a.N * nch, a.K, num_cus);
+  const int gpb = gemv_gpb(a.G);
+  const GemvPlan p = gemv_plan(a.N * nch, a.K, num_cus, gemv_max_kpw(gpb));
   GvParams k{};
   k.w0 = a.w0;
   k.w1 = a.w1;
@@ -591,7 +633,6 @@ hipError_t gemv_launch(const SkinnyArgs &a, int amode, int epi, int num_cus, int
     k.sh_s0 = sh->s;
     k.sh_out = sh->out;
   }
-  const int gpb = gemv_gpb(a.G);
   const size_t lds = gemv_lds_bytes(p, amode, sw ? 2 : 1, gpb);
   const dim3 grid((a.N + 15) / 16, nch), block(64 * p.kw);
 #define CAI4_GV_G(NT, AM, GPB)                                                             \
@@ -636,7 +677,7 @@ GemvPlan moe1_down_plan(int I, int top_k) {
 
 size_t moe1_down_lds(const GemvPlan &p, int top_k, int gpb) {
   const int nw = top_k * p.kw;
-  return (size_t)nw * (2 * p.kpw * 256 + p.kpw * gpb * 32) + (size_t)nw * 64 + 16;
+  return (size_t)nw * gv_wave_bytes(2, 1, p.kpw, gpb) + (size_t)nw * 64 + 16;
 }
 
 }  // namespace
@@ -647,9 +688,9 @@ bool gemv_moe1_supported(int H, int I, int G, int top_k, int E, int num_cus) {
   if (top_k < 1 || top_k > kMoeMaxTopK || E < 1 || E > kMoeMaxExperts) return false;
   if ((long)I * top_k > (1L << 30)) return false;
   // with a shared-expert slot: top_k + 1 rows of two activation planes
-  const GemvPlan gu = gemv_plan(I * (top_k + 1), H, num_cus);
+  const GemvPlan gu = gemv_plan(I * (top_k + 1), H, num_cus, 8);
   if (gu.kw < 1 || gu.kw > 16 || gu.kpw > 8) return false;
-  const GemvPlan gu0 = gemv_plan(I * top_k, H, num_cus);
+  const GemvPlan gu0 = gemv_plan(I * top_k, H, num_cus, 8);
   if (gu0.kw < 1 || gu0.kw > 16 || gu0.kpw > 8) return false;
   return gemv_lds_bytes(gu, A_XF32, 2, gpb) <= kGvMaxLds &&
          gemv_lds_bytes(gu0, A_GATHER, 2, gpb) <= kGvMaxLds;
@@ -667,7 +708,7 @@ bool gemv_moe1_down_fused(int H, int I, int G, int top_k, int num_cus) {
 hipError_t gemv_moe1_gate_up(const Moe1Args &m, int num_cus, hipStream_t st) {
   const int gpb = gemv_gpb(m.G);
   const int rows = m.top_k + (m.sh == 1 ? 1 : 0);
-  const GemvPlan p = gemv_plan(m.I * rows, m.H, num_cus);
+  const GemvPlan p = gemv_plan(m.I * rows, m.H, num_cus, 8);
   GvParams k{};
   k.w0 = m.gate;
   k.s0 = m.gate_s;

@@ -19,7 +19,10 @@ struct GemvPlan {
 // (chunk_rows = 1), max_chunks of them, modes A_GATHER / A_HILO.
 bool gemv_supported(const SkinnyArgs &a, int amode, int epi, int num_cus, int chunk_rows = 0,
                     int max_chunks = 0);
-GemvPlan gemv_plan(int N, int K, int num_cus);
+// max_kpw: most k-blocks per wave the instantiations cover (16; 8 for scale
+// groups of 32 or 64 columns, gemv_max_kpw).
+GemvPlan gemv_plan(int N, int K, int num_cus, int max_kpw = 16);
+inline int gemv_max_kpw(int gpb) { return gpb > 1 ? 8 : 16; }
 // The shared expert of one MoE token as an always-on slot of a grouped launch:
 // the chunk flagged pad = 1 reads its matrix w / s and writes f32 to out.
 struct GemvSharedSlot {
