@@ -515,17 +515,24 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
       sbase[nt] = a.scale_off + (uint32_t)(((rwi * NT + nt) * ngw * 16 + lr) * 2);
 
     if (mcount > 0) {
-      for (int kb = kb0; kb < kb1; kb += U) {
+      // Whole rounds of U k-blocks with no branch between them, then the
+      // remainder (its refills would all be dead).  A refill under a branch
+      // leaves the load counts of the two paths apart at the join, and the
+      // wait there must assume the refill just issued: one load in flight.
+      int kb = kb0;
+      for (; kb + U <= kb1; kb += U) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int k = kb + u;
-          if (k < kb1) {
-            compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, k, s0, g_lo, a.K, a.G, a.glog2,
-                                   a.sdt, acc);
-            load_w<NT>(ring[u], wr, wv, k + U, wk, k + U < kb1);
-          }
+          compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
+                                 a.sdt, acc);
+          load_w<NT>(ring[u], wr, wv, kb + u + U, wk, kb + u + U < kb1);
         }
       }
+#pragma unroll
+      for (int u = 0; u < U - 1; ++u)
+        if (kb + u < kb1)
+          compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
+                                 a.sdt, acc);
     }
   };
   if constexpr (SLICED) {
