@@ -890,17 +890,17 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       (fused1 || cai4::gemv_supported(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, 1, k));
   // One token whose shared expert has the routed experts' shape (and layout):
   // its down runs as an always-on slot (f32 out) of the grouped down launch,
-  // its gate/up as a GEMV beside the routed one writing the spare hi / lo row
-  // (sh_mode 2), or as a slot of the routed gate/up launch too (1; its f32
-  // activations then set that launch's register budget);
-  // CASCADIA_INT4_MOE1_SHARED = 0 / 1 / 2 chooses, 0 = its own FFN beside.
+  // its gate/up as a slot of the routed gate/up launch too (sh_mode 1, the
+  // default: no side stream), or as a GEMV beside the routed one writing the
+  // spare hi / lo row (2); CASCADIA_INT4_MOE1_SHARED = 0 / 1 / 2 chooses,
+  // 0 = its own FFN beside.
   int sh_mode = 0;
   if (one_tok && !fused1 && has_shared(L) && L->shared_inter == L->inter &&
       L->shared.tiling == CASCADIA_INT4_TILING_MFMA &&
       cai4::gemv_supported(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, 1, k + 1)) {
     const char *ev = getenv("CASCADIA_INT4_MOE1_SHARED");
-    sh_mode = ev ? atoi(ev) : 2;
-    if (sh_mode < 0 || sh_mode > 2) sh_mode = 2;
+    sh_mode = ev ? atoi(ev) : 1;
+    if (sh_mode < 0 || sh_mode > 2) sh_mode = 1;
   }
   const bool sh_slot = sh_mode != 0;
   float *sh = nullptr;

@@ -507,15 +507,13 @@ CAI4_DEV void gemv_body(const GvParams &a) {
 // Waves per SIMD each instantiation is compiled for (its VGPR budget: 512 /
 // waves, rounded down to 8): the plan's 28 waves per CU are 7 per SIMD.  Up to
 // 4 k-blocks per wave with one scale group and one activation plane fit 64
-// VGPRs (8); each of two planes and small groups costs one wave less; 8
-// k-blocks fit 72 (7), or 80 (6) for a gate/up pair over two planes; 16 fit 80
-// (96 for that pair); the routed gate/up with small groups takes one wave less.
+// VGPRs (8), with two planes or small groups 72 (7); 8 k-blocks fit 72 (7); 16
+// fit 80 (96 for a gate/up pair over two planes).
 template <int NT, int AM, int KPWM, int GPB, int MODE, int R>
 constexpr int gv_waves_per_simd() {
   constexpr bool two = AM == A_XF32 || AM == A_HILO;
-  constexpr int routed = MODE == GV_MOE_GATE_UP && R > 0 && GPB > 1 ? 1 : 0;  // routing registers
-  if constexpr (KPWM == 4) return 8 - (two ? 1 : 0) - (GPB > 1 ? 1 : 0) - routed;
-  if constexpr (KPWM == 8) return 7 - (two && NT == 2 ? 1 : 0) - routed;
+  if constexpr (KPWM == 4) return two || GPB > 1 ? 7 : 8;
+  if constexpr (KPWM == 8) return 7;
   return two && NT == 2 ? 5 : 6;
 }
 

@@ -63,7 +63,9 @@ struct Moe1Args {
   int sh;
   const uint8_t *sh_gate, *sh_gate_s, *sh_up, *sh_up_s;
 };
-// Whether the gate/up launch routes in-kernel (else route must hold ids).
+// Whether the gate/up launch routes in-kernel (else route must hold ids): up
+// to 256 experts, 4 per lane.  (384 experts routed in every workgroup, 8 per
+// lane, measured 2.6 us per layer slower on config 4 than a routing launch.)
 inline bool gemv_moe1_routes(const MoeRouting &r, int E) { return r.mode != ROUTE_IDS && E <= 256; }
 bool gemv_moe1_supported(int H, int I, int G, int top_k, int E, int num_cus);
 // Whether the down + combine launch fits (its workgroups of top_k slots each
