@@ -239,15 +239,35 @@ def test_sparse_tau_zero_matches_dense(orc):
     assert frac == 1.0 and np.array_equal(dense, sparse)
 
 
-def test_sparse_tau_small_close_to_dense(orc):
-    h = i = 32
-    flat = fake_expert(h, i)
-    x = orc.f32_to_bf16(np.arange(h, dtype=np.float32) * np.float32(0.05) - np.float32(0.5))
-    dense = orc.bf16_to_f32(orc.expert_forward(x, flat, h, i, 32, BF16))
-    sp, frac = orc.expert_forward_sparse(x, flat, h, i, 32, BF16, 0.10)
-    sp = orc.bf16_to_f32(sp)
-    assert 0.0 < frac <= 1.0
-    assert np.max(np.abs(dense - sp)) < np.max(np.abs(dense)) * 2 + 1
+@pytest.mark.parametrize("tau", [0.1, 0.3])
+def test_sparse_tau_matches_masked_dense(orc, tau):
+    """ffn_sparsity.rs:499-537, 756-867: at tau > 0 the output is the dense FFN
+    with the intermediate lanes whose |silu(gate)| is under tau * max zeroed
+    (numpy f64 over the pinned GEMVs), and the active fraction counts those
+    kept.  Random codes and scales, so the mask splits the lanes."""
+    h, i, g = 64, 96, 32
+    offs, sizes = orc.expert_offsets(h, i, g)
+    flat = orc.fill_bytes(5, 1, offs[5] + sizes[5])
+    for j in (1, 3, 5):  # the three scale sections
+        flat[offs[j]:offs[j] + sizes[j]] = orc.fill_scales(5, 10 + j, sizes[j] // 2, BF16).view(np.uint8)
+    x = orc.f32_to_bf16(orc.fill_normal_f32(5, 20, h))
+    xf = orc.bf16_to_f32(x)
+    gate = orc.gemv(flat[offs[0]:offs[1]], flat[offs[1]:offs[2]], xf, i, h, g, BF16)
+    up = orc.gemv(flat[offs[2]:offs[3]], flat[offs[3]:offs[4]], xf, i, h, g, BF16)
+    silu = gate.astype(np.float64) / (1.0 + np.exp(-gate.astype(np.float64)))
+    keep = np.abs(silu) >= tau * np.max(np.abs(silu))
+    assert 0 < keep.sum() < i  # the mask splits the lanes
+    m = np.where(keep, silu * up, 0.0)
+    dq = orc.dequant(flat[offs[4]:offs[5]], flat[offs[5]:], h, i, g, BF16).astype(np.float64)
+    want = dq @ m
+    got, frac = orc.expert_forward_sparse(x, flat, h, i, g, BF16, tau)
+    assert frac == pytest.approx(keep.sum() / i)
+    got = orc.bf16_to_f32(got).astype(np.float64)
+    # bf16 output: within a few bf16 ulps of the f64 reference
+    assert np.max(np.abs(got - want)) <= 2.0 ** -6 * np.max(np.abs(want))
+    # and the lanes masked out matter: the dense output differs
+    dense = orc.bf16_to_f32(orc.expert_forward(x, flat, h, i, g, BF16)).astype(np.float64)
+    assert np.max(np.abs(dense - want)) > 2.0 ** -6 * np.max(np.abs(want))
 
 
 def test_ffn_f32_tau_zero_matches_inline_dense(orc):
