@@ -178,6 +178,11 @@ CAI4_DEV buf_rsrc_t buf_rsrc(const void *base, size_t bytes) {
 CAI4_DEV u32x4_t buf_load16(buf_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// The same load marked non-temporal (the cache-policy operand's bit 1: `nt`
+// on gfx950): for weight bytes read once per call.
+CAI4_DEV u32x4_t buf_load16_nt(buf_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
 
 template <int CTRL>
 CAI4_DEV float dpp_f32(float v) {
