@@ -440,6 +440,10 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   }
 
   if constexpr (MODE == GV_MOE_DOWN) {
+    // (no multiply-add contraction: the crate rounds w * y, then the sum, as
+    // moe_combine_kernel does.  __fmul_rn / __fadd_rn are plain operators
+    // defined outside this scope, which the contraction would still fuse)
+#pragma clang fp contract(off)
     // ---- every slot's partials -> y_k (RNE bf16) -> the combine in slot order
     // (runner.rs:1806-1832: moe += w * y, multiply then add; h = residual +
     // shared + moe), as moe_combine_kernel does for more tokens ----
@@ -449,17 +453,17 @@ CAI4_DEV void gemv_body(const GvParams &a) {
     const int r16 = 16 * T + lr;
     if (r16 >= a.N) return;
     float h = a.residual ? a.residual[r16] : 0.f;
-    if (a.shared) h = __fadd_rn(h, a.shared[r16]);
+    if (a.shared) h = h + a.shared[r16];
     float moe = 0.f;
     for (int kk = 0; kk < a.top_k; ++kk) {
       if (a.pos[kk] < 0) continue;
       float y = 0.f;
       for (int v = 0; v < a.kw; ++v) y += red[(kk * a.kw + v) * 16 + lr];
-      moe = __fadd_rn(moe, __fmul_rn(a.wts[kk], bf16_to_f32(f32_to_bf16_rne(y))));
+      moe = moe + a.wts[kk] * bf16_to_f32(f32_to_bf16_rne(y));
     }
     // the whole combine, or the weighted expert sum only (residual and shared
     // added later, in the same order)
-    reinterpret_cast<float *>(a.out)[r16] = a.moe_partial ? moe : __fadd_rn(h, moe);
+    reinterpret_cast<float *>(a.out)[r16] = a.moe_partial ? moe : h + moe;
     return;
   }
 
