@@ -789,7 +789,8 @@ MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint
     return m;
   }
   // routing picks distinct experts per token; given ids may repeat one
-  const int C = cai4::moe_chunk_rows((int)T, given_ids ? (int)(T * top_k) : (int)T);
+  const int C = cai4::moe_chunk_rows((int)T, given_ids ? (int)(T * top_k) : (int)T,
+                                     L->tiling == CASCADIA_INT4_TILING_MFMA);
   const int maxc = cai4::moe_max_chunks((int)T, (int)L->n_experts, (int)top_k, C);
   m.gu = cai4::skinny_plan_grouped(I, H, G, C, maxc, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, d);
   m.dn = cai4::skinny_plan_grouped(H, I, G, C, maxc, cai4::A_HILO, cai4::EPI_BF16, d);

@@ -34,13 +34,19 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // and 4: 16 rows beat 32 at 256 tokens (config 3 598 -> 432 us per layer: the
 // 32-row down ran 8 waves per CU); 8 rows beat 16 at 32 tokens on config 3
 // (-6 %) but lost 16 % at 64 tokens on config 4, whose skewed routing gives
-// its hot experts many rows -- so 16 from 9 tokens up.
-int moe_chunk_rows(int T, int per_expert_max) {
+// its hot experts many rows -- so 16 from 9 tokens up.  With at most two rows
+// per expert and tiled experts (gemv_rows), one-row chunks on the grouped
+// one-token GEMV: two routed tokens, config 3 40.1 -> 37.3 us per layer,
+// config 4 (Zipf-skewed routing) 101.5 -> 100.4; at four tokens skewed routing
+// already lost 15 % that way (a hot expert streams once per row).
+int moe_chunk_rows(int T, int per_expert_max, bool gemv_rows) {
   // override 1 .. 32 (a 32-row chunk is the most one pass of the two-plane
   // down projection holds)
   const char *e = getenv("CASCADIA_INT4_MOE_CHUNK_ROWS");
   const int ev = e ? atoi(e) : 0;
-  const int c = ev >= 1 && ev <= 32 ? ev : T <= 8 ? 8 : 16;
+  const int c = ev >= 1 && ev <= 32 ? ev
+                : gemv_rows && per_expert_max <= 2 ? 1
+                : T <= 8 ? 8 : 16;
   return per_expert_max < c ? per_expert_max : c;
 }
 

@@ -50,7 +50,8 @@ int moe_tile_rows();
 
 // Rows per grouped chunk for T tokens, no expert receiving more than
 // per_expert_max of them (T when routing picks distinct experts per token).
-int moe_chunk_rows(int T, int per_expert_max);
+// gemv_rows: tiled experts (one-row chunks can run on the one-token GEMV).
+int moe_chunk_rows(int T, int per_expert_max, bool gemv_rows = false);
 // Upper bound on grouped chunks.
 int moe_max_chunks(int T, int E, int top_k, int chunk_rows);
 

@@ -198,7 +198,7 @@ def config4(cl, orc):
     return Layer(cl, orc, 384, 7168, 2048, 32, F16, 71, 2048)
 
 
-@pytest.mark.parametrize("T", [1, 8, 64, 1024])
+@pytest.mark.parametrize("T", [1, 2, 8, 64, 1024])
 def test_config4_moe_full(cl, orc, config4, T):
     """Kimi-K2 shape, one pipeline stage: 384 routed experts + 1 shared, H 7168,
     I 2048, G32 fp16, sigmoid routing renormalised x 2.827 over Zipf(1.1)

@@ -152,7 +152,7 @@ def test_routing_matches_oracle(cl, orc, E, k, mode, ties, T):
     assert np.all(np.abs(got_w.astype(np.float64) - want_w) <= 4 * ulp), "routing weights differ"
 
 
-@pytest.mark.parametrize("T", [1, 5, 40, 80])
+@pytest.mark.parametrize("T", [1, 2, 5, 40, 80])
 @pytest.mark.parametrize("mode,shared_inter,tiled,thr", [(1, 64, True, 0.0), (2, 0, True, 0.0),
                                                           (1, 0, False, 0.0), (2, 96, False, 0.2)])
 def test_moe_layer_small(cl, orc, T, mode, shared_inter, tiled, thr):
@@ -296,7 +296,7 @@ def test_moe_given_ids_and_determinism(cl, orc, T):
     check_layer(orc, a, x, blob, None, 0, E, h, i, g, F16, ids, w, 0.0, "given ids")
 
 
-@pytest.mark.parametrize("T", [1, 8])
+@pytest.mark.parametrize("T", [1, 2, 8])
 def test_moe_config3_minimax_shape(cl, orc, T):
     """Config 3 dims (H 3072, I 1536, G128 fp16, softmax over the top 8) on a
     64-expert subset."""
@@ -315,10 +315,12 @@ def test_moe_config3_minimax_shape(cl, orc, T):
                 f"config3 T={T}")
 
 
-def test_moe_config4_kimi_shape(cl, orc):
+@pytest.mark.parametrize("T", [2, 3])
+def test_moe_config4_kimi_shape(cl, orc, T):
     """Config 4 dims (H 7168, I 2048, G32 fp16, sigmoid routing renormalised
-    x 2.827, one shared expert) on a 24-expert subset, Zipf-skewed logits."""
-    E, k, h, i, g, T = 24, 8, 7168, 2048, 32, 3
+    x 2.827, one shared expert) on a 24-expert subset, Zipf-skewed logits; two
+    tokens run as one-row chunks on the grouped one-token GEMV."""
+    E, k, h, i, g = 24, 8, 7168, 2048, 32
     blob, shared, ex = build(cl, orc, E, h, i, g, F16, 41, shared_inter=2048)
     perm = np.random.default_rng(1).permutation(E)
     logits = (-1.1 * np.log1p(perm)[None, :] + orc.fill_normal_f32(42, T, T * E).reshape(T, E)).astype(np.float32)
