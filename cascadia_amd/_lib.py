@@ -76,6 +76,7 @@ _MP, _RP = C.POINTER(MoeLayer), C.POINTER(Routing)
 SIGNATURES = {
     "cascadia_int4_version": (C.c_char_p, []),
     "cascadia_int4_synchronize": (_i32, [_vp]),
+    "cascadia_int4_reload_tuning": (None, []),
     "cascadia_int4_dequant_gemv": (_i32, [_LP, _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_dequant_gemm_multi": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
     "cascadia_int4_dequant_gemm_bf16in": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),

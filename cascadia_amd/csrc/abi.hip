@@ -21,6 +21,7 @@
 #include "skinny.hpp"
 #include "sparse.hpp"
 #include "synth.hpp"
+#include "tuning.hpp"
 
 namespace {
 
@@ -31,6 +32,8 @@ struct DeviceState {
   size_t max_lds = 0;
   void *ws = nullptr;  // library-owned workspace (grow-only)
   size_t ws_bytes = 0;
+  void **retired = nullptr;  // earlier, smaller workspaces: held, never freed
+  size_t n_retired = 0;
   hipStream_t side = nullptr;  // second stream for independent work (default priority)
   hipEvent_t fork = nullptr, join = nullptr;
 };
@@ -112,10 +115,14 @@ int side_stream(int dev, hipStream_t *side, hipEvent_t *fork, hipEvent_t *join) 
 }
 
 // Library workspace of at least `bytes` on the current device.  Growing it
-// synchronises the device and frees the old buffer, which a stream capture
-// cannot record (and a captured graph may still use the old buffer): while
-// `st` is capturing, a call that would grow it is refused with ERR_ARG (pass
-// a workspace of the *_workspace_bytes size instead).
+// allocates a larger buffer (at least twice the old size) and RETIRES the old
+// one without freeing it: a graph captured while the old buffer was current
+// keeps its address in its kernel arguments and stays valid to replay.
+// Retired buffers are held until the process ends (their total stays below
+// the current buffer's size, since each growth at least doubles).  A growth
+// cannot be recorded by a stream capture: while `st` is capturing, a call that
+// would grow the workspace is refused with ERR_ARG (pass a workspace of the
+// *_workspace_bytes size instead).
 int lib_workspace(int dev, size_t bytes, void **out, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState &d = g_dev[dev];
@@ -123,17 +130,30 @@ int lib_workspace(int dev, size_t bytes, void **out, hipStream_t st) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
       return CASCADIA_INT4_ERR_ARG;
-    if (d.ws) {
-      if (hipDeviceSynchronize() != hipSuccess) return CASCADIA_INT4_ERR_DEVICE;
-      (void)hipFree(d.ws);
-      d.ws = nullptr;
-      d.ws_bytes = 0;
-    }
     size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
-    if (hipMalloc(&d.ws, sz) != hipSuccess) {
-      d.ws = nullptr;
-      return CASCADIA_INT4_ERR_NOMEM;
+    if (sz < 2 * d.ws_bytes) sz = 2 * d.ws_bytes;
+    void *p = nullptr;
+    if (hipMalloc(&p, sz) != hipSuccess) {
+      (void)hipGetLastError();
+      // the doubling is a preference, the request is the requirement
+      p = nullptr;
+      sz = bytes;
+      if (hipMalloc(&p, sz) != hipSuccess) {
+        (void)hipGetLastError();
+        return CASCADIA_INT4_ERR_NOMEM;
+      }
     }
+    if (d.ws) {
+      // kept alive, never reused: captured graphs may still address it
+      void **grown = static_cast<void **>(realloc(d.retired, (d.n_retired + 1) * sizeof(void *)));
+      if (!grown) {
+        (void)hipFree(p);
+        return CASCADIA_INT4_ERR_NOMEM;
+      }
+      d.retired = grown;
+      d.retired[d.n_retired++] = d.ws;
+    }
+    d.ws = p;
     d.ws_bytes = sz;
   }
   *out = d.ws;
@@ -229,8 +249,7 @@ int run_gemm(const uint8_t *w0, const uint8_t *s0, const uint8_t *w1, const uint
 // 512 rows at the K2.6 and Llama-3-8B FFN shapes; below, too few workgroups).
 // CASCADIA_INT4_FFN_TILE_TOKENS overrides.
 uint32_t ffn_tile_tokens() {
-  const char *e = getenv("CASCADIA_INT4_FFN_TILE_TOKENS");
-  const int n = e ? atoi(e) : 0;
+  const int n = cai4::tuning_env("CASCADIA_INT4_FFN_TILE_TOKENS", 0);
   return n > 0 ? (uint32_t)n : 512u;
 }
 
@@ -659,8 +678,7 @@ void expert_blob_sections(uint32_t hidden, uint32_t inter, uint32_t group, uint3
 // MFMA-tile GEMM of grouped.hip (any G of 32, 64, 128k; CASCADIA_INT4_PREFILL_TILES=1
 // takes it for every shape).
 bool prefill_tiles(const cascadia_int4_layout *L) {
-  const char *e = getenv("CASCADIA_INT4_PREFILL_TILES");
-  return (e && atoi(e) > 0) || L->group_size % 128 != 0;
+  return cai4::tuning_env("CASCADIA_INT4_PREFILL_TILES", 0) > 0 || L->group_size % 128 != 0;
 }
 
 // Prefill GEMM (M >= 64 tokens, MFMA-tiled weights).
@@ -899,8 +917,7 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   if (one_tok && !fused1 && has_shared(L) && L->shared_inter == L->inter &&
       L->shared.tiling == CASCADIA_INT4_TILING_MFMA &&
       cai4::gemv_supported(dn1, cai4::A_HILO, cai4::EPI_BF16, d.num_cus, 1, k + 1)) {
-    const char *ev = getenv("CASCADIA_INT4_MOE1_SHARED");
-    sh_mode = ev ? atoi(ev) : 1;
+    sh_mode = cai4::tuning_env("CASCADIA_INT4_MOE1_SHARED", 1);
     if (sh_mode < 0 || sh_mode > 2) sh_mode = 1;
   }
   const bool sh_slot = sh_mode != 0;

@@ -22,6 +22,7 @@
 #include "int4_common.hpp"
 #include "moe.hpp"
 #include "moe_route.hpp"
+#include "tuning.hpp"
 
 namespace cai4 {
 
@@ -42,8 +43,7 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 int moe_chunk_rows(int T, int per_expert_max, bool gemv_rows) {
   // override 1 .. 32 (a 32-row chunk is the most one pass of the two-plane
   // down projection holds)
-  const char *e = getenv("CASCADIA_INT4_MOE_CHUNK_ROWS");
-  const int ev = e ? atoi(e) : 0;
+  const int ev = tuning_env("CASCADIA_INT4_MOE_CHUNK_ROWS", 0);
   const int c = ev >= 1 && ev <= 32 ? ev
                 : gemv_rows && per_expert_max <= 2 ? 1
                 : T <= 8 ? 8 : 16;
@@ -51,14 +51,12 @@ int moe_chunk_rows(int T, int per_expert_max, bool gemv_rows) {
 }
 
 int moe_tile_tokens() {
-  const char *e = getenv("CASCADIA_INT4_MOE_TILE_TOKENS");
-  const int n = e ? atoi(e) : 0;
+  const int n = tuning_env("CASCADIA_INT4_MOE_TILE_TOKENS", 0);
   return n > 0 ? n : 512;
 }
 
 int moe_tile_rows() {
-  const char *e = getenv("CASCADIA_INT4_MOE_TILE_ROWS");
-  const int n = e ? atoi(e) : 0;
+  const int n = tuning_env("CASCADIA_INT4_MOE_TILE_ROWS", 0);
   return n > 0 ? n : 48;
 }
 
@@ -95,7 +93,9 @@ MoeWorkspace moe_workspace(int T, int H, int I, int E, int top_k, int chunk_rows
   w.counts = take(16);
   w.hi = take((n + 1) * I * 2);
   w.lo = take((n + 1) * I * 2);
-  w.y = take(n * H * 2);
+  // [n, H] bf16 expert outputs; a one-token layer with a shared expert also
+  // keeps its [H] f32 routed sum here, which is larger when top_k is 1
+  w.y = take(n * H * 2 > (size_t)H * 4 ? n * H * 2 : (size_t)H * 4);
   w.shared = take(shared_bytes);
   w.part = take(part_bytes);
   w.shared_ws = take(shared_ws_bytes);

@@ -51,6 +51,7 @@
 
 #include "int4_common.hpp"
 #include "skinny.hpp"
+#include "tuning.hpp"
 
 namespace cai4 {
 
@@ -632,26 +633,24 @@ __global__ __launch_bounds__(1024) void splitk_reduce_kernel(KParams a, int kspl
 namespace {
 
 int env_int(const char *name, int lo, int hi) {
-  if (const char *ev = getenv(name)) {
-    const int v = atoi(ev);
-    if (v >= lo && v <= hi) return v;
-  }
-  return 0;
+  const int v = tuning_env(name, 0);
+  return v >= lo && v <= hi ? v : 0;
 }
 
 size_t round16(size_t v) { return (v + 15) & ~(size_t)15; }
 
 // Plan overrides: CASCADIA_INT4_SKINNY_{RW,KSPLIT,WAVES} for every plan,
 // CASCADIA_INT4_GROUPED_{RW,KSPLIT,WAVES} for grouped (MoE) plans only, taking
-// precedence there.
-int plan_env(const char *what, bool grouped, int lo, int hi) {
-  char name[64];
-  if (grouped) {
-    snprintf(name, sizeof name, "CASCADIA_INT4_GROUPED_%s", what);
-    if (int v = env_int(name, lo, hi)) return v;
-  }
-  snprintf(name, sizeof name, "CASCADIA_INT4_SKINNY_%s", what);
-  return env_int(name, lo, hi);
+// precedence there.  `what` is 0 (RW), 1 (KSPLIT) or 2 (WAVES).
+int plan_env(int what, bool grouped, int lo, int hi) {
+  static const char *const kGrouped[3] = {"CASCADIA_INT4_GROUPED_RW",
+                                          "CASCADIA_INT4_GROUPED_KSPLIT",
+                                          "CASCADIA_INT4_GROUPED_WAVES"};
+  static const char *const kSkinny[3] = {"CASCADIA_INT4_SKINNY_RW", "CASCADIA_INT4_SKINNY_KSPLIT",
+                                         "CASCADIA_INT4_SKINNY_WAVES"};
+  if (grouped)
+    if (int v = env_int(kGrouped[what], lo, hi)) return v;
+  return env_int(kSkinny[what], lo, hi);
 }
 
 }  // namespace
@@ -713,7 +712,7 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   const bool grouped = m_chunks > 0;
   int ks_min = 0;
   const bool dense_auto =
-      !grouped && !plan_env("RW", false, 1, 16) && !plan_env("KSPLIT", false, 1, 64);
+      !grouped && !plan_env(0, false, 1, 16) && !plan_env(1, false, 1, 64);
   auto dense_window = [&](bool fewest_rows, int *rw_out, int *ks_out) {
     constexpr double kDenseStageBytes = 132.0 * 1024;
     const long lo = (long)d.num_cus * 7 / 8, hi = d.num_cus;
@@ -744,7 +743,7 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
       ks_min = ks;
     }
   }
-  if (int v = plan_env("RW", grouped, 1, 16)) rw = v <= maxw ? v : maxw;
+  if (int v = plan_env(0, grouped, 1, 16)) rw = v <= maxw ? v : maxw;
   p.rw = rw;
   p.row_blocks = (int)((units + rw - 1) / rw);
   long wgs0 = (long)p.row_blocks * p.m_chunks;
@@ -757,8 +756,8 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
     const size_t st = round16(act) + sc;
     return st > red ? st : red;
   };
-  const int ks_env = plan_env("KSPLIT", grouped, 1, 64);
-  const int kw_env = plan_env("WAVES", grouped, 1, 16);
+  const int ks_env = plan_env(1, grouped, 1, 64);
+  const int kw_env = plan_env(2, grouped, 1, 16);
   // K decomposition.  Split K across workgroups when fewer than half the CUs
   // would get a workgroup (the reduce launch costs more than that), and --
   // unsliced -- also when the staging does not fit in LDS; or (sliced) stage

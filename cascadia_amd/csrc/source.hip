@@ -586,8 +586,18 @@ int cascadia_int4_open_source(const char *model_dir, CascadiaInt4Source **out_ha
       return -3;
     s->int4_bin = true;
     s->bin_hidden = (uint32_t)hs->num;
-    s->bin_inter = ei && ei->kind == Json::NUM && ei->num > 0 ? (uint32_t)ei->num : 2048u;
-    if (s->bin_hidden % 32 || s->bin_inter % 32 || s->bin_inter > (1u << 20)) return -3;
+    if (!ei) {
+      // no expert_intermediate: the K2.6 runner's reader, whose
+      // ExpertWeights::open is fixed to HIDDEN x INTERMEDIATE = 7168 x 2048
+      // (runner.rs:697-705, format.rs:63, lib.rs:71-78)
+      if (s->bin_hidden != 7168u) return -3;
+      s->bin_inter = 2048u;
+    } else {
+      // ov_moe.rs:452-457: int4_bin requires expert_intermediate > 0
+      if (ei->kind != Json::NUM || !(ei->num >= 1) || ei->num > (double)(1u << 20)) return -3;
+      s->bin_inter = (uint32_t)ei->num;
+    }
+    if (s->bin_hidden % 32 || s->bin_inter % 32) return -3;
   } else {
     Json idx;
     if (!read_file(s->dir + "/model.safetensors.index.json", text) || !parse_json(text, idx))

@@ -26,12 +26,16 @@
  *   - Outputs are fully overwritten, as in the crate.  Calls are reentrant
  *     for distinct output buffers; a shared workspace (workspace == NULL, the
  *     library's own) makes concurrent calls on different streams race.
- *   - HIP graph capture: the library's own workspace grows by a device
- *     synchronisation and a reallocation, which a capture cannot record; a
- *     call on a capturing stream that would grow it returns
- *     CASCADIA_INT4_ERR_ARG.  Callers that capture pass a workspace of the
- *     matching *_workspace_bytes size (or warm the library's up first, or use
- *     cascadia_int4_expert_forward_noalloc).
+ *   - HIP graph capture: the library's own workspace grows by an allocation,
+ *     which a capture cannot record; a call on a capturing stream that would
+ *     grow it returns CASCADIA_INT4_ERR_ARG.  Callers that capture pass a
+ *     workspace of the matching *_workspace_bytes size, or use
+ *     cascadia_int4_expert_forward_noalloc, or warm the library's workspace
+ *     with an eager call of the same shape first.  A growth never frees the
+ *     buffer it replaces (the library keeps it until the process ends), so a
+ *     graph captured on the smaller buffer stays valid after a later, larger
+ *     eager call; it still shares that buffer with any eager call, so replays
+ *     and eager calls that use the library's workspace must not overlap.
  */
 #ifndef CASCADIA_INT4_H
 #define CASCADIA_INT4_H
@@ -93,6 +97,12 @@ const char *cascadia_int4_version(void);
 
 /* Wait for all work enqueued on `stream`. */
 int cascadia_int4_synchronize(void *stream);
+
+/* The launch-plan overrides CASCADIA_INT4_* (tuning and tests only; every
+ * default is measured) are read from the environment once per process, at the
+ * first call that needs each; this makes the next calls read them again.  No
+ * counterpart in the crate, which has no plan overrides. */
+void cascadia_int4_reload_tuning(void);
 
 /* y[r] = sum_c (nibble[r,c]-8) * scale[r, c/G] * x[c] for one f32 vector.
  * Replaces dequant_gemv_int4 (src/kernel.rs:31-71) and

@@ -695,7 +695,8 @@ float or_ffn_forward_sparse_axpy_f32_mode(const float *x, size_t hidden, size_t 
     const float a = fabsf(sg[i]);
     if (a > max_abs) max_abs = a;
   }
-  int dense = thresholds ? 1 : !(tau > 0.0f);
+  /* SparsityMode::is_dense (ffn_sparsity.rs:85-90): tau <= 0, so a NaN tau is sparse */
+  int dense = thresholds ? 1 : tau <= 0.0f;
   if (thresholds)
     for (size_t i = 0; i < inter; i++)
       if (!(thresholds[i] <= 0.0f)) dense = 0;

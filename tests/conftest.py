@@ -23,6 +23,25 @@ def orc():
     return oracle
 
 
+@pytest.fixture
+def tuning(monkeypatch):
+    """Set a CASCADIA_INT4_* tuning variable for one test: tuning(name, value).
+    The library reads those variables once per process, so every change is
+    followed by cascadia_int4_reload_tuning(); teardown restores the
+    environment and reloads again, so no setting leaks into later tests."""
+    import cascadia_amd
+
+    L = cascadia_amd.lib()
+
+    def setenv(name, value):
+        monkeypatch.setenv(name, str(value))
+        L.cascadia_int4_reload_tuning()
+
+    yield setenv
+    monkeypatch.undo()
+    L.cascadia_int4_reload_tuning()
+
+
 def rel_l2(got, want) -> float:
     got = np.asarray(got, np.float64).ravel()
     want = np.asarray(want, np.float64).ravel()

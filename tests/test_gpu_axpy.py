@@ -163,3 +163,39 @@ def test_capture_refuses_library_workspace_growth(cl, orc):
         assert torch.equal(y, y_eager), f"replay {rep}"
     # 0x99: codes 1, scale 1.0, each of 100 active rows adds 1
     assert float(y_eager[0]) == 100.0
+
+
+def test_capture_on_library_workspace_survives_growth(cl, orc):
+    """A graph captured on the library's own (already large enough) workspace
+    keeps replaying the eager result after a later, larger eager call has
+    grown that workspace: the growth keeps the old buffer alive instead of
+    freeing it under the graph.  Torch allocations made after the growth
+    must not alias the captured buffer either, so the replay's result is
+    compared after fresh allocations have been written."""
+    h, i = 4096, 64
+    pt = dev(orc.fill_bytes(6, 90, i * h // 2))
+    st = dev(np.full(i * (h // 32), 0x3F80, np.uint16).view(np.uint8))
+    s = torch.linspace(-1.0, 1.0, i, dtype=torch.float32, device="cuda")
+    small = torch.arange(0, i, 3, dtype=torch.int32, device="cuda")
+    y_eager = torch.zeros(h, dtype=torch.float32, device="cuda")
+    cl.dequant_axpy_int4_active(pt, st, s, small, i, h, y_eager)  # warms the workspace
+    y = torch.zeros(h, dtype=torch.float32, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            cl.dequant_axpy_int4_active(pt, st, s, small, i, h, y)
+    torch.cuda.current_stream().wait_stream(side)
+    # a much larger eager call grows the library workspace past the captured one
+    big = torch.zeros(1 << 18, dtype=torch.int32, device="cuda")
+    y_big = torch.zeros(h, dtype=torch.float32, device="cuda")
+    cl.dequant_axpy_int4_active(pt, st, s, big, i, h, y_big)
+    torch.cuda.synchronize()
+    junk = [torch.full((1 << 22,), 7.0, device="cuda") for _ in range(8)]
+    for rep in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager), f"replay {rep} after growth"
+    assert all(float(j[-1]) == 7.0 for j in junk), "a replay wrote into later allocations"

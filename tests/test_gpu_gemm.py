@@ -143,12 +143,12 @@ PLANS = [  # forced launch plans: row groups, waves per workgroup, split-K
 @pytest.mark.parametrize("plan", range(len(PLANS)))
 @pytest.mark.parametrize("n,k,group,sdt,seq", [(96, 1536, 32, BF16, 8), (130, 1152, 128, F16, 17),
                                                 (300, 2048, 64, F16, 1), (64, 4096, 128, F16, 40)])
-def test_forced_launch_plans(cl, orc, monkeypatch, plan, n, k, group, sdt, seq):
+def test_forced_launch_plans(cl, orc, tuning, plan, n, k, group, sdt, seq):
     """Every decomposition (row groups sharing staged activations, k-spans per
     workgroup, split-K across workgroups + the reduce kernel) matches the
     oracle, for both weight layouts and all activation kinds."""
     for key, val in PLANS[plan].items():
-        monkeypatch.setenv(key, val)
+        tuning(key, val)
     packed, scales = weights(orc, n, k, group, sdt, 3 * n + seq)
     P, S = dev(packed), dev(scales)
     pt, st = cl.tile_weights(P, S, n, k, group)
@@ -167,10 +167,10 @@ def test_forced_launch_plans(cl, orc, monkeypatch, plan, n, k, group, sdt, seq):
 
 
 @pytest.mark.parametrize("plan", range(len(PLANS)))
-def test_forced_launch_plans_expert(cl, orc, monkeypatch, plan):
+def test_forced_launch_plans_expert(cl, orc, tuning, plan):
     """The fused gate/up (SwiGLU, hi/lo planes) and down kernels under forced plans."""
     for key, val in PLANS[plan].items():
-        monkeypatch.setenv(key, val)
+        tuning(key, val)
     h, i, g, M = 1024, 768, 64, 6
     flat = orc.fill_bytes(5, 50, orc.expert_bytes(h, i, g))
     offs, sizes = orc.expert_offsets(h, i, g)

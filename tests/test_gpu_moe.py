@@ -217,6 +217,28 @@ def test_moe_one_token_given_ids(cl, orc, k, thr):
                 f"one token given ids k={k} thr={thr}")
 
 
+@pytest.mark.parametrize("h,shared_inter", [(256, 64), (1024, 256), (4096, 512)])
+def test_moe_one_token_top1_shared(cl, orc, h, shared_inter):
+    """One token, top-1 routing and a tiled shared expert, hidden <= 4096: the
+    fused down + combine launch writes the routed sum ([hidden] f32) into the
+    expert-output region while the shared expert runs beside it; at top_k 1
+    that region must still hold hidden f32 values without reaching the shared
+    expert's output."""
+    E, k, i, g, T = 8, 1, 128, 32, 1
+    blob, shared, ex = build(cl, orc, E, h, i, g, F16, 51, shared_inter, True)
+    logits = orc.fill_normal_f32(52, T, T * E).reshape(T, E)
+    x = orc.fill_normal_f32(53, T, T * h).reshape(T, h)
+    xd = dev(x)
+    ids_o = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w_o = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    for rep in range(3):
+        out = torch.empty((T, h), dtype=torch.float32, device="cuda")
+        cl.moe_forward(ex, xd, out, top_k=k, logits=dev(logits), mode=cl.ROUTE_SIGMOID_BIAS,
+                       scale=1.0, normalize=False, residual=xd, ids_out=ids_o, weights_out=w_o)
+        check_layer(orc, host(out), x, blob, shared, shared_inter, E, h, i, g, F16, host(ids_o),
+                    host(w_o), 0.0, f"top-1 one token h={h} shared={shared_inter} call {rep}")
+
+
 @pytest.mark.parametrize("E,shared_inter,mode", [(300, 128, 1), (300, 0, 2), (40, 128, 1)])
 def test_moe_one_token_routing_launch(cl, orc, E, shared_inter, mode):
     """One token: more than 256 experts route in a launch of their own (the
@@ -246,7 +268,7 @@ def test_moe_one_token_routing_launch(cl, orc, E, shared_inter, mode):
 @pytest.mark.parametrize("sh_mode", ["0", "1", "2"])
 @pytest.mark.parametrize("E,h,i,g,mode,si", [(24, 7168, 2048, 32, 1, 256), (260, 4608, 128, 128, 1, 256),
                                              (24, 7168, 2048, 32, 1, 2048), (260, 4608, 128, 128, 1, 128)])
-def test_moe_one_token_wide_hidden(cl, orc, monkeypatch, E, h, i, g, mode, si, sh_mode):
+def test_moe_one_token_wide_hidden(cl, orc, tuning, E, h, i, g, mode, si, sh_mode):
     """One token with more 16-row output tiles than CUs (hidden > 4096): the
     gate/up launch leaves a chunk table of one row per slot, the grouped down
     and the combine kernel follow; config 4 dims (G32, shared expert) on a
@@ -254,12 +276,12 @@ def test_moe_one_token_wide_hidden(cl, orc, monkeypatch, E, h, i, g, mode, si, s
     shared expert of the routed experts' inter size runs as an always-on slot
     of both launches (f32 x as hi / lo planes, f32 out); another size runs as
     its own FFN beside them.  CASCADIA_INT4_MOE1_SHARED picks how a shared
-    expert of the routed shape runs: 1 both halves as slots, 2 (default) the
-    gate/up as a GEMV beside the routed one and the down as a slot, 0 its own
-    FFN."""
+    expert of the routed shape runs: 1 (the default) both halves as slots, 2
+    the gate/up as a GEMV beside the routed one and the down as a slot, 0 its
+    own FFN."""
     if si != i and sh_mode != "2":
         pytest.skip("the mode applies to a shared expert of the routed shape")
-    monkeypatch.setenv("CASCADIA_INT4_MOE1_SHARED", sh_mode)
+    tuning("CASCADIA_INT4_MOE1_SHARED", sh_mode)
     k, T = 8, 1
     blob, shared, ex = build(cl, orc, E, h, i, g, F16, 33, si, True)
     logits = orc.fill_normal_f32(34, T, T * E).reshape(T, E)

@@ -108,6 +108,14 @@ def test_handle_api_error_codes(tmp_path):
     assert L.cascadia_int4_open_source(str(tmp_path).encode(), C.byref(h)) == -3
     (tmp_path / "model.safetensors.index.json").write_text('{"metadata": {}}')
     assert L.cascadia_int4_open_source(str(tmp_path).encode(), C.byref(h)) == -3
+    # int4_bin manifests: expert_intermediate 0 is refused (ov_moe.rs:452-457),
+    # and without it only the K2.6 reader's fixed 7168 hidden is accepted
+    # (runner.rs:697-705 over format.rs:63)
+    for inter, hidden in ((0, 3072), (0, 7168), (None, 3072)):
+        d = tmp_path / f"bin_{inter}_{hidden}"
+        d.mkdir()
+        write_int4_bin(str(d), hidden, inter, {}, with_inter=inter is not None)
+        assert L.cascadia_int4_open_source(str(d).encode(), C.byref(h)) == -3, (inter, hidden)
     assert L.cascadia_int4_prewarm(None, 0, 0) == -1
     assert L.cascadia_int4_expert_forward(None, 0, 0, None, None) == -1
     L.cascadia_int4_destroy_source(None)  # null-safe
@@ -160,6 +168,16 @@ def test_int4_bin_directory(orc, tmp_path, hidden, inter, with_inter):
             src.prewarm(layer, e)
         assert ei.value.rc == -2
     src.close()
+    # with a device present the open gets past hipGetDevice, so -3 here is the
+    # manifest's: expert_intermediate 0 (ov_moe.rs:452-457), or no
+    # expert_intermediate beside a hidden size other than K2.6's 7168
+    import ctypes as C
+    h = C.c_void_p()
+    for bad_inter, bad_hidden in ((0, hidden), (None, 3072)):
+        d = os.path.join(str(tmp_path), f"bad_{bad_inter}_{bad_hidden}")
+        os.makedirs(d)
+        write_int4_bin(d, bad_hidden, bad_inter, {}, with_inter=bad_inter is not None)
+        assert cl.lib().cascadia_int4_open_source(d.encode(), C.byref(h)) == -3
 
 
 @pytest.mark.gpu

@@ -52,10 +52,10 @@ def expert(orc, h, i, g, sdt, seed):
 @pytest.mark.parametrize("M", [65, 130, 257])
 @pytest.mark.parametrize("h,i,g,sdt", [(512, 384, 32, F16), (1024, 768, 64, BF16),
                                        (768, 1280, 128, F16), (512, 256, 256, BF16)])
-def test_expert_forward_tiles(cl, orc, monkeypatch, M, h, i, g, sdt):
+def test_expert_forward_tiles(cl, orc, tuning, M, h, i, g, sdt):
     """expert_forward over M rows on the tile GEMMs (bf16 rows, bf16 out;
     the tile threshold lowered to 65 rows)."""
-    monkeypatch.setenv("CASCADIA_INT4_FFN_TILE_TOKENS", "65")
+    tuning("CASCADIA_INT4_FFN_TILE_TOKENS", "65")
     flat = expert(orc, h, i, g, sdt, M + g)
     W = cl.ExpertWeights(dev(flat), h, i, g, sdt).tiled()
     xb = orc.fill_normal_bf16(M, 52, M * h)
@@ -67,10 +67,10 @@ def test_expert_forward_tiles(cl, orc, monkeypatch, M, h, i, g, sdt):
 
 
 @pytest.mark.parametrize("M,g", [(65, 32), (100, 64), (200, 128)])
-def test_ffn_f32_tiles(cl, orc, monkeypatch, M, g):
+def test_ffn_f32_tiles(cl, orc, tuning, M, g):
     """The f32-in / f32-out FFN (the shared expert) over M rows: x split into
     hi / lo planes, both planes through every MFMA."""
-    monkeypatch.setenv("CASCADIA_INT4_FFN_TILE_TOKENS", "65")
+    tuning("CASCADIA_INT4_FFN_TILE_TOKENS", "65")
     h, i, sdt = 512, 384, F16
     flat = expert(orc, h, i, g, sdt, 7 + g)
     W = cl.ExpertWeights(dev(flat), h, i, g, sdt).tiled()
@@ -86,14 +86,14 @@ def test_ffn_f32_tiles(cl, orc, monkeypatch, M, g):
 @pytest.mark.parametrize("T", [65, 200])
 @pytest.mark.parametrize("g,mode,shared_inter,thr", [(32, 1, 256, 0.0), (128, 2, 0, 0.0),
                                                      (64, 1, 128, 0.2)])
-def test_moe_tiles(cl, orc, monkeypatch, T, g, mode, shared_inter, thr, hot_rows):
+def test_moe_tiles(cl, orc, tuning, T, g, mode, shared_inter, thr, hot_rows):
     """MoE layers of 65+ tokens (routing by logits; the tile thresholds
     lowered to 65 tokens): every expert on the tile GEMMs (hot_rows 1), or the
     hybrid split -- experts with 48+ rows on tiles, the others on the skinny
     kernels' 16-row chunks."""
-    monkeypatch.setenv("CASCADIA_INT4_MOE_TILE_TOKENS", "65")
-    monkeypatch.setenv("CASCADIA_INT4_FFN_TILE_TOKENS", "65")
-    monkeypatch.setenv("CASCADIA_INT4_MOE_TILE_ROWS", hot_rows)
+    tuning("CASCADIA_INT4_MOE_TILE_TOKENS", "65")
+    tuning("CASCADIA_INT4_FFN_TILE_TOKENS", "65")
+    tuning("CASCADIA_INT4_MOE_TILE_ROWS", hot_rows)
     E, k, h, i, sdt = 12, 4, 512, 256, F16
     blob, shared, ex = build(cl, orc, E, h, i, g, sdt, 61 + g, shared_inter, True)
     logits = orc.fill_normal_f32(62, T, T * E).reshape(T, E)
@@ -108,10 +108,10 @@ def test_moe_tiles(cl, orc, monkeypatch, T, g, mode, shared_inter, thr, hot_rows
                 host(w_o), thr, f"tiles T={T} G{g} mode={mode}")
 
 
-def test_moe_tiles_hot_expert(cl, orc, monkeypatch):
+def test_moe_tiles_hot_expert(cl, orc, tuning):
     """Given ids sending every token to one expert (300 rows: three 128-row
     chunks, the last partial) plus scattered ones; two calls bit-identical."""
-    monkeypatch.setenv("CASCADIA_INT4_MOE_TILE_TOKENS", "65")
+    tuning("CASCADIA_INT4_MOE_TILE_TOKENS", "65")
     E, k, h, i, g, T = 9, 3, 384, 256, 32, 300
     blob, shared, ex = build(cl, orc, E, h, i, g, F16, 71, 128, True)
     rng = np.random.default_rng(3)
@@ -133,7 +133,7 @@ def test_moe_tiles_hot_expert(cl, orc, monkeypatch):
     check_layer(orc, outs[0], x, blob, shared, 128, E, h, i, g, F16, ids, w, 0.0, "hot expert")
 
 
-def test_tiles_match_skinny_path(cl, orc, monkeypatch):
+def test_tiles_match_skinny_path(cl, orc, tuning):
     """The same 80-token layer through both paths (the skinny grouped kernels
     forced by a high tile threshold): both within the bar of the oracle and of
     each other."""
@@ -144,8 +144,8 @@ def test_tiles_match_skinny_path(cl, orc, monkeypatch):
     xd = dev(x)
     res = []
     for thr_tokens in ("65", "100000"):
-        monkeypatch.setenv("CASCADIA_INT4_MOE_TILE_TOKENS", thr_tokens)
-        monkeypatch.setenv("CASCADIA_INT4_FFN_TILE_TOKENS", thr_tokens)
+        tuning("CASCADIA_INT4_MOE_TILE_TOKENS", thr_tokens)
+        tuning("CASCADIA_INT4_FFN_TILE_TOKENS", thr_tokens)
         o = torch.empty((T, h), dtype=torch.float32, device="cuda")
         cl.moe_forward(ex, xd, o, top_k=k, logits=dev(logits), mode=1, scale=2.5,
                        residual=xd)

@@ -764,6 +764,25 @@ def test_axpy_ffn_closed_form_exact_transpose(orc, tau):
     assert np.allclose(got, want, rtol=1e-4, atol=1e-4 * np.max(np.abs(want)))
 
 
+def test_nan_tau_is_sparse_everywhere(orc):
+    """SparsityMode::is_dense is `t <= 0.0` (ffn_sparsity.rs:85-90), so a NaN
+    tau is NOT dense: its cutoff NaN * max passes no lane (while max|silu| > 0).
+    Every oracle form must agree -- the mask, the GEMV-form sparse FFN and the
+    AXPY form -- with zero active lanes and an all-zero output."""
+    h, i, flat, down, down_s, x = _axpy_fixture()
+    nan = np.float32("nan")
+    _, act = orc.build_active_mask(np.array([1.0, -2.0, 0.5, -0.1], np.float32), nan)
+    assert act.size == 0
+    out, frac = orc.ffn_forward_f32(x, flat, h, i, 32, BF16, nan)
+    assert frac == 0.0 and np.all(out == 0.0)
+    pt, st = orc.transpose_requantize_down(down, down_s, h, i)
+    out, frac = orc.ffn_forward_sparse_axpy_f32(x, flat, pt, st, h, i, 32, BF16, nan)
+    assert frac == 0.0 and np.all(out == 0.0)
+    # all-zero gate: max|silu| == 0 makes every lane active whatever tau is
+    _, act = orc.build_active_mask(np.zeros(5, np.float32), nan)
+    assert act.size == 5
+
+
 def test_transpose_requantize_uses_f32_inverse(orc):
     """ffn_axpy.rs:406-419: codes are round(v * (1 / scale)) with the f32
     scale max|v| / 7, and the bf16 rounding of the scale is only what is
