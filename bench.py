@@ -72,6 +72,8 @@ def parse():
     ap.add_argument("--profile-moe", action="store_true",
                     help="run configs 3 and 4 at T=--moe-tokens (a few steps), for rocprofv3")
     ap.add_argument("--moe-tokens", type=int, default=1, help="tokens of --profile-moe")
+    ap.add_argument("--moe-config", type=int, default=0, choices=(0, 3, 4),
+                    help="--profile-moe: config 3 or 4 only (0: both)")
     ap.add_argument("--profile", action="store_true",
                     help="launch the headline kernels and a 256 MiB copy (counter calibration) "
                          "eagerly, without timing, for rocprofv3")
@@ -257,31 +259,42 @@ def read_traffic(m):
 # the other BASELINE configs
 # ---------------------------------------------------------------------------
 
-def hbm_ceiling(torch):
+def hbm_ceiling(cl, torch):
     """The box's measured streaming ceilings: a 1 GiB device copy (read +
-    write bytes) and a 1 GiB read-only reduction, event-timed."""
+    write bytes counted) and this library's streaming-read kernel
+    (cascadia_int4_stream_read: the decode GEMV's weight-stream pattern
+    without its arithmetic) over 60 MiB -- the size of config 1's gate/up --
+    rotating through 16 buffers (more than twice the Infinity Cache), and over
+    1 GiB; HIP events on the launch stream."""
     a = torch.ones(256 << 20, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
     for _ in range(3):
         b.copy_(a)
-        a.sum()
     torch.cuda.synchronize()
-    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     reps = 20
     e[0].record()
     for _ in range(reps):
         b.copy_(a)
     e[1].record()
-    for _ in range(reps):
-        a.sum()
-    e[2].record()
     torch.cuda.synchronize()
     nb = a.numel() * 4
     tc = e[0].elapsed_time(e[1]) / 1e3 / reps
-    tr = e[1].elapsed_time(e[2]) / 1e3 / reps
-    del a, b
-    return {"copy_GBps": round(2 * nb / tc / 1e9, 1), "read_GBps": round(nb / tr / 1e9, 1),
-            "bytes": nb, "note": "1 GiB device copy (read + write counted) and 1 GiB sum (read)"}
+    del b
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    out = {"copy_GBps": round(2 * nb / tc / 1e9, 1)}
+    small = [cl.fill_bytes(torch.empty(60 << 20, dtype=torch.uint8, device="cuda"), 9, j)
+             for j in range(16)]
+    for name, bufs, steps in (("read_60MiB_GBps", small, 320), ("read_1GiB_GBps", [a], 20)):
+        def rd(r, bufs=bufs):
+            cl.stream_read(bufs[r % len(bufs)], sink)
+        for r in range(len(bufs)):
+            rd(r)
+        _, ev = graph_time(torch, rd, steps)
+        out[name] = round(bufs[0].numel() * bufs[0].element_size() / (ev / steps) / 1e9, 1)
+    del a, small
+    torch.cuda.empty_cache()
+    return out
 
 
 def config0(cl, torch, sdt, cpu):
@@ -316,8 +329,7 @@ def config0(cl, torch, sdt, cpu):
     b = nb + nsb + k * 4 + n * 4
     res = {"us_per_call": round(t * 1e6, 3), "wall_us_per_call": round(wall / steps * 1e6, 3),
            "GB/s": round(b / t / 1e9, 1), "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
-           "kernel": "gemv_kernel (one token, MFMA-tiled weights)", "algorithmic_bytes": b,
-           "copies": ncp}
+           "algorithmic_bytes": b, "copies": ncp}
     del PS
     if cpu:
         hc = 16  # 139 MB of host copies: more than the host's last-level cache
@@ -330,10 +342,8 @@ def config0(cl, torch, sdt, cpu):
             orc.cpu_gemm(hp[r % hc], hs[r % hc], xh, n, k, 1, g, sdt, yh)
         cnt, dt = cpu_loop(run, CPU_SAMPLE_S)
         res["cpu_baseline"] = {"value": round(b * cnt / dt / 1e9, 3), "unit": "GB/s",
-                               "us_per_call": round(dt / cnt * 1e6, 2), "cores": orc.cpu_threads(),
-                               "kind": "port",
-                               "sample": f"{cnt} GEMVs over {hc} host copies in {dt:.1f}s "
-                                         "(dequant_gemv_int4_auto, AVX-512, OpenMP)"}
+                               "cores": orc.cpu_threads(), "kind": "port",
+                               "sample": f"{cnt} GEMVs, {hc} host copies, {dt:.1f}s"}
     return res
 
 
@@ -361,8 +371,7 @@ def config1_batches(cl, torch, sdt, copies, cpu):
              "GB/s": round(ffn_bytes(h, i, g, mm) * steps / ev / 1e9, 1),
              "hbm_frac": round(ffn_bytes(h, i, g, mm) * steps / ev / 1e9 / HBM_PEAK_GBS, 4),
              "tokens_per_s": round(mm * steps / ev, 1),
-             "gate_up_kernel": {"name": "skinny_kernel (fused gate/up + SiLU*up)",
-                                "us": round(t_gu * 1e6, 2), "algorithmic_bytes": gub,
+             "gate_up_kernel": {"us": round(t_gu * 1e6, 2), "algorithmic_bytes": gub,
                                 "frac": round(gub / t_gu / 1e9 / HBM_PEAK_GBS, 4)}}
         if cpu:
             e["cpu_baseline"] = cpu_chain_baseline(torch, copies, xm, mm, CPU_SAMPLE_S)
@@ -404,8 +413,7 @@ def config2(cl, torch, sdt, cpu):
         t = ev / reps
         fl = 2.0 * m * nn * kk
         e = {"us_per_call": round(t * 1e6, 1), "TFLOP/s": round(fl / t / 1e12, 1),
-             "mfma_frac": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": fl,
-             "kernel": "pf_gemm_kernel (+ pf_xsum_kernel, split-K reduce when planned)"}
+             "mfma_frac": round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": fl}
         if cpu:
             ns = 128
             xs = orc.bf16_to_f32(xb[:ns * kk].view(torch.int16).cpu().numpy().view(np.uint16))
@@ -417,8 +425,7 @@ def config2(cl, torch, sdt, cpu):
             cfl = 2.0 * nn * kk * ns * cnt
             e["cpu_baseline"] = {"value": round(cfl / dt / 1e12, 4), "unit": "TFLOP/s",
                                  "cores": orc.cpu_threads(), "kind": "port",
-                                 "sample": f"{cnt} x {ns} tokens (the crate's per-token GEMV loop "
-                                           f"for seq > 64) in {dt:.1f}s, AVX-512, OpenMP"}
+                                 "sample": f"{cnt}x{ns} tokens, per-token loop, {dt:.1f}s"}
         res[f"config2_prefill_M{m}_N{nn}"] = e
         del pre, xb, hostw
         torch.cuda.empty_cache()
@@ -440,19 +447,53 @@ def make_experts_dev(cl, torch, E, h, i, g, sdt, seed):
     return crate, stride, ex
 
 
+def marker(cl, torch):
+    """A dispatch that brackets a profiled region: one streaming read of 64 KiB
+    (its kernel runs nowhere else in the profile modes)."""
+    if not _MARK:
+        _MARK.append(torch.zeros(1 << 14, dtype=torch.float32, device="cuda"))
+        _MARK.append(torch.zeros(1024, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    cl.stream_read(_MARK[0], _MARK[1])
+    torch.cuda.synchronize()
+
+
+_MARK = []
+
+
+def calibrate(cl, torch):
+    """Counter calibration after a profiled region: five 256 MiB streaming
+    reads (true bytes read known) and five 256 MiB device copies (256 MiB
+    read, 256 MiB written), each its own dispatch."""
+    a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    for _ in range(5):
+        cl.stream_read(a, sink)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+
+
 def bench_moe(cl, torch, E, h, i, g, k, T, layers, mode, scale, shared_inter, steps,
-              zipf=None, nsets=64, cpu=False, cpu_tokens=4):
+              zipf=None, nsets=64, cpu=False, cpu_tokens=4, replicas=1, profile_steps=0):
     """MoE layer(s) for T tokens; steps rotate through `nsets` routing-logit
-    sets so that consecutive steps touch different experts.  With `cpu`, the
-    runner's per-(token, slot) loop on the host over the first `cpu_tokens`
-    tokens, through every layer, with the routing the GPU used."""
+    sets so that consecutive steps touch different experts, and through
+    `replicas` copies of every layer's experts (so that no expert a step
+    selects can still be in the Infinity Cache from a recent step).  With
+    `cpu`, the runner's per-(token, slot) loop on the host over the first
+    `cpu_tokens` tokens, through every layer, with the routing the GPU used.
+    With `profile_steps`, no timing: that many eager steps between two
+    marker dispatches, then the counter calibration; returns each step's
+    algorithmic bytes."""
     import numpy as np
 
     import oracle as orc
 
     sdt = cl.SCALE_F16
     stacks, crates, shared_host = [], [], []
-    for layer in range(layers):
+    for layer in range(layers * replicas):
         crate, stride, ex = make_experts_dev(cl, torch, E, h, i, g, sdt, 50 + layer)
         sh_host = None
         if shared_inter:
@@ -464,7 +505,7 @@ def bench_moe(cl, torch, E, h, i, g, k, T, layers, mode, scale, shared_inter, st
             sh_host = f.cpu().numpy() if cpu else None
             ex = cl.MoEExperts(ex.blobs, E, h, i, g, sdt, cl.TILING_MFMA, ex.stride, W.tiled())
         stacks.append(ex)
-        crates.append((crate, stride) if cpu else None)
+        crates.append((crate, stride) if cpu and layer < layers else None)
         shared_host.append(sh_host)
         if not cpu:
             del crate
@@ -488,17 +529,33 @@ def bench_moe(cl, torch, E, h, i, g, k, T, layers, mode, scale, shared_inter, st
     u_avg = sum(uniq) / len(uniq)
 
     def step(r):
+        rep = (r % replicas) * layers
         for layer in range(layers):
-            cl.moe_forward(stacks[layer], xs[layer], xs[layer + 1], top_k=k,
+            cl.moe_forward(stacks[rep + layer], xs[layer], xs[layer + 1], top_k=k,
                            logits=logits[(r + 7 * layer) % nsets], mode=mode, scale=scale,
                            residual=xs[layer])
     for r in range(5):
         step(r)
-    wall, ev = graph_time(torch, step, steps)
-    t = ev / steps
     per_expert = 3 * (i * h // 2 + i * (h // g) * 2)
     per_shared = 3 * (shared_inter * h // 2 + shared_inter * (h // g) * 2) if shared_inter else 0
-    byts = layers * (u_avg * per_expert + per_shared + T * h * 6 + T * E * 4 + T * k * 8)
+    fixed = per_shared + T * h * 6 + T * E * 4 + T * k * 8
+    if profile_steps:
+        marker(cl, torch)
+        for r in range(profile_steps):
+            step(r)
+        marker(cl, torch)
+        calibrate(cl, torch)
+        per_step = [sum(uniq[(r + 7 * layer) % nsets] * per_expert + fixed
+                        for layer in range(layers)) for r in range(profile_steps)]
+        del stacks, logits, crates, xs
+        torch.cuda.empty_cache()
+        return {"T": T, "layers": layers, "replicas": replicas, "steps": profile_steps,
+                "algorithmic_bytes_per_step": per_step,
+                "unique_experts": [uniq[(r + 7 * layer) % nsets] for r in range(profile_steps)
+                                   for layer in range(layers)]}
+    wall, ev = graph_time(torch, step, steps)
+    t = ev / steps
+    byts = layers * (u_avg * per_expert + fixed)
     flops = layers * 2.0 * T * (k + (1 if shared_inter else 0)) * 3 * h * i
     res = {"T": T, "layers": layers, "us_per_step": round(t * 1e6, 2),
            "wall_us_per_step": round(wall / steps * 1e6, 2),
@@ -507,8 +564,7 @@ def bench_moe(cl, torch, E, h, i, g, k, T, layers, mode, scale, shared_inter, st
            "TFLOP/s": round(flops / t / 1e12, 2),
            "mfma_frac": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4),
            "unique_experts_avg": round(u_avg, 1), "algorithmic_bytes_per_step": int(byts),
-           "kernels": "cascadia_int4_moe_forward per layer: routing/grouping, grouped gate/up "
-                      "(SwiGLU hi/lo) and down, shared expert, slot-order combine"}
+           "replicas": replicas}
     if cpu:
         S = min(T, cpu_tokens)
         plan = []
@@ -531,11 +587,8 @@ def bench_moe(cl, torch, E, h, i, g, k, T, layers, mode, scale, shared_inter, st
                                        0.0, stride=stride)
         cnt, dt = cpu_loop(run, CPU_SAMPLE_S)
         res["cpu_baseline"] = {"value": round(S * cnt / dt, 2), "unit": "tokens/s",
-                               "us_per_token": round(dt / (S * cnt) * 1e6, 1),
                                "cores": orc.cpu_threads(), "kind": "port",
-                               "sample": f"{cnt} x {S} tokens through {layers} layer(s) in "
-                                         f"{dt:.1f}s: the runner's per-(token, slot) "
-                                         "expert_forward loop + serial combine, AVX-512, OpenMP"}
+                               "sample": f"{cnt}x{S} tokens x {layers} layers, {dt:.1f}s"}
     del stacks, logits, crates, xs
     torch.cuda.empty_cache()
     return res
@@ -584,19 +637,30 @@ def f_rows(cl, torch, sdt, copies):
                                    "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
                                    "bytes_per_step": b, "copies": ncs}
     del SH
-    # the activation-sparse expert (tau > 0, ffn_sparsity.rs:756-867) at one
-    # token: algorithmic bytes gate and down in full, up for the active rows
-    # (this path reads up in full too: the fused gate/up GEMV).  Called
-    # through the C entry point with no count output, so it captures.
+    # The activation-sparse FFN at one token, tau 0.1 / 0.3, in the layout made
+    # for it (TILING_MFMA_UP_ROWS: gate and down tiled, up rows contiguous, so
+    # only the active up rows are read); the AXPY form also over the all-tiled
+    # layout (up read in 16-byte pieces of its tiles), for comparison.  One
+    # crate-layout up per weight copy (synthetic, seeded), so the up rows
+    # rotate with the rest.
+    nc = len(copies.w)
+    mat = i * h // 2 + i * (h // g) * 2
+    UPS = [(cl.fill_bytes(torch.empty(i * h // 2, dtype=torch.uint8, device="cuda"), 3, 800 + c),
+            cl.fill_scales(torch.empty(i * (h // g) * 2, dtype=torch.uint8, device="cuda"), 3,
+                           900 + c, sdt)) for c in range(nc)]
     xs1 = cl.fill_normal(torch.empty(h, dtype=torch.bfloat16, device="cuda"), 0, 23)
     os1 = torch.empty(h, dtype=torch.bfloat16, device="cuda")
-    nc = len(copies.w)
     for tau in (0.1, 0.3):
-        fr = cl.expert_forward_sparse(xs1.view(torch.int16), *copies.w[0].slices(),
+        ex = [cl._lib.Expert(W.gate_packed_bytes().data_ptr(), W.gate_scale_bits().data_ptr(),
+                             UPS[c][0].data_ptr(), UPS[c][1].data_ptr(),
+                             W.down_packed_bytes().data_ptr(), W.down_scale_bits().data_ptr(),
+                             cl.TILING_MFMA_UP_ROWS) for c, W in enumerate(copies.w)]
+        W0 = copies.w[0]
+        fr = cl.expert_forward_sparse(xs1.view(torch.int16), W0.gate_packed_bytes(),
+                                      W0.gate_scale_bits(), UPS[0][0], UPS[0][1],
+                                      W0.down_packed_bytes(), W0.down_scale_bits(),
                                       os1.view(torch.int16), tau, group_size=g, scale_dtype=sdt,
-                                      tiling=cl.TILING_MFMA)
-        ex = [cl._lib.Expert(*(t.data_ptr() for t in W.slices()), cl.TILING_MFMA)
-              for W in copies.w]
+                                      tiling=cl.TILING_MFMA_UP_ROWS)
 
         def sparse(r, tau=tau):
             cl.check("cascadia_int4_expert_forward_sparse", cl.lib().cascadia_int4_expert_forward_sparse(
@@ -607,21 +671,23 @@ def f_rows(cl, torch, sdt, copies):
         steps = 200
         _, ev = graph_time(torch, sparse, steps)
         t = ev / steps
-        mat = i * h // 2 + i * (h // g) * 2
-        b = 2 * mat + int(round(fr * i)) * (h // 2 + (h // g) * 2) + h * 2 * 2
+        na = int(round(fr * i))
+        # the crate's reads: gate and down in full, the active up rows
+        b = 2 * mat + na * (h // 2 + (h // g) * 2) + h * 2 * 2
         res[f"sparse_expert_M1_tau{tau}"] = {"us_per_call": round(t * 1e6, 2),
                                              "active_frac": round(fr, 4),
                                              "GB/s": round(b / t / 1e9, 1),
-                                             "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+                                             "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+                                             "layout": "mfma_up_rows"}
     # the composed AXPY-form sparse FFN (ffn_sparsity.rs:638-740): f32 in /
     # out, gate + mask + rows-subset up + AXPY down over config 1's
-    # transposed down, one token, tau 0.1 / 0.3
+    # transposed down
     src = cl.ExpertWeights(copies.crate[0], h, i, g, sdt)
     ptc, stc = cl.transpose_requantize_down(src.down_packed_bytes(), src.down_scale_bits(), h, i,
                                             group_size=g, scale_dtype=sdt)
     # one transposed down per weight copy, so that the active rows rotate too
     # (synthetic codes and bf16 scales of the transposed shape; the first is
-    # copy 0's true transpose, used for the active fraction)
+    # copy 0's true transpose)
     PTS = [(ptc, stc)] + [
         (cl.fill_bytes(torch.empty(i * h // 2, dtype=torch.uint8, device="cuda"), 2, 600 + c),
          cl.fill_scales(torch.empty(i * (h // 32) * 2, dtype=torch.uint8, device="cuda"), 2,
@@ -631,18 +697,21 @@ def f_rows(cl, torch, sdt, copies):
     of1 = torch.empty(h, dtype=torch.float32, device="cuda")
     wsx = torch.empty(cl.ffn_sparse_axpy_workspace_bytes(h, i, 1, g), dtype=torch.uint8,
                       device="cuda")
-    for tau in (0.1, 0.3):
+    for tau, lay in ((0.1, "up_rows"), (0.3, "up_rows"), (0.3, "tiled")):
         W0 = copies.w[0]
+        rows = lay == "up_rows"
+        til = cl.TILING_MFMA_UP_ROWS if rows else cl.TILING_MFMA
+        up0 = UPS[0] if rows else (W0.up_packed_bytes(), W0.up_scale_bits())
         fr = cl.ffn_forward_sparse_axpy_f32(xf1, h, i, W0.gate_packed_bytes(), W0.gate_scale_bits(),
-                                            W0.up_packed_bytes(), W0.up_scale_bits(), ptc, stc,
-                                            of1, tau, group_size=g, scale_dtype=sdt,
-                                            workspace=wsx, tiling=cl.TILING_MFMA)
-        exa = [cl._lib.Expert(*(t.data_ptr() for t in (W.gate_packed_bytes(), W.gate_scale_bits(),
-                                                        W.up_packed_bytes(), W.up_scale_bits())),
-                              PTS[c][0].data_ptr(), PTS[c][1].data_ptr(), cl.TILING_MFMA)
+                                            *up0, ptc, stc, of1, tau, group_size=g,
+                                            scale_dtype=sdt, workspace=wsx, tiling=til)
+        exa = [cl._lib.Expert(W.gate_packed_bytes().data_ptr(), W.gate_scale_bits().data_ptr(),
+                              (UPS[c][0] if rows else W.up_packed_bytes()).data_ptr(),
+                              (UPS[c][1] if rows else W.up_scale_bits()).data_ptr(),
+                              PTS[c][0].data_ptr(), PTS[c][1].data_ptr(), til)
                for c, W in enumerate(copies.w)]
 
-        def axffn(r, tau=tau):
+        def axffn(r, tau=tau, exa=exa):
             cl.check("cascadia_int4_ffn_forward_sparse_axpy_f32",
                      cl.lib().cascadia_int4_ffn_forward_sparse_axpy_f32(
                          h, i, g, sdt, C.byref(exa[r % nc]), xf1.data_ptr(), 1, tau, None,
@@ -653,20 +722,15 @@ def f_rows(cl, torch, sdt, copies):
         steps = 200
         _, ev = graph_time(torch, axffn, steps)
         t = ev / steps
-        mat = i * h // 2 + i * (h // g) * 2
         na = int(round(fr * i))
-        # algorithmic: the crate's reads (gate, the active up and transposed-down
-        # rows); read: this path's (gate and up in full -- the fused GEMV)
+        # algorithmic: the crate's reads (gate, the active up and transposed-down rows)
         b = mat + na * (h // 2 + (h // g) * 2) + na * (h // 2 + (h // 32) * 2) + h * 4 * 2
-        rd = 2 * mat + na * (h // 2 + (h // 32) * 2) + h * 4 * 2
-        res[f"sparse_axpy_ffn_M1_tau{tau}"] = {"us_per_call": round(t * 1e6, 2),
-                                               "active_frac": round(fr, 4),
-                                               "GB/s": round(b / t / 1e9, 1),
-                                               "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
-                                               "bytes_read": rd,
-                                               "read_GB/s": round(rd / t / 1e9, 1),
-                                               "note": "every copy rotates, transposed downs too"}
-    del ptc, stc, wsx, PTS
+        key = f"sparse_axpy_ffn_M1_tau{tau}" + ("" if rows else "_tiled_up")
+        res[key] = {"us_per_call": round(t * 1e6, 2), "active_frac": round(fr, 4),
+                    "GB/s": round(b / t / 1e9, 1),
+                    "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+                    "layout": "mfma_up_rows" if rows else "mfma"}
+    del ptc, stc, wsx, PTS, UPS
     # the AXPY form of the sparse down (ffn_axpy.rs:82-160): config 1's down
     # transposed to [inter, hidden], 13.4 % of the rows active (what tau 0.3
     # selects above), over rotating copies larger than 2x the Infinity Cache
@@ -705,16 +769,18 @@ def f_rows(cl, torch, sdt, copies):
 
 
 def all_configs(cl, torch, sdt, copies, cpu):
-    ex = {"hbm_ceiling": hbm_ceiling(torch)}
+    ex = {"hbm_ceiling": hbm_ceiling(cl, torch)}
     if cpu:
         ex["cpu_host"] = host_cpu()
     ex["config0_gemv"] = config0(cl, torch, sdt, cpu)
     ex.update(config1_batches(cl, torch, sdt, copies, cpu))
     ex.update(config2(cl, torch, sdt, cpu))
     for T in (1, 32, 256):
+        # one token's 8 experts (58 MB) fit the Infinity Cache a few steps over:
+        # eight copies of the layer rotate, so no step finds its experts there
         ex[f"config3_moe_T{T}"] = bench_moe(
             cl, torch, 256, 3072, 1536, 128, 8, T, 1, cl.ROUTE_SOFTMAX_TOPK, 1.0, 0,
-            200 if T < 256 else 40, cpu=cpu, cpu_tokens=8)
+            200 if T < 256 else 40, cpu=cpu, cpu_tokens=8, replicas=8 if T == 1 else 1)
     for T in (1, 8, 64, 1024):
         ex[f"config4_moe_T{T}"] = bench_moe(
             cl, torch, 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS, 2.827, 2048,
@@ -722,6 +788,39 @@ def all_configs(cl, torch, sdt, copies, cpu):
             cpu=cpu, cpu_tokens=4)
     ex.update(f_rows(cl, torch, sdt, copies))
     return ex
+
+
+def summary(line):
+    """The figures of every config in a few hundred characters, for the end of
+    the JSON line (a reader that keeps only the tail of the output still gets
+    them): [µs, fraction of roofline] per workload -- HBM for decode / MoE, bf16
+    MFMA for prefill; MoE entries [µs per step, HBM frac, MFMA frac, tokens/s]."""
+    ex = line.get("extra", {})
+    out = {"c1_M1": [round(line["ms_per_step"] * 1e3, 2), line["roofline"]["frac"]]}
+    c = ex.get("config0_gemv")
+    if c:
+        out["c0"] = [c["us_per_call"], c["hbm_frac"]]
+    for m in (4, 16):
+        c = ex.get(f"config1_M{m}")
+        if c:
+            out[f"c1_M{m}"] = [c["us_per_chain"], c["hbm_frac"]]
+    for (pm, pn) in PREFILL_SHAPES:
+        c = ex.get(f"config2_prefill_M{pm}_N{pn}")
+        if c:
+            out[f"c2_{pm}x{pn}"] = [c["us_per_call"], c["mfma_frac"]]
+    for cfg, ts in ((3, (1, 32, 256)), (4, (1, 8, 64, 1024))):
+        for T in ts:
+            c = ex.get(f"config{cfg}_moe_T{T}")
+            if c:
+                out[f"c{cfg}_T{T}"] = [c["us_per_step"], c["hbm_frac"], c["mfma_frac"],
+                                       c["tokens_per_s"]]
+    c = ex.get("sparse_axpy_ffn_M1_tau0.3")
+    if c:
+        out["axpy_tau0.3"] = [c["us_per_call"], round(c["us_per_call"] / out["c1_M1"][0], 3)]
+    c = ex.get("hbm_ceiling")
+    if c:
+        out["read_ceiling_GBps"] = c.get("read_60MiB_GBps")
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -751,12 +850,19 @@ def main():
             PS.append(cl.tile_weights(p, s, n, k, g))
         x = cl.fill_normal(torch.empty(k, dtype=torch.float32, device="cuda"), 0, 13)
         y = torch.empty(n, dtype=torch.float32, device="cuda")
+        for r in range(20):
+            pt, st = PS[r % ncp]
+            cl.dequant_gemv_int4(pt, st, x, n, k, y, group_size=g, scale_dtype=sdt,
+                                 tiling=cl.TILING_MFMA)
+        marker(cl, torch)  # the 200 launches between the markers are the profiled ones
         for r in range(200):
             pt, st = PS[r % ncp]
             cl.dequant_gemv_int4(pt, st, x, n, k, y, group_size=g, scale_dtype=sdt,
                                  tiling=cl.TILING_MFMA)
-        torch.cuda.synchronize()
-        print(json.dumps({"profile": "gemv", "launches": 200, "copies": ncp}), flush=True)
+        marker(cl, torch)
+        calibrate(cl, torch)
+        print(json.dumps({"profile": "gemv", "launches": 200, "copies": ncp,
+                          "algorithmic_bytes": nb + nsb + k * 4 + n * 4}), flush=True)
         return
     if args.profile_prefill:
         for (pm, pn) in PREFILL_SHAPES:
@@ -803,13 +909,20 @@ def main():
                           "copies": nc}), flush=True)
         return
     if args.profile_moe:
+        # eager steps between two marker dispatches (then the counter
+        # calibration), with the default bench's weight rotation; prints each
+        # step's algorithmic bytes
         T = args.moe_tokens
-        r3 = bench_moe(cl, torch, 256, 3072, 1536, 128, 8, T, 1, cl.ROUTE_SOFTMAX_TOPK, 1.0, 0,
-                       50 if T < 256 else 10, nsets=16)
-        r4 = bench_moe(cl, torch, 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS, 2.827,
-                       2048, 20 if T < 256 else 3, zipf=1.1, nsets=16)
-        print(json.dumps({"profile": "moe", f"config3_T{T}": r3, f"config4_T{T}": r4}),
-              flush=True)
+        out = {"profile": "moe"}
+        if args.moe_config in (0, 3):
+            out[f"config3_T{T}"] = bench_moe(
+                cl, torch, 256, 3072, 1536, 128, 8, T, 1, cl.ROUTE_SOFTMAX_TOPK, 1.0, 0, 0,
+                nsets=16, replicas=8 if T == 1 else 1, profile_steps=16 if T < 256 else 4)
+        if args.moe_config in (0, 4):
+            out[f"config4_T{T}"] = bench_moe(
+                cl, torch, 384, 7168, 2048, 32, 8, T, 4, cl.ROUTE_SIGMOID_BIAS, 2.827, 2048, 0,
+                zipf=1.1, nsets=16, profile_steps=8 if T < 256 else 2)
+        print(json.dumps(out), flush=True)
         return
     h, i, g, m = 4096, 14336, 128, args.m
     ncopies = chain_copies(cl, h, i, g)
@@ -857,7 +970,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4*bf16->f32",
+        "dtype": "int4*bf16->f32 (f32 accumulation; the SwiGLU intermediate as bf16 hi+lo "
+                 "planes, about 17 significant bits)",
         "data": "synthetic",
         "config": {"workload": "config1_llama3_8b_decode_ffn_chain", "M": m, "hidden": h,
                    "inter": i, "group": g, "scales": "fp16", "weight_copies": ncopies,
@@ -868,7 +982,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(m),
-                     "kernel": "gemv_kernel<2, A_BF16, 4, 1>: one-token fused gate/up + SiLU*up (EPI_SWIGLU)",
+                     "kernel": "gemv_kernel<2,0,4,1> fused gate/up",
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
     }
@@ -876,6 +990,10 @@ def main():
         line["cpu_baseline"] = cpu_chain_baseline(torch, copies, x, m, args.cpu_seconds)
     if not args.headline_only:
         line["extra"] = all_configs(cl, torch, sdt, copies, not args.no_cpu)
+        ceil = line["extra"]["hbm_ceiling"].get("read_60MiB_GBps")
+        if ceil:
+            line["roofline"]["frac_of_read_ceiling"] = round(achieved / ceil, 4)
+        line["summary"] = summary(line)
     print(json.dumps(line), flush=True)
 
 

@@ -11,13 +11,17 @@ was not built (``python cascadia_amd/build.py``).  There is no CPU fallback.
 import torch  # noqa: F401
 
 from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, CascadiaInt4Error,
-                   LIB_PATH, SCALE_BF16, SCALE_F16, SIGNATURES, TILING_CRATE, TILING_MFMA, check,
-                   lib)
+                   LIB_PATH, SCALE_BF16, SCALE_F16, SIGNATURES, TILING_CRATE, TILING_MFMA,
+                   TILING_MFMA_UP_ROWS, check, lib)
 
 lib()  # fail loudly at import when the HIP library is missing
 
 from .api import (GROUP_SIZE, HIDDEN, INTERMEDIATE, NIBBLES_PER_INT32, ExpertSource,  # noqa: E402
-                  ExpertWeights,
+                  ExpertWeights, GemmError, GemmTruncated, SparsityMode, bf16_bits_to_f32,
+                  build_active_mask, build_active_mask_mode, build_active_mask_per_channel,
+                  dequant_gemv_int4_rows_subset, dequant_gemv_int4_rows_subset_auto,
+                  expert_forward_sparse_mode, f32_to_bf16_bits, ffn_forward_sparse_f32_mode,
+                  stream_read,
                   debug_dequant, dequant_gemm_int4_multi_auto,
                   dequant_gemm_int4_multi_blocked_auto, dequant_gemv_int4,
                   dequant_gemv_int4_auto, expert_bytes, expert_forward, expert_forward_sparse,
@@ -45,5 +49,9 @@ __all__ = [
     "tiled_sizes", "TILING_CRATE", "TILING_MFMA", "MoEExperts", "moe_forward",
     "moe_workspace_bytes", "ov_gemv", "ov_to_crate", "quantize_int4_group", "ROUTE_IDS",
     "ROUTE_SIGMOID_BIAS",
-    "ROUTE_SOFTMAX_TOPK",
+    "ROUTE_SOFTMAX_TOPK", "TILING_MFMA_UP_ROWS", "GemmError", "GemmTruncated", "SparsityMode",
+    "bf16_bits_to_f32", "f32_to_bf16_bits", "build_active_mask", "build_active_mask_mode",
+    "build_active_mask_per_channel", "dequant_gemv_int4_rows_subset",
+    "dequant_gemv_int4_rows_subset_auto", "expert_forward_sparse_mode",
+    "ffn_forward_sparse_f32_mode", "stream_read",
 ]

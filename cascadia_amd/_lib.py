@@ -21,6 +21,7 @@ SCALE_BF16 = 0
 SCALE_F16 = 1
 TILING_CRATE = 0
 TILING_MFMA = 1
+TILING_MFMA_UP_ROWS = 2
 
 _ERRS = {ERR_NULL: "null pointer", ERR_ARG: "invalid argument (shape/length/alignment)",
          ERR_DEVICE: "HIP device error", ERR_NOMEM: "device allocation failed"}
@@ -78,6 +79,10 @@ SIGNATURES = {
     "cascadia_int4_synchronize": (_i32, [_vp]),
     "cascadia_int4_reload_tuning": (None, []),
     "cascadia_int4_dequant_gemv": (_i32, [_LP, _vp, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_dequant_gemv_rows_subset": (_i32, [_LP, _vp, _vp, _vp, _vp, _vp, _u32, _vp]),
+    "cascadia_int4_build_active_mask": (_i32, [_vp, _u32, C.c_float, _vp, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_f32_to_bf16": (_i32, [_vp, _sz, _vp, _vp]),
+    "cascadia_int4_bf16_to_f32": (_i32, [_vp, _sz, _vp, _vp]),
     "cascadia_int4_dequant_gemm_multi": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
     "cascadia_int4_dequant_gemm_bf16in": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
     "cascadia_int4_gemm_bf16": (_i32, [_LP, _vp, _vp, _vp, _u32, _vp, _vp]),
@@ -95,6 +100,7 @@ SIGNATURES = {
     "cascadia_int4_moe_workspace_bytes": (_sz, [_MP, _u32, _u32]),
     "cascadia_int4_moe_forward": (_i32, [_MP, _RP, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_debug_dequant": (_i32, [_LP, _vp, _vp, _vp, _vp]),
+    "cascadia_int4_stream_read": (_i32, [_vp, _sz, _vp, _vp]),
     "cascadia_int4_fill_synthetic": (_i32, [_u32, _u64, _u64, _sz, _f64, _f64, _u32, _vp, _vp]),
     "cascadia_int4_transpose_requantize_down": (_i32, [_u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp, _vp]),
     "cascadia_int4_axpy_workspace_bytes": (_sz, [_u32, _u32]),

@@ -18,8 +18,8 @@ import numpy as np
 import torch
 
 from ._lib import (ROUTE_IDS, ROUTE_SIGMOID_BIAS, ROUTE_SOFTMAX_TOPK, Expert, Layout, MoeLayer,
-                   OvSegment, Routing, SCALE_BF16, SCALE_F16, TILING_CRATE, TILING_MFMA, check,
-                   lib)
+                   OvSegment, Routing, SCALE_BF16, SCALE_F16, TILING_CRATE, TILING_MFMA,
+                   TILING_MFMA_UP_ROWS, check, lib)
 
 # K2.6 constants of the crate (lib.rs:71-78)
 HIDDEN = 7168
@@ -112,6 +112,149 @@ def dequant_gemv_int4(packed, scale_bits, x, n_rows, k_cols, y, group_size=GROUP
 dequant_gemv_int4_auto = dequant_gemv_int4  # kernel_avx512.rs:274-297
 
 
+def dequant_gemv_int4_rows_subset(packed, scale_bits, x, n_rows, k_cols, y, active_rows,
+                                  group_size=GROUP_SIZE, scale_dtype=SCALE_BF16,
+                                  tiling=TILING_CRATE):
+    """y[r] = (W x)[r] for r in active_rows only (ffn_sparsity.rs:187-243); the
+    other entries of y are not touched (pre-zero y where defined values are
+    needed).  x f32 [k_cols], y f32 [n_rows], active_rows a device tensor of
+    32-bit row ids (int32 or uint32); rows >= n_rows are skipped."""
+    _check_weights(packed, scale_bits, n_rows, k_cols, group_size, tiling)
+    _dev(x, "x"), _dev(y, "y"), _dev(active_rows, "active_rows")
+    _expect(x.dtype == torch.float32 and x.numel() == k_cols, "x must be f32 [k_cols]")
+    _expect(y.dtype == torch.float32 and y.numel() == n_rows, "y must be f32 [n_rows]")
+    _expect(active_rows.element_size() == 4 and not active_rows.is_floating_point(),
+            "active_rows must hold 32-bit row ids")
+    L = _layout(n_rows, k_cols, group_size, scale_dtype, tiling)
+    check("cascadia_int4_dequant_gemv_rows_subset", lib().cascadia_int4_dequant_gemv_rows_subset(
+        C.byref(L), packed.data_ptr(), scale_bits.data_ptr(), x.data_ptr(), y.data_ptr(),
+        active_rows.data_ptr(), active_rows.numel(), _stream()))
+    return y
+
+
+dequant_gemv_int4_rows_subset_auto = dequant_gemv_int4_rows_subset  # ffn_sparsity.rs:317-348
+
+
+# ---------------------------------------------------------------------------
+# scalar conversions (format.rs:130-160)
+# ---------------------------------------------------------------------------
+
+def _as_device(v, dtype) -> tuple:
+    """(device tensor, was_scalar) for a device tensor or a Python number."""
+    if isinstance(v, torch.Tensor):
+        return _dev(v, "x"), False
+    return torch.tensor([v], dtype=dtype, device="cuda"), True
+
+
+def f32_to_bf16_bits(x):
+    """format.rs:151-160 (RNE, NaN kept quiet): f32 -> bf16 bits, on the device.
+    x: an f32 device tensor (-> uint16 bits as int16 storage) or a Python
+    float (-> int)."""
+    t, scalar = _as_device(x, torch.float32)
+    _expect(t.dtype == torch.float32, "x must be f32")
+    out = torch.empty(t.shape, dtype=torch.int16, device=t.device)
+    check("cascadia_int4_f32_to_bf16", lib().cascadia_int4_f32_to_bf16(
+        t.data_ptr(), t.numel(), out.data_ptr(), _stream()))
+    return int(out.cpu().view(torch.uint16).item()) if scalar else out
+
+
+def bf16_bits_to_f32(bits):
+    """format.rs:130-135: bf16 bits -> f32 (exact), on the device.  bits: a
+    16-bit device tensor (-> f32 tensor) or a Python int (-> float)."""
+    if not isinstance(bits, torch.Tensor):
+        bits = torch.tensor([bits & 0xFFFF], dtype=torch.int32).to(torch.int16).cuda()
+        scalar = True
+    else:
+        _dev(bits, "bits")
+        scalar = False
+    _expect(bits.element_size() == 2, "bits must be 16-bit")
+    out = torch.empty(bits.shape, dtype=torch.float32, device=bits.device)
+    check("cascadia_int4_bf16_to_f32", lib().cascadia_int4_bf16_to_f32(
+        bits.data_ptr(), bits.numel(), out.data_ptr(), _stream()))
+    return float(out.cpu().item()) if scalar else out
+
+
+# ---------------------------------------------------------------------------
+# activation masks (ffn_sparsity.rs:71-179)
+# ---------------------------------------------------------------------------
+
+class SparsityMode:
+    """SparsityMode (ffn_sparsity.rs:71-91): Global(tau) -- one threshold for
+    every lane -- or PerChannel(thresholds) -- a device f32 tensor of one
+    threshold per intermediate lane."""
+
+    __slots__ = ("tau", "thresholds")
+
+    def __init__(self, tau: float = 0.0, thresholds: torch.Tensor | None = None):
+        self.tau, self.thresholds = float(tau), thresholds
+
+    @staticmethod
+    def Global(tau: float) -> "SparsityMode":  # noqa: N802 (the crate's variant name)
+        return SparsityMode(tau=tau)
+
+    @staticmethod
+    def PerChannel(thresholds: torch.Tensor) -> "SparsityMode":  # noqa: N802
+        return SparsityMode(thresholds=thresholds)
+
+    def is_dense(self) -> bool:
+        """ffn_sparsity.rs:85-90 (a NaN tau is not dense).  PerChannel reads the
+        thresholds back from the device."""
+        if self.thresholds is None:
+            return self.tau <= 0.0
+        t = self.thresholds
+        return t.numel() == 0 or bool((t <= 0.0).all().item())
+
+    @staticmethod
+    def of(mode) -> "SparsityMode":
+        """A SparsityMode from itself, a float (Global) or a tensor (PerChannel)."""
+        if isinstance(mode, SparsityMode):
+            return mode
+        if isinstance(mode, torch.Tensor):
+            return SparsityMode.PerChannel(mode)
+        return SparsityMode.Global(float(mode))
+
+
+def build_active_mask_mode(gate_out, mode):
+    """ffn_sparsity.rs:131-179 on one row: (silu_gate f32 [n], active u32
+    ids ascending) with |silu| >= cutoff * max|silu| (every lane when the max
+    is 0 or the mode is dense).  gate_out: f32 device tensor [n]; mode: a
+    SparsityMode, a float or a per-channel tensor.  Waits for the device to
+    size the list, as the crate returns a Vec."""
+    m = SparsityMode.of(mode)
+    _dev(gate_out, "gate_out")
+    _expect(gate_out.dtype == torch.float32, "gate_out must be f32")
+    n = gate_out.numel()
+    thr = 0
+    if m.thresholds is not None:
+        _dev(m.thresholds, "thresholds")
+        # ffn_sparsity.rs:116-123: one threshold per lane
+        _expect(m.thresholds.dtype == torch.float32 and m.thresholds.numel() == n,
+                f"per-channel thresholds length {m.thresholds.numel()} != gate_out length {n}")
+        thr = m.thresholds.data_ptr()
+    silu = torch.empty(n, dtype=torch.float32, device=gate_out.device)
+    act = torch.empty(n, dtype=torch.int32, device=gate_out.device)
+    cnt = torch.zeros(1, dtype=torch.int32, device=gate_out.device)
+    if n:
+        check("cascadia_int4_build_active_mask", lib().cascadia_int4_build_active_mask(
+            gate_out.data_ptr(), n, m.tau, thr, silu.data_ptr(), act.data_ptr(), cnt.data_ptr(),
+            _stream()))
+    k = int(cnt.item())
+    return silu, act[:k]
+
+
+def build_active_mask(gate_out, threshold: float):
+    """ffn_sparsity.rs:106-108 (SparsityMode::Global)."""
+    return build_active_mask_mode(gate_out, SparsityMode.Global(threshold))
+
+
+def build_active_mask_per_channel(gate_out, thresholds):
+    """ffn_sparsity.rs:115-125 (SparsityMode::PerChannel)."""
+    _expect(isinstance(thresholds, torch.Tensor) and thresholds.numel() == gate_out.numel(),
+            f"per-channel thresholds length {getattr(thresholds, 'numel', lambda: -1)()} != "
+            f"gate_out length {gate_out.numel()}")
+    return build_active_mask_mode(gate_out, SparsityMode.PerChannel(thresholds))
+
+
 def dequant_gemm_int4_multi_auto(packed, scale_bits, xs, n_rows, k_cols, seq, ys,
                                  group_size=GROUP_SIZE, scale_dtype=SCALE_BF16,
                                  tiling=TILING_CRATE):
@@ -159,45 +302,114 @@ def expert_bytes(hidden: int, inter: int, group_size: int = GROUP_SIZE) -> int:
     return int(lib().cascadia_int4_expert_bytes(hidden, inter, group_size))
 
 
+class GemmError(RuntimeError):
+    """GemmError (format.rs:28-33): an I/O failure opening an expert file."""
+
+
+class GemmTruncated(GemmError):
+    """GemmError::Truncated: the file holds fewer bytes than an expert."""
+
+    def __init__(self, expected: int, actual: int):
+        super().__init__(f"expert file truncated: expected {expected} bytes, got {actual}")
+        self.expected, self.actual = expected, actual
+
+
+def _section_sizes(hidden, inter, group_size, tiling):
+    """Byte sizes of the six sections (gate p/s, up p/s, down p/s) of an
+    expert in `tiling` (MFMA_UP_ROWS: gate and down tiled, up crate-layout)."""
+    crate_g = (inter * hidden // 2, inter * (hidden // group_size) * 2)
+    crate_d = (hidden * inter // 2, hidden * (inter // group_size) * 2)
+    if tiling == TILING_CRATE:
+        return [*crate_g, *crate_g, *crate_d]
+    tg = tiled_sizes(inter, hidden, group_size)
+    td = tiled_sizes(hidden, inter, group_size)
+    up = crate_g if tiling == TILING_MFMA_UP_ROWS else tg
+    return [*tg, *up, *td]
+
+
 class ExpertWeights:
     """One expert's flat blob in HBM with the six slice accessors of
-    format.rs:51-126 (any hidden / inter / group size)."""
+    format.rs:51-126 (any hidden / inter / group size).  In the crate layout
+    the sections are contiguous (format.rs:35-47); tiled blobs hold each
+    section 256-byte aligned."""
 
     def __init__(self, flat: torch.Tensor, hidden: int, inter: int, group_size: int = GROUP_SIZE,
                  scale_dtype: int = SCALE_BF16, tiling: int = TILING_CRATE):
         _dev(flat, "flat")
         _expect(flat.dtype == torch.uint8, "flat must be uint8")
+        _expect(tiling in (TILING_CRATE, TILING_MFMA, TILING_MFMA_UP_ROWS), "tiling")
         self.flat, self.hidden, self.inter = flat, hidden, inter
         self.group_size, self.scale_dtype, self.tiling = group_size, scale_dtype, tiling
-        if tiling == TILING_MFMA:
-            gp, gs = tiled_sizes(inter, hidden, group_size)
-            dp, ds = tiled_sizes(hidden, inter, group_size)
-            sz = [gp, gs, gp, gs, dp, ds]
-            o = [0]
+        sz = _section_sizes(hidden, inter, group_size, tiling)
+        o = [0]
+        if tiling == TILING_CRATE:
             for n in sz[:-1]:
-                o.append(o[-1] + ((n + 255) // 256) * 256)
-            need = int(lib().cascadia_int4_expert_tiled_bytes(hidden, inter, group_size))
-        else:
-            gp, gs = inter * hidden // 2, inter * (hidden // group_size) * 2
-            dp, ds = hidden * inter // 2, hidden * (inter // group_size) * 2
-            o = [0, gp, gp + gs, 2 * gp + gs, 2 * (gp + gs), 2 * (gp + gs) + dp]
-            sz = [gp, gs, gp, gs, dp, ds]
+                o.append(o[-1] + n)
             need = expert_bytes(hidden, inter, group_size)
+        else:
+            for n in sz[:-1]:
+                o.append(o[-1] + _align256(n))
+            need = o[-1] + sz[-1]
         _expect(flat.numel() >= need, f"flat expert too small: {flat.numel()} < {need}")
         self._slices = [flat[a:a + n] for a, n in zip(o, sz)]
 
-    def tiled(self) -> "ExpertWeights":
-        """The MFMA-tiled copy of this (crate-layout) expert."""
+    @staticmethod
+    def open(path, hidden: int = HIDDEN, inter: int = INTERMEDIATE,
+             group_size: int = GROUP_SIZE, scale_dtype: int = SCALE_BF16,
+             device: str | torch.device = "cuda") -> "ExpertWeights":
+        """ExpertWeights::open (format.rs:63-96): a flat expert file -- gate_p,
+        gate_s, up_p, up_s, down_p, down_s -- read into HBM.  The crate's dims
+        are K2.6's (HIDDEN x INTERMEDIATE, G 32, bf16 scales, lib.rs:71-78); a
+        file shorter than one expert raises GemmTruncated, an unreadable one
+        GemmError; extra bytes past the expert are ignored, as there."""
+        need = expert_bytes(hidden, inter, group_size)
+        try:
+            with open(path, "rb") as f:
+                f.seek(0, 2)
+                size = f.tell()
+                if size < need:
+                    raise GemmTruncated(need, size)
+                f.seek(0)
+                host = torch.empty(need, dtype=torch.uint8, pin_memory=True)
+                if f.readinto(memoryview(host.numpy())) != need:
+                    raise GemmError(f"{path}: short read")
+        except OSError as e:
+            raise GemmError(f"{path}: {e}") from e
+        flat = torch.empty(need + (-need) % 256, dtype=torch.uint8, device=device)
+        flat[:need].copy_(host, non_blocking=True)
+        torch.cuda.current_stream().synchronize()  # the pinned buffer is freed on return
+        return ExpertWeights(flat, hidden, inter, group_size, scale_dtype)
+
+    def tiled(self, up_rows: bool = False) -> "ExpertWeights":
+        """The MFMA-tiled copy of this (crate-layout) expert.  up_rows: keep up
+        in the crate layout (TILING_MFMA_UP_ROWS), for the activation-sparse
+        forms, which read up one row at a time."""
         _expect(self.tiling == TILING_CRATE, "already tiled")
-        nb = int(lib().cascadia_int4_expert_tiled_bytes(self.hidden, self.inter, self.group_size))
-        dst = torch.empty(nb, dtype=torch.uint8, device=self.flat.device)
-        src = _expert_struct(*self._slices)
-        out = Expert()
-        check("cascadia_int4_tile_expert", lib().cascadia_int4_tile_expert(
-            self.hidden, self.inter, self.group_size, C.byref(src), dst.data_ptr(), C.byref(out),
-            _stream()))
-        return ExpertWeights(dst, self.hidden, self.inter, self.group_size, self.scale_dtype,
-                             TILING_MFMA)
+        if not up_rows:
+            nb = int(lib().cascadia_int4_expert_tiled_bytes(self.hidden, self.inter,
+                                                            self.group_size))
+            dst = torch.empty(nb, dtype=torch.uint8, device=self.flat.device)
+            src = _expert_struct(*self._slices)
+            out = Expert()
+            check("cascadia_int4_tile_expert", lib().cascadia_int4_tile_expert(
+                self.hidden, self.inter, self.group_size, C.byref(src), dst.data_ptr(),
+                C.byref(out), _stream()))
+            return ExpertWeights(dst, self.hidden, self.inter, self.group_size,
+                                 self.scale_dtype, TILING_MFMA)
+        sz = _section_sizes(self.hidden, self.inter, self.group_size, TILING_MFMA_UP_ROWS)
+        o = [0]
+        for n in sz[:-1]:
+            o.append(o[-1] + _align256(n))
+        dst = torch.empty(o[-1] + _align256(sz[-1]), dtype=torch.uint8, device=self.flat.device)
+        H, I, G = self.hidden, self.inter, self.group_size
+        for src_i, (n, k) in ((0, (I, H)), (4, (H, I))):  # gate and down tiled
+            L = _layout(n, k, G, self.scale_dtype)
+            check("cascadia_int4_tile_weights", lib().cascadia_int4_tile_weights(
+                C.byref(L), self._slices[src_i].data_ptr(), self._slices[src_i + 1].data_ptr(),
+                dst.data_ptr() + o[src_i], dst.data_ptr() + o[src_i + 1], _stream()))
+        for j in (2, 3):  # up as it is
+            dst[o[j]:o[j] + sz[j]].copy_(self._slices[j])
+        return ExpertWeights(dst, H, I, G, self.scale_dtype, TILING_MFMA_UP_ROWS)
 
     def gate_packed_bytes(self): return self._slices[0]
     def gate_scale_bits(self): return self._slices[1]
@@ -222,19 +434,14 @@ def _ffn_dims(x, gate_packed, gate_scale, up_packed, up_scale, down_packed, down
               group_size, hidden=None, tiling=TILING_CRATE):
     hidden = hidden if hidden is not None else x.shape[-1]
     _expect(hidden % group_size == 0, "hidden must be a multiple of group_size")
-    if tiling == TILING_MFMA:
-        # tiled scales: [ceil(inter/16)*16, hidden/G] u16
-        inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
-        gp, gs = tiled_sizes(inter, hidden, group_size)
-        dp, ds = tiled_sizes(hidden, inter, group_size)
-    else:
-        # kernel.rs:86: intermediate inferred from the gate scale length
-        inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
-        gp, gs = inter * hidden // 2, inter * (hidden // group_size) * 2
-        dp, ds = hidden * inter // 2, hidden * (inter // group_size) * 2
+    # kernel.rs:86: intermediate inferred from the gate scale length (a
+    # tiled gate's scales cover inter rounded up to 16 rows; inter is a
+    # multiple of the group, so of 32)
+    inter = _nbytes(gate_scale) // 2 // (hidden // group_size)
     _expect(inter > 0 and inter % group_size == 0, "intermediate must be a multiple of group_size")
-    _expect(_nbytes(gate_packed) == gp and _nbytes(up_packed) == gp, "gate/up packed lengths")
-    _expect(_nbytes(up_scale) == gs and _nbytes(gate_scale) == gs, "gate/up scale lengths")
+    gp, gs, up, us, dp, ds = _section_sizes(hidden, inter, group_size, tiling)
+    _expect(_nbytes(gate_packed) == gp and _nbytes(up_packed) == up, "gate/up packed lengths")
+    _expect(_nbytes(gate_scale) == gs and _nbytes(up_scale) == us, "gate/up scale lengths")
     _expect(_nbytes(down_packed) == dp, "down packed length")
     _expect(_nbytes(down_scale) == ds, "down scale length")
     return hidden, inter
@@ -317,7 +524,7 @@ def _sparse_call(x, weights, out, threshold, thresholds, group_size, scale_dtype
     e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale,
                        tiling)
     ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
-    dense = thresholds is None and not threshold > 0.0  # SparsityMode::is_dense
+    dense = thresholds is None and threshold <= 0.0  # SparsityMode::is_dense (NaN: sparse)
     counts = None if dense else torch.empty(T, dtype=torch.int32, device=x.device)
     name = "cascadia_int4_ffn_forward_sparse_f32" if x_f32 else "cascadia_int4_expert_forward_sparse"
     check(name, getattr(lib(), name)(h, inter, group_size, scale_dtype, C.byref(e), x.data_ptr(),
@@ -360,13 +567,15 @@ def ffn_forward_sparse_axpy_f32_mode(x_f32, hidden, intermediate, gate_packed, g
     _expect(x_f32.numel() == T * hidden and out_f32.numel() == T * hidden,
             "x and out must be [n_tokens, hidden]")
     thr, tau = 0, 0.0
-    if isinstance(mode, torch.Tensor):
-        _dev(mode, "thresholds")
-        _expect(mode.dtype == torch.float32 and mode.numel() == intermediate,
-                f"per-channel thresholds length {mode.numel()} != intermediate {intermediate}")
-        thr = mode.contiguous().data_ptr()
+    m = SparsityMode.of(mode)
+    if m.thresholds is not None:
+        t = m.thresholds
+        _dev(t, "thresholds")
+        _expect(t.dtype == torch.float32 and t.numel() == intermediate,
+                f"per-channel thresholds length {t.numel()} != intermediate {intermediate}")
+        thr = t.data_ptr()
     else:
-        tau = float(mode)
+        tau = m.tau
     e = _expert_struct(gate_packed, gate_scale, up_packed, up_scale, down_packed_t,
                        down_scale_t_bits, tiling)
     ws = 0 if workspace is None else _dev(workspace, "workspace").data_ptr()
@@ -486,6 +695,29 @@ def ffn_forward_sparse_f32(x_f32, hidden, intermediate, gate_packed, gate_scale,
     return _sparse_call(x_f32, (gate_packed, gate_scale, up_packed, up_scale, down_packed,
                                 down_scale), out_f32, threshold, None, group_size, scale_dtype,
                         workspace, tiling, True, hidden, intermediate)
+
+
+def ffn_forward_sparse_f32_mode(x_f32, hidden, intermediate, gate_packed, gate_scale, up_packed,
+                                up_scale, down_packed, down_scale, out_f32, mode,
+                                group_size=GROUP_SIZE, scale_dtype=SCALE_BF16, workspace=None,
+                                tiling=TILING_CRATE):
+    """ffn_sparsity.rs:438-538, the body of both f32 entry points: mode is a
+    SparsityMode, a float (Global) or a per-channel device tensor."""
+    m = SparsityMode.of(mode)
+    return _sparse_call(x_f32, (gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                                down_scale), out_f32, m.tau, m.thresholds, group_size,
+                        scale_dtype, workspace, tiling, True, hidden, intermediate)
+
+
+def expert_forward_sparse_mode(x_bf16, gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                               down_scale, out_bf16, mode, group_size=GROUP_SIZE,
+                               scale_dtype=SCALE_BF16, workspace=None, tiling=TILING_CRATE):
+    """ffn_sparsity.rs:812-867: bf16 in / out, mode a SparsityMode, a float or
+    a per-channel device tensor; a dense mode is expert_forward."""
+    m = SparsityMode.of(mode)
+    return _sparse_call(x_bf16, (gate_packed, gate_scale, up_packed, up_scale, down_packed,
+                                 down_scale), out_bf16, m.tau, m.thresholds, group_size,
+                        scale_dtype, workspace, tiling, False)
 
 
 def ffn_forward_sparse_f32_per_channel(x_f32, hidden, intermediate, gate_packed, gate_scale,
@@ -755,6 +987,21 @@ class ExpertSource:
             self.close()
         except Exception:
             pass
+
+
+def stream_read(buf: torch.Tensor, sink: torch.Tensor | None = None) -> torch.Tensor:
+    """The benchmark's streaming-read ceiling: read every byte of `buf` the
+    way the decode GEMV streams its weights (8 KB per wave, non-temporal) and
+    XOR-fold the words into `sink` (int32 [1024], zeroed here when not given;
+    the XOR of its words is the XOR of buf's words)."""
+    _dev(buf, "buf")
+    if sink is None:
+        sink = torch.zeros(1024, dtype=torch.int32, device=buf.device)
+    _dev(sink, "sink")
+    _expect(sink.element_size() * sink.numel() == 4096, "sink must hold 1024 32-bit words")
+    check("cascadia_int4_stream_read", lib().cascadia_int4_stream_read(
+        buf.data_ptr(), _nbytes(buf), sink.data_ptr(), _stream()))
+    return sink
 
 
 def fill_bytes(out: torch.Tensor, seed: int, stream_id: int):

@@ -350,15 +350,18 @@ void expert_sections(uint32_t hidden, uint32_t inter, uint32_t group, size_t off
   off[5] = off[4] + dp;
 }
 
+// up_rows: the caller accepts CASCADIA_INT4_TILING_MFMA_UP_ROWS (the sparse
+// forms, which read up one row at a time).
 int check_expert(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
-                 const cascadia_int4_expert *e) {
+                 const cascadia_int4_expert *e, bool up_rows = false) {
   if (!e) return CASCADIA_INT4_ERR_NULL;
   if (!e->gate_packed || !e->gate_scale || !e->up_packed || !e->up_scale || !e->down_packed ||
       !e->down_scale)
     return CASCADIA_INT4_ERR_NULL;
   if (hidden == 0 || inter == 0 || group == 0 || group % 32) return CASCADIA_INT4_ERR_ARG;
   if (hidden % group || inter % group || sdt > 1) return CASCADIA_INT4_ERR_ARG;
-  if (e->tiling > CASCADIA_INT4_TILING_MFMA) return CASCADIA_INT4_ERR_ARG;
+  if (e->tiling > (up_rows ? CASCADIA_INT4_TILING_MFMA_UP_ROWS : CASCADIA_INT4_TILING_MFMA))
+    return CASCADIA_INT4_ERR_ARG;
   if (!aligned(e->gate_packed, 16) || !aligned(e->up_packed, 16) ||
       !aligned(e->down_packed, 16))
     return CASCADIA_INT4_ERR_ARG;
@@ -427,11 +430,15 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
                                  uint32_t n_tokens) {
   const cai4::SkinnyDevice d = device_props(dev);
   size_t part = 0;
-  const cai4::SkinnyPlan plans[4] = {
+  const cai4::SkinnyPlan plans[6] = {
       cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_XF32,
                         cai4::EPI_PAIR_F32, d),
       cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_BF16,
                         cai4::EPI_PAIR_F32, d),
+      cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_XF32,
+                        cai4::EPI_F32, d),
+      cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens, cai4::A_BF16,
+                        cai4::EPI_F32, d),
       cai4::skinny_plan((int)hidden, (int)inter, (int)group, (int)n_tokens, cai4::A_XF32,
                         cai4::EPI_F32, d),
       cai4::skinny_plan((int)hidden, (int)inter, (int)group, (int)n_tokens, cai4::A_XF32,
@@ -440,7 +447,7 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
   SparseWorkspace w;
   w.lanes = align256((size_t)n_tokens * inter * 4);
   w.slots = sparse_slot_bytes(inter, n_tokens);
-  w.cnt = align256((size_t)n_tokens * cai4::sparse_groups((int)inter) * 4);
+  w.cnt = align256((size_t)n_tokens * cai4::subset_groups((int)inter, 64) * 4);
   w.partials = part;
   w.total = 3 * w.lanes + w.slots + w.cnt + part;
   const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group, n_tokens, true);
@@ -490,6 +497,67 @@ int sparse_gate_up(const cascadia_int4_expert *e, uint32_t hidden, uint32_t inte
   return hip_status(cai4::sparse_slots(gate, (int)inter, (int)n_tokens, thr, stable, slots, st));
 }
 
+// The gate GEMM alone, f32 out, with the mask's max-|silu| slots (the
+// rows-subset forms, whose up is read later for the active lanes only): the
+// one-token GEMV's slot epilogue when it serves the shape, else any GEMM and
+// sparse_slots.  *n_slots: slot words per token.
+int sparse_gate(const uint8_t *gp, const uint8_t *gs, uint32_t tiling, uint32_t hidden,
+                uint32_t inter, uint32_t group, uint32_t sdt, const void *x, int amode,
+                uint32_t n_tokens, float *gate, const float *thr, bool stable, uint32_t *slots,
+                int *n_slots, void *part, bool may_alloc, hipStream_t st) {
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const cai4::SkinnyDevice d = device_props(dev);
+  cai4::SkinnyArgs g{};
+  g.w0 = gp;
+  g.s0 = gs;
+  g.x = x;
+  g.out = gate;
+  g.N = (int)inter;
+  g.K = (int)hidden;
+  g.G = (int)group;
+  g.M = (int)n_tokens;
+  g.sdt = (int)sdt;
+  g.tiled = (int)tiling;
+  g.slots = slots;
+  g.thr = thr;
+  g.silu_slot = stable ? 2 : 1;
+  if (n_tokens == 1 && cai4::gemv_supported(g, amode, cai4::EPI_F32, d.num_cus)) {
+    *n_slots = cai4::sparse_slots_per_token((int)inter, true);
+    return hip_status(cai4::gemv_launch(g, amode, cai4::EPI_F32, d.num_cus, 0, st));
+  }
+  int rc = run_gemm(gp, gs, nullptr, nullptr, (int)inter, (int)hidden, (int)group, (int)sdt,
+                    (int)tiling, x, nullptr, amode, (int)n_tokens, gate, nullptr, cai4::EPI_F32,
+                    st, part, may_alloc);
+  if (rc) return rc;
+  *n_slots = cai4::sparse_slots_per_token((int)inter, false);
+  return hip_status(cai4::sparse_slots(gate, (int)inter, (int)n_tokens, thr, stable, slots, st));
+}
+
+// The up matrix of an expert as rows for the rows-subset kernels.
+cai4::RowsMatrix up_rows(const cascadia_int4_expert *e, uint32_t hidden, uint32_t inter,
+                         uint32_t group, uint32_t sdt) {
+  cai4::RowsMatrix u{};
+  u.packed = e->up_packed;
+  u.scales = e->up_scale;
+  u.N = (int)inter;
+  u.K = (int)hidden;
+  u.G = (int)group;
+  u.sdt = (int)sdt;
+  u.tiled = e->tiling == CASCADIA_INT4_TILING_MFMA ? 1 : 0;
+  return u;
+}
+
+// Whether a sparse form reads up through the rows subset: every shape whose
+// hidden size the fused kernels take (a multiple of 32 up to 8192); the
+// mixed layout needs it.
+bool subset_path(uint32_t hidden) { return cai4::subset_supported((int)hidden); }
+
+// Gate and down layout of an expert (the mixed layout's are MFMA-tiled).
+int gd_tiling(const cascadia_int4_expert *e) {
+  return e->tiling == CASCADIA_INT4_TILING_CRATE ? 0 : 1;
+}
+
 // ffn_forward_sparse_f32_mode / expert_forward_sparse_mode
 // (ffn_sparsity.rs:438-538, 756-867): thresholds == nullptr is the global
 // tau, dense (the ordinary FFN) when tau <= 0.  Gate/up GEMM with the slots ->
@@ -498,13 +566,15 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
                   const cascadia_int4_expert *e, const void *x, bool x_f32, uint32_t n_tokens,
                   float tau, const float *thr, void *out, bool out_bf16, uint32_t *counts,
                   void *workspace, hipStream_t st) {
-  if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
+  if (int rc = check_expert(hidden, inter, group, sdt, e, true)) return rc;
+  const bool rows_up = e->tiling == CASCADIA_INT4_TILING_MFMA_UP_ROWS;
+  if (rows_up && !subset_path(hidden)) return CASCADIA_INT4_ERR_ARG;
   if (n_tokens == 0) return CASCADIA_INT4_OK;
   if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (n_tokens > 65535 || !aligned(x, 16) || (thr && !aligned(thr, 4)) ||
       (counts && !aligned(counts, 4)) || (workspace && !aligned(workspace, 16)))
     return CASCADIA_INT4_ERR_ARG;
-  if (!thr && tau <= 0.0f) {
+  if (!thr && tau <= 0.0f && !rows_up) {
     int rc = ffn_common(hidden, inter, group, sdt, e, x, x_f32, n_tokens, out, out_bf16,
                         workspace, st);
     if (rc || !counts) return rc;
@@ -529,6 +599,36 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   uint32_t *cnt = reinterpret_cast<uint32_t *>(b + 3 * w.lanes + w.slots);
   void *part = w.partials ? b + 3 * w.lanes + w.slots + w.cnt : nullptr;
   int n_slots = 0;
+  if (subset_path(hidden)) {
+    // gate in full, then per 128-lane group the mask and the up rows of the
+    // active lanes only (ffn_sparsity.rs:499-527), then the down in full
+    (void)upv;
+    int rc = sparse_gate(e->gate_packed, e->gate_scale, gd_tiling(e), hidden, inter, group, sdt,
+                         x, amode, n_tokens, gate, thr, true, slots, &n_slots, part, true, st);
+    if (rc) return rc;
+    cai4::SparseSubsetArgs a{};
+    a.gate = gate;
+    a.slots = slots;
+    a.n_slots = n_slots;
+    a.thr = thr;
+    a.tau = tau;
+    a.up = up_rows(e, hidden, inter, group, sdt);
+    a.x = x;
+    a.x_bf16 = x_f32 ? 0 : 1;
+    a.I = (int)inter;
+    a.H = (int)hidden;
+    a.lanes = cai4::subset_lanes((int)inter, device_props(dev).num_cus);
+    a.cnt = cnt;
+    a.inter = mid;
+    if ((rc = hip_status(cai4::sparse_subset_mask(a, (int)n_tokens, st)))) return rc;
+    if (counts && (rc = hip_status(cai4::sparse_counts(cnt, cai4::subset_groups((int)inter, a.lanes),
+                                                       (int)n_tokens, counts, st))))
+      return rc;
+    return run_gemm(e->down_packed, e->down_scale, nullptr, nullptr, (int)hidden, (int)inter,
+                    (int)group, (int)sdt, gd_tiling(e), mid, nullptr, cai4::A_XF32,
+                    (int)n_tokens, out, nullptr, out_bf16 ? cai4::EPI_BF16 : cai4::EPI_F32, st,
+                    part);
+  }
   int rc = sparse_gate_up(e, hidden, inter, group, sdt, x, amode, n_tokens, gate, upv, thr, true,
                           slots, &n_slots, part, true, st);
   if (rc) return rc;
@@ -564,16 +664,25 @@ AxpyFfnWorkspace axpy_ffn_workspace(int dev, uint32_t hidden, uint32_t inter, ui
                                     uint32_t n_tokens) {
   const cai4::SkinnyDevice d = device_props(dev);
   AxpyFfnWorkspace w;
-  const size_t row_set = (size_t)cai4::sparse_groups((int)inter) * hidden * 4;  // one token's
+  // one token's partial rows: one per lane group (128 lanes on the
+  // rows-subset path, 256 on the other)
+  const int groups = subset_path(hidden)
+                         ? cai4::subset_groups((int)inter, cai4::subset_lanes((int)inter, d.num_cus))
+                         : cai4::sparse_groups((int)inter);
+  const size_t row_set = (size_t)groups * hidden * 4;
   // at most ~32 MB of partial rows per launch pair
   const size_t fit = ((size_t)32 << 20) / row_set;
   w.chunk = (uint32_t)(fit < 1 ? 1 : fit < n_tokens ? fit : n_tokens);
   w.lanes = align256((size_t)n_tokens * inter * 4);
   w.slots = sparse_slot_bytes(inter, n_tokens);
-  w.cnt = align256((size_t)n_tokens * cai4::sparse_groups((int)inter) * 4);
-  w.part_gemm = align256(cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens,
-                                           cai4::A_XF32, cai4::EPI_PAIR_F32, d)
-                             .partial_bytes);
+  w.cnt = align256((size_t)n_tokens * groups * 4);
+  const size_t pp = cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens,
+                                      cai4::A_XF32, cai4::EPI_PAIR_F32, d)
+                        .partial_bytes;
+  const size_t pg = cai4::skinny_plan((int)inter, (int)hidden, (int)group, (int)n_tokens,
+                                      cai4::A_XF32, cai4::EPI_F32, d)
+                        .partial_bytes;  // the gate alone (rows-subset path)
+  w.part_gemm = align256(pp > pg ? pp : pg);
   w.rows = align256((size_t)w.chunk * row_set);
   w.total = 2 * w.lanes + w.slots + w.cnt + w.part_gemm + w.rows;
   return w;
@@ -589,7 +698,9 @@ int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
              const cascadia_int4_expert *e, const float *x, uint32_t n_tokens, float tau,
              const float *thr, float *out, uint32_t *counts_out, void *workspace,
              hipStream_t st) {
-  if (int rc = check_expert(hidden, inter, group, sdt, e)) return rc;
+  if (int rc = check_expert(hidden, inter, group, sdt, e, true)) return rc;
+  if (e->tiling == CASCADIA_INT4_TILING_MFMA_UP_ROWS && !subset_path(hidden))
+    return CASCADIA_INT4_ERR_ARG;
   if (n_tokens == 0) return CASCADIA_INT4_OK;
   if (!x || !out) return CASCADIA_INT4_ERR_NULL;
   if (hidden % 32 || n_tokens > 65535 || !aligned(x, 16) || !aligned(out, 16) ||
@@ -618,6 +729,39 @@ int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
   b += w.part_gemm;
   float *rows = reinterpret_cast<float *>(b);
   int n_slots = 0;
+  if (subset_path(hidden)) {
+    // gate in full; per 128-lane group the mask, the up rows and the
+    // transposed-down rows of the active lanes only, into the group's
+    // partial row; the partial rows added in group order
+    (void)upv;
+    int rc = sparse_gate(e->gate_packed, e->gate_scale, gd_tiling(e), hidden, inter, group, sdt,
+                         x, cai4::A_XF32, n_tokens, gate, thr, false, slots, &n_slots, part_gemm,
+                         workspace == nullptr, st);
+    if (rc) return rc;
+    cai4::SparseSubsetArgs a{};
+    a.gate = gate;
+    a.slots = slots;
+    a.n_slots = n_slots;
+    a.thr = thr;
+    a.tau = tau;
+    a.up = up_rows(e, hidden, inter, group, sdt);
+    a.x = x;
+    a.x_bf16 = 0;
+    a.I = (int)inter;
+    a.H = (int)hidden;
+    a.lanes = cai4::subset_lanes((int)inter, device_props(dev).num_cus);
+    a.cnt = cnt;
+    a.dt = e->down_packed;
+    a.dt_s = reinterpret_cast<const uint16_t *>(e->down_scale);
+    a.partial = rows;
+    hipError_t err = hipSuccess;
+    for (uint32_t t0 = 0; t0 < n_tokens && err == hipSuccess; t0 += w.chunk) {
+      const uint32_t nt = n_tokens - t0 < w.chunk ? n_tokens - t0 : w.chunk;
+      a.t0 = (int)t0;
+      err = cai4::sparse_subset_axpy(a, (int)nt, out, counts_out, st);
+    }
+    return hip_status(err);
+  }
   int rc = sparse_gate_up(e, hidden, inter, group, sdt, x, cai4::A_XF32, n_tokens, gate, upv,
                           thr, false, slots, &n_slots, part_gemm, workspace == nullptr, st);
   if (rc) return rc;
@@ -1213,6 +1357,59 @@ int cascadia_int4_dequant_gemv(const cascadia_int4_layout *L, const uint8_t *pac
   return cascadia_int4_dequant_gemm_multi(L, packed, scale_bits, x, 1, y, stream);
 }
 
+int cascadia_int4_dequant_gemv_rows_subset(const cascadia_int4_layout *L, const uint8_t *packed,
+                                           const uint8_t *scale_bits, const float *x, float *y,
+                                           const uint32_t *active_rows, uint32_t n_active,
+                                           void *stream) {
+  if (int rc = check_layout(L)) return rc;
+  if (int rc = check_weights(packed, scale_bits)) return rc;
+  if (n_active == 0) return CASCADIA_INT4_OK;
+  if (!x || !y || !active_rows) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(x, 16) || !aligned(y, 4) || !aligned(active_rows, 4) || n_active > (1u << 30))
+    return CASCADIA_INT4_ERR_ARG;
+  int dev;
+  if (int rc = current_device(&dev)) return rc;
+  const cai4::SkinnyDevice d = device_props(dev);
+  cai4::RowsMatrix w{};
+  w.packed = packed;
+  w.scales = scale_bits;
+  w.N = (int)L->n_rows;
+  w.K = (int)L->k_cols;
+  w.G = (int)L->group_size;
+  w.sdt = (int)L->scale_dtype;
+  w.tiled = (int)L->tiling;
+  return hip_status(cai4::rows_subset(w, x, false, active_rows, (int)n_active, y, d.max_lds,
+                                      d.num_cus, static_cast<hipStream_t>(stream)));
+}
+
+int cascadia_int4_build_active_mask(const float *gate_out, uint32_t n, float threshold,
+                                    const float *thresholds, float *silu_out,
+                                    uint32_t *active_out, uint32_t *n_active_out,
+                                    void *stream) {
+  if (n == 0) return CASCADIA_INT4_OK;
+  if (!gate_out || !silu_out || !active_out || !n_active_out) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(gate_out, 4) || !aligned(silu_out, 4) || !aligned(active_out, 4) ||
+      !aligned(n_active_out, 4) || (thresholds && !aligned(thresholds, 4)) || n > (1u << 24))
+    return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::build_active_mask(gate_out, (int)n, threshold, thresholds, silu_out,
+                                            active_out, n_active_out,
+                                            static_cast<hipStream_t>(stream)));
+}
+
+int cascadia_int4_f32_to_bf16(const float *x, size_t n, uint16_t *out_bf16, void *stream) {
+  if (n == 0) return CASCADIA_INT4_OK;
+  if (!x || !out_bf16) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(x, 4) || !aligned(out_bf16, 2)) return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::f32_to_bf16_n(x, out_bf16, n, static_cast<hipStream_t>(stream)));
+}
+
+int cascadia_int4_bf16_to_f32(const uint16_t *x_bf16, size_t n, float *out, void *stream) {
+  if (n == 0) return CASCADIA_INT4_OK;
+  if (!x_bf16 || !out) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(x_bf16, 2) || !aligned(out, 4)) return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::bf16_to_f32_n(x_bf16, out, n, static_cast<hipStream_t>(stream)));
+}
+
 int cascadia_int4_dequant_gemm_multi(const cascadia_int4_layout *L, const uint8_t *packed,
                                      const uint8_t *scale_bits, const float *xs, uint32_t seq,
                                      float *ys, void *stream) {
@@ -1600,6 +1797,13 @@ int cascadia_int4_quantize_bf16(const uint16_t *w_bf16, uint32_t n_rows, uint32_
     return CASCADIA_INT4_ERR_ARG;
   return hip_status(cai4::quantize_group(w_bf16, (int)n_rows, (int)k_cols, (int)group_size,
                                          packed, scale_bits, (hipStream_t)stream));
+}
+
+int cascadia_int4_stream_read(const void *buf, size_t bytes, uint32_t *sink, void *stream) {
+  if (bytes == 0) return CASCADIA_INT4_OK;
+  if (!buf || !sink) return CASCADIA_INT4_ERR_NULL;
+  if (!aligned(buf, 16) || bytes % 16 || !aligned(sink, 4)) return CASCADIA_INT4_ERR_ARG;
+  return hip_status(cai4::stream_read(buf, bytes, sink, static_cast<hipStream_t>(stream)));
 }
 
 int cascadia_int4_fill_synthetic(uint32_t kind, uint64_t seed, uint64_t stream_id, size_t n,

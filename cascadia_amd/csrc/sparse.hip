@@ -31,6 +31,7 @@
 //                        (deterministic), and the groups' counts.
 #include "int4_common.hpp"
 #include "sparse.hpp"
+#include "tuning.hpp"
 
 namespace cai4 {
 
@@ -277,15 +278,17 @@ __global__ void __launch_bounds__(1024)
   const float *p = partial + (size_t)tl * n_groups * H;
   float s = 0.0f;
   if (h < H) {
-    for (int k = wave; k < n_groups; k += 16 * 8) {
-      float v[8];
+    // 16 loads in flight per thread: up to 256 groups in one round
+    for (int k = wave; k < n_groups; k += 16 * 16) {
+      float v[16];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < 16; ++j) {
         const int kk = k + 16 * j;
-        v[j] = kk < n_groups ? p[(size_t)kk * H + h] : 0.0f;
+        v[j] = p[(size_t)(kk < n_groups ? kk : k) * H + h];
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s += v[j];
+      for (int j = 0; j < 16; ++j)
+        if (k + 16 * j < n_groups) s += v[j];
     }
   }
   s_sum[wave][lane] = s;
@@ -307,6 +310,456 @@ __global__ void __launch_bounds__(64)
                          uint32_t *__restrict__ counts) {
   const uint32_t c = wave_count_sum(cnt + (size_t)blockIdx.x * n_groups, n_groups, threadIdx.x);
   if (threadIdx.x == 0) counts[blockIdx.x] = c;
+}
+
+// ---------------------------------------------------------------------------
+// rows-subset GEMV (ffn_sparsity.rs:187-348) and the sparse forms over it
+// ---------------------------------------------------------------------------
+//
+// A row is read in 16-byte chunks, chunk c holding columns 32c .. 32c + 31
+// (inside one scale group: G is a multiple of 32); lane l of a wave takes
+// chunks l, l + 64, ...  Crate layout: chunk c is the row's bytes 16c ..
+// 16c + 15 (byte b = columns 2b | 2b + 1).  Tiled layout (layout.hip): part
+// c % 4 of the row's k-block c / 4, each dword's byte b holding columns b |
+// b + 4.  Per chunk a lane forms sum(n * x) over the nibble codes n and takes
+// the zero point off with the chunk's sum of x (q = n - 8); the chunk's scale
+// multiplies that, the lane adds its chunks, and the wave adds its lanes:
+// f32 throughout (the crate's per-row sum in another order).
+
+CAI4_DEV size_t rm_chunk(const RowsMatrix &w, int r, int c) {
+  if (!w.tiled) return (size_t)r * (size_t)(w.K / 2) + 16 * (size_t)c;
+  const size_t KB = (size_t)(w.K + 127) / 128;
+  return ((size_t)(r >> 4) * KB + (size_t)(c >> 2)) * 1024 + 16 * (size_t)((r & 15) + 16 * (c & 3));
+}
+CAI4_DEV size_t rm_scale(const RowsMatrix &w, int r, int c) {
+  const int NG = w.K / w.G, g = (32 * c) / w.G;
+  if (!w.tiled) return (size_t)r * NG + g;
+  return ((size_t)(r >> 4) * NG + g) * 16 + (r & 15);
+}
+
+// sum over the chunk's 32 columns of nibble * x, x the chunk's 32 values.
+template <bool TILED>
+CAI4_DEV float chunk_nx(const u32x4_t v, const float *xc) {
+  float s0 = 0.f, s1 = 0.f;
+  const uint32_t dw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const f32x4_t xa = *reinterpret_cast<const f32x4_t *>(xc + 8 * d);
+    const f32x4_t xb = *reinterpret_cast<const f32x4_t *>(xc + 8 * d + 4);
+    const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    const uint32_t t = dw[d] & 0x0F0F0F0Fu, u = (dw[d] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = (float)((t >> (8 * k)) & 0xFFu), b = (float)((u >> (8 * k)) & 0xFFu);
+      if (TILED) {  // byte k: columns k (low nibble) and k + 4 (high)
+        s0 = fmaf(a, xv[k], s0);
+        s1 = fmaf(b, xv[k + 4], s1);
+      } else {  // byte k: columns 2k and 2k + 1
+        s0 = fmaf(a, xv[2 * k], s0);
+        s1 = fmaf(b, xv[2 * k + 1], s1);
+      }
+    }
+  }
+  return s0 + s1;
+}
+
+CAI4_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// x in LDS: chunk c's 32 values at xs + kXPad * c (a 16-byte pad after every
+// chunk): the lanes of a wave read 32 consecutive values each, chunks apart,
+// and with an unpadded 128-byte stride every lane would hit the same banks.
+constexpr int kXPad = 36;
+
+// Stage one row of x (K values, f32 or bf16 bits) into xs as f32, chunk c at
+// xs + XS * c, and each 32-column chunk's sum into sxs, by all 256 threads:
+// rounds of kStageLoads 4-value loads per thread, all of a round issued
+// before any is used (a load per step would cost a memory round trip each),
+// then the LDS stores and the chunk sums (the 8 threads of a chunk add their
+// partial sums by shuffles).
+constexpr int kStageLoads = 8;
+template <int XS>
+CAI4_DEV void stage_x(const void *x, int x_bf16, int K, float *xs, float *sxs) {
+  const int n4 = K / 4;  // 4-value items; K is a multiple of 32, so n4 of 8
+  for (int i0 = 0; i0 < n4; i0 += 256 * kStageLoads) {
+    f32x4_t v[kStageLoads];
+#pragma unroll
+    for (int u = 0; u < kStageLoads; ++u) {
+      const int i = i0 + 256 * u + threadIdx.x;
+      const int ic = i < n4 ? i : n4 - 1;  // past the row: a valid item, unused
+      if (x_bf16) {
+        const u32x2_t b = reinterpret_cast<const u32x2_t *>(x)[ic];
+        v[u] = f32x4_t{bitsf(b.x << 16), bitsf(b.x & 0xFFFF0000u), bitsf(b.y << 16),
+                       bitsf(b.y & 0xFFFF0000u)};
+      } else {
+        v[u] = reinterpret_cast<const f32x4_t *>(x)[ic];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kStageLoads; ++u) {
+      const int i = i0 + 256 * u + threadIdx.x;
+      // uniform per 8-thread chunk: n4 and 256 are multiples of 8
+      if (i0 + 256 * u >= n4) break;
+      if (i < n4) *reinterpret_cast<f32x4_t *>(xs + XS * (i >> 3) + 4 * (i & 7)) = v[u];
+      float p = (v[u].x + v[u].y) + (v[u].z + v[u].w);
+      p += __shfl_xor(p, 1, 64);
+      p += __shfl_xor(p, 2, 64);
+      p += __shfl_xor(p, 4, 64);
+      if ((i & 7) == 0 && i < n4) sxs[i >> 3] = p;
+    }
+  }
+}
+
+// acc[u] += the dot products of rows r[u] (ok[u]) over this lane's chunk
+// slots j0 .. j0 + JB - 1 (chunk (j0 + j) * 64 + lane).  Every load of the
+// batch is issued before any is used, and unconditionally: a dead slot (row
+// not ok, chunk past K) reads a valid chunk (row r[u], the last chunk) whose
+// value is then not used -- a select between a load and a constant would make
+// the wave wait for each load in turn.  r[u] must be a valid row for every u.
+template <int RB, int JB, bool TILED, int SDT, int XS>
+CAI4_DEV void rows_dot(const RowsMatrix &w, const int (&r)[RB], const bool (&ok)[RB], int j0,
+                       int lane, const float *xs, const float *sxs, float (&acc)[RB]) {
+  const int nch = w.K >> 5;
+  u32x4_t v[RB][JB];
+  uint32_t sb[RB][JB];
+  const uint16_t *sc = reinterpret_cast<const uint16_t *>(w.scales);
+#pragma unroll
+  for (int u = 0; u < RB; ++u)
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int c0 = (j0 + j) * 64 + lane, c = c0 < nch ? c0 : nch - 1;
+      v[u][j] = *reinterpret_cast<const u32x4_t *>(w.packed + rm_chunk(w, r[u], c));
+      sb[u][j] = (uint32_t)sc[rm_scale(w, r[u], c)];
+    }
+#pragma unroll
+  for (int u = 0; u < RB; ++u)
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int c = (j0 + j) * 64 + lane;
+      if (ok[u] && c < nch) {
+        const float d = fmaf(-8.0f, sxs[c], chunk_nx<TILED>(v[u][j], xs + XS * c));
+        acc[u] = fmaf(scale_to_f32<SDT>(sb[u][j]), d, acc[u]);
+      }
+    }
+}
+
+// The standalone rows-subset GEMV: each wave takes RB listed rows at a time.
+template <bool TILED, int SDT, bool XL>
+__global__ void __launch_bounds__(256)
+    rows_subset_kernel(RowsMatrix w, const void *x, int x_bf16, const uint32_t *__restrict__ rows,
+                       int n, float *__restrict__ y, float *__restrict__ xg) {
+  constexpr int RB = 4, JB = 2;
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // read as f32x4
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float *xs, *sxs;
+  if (XL) {
+    stage_x<kXPad>(x, x_bf16, w.K, s_dyn, s_dyn + (w.K / 32) * kXPad);
+    __syncthreads();
+    xs = s_dyn;
+    sxs = s_dyn + (w.K / 32) * kXPad;
+  } else {  // x and its chunk sums staged once in global memory by the host's launch
+    xs = xg;
+    sxs = xg + w.K;
+  }
+  const int nch = w.K >> 5, jmax = (nch + 63) / 64;
+  for (int f0 = (blockIdx.x * 4 + wave) * RB; f0 < n; f0 += gridDim.x * 4 * RB) {
+    int r[RB];
+    bool ok[RB];
+    float acc[RB];
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int f = f0 + u;
+      const uint32_t rr = f < n ? rows[f] : 0xFFFFFFFFu;
+      ok[u] = rr < (uint32_t)w.N;
+      r[u] = ok[u] ? (int)rr : 0;
+      acc[u] = 0.f;
+    }
+    for (int j0 = 0; j0 < jmax; j0 += JB)
+      rows_dot<RB, JB, TILED, SDT, XL ? kXPad : 32>(w, r, ok, j0, lane, xs, sxs, acc);
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const float s = wave_sum(acc[u]);
+      if (lane == 0 && ok[u]) y[r[u]] = s;
+    }
+  }
+}
+
+// x (f32 or bf16) of one row -> f32 copy and chunk sums in global memory, for
+// a rows-subset GEMV whose K does not fit LDS.
+__global__ void __launch_bounds__(256)
+    stage_x_global_kernel(const void *x, int x_bf16, int K, float *__restrict__ xg) {
+  // one workgroup per 8192 columns: stage_x over that slice
+  const int c0 = blockIdx.x * 8192, k = K - c0 < 8192 ? K - c0 : 8192;
+  const void *xs = x_bf16 ? (const void *)(reinterpret_cast<const uint16_t *>(x) + c0)
+                          : (const void *)(reinterpret_cast<const float *>(x) + c0);
+  stage_x<32>(xs, x_bf16, k, xg + c0, xg + K + c0 / 32);
+}
+
+// f32 slots before the chunk sums in the fused kernels' LDS: the padded x,
+// which the AXPY's wave rows (2048 C values) reuse afterwards.
+__host__ __device__ inline int subset_x_floats(int H, int C) {
+  const int xf = (H / 32) * kXPad;
+  return xf > 2048 * C ? xf : 2048 * C;
+}
+
+// The fused sparse forms: workgroup (group g of kSubsetGroup lanes, token).
+// Threads 0 .. kSubsetGroup - 1 each test one lane; the active lanes are
+// listed in ascending order (ballot + mbcnt); wave w takes entries w, w + 4,
+// ... RB at a time, reading their up rows (and, AXPY, their transposed-down
+// rows) in one round of loads.  C: chunk slots per lane (K and H <= 2048 C).
+// AXPY: lane l owns columns 32(l + 64 j) .. + 31 of the output (j < C):
+// combined = inter * scale, acc += combined * n, the -8 applied once per
+// chunk slot at the end (ffn_axpy.rs:118-134); the four waves' rows are added
+// in wave order (3, 2, 1, 0) into the group's partial row.
+template <bool AXPY, bool TILED, int SDT, int C>
+__global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) {
+  constexpr int RB = C <= 2 ? 4 : 2;
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // read as f32x4
+  __shared__ float s_red[4];
+  __shared__ uint32_t s_flag[4], s_wn[2];
+  __shared__ uint32_t s_id[kSubsetGroup];
+  __shared__ float s_val[kSubsetGroup];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.x, tl = blockIdx.y, t = a.t0 + tl;
+  const int H = a.H;
+  // [max(H / 32 * kXPad, 2048 C)] f32: x (padded chunks), then the AXPY's
+  // wave rows; then [H / 32] chunk sums
+  float *xs = s_dyn;
+  float *sxs = s_dyn + subset_x_floats(H, C);
+  // the token's slots: every thread folds its share (loads issued first)
+  const uint32_t *sl = a.slots + (size_t)t * a.n_slots;
+  uint32_t sv[kSlotLoads];
+#pragma unroll
+  for (int u = 0; u < kSlotLoads; ++u) {
+    const int k = tid + 256 * u;
+    sv[u] = k < a.n_slots ? sl[k] : 0u;
+  }
+  const int i = g * a.lanes + tid;
+  const bool in = tid < a.lanes && i < a.I;
+  const float gv = in ? a.gate[(size_t)t * a.I + i] : 0.0f;
+  const float th = in && a.thr ? a.thr[i] : 0.0f;
+  stage_x<kXPad>(a.x_bf16 ? (const void *)(reinterpret_cast<const uint16_t *>(a.x) + (size_t)t * H)
+                          : (const void *)(reinterpret_cast<const float *>(a.x) + (size_t)t * H),
+                 a.x_bf16, H, xs, sxs);
+  float m = 0.0f;
+  uint32_t f = 0u;
+#pragma unroll
+  for (int u = 0; u < kSlotLoads; ++u) {
+    m = fmaxf(m, bitsf(sv[u] & 0x7FFFFFFFu));
+    f |= sv[u] >> 31;
+  }
+  for (int k = tid + 256 * kSlotLoads; k < a.n_slots; k += 256) {
+    const uint32_t u = sl[k];
+    m = fmaxf(m, bitsf(u & 0x7FFFFFFFu));
+    f |= u >> 31;
+  }
+  m = wave_max(m);
+  const bool fw = __ballot(f != 0u) != 0ull;
+  if (lane == 0) {
+    s_red[wave] = m;
+    s_flag[wave] = fw ? 1u : 0u;
+  }
+  __syncthreads();
+  float mx = 0.0f;
+  bool any = false;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mx = fmaxf(mx, s_red[w]);
+    any = any || s_flag[w] != 0u;
+  }
+  // SparsityMode::is_dense (ffn_sparsity.rs:85-90); the GEMV form's mask uses
+  // build_active_mask_mode's stable SiLU, the AXPY form the plain one
+  const bool sparse = a.thr ? any : !(a.tau <= 0.0f);
+  const bool all = !sparse || mx == 0.0f;
+  const float sg = !AXPY && sparse ? silu_stable(gv) : silu_plain(gv);
+  const bool on = in && (all || fabsf(sg) >= (a.thr ? th : a.tau) * mx);
+  if (!AXPY && in && !on) a.inter[(size_t)t * a.I + i] = 0.0f;
+  const uint64_t b = __ballot(on);
+  const uint32_t rank = wave_rank(b);
+  if (lane == 0 && wave < 2) s_wn[wave] = (uint32_t)__popcll(b);
+  __syncthreads();
+  const uint32_t n = s_wn[0] + s_wn[1];
+  if (on) {
+    const uint32_t at = (wave == 0 ? 0u : s_wn[0]) + rank;
+    s_id[at] = (uint32_t)i;
+    s_val[at] = sg;
+  }
+  if (tid == 0) a.cnt[(size_t)t * gridDim.x + g] = n;
+  __syncthreads();
+
+  const int nhc = H >> 5;
+  float acc[AXPY ? C : 1][AXPY ? 32 : 1];
+  float csum[AXPY ? C : 1];
+  if (AXPY) {
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      csum[j] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 32; ++k) acc[j][k] = 0.0f;
+    }
+  }
+  for (int f0 = wave; f0 < (int)n; f0 += 4 * RB) {
+    int r[RB];
+    bool ok[RB];
+    float up[RB];
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int fe = f0 + 4 * u;
+      ok[u] = fe < (int)n;
+      r[u] = (int)s_id[ok[u] ? fe : f0];
+      up[u] = 0.0f;
+    }
+    // the transposed down's rows of the batch, issued with the up rows
+    u32x4_t dq[AXPY ? RB : 1][AXPY ? C : 1];
+    uint32_t ds[AXPY ? RB : 1][AXPY ? C : 1];
+    if (AXPY) {  // unconditional, from valid addresses (see rows_dot)
+#pragma unroll
+      for (int u = 0; u < RB; ++u)
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+          const int c0 = j * 64 + lane, c = c0 < nhc ? c0 : nhc - 1;
+          dq[u][j] = *reinterpret_cast<const u32x4_t *>(a.dt + (size_t)r[u] * (H / 2) + 16 * c);
+          ds[u][j] = (uint32_t)a.dt_s[(size_t)r[u] * nhc + c];
+        }
+    }
+    rows_dot<RB, C, TILED, SDT, kXPad>(a.up, r, ok, 0, lane, xs, sxs, up);
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int fe = f0 + 4 * u;
+      // inter[r] = silu_gate[r] * up[r] (ffn_sparsity.rs:527, 711-716)
+      const float v = ok[u] ? s_val[fe] * wave_sum(up[u]) : 0.0f;
+      if (!AXPY) {
+        if (lane == 0 && ok[u]) a.inter[(size_t)t * a.I + r[u]] = v;
+      } else {
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+          // a dead slot adds nothing (v is 0 for a row past the list)
+          const float comb = j * 64 + lane < nhc ? v * bf16_to_f32(ds[u][j]) : 0.0f;
+          const uint32_t dw[4] = {dq[u][j].x, dq[u][j].y, dq[u][j].z, dq[u][j].w};
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t lo = dw[d] & 0x0F0F0F0Fu, hi = (dw[d] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {  // byte k of dword d: columns 8d + 2k, 8d + 2k + 1
+              acc[j][8 * d + 2 * k] =
+                  fmaf(comb, (float)((lo >> (8 * k)) & 0xFFu), acc[j][8 * d + 2 * k]);
+              acc[j][8 * d + 2 * k + 1] =
+                  fmaf(comb, (float)((hi >> (8 * k)) & 0xFFu), acc[j][8 * d + 2 * k + 1]);
+            }
+          }
+          csum[j] += comb;
+        }
+      }
+    }
+  }
+  if (!AXPY) return;
+#pragma unroll
+  for (int j = 0; j < C; ++j)
+#pragma unroll
+    for (int k = 0; k < 32; ++k) acc[j][k] = fmaf(-8.0f, csum[j], acc[j][k]);
+  // waves 3, 2, 1 hand their rows down through LDS (x is no longer read)
+  __syncthreads();
+  for (int w = 3; w >= 0; --w) {
+    if (wave == w) {
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        float *row = xs + (size_t)(j * 64 + lane) * 32;
+#pragma unroll
+        for (int k4 = 0; k4 < 8; ++k4) {
+          f32x4_t v = {acc[j][4 * k4], acc[j][4 * k4 + 1], acc[j][4 * k4 + 2], acc[j][4 * k4 + 3]};
+          if (w < 3) {
+            const f32x4_t p = *reinterpret_cast<const f32x4_t *>(row + 4 * k4);
+            v = f32x4_t{v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w};
+          }
+          if (w > 0) {
+            *reinterpret_cast<f32x4_t *>(row + 4 * k4) = v;
+          } else if (32 * (j * 64 + lane) < H) {
+            float *prow = a.partial + ((size_t)tl * gridDim.x + g) * H + 32 * (j * 64 + lane);
+            *reinterpret_cast<f32x4_t *>(prow + 4 * k4) = v;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// build_active_mask_mode (ffn_sparsity.rs:131-179) over one row, one
+// workgroup of 1024 threads: the stable SiLU of every lane and the max |silu|
+// (a NaN never raises it, as `m > max_abs` in the crate), then the active
+// lanes in ascending order, 1024 at a time (ballot, wave counts, a scan of the
+// 16 wave counts).
+__global__ void __launch_bounds__(1024)
+    build_mask_kernel(const float *__restrict__ gate, int n, float tau,
+                      const float *__restrict__ thr, float *__restrict__ silu,
+                      uint32_t *__restrict__ active, uint32_t *__restrict__ n_active) {
+  __shared__ float s_m[16];
+  __shared__ uint32_t s_f[16], s_c[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float m = 0.0f;
+  uint32_t pos = 0u;
+  for (int i = tid; i < n; i += 1024) {
+    const float v = silu_stable(gate[i]);
+    silu[i] = v;
+    const float a = fabsf(v);
+    m = a > m ? a : m;
+    if (thr && !(thr[i] <= 0.0f)) pos = 1u;
+  }
+  m = wave_max(m);
+  const bool pw = __ballot(pos != 0u) != 0ull;
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_f[wave] = pw ? 1u : 0u;
+  }
+  __syncthreads();
+  float mx = 0.0f;
+  bool any = false;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    mx = s_m[w] > mx ? s_m[w] : mx;
+    any = any || s_f[w] != 0u;
+  }
+  // SparsityMode::is_dense (ffn_sparsity.rs:85-90), or a zero max: every lane
+  const bool all = mx == 0.0f || (thr ? !any : tau <= 0.0f);
+  uint32_t base = 0u;
+  for (int i0 = 0; i0 < n; i0 += 1024) {
+    const int i = i0 + tid;
+    bool on = false;
+    if (i < n) {
+      const float cut = (thr ? thr[i] : tau) * mx;
+      on = all || fabsf(silu[i]) >= cut;
+    }
+    const uint64_t b = __ballot(on);
+    if (lane == 0) s_c[wave] = (uint32_t)__popcll(b);
+    __syncthreads();
+    uint32_t off = base, tot = 0u;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      if (w < wave) off += s_c[w];
+      tot += s_c[w];
+    }
+    if (on) active[off + wave_rank(b)] = (uint32_t)i;
+    base += tot;
+    __syncthreads();
+  }
+  if (tid == 0) *n_active = base;
+}
+
+__global__ void f32_to_bf16_kernel(const float *__restrict__ x, uint16_t *__restrict__ y,
+                                   size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = (uint16_t)f32_to_bf16_rne(x[i]);
+}
+
+__global__ void bf16_to_f32_kernel(const uint16_t *__restrict__ x, float *__restrict__ y,
+                                   size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = bf16_to_f32(x[i]);
 }
 
 }  // namespace
@@ -354,6 +807,139 @@ hipError_t sparse_counts(const uint32_t *cnt, int n_groups, int T, uint32_t *cou
 
 hipError_t fill_u32(uint32_t *p, int n, uint32_t v, hipStream_t st) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, n, v);
+  return hipGetLastError();
+}
+
+namespace {
+
+template <bool TILED, int SDT, bool XL>
+hipError_t rows_subset_launch(const RowsMatrix &w, const void *x, bool x_bf16,
+                              const uint32_t *rows, int n, float *y, int grid, size_t lds,
+                              float *xg, hipStream_t st) {
+  auto k = rows_subset_kernel<TILED, SDT, XL>;
+  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(k),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)lds) != hipSuccess)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, w, x, x_bf16 ? 1 : 0, rows, n, y, xg);
+  return hipGetLastError();
+}
+
+template <bool AXPY, bool TILED, int SDT, int C>
+hipError_t subset_launch(const SparseSubsetArgs &a, int T, hipStream_t st) {
+  const size_t lds = ((size_t)subset_x_floats(a.H, C) + a.H / 32) * 4;
+  auto k = sparse_subset_kernel<AXPY, TILED, SDT, C>;
+  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(k),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)lds) != hipSuccess)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3((unsigned)subset_groups(a.I, a.lanes), (unsigned)T), dim3(256), lds,
+                     st, a);
+  return hipGetLastError();
+}
+
+template <bool AXPY>
+hipError_t subset_dispatch(const SparseSubsetArgs &a, int T, hipStream_t st) {
+  const int c = a.H <= 2048 && a.up.K <= 2048 ? 1 : a.H <= 4096 && a.up.K <= 4096 ? 2 : 4;
+  const bool tiled = a.up.tiled != 0, f16 = a.up.sdt != 0;
+#define CAI4_SUBSET(CC)                                                            \
+  if (c == CC) {                                                                   \
+    if (tiled)                                                                     \
+      return f16 ? subset_launch<AXPY, true, SCALE_F16, CC>(a, T, st)              \
+                 : subset_launch<AXPY, true, SCALE_BF16, CC>(a, T, st);            \
+    return f16 ? subset_launch<AXPY, false, SCALE_F16, CC>(a, T, st)               \
+               : subset_launch<AXPY, false, SCALE_BF16, CC>(a, T, st);             \
+  }
+  CAI4_SUBSET(1)
+  CAI4_SUBSET(2)
+  CAI4_SUBSET(4)
+#undef CAI4_SUBSET
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t rows_subset(const RowsMatrix &w, const void *x, bool x_bf16, const uint32_t *rows,
+                       int n, float *y, size_t max_lds, int num_cus, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const size_t lds = ((size_t)(w.K / 32) * kXPad + (size_t)w.K / 32) * 4;
+  const bool xl = lds <= max_lds;
+  const size_t gbytes = ((size_t)w.K + (size_t)w.K / 32) * 4;  // x in global memory: unpadded
+  float *xg = nullptr;
+  if (!xl) {
+    // x too long for LDS: its f32 copy and chunk sums in global memory, freed
+    // once the stream has used them
+    if (hipMallocAsync(reinterpret_cast<void **>(&xg), gbytes, st) != hipSuccess)
+      return hipErrorOutOfMemory;
+    hipLaunchKernelGGL(stage_x_global_kernel, dim3((unsigned)((w.K + 8191) / 8192)), dim3(256), 0,
+                       st, x, x_bf16 ? 1 : 0, w.K, xg);
+    if (hipError_t e = hipGetLastError()) return e;
+  }
+  // 16 rows per workgroup per round, at most two rounds of workgroups per CU
+  int grid = (n + 15) / 16;
+  if (grid > 2 * num_cus) grid = 2 * num_cus;
+  hipError_t e;
+  const bool tiled = w.tiled != 0, f16 = w.sdt != 0;
+  const size_t l = xl ? lds : 0;
+  if (xl) {
+    e = tiled ? (f16 ? rows_subset_launch<true, SCALE_F16, true>(w, x, x_bf16, rows, n, y, grid, l, xg, st)
+                     : rows_subset_launch<true, SCALE_BF16, true>(w, x, x_bf16, rows, n, y, grid, l, xg, st))
+              : (f16 ? rows_subset_launch<false, SCALE_F16, true>(w, x, x_bf16, rows, n, y, grid, l, xg, st)
+                     : rows_subset_launch<false, SCALE_BF16, true>(w, x, x_bf16, rows, n, y, grid, l, xg, st));
+  } else {
+    e = tiled ? (f16 ? rows_subset_launch<true, SCALE_F16, false>(w, x, x_bf16, rows, n, y, grid, l, xg, st)
+                     : rows_subset_launch<true, SCALE_BF16, false>(w, x, x_bf16, rows, n, y, grid, l, xg, st))
+              : (f16 ? rows_subset_launch<false, SCALE_F16, false>(w, x, x_bf16, rows, n, y, grid, l, xg, st)
+                     : rows_subset_launch<false, SCALE_BF16, false>(w, x, x_bf16, rows, n, y, grid, l, xg, st));
+    const hipError_t f = hipFreeAsync(xg, st);
+    if (e == hipSuccess) e = f;
+  }
+  return e;
+}
+
+int subset_lanes(int I, int num_cus) {
+  const int ev = tuning_env("CASCADIA_INT4_SUBSET_LANES", 0);
+  if (ev == 64 || ev == 128) return ev;
+  return subset_groups(I, kSubsetGroup) < num_cus ? 64 : kSubsetGroup;
+}
+
+hipError_t sparse_subset_mask(const SparseSubsetArgs &a, int T, hipStream_t st) {
+  if (a.lanes != 64 && a.lanes != kSubsetGroup) return hipErrorInvalidValue;
+  return subset_dispatch<false>(a, T, st);
+}
+
+hipError_t sparse_subset_axpy(const SparseSubsetArgs &a, int n_tokens, float *out,
+                              uint32_t *counts, hipStream_t st) {
+  if (a.lanes != 64 && a.lanes != kSubsetGroup) return hipErrorInvalidValue;
+  if (hipError_t e = subset_dispatch<true>(a, n_tokens, st)) return e;
+  const int ng = subset_groups(a.I, a.lanes);
+  hipLaunchKernelGGL(sparse_axpy_reduce_kernel,
+                     dim3((unsigned)((a.H + 63) / 64), (unsigned)n_tokens), dim3(1024), 0, st,
+                     a.partial, ng, a.H, out, a.cnt, counts, a.t0);
+  return hipGetLastError();
+}
+
+hipError_t build_active_mask(const float *gate, int n, float tau, const float *thr, float *silu,
+                             uint32_t *active, uint32_t *n_active, hipStream_t st) {
+  hipLaunchKernelGGL(build_mask_kernel, dim3(1), dim3(1024), 0, st, gate, n, tau, thr, silu,
+                     active, n_active);
+  return hipGetLastError();
+}
+
+namespace {
+unsigned conv_grid(size_t n) {
+  const size_t g = (n + 255) / 256;
+  return (unsigned)(g > 4096 ? 4096 : g);
+}
+}  // namespace
+
+hipError_t f32_to_bf16_n(const float *x, uint16_t *out, size_t n, hipStream_t st) {
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(conv_grid(n)), dim3(256), 0, st, x, out, n);
+  return hipGetLastError();
+}
+
+hipError_t bf16_to_f32_n(const uint16_t *x, float *out, size_t n, hipStream_t st) {
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(conv_grid(n)), dim3(256), 0, st, x, out, n);
   return hipGetLastError();
 }
 

@@ -166,4 +166,47 @@ hipError_t debug_dequant(const uint8_t *packed, const uint8_t *scale_bits, int N
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// streaming read (the benchmark's HBM read ceiling)
+// ---------------------------------------------------------------------------
+
+// Each wave reads one contiguous 8 KB run (eight 1 KB wave loads, 16 bytes per
+// lane, non-temporal, all issued before any is used: the access pattern of the
+// decode GEMV's weight stream), XORs it, and each workgroup folds its eight
+// waves into sink[blockIdx.x % 1024] by an atomic XOR, so no load is dead.
+// Offsets past `bytes` read zeros (the buffer resource's range).
+__global__ void __launch_bounds__(512)
+    stream_read_kernel(const uint8_t *__restrict__ buf, size_t bytes, uint32_t *__restrict__ sink) {
+  __shared__ uint32_t s_x[8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const size_t base = ((size_t)blockIdx.x * 8 + wave) * 8192;
+  // one resource per 8 KB run (ranges up to 2 GiB; the run's bytes from base)
+  const size_t left = bytes > base ? bytes - base : 0;
+  const buf_rsrc_t r = buf_rsrc(buf + (left ? base : 0), left < 8192 ? left : 8192);
+  u32x4_t v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = buf_load16_nt(r, (uint32_t)(1024 * j + 16 * lane));
+  uint32_t x = 0u;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o, 64);
+  if (lane == 0) s_x[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t w = 0u;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w ^= s_x[k];
+    atomicXor(sink + (blockIdx.x & 1023u), w);
+  }
+}
+
+hipError_t stream_read(const void *buf, size_t bytes, uint32_t *sink, hipStream_t st) {
+  const size_t grid = (bytes + 65535) / 65536;  // 8 waves x 8 KB per workgroup
+  if (grid == 0 || grid > 0x7FFFFFFFu) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)grid), dim3(512), 0, st,
+                     static_cast<const uint8_t *>(buf), bytes, sink);
+  return hipGetLastError();
+}
+
 }  // namespace cai4

@@ -64,6 +64,12 @@ extern "C" {
  * scale bits, moved; results are bit-identical between the two. */
 #define CASCADIA_INT4_TILING_CRATE 0u
 #define CASCADIA_INT4_TILING_MFMA 1u
+/* Experts only (cascadia_int4_expert.tiling), for the activation-sparse
+ * entry points, which read up one row at a time for the active lanes only:
+ * gate and down MFMA-tiled, up in the crate layout (each row contiguous, so
+ * an inactive row costs no bytes).  The other expert entry points refuse it
+ * with CASCADIA_INT4_ERR_ARG. */
+#define CASCADIA_INT4_TILING_MFMA_UP_ROWS 2u
 
 /* Routing rules for the MoE entry point. */
 #define CASCADIA_INT4_ROUTE_IDS 0u          /* caller supplies ids/weights */
@@ -111,6 +117,42 @@ void cascadia_int4_reload_tuning(void);
 int cascadia_int4_dequant_gemv(const cascadia_int4_layout *layout, const uint8_t *packed,
                                const uint8_t *scale_bits, const float *x, float *y,
                                void *stream);
+
+/* y[r] for the rows r listed in active_rows[0 .. n_active) only: the same
+ * dot products as cascadia_int4_dequant_gemv, every other y left untouched
+ * (the caller zeroes it when it needs defined values there; a row listed
+ * twice is written twice with the same value).  Replaces
+ * dequant_gemv_int4_rows_subset (src/ffn_sparsity.rs:187-243) and
+ * dequant_gemv_int4_rows_subset_auto (:317-348).  Rows >= n_rows are skipped
+ * (the crate's debug_assert).  Only the listed rows' bytes are read; in the
+ * CRATE layout a row is contiguous, in the MFMA layout its bytes are spread
+ * over 16-byte pieces of its tile.  x: f32 [k_cols], 16-byte aligned;
+ * active_rows: u32 [n_active]; y: f32 [n_rows].  f32 arithmetic. */
+int cascadia_int4_dequant_gemv_rows_subset(const cascadia_int4_layout *layout,
+                                           const uint8_t *packed, const uint8_t *scale_bits,
+                                           const float *x, float *y,
+                                           const uint32_t *active_rows, uint32_t n_active,
+                                           void *stream);
+
+/* build_active_mask_mode (src/ffn_sparsity.rs:131-179; build_active_mask
+ * :106-108 when thresholds is NULL, build_active_mask_per_channel :115-125
+ * when it is not) on one row of n gate values: silu_out[i] = the stable SiLU
+ * g >= 0 ? g / (1 + e^-g) : g e^g / (1 + e^g); active_out[0 .. *n_active_out)
+ * = the lanes with |silu| >= cutoff * max|silu|, ascending (cutoff =
+ * threshold, or thresholds[i]), or every lane when max|silu| is 0 or the mode
+ * is dense (threshold <= 0 with thresholds NULL; no thresholds[i] > 0).
+ * Device pointers: gate_out, silu_out f32 [n]; thresholds f32 [n] or NULL;
+ * active_out u32 [n]; n_active_out u32 [1]. */
+int cascadia_int4_build_active_mask(const float *gate_out, uint32_t n, float threshold,
+                                    const float *thresholds, float *silu_out,
+                                    uint32_t *active_out, uint32_t *n_active_out,
+                                    void *stream);
+
+/* f32 -> bf16 bits, round to nearest even with NaN kept quiet
+ * (f32_to_bf16_bits, src/format.rs:151-160), and bf16 bits -> f32 exactly
+ * (bf16_bits_to_f32, :130-135), over n device values. */
+int cascadia_int4_f32_to_bf16(const float *x, size_t n, uint16_t *out_bf16, void *stream);
+int cascadia_int4_bf16_to_f32(const uint16_t *x_bf16, size_t n, float *out, void *stream);
 
 /* ys[t*n_rows + r] for t < seq, f32 activations xs [seq, k_cols].
  * Replaces dequant_gemm_int4_multi_auto (src/kernel_avx512_multi.rs:207-245)
@@ -243,9 +285,13 @@ int cascadia_int4_dequant_axpy_active(const uint8_t *packed_t, const uint8_t *sc
  * mask :131-179): gate in full, s = stable SiLU(gate), lanes with |s| >=
  * cutoff * max|s| active (cutoff = threshold, or thresholds[i] when
  * thresholds, device f32 [inter], is not NULL: SparsityMode::PerChannel), up
- * for the active rows only, intermediate s * up on them and 0 elsewhere, down
- * in full.  threshold <= 0 with thresholds NULL is the dense FFN
- * (cascadia_int4_ffn_forward_f32 / cascadia_int4_expert_forward_device).
+ * for the active rows only (the rows-subset GEMV: for hidden a multiple of 32
+ * up to 8192 only those rows' bytes are read; a wider hidden reads up in
+ * full), intermediate s * up on them and 0 elsewhere, down in full.
+ * threshold <= 0 with thresholds NULL is the dense FFN
+ * (cascadia_int4_ffn_forward_f32 / cascadia_int4_expert_forward_device), or,
+ * for an expert in CASCADIA_INT4_TILING_MFMA_UP_ROWS, every lane active on
+ * the sparse path.
  * Every token row is masked on its own; active_counts (device u32
  * [n_tokens], may be NULL) receives each row's active-lane count (the
  * crate's return value is count / inter).  _f32: x, out f32; _sparse: x, out
@@ -278,7 +324,13 @@ int cascadia_int4_expert_forward_sparse(uint32_t hidden, uint32_t inter, uint32_
  * dequant(down_t[r, :]) -- the down matrix in the transposed layout of
  * cascadia_int4_transpose_requantize_down, given in expert->down_packed /
  * down_scale (as the crate passes down_packed_t / down_scale_t_bits in the
- * down slots); gate/up in expert->tiling.  x, out: f32 [n_tokens, hidden]
+ * down slots); gate/up in expert->tiling (CRATE, MFMA, or MFMA_UP_ROWS:
+ * gate tiled, up in the crate layout).  For hidden a multiple of 32 up to
+ * 8192 the up rows and the transposed-down rows are read for the active lanes
+ * only (one fused kernel per 128 lanes after the gate GEMV); a wider hidden
+ * reads up in full.  The sum over the active lanes is added per 128-lane
+ * group and the groups in order (deterministic; the crate adds them in one
+ * ascending pass).  x, out: f32 [n_tokens, hidden]
  * (out fully overwritten); active_counts (device u32 [n_tokens], may be NULL)
  * receives each row's active-lane count (the crate returns count / inter).
  * workspace: >= cascadia_int4_ffn_sparse_axpy_workspace_bytes or NULL. */
@@ -445,6 +497,15 @@ int cascadia_int4_ov_gemv(const cascadia_int4_ov_segment *segs, uint32_t n_segs,
 int cascadia_int4_quantize_bf16(const uint16_t *w_bf16, uint32_t n_rows, uint32_t k_cols,
                                 uint32_t group_size, uint8_t *packed, uint16_t *scale_bits,
                                 void *stream);
+
+/* Streaming read of bytes at buf (16-byte aligned, a multiple of 16): each
+ * wave reads one contiguous 8 KB run with non-temporal 16-byte loads, the
+ * access pattern of the decode GEMV's weight stream, without its arithmetic.
+ * The XOR of every 32-bit word is folded into sink (device u32 [1024], zeroed
+ * by the caller): the XOR of the 1024 words is the XOR of the data.  No
+ * counterpart in the crate: the HBM read ceiling the benchmark reports beside
+ * the decode kernels' rates. */
+int cascadia_int4_stream_read(const void *buf, size_t bytes, uint32_t *sink, void *stream);
 
 /* Seeded synthetic data, the same generator as the test oracle.
  * kind 0: bytes (uniform nibbles), n = byte count, out u8.

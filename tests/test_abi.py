@@ -138,3 +138,37 @@ def test_python_mirror_rejects_host_tensors(cl):
     s = torch.zeros(64 * 2 * 2, dtype=torch.uint8)
     with pytest.raises(ValueError):
         cl.dequant_gemv_int4(p, s, torch.zeros(128), 64, 128, torch.zeros(64))
+
+
+def test_expert_weights_open_errors(cl, tmp_path):
+    """format.rs:63-72: a file shorter than one expert is GemmError::Truncated
+    (expected / actual), a missing one an I/O GemmError -- both raised on the
+    host before any device work."""
+    p = tmp_path / "short.bin"
+    p.write_bytes(b"\x88" * 100)
+    with pytest.raises(cl.GemmTruncated) as ei:
+        cl.ExpertWeights.open(str(p), hidden=512, inter=256, group_size=32)
+    assert ei.value.expected == cl.expert_bytes(512, 256, 32) and ei.value.actual == 100
+    with pytest.raises(cl.GemmError):
+        cl.ExpertWeights.open(str(tmp_path / "missing.bin"))
+    # the crate's own dims by default: K2.6's 7168 x 2048, G 32
+    with pytest.raises(cl.GemmTruncated) as ei:
+        cl.ExpertWeights.open(str(p))
+    assert ei.value.expected == cl.expert_bytes(cl.HIDDEN, cl.INTERMEDIATE, cl.GROUP_SIZE)
+
+
+def test_sparsity_mode_is_dense():
+    """SparsityMode::is_dense (ffn_sparsity.rs:85-90): Global(t) is dense for
+    t <= 0 only, so a NaN tau is sparse; a per-channel vector is dense when
+    empty or every entry is <= 0 (a NaN entry is not)."""
+    import torch
+
+    import cascadia_amd as cl
+
+    M = cl.SparsityMode
+    assert M.Global(0.0).is_dense() and M.Global(-1.0).is_dense()
+    assert not M.Global(float("nan")).is_dense() and not M.Global(0.1).is_dense()
+    assert M.PerChannel(torch.tensor([0.0, -1.0])).is_dense()
+    assert M.PerChannel(torch.empty(0)).is_dense()
+    assert not M.PerChannel(torch.tensor([0.0, float("nan")])).is_dense()
+    assert M.of(0.3).tau == 0.3 and M.of(torch.zeros(2)).thresholds is not None

@@ -241,9 +241,12 @@ def test_expert_forward_fixture_bins(cl, orc):
         assert_f32_close(host(o32).reshape(T, h), want32, os.path.basename(f) + " f32")
 
 
+@pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("M", [1, 4, 16])
-def test_expert_forward_config1_llama_ffn(cl, orc, M):
-    """Config 1: Llama-3-8B FFN, H 4096, I 14336, G128 fp16, bf16 x, M tokens."""
+def test_expert_forward_config1_llama_ffn(cl, orc, M, tiled):
+    """Config 1: Llama-3-8B FFN, H 4096, I 14336, G128 fp16, bf16 x, M tokens,
+    in the crate layout and MFMA-tiled (the layout the bench times: the
+    one-token GEMV at M = 1, the skinny kernel at 4 and 16)."""
     h, i, g = 4096, 14336, 128
     nbytes = orc.expert_bytes(h, i, g)
     flat = orc.fill_bytes(1, 21, nbytes)
@@ -252,11 +255,14 @@ def test_expert_forward_config1_llama_ffn(cl, orc, M):
         flat[offs[s]:offs[s] + sizes[s]] = orc.fill_scales(1, 30 + s, sizes[s] // 2, F16).view(np.uint8)
     xb = orc.fill_normal_bf16(M, 22, M * h)
     W = cl.ExpertWeights(dev(flat), h, i, g, F16)
+    if tiled:
+        W = W.tiled()
     out = torch.empty(M * h, dtype=torch.int16, device="cuda")
-    cl.expert_forward(dev(xb.view(np.int16).reshape(M, h)), *W.slices(), out, group_size=g, scale_dtype=F16)
+    cl.expert_forward(dev(xb.view(np.int16).reshape(M, h)), *W.slices(), out, group_size=g,
+                      scale_dtype=F16, tiling=cl.TILING_MFMA if tiled else cl.TILING_CRATE)
     got = host(out).view(np.uint16).reshape(M, h)
     want = orc.cpu_expert_forward(xb, M, flat, h, i, g, F16)
-    assert_bf16_close(got, want, f"config1 M={M}")
+    assert_bf16_close(got, want, f"config1 M={M} tiled={tiled}")
 
 
 FEW_SHAPES = [  # n, k, group, sdt, seq: 2..16 tokens over tiled weights, G % 128 == 0
@@ -536,3 +542,15 @@ def test_tiled_expert_bit_identical(cl, orc, M):
             assert_bf16_close(host(o1).view(np.uint16), host(o0).view(np.uint16), f"M=1 {h}x{i}")
         else:
             assert np.array_equal(host(o0), host(o1))
+
+
+@pytest.mark.parametrize("nbytes", [16, 8192, 3 * (1 << 20) + 48, 64 << 20])
+def test_stream_read_ceiling_kernel(cl, orc, nbytes):
+    """The benchmark's streaming-read kernel reads every byte: the XOR of its
+    1024 sink words equals the XOR of the buffer's 32-bit words (runs that end
+    inside an 8 KB wave run, a whole 64 MiB)."""
+    data = orc.fill_bytes(nbytes % 997, 3, nbytes)
+    sink = cl.stream_read(dev(data))
+    want = np.bitwise_xor.reduce(data.view(np.uint32))
+    got = np.bitwise_xor.reduce(host(sink).view(np.uint32))
+    assert got == want

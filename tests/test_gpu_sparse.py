@@ -67,23 +67,36 @@ def pick_x(orc, flat, h, i, g, sdt, tau, thr, seed):
     raise AssertionError("no seed keeps every lane away from the cutoff")
 
 
-CASES = [  # h, i, G, sdt, tiled
+CASES = [  # h, i, G, sdt, layout: False crate, True tiled, "rows" gate/down tiled + crate up
     (512, 256, 32, BF16, False),
     (7168, 2048, 32, BF16, True),   # the crate's HIDDEN / INTERMEDIATE
     (7168, 2048, 32, BF16, False),
+    (7168, 2048, 32, BF16, "rows"),
     (4096, 1024, 128, F16, True),
+    (4096, 1024, 128, F16, "rows"),
     (3072, 1536, 64, F16, False),
 ]
+
+
+def _til(cl, tiled):
+    return cl.TILING_MFMA_UP_ROWS if tiled == "rows" else cl.TILING_MFMA if tiled else cl.TILING_CRATE
+
+
+def layout(cl, W, tiled):
+    """(expert weights, tiling) for a test layout: False = the crate's, True =
+    MFMA-tiled, "rows" = TILING_MFMA_UP_ROWS (up kept in rows)."""
+    if tiled == "rows":
+        return W.tiled(up_rows=True), cl.TILING_MFMA_UP_ROWS
+    if tiled:
+        return W.tiled(), cl.TILING_MFMA
+    return W, cl.TILING_CRATE
 
 
 @pytest.mark.parametrize("h,i,g,sdt,tiled", CASES)
 @pytest.mark.parametrize("tau", [0.05, 0.3, 1.0])
 def test_expert_forward_sparse_global(cl, orc, h, i, g, sdt, tiled, tau):
     flat = make_expert(orc, h, i, g, sdt, h + i + g)
-    W = cl.ExpertWeights(dev(flat), h, i, g, sdt)
-    til = cl.TILING_MFMA if tiled else cl.TILING_CRATE
-    if tiled:
-        W = W.tiled()
+    W, til = layout(cl, cl.ExpertWeights(dev(flat), h, i, g, sdt), tiled)
     T = 3
     xb = np.stack([pick_x(orc, flat, h, i, g, sdt, tau, None, 100 * t + int(tau * 100))
                    for t in range(T)])
@@ -109,13 +122,10 @@ def test_expert_forward_sparse_global(cl, orc, h, i, g, sdt, tiled, tau):
         assert_f32_close(got32[t], want, f"f32 {h}x{i} tau {tau} token {t}")
 
 
-@pytest.mark.parametrize("h,i,g,sdt,tiled", [CASES[0], CASES[1], CASES[3]])
+@pytest.mark.parametrize("h,i,g,sdt,tiled", [CASES[0], CASES[1], CASES[3], CASES[4]])
 def test_sparse_per_channel(cl, orc, h, i, g, sdt, tiled):
     flat = make_expert(orc, h, i, g, sdt, 3 * h + i)
-    W = cl.ExpertWeights(dev(flat), h, i, g, sdt)
-    til = cl.TILING_MFMA if tiled else cl.TILING_CRATE
-    if tiled:
-        W = W.tiled()
+    W, til = layout(cl, cl.ExpertWeights(dev(flat), h, i, g, sdt), tiled)
     rng = np.random.default_rng(h + i)
     thr = rng.uniform(-0.1, 0.6, i).astype(np.float32)  # some lanes always on
     xb = pick_x(orc, flat, h, i, g, sdt, 0.0, thr, 7)
@@ -177,14 +187,18 @@ def _axpy_case(cl, orc, h, i, g, sdt, tiled, seed):
     W = cl.ExpertWeights(dev(flat), h, i, g, sdt)
     pt, st = cl.transpose_requantize_down(W.down_packed_bytes(), W.down_scale_bits(), h, i,
                                           group_size=g, scale_dtype=sdt)
-    Wt = W.tiled() if tiled else W
+    Wt, til = layout(cl, W, tiled)
     return flat, Wt, pt, st
 
 
 @pytest.mark.parametrize("tau", [0.0, 0.1, 0.3])
 @pytest.mark.parametrize("h,i,g,sdt,tiled", [(512, 256, 32, BF16, False),
                                              (7168, 2048, 32, BF16, True),
-                                             (4096, 14336, 128, F16, True)])
+                                             (7168, 2048, 32, BF16, "rows"),
+                                             (4096, 14336, 128, F16, True),
+                                             (4096, 14336, 128, F16, "rows"),
+                                             (3072, 1536, 128, F16, "rows"),
+                                             (9216, 512, 128, F16, True)])
 def test_axpy_ffn_matches_oracle(cl, orc, h, i, g, sdt, tiled, tau):
     """One token: output within rel-L2 1e-3 / max-abs 2e-2 of the oracle fed
     the same transposed down (bit-identical to the crate's for G 32 bf16; for
@@ -198,7 +212,7 @@ def test_axpy_ffn_matches_oracle(cl, orc, h, i, g, sdt, tiled, tau):
     frac = cl.ffn_forward_sparse_axpy_f32(dev(x), h, i, W.gate_packed_bytes(), W.gate_scale_bits(),
                                           W.up_packed_bytes(), W.up_scale_bits(), pt, st, out, tau,
                                           group_size=g, scale_dtype=sdt,
-                                          tiling=cl.TILING_MFMA if tiled else cl.TILING_CRATE)
+                                          tiling=_til(cl, tiled))
     want, wfrac = orc.ffn_forward_sparse_axpy_f32(x, flat, host(pt), host(st), h, i, g, sdt, tau)
     assert frac == wfrac, f"active fraction {frac} != {wfrac}"
     assert_f32_close(host(out), want, f"axpy ffn {h}x{i} G{g} tau={tau}")
@@ -263,3 +277,163 @@ def test_zero_token_rows(cl, orc):
         assert cl.ffn_forward_sparse_axpy_f32(xf, h, i, *W.slices()[:4], pt, st, of, 0.3,
                                               **kw) == []
     torch.cuda.synchronize()
+
+
+# ----------------------------------------------------------------------------
+# the rows-subset GEMV on its own (ffn_sparsity.rs:187-348)
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k,g,sdt,tiled", [(300, 4096, 128, F16, False), (300, 4096, 128, F16, True),
+                                             (130, 7168, 32, BF16, False), (64, 1024, 64, F16, True),
+                                             (40, 65536, 128, F16, False)])
+def test_rows_subset_gemv(cl, orc, n, k, g, sdt, tiled):
+    """Listed rows (ascending, shuffled, repeated, and ids past n_rows, which
+    are skipped) equal the oracle's GEMV rows within the GEMV bar; every other
+    entry of y keeps the caller's value (the crate touches only active rows,
+    ffn_sparsity.rs:184-186).  k = 65536 stages x through global memory (its
+    f32 copy exceeds the LDS)."""
+    rng = np.random.default_rng(n + k)
+    packed = orc.fill_bytes(n, k, n * k // 2)
+    scales = orc.fill_scales(n, k + 1, n * (k // g), sdt).view(np.uint8)
+    x = orc.fill_normal_f32(n, 7, k)
+    want = orc.gemv(packed, scales, x, n, k, g, sdt)
+    P, S = dev(packed), dev(scales)
+    if tiled:
+        P, S = cl.tile_weights(P, S, n, k, g)
+    rows = np.sort(rng.choice(n, size=n // 3, replace=False))
+    rows = np.concatenate([rows, rows[:5], [n, n + 7, 2 ** 31]]).astype(np.uint32)
+    rng.shuffle(rows)
+    y = torch.full((n,), 7.0, dtype=torch.float32, device="cuda")
+    cl.dequant_gemv_int4_rows_subset(P, S, dev(x), n, k, y, dev(rows.view(np.int32)), group_size=g,
+                                     scale_dtype=sdt,
+                                     tiling=cl.TILING_MFMA if tiled else cl.TILING_CRATE)
+    got = host(y)
+    on = np.zeros(n, bool)
+    on[rows[rows < n]] = True
+    assert np.all(got[~on] == 7.0), "rows outside the list were written"
+    assert_f32_close(got[on], want[on], f"rows subset {n}x{k} G{g} tiled={tiled}")
+    # an empty list reads nothing and writes nothing
+    cl.dequant_gemv_int4_rows_subset(P, S, dev(x), n, k, y, torch.empty(0, dtype=torch.int32,
+                                                                           device="cuda"),
+                                     group_size=g, scale_dtype=sdt,
+                                     tiling=cl.TILING_MFMA if tiled else cl.TILING_CRATE)
+    assert np.array_equal(host(y), got)
+
+
+# ----------------------------------------------------------------------------
+# the mask builders and the mode-taking entry points (ffn_sparsity.rs:71-179)
+# ----------------------------------------------------------------------------
+
+def test_build_active_mask_modes(cl, orc):
+    """silu within 4 ulps of the oracle's (the exp of two libms); the active
+    ids exactly those the crate's rule gives on the GPU's own silu values
+    (|silu| >= cutoff * max, ascending), and the oracle's ids wherever a lane
+    is not within 1e-5 of its cutoff; the dense cases (tau <= 0, every
+    per-channel threshold <= 0, an all-zero gate) list every lane, a NaN tau
+    none (is_dense is `t <= 0`), tau 1 the max lane alone."""
+    n = 3000
+    gate = (orc.fill_normal_f32(5, 5, n) * np.float32(3)).astype(np.float32)
+    rng = np.random.default_rng(2)
+    pc = rng.uniform(-0.2, 0.7, n).astype(np.float32)
+    cases = [("global 0.3", 0.3, None), ("global 0", 0.0, None), ("global -1", -1.0, None),
+             ("global nan", float("nan"), None), ("global 1", 1.0, None),
+             ("per-channel", 0.0, pc), ("per-channel <= 0", 0.0, -np.abs(pc))]
+    G = dev(gate)
+    for what, tau, thr in cases:
+        if thr is None:
+            silu, act = cl.build_active_mask(G, tau)
+        else:
+            silu, act = cl.build_active_mask_per_channel(G, dev(thr))
+        s = host(silu)
+        a = host(act).astype(np.int64)
+        ws, wa = orc.build_active_mask(gate, tau, thresholds=thr)
+        assert np.all(np.abs(s.astype(np.float64) - ws) <= 4 * np.spacing(np.abs(ws))), what
+        mx = np.max(np.abs(s))
+        dense = (thr is None and tau <= 0.0) or (thr is not None and np.all(thr <= 0.0))
+        cut = (thr if thr is not None else np.float32(tau)) * np.float32(mx)
+        mine = np.arange(n) if dense else np.nonzero(np.abs(s) >= cut)[0]
+        assert np.array_equal(a, mine), f"{what}: ids differ from the rule on the GPU's silu"
+        near = np.abs(np.abs(ws) - ((thr if thr is not None else tau) * np.max(np.abs(ws)))) \
+            <= 1e-5 * np.max(np.abs(ws))
+        far = ~near if not dense else np.ones(n, bool)
+        assert np.array_equal(np.isin(np.arange(n), a)[far], np.isin(np.arange(n), wa)[far]), what
+        if what == "global nan":
+            assert a.size == 0
+        if what == "global 1":
+            assert a.size == 1 and a[0] == int(np.argmax(np.abs(s)))
+    silu, act = cl.build_active_mask_mode(dev(np.zeros(17, np.float32)), cl.SparsityMode.Global(0.5))
+    assert host(act).size == 17 and not np.any(host(silu))  # max 0: every lane
+    with pytest.raises(ValueError):
+        cl.build_active_mask_per_channel(G, dev(pc[:-1]))
+
+
+def test_mode_entry_points_match_named_ones(cl, orc):
+    """expert_forward_sparse_mode / ffn_forward_sparse_f32_mode with
+    SparsityMode.Global / PerChannel (or a float / tensor) give the named
+    entry points' results bit for bit (ffn_sparsity.rs:756-815, 373-436)."""
+    h, i, g, sdt = 1024, 512, 64, F16
+    flat = make_expert(orc, h, i, g, sdt, 77)
+    W, til = layout(cl, cl.ExpertWeights(dev(flat), h, i, g, sdt), "rows")
+    kw = dict(group_size=g, scale_dtype=sdt, tiling=til)
+    xb = dev(orc.fill_normal_bf16(3, 3, 2 * h).view(np.int16))
+    xf = dev(orc.fill_normal_f32(3, 4, 2 * h))
+    thr = dev(np.random.default_rng(1).uniform(0.0, 0.5, i).astype(np.float32))
+    outs = []
+    for mode in (cl.SparsityMode.Global(0.2), 0.2):
+        o = torch.empty(2 * h, dtype=torch.int16, device="cuda")
+        outs.append((cl.expert_forward_sparse_mode(xb, *W.slices(), o, mode, **kw), host(o)))
+    o = torch.empty(2 * h, dtype=torch.int16, device="cuda")
+    ref = (cl.expert_forward_sparse(xb, *W.slices(), o, 0.2, **kw), host(o))
+    for f, v in outs:
+        assert f == ref[0] and np.array_equal(v, ref[1])
+    o1 = torch.empty(2 * h, dtype=torch.float32, device="cuda")
+    o2 = torch.empty(2 * h, dtype=torch.float32, device="cuda")
+    f1 = cl.ffn_forward_sparse_f32_mode(xf, h, i, *W.slices(), o1, cl.SparsityMode.PerChannel(thr),
+                                        **kw)
+    f2 = cl.ffn_forward_sparse_f32_per_channel(xf, h, i, *W.slices(), o2, thr, **kw)
+    assert f1 == f2 and torch.equal(o1, o2)
+
+
+def test_mixed_layout_only_on_sparse_entry_points(cl, orc):
+    """TILING_MFMA_UP_ROWS is an activation-sparse layout: the dense expert
+    entry points refuse it (ERR_ARG) rather than misread the up rows."""
+    h, i, g = 512, 256, 32
+    flat = make_expert(orc, h, i, g, BF16, 13)
+    W, til = layout(cl, cl.ExpertWeights(dev(flat), h, i, g, BF16), "rows")
+    xb = torch.zeros(h, dtype=torch.int16, device="cuda")
+    with pytest.raises(cl.CascadiaInt4Error) as ei:
+        cl.expert_forward(xb, *W.slices(), torch.empty_like(xb), group_size=g, tiling=til)
+    assert ei.value.rc == -2
+
+
+def test_bf16_conversions(cl, orc):
+    """f32_to_bf16_bits (format.rs:151-160) bit-identical to the oracle's,
+    which is pinned to half 2.7.1's from_f32, over random bit patterns and the
+    special values; bf16_bits_to_f32 exact on all 65,536 patterns."""
+    rng = np.random.default_rng(4)
+    bits = rng.integers(0, 2 ** 32, 1 << 16, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001,
+                        0xFFFFFFFF, 0x00000001, 0x3F808000, 0x3F818000, 0x7F7FFFFF],
+                       np.uint32)
+    x = np.concatenate([bits, special]).view(np.float32)
+    got = host(cl.f32_to_bf16_bits(dev(x))).view(np.uint16)
+    assert np.array_equal(got, orc.f32_to_bf16(x))
+    allb = np.arange(1 << 16, dtype=np.uint16)
+    back = host(cl.bf16_bits_to_f32(dev(allb.view(np.int16)))).view(np.uint32)
+    assert np.array_equal(back, allb.astype(np.uint32) << 16)
+    assert cl.f32_to_bf16_bits(1.0) == 0x3F80 and cl.bf16_bits_to_f32(0x4049) == 3.140625
+
+
+def test_expert_weights_open(cl, orc, tmp_path):
+    """ExpertWeights::open (format.rs:63-96): the file's bytes land in HBM
+    unchanged (bytes past one expert ignored) and run as that expert."""
+    h, i, g = 512, 256, 32
+    flat = make_expert(orc, h, i, g, BF16, 21)
+    p = tmp_path / "expert_000.bin"
+    p.write_bytes(bytes(flat) + b"\x00" * 100)
+    W = cl.ExpertWeights.open(str(p), hidden=h, inter=i, group_size=g)
+    assert np.array_equal(host(W.flat)[:flat.size], flat)
+    xb = orc.fill_normal_bf16(2, 2, h)
+    out = torch.empty(h, dtype=torch.int16, device="cuda")
+    cl.expert_forward(dev(xb.view(np.int16)), *W.slices(), out, group_size=g)
+    assert_bf16_close(host(out).view(np.uint16), orc.expert_forward(xb, flat, h, i, g, BF16), "open")
