@@ -321,8 +321,9 @@ __global__ void __launch_bounds__(64)
 // chunks l, l + 64, ...  Crate layout: chunk c is the row's bytes 16c ..
 // 16c + 15 (byte b = columns 2b | 2b + 1).  Tiled layout (layout.hip): part
 // c % 4 of the row's k-block c / 4, each dword's byte b holding columns b |
-// b + 4.  Per chunk a lane forms sum(n * x) over the nibble codes n and takes
-// the zero point off with the chunk's sum of x (q = n - 8); the chunk's scale
+// b + 4.  Per chunk a lane forms sum((128 + n) * x) over the nibble codes n
+// (nib128) and takes the offset off with the chunk's sum of x (q = n - 8, so
+// 136 x sum); the chunk's scale
 // multiplies that, the lane adds its chunks, and the wave adds its lanes:
 // f32 throughout (the crate's per-row sum in another order).
 
@@ -337,7 +338,18 @@ CAI4_DEV size_t rm_scale(const RowsMatrix &w, int r, int c) {
   return ((size_t)(r >> 4) * NG + g) * 16 + (r & 15);
 }
 
-// sum over the chunk's 32 columns of nibble * x, x the chunk's 32 values.
+// The f32 value 128 + n of byte k of a dword whose bytes hold nibble codes n
+// (0..15): one v_perm placing the byte under the exponent byte 0x43 (the
+// f32 128 is 0x43000000 and its unit in the last place 2^-16, so the byte at
+// bits 16..19 adds n exactly).
+template <int K>
+CAI4_DEV float nib128(uint32_t t) {
+  return bitsf(__builtin_amdgcn_perm(0x43000000u, t, 0x07000C0Cu | ((uint32_t)K << 16)));
+}
+
+// sum over the chunk's 32 columns of (128 + nibble) * x, x the chunk's 32
+// values; the caller removes the 136 = 128 + 8 offset with the chunk's sum
+// of x (q = n - 8).
 template <bool TILED>
 CAI4_DEV float chunk_nx(const u32x4_t v, const float *xc) {
   float s0 = 0.f, s1 = 0.f;
@@ -348,15 +360,16 @@ CAI4_DEV float chunk_nx(const u32x4_t v, const float *xc) {
     const f32x4_t xb = *reinterpret_cast<const f32x4_t *>(xc + 8 * d + 4);
     const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
     const uint32_t t = dw[d] & 0x0F0F0F0Fu, u = (dw[d] >> 4) & 0x0F0F0F0Fu;
+    const float a[4] = {nib128<0>(t), nib128<1>(t), nib128<2>(t), nib128<3>(t)};
+    const float b[4] = {nib128<0>(u), nib128<1>(u), nib128<2>(u), nib128<3>(u)};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float a = (float)((t >> (8 * k)) & 0xFFu), b = (float)((u >> (8 * k)) & 0xFFu);
       if (TILED) {  // byte k: columns k (low nibble) and k + 4 (high)
-        s0 = fmaf(a, xv[k], s0);
-        s1 = fmaf(b, xv[k + 4], s1);
+        s0 = fmaf(a[k], xv[k], s0);
+        s1 = fmaf(b[k], xv[k + 4], s1);
       } else {  // byte k: columns 2k and 2k + 1
-        s0 = fmaf(a, xv[2 * k], s0);
-        s1 = fmaf(b, xv[2 * k + 1], s1);
+        s0 = fmaf(a[k], xv[2 * k], s0);
+        s1 = fmaf(b[k], xv[2 * k + 1], s1);
       }
     }
   }
@@ -413,35 +426,48 @@ CAI4_DEV void stage_x(const void *x, int x_bf16, int K, float *xs, float *sxs) {
   }
 }
 
-// acc[u] += the dot products of rows r[u] (ok[u]) over this lane's chunk
-// slots j0 .. j0 + JB - 1 (chunk (j0 + j) * 64 + lane).  Every load of the
-// batch is issued before any is used, and unconditionally: a dead slot (row
-// not ok, chunk past K) reads a valid chunk (row r[u], the last chunk) whose
-// value is then not used -- a select between a load and a constant would make
-// the wave wait for each load in turn.  r[u] must be a valid row for every u.
-template <int RB, int JB, bool TILED, int SDT, int XS>
-CAI4_DEV void rows_dot(const RowsMatrix &w, const int (&r)[RB], const bool (&ok)[RB], int j0,
-                       int lane, const float *xs, const float *sxs, float (&acc)[RB]) {
-  const int nch = w.K >> 5;
+// One batch of rows-subset loads: row r[u]'s chunk (j0 + j) * 64 + lane and
+// its scale, for RB rows and JB chunk slots, issued unconditionally: a dead
+// slot (row not ok, chunk past K) reads a valid chunk (row r[u], the last
+// chunk) whose value rows_dot does not use -- a select between a load and a
+// constant would make the wave wait for each load in turn.  r[u] must be a
+// valid row for every u.
+template <int RB, int JB>
+struct RowsBatch {
   u32x4_t v[RB][JB];
   uint32_t sb[RB][JB];
+};
+// live: how many of the RB rows are in use, uniform over the wave (the rest
+// load nothing: a scalar branch skips them).
+template <int RB, int JB>
+CAI4_DEV void rows_load(const RowsMatrix &w, const int (&r)[RB], int j0, int lane,
+                        RowsBatch<RB, JB> &b, int live = RB) {
+  const int nch = w.K >> 5;
   const uint16_t *sc = reinterpret_cast<const uint16_t *>(w.scales);
 #pragma unroll
   for (int u = 0; u < RB; ++u)
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
+      if (u >= live) continue;
       const int c0 = (j0 + j) * 64 + lane, c = c0 < nch ? c0 : nch - 1;
-      v[u][j] = *reinterpret_cast<const u32x4_t *>(w.packed + rm_chunk(w, r[u], c));
-      sb[u][j] = (uint32_t)sc[rm_scale(w, r[u], c)];
+      b.v[u][j] = *reinterpret_cast<const u32x4_t *>(w.packed + rm_chunk(w, r[u], c));
+      b.sb[u][j] = (uint32_t)sc[rm_scale(w, r[u], c)];
     }
+}
+
+// acc[u] += the dot products of the batch's rows (ok[u]) over its chunks.
+template <int RB, int JB, bool TILED, int SDT, int XS>
+CAI4_DEV void rows_dot(const RowsMatrix &w, const RowsBatch<RB, JB> &b, const bool (&ok)[RB],
+                       int j0, int lane, const float *xs, const float *sxs, float (&acc)[RB]) {
+  const int nch = w.K >> 5;
 #pragma unroll
   for (int u = 0; u < RB; ++u)
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
       const int c = (j0 + j) * 64 + lane;
       if (ok[u] && c < nch) {
-        const float d = fmaf(-8.0f, sxs[c], chunk_nx<TILED>(v[u][j], xs + XS * c));
-        acc[u] = fmaf(scale_to_f32<SDT>(sb[u][j]), d, acc[u]);
+        const float d = fmaf(-136.0f, sxs[c], chunk_nx<TILED>(b.v[u][j], xs + XS * c));
+        acc[u] = fmaf(scale_to_f32<SDT>(b.sb[u][j]), d, acc[u]);
       }
     }
 }
@@ -477,8 +503,11 @@ __global__ void __launch_bounds__(256)
       r[u] = ok[u] ? (int)rr : 0;
       acc[u] = 0.f;
     }
-    for (int j0 = 0; j0 < jmax; j0 += JB)
-      rows_dot<RB, JB, TILED, SDT, XL ? kXPad : 32>(w, r, ok, j0, lane, xs, sxs, acc);
+    for (int j0 = 0; j0 < jmax; j0 += JB) {
+      RowsBatch<RB, JB> bt;
+      rows_load<RB, JB>(w, r, j0, lane, bt);
+      rows_dot<RB, JB, TILED, SDT, XL ? kXPad : 32>(w, bt, ok, j0, lane, xs, sxs, acc);
+    }
 #pragma unroll
     for (int u = 0; u < RB; ++u) {
       const float s = wave_sum(acc[u]);
@@ -499,10 +528,11 @@ __global__ void __launch_bounds__(256)
 }
 
 // f32 slots before the chunk sums in the fused kernels' LDS: the padded x,
-// which the AXPY's wave rows (2048 C values) reuse afterwards.
+// which the AXPY's padded wave rows (four waves x 64 C rows of kXPad) reuse
+// afterwards.
 __host__ __device__ inline int subset_x_floats(int H, int C) {
-  const int xf = (H / 32) * kXPad;
-  return xf > 2048 * C ? xf : 2048 * C;
+  const int xf = (H / 32) * kXPad, rf = 4 * 64 * C * kXPad;  // x, or four waves' rows
+  return xf > rf ? xf : rf;
 }
 
 // The fused sparse forms: workgroup (group g of kSubsetGroup lanes, token).
@@ -511,12 +541,14 @@ __host__ __device__ inline int subset_x_floats(int H, int C) {
 // ... RB at a time, reading their up rows (and, AXPY, their transposed-down
 // rows) in one round of loads.  C: chunk slots per lane (K and H <= 2048 C).
 // AXPY: lane l owns columns 32(l + 64 j) .. + 31 of the output (j < C):
-// combined = inter * scale, acc += combined * n, the -8 applied once per
-// chunk slot at the end (ffn_axpy.rs:118-134); the four waves' rows are added
-// in wave order (3, 2, 1, 0) into the group's partial row.
+// combined = inter * scale, acc += combined * (128 + n), the offset (-136 per
+// unit of combined) applied once per chunk slot at the end (the -8 of
+// ffn_axpy.rs:118-134, plus nib128's 128); the four waves' rows are added in
+// wave order (0, 1, 2, 3) into the group's partial row.  LDS (dynamic):
+// subset_x_floats + H / 32 floats, up to 148 KB (gfx950: 160 KB per CU).
 template <bool AXPY, bool TILED, int SDT, int C>
 __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) {
-  constexpr int RB = C <= 2 ? 4 : 2;
+  constexpr int RB = C <= 2 ? 8 : 4;
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // read as f32x4
   __shared__ float s_red[4];
   __shared__ uint32_t s_flag[4], s_wn[2];
@@ -525,8 +557,8 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x, tl = blockIdx.y, t = a.t0 + tl;
   const int H = a.H;
-  // [max(H / 32 * kXPad, 2048 C)] f32: x (padded chunks), then the AXPY's
-  // wave rows; then [H / 32] chunk sums
+  // [subset_x_floats] f32: x (padded chunks), then the AXPY's wave rows;
+  // then [H / 32] chunk sums
   float *xs = s_dyn;
   float *sxs = s_dyn + subset_x_floats(H, C);
   // the token's slots: every thread folds its share (loads issued first)
@@ -601,53 +633,67 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
       for (int k = 0; k < 32; ++k) acc[j][k] = 0.0f;
     }
   }
-  for (int f0 = wave; f0 < (int)n; f0 += 4 * RB) {
+  // the list length and the wave index as scalars: rows past the list are
+  // skipped by scalar branches, not loaded
+  const int ns = __builtin_amdgcn_readfirstlane((int)n);
+  const int ws = __builtin_amdgcn_readfirstlane(wave);
+  for (int f0 = ws; f0 < ns; f0 += 4 * RB) {
     int r[RB];
     bool ok[RB];
     float up[RB];
+    const int live = (ns - f0 + 3) / 4 < RB ? (ns - f0 + 3) / 4 : RB;
 #pragma unroll
     for (int u = 0; u < RB; ++u) {
       const int fe = f0 + 4 * u;
-      ok[u] = fe < (int)n;
+      ok[u] = u < live;
       r[u] = (int)s_id[ok[u] ? fe : f0];
       up[u] = 0.0f;
     }
-    // the transposed down's rows of the batch, issued with the up rows
+    // the up rows, then the transposed down's rows of the batch: one round
+    // of loads (unconditional, from valid addresses, as rows_load's).  The
+    // scheduling barrier keeps every load ahead of the arithmetic; waiting
+    // for the up rows then leaves the down rows in flight.
+    RowsBatch<RB, C> ub;
+    rows_load<RB, C>(a.up, r, 0, lane, ub, live);
     u32x4_t dq[AXPY ? RB : 1][AXPY ? C : 1];
     uint32_t ds[AXPY ? RB : 1][AXPY ? C : 1];
-    if (AXPY) {  // unconditional, from valid addresses (see rows_dot)
+    if (AXPY) {
 #pragma unroll
       for (int u = 0; u < RB; ++u)
 #pragma unroll
         for (int j = 0; j < C; ++j) {
+          if (u >= live) continue;
           const int c0 = j * 64 + lane, c = c0 < nhc ? c0 : nhc - 1;
           dq[u][j] = *reinterpret_cast<const u32x4_t *>(a.dt + (size_t)r[u] * (H / 2) + 16 * c);
           ds[u][j] = (uint32_t)a.dt_s[(size_t)r[u] * nhc + c];
         }
     }
-    rows_dot<RB, C, TILED, SDT, kXPad>(a.up, r, ok, 0, lane, xs, sxs, up);
+    __builtin_amdgcn_sched_barrier(0);
+    rows_dot<RB, C, TILED, SDT, kXPad>(a.up, ub, ok, 0, lane, xs, sxs, up);
 #pragma unroll
     for (int u = 0; u < RB; ++u) {
+      if (u >= live) continue;
       const int fe = f0 + 4 * u;
       // inter[r] = silu_gate[r] * up[r] (ffn_sparsity.rs:527, 711-716)
-      const float v = ok[u] ? s_val[fe] * wave_sum(up[u]) : 0.0f;
+      const float v = s_val[fe] * wave_sum(up[u]);
       if (!AXPY) {
-        if (lane == 0 && ok[u]) a.inter[(size_t)t * a.I + r[u]] = v;
+        if (lane == 0) a.inter[(size_t)t * a.I + r[u]] = v;
       } else {
 #pragma unroll
         for (int j = 0; j < C; ++j) {
-          // a dead slot adds nothing (v is 0 for a row past the list)
+          // a chunk slot past the row adds nothing
           const float comb = j * 64 + lane < nhc ? v * bf16_to_f32(ds[u][j]) : 0.0f;
           const uint32_t dw[4] = {dq[u][j].x, dq[u][j].y, dq[u][j].z, dq[u][j].w};
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
             const uint32_t lo = dw[d] & 0x0F0F0F0Fu, hi = (dw[d] >> 4) & 0x0F0F0F0Fu;
+            // byte k of dword d: columns 8d + 2k (low nibble), 8d + 2k + 1
+            const float a4[4] = {nib128<0>(lo), nib128<1>(lo), nib128<2>(lo), nib128<3>(lo)};
+            const float b4[4] = {nib128<0>(hi), nib128<1>(hi), nib128<2>(hi), nib128<3>(hi)};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {  // byte k of dword d: columns 8d + 2k, 8d + 2k + 1
-              acc[j][8 * d + 2 * k] =
-                  fmaf(comb, (float)((lo >> (8 * k)) & 0xFFu), acc[j][8 * d + 2 * k]);
-              acc[j][8 * d + 2 * k + 1] =
-                  fmaf(comb, (float)((hi >> (8 * k)) & 0xFFu), acc[j][8 * d + 2 * k + 1]);
+            for (int k = 0; k < 4; ++k) {
+              acc[j][8 * d + 2 * k] = fmaf(comb, a4[k], acc[j][8 * d + 2 * k]);
+              acc[j][8 * d + 2 * k + 1] = fmaf(comb, b4[k], acc[j][8 * d + 2 * k + 1]);
             }
           }
           csum[j] += comb;
@@ -659,31 +705,41 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
 #pragma unroll
   for (int j = 0; j < C; ++j)
 #pragma unroll
-    for (int k = 0; k < 32; ++k) acc[j][k] = fmaf(-8.0f, csum[j], acc[j][k]);
-  // waves 3, 2, 1 hand their rows down through LDS (x is no longer read)
+    for (int k = 0; k < 32; ++k) acc[j][k] = fmaf(-136.0f, csum[j], acc[j][k]);
+  // every wave stores its rows in an LDS region of its own (x is no longer
+  // read; rows kXPad floats apart, as x's chunks, so the lanes' 16-byte
+  // stores fall in different banks); after one barrier each thread adds the
+  // four waves' values of 32 C / 4 columns in wave order and stores them
   __syncthreads();
-  for (int w = 3; w >= 0; --w) {
-    if (wave == w) {
+  {
+    float *mine = xs + (size_t)wave * (64 * C * kXPad);
 #pragma unroll
-      for (int j = 0; j < C; ++j) {
-        float *row = xs + (size_t)(j * 64 + lane) * 32;
+    for (int j = 0; j < C; ++j) {
+      float *row = mine + (size_t)(j * 64 + lane) * kXPad;
 #pragma unroll
-        for (int k4 = 0; k4 < 8; ++k4) {
-          f32x4_t v = {acc[j][4 * k4], acc[j][4 * k4 + 1], acc[j][4 * k4 + 2], acc[j][4 * k4 + 3]};
-          if (w < 3) {
-            const f32x4_t p = *reinterpret_cast<const f32x4_t *>(row + 4 * k4);
-            v = f32x4_t{v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w};
-          }
-          if (w > 0) {
-            *reinterpret_cast<f32x4_t *>(row + 4 * k4) = v;
-          } else if (32 * (j * 64 + lane) < H) {
-            float *prow = a.partial + ((size_t)tl * gridDim.x + g) * H + 32 * (j * 64 + lane);
-            *reinterpret_cast<f32x4_t *>(prow + 4 * k4) = v;
-          }
+      for (int k4 = 0; k4 < 8; ++k4)
+        *reinterpret_cast<f32x4_t *>(row + 4 * k4) =
+            f32x4_t{acc[j][4 * k4], acc[j][4 * k4 + 1], acc[j][4 * k4 + 2], acc[j][4 * k4 + 3]};
+    }
+  }
+  __syncthreads();
+  {
+    constexpr int PER = 32 * C / 4;  // columns per thread: 64 C rows of 32 over 256 threads
+    const int q = (tid * PER) / 32, k0 = (tid * PER) % 32;  // row, first column in it
+    float *prow = a.partial + ((size_t)tl * gridDim.x + g) * H + 32 * q + k0;
+    if (32 * q < H) {
+#pragma unroll
+      for (int k4 = 0; k4 < PER / 4; ++k4) {
+        f32x4_t v = *reinterpret_cast<const f32x4_t *>(xs + (size_t)q * kXPad + k0 + 4 * k4);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+          const f32x4_t p = *reinterpret_cast<const f32x4_t *>(
+              xs + (size_t)w * (64 * C * kXPad) + (size_t)q * kXPad + k0 + 4 * k4);
+          v = f32x4_t{v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w};
         }
+        *reinterpret_cast<f32x4_t *>(prow + 4 * k4) = v;
       }
     }
-    __syncthreads();
   }
 }
 
@@ -817,10 +873,6 @@ hipError_t rows_subset_launch(const RowsMatrix &w, const void *x, bool x_bf16,
                               const uint32_t *rows, int n, float *y, int grid, size_t lds,
                               float *xg, hipStream_t st) {
   auto k = rows_subset_kernel<TILED, SDT, XL>;
-  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(k),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)lds) != hipSuccess)
-    return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, w, x, x_bf16 ? 1 : 0, rows, n, y, xg);
   return hipGetLastError();
 }
@@ -829,10 +881,6 @@ template <bool AXPY, bool TILED, int SDT, int C>
 hipError_t subset_launch(const SparseSubsetArgs &a, int T, hipStream_t st) {
   const size_t lds = ((size_t)subset_x_floats(a.H, C) + a.H / 32) * 4;
   auto k = sparse_subset_kernel<AXPY, TILED, SDT, C>;
-  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void *>(k),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)lds) != hipSuccess)
-    return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3((unsigned)subset_groups(a.I, a.lanes), (unsigned)T), dim3(256), lds,
                      st, a);
   return hipGetLastError();
