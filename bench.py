@@ -48,6 +48,9 @@ MALL_BYTES = 256 << 20
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "config1_gate_up_traffic.json")
+# counter-measured HBM bytes / algorithmic bytes of the other decode workloads
+# (rocprofv3 FETCH_SIZE + WRITE_SIZE passes over the bench's profile modes)
+TRAFFIC_ALL = os.path.join(ROOT, "profiles", "traffic.json")
 PREFILL_SHAPES = [(512, 4096), (512, 14336), (2048, 4096), (2048, 14336)]
 CPU_SAMPLE_S = 2.0  # CPU seconds per secondary baseline
 
@@ -787,6 +790,14 @@ def all_configs(cl, torch, sdt, copies, cpu):
             50 if T < 64 else (20 if T == 64 else 5), zipf=1.1, nsets=16 if T == 1024 else 64,
             cpu=cpu, cpu_tokens=4)
     ex.update(f_rows(cl, torch, sdt, copies))
+    try:
+        with open(TRAFFIC_ALL) as f:
+            tr = json.load(f)
+        for key, e in ex.items():
+            if key in tr and isinstance(e, dict):
+                e["traffic_ratio"] = tr[key]["ratio"]  # HBM bytes / algorithmic, counters
+    except (OSError, ValueError, KeyError):
+        pass
     return ex
 
 
