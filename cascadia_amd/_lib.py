@@ -125,6 +125,10 @@ SIGNATURES = {
     "cascadia_int4_source_set_cache_limits": (_i32, [_vp, _u64, _u64]),
     "cascadia_int4_source_cache_stats": (_i32, [_vp, C.POINTER(_u64), C.POINTER(_u64),
                                                 C.POINTER(_u64)]),
+    "cascadia_int4_prefetch": (_i32, [_vp, _u32, _u32]),
+    "cascadia_int4_prefetch_wait": (_i32, [_vp]),
+    "cascadia_int4_prefetch_stats": (_i32, [_vp, C.POINTER(_u64), C.POINTER(_u64),
+                                            C.POINTER(_u64), C.POINTER(_u64)]),
 }
 
 _lib = None

@@ -977,6 +977,24 @@ class ExpertSource:
             self._h, C.byref(a), C.byref(b), C.byref(c)))
         return a.value, b.value, c.value
 
+    def prefetch(self, layer: int, expert: int) -> None:
+        """Queue an expert for the handle's background loader (the runner's
+        Prefetcher, runner.rs:282-360): never blocks, drops the request when
+        4096 are queued."""
+        check("cascadia_int4_prefetch", lib().cascadia_int4_prefetch(self._h, layer, expert))
+
+    def prefetch_wait(self) -> None:
+        """Wait until every queued prefetch has been handled."""
+        check("cascadia_int4_prefetch_wait", lib().cascadia_int4_prefetch_wait(self._h))
+
+    def prefetch_stats(self):
+        """(submitted, dropped, processed, loaded into HBM) -- the runner's
+        submits / drops / processed counters (runner.rs:341-350) plus loads."""
+        v = [C.c_uint64() for _ in range(4)]
+        check("cascadia_int4_prefetch_stats", lib().cascadia_int4_prefetch_stats(
+            self._h, *(C.byref(x) for x in v)))
+        return tuple(x.value for x in v)
+
     def close(self) -> None:
         if self._h:
             lib().cascadia_int4_destroy_source(self._h)

@@ -48,7 +48,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <condition_variable>
+#include <deque>
 #include <list>
+#include <set>
+#include <thread>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -328,6 +332,16 @@ struct CascadiaInt4Source {
   void *ws = nullptr;
   size_t io_elems = 0, ws_bytes = 0;
   std::mutex mu;
+  // experts a prefetch is loading (guarded by mu); loaders wait on loaded_cv
+  std::set<ExpertKey> inflight;
+  std::condition_variable loaded_cv;
+  // the prefetcher (runner.rs:282-360): a bounded queue, its thread, counters
+  std::mutex qmu;
+  std::condition_variable qcv;
+  std::deque<ExpertKey> queue;
+  std::thread worker;
+  bool stop = false, busy = false;
+  uint64_t submits = 0, drops = 0, processed = 0, loaded = 0;
 };
 
 namespace {
@@ -423,11 +437,23 @@ bool malloc_evicting(CascadiaInt4Source *s, void **p, size_t bytes) {
   }
 }
 
-// The six sections of expert (L, E) from the safetensors shards into the
-// pinned host buffer *host (allocated here): 0, or -2.
-int read_safetensors_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, void **host,
-                            uint32_t *hidden_o, uint32_t *inter_o, uint32_t *group_o,
-                            uint32_t *sdt_o) {
+// Where one expert's six sections are (flat-blob order, format.rs:35-47) and
+// its dims.  Resolving it may open shards, so it is made under the handle's
+// lock; the reads it describes need no lock (shard descriptors stay open
+// until the handle is destroyed).
+struct ExpertPlan {
+  uint32_t hidden = 0, inter = 0, group = 0, sdt = 0;
+  int fd[6] = {-1, -1, -1, -1, -1, -1};
+  size_t off[6] = {0, 0, 0, 0, 0, 0}, len[6] = {0, 0, 0, 0, 0, 0};
+  int own_fd = -1;  // int4_bin: the expert file, opened for this plan
+  ~ExpertPlan() {
+    if (own_fd >= 0) close(own_fd);
+  }
+};
+
+// Expert (L, E) of a safetensors directory: 0, or -2.
+int plan_safetensors_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert,
+                            ExpertPlan *p) {
   const std::string base = "language_model.model.layers." + std::to_string(layer) +
                            ".mlp.experts." + std::to_string(expert) + ".";
   static const char *kNames[6] = {"gate_proj.weight_packed", "gate_proj.weight_scale",
@@ -453,104 +479,203 @@ int read_safetensors_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expe
   for (int i = 0; i < 6; ++i)
     if (t[i]->bytes != want[i]) return -2;
   if (group % 32 || inter % group || inter > (1 << 30) || hidden > (1 << 30)) return -2;
-  const size_t flat = pin * 2 + sin * 2 + pdn + sdn;
-  if (hipHostMalloc(host, flat, hipHostMallocDefault) != hipSuccess) return -3;
-  size_t off = 0;
-  for (int i = 0; i < 6; ++i) {  // flat-blob order (format.rs:35-47)
-    if (!pread_all(sh[i]->fd, static_cast<uint8_t *>(*host) + off, want[i], t[i]->offset)) {
-      (void)hipHostFree(*host);
-      *host = nullptr;
-      return -2;
-    }
-    off += want[i];
+  for (int i = 0; i < 6; ++i) {
+    p->fd[i] = sh[i]->fd;
+    p->off[i] = t[i]->offset;
+    p->len[i] = want[i];
   }
-  *hidden_o = (uint32_t)hidden;
-  *inter_o = (uint32_t)inter;
-  *group_o = (uint32_t)group;
-  *sdt_o = t[1]->dtype == "F16" ? CASCADIA_INT4_SCALE_F16 : CASCADIA_INT4_SCALE_BF16;
+  p->hidden = (uint32_t)hidden;
+  p->inter = (uint32_t)inter;
+  p->group = (uint32_t)group;
+  p->sdt = t[1]->dtype == "F16" ? CASCADIA_INT4_SCALE_F16 : CASCADIA_INT4_SCALE_BF16;
   return 0;
 }
 
 // experts/layer_LL/expert_EEE.bin (manifest.rs:137-142): the flat blob of
 // format.rs:35-47 at the manifest's dims, G 32, bf16 scales: 0, or -2.
-int read_bin_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, void **host,
-                    uint32_t *hidden_o, uint32_t *inter_o, uint32_t *group_o, uint32_t *sdt_o) {
+int plan_bin_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, ExpertPlan *p) {
   char name[64];
   snprintf(name, sizeof name, "/experts/layer_%02u/expert_%03u.bin", layer, expert);
   const int fd = open((s->dir + name).c_str(), O_RDONLY);
   if (fd < 0) return -2;
+  p->own_fd = fd;
   const size_t flat = cascadia_int4_expert_bytes(s->bin_hidden, s->bin_inter, 32);
   struct stat stt;
-  int rc = 0;
-  if (fstat(fd, &stt) != 0 || (size_t)stt.st_size != flat) rc = -2;
-  if (!rc && hipHostMalloc(host, flat, hipHostMallocDefault) != hipSuccess) rc = -3;
-  if (!rc && !pread_all(fd, *host, flat, 0)) {
-    (void)hipHostFree(*host);
-    *host = nullptr;
-    rc = -2;
-  }
-  close(fd);
-  if (rc) return rc;
-  *hidden_o = s->bin_hidden;
-  *inter_o = s->bin_inter;
-  *group_o = 32;
-  *sdt_o = CASCADIA_INT4_SCALE_BF16;
+  if (!flat || fstat(fd, &stt) != 0 || (size_t)stt.st_size != flat) return -2;
+  p->fd[0] = fd;
+  p->off[0] = 0;
+  p->len[0] = flat;  // one read of the whole blob
+  p->hidden = s->bin_hidden;
+  p->inter = s->bin_inter;
+  p->group = 32;
+  p->sdt = CASCADIA_INT4_SCALE_BF16;
   return 0;
 }
 
+int plan_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, ExpertPlan *p) {
+  return s->int4_bin ? plan_bin_expert(s, layer, expert, p)
+                     : plan_safetensors_expert(s, layer, expert, p);
+}
+
+// The planned sections into a pinned host buffer *host (allocated here, in
+// the flat-blob order): 0, -2 (a short read), -3 (no pinned memory).
+int read_plan(const ExpertPlan &p, void **host) {
+  size_t flat = 0;
+  for (int i = 0; i < 6; ++i) flat += p.len[i];
+  if (hipHostMalloc(host, flat, hipHostMallocDefault) != hipSuccess) {
+    *host = nullptr;
+    return -3;
+  }
+  size_t off = 0;
+  for (int i = 0; i < 6; ++i) {
+    if (!p.len[i]) continue;
+    if (!pread_all(p.fd[i], static_cast<uint8_t *>(*host) + off, p.len[i], p.off[i])) {
+      (void)hipHostFree(*host);
+      *host = nullptr;
+      return -2;
+    }
+    off += p.len[i];
+  }
+  return 0;
+}
+
+// Upload the flat blob at `host` to dflat, tile it into dtiled on `st` and
+// wait: 0, -2, -3.  dflat / dtiled are the caller's.
+int upload_expert(const ExpertPlan &p, const void *host, void *dflat, void *dtiled,
+                  cascadia_int4_expert *tiled_out, hipStream_t st) {
+  const size_t flat = cascadia_int4_expert_bytes(p.hidden, p.inter, p.group);
+  cascadia_int4_expert src{};
+  if (hipMemcpyAsync(dflat, host, flat, hipMemcpyHostToDevice, st) != hipSuccess) return -3;
+  if (cascadia_int4_expert_from_flat(static_cast<uint8_t *>(dflat), p.hidden, p.inter, p.group,
+                                     &src) != 0)
+    return -2;
+  if (cascadia_int4_tile_expert(p.hidden, p.inter, p.group, &src, static_cast<uint8_t *>(dtiled),
+                                tiled_out, st) != 0)
+    return -3;
+  return hipStreamSynchronize(st) == hipSuccess ? 0 : -3;
+}
+
+// Make an uploaded expert resident, most recently used first.
+DeviceExpert *insert_expert(CascadiaInt4Source *s, const ExpertKey &key, const ExpertPlan &p,
+                            void *dtiled, const cascadia_int4_expert &e) {
+  DeviceExpert de;
+  de.blob = dtiled;
+  de.bytes = cascadia_int4_expert_tiled_bytes(p.hidden, p.inter, p.group);
+  de.e = e;
+  de.hidden = p.hidden;
+  de.inter = p.inter;
+  de.group = p.group;
+  de.sdt = p.sdt;
+  s->lru.emplace_front(key, de);
+  s->experts[key] = s->lru.begin();
+  s->resident_bytes += de.bytes;
+  return &s->lru.front().second;
+}
+
 // 0, -2 (the expert's data missing or inconsistent), -3 (HIP failure or no
-// room in HBM even with every other expert evicted)
-int load_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, DeviceExpert **out) {
+// room in HBM even with every other expert evicted).  The caller holds lk on
+// the handle's lock; an expert a prefetch is loading is waited for, not read
+// a second time.
+int load_expert(CascadiaInt4Source *s, uint32_t layer, uint32_t expert, DeviceExpert **out,
+                std::unique_lock<std::mutex> &lk) {
   const ExpertKey key = std::make_pair(layer, expert);
+  s->loaded_cv.wait(lk, [&] { return s->inflight.count(key) == 0; });
   auto it = s->experts.find(key);
   if (it != s->experts.end()) {
     s->lru.splice(s->lru.begin(), s->lru, it->second);  // most recently used
     *out = &it->second->second;
     return 0;
   }
+  ExpertPlan p;
+  int rc = plan_expert(s, layer, expert, &p);
   void *host = nullptr;
-  uint32_t hidden = 0, inter = 0, group = 0, sdt = 0;
-  int rc = s->int4_bin ? read_bin_expert(s, layer, expert, &host, &hidden, &inter, &group, &sdt)
-                       : read_safetensors_expert(s, layer, expert, &host, &hidden, &inter, &group,
-                                                 &sdt);
+  if (!rc) rc = read_plan(p, &host);
   if (rc) return rc;
-  const size_t flat = cascadia_int4_expert_bytes(hidden, inter, group);
-  const size_t tiled = cascadia_int4_expert_tiled_bytes(hidden, inter, group);
+  const size_t flat = cascadia_int4_expert_bytes(p.hidden, p.inter, p.group);
+  const size_t tiled = cascadia_int4_expert_tiled_bytes(p.hidden, p.inter, p.group);
   if (!flat || !tiled) {
     (void)hipHostFree(host);
     return -2;
   }
   make_room(s, tiled);
   void *dflat = nullptr, *dtiled = nullptr;
-  DeviceExpert de;
-  cascadia_int4_expert src{};
+  cascadia_int4_expert e{};
   if (!malloc_evicting(s, &dtiled, tiled) || !malloc_evicting(s, &dflat, flat)) rc = -3;
-  if (!rc && hipMemcpyAsync(dflat, host, flat, hipMemcpyHostToDevice, s->stream) != hipSuccess)
-    rc = -3;
-  if (!rc && cascadia_int4_expert_from_flat(static_cast<uint8_t *>(dflat), hidden, inter, group,
-                                            &src) != 0)
-    rc = -2;
-  if (!rc && cascadia_int4_tile_expert(hidden, inter, group, &src, static_cast<uint8_t *>(dtiled),
-                                       &de.e, s->stream) != 0)
-    rc = -3;
-  if (!rc && hipStreamSynchronize(s->stream) != hipSuccess) rc = -3;
+  if (!rc) rc = upload_expert(p, host, dflat, dtiled, &e, s->stream);
   (void)hipHostFree(host);
   if (dflat) (void)hipFree(dflat);
   if (rc) {
     if (dtiled) (void)hipFree(dtiled);
     return rc;
   }
-  de.blob = dtiled;
-  de.bytes = tiled;
-  de.hidden = hidden;
-  de.inter = inter;
-  de.group = group;
-  de.sdt = sdt;
-  s->lru.emplace_front(key, de);
-  s->experts[key] = s->lru.begin();
-  s->resident_bytes += tiled;
-  *out = &s->lru.front().second;
+  *out = insert_expert(s, key, p, dtiled, e);
   return 0;
+}
+
+// One prefetch request on the prefetcher's thread: the disk read and the
+// upload run without the handle's lock (foreground calls go on meanwhile;
+// one for this expert waits for it), the allocation and the insertion with
+// it.  Errors are dropped: the expert then loads on first use, as a miss.
+// True when the expert was loaded.
+bool prefetch_one(CascadiaInt4Source *s, const ExpertKey &key, hipStream_t ps) {
+  ExpertPlan p;
+  {
+    std::lock_guard<std::mutex> lk(s->mu);
+    if (s->experts.count(key) || s->inflight.count(key)) return false;  // resident or loading
+    if (plan_expert(s, key.first, key.second, &p) != 0) return false;
+    s->inflight.insert(key);
+  }
+  void *host = nullptr, *dflat = nullptr, *dtiled = nullptr;
+  cascadia_int4_expert e{};
+  int rc = read_plan(p, &host);
+  const size_t flat = cascadia_int4_expert_bytes(p.hidden, p.inter, p.group);
+  const size_t tiled = cascadia_int4_expert_tiled_bytes(p.hidden, p.inter, p.group);
+  if (!rc && (!flat || !tiled)) rc = -2;
+  if (!rc) {
+    std::lock_guard<std::mutex> lk(s->mu);
+    make_room(s, tiled);
+    if (!malloc_evicting(s, &dtiled, tiled) || !malloc_evicting(s, &dflat, flat)) rc = -3;
+  }
+  if (!rc) rc = upload_expert(p, host, dflat, dtiled, &e, ps);
+  if (host) (void)hipHostFree(host);
+  if (dflat) (void)hipFree(dflat);
+  std::lock_guard<std::mutex> lk(s->mu);
+  if (rc) {
+    if (dtiled) (void)hipFree(dtiled);
+  } else {
+    make_room(s, tiled);  // limits may have been reached while it loaded
+    insert_expert(s, key, p, dtiled, e);
+  }
+  s->inflight.erase(key);
+  s->loaded_cv.notify_all();
+  return rc == 0;
+}
+
+// The prefetcher's thread: requests in queue order until the handle stops.
+void prefetch_loop(CascadiaInt4Source *s) {
+  const bool dev_ok = hipSetDevice(s->device) == hipSuccess;
+  hipStream_t ps = nullptr;
+  const bool ok = dev_ok && hipStreamCreateWithFlags(&ps, hipStreamNonBlocking) == hipSuccess;
+  for (;;) {
+    ExpertKey key;
+    {
+      std::unique_lock<std::mutex> q(s->qmu);
+      s->qcv.wait(q, [&] { return s->stop || !s->queue.empty(); });
+      if (s->stop) break;
+      key = s->queue.front();
+      s->queue.pop_front();
+      s->busy = true;
+    }
+    const bool loaded = ok && prefetch_one(s, key, ps);
+    {
+      std::lock_guard<std::mutex> q(s->qmu);
+      ++s->processed;
+      if (loaded) ++s->loaded;
+      s->busy = false;
+    }
+    s->qcv.notify_all();
+  }
+  if (ps) (void)hipStreamDestroy(ps);
 }
 
 // Make the handle's device current for the call; restore the caller's after.
@@ -617,6 +742,13 @@ int cascadia_int4_open_source(const char *model_dir, CascadiaInt4Source **out_ha
 
 void cascadia_int4_destroy_source(CascadiaInt4Source *handle) {
   if (!handle) return;
+  {  // stop the prefetcher: queued requests are dropped, a load in progress finishes
+    std::lock_guard<std::mutex> q(handle->qmu);
+    handle->stop = true;
+    handle->queue.clear();
+  }
+  handle->qcv.notify_all();
+  if (handle->worker.joinable()) handle->worker.join();
   {
     DeviceScope ds(handle->device);
     if (handle->stream) (void)hipStreamSynchronize(handle->stream);
@@ -631,21 +763,64 @@ void cascadia_int4_destroy_source(CascadiaInt4Source *handle) {
 
 int cascadia_int4_prewarm(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert) {
   if (!handle) return -1;
-  std::lock_guard<std::mutex> lk(handle->mu);
+  std::unique_lock<std::mutex> lk(handle->mu);
   DeviceScope ds(handle->device);
   if (!ds.ok) return -3;
   DeviceExpert *de = nullptr;
-  return load_expert(handle, layer, expert, &de);
+  return load_expert(handle, layer, expert, &de, lk);
+}
+
+int cascadia_int4_prefetch(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert) {
+  if (!handle) return -1;
+  constexpr size_t kQueue = 4096;  // the runner's sync_channel bound (runner.rs:296-300)
+  {
+    std::lock_guard<std::mutex> q(handle->qmu);
+    if (handle->stop) return 0;
+    if (!handle->worker.joinable()) {
+      try {
+        handle->worker = std::thread(prefetch_loop, handle);
+      } catch (...) {
+        ++handle->drops;  // no thread: the request is dropped, as on overflow
+        return 0;
+      }
+    }
+    if (handle->queue.size() >= kQueue) {
+      ++handle->drops;
+      return 0;
+    }
+    handle->queue.emplace_back(layer, expert);
+    ++handle->submits;
+  }
+  handle->qcv.notify_all();
+  return 0;
+}
+
+int cascadia_int4_prefetch_wait(CascadiaInt4Source *handle) {
+  if (!handle) return -1;
+  std::unique_lock<std::mutex> q(handle->qmu);
+  handle->qcv.wait(q, [&] { return handle->stop || (handle->queue.empty() && !handle->busy); });
+  return 0;
+}
+
+int cascadia_int4_prefetch_stats(CascadiaInt4Source *handle, uint64_t *submits, uint64_t *drops,
+                                 uint64_t *processed, uint64_t *loaded) {
+  if (!handle) return -1;
+  std::lock_guard<std::mutex> q(handle->qmu);
+  if (submits) *submits = handle->submits;
+  if (drops) *drops = handle->drops;
+  if (processed) *processed = handle->processed;
+  if (loaded) *loaded = handle->loaded;
+  return 0;
 }
 
 int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert,
                                  const float *x_f32, float *out_f32) {
   if (!handle || !x_f32 || !out_f32) return -1;
-  std::lock_guard<std::mutex> lk(handle->mu);
+  std::unique_lock<std::mutex> lk(handle->mu);
   DeviceScope ds(handle->device);
   if (!ds.ok) return -3;
   DeviceExpert *de = nullptr;
-  if (int rc = load_expert(handle, layer, expert, &de)) return rc;
+  if (int rc = load_expert(handle, layer, expert, &de, lk)) return rc;
   const uint32_t h = de->hidden;
   const size_t need_ws = cascadia_int4_ffn_workspace_bytes(h, de->inter, de->group, 1);
   if (handle->io_elems < h) {
@@ -666,7 +841,7 @@ int cascadia_int4_expert_forward(CascadiaInt4Source *handle, uint32_t layer, uin
     handle->ws_bytes = need_ws;
   }
   // the expert may have been evicted to make room for the buffers: reload
-  if (int rc = load_expert(handle, layer, expert, &de)) return rc;
+  if (int rc = load_expert(handle, layer, expert, &de, lk)) return rc;
   std::vector<uint16_t> xb(h), ob(h);
   for (uint32_t i = 0; i < h; ++i) xb[i] = f32_to_bf16_host(x_f32[i]);  // c_ffi.rs:323
   if (hipMemcpyAsync(handle->x_dev, xb.data(), (size_t)h * 2, hipMemcpyHostToDevice,

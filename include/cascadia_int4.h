@@ -449,6 +449,28 @@ int cascadia_int4_source_set_cache_limits(CascadiaInt4Source *handle, uint64_t m
 int cascadia_int4_source_cache_stats(CascadiaInt4Source *handle, uint64_t *cached,
                                      uint64_t *evictions, uint64_t *resident_bytes);
 
+/* Expert prefetch: the runner's Prefetcher (runner.rs:282-360) over
+ * prefetch_expert (safetensors_source.rs:308-330), which asks the OS to page
+ * an expert in ahead of use.  Here the page-in goes all the way to HBM:
+ * cascadia_int4_prefetch queues (layer, expert) for a background thread of
+ * the handle (started by the first call) that reads the expert into pinned
+ * host memory, uploads and tiles it on a stream of its own and adds it to the
+ * expert cache (the LRU limits apply), so that a later prewarm or
+ * expert_forward finds it resident.  The call never blocks: with 4096
+ * requests queued it drops the request (the runner's try_submit); an expert
+ * already resident or being loaded is skipped, and one that cannot be read is
+ * left to load (and report its error) on first use.  prewarm / expert_forward
+ * of an expert the thread is loading wait for that load rather than read it a
+ * second time.  cascadia_int4_prefetch_wait returns once the queue is empty
+ * and no load is in progress.  cascadia_int4_prefetch_stats: requests
+ * queued, dropped, taken off the queue, and loaded into HBM by the thread.
+ * destroy_source drops the queued requests and joins the thread.  Codes: 0,
+ * -1 null handle. */
+int cascadia_int4_prefetch(CascadiaInt4Source *handle, uint32_t layer, uint32_t expert);
+int cascadia_int4_prefetch_wait(CascadiaInt4Source *handle);
+int cascadia_int4_prefetch_stats(CascadiaInt4Source *handle, uint64_t *submits, uint64_t *drops,
+                                 uint64_t *processed, uint64_t *loaded);
+
 /* ---- the OpenVINO CascadiaInt4Gemv format (crates/cascadia-ov-genai-shim/
  *      cpp/gemv_offload.cpp) ---- */
 

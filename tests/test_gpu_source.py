@@ -263,3 +263,63 @@ def test_corrupt_shard_headers(orc, tmp_path):
         src.prewarm(0, 0)
     assert ei.value.rc == -2
     src.close()
+
+
+@pytest.mark.gpu
+def test_expert_prefetch(orc, tmp_path):
+    """The prefetcher (runner.rs:282-360): queued experts become resident in
+    HBM without a foreground call, counted as loaded; a later expert_forward
+    gives the same result as a cold load; an expert already resident is
+    skipped, a missing one is processed but not loaded (its error comes on
+    first use); a forward issued while its expert is being prefetched waits
+    for that load; the LRU limits still apply; close() with requests queued
+    returns."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import cascadia_amd as cl
+
+    h, i, g = 1024, 512, 32
+    keys = [(0, e) for e in range(6)]
+    data = {k: (h, i, g, BF16, make_expert(orc, h, i, g, BF16, 70 + k[1])) for k in keys}
+    write_model(str(tmp_path), data)
+    x = orc.fill_normal_f32(6, 6, h)
+
+    def run(src, k):
+        out = np.empty(h, np.float32)
+        src.expert_forward(*k, x, out)
+        return out
+
+    cold = cl.ExpertSource(str(tmp_path))
+    want = {k: run(cold, k) for k in keys}
+    cold.close()
+
+    src = cl.ExpertSource(str(tmp_path))
+    for k in keys[:4]:
+        src.prefetch(*k)
+    src.prefetch(0, 99)  # not in the directory
+    src.prefetch_wait()
+    sub, drop, proc, loaded = src.prefetch_stats()
+    assert (sub, drop, proc, loaded) == (5, 0, 5, 4)
+    assert src.cache_stats()[0] == 4
+    for k in keys[:4]:
+        assert np.array_equal(run(src, k), want[k]), f"prefetched expert {k}"
+    assert src.prefetch_stats()[3] == 4 and src.cache_stats()[0] == 4  # no reload
+    src.prefetch(*keys[0])  # resident: skipped
+    src.prefetch_wait()
+    assert src.prefetch_stats()[2:] == (6, 4)
+    with pytest.raises(cl.CascadiaInt4Error) as ei:
+        src.prewarm(0, 99)
+    assert ei.value.rc == -2
+    # a forward right behind its prefetch: waits for that load or loads it itself
+    src.prefetch(*keys[4])
+    assert np.array_equal(run(src, keys[4]), want[keys[4]])
+    src.prefetch_wait()
+    # limits: two experts at most, prefetches evict like loads do
+    src.set_cache_limits(max_experts=2)
+    src.prefetch(*keys[5])
+    src.prefetch_wait()
+    assert src.cache_stats()[0] == 2
+    assert np.array_equal(run(src, keys[5]), want[keys[5]])
+    for k in keys:
+        src.prefetch(*k)
+    src.close()  # queued requests dropped, the thread joined
