@@ -297,6 +297,39 @@ def hbm_ceiling(cl, torch):
         out[name] = round(bufs[0].numel() * bufs[0].element_size() / (ev / steps) / 1e9, 1)
     del a, small
     torch.cuda.empty_cache()
+    out["read_us_by_bytes"] = read_floor(cl, torch, sink)
+    return out
+
+
+# The byte counts the decode entries are set against: a 64 KiB read (the
+# floor of one launch in a graph replay), config 0's GEMV, config 1's down and
+# its fused gate/up.
+READ_FLOOR_BYTES = {"64KiB": 64 << 10, "config0": 4096 * 4096 // 2 + 4096 * 32 * 2,
+                    "config1_down": 4096 * 14336 // 2 + 4096 * 112 * 2,
+                    "config1_gate_up": 2 * (14336 * 4096 // 2 + 14336 * 32 * 2)}
+
+
+def read_floor(cl, torch, sink):
+    """Microseconds per launch of the streaming-read kernel over each size of
+    READ_FLOOR_BYTES (graph replays, buffers rotating past twice the Infinity
+    Cache): what a plain read of a workload's weight bytes costs on this box,
+    launch and first-byte latency included."""
+    out = {}
+    for name, nbytes in READ_FLOOR_BYTES.items():
+        nb = (nbytes + 8191) // 8192 * 8192
+        nbuf = max(2, min(64, math.ceil(2 * MALL_BYTES / nb) + 1))
+        bufs = [cl.fill_bytes(torch.empty(nb, dtype=torch.uint8, device="cuda"), 9, j)
+                for j in range(nbuf)]
+
+        def rd(r, bufs=bufs):
+            cl.stream_read(bufs[r % len(bufs)], sink)
+        for r in range(nbuf):
+            rd(r)
+        steps = 1000 if nb < (32 << 20) else 300
+        _, ev = graph_time(torch, rd, steps)
+        out[name] = round(ev / steps * 1e6, 3)
+        del bufs
+    torch.cuda.empty_cache()
     return out
 
 
@@ -831,6 +864,14 @@ def summary(line):
     c = ex.get("hbm_ceiling")
     if c:
         out["read_ceiling_GBps"] = c.get("read_60MiB_GBps")
+        rf = c.get("read_us_by_bytes")
+        if rf:
+            # time of a plain read of the same bytes / the workload's time
+            out["vs_same_bytes_read"] = {
+                "c0": round(rf["config0"] / out["c0"][0], 3) if "c0" in out else None,
+                "c1_M1_chain": round((rf["config1_gate_up"] + rf["config1_down"]) /
+                                     out["c1_M1"][0], 3),
+                "floor_64KiB_us": rf["64KiB"]}
     return out
 
 

@@ -454,12 +454,25 @@ CAI4_DEV void gemv_body(const GvParams &a) {
     if (r16 >= a.N) return;
     float h = a.residual ? a.residual[r16] : 0.f;
     if (a.shared) h = h + a.shared[r16];
-    float moe = 0.f;
-    for (int kk = 0; kk < a.top_k; ++kk) {
-      if (a.pos[kk] < 0) continue;
-      float y = 0.f;
-      for (int v = 0; v < a.kw; ++v) y += red[(kk * a.kw + v) * 16 + lr];
-      moe = moe + a.wts[kk] * bf16_to_f32(f32_to_bf16_rne(y));
+    // the top_k * kw <= 16 partials (slot-major, wave order within a slot),
+    // every LDS read issued before the first add: a read per add waited for
+    // each in turn (16 dependent LDS round trips at the workgroup's tail)
+    const int n = a.top_k * a.kw;
+    float pv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pv[i] = red[min(i, n - 1) * 16 + lr];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(pv[i]));  // issued here, not per add
+    float moe = 0.f, y = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i >= n) break;  // uniform
+      y += pv[i];
+      if ((i + 1) % a.kw == 0) {  // slot i / kw complete
+        const int kk = i / a.kw;
+        if (a.pos[kk] >= 0) moe = moe + a.wts[kk] * bf16_to_f32(f32_to_bf16_rne(y));
+        y = 0.f;
+      }
     }
     // the whole combine, or the weighted expert sum only (residual and shared
     // added later, in the same order)
@@ -474,9 +487,29 @@ CAI4_DEV void gemv_body(const GvParams &a) {
   }
   __syncthreads();
   if (wave > 0) return;
-  for (int w = 1; w < a.kw; ++w) {
+  // added in wave order, the LDS reads of eight partials issued before their
+  // adds (clamped indices: always inside the kw - 1 partials): a read per add
+  // waited for each in turn, ~0.5 us at the tail of a 16-wave workgroup
+  for (int w0 = 1; w0 < a.kw; w0 += 8) {
+    float v[8][NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[nt] += red[((w - 1) * NT + nt) * 16 + lr];
+    for (int q = 0; q < 8; ++q) {
+      const int w = min(w0 + q, a.kw - 1);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) v[q][nt] = red[((w - 1) * NT + nt) * 16 + lr];
+    }
+    // pin every read here (the compiler would otherwise sink each into the
+    // branch of its add, one LDS round trip apiece)
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(v[q][nt]));
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (w0 + q >= a.kw) break;  // uniform
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[nt] += v[q][nt];
+    }
   }
   if (lg != 0) return;  // D row 0 = the token: lanes 0-15, component 0
   const int r16 = 16 * T + lr;

@@ -357,7 +357,17 @@ __global__ __launch_bounds__(256) void pf_reduce_kernel(const float *part, void 
   const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;  // n is a multiple of 4
   f32x4_t s = *reinterpret_cast<const f32x4_t *>(part + i);
-  for (int z = 1; z < ksplit; ++z) s += *reinterpret_cast<const f32x4_t *>(part + z * n + i);
+  // ksplit <= 4: the other slices' loads all issued (clamped to the last
+  // slice) before the adds, which go in slice order
+  f32x4_t v[3];
+#pragma unroll
+  for (int z = 1; z < 4; ++z)
+    v[z - 1] = *reinterpret_cast<const f32x4_t *>(part + (size_t)min(z, ksplit - 1) * n + i);
+#pragma unroll
+  for (int z = 1; z < 4; ++z) asm volatile("" : "+v"(v[z - 1]));
+#pragma unroll
+  for (int z = 1; z < 4; ++z)
+    if (z < ksplit) s += v[z - 1];
   if (out_f32) {
     *reinterpret_cast<f32x4_t *>(reinterpret_cast<float *>(y) + i) = s;
   } else {

@@ -561,12 +561,35 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
     }
     __syncthreads();
     if (kwi > 0) return;
-    for (int w = 1; w < a.kw; ++w) {
+    // in wave order, the LDS reads of GR spans issued before their adds
+    // (clamped: always inside the kw - 1 spans written) and pinned there; a
+    // read per add waited for each in turn
+    constexpr int GR = MT * NT >= 8 ? 1 : 8 / (MT * NT);
+    for (int w0 = 1; w0 < a.kw; w0 += GR) {
+      f32x4_t v[GR][MT][NT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int q = 0; q < GR; ++q) {
+        const int w = min(w0 + q, a.kw - 1);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          acc[mt][nt] += red[((size_t)((w - 1) * a.rw + rwi) * NI + mt * NT + nt) * 64 + lane];
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            v[q][mt][nt] = red[((size_t)((w - 1) * a.rw + rwi) * NI + mt * NT + nt) * 64 + lane];
+      }
+#pragma unroll
+      for (int q = 0; q < GR; ++q)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(v[q][mt][nt]));
+#pragma unroll
+      for (int q = 0; q < GR; ++q) {
+        if (w0 + q >= a.kw) break;  // uniform
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[mt][nt] += v[q][mt][nt];
+      }
     }
   }
   if (mcount <= 0) return;
@@ -613,9 +636,12 @@ __global__ __launch_bounds__(1024) void splitk_reduce_kernel(KParams a, int kspl
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        v[j][nt] = z0 + j < ksplit ? a.part[(size_t)(z0 + j) * zstride + base + nt * 64]
-                                   : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int nt = 0; nt < NT; ++nt)  // clamped: every load in range, all four in flight
+        v[j][nt] = a.part[(size_t)min(z0 + j, ksplit - 1) * zstride + base + nt * 64];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(v[j][nt]));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (z0 + j < ksplit) {
