@@ -57,12 +57,13 @@ def make_experts(orc, E, h, i, g, sdt, seed):
     return blob, stride
 
 
-def make_shared(orc, h, i, g, sdt, seed):
+def make_shared(orc, h, i, g, sdt, seed, sigma=0.02, offset=1e-3):
     per = orc.expert_bytes(h, i, g)
     b = orc.fill_bytes(seed, 900, per)
     offs, sizes = orc.expert_offsets(h, i, g)
     for s in (1, 3, 5):
-        b[offs[s]:offs[s] + sizes[s]] = orc.fill_scales(seed, 910 + s, sizes[s] // 2, sdt).view(np.uint8)
+        b[offs[s]:offs[s] + sizes[s]] = orc.fill_scales(seed, 910 + s, sizes[s] // 2, sdt, sigma,
+                                                        offset).view(np.uint8)
     return b
 
 
