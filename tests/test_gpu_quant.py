@@ -91,3 +91,38 @@ def test_quantize_rejects_bad_shapes(cl):
         cl.quantize_int4_group(w, 8, 96, 64)  # k_cols not a multiple of the group
     with pytest.raises(ValueError):
         cl.quantize_int4_group(w, 8, 128, 32)  # length mismatch (kernel.rs-style assert)
+
+
+def test_quantised_expert_vs_fp32_swiglu(cl, orc):
+    """ov_moe.rs:888-920 on the device: the crate's test expert (hidden 64,
+    inter 32, its hashed weights in [-0.1, 0.1)) quantised by the GPU
+    quantiser from bf16, then expert_forward on the GPU, within rel-L2 0.1 of
+    the fp32 SwiGLU of the unquantised weights -- the crate's bar (this case
+    measures 0.084 through the oracle); and equal to the oracle's expert on
+    the oracle's bytes at the parity bars."""
+    h, m, g = 64, 32, 32
+
+    def mk(n, seed):  # the crate test's generator (ov_moe.rs:888-920)
+        i = np.arange(n, dtype=np.uint64)
+        v = ((i * 2654435761 + seed) & 0xFFFFFFFF) % 1000
+        return ((v.astype(np.float32) / np.float32(1000) - np.float32(0.5)) *
+                np.float32(0.2)).astype(np.float32)
+
+    gate, up, down, x = mk(m * h, 1), mk(m * h, 2), mk(h * m, 3), mk(h, 4)
+    parts, want_flat = [], []
+    for w, n, k in ((gate, m, h), (up, m, h), (down, h, m)):
+        wb = orc.f32_to_bf16(w).reshape(-1)
+        p, s = cl.quantize_int4_group(dev(wb.view(np.int16)), n, k, g)
+        parts += [p, s]
+        op, os_ = orc.quantize_int4_group(wb, n, k, g)
+        want_flat += [op.view(np.uint8).reshape(-1), os_.view(np.uint8).reshape(-1)]
+    xb = orc.f32_to_bf16(x)
+    out = torch.empty(h, dtype=torch.int16, device="cuda")
+    cl.expert_forward(dev(xb.view(np.int16)), *parts, out, group_size=g, scale_dtype=cl.SCALE_BF16)
+    got = orc.bf16_to_f32(host(out).view(np.uint16))
+    G, U, D = (a.astype(np.float64) for a in (gate.reshape(m, h), up.reshape(m, h), down.reshape(h, m)))
+    gg, uu = G @ x, U @ x
+    fp32 = D @ ((gg / (1 + np.exp(-gg))) * uu)
+    assert rel_l2(got, fp32) < 0.1, f"int4 expert vs fp32 SwiGLU rel_l2={rel_l2(got, fp32):.3g}"
+    want = orc.bf16_to_f32(orc.expert_forward(xb, np.concatenate(want_flat), h, m, g, BF16))
+    assert rel_l2(got, want) <= REL_L2_TOL and max_abs(got, want) <= MAX_ABS_TOL
