@@ -1211,6 +1211,8 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       g.K = H;
       g.ldy = I;
       g.epi = cai4::GG_SWIGLU_HILO;
+      g.seeds_out = si;  // the hot rows' down seeds, from the planes as they are written
+      g.seeds_gw = cai4::gg_group_width(G);
       e = cai4::gg_grouped(g, m.ws.max_chunks, st);
     }
     if (e == hipSuccess) {
@@ -1230,9 +1232,6 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       a2.ldo = I;
       e = cai4::skinny_launch(a2, m.gu, cai4::A_GATHER, cai4::EPI_SWIGLU_HILO, st);
     }
-    if (e == hipSuccess)
-      e = cai4::gg_prep(1, hi, lo, nullptr, nullptr, nullptr, si, (int)n, m.rows_pad, I, G, counts,
-                        st);
     if (e == hipSuccess) {
       cai4::GgArgs dn = a;
       dn.w0 = L->experts + off[4];

@@ -343,6 +343,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
 
   // epilogue: D lane l holds column l % 16 and rows 4 (l / 16) + v
   constexpr int NOUT = SW ? NT / 2 : NT;
+  // SwiGLU: this lane's sum of hi + lo over its NOUT columns, per row
+  float rsum[SW ? MS : 1][4];
+#pragma unroll
+  for (int i = 0; i < (SW ? MS : 1); ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) rsum[i][v] = 0.f;
 #pragma unroll
   for (int i = 0; i < MS; ++i) {
 #pragma unroll
@@ -358,14 +364,64 @@ __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
         if constexpr (SW) {
           const float h = silu_f32(y) * acc[i][j + NT / 2][v];
           const uint32_t hb = fbits(h) >> 16;  // hi = h truncated, lo = RNE(h - hi)
+          const uint32_t lb = f32_to_bf16_rne(h - bitsf(hb << 16));
           reinterpret_cast<uint16_t *>(a.y)[o] = (uint16_t)hb;
-          reinterpret_cast<uint16_t *>(a.y2)[o] = (uint16_t)f32_to_bf16_rne(h - bitsf(hb << 16));
+          reinterpret_cast<uint16_t *>(a.y2)[o] = (uint16_t)lb;
+          rsum[SW ? i : 0][v] += bitsf(hb << 16) + bf16_to_f32(lb);
         } else if (a.part) {
           a.part[(size_t)blockIdx.z * a.M * a.N + (size_t)(row0 + m) * a.N + n] = y;
         } else if (a.epi == GG_F32) {
           reinterpret_cast<float *>(a.y)[o] = y;
         } else {
           reinterpret_cast<uint16_t *>(a.y)[o] = (uint16_t)f32_to_bf16_rne(y);
+        }
+      }
+    }
+  }
+  if constexpr (SW) {
+    // the seeds of the planes just written, for the GEMM that reads them as A
+    // (in place of a pass over them): per row, the 16 lanes of a DPP row add
+    // their columns; a group wider than one wave's 8 NT columns adds its
+    // waves' sums through LDS in wave order
+    if (a.seeds_out) {
+      const int per = a.seeds_gw / (8 * NT);  // waves (wn) per group: 1, 2 or 4
+      const int c0 = T0 * 16 + 16 * wn * (NT / 2);  // the wave's first output column
+      float t[MS][4];
+#pragma unroll
+      for (int i = 0; i < MS; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) t[i][v] = row16_sum(rsum[i][v]);
+      float *so = a.seeds_out + (size_t)(c0 / a.seeds_gw) * a.rows_pad + row0;
+      if (per == 1) {
+        if (lr == 0 && c0 < a.N) {
+#pragma unroll
+          for (int i = 0; i < MS; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int m = wm * P::RM + 16 * i + 4 * lg + v;
+              if (m < mrows) so[m] = -136.f * t[i][v];
+            }
+        }
+      } else {
+        __syncthreads();  // every wave is past its last read of the stages
+        float *part = reinterpret_cast<float *>(stages);  // [WN][BM]
+        if (lr == 0) {
+#pragma unroll
+          for (int i = 0; i < MS; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) part[wn * P::BM + wm * P::RM + 16 * i + 4 * lg + v] = t[i][v];
+        }
+        __syncthreads();
+        if (wn % per == 0 && lr == 0 && c0 < a.N) {
+#pragma unroll
+          for (int i = 0; i < MS; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int m = wm * P::RM + 16 * i + 4 * lg + v;
+              float sum = part[wn * P::BM + m];
+              for (int q = 1; q < per; ++q) sum += part[(wn + q) * P::BM + m];
+              if (m < mrows) so[m] = -136.f * sum;
+            }
         }
       }
     }
@@ -542,6 +598,7 @@ size_t gg_dense_workspace(int M, int N, int K, int G, int amode, int epi, int nu
 
 hipError_t gg_dense(GgArgs a, int amode, void *ws, int num_cus, hipStream_t st) {
   a.rows_pad = gg_rows_pad(a.M);
+  a.seeds_out = nullptr;  // (the dense FFN's down makes its own seeds)
   uint8_t *w = static_cast<uint8_t *>(ws);
   float *seeds = reinterpret_cast<float *>(w);
   a.seeds = seeds;
@@ -606,6 +663,9 @@ hipError_t gg_grouped(const GgArgs &a0, int max_tiles, hipStream_t st) {
   a.part = nullptr;
   if (max_tiles <= 0) return hipSuccess;
   const bool sw = a.epi == GG_SWIGLU_HILO;
+  // the epilogue's seeds: SwiGLU only, groups of one, two or four waves' 32 columns
+  if (a.seeds_out && (!sw || (a.seeds_gw != 32 && a.seeds_gw != 64 && a.seeds_gw != 128)))
+    return hipErrorInvalidValue;
   const unsigned gx = sw ? (a.N + 127) / 128 : (a.N + 255) / 256;
   if (a.hilo) {  // 64-row tiles: two per table entry
     a.tile_split = kGgChunkRows / 64;

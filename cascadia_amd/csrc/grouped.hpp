@@ -31,6 +31,11 @@ struct GgArgs {
   int epi;       // GgEpi
   float *part;   // dense split-K partials [ksplit][M][N] (f32), or null
   int kper;      // k-blocks per K slice (blockIdx.z)
+  // SwiGLU only, or null: the seeds of the hi / lo planes the epilogue writes,
+  // for a GEMM that takes them as A: [N / seeds_gw][rows_pad], -136 * the sum
+  // of hi + lo over each group of seeds_gw output columns (32, 64 or 128)
+  float *seeds_out;
+  int seeds_gw;
 };
 
 // Columns per seed group: min(G, 128).
