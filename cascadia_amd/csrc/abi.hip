@@ -945,8 +945,11 @@ MoePlan moe_plan(int dev, const cascadia_int4_moe_layer *L, uint32_t top_k, uint
     m.dn = cai4::skinny_plan_grouped(H, I, G, C2, maxc2, cai4::A_HILO, cai4::EPI_BF16, d);
     const size_t part =
         m.gu.partial_bytes > m.dn.partial_bytes ? m.gu.partial_bytes : m.dn.partial_bytes;
+    // the token rows as bf16 and their seeds (per token), the down's seeds
+    // (per grouped row)
     m.ws = cai4::moe_workspace((int)T, H, I, (int)L->n_experts, (int)top_k, C, part, sh, sh_ws,
-                               (size_t)n * H * 2, (size_t)(H / gw) * m.rows_pad * 4,
+                               (size_t)T * H * 2,
+                               (size_t)(H / gw) * cai4::gg_rows_pad((int)T) * 4,
                                (size_t)(I / gw) * m.rows_pad * 4, C2);
     return m;
   }
@@ -1160,9 +1163,10 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
   }
   hipError_t e = hipSuccess;
   if (m.tiles) {
-    // many tokens: route, group into 128-row chunks, gather the rows as bf16
+    // many tokens: route, group into 128-row chunks, the token rows as bf16
     // with their seeds, then the grouped MFMA-tile gate/up (SwiGLU -> hi / lo
-    // planes) and down (-> bf16 per (token, slot)) over all experts at once
+    // planes, reading its rows through the row map) and down (-> bf16 per
+    // (token, slot)) over all experts at once
     if (R->mode == CASCADIA_INT4_ROUTE_IDS) {
       e = hipMemcpyAsync(ids, R->ids, n * 4, hipMemcpyDeviceToDevice, st);
       if (e == hipSuccess) e = hipMemcpyAsync(wts, R->weights, n * 4, hipMemcpyDeviceToDevice, st);
@@ -1187,9 +1191,11 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
     uint16_t *xg = reinterpret_cast<uint16_t *>(W + m.ws.xg);
     float *sx = reinterpret_cast<float *>(W + m.ws.seeds_x);
     float *si = reinterpret_cast<float *>(W + m.ws.seeds_i);
-    if (e == hipSuccess)  // grouped row r <- bf16(x[row_map[r]]), the row count from the grouping
-      e = cai4::gg_prep(2, x, nullptr, row_map, xg, nullptr, sx, (int)n, m.rows_pad, H, G, counts,
-                        st);
+    // the token rows as bf16 with their seeds, once per token: the hot
+    // gate/up reads its rows through the row map (no copy per assignment)
+    const int Tp = cai4::gg_rows_pad((int)T);
+    if (e == hipSuccess)
+      e = cai4::gg_prep(2, x, nullptr, nullptr, xg, nullptr, sx, (int)T, Tp, H, G, nullptr, st);
     cai4::GgArgs a{};
     a.estride = L->expert_stride;
     a.tiles = chunks;
@@ -1205,6 +1211,9 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       g.s1 = L->experts + off[3];
       g.x = xg;
       g.seeds = sx;
+      g.rows_pad = Tp;
+      g.row_map = row_map;
+      g.x_rows = (int)T;
       g.y = hi;
       g.y2 = lo;
       g.N = I;
@@ -1213,6 +1222,7 @@ int moe_forward(const cascadia_int4_moe_layer *L, const cascadia_int4_routing *R
       g.epi = cai4::GG_SWIGLU_HILO;
       g.seeds_out = si;  // the hot rows' down seeds, from the planes as they are written
       g.seeds_gw = cai4::gg_group_width(G);
+      g.seeds_rp = m.rows_pad;
       e = cai4::gg_grouped(g, m.ws.max_chunks, st);
     }
     if (e == hipSuccess) {

@@ -98,10 +98,17 @@ struct Gg {
 
 // What a wave's loads of a k-block read: its rsrcs (the weight / scale ones
 // are the wave's own matrix in SwiGLU mode) and geometry.
+constexpr uint32_t kGgOOB = 0x80000000u;  // an offset past every range: no data moves
+
 struct GgLd {
   rsrc_t xr0, xr1, wr, sr, qr;
   int K, KB, NG, G, Rp, wave, lane, half;  // half: SwiGLU, the wave loads up tiles
   int mrows;  // live rows of the tile
+  // rows through a row map (GgArgs::row_map): each A load's byte offset at
+  // k-block 0 (its x row and chunk; kGgOOB for a row past the count) and the
+  // seed lane's (one x row and group per lane, 4 bytes)
+  int ind;
+  uint32_t aoff[4], soff;
 };
 
 template <class P, int GPK, bool SW>
@@ -114,7 +121,8 @@ CAI4_DEV void gg_load(int l, uint8_t *buf, const GgLd &d, int kb) {
     const int q = (lane & 15) ^ (row & 15);
     if (4 * rb < d.mrows)
       gg_dma<16>(P::PL > 1 && pl ? d.xr1 : d.xr0, lds_addr(buf + P::A + blk * 1024),
-                 (uint32_t)(row * d.K + kb * 128 + 8 * q) * 2);
+                 d.ind ? d.aoff[l < 4 ? l : 0] + (uint32_t)kb * 256
+                       : (uint32_t)(row * d.K + kb * 128 + 8 * q) * 2);
     else if (lane == 0)
       // a block of dead rows (past the tile's count, never stored): one 4-byte
       // load instead, so that every stage issues the same number of loads (the
@@ -135,6 +143,12 @@ CAI4_DEV void gg_load(int l, uint8_t *buf, const GgLd &d, int kb) {
     if (i < P::SLANES)
       gg_dma<4>(d.sr, lds_addr(buf + P::S + (d.wave * P::SLANES + (i & ~63)) * 4),
                 (uint32_t)((mt * d.NG + g0) * 32 + 4 * j));
+  } else if (d.ind) {
+    // seeds through the row map: one row of one group per lane
+    constexpr int XL4 = GPK * P::BM / P::W;
+    if (lane < XL4)
+      gg_dma<4>(d.qr, lds_addr(buf + P::X + d.wave * XL4 * 4),
+                d.soff + (uint32_t)(kb * GPK * d.Rp) * 4);
   } else {
     // seeds: 4 rows of one group per lane
     if (lane < P::XLANES) {
@@ -316,6 +330,29 @@ __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
   d.lane = lane;
   d.half = half;
   d.mrows = mrows;
+  d.ind = 0;
+  // rows through a row map: the grouped one-plane shapes only (gg_grouped
+  // refuses the others); uniform
+  if constexpr (!HILO && P::AL <= 4 && GPK * P::BM / P::W <= 64) {
+    if (a.row_map) {
+      d.ind = 1;
+      d.xr0 = rsrc(a.x, (size_t)a.x_rows * a.K * 2);
+      d.qr = rsrc(a.seeds, (size_t)KB * GPK * a.rows_pad * 4);
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const int blk = wave * P::AL + l, rb = blk % (P::BM / 4);
+        const int row = 4 * rb + (lane >> 4), q = (lane & 15) ^ (row & 15);
+        d.aoff[l] = l < P::AL && row < mrows
+                        ? (uint32_t)(((size_t)a.row_map[row0 + row] * a.K + 8 * q) * 2)
+                        : kGgOOB;
+      }
+      constexpr int XL4 = GPK * P::BM / P::W;
+      const int idx = wave * XL4 + lane, g = idx / P::BM, rq = idx - g * P::BM;
+      d.soff = lane < XL4 && rq < mrows
+                   ? (uint32_t)(((size_t)g * a.rows_pad + a.row_map[row0 + rq]) * 4)
+                   : kGgOOB;
+    }
+  }
 
   f32x4_t acc[MS][NT];
 #pragma unroll
@@ -391,7 +428,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
       for (int i = 0; i < MS; ++i)
 #pragma unroll
         for (int v = 0; v < 4; ++v) t[i][v] = row16_sum(rsum[i][v]);
-      float *so = a.seeds_out + (size_t)(c0 / a.seeds_gw) * a.rows_pad + row0;
+      float *so = a.seeds_out + (size_t)(c0 / a.seeds_gw) * a.seeds_rp + row0;
       if (per == 1) {
         if (lr == 0 && c0 < a.N) {
 #pragma unroll
@@ -491,7 +528,7 @@ __global__ __launch_bounds__(256) void gg_prep_kernel(int mode, const void *src,
   if (r >= rows) return;  // whole waves; no barriers here
   const int gw = 8 * L;   // columns per seed group
   size_t srow = (size_t)r;
-  if (mode == 2) srow = (size_t)row_map[r];
+  if (mode == 2 && row_map) srow = (size_t)row_map[r];
   for (int c0 = 0; c0 < K; c0 += 512) {
     const int c = c0 + 8 * lane;
     float t = 0.f;
@@ -599,6 +636,7 @@ size_t gg_dense_workspace(int M, int N, int K, int G, int amode, int epi, int nu
 hipError_t gg_dense(GgArgs a, int amode, void *ws, int num_cus, hipStream_t st) {
   a.rows_pad = gg_rows_pad(a.M);
   a.seeds_out = nullptr;  // (the dense FFN's down makes its own seeds)
+  a.row_map = nullptr;
   uint8_t *w = static_cast<uint8_t *>(ws);
   float *seeds = reinterpret_cast<float *>(w);
   a.seeds = seeds;
@@ -664,7 +702,11 @@ hipError_t gg_grouped(const GgArgs &a0, int max_tiles, hipStream_t st) {
   if (max_tiles <= 0) return hipSuccess;
   const bool sw = a.epi == GG_SWIGLU_HILO;
   // the epilogue's seeds: SwiGLU only, groups of one, two or four waves' 32 columns
-  if (a.seeds_out && (!sw || (a.seeds_gw != 32 && a.seeds_gw != 64 && a.seeds_gw != 128)))
+  if (a.seeds_out && (!sw || a.seeds_rp <= 0 ||
+                      (a.seeds_gw != 32 && a.seeds_gw != 64 && a.seeds_gw != 128)))
+    return hipErrorInvalidValue;
+  // rows through a row map: one bf16 plane, x rows addressable in 31 bits
+  if (a.row_map && (a.hilo || a.x_rows <= 0 || (size_t)a.x_rows * a.K * 2 > 0x7FFFFFFFu))
     return hipErrorInvalidValue;
   const unsigned gx = sw ? (a.N + 127) / 128 : (a.N + 255) / 256;
   if (a.hilo) {  // 64-row tiles: two per table entry

@@ -35,7 +35,12 @@ struct GgArgs {
   // for a GEMM that takes them as A: [N / seeds_gw][rows_pad], -136 * the sum
   // of hi + lo over each group of seeds_gw output columns (32, 64 or 128)
   float *seeds_out;
-  int seeds_gw;
+  int seeds_gw, seeds_rp;  // group width, row stride of seeds_out
+  // grouped, one bf16 plane only, or null: A row r of the table is x row
+  // row_map[r] (x: [x_rows, K], seeds [K / gw][rows_pad] per x row), so the
+  // rows need no gathered copy
+  const int32_t *row_map;
+  int x_rows;
 };
 
 // Columns per seed group: min(G, 128).
@@ -48,8 +53,8 @@ bool gg_supported(int K, int G, int tiled);
 // Seeds (and converted activations) of A, one wave per row:
 //   mode 0: bf16 rows x [rows, K] -> seeds;
 //   mode 1: bf16 hi/lo planes x, x2 -> seeds of hi + lo;
-//   mode 2: f32 rows src gathered through row_map (row r = src row row_map[r])
-//           -> bf16 (RNE) rows into out + seeds;
+//   mode 2: f32 rows src gathered through row_map (row r = src row row_map[r];
+//           src row r when row_map is null) -> bf16 (RNE) rows into out + seeds;
 //   mode 3: f32 rows src -> hi/lo planes out / out2 + seeds.
 // rows_dev (device, may be null): the row count, when only the device knows
 // it (rows is then an upper bound).
