@@ -96,10 +96,10 @@ struct Gg {
   static_assert(3 * BYTES <= 160 * 1024, "LDS");
 };
 
-// What a wave's loads of a k-block read: its rsrcs (the weight / scale ones
-// are the wave's own matrix in SwiGLU mode) and geometry.
 constexpr uint32_t kGgOOB = 0x80000000u;  // an offset past every range: no data moves
 
+// What a wave's loads of a k-block read: its rsrcs (the weight / scale ones
+// are the wave's own matrix in SwiGLU mode) and geometry.
 struct GgLd {
   rsrc_t xr0, xr1, wr, sr, qr;
   int K, KB, NG, G, Rp, wave, lane, half;  // half: SwiGLU, the wave loads up tiles
