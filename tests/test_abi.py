@@ -172,3 +172,19 @@ def test_sparsity_mode_is_dense():
     assert M.PerChannel(torch.empty(0)).is_dense()
     assert not M.PerChannel(torch.tensor([0.0, float("nan")])).is_dense()
     assert M.of(0.3).tau == 0.3 and M.of(torch.zeros(2)).thresholds is not None
+
+
+def test_cpp_header_compiles():
+    """include/cascadia_int4.hpp (the C++ mirror of the crate's API) and the
+    program that tests it on the GPU compile as C++17, warnings as errors."""
+    import shutil
+    import subprocess
+
+    if not shutil.which("g++") or not os.path.isdir("/opt/rocm/include"):
+        pytest.skip("no g++ or ROCm headers")
+    src = os.path.join(ROOT, "tests", "cpp", "test_cpp_api.cpp")
+    r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-Werror",
+                        "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                        "-I" + os.path.join(ROOT, "include"), src],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-3000:]
