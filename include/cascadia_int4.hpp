@@ -665,8 +665,20 @@ class ExpertWeights {
                       "file too small: expected at least " + std::to_string(need) + ", got " +
                           std::to_string(got),
                       need, got);
+    return from_host(host.data(), need, hidden, intermediate, group, sdt);
+  }
+
+  // One flat expert already in host memory (no crate counterpart: open's
+  // upload without the file), exactly cascadia_int4_expert_bytes long.
+  static ExpertWeights from_host(const uint8_t *flat, size_t len, size_t hidden,
+                                 size_t intermediate, size_t group = GROUP_SIZE,
+                                 ScaleDtype sdt = ScaleDtype::Bf16) {
+    const size_t need = cascadia_int4_expert_bytes((uint32_t)hidden, (uint32_t)intermediate,
+                                                   (uint32_t)group);
+    detail::require(need > 0, "unsupported expert dims");
+    detail::require(flat && len == need, "flat expert length does not match its dims");
     ExpertWeights w(hidden, intermediate, group, sdt, Tiling::Crate, DeviceBuffer<uint8_t>(need));
-    w.blob_.upload(host.data());
+    w.blob_.upload(flat);
     w.slice();
     return w;
   }
@@ -741,5 +753,289 @@ inline void expert_forward(const ExpertWeights &w, DeviceSlice<const uint16_t> x
                  w.up_scale_bits(), w.down_packed_bytes(), w.down_scale_bits(), out_bf16, o,
                  w.intermediate());
 }
+
+// ---- the sparse-MoE layer (runner.rs:1806-1832, batched over tokens) ----
+
+// The routed experts of one layer in one device blob: expert e at e * stride()
+// (a multiple of 256), in the crate's flat order or MFMA-tiled.
+class ExpertStack {
+ public:
+  // n_experts flat experts (format.rs:35-47) back to back in host memory;
+  // o.tiling Crate keeps their bytes, Mfma tiles each on the device.
+  static ExpertStack upload(const uint8_t *host_flat, size_t n_experts, size_t hidden,
+                            size_t intermediate, const Options &o = {}) {
+    detail::require(host_flat && n_experts > 0, "no experts");
+    detail::require(o.tiling == Tiling::Crate || o.tiling == Tiling::Mfma,
+                    "experts are crate-layout or MFMA-tiled");
+    const uint32_t h = (uint32_t)hidden, i = (uint32_t)intermediate, g = (uint32_t)o.group_size;
+    const size_t flat = cascadia_int4_expert_bytes(h, i, g);
+    detail::require(flat > 0, "unsupported expert dims");
+    const size_t per = o.tiling == Tiling::Crate ? flat : cascadia_int4_expert_tiled_bytes(h, i, g);
+    ExpertStack s(hidden, intermediate, n_experts, (per + 255) / 256 * 256, o);
+    s.blob_ = DeviceBuffer<uint8_t>(n_experts * s.stride_);
+    if (o.tiling == Tiling::Crate) {
+      std::vector<uint8_t> staged(s.blob_.size(), 0);
+      for (size_t e = 0; e < n_experts; ++e)
+        std::memcpy(staged.data() + e * s.stride_, host_flat + e * flat, flat);
+      s.blob_.upload(staged.data());
+      return s;
+    }
+    DeviceBuffer<uint8_t> one(flat);
+    for (size_t e = 0; e < n_experts; ++e) {
+      one.upload(host_flat + e * flat);
+      cascadia_int4_expert src{}, dst{};
+      detail::check(cascadia_int4_expert_from_flat(one.data(), h, i, g, &src),
+                    "cascadia_int4_expert_from_flat");
+      detail::check(cascadia_int4_tile_expert(h, i, g, &src, s.blob_.data() + e * s.stride_, &dst,
+                                              nullptr),
+                    "cascadia_int4_tile_expert");
+      // `one` is refilled by the next upload: the tiling must have read it
+      detail::check(cascadia_int4_synchronize(nullptr), "cascadia_int4_synchronize");
+    }
+    return s;
+  }
+  const uint8_t *data() const { return blob_.data(); }
+  size_t stride() const { return stride_; }
+  size_t n_experts() const { return n_; }
+  size_t hidden() const { return hidden_; }
+  size_t intermediate() const { return inter_; }
+  Options options() const { return o_; }
+
+ private:
+  ExpertStack(size_t h, size_t i, size_t n, size_t stride, const Options &o)
+      : hidden_(h), inter_(i), n_(n), stride_(stride), o_(o) {}
+  size_t hidden_, inter_, n_, stride_;
+  Options o_;
+  DeviceBuffer<uint8_t> blob_;
+};
+
+// One layer's experts: the routed stack and an optional shared expert
+// (shell_int4.rs:629) of the same hidden size, group, scale dtype and layout.
+// Refers to, does not own, the weights.
+class MoeLayer {
+ public:
+  explicit MoeLayer(const ExpertStack &routed) {
+    const Options o = routed.options();
+    detail::require(routed.n_experts() <= 1024, "at most 1024 experts");
+    l_.hidden = (uint32_t)routed.hidden();
+    l_.inter = (uint32_t)routed.intermediate();
+    l_.group_size = (uint32_t)o.group_size;
+    l_.scale_dtype = (uint32_t)o.scale_dtype;
+    l_.tiling = (uint32_t)o.tiling;
+    l_.n_experts = (uint32_t)routed.n_experts();
+    l_.experts = routed.data();
+    l_.expert_stride = routed.stride();
+  }
+  MoeLayer &with_shared(const ExpertWeights &shared) {
+    const Options s = shared.options();
+    detail::require(shared.hidden() == l_.hidden && s.group_size == l_.group_size &&
+                        (uint32_t)s.scale_dtype == l_.scale_dtype &&
+                        (uint32_t)s.tiling == l_.tiling,
+                    "the shared expert must match the routed experts' hidden size, group, "
+                    "scale dtype and layout");
+    l_.shared = shared.c_expert();
+    l_.shared_inter = (uint32_t)shared.intermediate();
+    return *this;
+  }
+  size_t hidden() const { return l_.hidden; }
+  size_t n_experts() const { return l_.n_experts; }
+  bool has_shared() const { return l_.shared.gate_packed != nullptr; }
+  const cascadia_int4_moe_layer &c_layer() const { return l_; }
+  // device workspace bytes of moe_forward (Options::workspace)
+  size_t workspace_bytes(size_t top_k, size_t n_tokens) const {
+    return cascadia_int4_moe_workspace_bytes(&l_, (uint32_t)top_k, (uint32_t)n_tokens);
+  }
+
+ private:
+  cascadia_int4_moe_layer l_{};
+};
+
+// How tokens pick their top_k experts (shell_int4.rs:588-620, glm/gate.rs:24-62,
+// or given ids / weights); slots with a weight below threshold are skipped
+// (runner.rs:1811).
+class Routing {
+ public:
+  // s = sigmoid(logit); top_k by s + bias (ties to the lower id);
+  // w = s / (sum s + 1e-20) * scale when normalize, else s * scale.
+  static Routing sigmoid_bias(DeviceSlice<const float> logits, size_t top_k, float scale,
+                              bool normalize, DeviceSlice<const float> bias = {}) {
+    Routing r(CASCADIA_INT4_ROUTE_SIGMOID_BIAS, top_k);
+    r.r_.logits = logits.data;
+    r.r_.bias = bias.data;
+    r.r_.scale = scale;
+    r.r_.normalize = normalize ? 1u : 0u;
+    r.logits_len_ = logits.len;
+    r.bias_len_ = bias.len;
+    return r;
+  }
+  // the top_k logits (ties to the lower id), w = softmax over them
+  static Routing softmax_topk(DeviceSlice<const float> logits, size_t top_k) {
+    Routing r(CASCADIA_INT4_ROUTE_SOFTMAX_TOPK, top_k);
+    r.r_.logits = logits.data;
+    r.logits_len_ = logits.len;
+    return r;
+  }
+  // [n_tokens, top_k] expert ids and weights
+  static Routing given(DeviceSlice<const int32_t> ids, DeviceSlice<const float> weights,
+                       size_t top_k) {
+    Routing r(CASCADIA_INT4_ROUTE_IDS, top_k);
+    detail::require(ids.len == weights.len, "ids and weights differ in length");
+    r.r_.ids = ids.data;
+    r.r_.weights = weights.data;
+    r.ids_len_ = ids.len;
+    return r;
+  }
+  Routing &threshold(float t) {
+    r_.threshold = t;
+    return *this;
+  }
+  size_t top_k() const { return r_.top_k; }
+  const cascadia_int4_routing &c_routing() const { return r_; }
+
+  // the argument lengths for n_tokens tokens over n_experts
+  void check(size_t n_tokens, size_t n_experts) const {
+    detail::require(r_.top_k >= 1 && r_.top_k <= 16 && r_.top_k <= n_experts,
+                    "top_k must be 1..16 and at most the expert count");
+    if (r_.mode == CASCADIA_INT4_ROUTE_IDS) {
+      detail::require(ids_len_ == n_tokens * r_.top_k, "ids must be n_tokens x top_k");
+      return;
+    }
+    detail::require(logits_len_ == n_tokens * n_experts, "logits must be n_tokens x n_experts");
+    detail::require(bias_len_ == 0 || bias_len_ == n_experts, "bias must be n_experts long");
+  }
+
+ private:
+  Routing(uint32_t mode, size_t top_k) {
+    detail::require(top_k <= 16, "top_k must be at most 16");
+    r_.mode = mode;
+    r_.top_k = (uint32_t)top_k;
+    r_.scale = 1.f;
+  }
+  cascadia_int4_routing r_{};
+  size_t logits_len_ = 0, bias_len_ = 0, ids_len_ = 0;
+};
+
+// One MoE layer for n_tokens tokens: out_t = residual_t + shared(x_t) +
+// sum over the routed slots, in slot order, of w * bf16->f32(expert(bf16(x_t)))
+// (runner.rs:1806-1832).  x, out, residual (empty: zero): f32 [n_tokens,
+// hidden]; ids_out / weights_out (may be empty) receive the routing.  call
+// supplies the stream, synchronisation and workspace.
+inline void moe_forward(const MoeLayer &layer, const Routing &routing,
+                        DeviceSlice<const float> x, size_t n_tokens, DeviceSlice<float> out,
+                        DeviceSlice<const float> residual = {},
+                        DeviceSlice<int32_t> ids_out = {}, DeviceSlice<float> weights_out = {},
+                        const Options &call = {}) {
+  const size_t h = layer.hidden(), k = routing.top_k();
+  detail::require(n_tokens > 0 && n_tokens <= UINT32_MAX, "n_tokens must be 1..2^32-1");
+  routing.check(n_tokens, layer.n_experts());
+  detail::require(x.len == n_tokens * h && out.len == n_tokens * h,
+                  "x and out must be n_tokens x hidden");
+  detail::require(residual.data == nullptr || residual.len == n_tokens * h,
+                  "residual must be n_tokens x hidden");
+  detail::require(ids_out.data == nullptr || ids_out.len == n_tokens * k,
+                  "ids_out must be n_tokens x top_k");
+  detail::require(weights_out.data == nullptr || weights_out.len == n_tokens * k,
+                  "weights_out must be n_tokens x top_k");
+  detail::check(cascadia_int4_moe_forward(&layer.c_layer(), &routing.c_routing(), x.data,
+                                          residual.data, (uint32_t)n_tokens, out.data,
+                                          ids_out.data, weights_out.data, call.workspace,
+                                          call.stream),
+                "cascadia_int4_moe_forward");
+  detail::finish(call);
+}
+
+// ---- the crate's C handle API (c_ffi.rs:35-341) as an owning object ----
+
+// A model directory (safetensors, or an int4_bin manifest with flat expert
+// files) whose experts are read once and kept in HBM.  Calls are
+// synchronous; the handle serialises them.
+class Source {
+ public:
+  struct CacheStats {
+    uint64_t cached, evictions, resident_bytes;
+  };
+  struct PrefetchStats {
+    uint64_t submits, drops, processed, loaded;
+  };
+
+  // c_ffi.rs open_source: -2 (invalid UTF-8) -> invalid_argument, -3 (not a
+  // model directory) -> GemmError::Io.
+  static Source open(const std::string &model_dir) {
+    CascadiaInt4Source *h = nullptr;
+    const int rc = cascadia_int4_open_source(model_dir.c_str(), &h);
+    if (rc == -3) throw GemmError(GemmError::Kind::Io, "io: cannot open model dir " + model_dir);
+    if (rc != 0)
+      throw std::invalid_argument("cascadia_int4_open_source: " + std::to_string(rc));
+    return Source(h);
+  }
+  ~Source() { cascadia_int4_destroy_source(h_); }
+  Source(Source &&o) noexcept : h_(o.h_) { o.h_ = nullptr; }
+  Source &operator=(Source &&o) noexcept {
+    std::swap(h_, o.h_);
+    return *this;
+  }
+  Source(const Source &) = delete;
+  Source &operator=(const Source &) = delete;
+
+  // Read (layer, expert) into HBM now.
+  void prewarm(uint32_t layer, uint32_t expert) {
+    expert_call(cascadia_int4_prewarm(h_, layer, expert), layer, expert);
+  }
+  // x, out: host arrays of the model's hidden size; f32 -> bf16 at entry,
+  // bf16 -> f32 at exit (c_ffi.rs:323-339).
+  void expert_forward(uint32_t layer, uint32_t expert, const float *x, float *out) {
+    detail::require(x && out, "null x or out");
+    expert_call(cascadia_int4_expert_forward(h_, layer, expert, x, out), layer, expert);
+  }
+  std::vector<float> expert_forward(uint32_t layer, uint32_t expert, const std::vector<float> &x) {
+    std::vector<float> out(x.size());
+    expert_forward(layer, expert, x.data(), out.data());
+    return out;
+  }
+
+  // The expert cache (runner.rs:148-170): at most max_experts resident and
+  // max_bytes of HBM (0 = unbounded); lowering a limit evicts at once.
+  void set_cache_limits(uint64_t max_experts, uint64_t max_bytes) {
+    device_call(cascadia_int4_source_set_cache_limits(h_, max_experts, max_bytes),
+                "cascadia_int4_source_set_cache_limits");
+  }
+  CacheStats cache_stats() const {
+    CacheStats s{};
+    device_call(cascadia_int4_source_cache_stats(h_, &s.cached, &s.evictions, &s.resident_bytes),
+                "cascadia_int4_source_cache_stats");
+    return s;
+  }
+
+  // The runner's Prefetcher (runner.rs:282-360): queue (layer, expert) for the
+  // handle's loader thread; never blocks (a full queue drops the request).
+  void prefetch(uint32_t layer, uint32_t expert) {
+    device_call(cascadia_int4_prefetch(h_, layer, expert), "cascadia_int4_prefetch");
+  }
+  void prefetch_wait() { device_call(cascadia_int4_prefetch_wait(h_), "cascadia_int4_prefetch_wait"); }
+  PrefetchStats prefetch_stats() const {
+    PrefetchStats s{};
+    device_call(cascadia_int4_prefetch_stats(h_, &s.submits, &s.drops, &s.processed, &s.loaded),
+                "cascadia_int4_prefetch_stats");
+    return s;
+  }
+
+  CascadiaInt4Source *handle() const { return h_; }
+
+ private:
+  explicit Source(CascadiaInt4Source *h) : h_(h) {}
+  // -2: the expert cannot be read (missing, short, or not in the index)
+  static void expert_call(int rc, uint32_t layer, uint32_t expert) {
+    if (rc == -2)
+      throw GemmError(GemmError::Kind::Io, "io: cannot read expert " + std::to_string(expert) +
+                                               " of layer " + std::to_string(layer));
+    device_call(rc, "cascadia_int4 source call");
+  }
+  static void device_call(int rc, const char *fn) {
+    if (rc == 0) return;
+    if (rc == -1) throw std::invalid_argument(std::string(fn) + ": null handle");
+    throw DeviceError(fn, rc);
+  }
+  CascadiaInt4Source *h_ = nullptr;
+};
 
 }  // namespace cascadia_int4

@@ -15,6 +15,9 @@
 #include <string>
 #include <vector>
 
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include "cascadia_int4.hpp"
 #include "../../oracle/int4_oracle.h"
 
@@ -141,6 +144,62 @@ HostExpert make_expert(size_t hidden, size_t inter, size_t group, uint64_t seed)
     std::copy(s.begin(), s.end(), e.flat.begin() + e.off[k]);
   }
   return e;
+}
+
+double bf16_ulp(double v) {
+  return std::ldexp(1.0, (int)std::floor(std::log2(std::fmax(std::fabs(v), 0x1p-126))) - 7);
+}
+
+// One MoE layer's output against the oracle's layer on the GPU's own routing
+// (a near-tie resolved one libm ulp apart cannot move a token between the
+// sides): h and h - residual (the experts' part) within rel-L2 1e-3, every
+// element within max-abs 2e-2 or, where routed outputs are large enough that
+// one bf16 ulp exceeds that, within sum_k w_k ulp(y_k) plus 1e-5 max |h - x|
+// (each expert output is rounded to bf16, kernel.rs:133-135).
+void check_moe(const std::vector<float> &got, const std::vector<float> &x, size_t T, size_t h,
+               size_t inter, const std::vector<uint8_t> &experts, size_t stride, size_t E,
+               const HostExpert *shared, const std::vector<int32_t> &ids,
+               const std::vector<float> &w, size_t k, float thr, const std::string &what) {
+  std::vector<int64_t> ids64(ids.begin(), ids.end());
+  std::vector<float> want(T * h);
+  or_moe_layer(x.data(), T, h, inter, 32, OR_SCALE_BF16, OR_ORDER_AVX512, experts.data(), stride,
+               E, shared ? shared->flat.data() : nullptr, shared ? shared->inter : 0,
+               ids64.data(), w.data(), k, thr, want.data());
+  const double r = rel_l2(got, want);
+  std::vector<float> dg(T * h), dw(T * h);
+  double dmax = 0;
+  for (size_t q = 0; q < T * h; ++q) {
+    dg[q] = got[q] - x[q];
+    dw[q] = want[q] - x[q];
+    dmax = std::fmax(dmax, std::fabs((double)dw[q]));
+  }
+  const double rd = rel_l2(dg, dw);
+  if (!(r <= 1e-3 && rd <= 1e-3))
+    fail(what + ": rel_l2 " + std::to_string(r) + ", experts' part " + std::to_string(rd));
+  for (size_t t = 0; t < T; ++t) {
+    std::vector<uint16_t> xb(h), y(h);
+    for (size_t c = 0; c < h; ++c) xb[c] = or_f32_to_bf16(x[t * h + c]);
+    std::vector<double> allow(h, 0.0);
+    for (size_t s = 0; s < k; ++s) {
+      if (w[t * k + s] < thr) continue;
+      const uint8_t *e = experts.data() + (size_t)ids[t * k + s] * stride;
+      or_expert_forward(xb.data(), h, inter, 32, OR_SCALE_BF16, OR_ORDER_AVX512, e, y.data());
+      for (size_t c = 0; c < h; ++c)
+        allow[c] += std::fabs((double)w[t * k + s]) * bf16_ulp(or_bf16_to_f32(y[c]));
+    }
+    for (size_t c = 0; c < h; ++c) {
+      const double a = std::fmax(2e-2, allow[c] + 1e-5 * dmax);
+      if (std::fabs((double)got[t * h + c] - want[t * h + c]) > a)
+        fail(what + ": token " + std::to_string(t) + " element " + std::to_string(c));
+    }
+  }
+  pass(what + " (rel_l2 " + std::to_string(r) + ", experts' part " + std::to_string(rd) + ")");
+}
+
+void write_file(const std::string &path, const std::string &text) {
+  std::FILE *f = std::fopen(path.c_str(), "wb");
+  if (!f || std::fwrite(text.data(), 1, text.size(), f) != text.size()) fail("write " + path);
+  std::fclose(f);
 }
 
 }  // namespace
@@ -359,6 +418,176 @@ int main(int argc, char **argv) {
       or_quantize_int4_group(wb.data(), qn, qk, 32, wp.data(), ws.data());
       if (qz.first.download() != wp || qz.second.download() != ws) fail("quantize_int4_group bytes");
       pass("quantize_int4_group codes and scales exact");
+    }
+
+    // ---- one sparse-MoE layer (runner.rs:1806-1832): both layouts, a shared
+    //      expert, the three routing modes, one token and several ----
+    {
+      const size_t E = 8, h = 256, i = 128, k = 2, si = 64;
+      const size_t per = or_expert_bytes(h, i, 32), stride = (per + 255) / 256 * 256;
+      std::vector<uint8_t> flat(E * per), strided(E * stride, 0);
+      for (size_t e = 0; e < E; ++e) {
+        const HostExpert he = make_expert(h, i, 32, 40 + e);
+        std::copy(he.flat.begin(), he.flat.end(), flat.begin() + e * per);
+        std::copy(he.flat.begin(), he.flat.end(), strided.begin() + e * stride);
+      }
+      const HostExpert shared = make_expert(h, si, 32, 60);
+      for (ci::Tiling tl : {ci::Tiling::Crate, ci::Tiling::Mfma}) {
+        const std::string lay = tl == ci::Tiling::Crate ? "crate" : "tiled";
+        ci::Options wo;
+        wo.tiling = tl;
+        const ci::ExpertStack stack = ci::ExpertStack::upload(flat.data(), E, h, i, wo);
+        ci::ExpertWeights sh = ci::ExpertWeights::from_host(shared.flat.data(), shared.flat.size(),
+                                                            h, si, 32);
+        if (tl == ci::Tiling::Mfma) sh = sh.tiled();
+        ci::MoeLayer layer(stack);
+        layer.with_shared(sh);
+        for (size_t T : {size_t(1), size_t(5)}) {
+          const std::string tag = lay + " T" + std::to_string(T);
+          const std::vector<float> x = normal(70 + T, 1, T * h), logits = normal(70 + T, 2, T * E);
+          const std::vector<float> bias = normal(70 + T, 3, E);
+          auto dx = dev(x);
+          auto dl = dev(logits);
+          auto db = dev(bias);
+          ci::DeviceBuffer<float> out(T * h), wts(T * k);
+          ci::DeviceBuffer<int32_t> ids(T * k);
+          // sigmoid + bias, renormalised x 2.5, residual = x
+          ci::moe_forward(layer, ci::Routing::sigmoid_bias(dl, k, 2.5f, true, db), dx, T, out, dx,
+                          ids, wts);
+          const std::vector<int32_t> gi = ids.download();
+          const std::vector<float> gw = wts.download();
+          for (size_t t = 0; t < T; ++t) {
+            int64_t wi[k];
+            float ww[k];
+            or_route_sigmoid_bias(logits.data() + t * E, bias.data(), E, k, 2.5f, 1, wi, ww);
+            for (size_t s = 0; s < k; ++s) {
+              if (gi[t * k + s] != wi[s]) fail("moe routing ids " + tag);
+              if (std::fabs((double)gw[t * k + s] - ww[s]) >
+                  4 * std::ldexp(1.0, (int)std::floor(std::log2(std::fabs(ww[s]))) - 23))
+                fail("moe routing weights " + tag);
+            }
+          }
+          pass("moe_forward routing (sigmoid + bias) ids exact, weights within 4 ulp, " + tag);
+          check_moe(out.download(), x, T, h, i, strided, stride, E, &shared, gi, gw, k, 0.f,
+                    "moe_forward sigmoid + bias + shared, " + tag);
+
+          // given ids / weights with a skip threshold, no shared expert, no residual
+          ci::MoeLayer plain(stack);
+          std::vector<int32_t> gid(T * k);
+          std::vector<float> gwt(T * k);
+          for (size_t q = 0; q < T * k; ++q) {
+            gid[q] = (int32_t)((q * 5 + T) % E);
+            gwt[q] = 0.1f + 0.2f * (float)(q % 4);
+          }
+          auto dgi = dev(gid);
+          auto dgw = dev(gwt);
+          ci::DeviceBuffer<float> out2(T * h);
+          ci::moe_forward(plain, ci::Routing::given(dgi, dgw, k).threshold(0.3f), dx, T, out2);
+          // no residual: the layer's output is the routed sum alone; the
+          // oracle's layer adds x
+          std::vector<float> got2 = out2.download();
+          for (size_t q = 0; q < T * h; ++q) got2[q] += x[q];
+          check_moe(got2, x, T, h, i, strided, stride, E, nullptr, gid, gwt, k, 0.3f,
+                    "moe_forward given ids, threshold 0.3, no residual, " + tag);
+        }
+      }
+      // softmax over the top-k logits, crate layout, 3 tokens
+      {
+        const size_t T = 3;
+        const ci::ExpertStack stack = ci::ExpertStack::upload(flat.data(), E, h, i);
+        ci::MoeLayer layer(stack);
+        const std::vector<float> x = normal(90, 1, T * h), logits = normal(90, 2, T * E);
+        auto dx = dev(x);
+        auto dl = dev(logits);
+        ci::DeviceBuffer<float> out(T * h), wts(T * k);
+        ci::DeviceBuffer<int32_t> ids(T * k);
+        ci::moe_forward(layer, ci::Routing::softmax_topk(dl, k), dx, T, out, dx, ids, wts);
+        const std::vector<int32_t> gi = ids.download();
+        const std::vector<float> gw = wts.download();
+        for (size_t t = 0; t < T; ++t) {
+          int64_t wi[k];
+          float ww[k];
+          or_route_softmax_topk(logits.data() + t * E, E, k, wi, ww);
+          for (size_t s = 0; s < k; ++s)
+            if (gi[t * k + s] != wi[s]) fail("softmax routing ids");
+        }
+        check_moe(out.download(), x, T, h, i, strided, stride, E, nullptr, gi, gw, k, 0.f,
+                  "moe_forward softmax top-k, crate T3");
+        expect_invalid([&] {
+          ci::DeviceBuffer<float> o(T * h - 1);
+          ci::moe_forward(layer, ci::Routing::softmax_topk(dl, k), dx, T, o);
+        }, "moe_forward with out one short");
+        expect_invalid([&] {
+          ci::moe_forward(layer, ci::Routing::softmax_topk(ci::DeviceSlice<const float>(dl.data(), T * E - 1), k),
+                          dx, T, ci::DeviceSlice<float>(nullptr, T * h));
+        }, "moe_forward with logits one short");
+      }
+    }
+
+    // ---- the handle API over an int4_bin directory (c_ffi.rs:35-341,
+    //      manifest.rs:137-142): forward, prefetch, the cache, errors ----
+    {
+      const size_t h = 64, i = 32;
+      char tmpl[] = "/tmp/cascadia_cpp_api_XXXXXX";
+      if (!mkdtemp(tmpl)) fail("mkdtemp");
+      const std::string dir = tmpl, edir = dir + "/experts", ldir = edir + "/layer_00";
+      if (mkdir(edir.c_str(), 0700) || mkdir(ldir.c_str(), 0700)) fail("mkdir");
+      write_file(dir + "/manifest.json",
+                 "{\"arch\": \"test\", \"experts_format\": \"int4_bin\", \"hidden_size\": 64, "
+                 "\"expert_intermediate\": 32, \"num_experts\": 8, \"top_k\": 2}");
+      std::vector<uint8_t> fix(or_expert_bytes(h, i, 32));
+      std::FILE *f = std::fopen(argv[1], "rb");
+      if (!f || std::fread(fix.data(), 1, fix.size(), f) != fix.size()) fail("read fixture");
+      std::fclose(f);
+      const HostExpert e1 = make_expert(h, i, 32, 80);
+      write_file(ldir + "/expert_000.bin", std::string(fix.begin(), fix.end()));
+      write_file(ldir + "/expert_001.bin", std::string(e1.flat.begin(), e1.flat.end()));
+      {
+        ci::Source src = ci::Source::open(dir);
+        src.prefetch(0, 1);
+        src.prefetch_wait();
+        const ci::Source::PrefetchStats ps = src.prefetch_stats();
+        if (ps.submits != 1 || ps.processed != 1 || ps.loaded != 1 || ps.drops != 0)
+          fail("prefetch stats");
+        pass("Source::prefetch loaded expert 1 ahead of use");
+        const std::vector<uint8_t> *flats[2] = {&fix, &e1.flat};
+        for (uint32_t e = 0; e < 2; ++e) {
+          const std::vector<float> x = normal(81, e, h);
+          const std::vector<float> got = src.expert_forward(0, e, x);
+          std::vector<uint16_t> xb(h), want(h), gotb(h);
+          for (size_t c = 0; c < h; ++c) {
+            xb[c] = or_f32_to_bf16(x[c]);
+            gotb[c] = ci::f32_to_bf16_bits(got[c]);
+            if (ci::bf16_bits_to_f32(gotb[c]) != got[c]) fail("Source output not a bf16 value");
+          }
+          or_expert_forward(xb.data(), h, i, 32, OR_SCALE_BF16, OR_ORDER_AVX512,
+                            flats[e]->data(), want.data());
+          check_close_bf16(gotb, want, "Source::expert_forward expert " + std::to_string(e));
+        }
+        ci::Source::CacheStats cs = src.cache_stats();
+        if (cs.cached != 2 || cs.evictions != 0) fail("cache stats after two experts");
+        src.set_cache_limits(1, 0);
+        cs = src.cache_stats();
+        if (cs.cached != 1 || cs.evictions != 1) fail("cache limit of one expert");
+        pass("Source cache: two resident, a limit of one evicts one");
+        try {
+          src.prewarm(0, 7);
+          fail("prewarm of a missing expert");
+        } catch (const ci::GemmError &e) {
+          pass("Source::prewarm of a missing expert file -> GemmError::Io");
+        }
+      }
+      try {
+        (void)ci::Source::open(dir + "/no_such_dir");
+        fail("open of a missing directory");
+      } catch (const ci::GemmError &e) {
+        pass("Source::open of a missing directory -> GemmError::Io");
+      }
+      for (const char *name : {"/expert_000.bin", "/expert_001.bin"}) std::remove((ldir + name).c_str());
+      std::remove((dir + "/manifest.json").c_str());
+      rmdir(ldir.c_str());
+      rmdir(edir.c_str());
+      rmdir(dir.c_str());
     }
   } catch (const std::exception &e) {
     fail(std::string("exception: ") + e.what());
