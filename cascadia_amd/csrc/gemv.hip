@@ -143,9 +143,10 @@ __host__ __device__ inline int gv_wave_bytes(int planes, int nt, int kpw, int gp
 // k-blocks per wave (sizes the per-wave register arrays: fewer registers, more
 // resident waves); GPB: scale groups per 128-column k-block (128 / G for G of
 // 32 or 64, else 1).  With GPB > 1 each MFMA step must cover whole groups: the
-// weight fragment's four dwords are transposed across the four 16-lane rows
-// (step s then holds columns 32 s .. 32 s + 31) and the activations are read
-// to match; every group gets its own seed and scale.  MODE: GvMode; R: routing
+// tiled layout stores such blocks with the fragment's four dwords transposed
+// across the four 16-lane rows (layout.hip; step s then holds columns
+// 32 s .. 32 s + 31) and the activations are read to match; every group gets
+// its own seed and scale.  MODE: GvMode; R: routing
 // registers per lane (GV_MOE_GATE_UP; 0: given ids and weights only).
 template <int NT, int AM, int RING, int KPWM, int GPB, int MODE, int R, bool SHWG = false>
 CAI4_DEV void gemv_body(const GvParams &a) {
@@ -405,7 +406,7 @@ CAI4_DEV void gemv_body(const GvParams &a) {
       lds_read_f32<GPB>(sdp + j * GPB, sd);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const u32x4_t b = GPB > 1 ? xpose_rows(ring[u][nt]) : ring[u][nt];
+        const u32x4_t b = ring[u][nt];
         const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
         float sc[GPB];  // row lr's scales of the k-block's groups
         lds_read_f32<GPB>(scp + (nt * a.kpw + j) * 16 * GPB, sc);

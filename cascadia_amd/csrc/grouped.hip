@@ -12,11 +12,12 @@
 // seed -136 * sum(x) over the group's columns (computed once per row and
 // group by gg_prep) and is scaled in f32 when the group ends, acc += s * p.
 // A group of 32 or 64 columns spans one or two 32-column MFMA steps: the
-// weight fragment's four dwords (one 32-column segment of the 128-column
-// k-block each, per 16-lane row) are transposed across the lane rows
-// (xpose_rows) so that step s holds columns 32 s .. 32 s + 31, and the
-// activation fragment of lane row c in step s is chunk 4 s + c.  Groups of
-// 128 or more keep the untransposed order (step s = chunk 4 c + s).
+// tiled layout stores those matrices' fragments with their four dwords (one
+// 32-column segment of the 128-column k-block each, per 16-lane row)
+// transposed across the lane rows (layout.hip), so that step s holds columns
+// 32 s .. 32 s + 31 as loaded, and the activation fragment of lane row c in
+// step s is chunk 4 s + c.  Groups of 128 or more keep the untransposed order
+// (step s = chunk 4 c + s).
 //
 // Two-plane activations (hilo): the A operand is hi + lo (two bf16 planes
 // whose sum carries an f32 value to 2^-16: the SwiGLU intermediate, or an f32
@@ -212,7 +213,6 @@ CAI4_DEV void gg_compute(const uint8_t *buf, int wm, int wn, int lane, int sdt, 
   for (int j = 0; j < NT; ++j) {
     const int tile = gg_tile<P, NT, SW>(wn, j);
     b[j] = *reinterpret_cast<const u32x4_t *>(buf + P::B + tile * 1024 + 16 * lane);
-    if constexpr (GPK > 1) b[j] = xpose_rows(b[j]);
 #pragma unroll
     for (int g = 0; g < GPK; ++g) {
       const uint32_t bits =

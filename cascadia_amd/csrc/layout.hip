@@ -17,6 +17,18 @@
 // yields the dword's 8 columns in natural order and the activations need no
 // re-ordering.  The nibble codes and scale bits are moved, never changed, so
 // every kernel computes bit-identical results from either layout.
+//
+// Groups of fewer than 128 columns (G not a multiple of 128): every 32-column
+// MFMA step must cover whole groups, so its lanes' dwords must be the block's
+// columns 32 s .. 32 s + 31.  Those blocks are stored with the dwords
+// transposed across the four 16-lane rows -- dword s of lane row c is dword c
+// of lane row s above:
+//
+//   packed_tiled[(T*KB + kb)*1024 + 16*l + 4*s .. +4]
+//       = swz(packed[16*T + (l & 15)][kb*64 + 16*s + 4*(l >> 4) .. +4])
+//
+// -- so the kernels load a step's fragment as stored (the transpose, four
+// lane permutes per fragment, was otherwise paid in every k-loop).
 #include "int4_common.hpp"
 #include "layout.hpp"
 
@@ -37,7 +49,7 @@ CAI4_DEV uint32_t swizzle_dword(uint32_t d) {
   return r;
 }
 
-__global__ void tile_packed_kernel(const uint8_t *__restrict__ packed, int N, int K,
+__global__ void tile_packed_kernel(const uint8_t *__restrict__ packed, int N, int K, int xposed,
                                    uint8_t *__restrict__ out) {
   const size_t kbt = (size_t)(K + 127) / 128;
   const size_t total = (size_t)((N + 15) / 16) * kbt * 64;  // 16-byte chunks
@@ -47,17 +59,21 @@ __global__ void tile_packed_kernel(const uint8_t *__restrict__ packed, int N, in
     const size_t l = i & 63, blk = i >> 6;
     const size_t T = blk / kbt, kb = blk % kbt;
     const size_t r = 16 * T + (l & 15);
-    const size_t byte0 = kb * 64 + 16 * (l >> 4);
-    u32x4_t v = {0u, 0u, 0u, 0u};
-    // row_bytes is a multiple of 16: a chunk is wholly inside the row or past it
-    if (r < (size_t)N && byte0 < row_bytes) {
-      v = *reinterpret_cast<const u32x4_t *>(packed + r * row_bytes + byte0);
-      v.x = swizzle_dword(v.x);
-      v.y = swizzle_dword(v.y);
-      v.z = swizzle_dword(v.z);
-      v.w = swizzle_dword(v.w);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (r < (size_t)N) {
+      const uint8_t *row = packed + r * row_bytes;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        // untransposed: dword s of the lane's own 16 bytes; transposed: dword
+        // (lane row) of lane row s's 16 bytes.  row_bytes is a multiple of 16:
+        // a 16-byte part is wholly inside the row or past it.
+        const size_t part = kb * 64 + 16 * (xposed ? (size_t)s : (l >> 4));
+        const size_t dw = xposed ? (l >> 4) : (size_t)s;
+        if (part < row_bytes)
+          w[s] = swizzle_dword(*reinterpret_cast<const uint32_t *>(row + part + 4 * dw));
+      }
     }
-    reinterpret_cast<u32x4_t *>(out)[i] = v;
+    reinterpret_cast<u32x4_t *>(out)[i] = u32x4_t{w[0], w[1], w[2], w[3]};
   }
 }
 
@@ -79,7 +95,7 @@ hipError_t tile_weights(const uint8_t *packed, const uint8_t *scale_bits, int N,
   size_t grid = (chunks + 255) / 256;
   if (grid > 16384) grid = 16384;
   hipLaunchKernelGGL(tile_packed_kernel, dim3(grid), dim3(256), 0, st, packed, N, K,
-                     packed_tiled);
+                     tiled_xposed(G) ? 1 : 0, packed_tiled);
   if (hipError_t e = hipGetLastError()) return e;
   const size_t ns = (size_t)((N + 15) / 16) * (K / G) * 16;
   grid = (ns + 255) / 256;

@@ -36,10 +36,12 @@
 //
 // k-slot mapping.  G % 128 == 0 ("contiguous"): MFMA step s of a k-block
 // takes dword s of each lane's chunk; all 128 columns share one scale.
-// Otherwise ("transposed", G = 32, 64, ...): the chunks are transposed across
-// the four lane rows with v_permlane32_swap / v_permlane16_swap so that step
-// s covers columns 32s..32s+31 of the block -- inside one group for any G
-// that is a multiple of 32.  K must be a multiple of 32 and of G.
+// Otherwise ("transposed", G = 32, 64, ...): step s covers columns
+// 32s..32s+31 of the block -- inside one group for any G that is a multiple
+// of 32 -- from the chunks transposed across the four lane rows: stored so in
+// the tiled layout (layout.hip), transposed after the load with
+// v_permlane32_swap / v_permlane16_swap for the crate's bytes.  K must be a
+// multiple of 32 and of G.
 //
 // Token slots of a 16-slot MFMA tile:
 //   A_BF16 / A_GATHER: slot i = token i (exact bf16 products);
@@ -275,10 +277,11 @@ CAI4_DEV void load_w(u32x4_t (&b)[NT], const rsrc_t (&wr)[NT], const uint32_t (&
 }
 
 // MFMAs of one k-block: weights from registers, activations and scales from LDS.
+// xp: the fragments are the crate's bytes, not yet transposed (TR only).
 template <int NT, int MT, bool TR>
 CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&abase)[MT],
                          const uint32_t (&sbase)[NT], int k, int kr0, int g_lo, int K, int G,
-                         int glog2, int sdt, f32x4_t (&acc)[MT][NT]) {
+                         int glog2, int sdt, bool xp, f32x4_t (&acc)[MT][NT]) {
   const u32x4_t B136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
   const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
   const uint32_t koff = (uint32_t)(k - kr0) * 256;
@@ -315,8 +318,10 @@ CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&
     }
   } else {
     const int nsteps = min(4, (K - kbase) >> 5);
+    if (xp) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) b[nt] = xpose_rows(b[nt]);
+      for (int nt = 0; nt < NT; ++nt) b[nt] = xpose_rows(b[nt]);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s >= nsteps) break;
@@ -531,7 +536,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
-                                 a.sdt, acc);
+                                 a.sdt, !a.tiled, acc);
           load_w<NT>(ring[u], wr, wv, kb + u + U, wk, kb + u + U < kb1);
         }
       }
@@ -539,7 +544,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
       for (int u = 0; u < U - 1; ++u)
         if (kb + u < kb1)
           compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
-                                 a.sdt, acc);
+                                 a.sdt, !a.tiled, acc);
     }
   };
   if constexpr (SLICED) {

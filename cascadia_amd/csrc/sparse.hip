@@ -30,6 +30,7 @@
 //   sparse_axpy_reduce_kernel  the partial rows added in group order
 //                        (deterministic), and the groups' counts.
 #include "int4_common.hpp"
+#include "layout.hpp"
 #include "sparse.hpp"
 #include "tuning.hpp"
 
@@ -320,8 +321,9 @@ __global__ void __launch_bounds__(64)
 // (inside one scale group: G is a multiple of 32); lane l of a wave takes
 // chunks l, l + 64, ...  Crate layout: chunk c is the row's bytes 16c ..
 // 16c + 15 (byte b = columns 2b | 2b + 1).  Tiled layout (layout.hip): part
-// c % 4 of the row's k-block c / 4, each dword's byte b holding columns b |
-// b + 4.  Per chunk a lane forms sum((128 + n) * x) over the nibble codes n
+// c % 4 of the row's k-block c / 4 (its four dwords 256 bytes apart when the
+// groups are narrower than 128 columns), each dword's byte b holding columns
+// b | b + 4.  Per chunk a lane forms sum((128 + n) * x) over the nibble codes n
 // (nib128) and takes the offset off with the chunk's sum of x (q = n - 8, so
 // 136 x sum); the chunk's scale
 // multiplies that, the lane adds its chunks, and the wave adds its lanes:
@@ -331,6 +333,19 @@ CAI4_DEV size_t rm_chunk(const RowsMatrix &w, int r, int c) {
   if (!w.tiled) return (size_t)r * (size_t)(w.K / 2) + 16 * (size_t)c;
   const size_t KB = (size_t)(w.K + 127) / 128;
   return ((size_t)(r >> 4) * KB + (size_t)(c >> 2)) * 1024 + 16 * (size_t)((r & 15) + 16 * (c & 3));
+}
+// Chunk c of row r, dword d = its columns 8 d .. 8 d + 7.  A tiled matrix
+// whose groups are narrower than 128 columns stores its blocks with the
+// dwords transposed across the lane rows (layout.hip): dword d of lane row
+// c % 4 sits at dword c % 4 of lane row d, 256 bytes apart.
+CAI4_DEV u32x4_t rm_load(const RowsMatrix &w, int r, int c) {
+  if (!w.tiled || !tiled_xposed(w.G))
+    return *reinterpret_cast<const u32x4_t *>(w.packed + rm_chunk(w, r, c));
+  const size_t KB = (size_t)(w.K + 127) / 128;
+  const uint32_t *p = reinterpret_cast<const uint32_t *>(
+      w.packed + ((size_t)(r >> 4) * KB + (size_t)(c >> 2)) * 1024 + 16 * (size_t)(r & 15) +
+      4 * (size_t)(c & 3));
+  return u32x4_t{p[0], p[64], p[128], p[192]};
 }
 CAI4_DEV size_t rm_scale(const RowsMatrix &w, int r, int c) {
   const int NG = w.K / w.G, g = (32 * c) / w.G;
@@ -450,7 +465,7 @@ CAI4_DEV void rows_load(const RowsMatrix &w, const int (&r)[RB], int j0, int lan
     for (int j = 0; j < JB; ++j) {
       if (u >= live) continue;
       const int c0 = (j0 + j) * 64 + lane, c = c0 < nch ? c0 : nch - 1;
-      b.v[u][j] = *reinterpret_cast<const u32x4_t *>(w.packed + rm_chunk(w, r[u], c));
+      b.v[u][j] = rm_load(w, r[u], c);
       b.sb[u][j] = (uint32_t)sc[rm_scale(w, r[u], c)];
     }
 }

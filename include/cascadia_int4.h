@@ -60,8 +60,11 @@ extern "C" {
 /* Weight byte layouts.  CRATE is the crate's row-major layout, unchanged.
  * MFMA is the tiled device layout made by cascadia_int4_tile_weights: each
  * (16-row tile, 128-column k-block) is one contiguous 1 KB block in MFMA lane
- * order, so the decode kernels stream HBM sequentially.  Same codes and
- * scale bits, moved; results are bit-identical between the two. */
+ * order, so the decode kernels stream HBM sequentially; for groups narrower
+ * than 128 columns the blocks hold their dwords transposed across the four
+ * 16-lane rows, so a tiled copy is read with the group size it was made
+ * for.  Same codes and scale bits, moved; results are bit-identical between
+ * the two. */
 #define CASCADIA_INT4_TILING_CRATE 0u
 #define CASCADIA_INT4_TILING_MFMA 1u
 /* Experts only (cascadia_int4_expert.tiling), for the activation-sparse

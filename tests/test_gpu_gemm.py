@@ -483,14 +483,19 @@ def np_tile(packed, scales, n, k, g):
     sw = np.zeros_like(d)
     for b in range(4):
         sw |= (nib[b] | (nib[b + 4] << 4)) << (8 * b)
-    out = sw.view(np.uint8)
+    if g % 128:
+        # groups narrower than a block: dword s of lane row c is dword c of
+        # lane row s above (each 32-column MFMA step reads whole groups)
+        sw = sw.reshape(T, KB, 4, 16, 4).transpose(0, 1, 4, 3, 2).reshape(-1)
+    out = np.ascontiguousarray(sw).view(np.uint8)
     S = np.zeros((T * 16, NG), np.uint16)
     S[:n] = np.frombuffer(scales.tobytes(), "<u2").reshape(n, NG)
     sout = S.reshape(T, 16, NG).transpose(0, 2, 1).reshape(-1)
     return out, sout.view(np.uint8)
 
 
-@pytest.mark.parametrize("n,k,group", [(50, 256, 64), (33, 96, 32), (130, 384, 128), (7, 32, 32)])
+@pytest.mark.parametrize("n,k,group", [(50, 256, 64), (33, 96, 32), (130, 384, 128), (7, 32, 32),
+                                       (20, 480, 96), (17, 512, 256)])
 def test_tile_weights_bytes(cl, orc, n, k, group):
     packed, scales = weights(orc, n, k, group, F16, 5)
     pt, st = cl.tile_weights(dev(packed), dev(scales), n, k, group)
