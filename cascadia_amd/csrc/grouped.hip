@@ -282,7 +282,9 @@ CAI4_DEV void gg_stage(uint8_t *cur, uint8_t *nxt2, const GgLd &d, int kb, int K
   gg_compute<P, MS, NT, GPK, HILO, SW>(cur, wm, wn, d.lane, sdt, mt_live, nx, acc);
 }
 
-template <int MS, int NT, int WM, int WN, int GPK, bool HILO, bool SW>
+// SDT: the scale dtype (a.sdt) as a constant, so that each scale's f32
+// conversion is one instruction in the k-loop.
+template <int MS, int NT, int WM, int WN, int GPK, bool HILO, bool SW, int SDT>
 __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
   using P = Gg<MS, NT, WM, WN, GPK, HILO, SW>;
   __shared__ __attribute__((aligned(16))) uint8_t stages[3 * P::BYTES];
@@ -374,7 +376,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gg_kernel(GgArgs a) {
   for (int kb = kb0; kb < KE; ++kb) {
     const int nx2 = cur == 0 ? 2 : cur - 1;  // (cur + 2) % 3
     gg_stage<P, MS, NT, GPK, HILO, SW>(stages + cur * P::BYTES, stages + nx2 * P::BYTES, d, kb,
-                                       KE, wm, wn, a.sdt, mt_live, acc);
+                                       KE, wm, wn, SDT, mt_live, acc);
     cur = cur == 2 ? 0 : cur + 1;
   }
 
@@ -567,8 +569,12 @@ __global__ __launch_bounds__(256) void gg_prep_kernel(int mode, const void *src,
 
 template <int MS, int NT, int WM, int WN, int GPK, bool HILO, bool SW>
 hipError_t gg_launch(const GgArgs &a, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((gg_kernel<MS, NT, WM, WN, GPK, HILO, SW>), grid,
-                     dim3(64 * WM * WN), 0, st, a);
+  if (a.sdt)
+    hipLaunchKernelGGL((gg_kernel<MS, NT, WM, WN, GPK, HILO, SW, SCALE_F16>), grid,
+                       dim3(64 * WM * WN), 0, st, a);
+  else
+    hipLaunchKernelGGL((gg_kernel<MS, NT, WM, WN, GPK, HILO, SW, SCALE_BF16>), grid,
+                       dim3(64 * WM * WN), 0, st, a);
   return hipGetLastError();
 }
 
