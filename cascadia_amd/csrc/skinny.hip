@@ -411,7 +411,9 @@ CAI4_DEV void epilogue(const KParams &a, f32x4_t (&acc)[MT][NT], int unit, int m
   }
 }
 
-template <int NT, int MT, bool TR, bool SW, bool SLICED>
+// SDT: the scale dtype (a.sdt) as a constant: one conversion instruction per
+// scale in the k-loop.
+template <int NT, int MT, bool TR, bool SW, bool SLICED, int SDT>
 __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int U = skinny_ring_depth(NT);
@@ -536,7 +538,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
-                                 a.sdt, !a.tiled, acc);
+                                 SDT, !a.tiled, acc);
           load_w<NT>(ring[u], wr, wv, kb + u + U, wk, kb + u + U < kb1);
         }
       }
@@ -544,7 +546,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
       for (int u = 0; u < U - 1; ++u)
         if (kb + u < kb1)
           compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
-                                 a.sdt, !a.tiled, acc);
+                                 SDT, !a.tiled, acc);
     }
   };
   if constexpr (SLICED) {
@@ -874,10 +876,22 @@ namespace {
 template <int NT, int MT, bool TR, bool SW>
 hipError_t launch_one(const KParams &k, const SkinnyPlan &p, hipStream_t st) {
   dim3 grid(p.row_blocks, p.m_chunks, p.ksplit), block(64 * p.rw * p.kw, 1, 1);
-  if (p.kslice < p.kper)
-    hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, true>), grid, block, p.lds_bytes, st, k);
-  else
-    hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, false>), grid, block, p.lds_bytes, st, k);
+  const bool sliced = p.kslice < p.kper;
+  if (k.sdt) {
+    if (sliced)
+      hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, true, SCALE_F16>), grid, block,
+                         p.lds_bytes, st, k);
+    else
+      hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, false, SCALE_F16>), grid, block,
+                         p.lds_bytes, st, k);
+  } else {
+    if (sliced)
+      hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, true, SCALE_BF16>), grid, block,
+                         p.lds_bytes, st, k);
+    else
+      hipLaunchKernelGGL((skinny_kernel<NT, MT, TR, SW, false, SCALE_BF16>), grid, block,
+                         p.lds_bytes, st, k);
+  }
   if (hipError_t e = hipGetLastError()) return e;
   if (p.ksplit > 1) {
     dim3 g2(p.row_blocks, p.m_chunks, p.mt), b2(64 * p.rw, 1, 1);
