@@ -278,11 +278,14 @@ CAI4_DEV void load_w(u32x4_t (&b)[NT], const rsrc_t (&wr)[NT], const uint32_t (&
 
 // MFMAs of one k-block: weights from registers, activations and scales from LDS.
 // xp: the fragments are the crate's bytes, not yet transposed (TR only).
+// B136: the constant -136 bf16 operand of the zero-point MFMAs, kept in
+// registers by the caller for the whole loop (a constant built here was
+// rebuilt before every MFMA that used it).
 template <int NT, int MT, bool TR>
-CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&abase)[MT],
-                         const uint32_t (&sbase)[NT], int k, int kr0, int g_lo, int K, int G,
-                         int glog2, int sdt, bool xp, f32x4_t (&acc)[MT][NT]) {
-  const u32x4_t B136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
+CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const u32x4_t B136, const uint8_t *lds,
+                         const uint32_t (&abase)[MT], const uint32_t (&sbase)[NT], int k, int kr0,
+                         int g_lo, int K, int G, int glog2, int sdt, bool xp,
+                         f32x4_t (&acc)[MT][NT]) {
   const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
   const uint32_t koff = (uint32_t)(k - kr0) * 256;
   u32x4_t af[MT][4];
@@ -322,26 +325,47 @@ CAI4_DEV void compute_kb(u32x4_t (&b)[NT], const uint8_t *lds, const uint32_t (&
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) b[nt] = xpose_rows(b[nt]);
     }
+    // the scale group of each 32-column step, once per k-block (uniform;
+    // steps past K take the last valid one), then every step's scales, their
+    // LDS reads in flight together
+    int gs[4];
+    if (glog2 >= 0) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) gs[s] = ((kbase + 32 * min(s, nsteps - 1)) >> glog2) - g_lo;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) gs[s] = (kbase + 32 * min(s, nsteps - 1)) / G - g_lo;
+    }
+    float sc[4][NT];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        sc[s][nt] = scale_bits_f32(
+            *reinterpret_cast<const uint16_t *>(lds + sbase[nt] + 32 * gs[s]), sdt);
+    // one 32-column step: both tiles' fragments decoded, then the MFMAs,
+    // then the scaled adds
+    auto step = [&](int s) {
+      u32x4_t d[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        d[nt] = decode8(s == 0 ? b[nt].x : s == 1 ? b[nt].y : s == 2 ? b[nt].z : b[nt].w);
+      f32x4_t p[MT][NT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const f32x4_t corr = mfma_bf16(af[mt][s], B136, zero4);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) p[mt][nt] = mfma_bf16(af[mt][s], d[nt], corr);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] += sc[s][nt] * p[mt][nt];
+    };
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s >= nsteps) break;
-      const int col = kbase + 32 * s;
-      const int g = (glog2 >= 0 ? (col >> glog2) : col / G) - g_lo;
-      f32x4_t corr[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) corr[mt] = mfma_bf16(af[mt][s], B136, zero4);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float sc =
-            scale_bits_f32(*reinterpret_cast<const uint16_t *>(lds + sbase[nt] + 32 * g), sdt);
-        const uint32_t dw = s == 0 ? b[nt].x : s == 1 ? b[nt].y : s == 2 ? b[nt].z : b[nt].w;
-        const u32x4_t d = decode8(dw);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const f32x4_t p = mfma_bf16(af[mt][s], d, corr[mt]);
-          acc[mt][nt] += sc * p;
-        }
-      }
+      step(s);
     }
   }
 }
@@ -529,6 +553,8 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
       sbase[nt] = a.scale_off + (uint32_t)(((rwi * NT + nt) * ngw * 16 + lr) * 2);
 
     if (mcount > 0) {
+      u32x4_t B136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};  // bf16 -136 x 8
+      asm volatile("" : "+v"(B136));  // one register copy for the loop, not rebuilt per use
       // Whole rounds of U k-blocks with no branch between them, then the
       // remainder (its refills would all be dead).  A refill under a branch
       // leaves the load counts of the two paths apart at the join, and the
@@ -537,7 +563,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
       for (; kb + U <= kb1; kb += U) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
+          compute_kb<NT, MT, TR>(ring[u], B136, lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
                                  SDT, !a.tiled, acc);
           load_w<NT>(ring[u], wr, wv, kb + u + U, wk, kb + u + U < kb1);
         }
@@ -545,7 +571,7 @@ __global__ __launch_bounds__(skinny_max_threads(MT)) void skinny_kernel(KParams 
 #pragma unroll
       for (int u = 0; u < U - 1; ++u)
         if (kb + u < kb1)
-          compute_kb<NT, MT, TR>(ring[u], lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
+          compute_kb<NT, MT, TR>(ring[u], B136, lds, abase, sbase, kb + u, s0, g_lo, a.K, a.G, a.glog2,
                                  SDT, !a.tiled, acc);
     }
   };
