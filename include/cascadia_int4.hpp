@@ -207,10 +207,17 @@ inline void down_args(const Expert &x, DeviceSlice<const uint8_t> dp,
   matrix_args(dp, ds, x.hidden, x.inter, gd_o);
 }
 
-// Per-thread device scratch for the active counts the sparse calls return.
+// Per-thread device scratch for the active counts the sparse calls return,
+// one word on each device the thread calls on (the sparse calls read it back
+// before they return, so a thread's calls never overlap on it).
 inline uint32_t *count_scratch() {
-  thread_local DeviceBuffer<uint32_t> buf(1);
-  return buf.data();
+  constexpr int kMaxDevices = 64;
+  thread_local DeviceBuffer<uint32_t> bufs[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    throw DeviceError("hipGetDevice", CASCADIA_INT4_ERR_DEVICE);
+  if (!bufs[dev].data()) bufs[dev] = DeviceBuffer<uint32_t>(1);
+  return bufs[dev].data();
 }
 
 // The count a sparse call left in count_scratch() (waits for the call).
