@@ -861,7 +861,27 @@ SkinnyPlan plan_core(int N, int K, int G, int m_rows, int m_chunks, int amode, i
   // tokens: 7 %) the split ran faster.
   KPlan q = plan_k(false);
   if (2.0 * partials(q) > 0.2 * wbytes) q = plan_k(true);
-  if (dense_auto && sw && (long)q.ksplit * wgs0 < (long)d.num_cus * 7 / 8) {
+  // Dense SwiGLU pairs of at most 8 token rows: one round of workgroups (the
+  // window above, fewest staged + partial bytes) of 8 waves each -- fewer,
+  // longer weight streams per CU than the rule below gives.  Measured on
+  // config 1's chain at 2 / 4 / 8 tokens: 27.0 -> 26.4, 32.1-32.4 -> 31.1-31.4,
+  // 33.2 -> 32.4-32.8 us; at 16 tokens the window splits K and lost 7 %.
+  constexpr int kSwWaves = 8;
+  if (dense_auto && sw && p.act_rows <= 8) {
+    int r, ks;
+    if (dense_window(false, &r, &ks)) {
+      rw = r;
+      p.rw = rw;
+      p.row_blocks = (int)((units + rw - 1) / rw);
+      wgs0 = (long)p.row_blocks * p.m_chunks;
+      ks_min = ks;
+      q = plan_k(false);
+      if (2.0 * partials(q) > 0.2 * wbytes) q = plan_k(true);
+      q.kw = kSwWaves / rw < 1 ? 1 : kSwWaves / rw;
+      if (q.kw > q.kslice) q.kw = q.kslice;
+      while (q.kw > 1 && lds_need(q.kslice, q.kw) > d.max_lds) --q.kw;
+    }
+  } else if (dense_auto && sw && (long)q.ksplit * wgs0 < (long)d.num_cus * 7 / 8) {
     int r, ks;
     if (dense_window(false, &r, &ks)) {
       rw = r;
