@@ -623,7 +623,11 @@ GemvPlan gemv_plan(int N, int K, int num_cus, int max_kpw) {
   // sized by the k-blocks per wave): many short independent streams
   const long waves = (long)kGvWavesPerCu * num_cus;
   int kw = (int)((2 * waves + tiles) / (2L * tiles));  // nearest
-  if (kw > 16) kw = 16;
+  // at most 8 waves per tile to start from (the loop below adds waves when a
+  // wave's k-range would exceed max_kpw): config 0 (one tile per CU) ran
+  // 4.53-4.58 -> 4.44-4.45 us with 8 waves of 4 k-blocks instead of 16 of 2;
+  // the decode chain and the one-token MoE layers measured the same
+  if (kw > 8) kw = 8;
   if (kw < 1) kw = 1;
   if (kw > KB) kw = KB;
   int kpw = (KB + kw - 1) / kw;
