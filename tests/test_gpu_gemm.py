@@ -110,6 +110,8 @@ SHAPES = [  # n, k, group, sdt, seq
     (130, 384, 128, F16, 17), (33, 96, 32, BF16, 5), (64, 4096, 128, F16, 64),
     (40, 512, 128, F16, 65), (17, 160, 32, F16, 2), (256, 2048, 32, F16, 16),
     (7, 32, 32, BF16, 9), (300, 7168, 32, F16, 1),
+    # groups that are not a power of two (32-column steps grouped by division)
+    (48, 480, 96, BF16, 3), (24, 960, 160, F16, 6),
     # stagings far larger than LDS: K staged in slices inside each workgroup
     (512, 8192, 128, F16, 64), (300, 16384, 32, BF16, 48),
 ]
