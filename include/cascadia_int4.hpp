@@ -113,8 +113,13 @@ class DeviceBuffer {
   operator DeviceSlice<T>() const { return slice(); }
   operator DeviceSlice<const T>() const { return {p_, len_}; }
   // host -> device / device -> host copies of the whole buffer
-  void upload(const T *host) {
-    if (len_ && hipMemcpy(p_, host, len_ * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+  void upload(const T *host) { upload(host, 0, len_); }
+  // host[0 .. count) -> elements [offset, offset + count)
+  void upload(const T *host, size_t offset, size_t count) {
+    if (offset > len_ || count > len_ - offset)
+      throw std::out_of_range("DeviceBuffer::upload past the end");
+    if (count && hipMemcpy(p_ + offset, host, count * sizeof(T), hipMemcpyHostToDevice) !=
+                     hipSuccess)
       throw DeviceError("hipMemcpy", CASCADIA_INT4_ERR_DEVICE);
   }
   std::vector<T> download() const {
@@ -780,11 +785,8 @@ class ExpertStack {
     const size_t per = o.tiling == Tiling::Crate ? flat : cascadia_int4_expert_tiled_bytes(h, i, g);
     ExpertStack s(hidden, intermediate, n_experts, (per + 255) / 256 * 256, o);
     s.blob_ = DeviceBuffer<uint8_t>(n_experts * s.stride_);
-    if (o.tiling == Tiling::Crate) {
-      std::vector<uint8_t> staged(s.blob_.size(), 0);
-      for (size_t e = 0; e < n_experts; ++e)
-        std::memcpy(staged.data() + e * s.stride_, host_flat + e * flat, flat);
-      s.blob_.upload(staged.data());
+    if (o.tiling == Tiling::Crate) {  // each expert at its stride; the padding is never read
+      for (size_t e = 0; e < n_experts; ++e) s.blob_.upload(host_flat + e * flat, e * s.stride_, flat);
       return s;
     }
     DeviceBuffer<uint8_t> one(flat);
