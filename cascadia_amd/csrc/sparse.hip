@@ -409,14 +409,14 @@ constexpr int kXPad = 36;
 // then the LDS stores and the chunk sums (the 8 threads of a chunk add their
 // partial sums by shuffles).
 constexpr int kStageLoads = 8;
-template <int XS>
+template <int XS, int NT = 256>  // NT: the workgroup's threads
 CAI4_DEV void stage_x(const void *x, int x_bf16, int K, float *xs, float *sxs) {
   const int n4 = K / 4;  // 4-value items; K is a multiple of 32, so n4 of 8
-  for (int i0 = 0; i0 < n4; i0 += 256 * kStageLoads) {
+  for (int i0 = 0; i0 < n4; i0 += NT * kStageLoads) {
     f32x4_t v[kStageLoads];
 #pragma unroll
     for (int u = 0; u < kStageLoads; ++u) {
-      const int i = i0 + 256 * u + threadIdx.x;
+      const int i = i0 + NT * u + threadIdx.x;
       const int ic = i < n4 ? i : n4 - 1;  // past the row: a valid item, unused
       if (x_bf16) {
         const u32x2_t b = reinterpret_cast<const u32x2_t *>(x)[ic];
@@ -428,9 +428,9 @@ CAI4_DEV void stage_x(const void *x, int x_bf16, int K, float *xs, float *sxs) {
     }
 #pragma unroll
     for (int u = 0; u < kStageLoads; ++u) {
-      const int i = i0 + 256 * u + threadIdx.x;
-      // uniform per 8-thread chunk: n4 and 256 are multiples of 8
-      if (i0 + 256 * u >= n4) break;
+      const int i = i0 + NT * u + threadIdx.x;
+      // uniform per 8-thread chunk: n4 and NT are multiples of 8
+      if (i0 + NT * u >= n4) break;
       if (i < n4) *reinterpret_cast<f32x4_t *>(xs + XS * (i >> 3) + 4 * (i & 7)) = v[u];
       float p = (v[u].x + v[u].y) + (v[u].z + v[u].w);
       p += __shfl_xor(p, 1, 64);
@@ -543,30 +543,40 @@ __global__ void __launch_bounds__(256)
 }
 
 // f32 slots before the chunk sums in the fused kernels' LDS: the padded x,
-// which the AXPY's padded wave rows (four waves x 64 C rows of kXPad) reuse
+// which the AXPY's padded wave rows (NW waves x 64 C rows of kXPad) reuse
 // afterwards.
-__host__ __device__ inline int subset_x_floats(int H, int C) {
-  const int xf = (H / 32) * kXPad, rf = 4 * 64 * C * kXPad;  // x, or four waves' rows
+__host__ __device__ inline int subset_x_floats(int H, int C, int NW, bool axpy) {
+  const int xf = (H / 32) * kXPad, rf = axpy ? NW * 64 * C * kXPad : 0;  // x, the waves' rows
   return xf > rf ? xf : rf;
 }
 
+// Waves per workgroup of the fused kernels: a group's active rows spread over
+// 8 waves, so that a group with many active lanes has fewer rows per wave,
+// except where the AXPY form's 8 output rows per lane would not fit the LDS
+// (C = 4).  Measured (config 1, one token, tau 0.1 / 0.3): AXPY form 34.4 /
+// 26.6 -> 29.7 / 24.7 us, GEMV form 34.2 / 28.6 -> 30.4 / 26.9 us.
+constexpr int subset_waves(bool axpy, int C) { return !axpy || C <= 2 ? 8 : 4; }
+
 // The fused sparse forms: workgroup (group g of kSubsetGroup lanes, token).
 // Threads 0 .. kSubsetGroup - 1 each test one lane; the active lanes are
-// listed in ascending order (ballot + mbcnt); wave w takes entries w, w + 4,
-// ... RB at a time, reading their up rows (and, AXPY, their transposed-down
-// rows) in one round of loads.  C: chunk slots per lane (K and H <= 2048 C).
-// AXPY: lane l owns columns 32(l + 64 j) .. + 31 of the output (j < C):
-// combined = inter * scale, acc += combined * (128 + n), the offset (-136 per
-// unit of combined) applied once per chunk slot at the end (the -8 of
-// ffn_axpy.rs:118-134, plus nib128's 128); the four waves' rows are added in
-// wave order (0, 1, 2, 3) into the group's partial row.  LDS (dynamic):
+// listed in ascending order (ballot + mbcnt); wave w of NW takes entries w,
+// w + NW, ... RB at a time, reading their up rows (and, AXPY, their
+// transposed-down rows) in one round of loads.  C: chunk slots per lane (K and
+// H <= 2048 C).  AXPY: lane l owns columns 32(l + 64 j) .. + 31 of the output
+// (j < C): combined = inter * scale, acc += combined * (128 + n), the offset
+// (-136 per unit of combined) applied once per chunk slot at the end (the -8
+// of ffn_axpy.rs:118-134, plus nib128's 128); the waves' rows are added in
+// wave order (0, 1, ..., NW - 1) into the group's partial row.  LDS (dynamic):
 // subset_x_floats + H / 32 floats, up to 148 KB (gfx950: 160 KB per CU).
-template <bool AXPY, bool TILED, int SDT, int C>
-__global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) {
-  constexpr int RB = C <= 2 ? 8 : 4;
+template <bool AXPY, bool TILED, int SDT, int C, int NW>
+__global__ void __launch_bounds__(64 * NW) sparse_subset_kernel(SparseSubsetArgs a) {
+  // rows per wave per round: 32 per workgroup round at C <= 2 (8 waves
+  // hold half the rows each within 256 VGPRs)
+  constexpr int RB = C <= 2 && NW == 4 ? 8 : 4, NT = 64 * NW;
+  static_assert(NW == 4 || NW == 8, "waves per workgroup");
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // read as f32x4
-  __shared__ float s_red[4];
-  __shared__ uint32_t s_flag[4], s_wn[2];
+  __shared__ float s_red[NW];
+  __shared__ uint32_t s_flag[NW], s_wn[2];
   __shared__ uint32_t s_id[kSubsetGroup];
   __shared__ float s_val[kSubsetGroup];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -575,20 +585,20 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
   // [subset_x_floats] f32: x (padded chunks), then the AXPY's wave rows;
   // then [H / 32] chunk sums
   float *xs = s_dyn;
-  float *sxs = s_dyn + subset_x_floats(H, C);
+  float *sxs = s_dyn + subset_x_floats(H, C, NW, AXPY);
   // the token's slots: every thread folds its share (loads issued first)
   const uint32_t *sl = a.slots + (size_t)t * a.n_slots;
   uint32_t sv[kSlotLoads];
 #pragma unroll
   for (int u = 0; u < kSlotLoads; ++u) {
-    const int k = tid + 256 * u;
+    const int k = tid + NT * u;
     sv[u] = k < a.n_slots ? sl[k] : 0u;
   }
   const int i = g * a.lanes + tid;
   const bool in = tid < a.lanes && i < a.I;
   const float gv = in ? a.gate[(size_t)t * a.I + i] : 0.0f;
   const float th = in && a.thr ? a.thr[i] : 0.0f;
-  stage_x<kXPad>(a.x_bf16 ? (const void *)(reinterpret_cast<const uint16_t *>(a.x) + (size_t)t * H)
+  stage_x<kXPad, NT>(a.x_bf16 ? (const void *)(reinterpret_cast<const uint16_t *>(a.x) + (size_t)t * H)
                           : (const void *)(reinterpret_cast<const float *>(a.x) + (size_t)t * H),
                  a.x_bf16, H, xs, sxs);
   float m = 0.0f;
@@ -598,7 +608,7 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
     m = fmaxf(m, bitsf(sv[u] & 0x7FFFFFFFu));
     f |= sv[u] >> 31;
   }
-  for (int k = tid + 256 * kSlotLoads; k < a.n_slots; k += 256) {
+  for (int k = tid + NT * kSlotLoads; k < a.n_slots; k += NT) {
     const uint32_t u = sl[k];
     m = fmaxf(m, bitsf(u & 0x7FFFFFFFu));
     f |= u >> 31;
@@ -613,7 +623,7 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
   float mx = 0.0f;
   bool any = false;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < NW; ++w) {
     mx = fmaxf(mx, s_red[w]);
     any = any || s_flag[w] != 0u;
   }
@@ -652,14 +662,14 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
   // skipped by scalar branches, not loaded
   const int ns = __builtin_amdgcn_readfirstlane((int)n);
   const int ws = __builtin_amdgcn_readfirstlane(wave);
-  for (int f0 = ws; f0 < ns; f0 += 4 * RB) {
+  for (int f0 = ws; f0 < ns; f0 += NW * RB) {
     int r[RB];
     bool ok[RB];
     float up[RB];
-    const int live = (ns - f0 + 3) / 4 < RB ? (ns - f0 + 3) / 4 : RB;
+    const int live = (ns - f0 + NW - 1) / NW < RB ? (ns - f0 + NW - 1) / NW : RB;
 #pragma unroll
     for (int u = 0; u < RB; ++u) {
-      const int fe = f0 + 4 * u;
+      const int fe = f0 + NW * u;
       ok[u] = u < live;
       r[u] = (int)s_id[ok[u] ? fe : f0];
       up[u] = 0.0f;
@@ -688,7 +698,7 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
 #pragma unroll
     for (int u = 0; u < RB; ++u) {
       if (u >= live) continue;
-      const int fe = f0 + 4 * u;
+      const int fe = f0 + NW * u;
       // inter[r] = silu_gate[r] * up[r] (ffn_sparsity.rs:527, 711-716)
       const float v = s_val[fe] * wave_sum(up[u]);
       if (!AXPY) {
@@ -724,7 +734,7 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
   // every wave stores its rows in an LDS region of its own (x is no longer
   // read; rows kXPad floats apart, as x's chunks, so the lanes' 16-byte
   // stores fall in different banks); after one barrier each thread adds the
-  // four waves' values of 32 C / 4 columns in wave order and stores them
+  // NW waves' values of 32 C / NW columns in wave order and stores them
   __syncthreads();
   {
     float *mine = xs + (size_t)wave * (64 * C * kXPad);
@@ -739,7 +749,8 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
   }
   __syncthreads();
   {
-    constexpr int PER = 32 * C / 4;  // columns per thread: 64 C rows of 32 over 256 threads
+    constexpr int PER = 32 * C / NW;  // columns per thread: 64 C rows of 32 over NT threads
+    static_assert(PER % 4 == 0, "whole f32x4 per thread");
     const int q = (tid * PER) / 32, k0 = (tid * PER) % 32;  // row, first column in it
     float *prow = a.partial + ((size_t)tl * gridDim.x + g) * H + 32 * q + k0;
     if (32 * q < H) {
@@ -747,7 +758,7 @@ __global__ void __launch_bounds__(256) sparse_subset_kernel(SparseSubsetArgs a) 
       for (int k4 = 0; k4 < PER / 4; ++k4) {
         f32x4_t v = *reinterpret_cast<const f32x4_t *>(xs + (size_t)q * kXPad + k0 + 4 * k4);
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
+        for (int w = 1; w < NW; ++w) {
           const f32x4_t p = *reinterpret_cast<const f32x4_t *>(
               xs + (size_t)w * (64 * C * kXPad) + (size_t)q * kXPad + k0 + 4 * k4);
           v = f32x4_t{v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w};
@@ -894,10 +905,11 @@ hipError_t rows_subset_launch(const RowsMatrix &w, const void *x, bool x_bf16,
 
 template <bool AXPY, bool TILED, int SDT, int C>
 hipError_t subset_launch(const SparseSubsetArgs &a, int T, hipStream_t st) {
-  const size_t lds = ((size_t)subset_x_floats(a.H, C) + a.H / 32) * 4;
-  auto k = sparse_subset_kernel<AXPY, TILED, SDT, C>;
-  hipLaunchKernelGGL(k, dim3((unsigned)subset_groups(a.I, a.lanes), (unsigned)T), dim3(256), lds,
-                     st, a);
+  constexpr int NW = subset_waves(AXPY, C);
+  const size_t lds = ((size_t)subset_x_floats(a.H, C, NW, AXPY) + a.H / 32) * 4;
+  auto k = sparse_subset_kernel<AXPY, TILED, SDT, C, NW>;
+  hipLaunchKernelGGL(k, dim3((unsigned)subset_groups(a.I, a.lanes), (unsigned)T), dim3(64 * NW),
+                     lds, st, a);
   return hipGetLastError();
 }
 
