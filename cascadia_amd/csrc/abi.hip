@@ -447,7 +447,9 @@ SparseWorkspace sparse_workspace(int dev, uint32_t hidden, uint32_t inter, uint3
   SparseWorkspace w;
   w.lanes = align256((size_t)n_tokens * inter * 4);
   w.slots = sparse_slot_bytes(inter, n_tokens);
-  w.cnt = align256((size_t)n_tokens * cai4::subset_groups((int)inter, 64) * 4);
+  w.cnt = align256((size_t)n_tokens *
+                   cai4::subset_groups((int)inter, cai4::subset_lanes((int)inter, d.num_cus, false)) *
+                   4);
   w.partials = part;
   w.total = 3 * w.lanes + w.slots + w.cnt + part;
   const FfnWorkspace f = ffn_workspace(dev, hidden, inter, group, n_tokens, true);
@@ -617,7 +619,7 @@ int sparse_common(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
     a.x_bf16 = x_f32 ? 0 : 1;
     a.I = (int)inter;
     a.H = (int)hidden;
-    a.lanes = cai4::subset_lanes((int)inter, device_props(dev).num_cus);
+    a.lanes = cai4::subset_lanes((int)inter, device_props(dev).num_cus, false);
     a.cnt = cnt;
     a.inter = mid;
     if ((rc = hip_status(cai4::sparse_subset_mask(a, (int)n_tokens, st)))) return rc;
@@ -667,7 +669,8 @@ AxpyFfnWorkspace axpy_ffn_workspace(int dev, uint32_t hidden, uint32_t inter, ui
   // one token's partial rows: one per lane group (128 lanes on the
   // rows-subset path, 256 on the other)
   const int groups = subset_path(hidden)
-                         ? cai4::subset_groups((int)inter, cai4::subset_lanes((int)inter, d.num_cus))
+                         ? cai4::subset_groups((int)inter,
+                                               cai4::subset_lanes((int)inter, d.num_cus, true))
                          : cai4::sparse_groups((int)inter);
   const size_t row_set = (size_t)groups * hidden * 4;
   // at most ~32 MB of partial rows per launch pair
@@ -749,7 +752,7 @@ int axpy_ffn(uint32_t hidden, uint32_t inter, uint32_t group, uint32_t sdt,
     a.x_bf16 = 0;
     a.I = (int)inter;
     a.H = (int)hidden;
-    a.lanes = cai4::subset_lanes((int)inter, device_props(dev).num_cus);
+    a.lanes = cai4::subset_lanes((int)inter, device_props(dev).num_cus, true);
     a.cnt = cnt;
     a.dt = e->down_packed;
     a.dt_s = reinterpret_cast<const uint16_t *>(e->down_scale);

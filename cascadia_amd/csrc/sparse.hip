@@ -557,9 +557,9 @@ __host__ __device__ inline int subset_x_floats(int H, int C, int NW, bool axpy) 
 // 26.6 -> 29.7 / 24.7 us, GEMV form 34.2 / 28.6 -> 30.4 / 26.9 us.
 constexpr int subset_waves(bool axpy, int C) { return !axpy || C <= 2 ? 8 : 4; }
 
-// The fused sparse forms: workgroup (group g of kSubsetGroup lanes, token).
-// Threads 0 .. kSubsetGroup - 1 each test one lane; the active lanes are
-// listed in ascending order (ballot + mbcnt); wave w of NW takes entries w,
+// The fused sparse forms: workgroup (group g of a.lanes lanes, 16 to
+// kSubsetGroup, token).  Threads 0 .. a.lanes - 1 each test one lane; the
+// active lanes are listed in ascending order (ballot + mbcnt); wave w of NW takes entries w,
 // w + NW, ... RB at a time, reading their up rows (and, AXPY, their
 // transposed-down rows) in one round of loads.  C: chunk slots per lane (K and
 // H <= 2048 C).  AXPY: lane l owns columns 32(l + 64 j) .. + 31 of the output
@@ -972,20 +972,34 @@ hipError_t rows_subset(const RowsMatrix &w, const void *x, bool x_bf16, const ui
   return e;
 }
 
-int subset_lanes(int I, int num_cus) {
+int subset_lanes(int I, int num_cus, bool axpy) {
   const int ev = tuning_env("CASCADIA_INT4_SUBSET_LANES", 0);
-  if (ev == 64 || ev == 128) return ev;
-  return subset_groups(I, kSubsetGroup) < num_cus ? 64 : kSubsetGroup;
+  if (subset_lanes_ok(ev)) return ev;
+  if (subset_groups(I, kSubsetGroup) >= num_cus) return kSubsetGroup;
+  // Smaller groups for small intermediates (2048 lanes in 64-lane groups left
+  // 224 CUs idle).  The GEMV form halves its group while the groups number
+  // fewer than the CUs, to 8 lanes; the AXPY form, whose workgroups each add
+  // a partial row and hold the LDS of a CU, while they cover under half the
+  // CUs, to 16.  Measured (one token, tau 0.1 / 0.3): H 7168, I 2048 GEMV
+  // form 32.0 / 26.3 us at 64 lanes, 21.2 / 19.7 at 16, 19.3 / 18.8 at 8;
+  // H 4096, I 14336 GEMV form 30.4 / 26.9 at 64, 29.6 / 26.8 at 32, the AXPY
+  // form 29.7 / 24.7 at 64 against 35.9 / 31.5 at 32.
+  int lanes = 64;
+  if (axpy)
+    while (lanes > 16 && subset_groups(I, lanes) < num_cus / 2) lanes /= 2;
+  else
+    while (lanes > 8 && subset_groups(I, lanes) < num_cus) lanes /= 2;
+  return lanes;
 }
 
 hipError_t sparse_subset_mask(const SparseSubsetArgs &a, int T, hipStream_t st) {
-  if (a.lanes != 64 && a.lanes != kSubsetGroup) return hipErrorInvalidValue;
+  if (!subset_lanes_ok(a.lanes)) return hipErrorInvalidValue;
   return subset_dispatch<false>(a, T, st);
 }
 
 hipError_t sparse_subset_axpy(const SparseSubsetArgs &a, int n_tokens, float *out,
                               uint32_t *counts, hipStream_t st) {
-  if (a.lanes != 64 && a.lanes != kSubsetGroup) return hipErrorInvalidValue;
+  if (!subset_lanes_ok(a.lanes)) return hipErrorInvalidValue;
   if (hipError_t e = subset_dispatch<true>(a, n_tokens, st)) return e;
   const int ng = subset_groups(a.I, a.lanes);
   hipLaunchKernelGGL(sparse_axpy_reduce_kernel,

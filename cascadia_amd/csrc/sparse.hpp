@@ -76,9 +76,13 @@ hipError_t rows_subset(const RowsMatrix &w, const void *x, bool x_bf16, const ui
                        int n, float *y, size_t max_lds, int num_cus, hipStream_t st);
 
 // Intermediate lanes per workgroup of the fused rows-subset sparse kernels:
-// 128, or 64 when 128-lane groups would leave CUs idle (subset_lanes).
+// 128, or 64 when 128-lane groups would leave CUs idle, down to 8 (GEMV form)
+// or 16 (AXPY form) for small intermediates (subset_lanes).
 constexpr int kSubsetGroup = 128;
-int subset_lanes(int I, int num_cus);
+int subset_lanes(int I, int num_cus, bool axpy);
+inline bool subset_lanes_ok(int lanes) {
+  return lanes == 8 || lanes == 16 || lanes == 32 || lanes == 64 || lanes == kSubsetGroup;
+}
 inline int subset_groups(int I, int lanes) { return (I + lanes - 1) / lanes; }
 // The fused kernels stage one token's x (H f32 + H / 32 chunk sums) in LDS and
 // hold the transposed down's H columns of a lane in registers: H a multiple of
@@ -99,7 +103,7 @@ struct SparseSubsetArgs {
   const void *x;     // [T, H] f32, or bf16 bits when x_bf16
   int x_bf16;
   int I, H;
-  int lanes;         // lanes per workgroup (group): subset_lanes(I, CUs)
+  int lanes;         // lanes per workgroup (group): subset_lanes(I, CUs, form)
   uint32_t *cnt;     // [T, subset_groups(I, lanes)] active lanes per group
   // GEMV form: inter [T, I] = silu * up on active lanes, else 0 (stable
   // SiLU, build_active_mask_mode's)
