@@ -928,17 +928,28 @@ def main():
         return
     if args.profile_sparse:
         # 50 calls each of the GEMV form (expert_forward_sparse) and the AXPY
-        # form (ffn_forward_sparse_axpy_f32) at tau 0.3, weight copies rotating
-        # past the Infinity Cache
+        # form (ffn_forward_sparse_axpy_f32) at tau 0.3 on the layout the
+        # default run times (gate and down tiled, up rows contiguous), weight
+        # copies rotating past the Infinity Cache
+        import ctypes as C
+
         h, i, g = 4096, 14336, 128
         nc = chain_copies(cl, h, i, g)
         copies = Copies(cl, torch, h, i, g, sdt, nc, keep_crate=1)
+        UPS = [(cl.fill_bytes(torch.empty(i * h // 2, dtype=torch.uint8, device="cuda"), 3, 800 + c),
+                cl.fill_scales(torch.empty(i * (h // g) * 2, dtype=torch.uint8, device="cuda"), 3,
+                               900 + c, sdt)) for c in range(nc)]
         xs1 = cl.fill_normal(torch.empty(h, dtype=torch.bfloat16, device="cuda"), 0, 23)
         os1 = torch.empty(h, dtype=torch.bfloat16, device="cuda")
+        st = torch.cuda.current_stream().cuda_stream
+        ex = [cl._lib.Expert(W.gate_packed_bytes().data_ptr(), W.gate_scale_bits().data_ptr(),
+                             UPS[c][0].data_ptr(), UPS[c][1].data_ptr(),
+                             W.down_packed_bytes().data_ptr(), W.down_scale_bits().data_ptr(),
+                             cl.TILING_MFMA_UP_ROWS) for c, W in enumerate(copies.w)]
         for r in range(50):
-            fr = cl.expert_forward_sparse(xs1.view(torch.int16), *copies.w[r % nc].slices(),
-                                          os1.view(torch.int16), 0.3, group_size=g,
-                                          scale_dtype=sdt, tiling=cl.TILING_MFMA)
+            cl.check("cascadia_int4_expert_forward_sparse", cl.lib().cascadia_int4_expert_forward_sparse(
+                h, i, g, sdt, C.byref(ex[r % nc]), xs1.data_ptr(), 1, 0.3, None, os1.data_ptr(),
+                None, None, st))
         src = cl.ExpertWeights(copies.crate[0], h, i, g, sdt)
         pts = [cl.transpose_requantize_down(src.down_packed_bytes(), src.down_scale_bits(), h, i,
                                             group_size=g, scale_dtype=sdt)]
@@ -948,17 +959,18 @@ def main():
         xf1, of1 = xs1.float(), torch.empty(h, dtype=torch.float32, device="cuda")
         ws = torch.empty(cl.ffn_sparse_axpy_workspace_bytes(h, i, 1, g), dtype=torch.uint8,
                          device="cuda")
+        exa = [cl._lib.Expert(W.gate_packed_bytes().data_ptr(), W.gate_scale_bits().data_ptr(),
+                              UPS[c][0].data_ptr(), UPS[c][1].data_ptr(), pts[c][0].data_ptr(),
+                              pts[c][1].data_ptr(), cl.TILING_MFMA_UP_ROWS)
+               for c, W in enumerate(copies.w)]
         for r in range(50):
-            W = copies.w[r % nc]
-            fa = cl.ffn_forward_sparse_axpy_f32(xf1, h, i, W.gate_packed_bytes(), W.gate_scale_bits(),
-                                                W.up_packed_bytes(), W.up_scale_bits(),
-                                                *pts[r % nc], of1, 0.3, group_size=g,
-                                                scale_dtype=sdt, workspace=ws,
-                                                tiling=cl.TILING_MFMA)
+            cl.check("cascadia_int4_ffn_forward_sparse_axpy_f32",
+                     cl.lib().cascadia_int4_ffn_forward_sparse_axpy_f32(
+                         h, i, g, sdt, C.byref(exa[r % nc]), xf1.data_ptr(), 1, 0.3, None,
+                         of1.data_ptr(), None, ws.data_ptr(), st))
         torch.cuda.synchronize()
         print(json.dumps({"profile": "sparse_expert+sparse_axpy_ffn", "tau": 0.3,
-                          "active_frac": fr, "active_frac_axpy_copy": fa, "launches": 50,
-                          "copies": nc}), flush=True)
+                          "layout": "mfma_up_rows", "launches": 50, "copies": nc}), flush=True)
         return
     if args.profile_moe:
         # eager steps between two marker dispatches (then the counter
