@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--headline-only]
     python bench.py --profile | --profile-gemv | --profile-prefill | --profile-moe | --profile-sparse
+                    | --profile-batches
         (launch one workload eagerly, untimed, for rocprofv3)
 
 Headline: the Llama-3-8B-shaped decode FFN chain,
@@ -69,6 +70,9 @@ def parse():
                     help="launch the config 0 GEMV 200 times over rotating copies, for rocprofv3")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="launch the config 2 prefill GEMMs eagerly, without timing, for rocprofv3")
+    ap.add_argument("--profile-batches", action="store_true",
+                    help="run the config 1 chain at M = 4 and 16, 40 eager calls each, for "
+                         "rocprofv3")
     ap.add_argument("--profile-sparse", action="store_true",
                     help="launch the config 1 activation-sparse expert (tau 0.3) 50 times "
                          "eagerly, for rocprofv3")
@@ -925,6 +929,21 @@ def main():
             del pre
         print(json.dumps({"profile": "prefill", "shapes": PREFILL_SHAPES, "launches": 5}),
               flush=True)
+        return
+    if args.profile_batches:
+        # the config 1 chain at M = 4 and 16 (the skinny kernels, the down's K
+        # split and its reduce), 40 eager calls each over rotating copies
+        h, i, g = 4096, 14336, 128
+        copies = Copies(cl, torch, h, i, g, sdt, chain_copies(cl, h, i, g), keep_crate=0)
+        for mm in (4, 16):
+            xm = cl.fill_normal(torch.empty((mm, h), dtype=torch.bfloat16, device="cuda"), 0, 22)
+            om = torch.empty((mm, h), dtype=torch.bfloat16, device="cuda")
+            fn = chain_fn(cl, copies, xm, om, sdt)
+            for k in range(40):
+                fn(k)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": "config1_batches", "M": [4, 16], "launches": 40,
+                          "copies": len(copies.w)}), flush=True)
         return
     if args.profile_sparse:
         # 50 calls each of the GEMV form (expert_forward_sparse) and the AXPY
