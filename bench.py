@@ -887,7 +887,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; --gpus N > 1 is not supported "
-                                   "(the path is single-GPU; sharding is documented in DESIGN.md)"}))
+                                   "(value is one GPU's throughput; the path is not sharded)"}))
         sys.exit(2)
     import torch
 
